@@ -1,0 +1,140 @@
+/*
+ * opentars_amd: the openTARS golden model's quantized matrix path on MI355X (gfx950).
+ *
+ * C ABI of libopentars_amd.so. Plain pointers and sizes only. Every pointer is a device
+ * pointer (hipMalloc'd or a torch CUDA/HIP tensor's data_ptr) except where noted; `stream` is a
+ * hipStream_t (NULL = the null stream). Work is enqueued on `stream` and is stream-ordered with
+ * whatever else the caller puts there; nothing synchronizes the host. No entry point allocates.
+ *
+ * Every entry point validates its arguments on the host before it launches anything and returns
+ * a status. On a non-zero status nothing was launched and nothing was written, mirroring the
+ * golden model's "every check before any write" rule (tars_mini/golden.py:450-472).
+ *
+ * Results are bit-exact against the golden model's arithmetic (tars_mini/golden.py,
+ * tars_mini/numerics.py): exact int32 dot products, then the fp32 epilogue one rounded step at a
+ * time (round-to-nearest-even, subnormals flushed on the way in and out, canonical NaN, no FMA).
+ * Results never depend on launch geometry.
+ */
+#ifndef OPENTARS_AMD_H
+#define OPENTARS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: 0, or minus the contract's error code (tars_mini/contract.py:107-111) ---- */
+#define TARS_OK           0
+#define TARS_E_FIELD     (-6)   /* a field value the contract rejects (act/out code, K > 65535, ...) */
+#define TARS_E_ALIGN     (-7)   /* shape / alignment / stride rule (N % 16, K % 16, 16-byte offsets) */
+#define TARS_E_RANGE     (-8)   /* a size that cannot be addressed (overflowing extents)              */
+#define TARS_E_OVERLAP   (-9)   /* an output overlaps an input: the golden's ContractError            */
+#define TARS_E_ARG       (-10)  /* a NULL pointer where data is required, or a bad block list        */
+#define TARS_E_DEVICE    (-11)  /* the HIP runtime refused the launch (no device, bad stream, ...)   */
+
+/* ---- epilogue codes (tars_mini/contract.py:96-101) ---- */
+#define TARS_ACT_NONE     0
+#define TARS_ACT_RELU     1
+#define TARS_ACT_RELU6    2
+#define TARS_ACT_GELU     3
+#define TARS_ACT_SILU     4
+#define TARS_ACT_SIGMOID  5
+#define TARS_ACT_SOFTPLUS 6
+#define TARS_ACT_EXP      7
+#define TARS_OUT_FP32     0
+#define TARS_OUT_BF16     1
+#define TARS_OUT_INT8     2     /* q8(y, out_scale): out_scale_bits is its fp32 encoding */
+
+/* ---- W4A16 activation dtypes (tars_mini/contract.py:92) ---- */
+#define TARS_DT_BF16      0
+#define TARS_DT_FP32      4
+
+/*
+ * Per-token INT8 quantization of fp32 rows.
+ * Replaces numerics.quant_rows (tars_mini/numerics.py:383-390) as run by the ROW_QUANT descriptor
+ * (tars_mini/golden.py:369-372, emitted by Dev.quant, tars_mini/llm.py:97-104).
+ *   x  fp32 [M, K], row stride lda bytes      q  int8 [M, K], row stride ldq bytes
+ *   s  fp32 [M] row scales (amax * fp32(1/127))
+ * Rules: M >= 1, K >= 16, K % 16 == 0, lda/ldq multiples of 16 holding a row, 16-byte aligned
+ * pointers; q and s must not overlap x or each other.
+ */
+int tars_quant_rows(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s,
+                    int32_t M, int32_t K, void* stream);
+
+/*
+ * W8A8 GEMM / GEMV with the golden epilogue:
+ *   y[m,n] = convert(act(((i2f(sum_k A[m,k] W[n,k]) * srow[m]) * scol[n]) + bias[n]))
+ * Replaces Machine._gemm (tars_mini/golden.py:326-349) for OP_GEMM with QM_ROWCOL (srow given),
+ * QM_CHANNEL (srow NULL, scol_count == N) and QM_TENSOR (srow NULL, scol_count == 1); emitted by
+ * Dev.gemm_rc (tars_mini/llm.py:111-118).
+ *   A     int8 [M, K], row stride lda bytes      W     int8 [N, K] dense row-major
+ *   srow  fp32 [M] or NULL                        scol  fp32 [scol_count]
+ *   bias  fp32 [N] or NULL                        Y     [M, N] of the output format, stride ldy
+ * M == 1 runs the HBM-streaming GEMV (packed int8 dot products); M >= 2 runs INT8 MFMA tiles.
+ * Rules: N % 16 == 0, K % 16 == 0, 16 <= K <= 65535, act in 0..7, out in {FP32, BF16, INT8},
+ * out_scale_bits == 0 unless out == INT8, 16-byte aligned pointers and strides.
+ */
+int tars_gemm_w8a8(const int8_t* A, int64_t lda, const float* srow,
+                   const int8_t* W, const float* scol, int32_t scol_count, const float* bias,
+                   void* Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
+                   int32_t act, int32_t out, uint32_t out_scale_bits, void* stream);
+
+/*
+ * W8A8 with K split into blocks that share one quantized activation row block and one
+ * per-channel scale vector: block i covers columns [c_i, c_i + K_i) of A (c_0 = 0) with its own
+ * dense weights W_i [N, K_i]; each block's partial is a full W8A8 result in fp32 and the partials
+ * add in block order, y = ((y_0 + y_1) + y_2) + ...  fp32 output only.
+ * Replaces QwenLowering.lin_k + the ELT_ADD loop (tars_mini/llm.py:303-321, 627-635, 753-761;
+ * tars_mini/golden.py:411-412).
+ *   W_blocks, K_blocks: HOST arrays of nblocks device pointers / block widths (1 <= nblocks <= 8,
+ *   every K_i % 16 == 0, 16 <= K_i <= 65535).
+ */
+int tars_gemm_w8a8_ksplit(const int8_t* A, int64_t lda, const float* srow,
+                          const int8_t* const* W_blocks, const int32_t* K_blocks, int32_t nblocks,
+                          const float* scol, float* Y, int64_t ldy, int32_t M, int32_t N,
+                          void* stream);
+
+/*
+ * Block-FP alignment of W4A16 activations: fp32 or bf16 [M, K] -> int16 mantissas [M, K] and one
+ * fp32 scale per 128-wide group [M, K/128].
+ * Replaces numerics.align_w4_groups (tars_mini/numerics.py:55-98).
+ *   x: a_dtype TARS_DT_FP32 or TARS_DT_BF16, row stride lda bytes; q row stride ldq bytes;
+ *   scales row stride lds bytes (multiple of 4). Rules: K % 128 == 0, K >= 128.
+ */
+int tars_align_w4(const void* x, int64_t lda, int32_t a_dtype, int16_t* q, int64_t ldq,
+                  float* scales, int64_t lds, int32_t M, int32_t K, void* stream);
+
+/*
+ * W4A16 group-128 GEMV/GEMM with fp16 group scales and block-FP activations:
+ *   per group g: term = (i2f(dot_g) * ws[n,g]) * xs[m,g]; four fp32 banks add terms g % 4 in g
+ *   order from +0; y = (b0 + b1) + (b2 + b3); then bias, act, convert.
+ * Replaces Machine._gemm_w4 (tars_mini/golden.py:295-324), emitted by Dev.gemm_w4
+ * (tars_mini/llm.py:120-132).
+ *   x   fp32 / bf16 [M, K], stride lda       Wp  uint8 [N, K/2] nibbles (low = even k), 128-B aligned
+ *   ws  uint16 [N, K/128] binary16 bits      bias fp32 [N] or NULL; Y as tars_gemm_w8a8
+ * Rules: K % 256 == 0, 256 <= K <= 8192, N % 16 == 0 (tars_mini/golden.py:96-99, 140-147).
+ */
+int tars_gemm_w4a16(const void* x, int64_t lda, int32_t a_dtype,
+                    const uint8_t* Wp, const uint16_t* ws, const float* bias,
+                    void* Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
+                    int32_t act, int32_t out, uint32_t out_scale_bits, void* stream);
+
+/* Library version string ("opentars_amd <semver> gfx950"). Host only, never fails. */
+const char* tars_version(void);
+
+/* Text of the last non-zero status on the calling thread ("" if none). Host only. */
+const char* tars_last_error(void);
+
+/*
+ * Kernel-family selection for W8A8 with M >= 2 (test and benchmark control, not part of the
+ * reference's interface): 0 = automatic, 1 = force the dot-product GEMV family for every M,
+ * 2 = force the MFMA family for every M. Returns the previous setting. Process-wide.
+ */
+int tars_set_w8a8_path(int path);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPENTARS_AMD_H */

@@ -1,0 +1,63 @@
+"""ctypes binding of libopentars_amd.so (the C ABI declared in include/opentars_amd.h).
+
+The library is built in-tree by opentars_amd.build. Loading fails loudly when it is missing:
+there is no CPU fallback anywhere in the package.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_char_p, c_int, c_int32, c_int64, c_uint32, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libopentars_amd.so"
+
+# Status codes (include/opentars_amd.h)
+OK, E_FIELD, E_ALIGN, E_RANGE, E_OVERLAP, E_ARG, E_DEVICE = 0, -6, -7, -8, -9, -10, -11
+STATUS_NAMES = {OK: "OK", E_FIELD: "E_FIELD", E_ALIGN: "E_ALIGN", E_RANGE: "E_RANGE",
+                E_OVERLAP: "E_OVERLAP", E_ARG: "E_ARG", E_DEVICE: "E_DEVICE"}
+
+# Every exported entry point: name -> (restype, argtypes)
+SIGNATURES = {
+    "tars_quant_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p]),
+    "tars_gemm_w8a8": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
+                               c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_uint32,
+                               c_void_p]),
+    "tars_gemm_w8a8_ksplit": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
+                                      c_void_p, c_int64, c_int32, c_int32, c_void_p]),
+    "tars_align_w4": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_int64, c_void_p, c_int64, c_int32,
+                              c_int32, c_void_p]),
+    "tars_gemm_w4a16": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                c_int32, c_int32, c_int32, c_int32, c_int32, c_uint32, c_void_p]),
+    "tars_version": (c_char_p, []),
+    "tars_last_error": (c_char_p, []),
+    "tars_set_w8a8_path": (c_int, [c_int]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once). Raises LibraryMissing when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise LibraryMissing(f"{LIB_PATH} is not built; run `python -m opentars_amd.build` "
+                                 "(the HIP path has no fallback)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().tars_last_error().decode()
+
+
+def version() -> str:
+    return lib().tars_version().decode()

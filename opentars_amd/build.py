@@ -1,0 +1,57 @@
+"""Build libopentars_amd.so in-tree with hipcc for gfx950.
+
+    python -m opentars_amd.build            # or __graft_entry__.build()
+
+Flags that matter for bit-exactness:
+  -ffp-contract=off      no multiply-add fusion anywhere: every fp32 step rounds on its own
+  (no -ffast-math, no -fgpu-flush-denormals-to-zero): fp32 subnormals are preserved by the
+                         hardware and flushed explicitly after each step, as the reference does
+  -packed-fp32-ops off   scalar fp32 instructions only
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libopentars_amd.so"
+SOURCES = ["abi.hip", "quant_rows.hip", "gemv_w8a8.hip", "gemm_w8a8_mfma.hip", "w4a16.hip"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the HIP toolchain is required to build opentars_amd")
+
+
+def flags() -> list[str]:
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wall", "-Wno-unused-function", "-I", str(PKG.parent / "include")]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into one shared library next to this file (always rebuilds)."""
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *flags(), *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+    if err.strip() and verbose:
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,280 @@
+// The C ABI of libopentars_amd.so (include/opentars_amd.h): argument checks, then dispatch.
+//
+// Checks follow the golden model's order for a GEMM descriptor (tars_mini/golden.py:59-169):
+// field values (E_FIELD) before shapes and alignment (E_ALIGN) before extents (E_RANGE), then
+// the output-overlaps-input refusal (golden.py:473-479, a ContractError there). All checks run on
+// the host before anything is enqueued, so a failing call writes nothing.
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/opentars_amd.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+int g_w8a8_path = 0;  // 0 auto, 1 GEMV family, 2 MFMA family
+
+int fail(int code, const char* what) {
+  g_last_error = what;
+  return code;
+}
+
+struct Span {
+  uintptr_t lo, hi;  // [lo, hi)
+};
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Row segments of a strided matrix: rows of `row_bytes` every `ld` bytes.
+std::vector<Span> rows(const void* base, int64_t ld, int64_t nrows, int64_t row_bytes) {
+  std::vector<Span> v;
+  v.reserve(static_cast<size_t>(nrows));
+  const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+  for (int64_t r = 0; r < nrows; ++r) v.push_back({b + static_cast<uintptr_t>(r * ld), b + static_cast<uintptr_t>(r * ld + row_bytes)});
+  return v;
+}
+
+std::vector<Span> one(const void* base, int64_t bytes) {
+  const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+  return {{b, b + static_cast<uintptr_t>(bytes)}};
+}
+
+// Whether any input segment intersects any output segment (outputs ascending and disjoint).
+bool overlaps(const std::vector<Span>& in, const std::vector<Span>& out) {
+  for (const Span& s : in) {
+    auto it = std::upper_bound(out.begin(), out.end(), s.lo,
+                               [](uintptr_t lo, const Span& o) { return lo < o.hi; });
+    if (it != out.end() && it->lo < s.hi) return true;
+  }
+  return false;
+}
+
+// Extent check: ld * (rows - 1) + row_bytes stays inside the address space.
+bool extent_ok(const void* base, int64_t ld, int64_t nrows, int64_t row_bytes) {
+  if (nrows <= 0) return true;
+  const unsigned __int128 end = static_cast<unsigned __int128>(reinterpret_cast<uintptr_t>(base)) +
+                                static_cast<unsigned __int128>(ld) * static_cast<unsigned __int128>(nrows - 1) +
+                                static_cast<unsigned __int128>(row_bytes);
+  return end <= static_cast<unsigned __int128>(UINTPTR_MAX);
+}
+
+int esize(int out) { return out == TARS_OUT_FP32 ? 4 : out == TARS_OUT_BF16 ? 2 : 1; }
+
+int check_epilogue(int act, int out, uint32_t out_scale_bits) {
+  if (act < 0 || act > 7) return fail(TARS_E_FIELD, "act must be 0..7");
+  if (out != TARS_OUT_FP32 && out != TARS_OUT_BF16 && out != TARS_OUT_INT8)
+    return fail(TARS_E_FIELD, "out must be FP32, BF16 or INT8 (FP16 is not a GEMM output)");
+  if (out != TARS_OUT_INT8 && out_scale_bits != 0)
+    return fail(TARS_E_FIELD, "out_scale is only meaningful for INT8 output");
+  return TARS_OK;
+}
+
+int launched(hipError_t e) {
+  if (e != hipSuccess) {
+    g_last_error = std::string("HIP launch failed: ") + hipGetErrorString(e);
+    return TARS_E_DEVICE;
+  }
+  return TARS_OK;
+}
+
+float f32_of(uint32_t b) {
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tars_version(void) { return "opentars_amd 0.1.0 gfx950"; }
+
+const char* tars_last_error(void) { return g_last_error.c_str(); }
+
+int tars_set_w8a8_path(int path) {
+  const int prev = g_w8a8_path;
+  g_w8a8_path = (path >= 0 && path <= 2) ? path : 0;
+  return prev;
+}
+
+int tars_quant_rows(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s, int32_t M,
+                    int32_t K, void* stream) {
+  g_last_error.clear();
+  if (!x || !q || !s) return fail(TARS_E_ARG, "NULL pointer");
+  if (M <= 0 || K <= 0 || K % 16) return fail(TARS_E_ALIGN, "M >= 1, K >= 16 and K % 16 == 0");
+  if (lda == 0) lda = 4LL * K;
+  if (ldq == 0) ldq = K;
+  if (lda < 4LL * K || lda % 16 || ldq < K || ldq % 16)
+    return fail(TARS_E_ALIGN, "strides must be multiples of 16 holding a row");
+  if (!aligned(x, 16) || !aligned(q, 16) || !aligned(s, 16)) return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+  if (!extent_ok(x, lda, M, 4LL * K) || !extent_ok(q, ldq, M, K)) return fail(TARS_E_RANGE, "extent overflows");
+  const auto xin = rows(x, lda, M, 4LL * K);
+  const auto qout = rows(q, ldq, M, K);
+  const auto sout = one(s, 4LL * M);
+  if (overlaps(xin, qout) || overlaps(xin, sout) || overlaps(sout, qout))
+    return fail(TARS_E_OVERLAP, "an output overlaps an input");
+  tars::QuantArgs a{x, lda, q, ldq, s, M, K};
+  return launched(tars::launch_quant_rows(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_gemm_w8a8(const int8_t* A, int64_t lda, const float* srow, const int8_t* W,
+                   const float* scol, int32_t scol_count, const float* bias, void* Y, int64_t ldy,
+                   int32_t M, int32_t N, int32_t K, int32_t act, int32_t out,
+                   uint32_t out_scale_bits, void* stream) {
+  g_last_error.clear();
+  if (!A || !W || !scol || !Y) return fail(TARS_E_ARG, "NULL pointer");
+  if (int rc = check_epilogue(act, out, out_scale_bits)) return rc;
+  if (scol_count != N && !(scol_count == 1 && srow == nullptr))
+    return fail(TARS_E_FIELD, "scol_count must be N (or 1 without row scales)");
+  if (K > 65535) return fail(TARS_E_FIELD, "K must fit the 16-bit field (|acc| < 2^31)");
+  if (M <= 0 || N <= 0 || N % 16 || K <= 0 || K % 16) return fail(TARS_E_ALIGN, "M, N, K >= 1; N % 16 == 0; K % 16 == 0");
+  const int64_t yrow = static_cast<int64_t>(N) * esize(out);
+  if (lda == 0) lda = K;
+  if (ldy == 0) ldy = yrow;
+  if (lda < K || lda % 16 || ldy < yrow || ldy % 16) return fail(TARS_E_ALIGN, "strides must be multiples of 16 holding a row");
+  if (!aligned(A, 16) || !aligned(W, 16) || !aligned(scol, 16) || !aligned(Y, 16) ||
+      (srow && !aligned(srow, 16)) || (bias && !aligned(bias, 16)))
+    return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+  if (!extent_ok(A, lda, M, K) || !extent_ok(W, K, N, K) || !extent_ok(Y, ldy, M, yrow))
+    return fail(TARS_E_RANGE, "extent overflows");
+  const auto yout = rows(Y, ldy, M, yrow);
+  if (overlaps(rows(A, lda, M, K), yout) || overlaps(one(W, static_cast<int64_t>(N) * K), yout) ||
+      overlaps(one(scol, 4LL * scol_count), yout) || (srow && overlaps(one(srow, 4LL * M), yout)) ||
+      (bias && overlaps(one(bias, 4LL * N), yout)))
+    return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::W8A8Args a{};
+  a.A = A;
+  a.lda = lda;
+  a.W = W;
+  a.epi = tars::RowColEpilogue{srow, scol, scol_count == 1 && N != 1 ? 1 : 0, bias, act, out,
+                               f32_of(out_scale_bits)};
+  a.Y = Y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  const bool gemv = g_w8a8_path == 1 || (g_w8a8_path == 0 && M == 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return launched(gemv ? tars::launch_gemv_w8a8(a, s) : tars::launch_gemm_w8a8_mfma(a, s));
+}
+
+int tars_gemm_w8a8_ksplit(const int8_t* A, int64_t lda, const float* srow,
+                          const int8_t* const* W_blocks, const int32_t* K_blocks, int32_t nblocks,
+                          const float* scol, float* Y, int64_t ldy, int32_t M, int32_t N,
+                          void* stream) {
+  g_last_error.clear();
+  if (!A || !scol || !Y || !W_blocks || !K_blocks) return fail(TARS_E_ARG, "NULL pointer");
+  if (nblocks < 1 || nblocks > tars::kMaxBlocks) return fail(TARS_E_ARG, "1 <= nblocks <= 8");
+  int64_t ktot = 0;
+  for (int i = 0; i < nblocks; ++i) {
+    if (!W_blocks[i]) return fail(TARS_E_ARG, "NULL weight block");
+    if (K_blocks[i] > 65535) return fail(TARS_E_FIELD, "block K must fit the 16-bit field");
+    if (K_blocks[i] <= 0 || K_blocks[i] % 16) return fail(TARS_E_ALIGN, "block K >= 16 and % 16 == 0");
+    if (!aligned(W_blocks[i], 16)) return fail(TARS_E_ALIGN, "weight blocks must be 16-byte aligned");
+    ktot += K_blocks[i];
+  }
+  if (M <= 0 || N <= 0 || N % 16) return fail(TARS_E_ALIGN, "M, N >= 1; N % 16 == 0");
+  if (lda == 0) lda = ktot;
+  if (ldy == 0) ldy = 4LL * N;
+  if (lda < ktot || lda % 16 || ldy < 4LL * N || ldy % 16) return fail(TARS_E_ALIGN, "strides must be multiples of 16 holding a row");
+  if (!aligned(A, 16) || !aligned(scol, 16) || !aligned(Y, 16) || (srow && !aligned(srow, 16)))
+    return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+  if (!extent_ok(A, lda, M, ktot) || !extent_ok(Y, ldy, M, 4LL * N)) return fail(TARS_E_RANGE, "extent overflows");
+  const auto yout = rows(Y, ldy, M, 4LL * N);
+  bool ov = overlaps(rows(A, lda, M, ktot), yout) || overlaps(one(scol, 4LL * N), yout) ||
+            (srow && overlaps(one(srow, 4LL * M), yout));
+  for (int i = 0; i < nblocks && !ov; ++i) ov = overlaps(one(W_blocks[i], static_cast<int64_t>(N) * K_blocks[i]), yout);
+  if (ov) return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::KSplitArgs a{};
+  a.A = A;
+  a.lda = lda;
+  a.srow = srow;
+  a.scol = scol;
+  int koff = 0;
+  for (int i = 0; i < nblocks; ++i) {
+    a.W[i] = W_blocks[i];
+    a.K[i] = K_blocks[i];
+    a.koff[i] = koff;
+    koff += K_blocks[i];
+  }
+  a.nblocks = nblocks;
+  a.Y = Y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  const bool gemv = g_w8a8_path == 1 || (g_w8a8_path == 0 && M == 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return launched(gemv ? tars::launch_gemv_w8a8_ksplit(a, s) : tars::launch_gemm_w8a8_ksplit_mfma(a, s));
+}
+
+int tars_align_w4(const void* x, int64_t lda, int32_t a_dtype, int16_t* q, int64_t ldq,
+                  float* scales, int64_t lds, int32_t M, int32_t K, void* stream) {
+  g_last_error.clear();
+  if (!x || !q || !scales) return fail(TARS_E_ARG, "NULL pointer");
+  if (a_dtype != TARS_DT_FP32 && a_dtype != TARS_DT_BF16) return fail(TARS_E_FIELD, "a_dtype must be FP32 or BF16");
+  if (M <= 0 || K <= 0 || K % 128) return fail(TARS_E_ALIGN, "M >= 1 and K a nonzero multiple of 128");
+  const int64_t xrow = static_cast<int64_t>(K) * (a_dtype == TARS_DT_FP32 ? 4 : 2);
+  const int64_t srow_bytes = 4LL * (K / 128);
+  if (lda == 0) lda = xrow;
+  if (ldq == 0) ldq = 2LL * K;
+  if (lds == 0) lds = srow_bytes;
+  if (lda < xrow || lda % 16 || ldq < 2LL * K || ldq % 16 || lds < srow_bytes || lds % 4)
+    return fail(TARS_E_ALIGN, "strides must hold a row (x and q multiples of 16, scales of 4)");
+  if (!aligned(x, 16) || !aligned(q, 16) || !aligned(scales, 4)) return fail(TARS_E_ALIGN, "pointer alignment");
+  if (!extent_ok(x, lda, M, xrow) || !extent_ok(q, ldq, M, 2LL * K) || !extent_ok(scales, lds, M, srow_bytes))
+    return fail(TARS_E_RANGE, "extent overflows");
+  const auto xin = rows(x, lda, M, xrow);
+  const auto qout = rows(q, ldq, M, 2LL * K);
+  const auto sout = rows(scales, lds, M, srow_bytes);
+  if (overlaps(xin, qout) || overlaps(xin, sout) || overlaps(sout, qout))
+    return fail(TARS_E_OVERLAP, "an output overlaps an input");
+  tars::AlignArgs a{x, lda, a_dtype == TARS_DT_BF16 ? 1 : 0, q, ldq, scales, lds, M, K};
+  return launched(tars::launch_align_w4(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_gemm_w4a16(const void* x, int64_t lda, int32_t a_dtype, const uint8_t* Wp,
+                    const uint16_t* ws, const float* bias, void* Y, int64_t ldy, int32_t M,
+                    int32_t N, int32_t K, int32_t act, int32_t out, uint32_t out_scale_bits,
+                    void* stream) {
+  g_last_error.clear();
+  if (!x || !Wp || !ws || !Y) return fail(TARS_E_ARG, "NULL pointer");
+  if (a_dtype != TARS_DT_FP32 && a_dtype != TARS_DT_BF16) return fail(TARS_E_FIELD, "a_dtype must be FP32 or BF16");
+  if (int rc = check_epilogue(act, out, out_scale_bits)) return rc;
+  if (M <= 0 || N <= 0 || N % 16 || K <= 0 || K % 16) return fail(TARS_E_ALIGN, "M, N, K >= 1; N % 16 == 0; K % 16 == 0");
+  if (K < 256 || K % 256 || K > 8192 || !aligned(Wp, 128))
+    return fail(TARS_E_ALIGN, "W4A16: K % 256 == 0, 256 <= K <= 8192, weights 128-byte aligned");
+  const int64_t xrow = static_cast<int64_t>(K) * (a_dtype == TARS_DT_FP32 ? 4 : 2);
+  const int64_t yrow = static_cast<int64_t>(N) * esize(out);
+  if (lda == 0) lda = xrow;
+  if (ldy == 0) ldy = yrow;
+  if (lda < xrow || lda % 16 || ldy < yrow || ldy % 16) return fail(TARS_E_ALIGN, "strides must be multiples of 16 holding a row");
+  if (!aligned(x, 16) || !aligned(ws, 16) || !aligned(Y, 16) || (bias && !aligned(bias, 16)))
+    return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+  if (!extent_ok(x, lda, M, xrow) || !extent_ok(Y, ldy, M, yrow)) return fail(TARS_E_RANGE, "extent overflows");
+  const auto yout = rows(Y, ldy, M, yrow);
+  if (overlaps(rows(x, lda, M, xrow), yout) || overlaps(one(Wp, static_cast<int64_t>(N) * K / 2), yout) ||
+      overlaps(one(ws, 2LL * N * (K / 128)), yout) || (bias && overlaps(one(bias, 4LL * N), yout)))
+    return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::W4Args a{};
+  a.x = x;
+  a.lda = lda;
+  a.bf16 = a_dtype == TARS_DT_BF16 ? 1 : 0;
+  a.Wp = Wp;
+  a.ws = ws;
+  a.bias = bias;
+  a.act = act;
+  a.out = out;
+  a.out_scale = f32_of(out_scale_bits);
+  a.Y = Y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  return launched(tars::launch_gemv_w4a16(a, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

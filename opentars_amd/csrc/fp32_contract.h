@@ -1,0 +1,215 @@
+// Device-side fp32 steps of the golden model's numeric contract (tars_mini/numerics.py).
+//
+// Every step rounds once to nearest-even with fp32 subnormals handled in hardware (the kernels'
+// fp32 denorm mode is "preserve"), then flushes a subnormal input or result to a zero of the same
+// sign with a bit test, and replaces any NaN with 0x7FC00000. That is exactly numpy's float32
+// multiply/add followed by the reference's ftz()/canon(). The library is compiled with
+// -ffp-contract=off, so no multiply and add pair is ever fused.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tars {
+
+constexpr uint32_t kSign = 0x80000000u;
+constexpr uint32_t kExpo = 0x7F800000u;
+constexpr uint32_t kMant = 0x007FFFFFu;
+constexpr uint32_t kCanonNaN = 0x7FC00000u;
+
+__device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ float ffrom(uint32_t b) { return __uint_as_float(b); }
+
+__device__ __forceinline__ bool is_nan(float x) { return (fbits(x) & 0x7FFFFFFFu) > kExpo; }
+
+// numerics.py:26-31
+__device__ __forceinline__ float ftz(float x) {
+  const uint32_t b = fbits(x);
+  return (b & kExpo) ? x : ffrom(b & kSign);
+}
+
+// numerics.py:34-37
+__device__ __forceinline__ float canon(float x) { return is_nan(x) ? ffrom(kCanonNaN) : x; }
+
+// numerics.py:40-47: one rounded operation, FTZ in and out, canonical NaN
+__device__ __forceinline__ float fmul(float a, float b) { return canon(ftz(__fmul_rn(ftz(a), ftz(b)))); }
+__device__ __forceinline__ float fadd(float a, float b) { return canon(ftz(__fadd_rn(ftz(a), ftz(b)))); }
+
+// numerics.py:50-52: int32 -> fp32 round-to-nearest-even (v_cvt_f32_i32)
+__device__ __forceinline__ float i2f(int32_t i) { return static_cast<float>(i); }
+
+// numerics.py:111-113, 265-267
+__device__ __forceinline__ float fneg(float x) { return ffrom(fbits(x) ^ kSign); }
+__device__ __forceinline__ float fabs_c(float x) { return ffrom(fbits(ftz(x)) & 0x7FFFFFFFu); }
+
+// The constants of the reference's fixed sequences, by encoding (numerics.py:116-123, 234-238).
+constexpr uint32_t kOne = 0x3F800000u, kTwo = 0x40000000u, kHalf = 0x3F000000u;
+constexpr uint32_t kLog2e = 0x3FB8AA3Bu, kNegLn2Hi = 0xBF317200u, kNegLn2Lo = 0xB5BFBE8Eu;
+constexpr uint32_t kExpHi = 0x42B20000u /* 89 */, kExpLo = 0xC2D00000u /* -104 */;
+constexpr uint32_t kRecipSeed = 0x7EF311C7u;
+constexpr uint32_t kGeluA = 0x3D372713u, kGeluC = 0x3F4C422Au;
+constexpr uint32_t kSoftplusHi = 0x41A00000u /* 20 */;
+constexpr uint32_t kQ127 = 0x42FE0000u, kInv127 = 0x3C010204u;
+
+// Positive normal y with e added to its biased exponent: >= 255 -> +inf, <= 0 -> +0; the sign bit
+// is not carried (numerics.py:126-132).
+__device__ __forceinline__ float add_to_exponent(float y, int e) {
+  const uint32_t yb = fbits(y);
+  const int field = static_cast<int>((yb >> 23) & 0xFFu) + e;
+  if (field >= 255) return ffrom(kExpo);
+  if (field <= 0) return 0.0f;
+  return ffrom((static_cast<uint32_t>(field) << 23) | (yb & kMant));
+}
+
+// 1/x: seed from the magic constant, three correction-form Newton steps, exponent surgery
+// (numerics.py:153-168).
+__device__ __forceinline__ float recip_f(float x) {
+  const uint32_t xb = fbits(ftz(x));
+  const uint32_t sgn = xb & kSign, mag = xb & 0x7FFFFFFFu;
+  if (mag > kExpo) return ffrom(kCanonNaN);
+  if (mag == 0) return ffrom(sgn | kExpo);
+  if (mag == kExpo) return ffrom(sgn);
+  const uint32_t mb = (mag & kMant) | (127u << 23);
+  const float m = ffrom(mb);
+  float y = ffrom(kRecipSeed - mb);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float err = fadd(ffrom(kOne), fneg(fmul(m, y)));
+    y = fadd(y, fmul(y, err));
+  }
+  return ffrom(fbits(add_to_exponent(y, 127 - static_cast<int>(mag >> 23))) | sgn);
+}
+
+// e^x (numerics.py:135-150).
+__device__ __forceinline__ float exp_f(float x) {
+  x = ftz(x);
+  if (is_nan(x)) return ffrom(kCanonNaN);
+  float n = rintf(fmul(x, ffrom(kLog2e)));
+  n = fminf(fmaxf(n, -200.0f), 200.0f);
+  const float r = fadd(fadd(x, fmul(n, ffrom(kNegLn2Hi))), fmul(n, ffrom(kNegLn2Lo)));
+  const uint32_t coeffs[6] = {0x3C088889u, 0x3D2AAAABu, 0x3E2AAAABu, 0x3F000000u, 0x3F800000u,
+                              0x3F800000u};
+  float p = ffrom(0x3AB60B61u);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) p = fadd(fmul(p, r), ffrom(coeffs[i]));
+  float y = add_to_exponent(p, static_cast<int>(n));
+  if (x >= ffrom(kExpHi)) y = ffrom(kExpo);
+  else if (x <= ffrom(kExpLo)) y = 0.0f;
+  return canon(y);
+}
+
+__device__ __forceinline__ float relu_plain(float x) { return x > 0.0f ? x : 0.0f; }
+
+// numerics.py:241-244
+__device__ __forceinline__ float sigmoid_f(float x) {
+  x = ftz(x);
+  return recip_f(fadd(ffrom(kOne), exp_f(fneg(x))));
+}
+
+// numerics.py:204-207
+__device__ __forceinline__ float silu_f(float x) {
+  x = ftz(x);
+  return fmul(x, recip_f(fadd(ffrom(kOne), exp_f(fneg(x)))));
+}
+
+// numerics.py:194-201
+__device__ __forceinline__ float gelu_f(float x) {
+  x = ftz(x);
+  const float cube = fmul(fmul(x, x), x);
+  const float u = fmul(ffrom(kGeluC), fadd(x, fmul(ffrom(kGeluA), cube)));
+  const float t = fadd(ffrom(kOne), fneg(fmul(ffrom(kTwo), recip_f(fadd(exp_f(fmul(ffrom(kTwo), u)), ffrom(kOne))))));
+  return fmul(fmul(ffrom(kHalf), x), fadd(ffrom(kOne), t));
+}
+
+// numerics.py:247-262
+__device__ __forceinline__ float softplus_f(float x) {
+  x = ftz(x);
+  if (is_nan(x)) return ffrom(kCanonNaN);
+  const float t = exp_f(fneg(fabs_c(x)));
+  const float s = fmul(t, recip_f(fadd(t, ffrom(kTwo))));
+  const float z = fmul(s, s);
+  const uint32_t coeffs[8] = {0x3D888889u, 0x3D9D89D9u, 0x3DBA2E8Cu, 0x3DE38E39u,
+                              0x3E124925u, 0x3E4CCCCDu, 0x3EAAAAABu, 0x3F800000u};
+  float p = ffrom(0x3D70F0F1u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p = fadd(fmul(p, z), ffrom(coeffs[i]));
+  const float y = fadd(relu_plain(x), fmul(fmul(ffrom(kTwo), s), p));
+  return canon(x > ffrom(kSoftplusHi) ? x : y);
+}
+
+// The epilogue activation by code (numerics.py:210-230).
+__device__ __forceinline__ float act_fn(float x, int act) {
+  x = ftz(x);
+  switch (act) {
+    case 0: return x;
+    case 1: return relu_plain(x);
+    case 2: { const float r = relu_plain(x); return r > 6.0f ? 6.0f : r; }
+    case 3: return gelu_f(x);
+    case 4: return silu_f(x);
+    case 5: return sigmoid_f(x);
+    case 6: return softplus_f(x);
+    default: return exp_f(x);
+  }
+}
+
+// numerics.py:282-286: rint(fmul(x, inv)) ties-to-even, NaN -> 0, clamp to [-127, 127]
+__device__ __forceinline__ int8_t q8(float x, float inv) {
+  float y = fmul(x, inv);
+  if (is_nan(y)) y = 0.0f;
+  y = rintf(y);
+  y = fminf(fmaxf(y, -127.0f), 127.0f);
+  return static_cast<int8_t>(static_cast<int>(y));
+}
+
+// numerics.py:270-275: FTZ, round-to-nearest-even to the top 16 bits, NaN -> 0x7FC0
+__device__ __forceinline__ uint16_t to_bf16_bits(float x) {
+  const uint32_t b = fbits(ftz(x));
+  if ((b & 0x7FFFFFFFu) > kExpo) return 0x7FC0u;
+  return static_cast<uint16_t>((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+// numerics.py:21-23: binary16 bits -> fp32, exact for subnormals, canonical NaN
+__device__ __forceinline__ float from_fp16_bits(uint32_t h) {
+  const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, f = h & 0x3FFu;
+  if (e == 31) return ffrom(f ? kCanonNaN : (s | kExpo));
+  if (e == 0) {
+    // f * 2^-24: exact (f < 2^10, the product is a normal fp32)
+    const float v = static_cast<float>(f) * 5.9604644775390625e-08f;
+    return ffrom(fbits(v) | s);
+  }
+  return ffrom(s | ((e + 112u) << 23) | (f << 13));
+}
+
+// Stores one epilogue result in the output format (golden.py:273-280).
+__device__ __forceinline__ void store_out(void* Y, int64_t byte_row, int n, int out, float y,
+                                          float out_scale) {
+  char* row = static_cast<char*>(Y) + byte_row;
+  if (out == 0) {
+    reinterpret_cast<float*>(row)[n] = ftz(y);
+  } else if (out == 1) {
+    reinterpret_cast<uint16_t*>(row)[n] = to_bf16_bits(y);
+  } else {
+    reinterpret_cast<int8_t*>(row)[n] = q8(y, out_scale);
+  }
+}
+
+// The W8A8 epilogue after the exact integer sum (golden.py:340-349).
+struct RowColEpilogue {
+  const float* srow;   // nullptr: no row scale (QM_CHANNEL / QM_TENSOR)
+  const float* scol;
+  int scol_per_tensor; // 1: scol[0] for every column (QM_TENSOR)
+  const float* bias;   // nullptr: none
+  int act;
+  int out;
+  float out_scale;
+
+  __device__ __forceinline__ float value(int32_t acc, int m, int n) const {
+    float y = i2f(acc);
+    if (srow) y = fmul(y, srow[m]);
+    y = fmul(y, scol[scol_per_tensor ? 0 : n]);
+    if (bias) y = fadd(y, bias[n]);
+    return act_fn(y, act);
+  }
+};
+
+}  // namespace tars

@@ -1,0 +1,156 @@
+"""The C ABI boundary on a CPU-only host: the library loads, exports what the header declares, and
+rejects bad arguments with the contract's codes before it touches a device.
+
+Every call below fails validation by construction; the placeholder addresses are never
+dereferenced and no kernel is launched (a call that would pass validation is never made here)."""
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from opentars_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "opentars_amd.h"
+
+P = 0x7F0000000000          # a 16-byte (and 128-byte) aligned placeholder address, never dereferenced
+MB = 1 << 20
+
+
+def declared() -> list[str]:
+    return re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(tars_\w+)\s*\(", HEADER.read_text(), re.M)
+
+
+def test_header_declares_the_entry_points():
+    names = declared()
+    assert set(names) == set(_lib.SIGNATURES), names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert _lib.version().startswith("opentars_amd")
+
+
+def status_codes_match_header():
+    text = HEADER.read_text()
+    return {m.group(1): int(m.group(2)) for m in re.finditer(r"#define TARS_(E_\w+|OK)\s+\(?(-?\d+)\)?", text)}
+
+
+def test_status_codes_match_header():
+    codes = status_codes_match_header()
+    assert codes["OK"] == _lib.OK and codes["E_FIELD"] == _lib.E_FIELD and codes["E_ALIGN"] == _lib.E_ALIGN
+    assert codes["E_RANGE"] == _lib.E_RANGE and codes["E_OVERLAP"] == _lib.E_OVERLAP
+    assert codes["E_ARG"] == _lib.E_ARG and codes["E_DEVICE"] == _lib.E_DEVICE
+    # the contract's own numbering (tars_mini/contract.py:108): E_FIELD 6, E_ALIGN 7, E_RANGE 8
+    assert (_lib.E_FIELD, _lib.E_ALIGN, _lib.E_RANGE) == (-6, -7, -8)
+
+
+def w8(**kw):
+    """A tars_gemm_w8a8 call with a valid-looking layout overridden by kw (must fail validation)."""
+    a = dict(A=P, lda=0, srow=P + 1 * MB, W=P + 2 * MB, scol=P + 3 * MB, bias=None,
+             Y=P + 4 * MB, ldy=0, M=1, N=64, K=1024, act=0, out=0, osb=0)
+    a.update(kw)
+    a.setdefault("scol_count", a["N"])
+    rc = _lib.lib().tars_gemm_w8a8(a["A"], a["lda"], a["srow"], a["W"], a["scol"], a["scol_count"], a["bias"],
+                                   a["Y"], a["ldy"], a["M"], a["N"], a["K"], a["act"], a["out"], a["osb"], None)
+    assert rc != _lib.OK, "test bug: this call would have launched"
+    return rc
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(act=8), _lib.E_FIELD),
+    (dict(out=3), _lib.E_FIELD),                         # FP16 is not a GEMM output (golden.py:90)
+    (dict(osb=0x40A00000), _lib.E_FIELD),                # OUT_SCALE without INT8 (golden.py:92)
+    (dict(K=65536 + 16), _lib.E_FIELD),
+    (dict(scol_count=1), _lib.E_FIELD),                  # a row scale needs per-channel scales
+    (dict(N=40), _lib.E_ALIGN),
+    (dict(K=1000), _lib.E_ALIGN),
+    (dict(M=0), _lib.E_ALIGN),
+    (dict(lda=1008), _lib.E_ALIGN),                      # stride must hold a row
+    (dict(lda=1032), _lib.E_ALIGN),                      # and be a multiple of 16
+    (dict(ldy=128), _lib.E_ALIGN),
+    (dict(A=P + 4), _lib.E_ALIGN),
+    (dict(srow=P + 1 * MB + 8), _lib.E_ALIGN),
+    (dict(Y=P + 2 * MB), _lib.E_OVERLAP),                # output on the weights
+    (dict(Y=P + 2 * MB + 64 * 1024 - 16), _lib.E_OVERLAP),
+    (dict(Y=P - 128), _lib.E_OVERLAP),                   # output running into A
+    (dict(W=None), _lib.E_ARG),
+    (dict(act=9, N=40), _lib.E_FIELD),                   # E_FIELD is checked before E_ALIGN
+])
+def test_w8a8_validation(kw, code):
+    assert w8(**kw) == code
+    assert _lib.last_error()
+
+
+def test_ksplit_validation():
+    lib = _lib.lib()
+    import ctypes
+    ptrs = (ctypes.c_void_p * 2)(P + 2 * MB, P + 3 * MB)
+
+    def call(ks, n=64, y=P + 6 * MB, nb=2):
+        karr = (ctypes.c_int32 * 2)(*ks)
+        rc = lib.tars_gemm_w8a8_ksplit(P, 0, P + MB, ptrs, karr, nb, P + 5 * MB, y, 0, 1, n, None)
+        assert rc != _lib.OK
+        return rc
+    assert call([4096, 2810]) == _lib.E_ALIGN
+    assert call([4096, 70000]) == _lib.E_FIELD
+    assert call([4096, 2816], n=40) == _lib.E_ALIGN
+    assert call([4096, 2816], nb=9) == _lib.E_ARG
+    assert call([4096, 2816], y=P + 3 * MB) == _lib.E_OVERLAP
+
+
+def test_w4_validation():
+    lib = _lib.lib()
+
+    def call(K=1536, N=64, W=P + 2 * MB, dt=4, act=0, out=0, osb=0, Y=P + 4 * MB, lda=0):
+        rc = lib.tars_gemm_w4a16(P, lda, dt, W, P + 3 * MB, None, Y, 0, 1, N, K, act, out, osb, None)
+        assert rc != _lib.OK
+        return rc
+    assert call(K=384) == _lib.E_ALIGN            # K % 256 (golden.py:145-147)
+    assert call(K=128) == _lib.E_ALIGN
+    assert call(K=8448) == _lib.E_ALIGN           # K <= 8192
+    assert call(W=P + 2 * MB + 64) == _lib.E_ALIGN  # weights on a 128-byte boundary
+    assert call(dt=1) == _lib.E_FIELD             # activations fp32 or bf16 only
+    assert call(out=3) == _lib.E_FIELD
+    assert call(lda=1024) == _lib.E_ALIGN         # 1024 bytes < one fp32 K=1536 row
+    assert call(Y=P + 2 * MB + 512) == _lib.E_OVERLAP
+
+
+def test_quant_and_align_validation():
+    lib = _lib.lib()
+    assert lib.tars_quant_rows(P, 0, P + MB, 0, P + 2 * MB, 1, 1000, None) == _lib.E_ALIGN
+    assert lib.tars_quant_rows(P, 0, P + 16, 0, P + 2 * MB, 1, 1024, None) == _lib.E_OVERLAP
+    assert lib.tars_quant_rows(P, 0, P + MB, 0, P + 2, 1, 1024, None) == _lib.E_ALIGN
+    assert lib.tars_quant_rows(None, 0, P + MB, 0, P + 2 * MB, 1, 1024, None) == _lib.E_ARG
+    assert lib.tars_align_w4(P, 0, 4, P + MB, 0, P + 2 * MB, 0, 1, 200, None) == _lib.E_ALIGN
+    assert lib.tars_align_w4(P, 0, 2, P + MB, 0, P + 2 * MB, 0, 1, 256, None) == _lib.E_FIELD
+    assert lib.tars_align_w4(P, 0, 4, P + 64, 0, P + 2 * MB, 0, 1, 256, None) == _lib.E_OVERLAP
+
+
+def _gfx950_disassembly(tmp_path: Path) -> str:
+    objdump = shutil.which("llvm-objdump") or "/opt/rocm/llvm/bin/llvm-objdump"
+    if not Path(objdump).exists():
+        pytest.skip("llvm-objdump not available")
+    lib = tmp_path / "lib.so"
+    shutil.copy(_lib.LIB_PATH, lib)
+    subprocess.run([objdump, "--offloading", str(lib)], cwd=tmp_path, capture_output=True, check=True)
+    objs = sorted(tmp_path.glob("lib.so.*gfx950"))
+    assert objs, "no gfx950 code object in the library"
+    return "\n".join(subprocess.run([objdump, "-d", "--mcpu=gfx950", str(o)], capture_output=True, text=True,
+                                    check=True).stdout for o in objs)
+
+
+def test_codegen_has_no_fused_or_packed_fp32(tmp_path):
+    """The epilogues must round every multiply and add on its own: the built gfx950 code holds no
+    fused multiply-add and no packed fp32 instruction, and no kernel spills to scratch."""
+    dis = _gfx950_disassembly(tmp_path)
+    forbidden = re.findall(r"\bv_(?:fma|fmac|mad|fmaak|fmamk|mac)_f32\w*|\bv_pk_(?:fma|mul|add)_f32\w*", dis)
+    assert not forbidden, sorted(set(forbidden))
+    assert "scratch_" not in dis
+    assert "v_mfma_i32_16x16x64_i8" in dis and "v_dot4" in dis

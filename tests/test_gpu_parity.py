@@ -1,0 +1,339 @@
+"""Bit-exact parity of the HIP path (through the C ABI) with the CPU oracle and with the vectors the
+reference golden model wrote itself. Needs a gfx950 GPU."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import golden as G
+from oracle import numerics as F
+from opentars_amd import ops
+from opentars_amd.contract import (ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, ACT_SOFTPLUS, OUT_BF16, OUT_FP32,
+                                   OUT_INT8)
+
+pytestmark = pytest.mark.gpu
+
+VEC = np.load(Path(__file__).resolve().parent / "golden" / "ref_vectors.npz")
+f32 = np.float32
+
+
+def cuda(a) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def same(a, b) -> bool:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return a.shape == b.shape and a.tobytes() == b.tobytes()
+
+
+def mismatch(a, b) -> str:
+    a, b = np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8)
+    if a.shape != b.shape:
+        return f"shape {a.shape} vs {b.shape}"
+    idx = np.nonzero(a != b)[0]
+    return f"{idx.size} differing bytes, first at {idx[:8].tolist()}"
+
+
+def w8_inputs(seed: int, M: int, N: int, K: int):
+    """Seeded C1-style operands: int8 weights in [-127, 127], per-channel scales in [1e-3, 1e-2],
+    N(0,1) activations quantized per token by the oracle."""
+    rng = np.random.default_rng(seed)
+    W = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    scol = rng.uniform(1e-3, 1e-2, N).astype(f32)
+    x = rng.normal(0, 1, (M, K)).astype(f32)
+    q, s = F.quant_rows(x)
+    return x, q, s, W, scol, rng
+
+
+def oracle_rowcol_blocked(q, s, W, scol, rows: int = 16384, **kw):
+    """The oracle on row blocks of W (each output element is independent; bounds host memory)."""
+    return np.concatenate([G.gemm_rowcol(q, s, W[i:i + rows], scol[i:i + rows] if scol.size > 1 else scol,
+                                         **({**kw, "bias": kw["bias"][i:i + rows]} if kw.get("bias") is not None else kw))
+                           for i in range(0, W.shape[0], rows)], axis=1)
+
+
+# ------------------------------------------------------------------------------ quant_rows
+@pytest.mark.parametrize("name", ["qr_1x1024", "qr_4x1024", "qr_4x3072", "qr_1x6912", "qr_3x2048", "qr_edge"])
+def test_quant_rows_reference_vectors(name):
+    x = VEC[name + "_x"]
+    q, s = ops.quant_rows(cuda(x))
+    assert same(host(q), VEC[name + "_q"]), mismatch(host(q), VEC[name + "_q"])
+    assert same(host(s), VEC[name + "_s"])
+
+
+@pytest.mark.parametrize("M,K", [(1, 16), (1, 1024), (1, 6912), (4, 3072), (256, 1024), (7, 65520), (3, 4112)])
+def test_quant_rows_seeded(M, K):
+    rng = np.random.default_rng(M * 100003 + K)
+    x = (rng.normal(0, 1, (M, K)) * np.exp2(rng.integers(-60, 60, (M, 1)))).astype(f32)
+    x[0, K // 2] = 0.0
+    q, s = ops.quant_rows(cuda(x))
+    wq, ws = F.quant_rows(x)
+    assert same(host(q), wq) and same(host(s), ws)
+
+
+def test_quant_rows_strided_rows_and_gaps():
+    rng = np.random.default_rng(9)
+    M, K, pad = 5, 1024, 64
+    big = cuda(rng.normal(0, 1, (M, K + pad)).astype(f32))
+    x = big[:, :K]
+    qbuf = torch.full((M, K + 48), 99, dtype=torch.int8, device="cuda")
+    q = qbuf[:, :K]
+    s = torch.empty(M, dtype=torch.float32, device="cuda")
+    ops.quant_rows(x, q=q, s=s)
+    wq, ws = F.quant_rows(host(x).copy())
+    assert same(host(q).copy(), wq) and same(host(s), ws)
+    assert (host(qbuf)[:, K:] == 99).all()
+
+
+# ------------------------------------------------------------------------------ W8A8 GEMV (M = 1)
+@pytest.mark.parametrize("seed", range(5))
+def test_c1_gemv_qwen3_gate_proj(seed):
+    """Config 1: M=1, K=1024, N=3072, bit-exact."""
+    x, q, s, W, scol, _ = w8_inputs(seed, 1, 3072, 1024)
+    qg, sg = ops.quant_rows(cuda(x))
+    assert same(host(qg), q) and same(host(sg), s)
+    y = ops.gemm_rowcol(qg, sg, cuda(W), cuda(scol))
+    want = G.gemm_rowcol(q, s, W, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("K", [16, 32, 48, 112, 496, 784, 1024, 1040, 2048, 2816, 3072, 3456, 4096, 4112, 6912,
+                               8192, 9216, 20000])
+def test_gemv_every_k_shape(K):
+    x, q, s, W, scol, _ = w8_inputs(K, 1, 96, K)
+    y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol))
+    assert same(host(y), G.gemm_rowcol(q, s, W, scol))
+
+
+@pytest.mark.parametrize("path", ["gemv", "mfma"])
+@pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
+                                     (ACT_SOFTPLUS, OUT_INT8), (ACT_GELU, OUT_FP32)])
+def test_epilogue_matrix(path, qm, bias, act, out):
+    """Every scale mode x bias x activation/format (the reference's GEMV test grid), with a huge
+    scale (inf products), a zero activation chunk, and random int8 including -128."""
+    rng = np.random.default_rng(hash((path, qm, bias, act, out)) & 0xFFFF)
+    M, N, K = (1 if path == "gemv" else 3), 48, 16 * int(rng.integers(1, 40))
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    A[:, 16:32] = 0
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
+    sc[N // 2] = 3e30
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32) if bias else None
+    osc = f32(5.0) if out == OUT_INT8 else None
+    prev = ops.set_w8a8_path(path)
+    try:
+        y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc),
+                            None if b is None else cuda(b), act=act, out=out, out_scale=osc)
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+def test_gemv_nan_from_inf_scale_is_canonical():
+    A = np.zeros((1, 16), np.int8)
+    W = np.ones((16, 16), np.int8)
+    y = host(ops.gemm_rowcol(cuda(A), None, cuda(W), cuda(np.array([np.inf], f32))))
+    assert (y.view(np.uint32) == 0x7FC00000).all()
+
+
+def test_worked_example_on_gpu():
+    """The contract document's fused example (tests/test_contract.py:47-84): element (0, 1) is bf16 0x3F16."""
+    rng = np.random.default_rng(2026)
+    A = rng.integers(-128, 128, (2, 32), dtype=np.int8)
+    W = rng.integers(-128, 128, (16, 32), dtype=np.int8)
+    S = (rng.uniform(0.5, 2.0, 16) / 4096).astype(f32)
+    B = rng.uniform(-8, 8, 16).astype(f32)
+    for path in ("gemv", "mfma"):
+        prev = ops.set_w8a8_path(path)
+        try:
+            y = host(ops.gemm_rowcol(cuda(A), None, cuda(W), cuda(S), cuda(B), act=ACT_RELU, out=OUT_BF16))
+        finally:
+            ops.set_w8a8_path(prev)
+        assert y[0, 1] == 0x3F16
+        assert same(y, G.gemm_rowcol(A, None, W, S, B, act=ACT_RELU, out=OUT_BF16))
+
+
+def test_lm_head_full_size():
+    """The Qwen3-0.6B lm_head at full size in one launch: K=1024, N=151936, bit-exact with the
+    oracle (which the reference computes as 4 blocks of 37984 rows; elements are independent)."""
+    x, q, s, W, scol, _ = w8_inputs(77, 1, 151936, 1024)
+    y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol))
+    want = oracle_rowcol_blocked(q, s, W, scol, rows=37984)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+def test_strided_rows_and_untouched_gaps():
+    """Strided A and Y rows give the dense result and leave the gaps untouched (test_golden.py:261-289)."""
+    rng = np.random.default_rng(21)
+    for path, M in (("gemv", 1), ("gemv", 3), ("mfma", 3), ("mfma", 40)):
+        N, K = 64, 272
+        A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+        W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+        sc = rng.uniform(1e-3, 1e-2, N).astype(f32)
+        sr = rng.uniform(0.5, 2, M).astype(f32)
+        abig = cuda(np.concatenate([A, np.zeros((M, 48), np.int8)], axis=1))
+        ybig = torch.full((M, N + 12), -7.0, dtype=torch.float32, device="cuda")
+        prev = ops.set_w8a8_path(path)
+        try:
+            ops.gemm_rowcol(abig[:, :K], cuda(sr), cuda(W), cuda(sc), y=ybig[:, :N])
+        finally:
+            ops.set_w8a8_path(prev)
+        yb = host(ybig)
+        assert same(yb[:, :N].copy(), G.gemm_rowcol(A, sr, W, sc)), (path, M)
+        assert (yb[:, N:] == -7.0).all()
+
+
+def test_overlap_is_refused_and_nothing_is_written():
+    rng = np.random.default_rng(3)
+    buf = torch.zeros(64 * 1024 + 4096, dtype=torch.int8, device="cuda")
+    W = buf[:16 * 1024].view(16, 1024)
+    W.copy_(cuda(rng.integers(-128, 128, (16, 1024), dtype=np.int8)))
+    q = cuda(rng.integers(-128, 128, (1, 1024), dtype=np.int8))
+    before = host(buf).copy()
+    y = buf[1024:1024 + 64].view(torch.float32).view(1, 16)          # inside W
+    with pytest.raises(ops.ContractError):
+        ops.gemm_rowcol(q, None, W, cuda(np.ones(16, f32)), y=y)
+    assert same(host(buf), before)
+
+
+# ------------------------------------------------------------------------------ K split (config 2)
+@pytest.mark.parametrize("split", [[3456, 3456], [4096, 2816], [2304, 2304, 2304]])
+@pytest.mark.parametrize("M", [1, 4])
+def test_c2_gemma3_down_ksplit(split, M):
+    """Config 2: Gemma-3-1B down_proj, K=6912 N=1152 as K blocks sharing the per-channel scales;
+    the per-block partials add in fp32 in block order. Both the reference's 3456+3456 and the
+    4096+2816 split, bit-exact, and the two splits differ."""
+    x, q, s, W, scol, _ = w8_inputs(sum(split) + M, M, 1152, 6912)
+    blocks, c0 = [], 0
+    for k in split:
+        blocks.append(np.ascontiguousarray(W[:, c0:c0 + k]))
+        c0 += k
+    qg, sg = ops.quant_rows(cuda(x))
+    y = ops.gemm_rowcol_ksplit(qg, sg, [cuda(b) for b in blocks], cuda(scol))
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+def test_ksplit_both_paths_agree():
+    x, q, s, W, scol, _ = w8_inputs(5, 2, 256, 6912)
+    blocks = [np.ascontiguousarray(W[:, :4096]), np.ascontiguousarray(W[:, 4096:])]
+    outs = []
+    for path in ("gemv", "mfma"):
+        prev = ops.set_w8a8_path(path)
+        try:
+            outs.append(host(ops.gemm_rowcol_ksplit(cuda(q), cuda(s), [cuda(b) for b in blocks], cuda(scol))))
+        finally:
+            ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(outs[0], want) and same(outs[1], want)
+
+
+# ------------------------------------------------------------------------------ prefill GEMM (config 4)
+@pytest.mark.parametrize("M", [4, 256])
+@pytest.mark.parametrize("K,N", [(1024, 3072), (3072, 1024)])
+def test_c4_prefill_gemm(M, K, N):
+    x, q, s, W, scol, _ = w8_inputs(M * 7 + K, M, N, K)
+    qg, sg = ops.quant_rows(cuda(x))
+    assert same(host(qg), q) and same(host(sg), s)
+    y = ops.gemm_rowcol(qg, sg, cuda(W), cuda(scol))
+    want = G.gemm_rowcol(q, s, W, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("M", [2, 3, 5, 16, 17, 31, 33, 64, 100, 300])
+@pytest.mark.parametrize("K", [64, 1040, 5000 // 16 * 16])
+def test_mfma_ragged_m_and_k(M, K):
+    x, q, s, W, scol, rng = w8_inputs(M * 1000 + K, M, 80, K)
+    b = rng.normal(0, 1, 80).astype(f32)
+    y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol), cuda(b), act=ACT_SILU)
+    want = G.gemm_rowcol(q, s, W, scol, b, act=ACT_SILU)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+def test_gemv_family_for_prefill_rows_matches():
+    x, q, s, W, scol, _ = w8_inputs(11, 4, 3072, 1024)
+    prev = ops.set_w8a8_path("gemv")
+    try:
+        y = host(ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol)))
+    finally:
+        ops.set_w8a8_path(prev)
+    assert same(y, G.gemm_rowcol(q, s, W, scol))
+
+
+# ------------------------------------------------------------------------------ W4A16 (config 5)
+@pytest.mark.parametrize("i", range(8))
+def test_w4_reference_vectors(i):
+    k = f"w4_{i}"
+    m, n, K, half, bias, act, fmt, osb = (int(v) for v in VEC[k + "_meta"])
+    x = VEC[k + "_x"]
+    y = ops.gemm_w4(cuda(x), cuda(VEC[k + "_wp"]), cuda(VEC[k + "_ws"]),
+                    bias=cuda(VEC[k + "_bias"]) if bias else None, act=act, out=fmt,
+                    out_scale=np.array([osb], np.uint32).view(f32)[0], x_is_bf16=bool(half))
+    got = np.ascontiguousarray(host(y)).view(np.uint8).ravel()
+    assert got.tobytes() == VEC[k + "_y"].tobytes(), mismatch(got, VEC[k + "_y"])
+
+
+def w4_inputs(seed: int, M: int, N: int, K: int):
+    rng = np.random.default_rng(seed)
+    nib = rng.integers(-8, 8, (N, K))
+    Wp = G.pack_int4(nib)
+    ws = rng.uniform(1e-3, 1e-2, (N, K // 128)).astype(np.float16).view(np.uint16)
+    x = rng.normal(0, 1, (M, K)).astype(f32)
+    return x, Wp, ws, rng
+
+
+@pytest.mark.parametrize("K,N", [(1536, 12288), (6144, 1536)])
+@pytest.mark.parametrize("seed", range(2))
+def test_c5_w4a16_gemma4(K, N, seed):
+    """Config 5: Gemma-4-E2B-style W4A16 GEMV, bit-exact (no tolerance needed)."""
+    x, Wp, ws, _ = w4_inputs(seed * 31 + K, 1, N, K)
+    y = ops.gemm_w4(cuda(x), cuda(Wp), cuda(ws))
+    want = G.gemm_w4(x, Wp, ws)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("K", [256, 512, 768, 1024, 2048, 4096, 8192])
+@pytest.mark.parametrize("M", [1, 3])
+def test_w4_shapes_bf16_bias_act(K, M):
+    x, Wp, ws, rng = w4_inputs(K + M, M, 48, K)
+    x = (x * np.exp2(rng.integers(-30, 30, (M, K // 128, 1))).repeat(128, axis=2).reshape(M, K)).astype(f32)
+    xb = F.to_bf16_bits(x)
+    b = rng.normal(0, 1, 48).astype(f32)
+    y = ops.gemm_w4(cuda(xb), cuda(Wp), cuda(ws), bias=cuda(b), act=ACT_GELU, out=OUT_BF16, x_is_bf16=True)
+    want = G.gemm_w4(xb, Wp, ws, bias=b, act=ACT_GELU, out=OUT_BF16, x_is_bf16=True)
+    assert same(host(y), want), mismatch(host(y), want)
+    y2 = ops.gemm_w4(cuda(x), cuda(Wp), cuda(ws), out=OUT_INT8, out_scale=f32(0.25))
+    assert same(host(y2), G.gemm_w4(x, Wp, ws, out=OUT_INT8, out_scale=f32(0.25)))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_align_w4_groups(bf16):
+    rng = np.random.default_rng(44)
+    M, K = 4, 1024
+    x = (rng.normal(0, 1, (M, K // 128, 128)) * np.exp2(rng.integers(-140, 120, (M, K // 128, 1)))).reshape(M, K)
+    x = x.astype(f32)
+    x[0, 5], x[1, 300], x[1, 301], x[2, 700] = np.nan, np.inf, -np.inf, 3e38
+    x[3, :128] = np.array([1, 0x80000001, 0x00400000], np.uint32).view(f32).repeat(43)[:128]
+    xin = F.to_bf16_bits(x) if bf16 else x
+    q, s = ops.align_w4_groups(cuda(xin), x_is_bf16=bf16)
+    wq, ws = F.align_w4_groups(F.bf16_bits_to_f32(xin) if bf16 else x)
+    assert same(host(q), wq) and same(host(s), ws)
