@@ -1,0 +1,496 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 / W4A16 matrix path on one MI355X.
+
+Headline workload (`value`): one Qwen3-0.6B decode step's linear set at M = 1, as the golden model
+runs it: 28 layers x (q 1024->2048, k 1024->1024, v 1024->1024, o 2048->1024, gate/up 1024->3072,
+down 3072->1024) plus the lm_head 1024->151936, each preceded by its per-token quantizer (q/k/v share
+one quantization, gate/up share one, o and down have their own, the head its own). Weights are
+seeded random int8 with per-channel fp32 scales (~596 MB of weights per step), resident in HBM
+before timing. A step is captured once as a HIP graph (the C ABI validates every call at capture)
+and replayed; `value` = algorithmic HBM bytes of the step / step time.
+
+Also reported (in "configs"): every BASELINE workload as us/call, GB/s and roofline fraction (and
+TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight copies so the 256 MB
+MALL cannot serve it; per-kernel durations from HIP events around each launch of the decode step;
+and the CPU baseline (the numpy oracle, single core) on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-configs] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+INT8_PEAK = 5.0e15         # MI355X dense INT8 MFMA, ops/s
+ROTATE_BYTES = 512 << 20   # distinct weight bytes each single-config measurement cycles through
+
+QWEN3_LAYERS = 28
+QWEN3_H, QWEN3_Q, QWEN3_KV, QWEN3_FF, QWEN3_VOCAB = 1024, 2048, 1024, 3072, 151936
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config measurements")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample length")
+    ap.add_argument("--detail", type=str, default="", help="also write the full result JSON here")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------------------ launch plumbing
+class Launch:
+    """One C-ABI call with its arguments resolved to raw pointers (no per-call Python checks).
+    `operands` keeps the device tensors it reads and writes (for checks and the CPU baseline)."""
+
+    def __init__(self, kind: str, fn, args: tuple, nbytes: int, ops: int, name: str, operands: dict):
+        self.kind, self.fn, self.args, self.nbytes, self.ops, self.name = kind, fn, args, nbytes, ops, name
+        self.operands = operands
+
+    def __call__(self, stream: int) -> None:
+        rc = self.fn(*self.args, stream)
+        if rc != 0:
+            from opentars_amd import _lib
+            raise RuntimeError(f"{self.name}: status {rc}: {_lib.last_error()}")
+
+
+def quant_launch(lib, x, q, s, name=""):
+    M, K = x.shape
+    return Launch("quant_rows", lib.tars_quant_rows,
+                  (x.data_ptr(), x.stride(0) * 4, q.data_ptr(), q.stride(0), s.data_ptr(), M, K),
+                  4 * M * K + M * K + 4 * M, 0, name, dict(x=x, q=q, s=s))
+
+
+def w8_launch(lib, q, s, W, scol, y, name=""):
+    M, K = q.shape
+    N = W.shape[0]
+    return Launch("gemm_w8a8", lib.tars_gemm_w8a8,
+                  (q.data_ptr(), q.stride(0), s.data_ptr(), W.data_ptr(), scol.data_ptr(), N, None,
+                   y.data_ptr(), y.stride(0) * 4, M, N, K, 0, 0, 0),
+                  N * K + 4 * N + M * K + 4 * M + 4 * M * N, 2 * M * N * K, name,
+                  dict(q=q, s=s, W=W, scol=scol, y=y))
+
+
+def ksplit_launch(lib, q, s, blocks, scol, y, name=""):
+    M = q.shape[0]
+    N = blocks[0].shape[0]
+    nb = len(blocks)
+    ptrs = (ctypes.c_void_p * nb)(*[b.data_ptr() for b in blocks])
+    ks = (ctypes.c_int32 * nb)(*[b.shape[1] for b in blocks])
+    K = sum(b.shape[1] for b in blocks)
+    return Launch("gemm_w8a8_ksplit", lib.tars_gemm_w8a8_ksplit,
+                  (q.data_ptr(), q.stride(0), s.data_ptr(), ptrs, ks, nb, scol.data_ptr(), y.data_ptr(),
+                   y.stride(0) * 4, M, N),
+                  N * K + 4 * N + M * K + 4 * M + 4 * M * N, 2 * M * N * K, name,
+                  dict(q=q, s=s, blocks=blocks, scol=scol, y=y, ptrs=ptrs, ks=ks))
+
+
+def w4_launch(lib, x, Wp, ws, y, name=""):
+    M, K = x.shape
+    N = Wp.shape[0]
+    return Launch("gemm_w4a16", lib.tars_gemm_w4a16,
+                  (x.data_ptr(), x.stride(0) * 4, 4, Wp.data_ptr(), ws.data_ptr(), None, y.data_ptr(),
+                   y.stride(0) * 4, M, N, K, 0, 0, 0),
+                  N * K // 2 + 2 * N * (K // 128) + 4 * M * K + 4 * M * N, 2 * M * N * K, name,
+                  dict(x=x, Wp=Wp, ws=ws, y=y))
+
+
+# ------------------------------------------------------------------------------ workloads
+def rand_int8(torch, gen, n, k):
+    return torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=gen)
+
+
+def rand_scales(torch, gen, n):
+    return (torch.rand(n, device="cuda", generator=gen) * 9e-3 + 1e-3).to(torch.float32)
+
+
+def decode_set(torch, lib, seed: int):
+    """The Qwen3-0.6B decode-step launches in model order, with their device buffers."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    H, Q, KV, FF = QWEN3_H, QWEN3_Q, QWEN3_KV, QWEN3_FF
+    keep, launches = [], []
+
+    def act(k):
+        x = torch.randn((1, k), device="cuda", generator=gen, dtype=torch.float32)
+        q = torch.empty((1, k), dtype=torch.int8, device="cuda")
+        s = torch.empty((1,), dtype=torch.float32, device="cuda")
+        keep.extend([x, q, s])
+        return x, q, s
+
+    def lin(n, k):
+        W, sc, y = rand_int8(torch, gen, n, k), rand_scales(torch, gen, n), torch.empty((1, n), device="cuda")
+        keep.extend([W, sc, y])
+        return W, sc, y
+
+    for layer in range(QWEN3_LAYERS):
+        x, q, s = act(H)
+        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_attn_in"))
+        for nm, n in (("q", Q), ("k", KV), ("v", KV)):
+            W, sc, y = lin(n, H)
+            launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.{nm}_proj"))
+        x, q, s = act(Q)
+        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_attn_out"))
+        W, sc, y = lin(H, Q)
+        launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.o_proj"))
+        x, q, s = act(H)
+        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_mlp_in"))
+        for nm in ("gate", "up"):
+            W, sc, y = lin(FF, H)
+            launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.{nm}_proj"))
+        x, q, s = act(FF)
+        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_mlp_mid"))
+        W, sc, y = lin(H, FF)
+        launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.down_proj"))
+    x, q, s = act(H)
+    launches.append(quant_launch(lib, x, q, s, "head.quant"))
+    W, sc, y = lin(QWEN3_VOCAB, H)
+    launches.append(w8_launch(lib, q, s, W, sc, y, "lm_head"))
+    return launches, keep
+
+
+def capture(torch, launches):
+    """A HIP graph of the launches in order (torch's capture stream is the current stream)."""
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for l in launches:                  # one eager pass on the capture stream first
+            l(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream().cuda_stream
+        for l in launches:
+            l(s)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps: int, warmup: int) -> float:
+    """Seconds per replay (events on the current stream, synchronized on both sides)."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def per_launch_times(torch, launches, passes: int = 3):
+    """HIP-event duration of every launch (eager, in model order, so caches are as cold as in the
+    step): returns {index: [seconds, ...]}."""
+    out = {i: [] for i in range(len(launches))}
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(passes):
+        evs = []
+        for l in launches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            l(s)
+            b.record()
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(evs):
+            out[i].append(a.elapsed_time(b) / 1e3)
+    return out
+
+
+def kernel_family(l: Launch) -> str:
+    """Which HIP kernel instance a launch runs (mirrors the dispatch in the library)."""
+    if l.kind != "gemm_w8a8":
+        return l.kind
+    M, N, K = l.args[9], l.args[10], l.args[11]
+    if M == 1:
+        c = K // 16
+        return f"gemv_w8a8<K={K}>" if c <= 64 * 8 else "gemv_w8a8<any K>"
+    return "gemm_w8a8_mfma"
+
+
+# ------------------------------------------------------------------------------ single configs
+def rotated(torch, make, per_copy_bytes: int):
+    """Enough independent copies of a workload to cycle through ROTATE_BYTES."""
+    n = max(2, -(-ROTATE_BYTES // max(per_copy_bytes, 1)))
+    return [make(i) for i in range(n)]
+
+
+def measure_config(torch, launches, reps_target: int = 2000) -> dict:
+    g = capture(torch, launches)
+    reps = max(3, reps_target // len(launches))
+    t = time_graph(torch, g, reps, warmup=2) / len(launches)
+    nbytes, ops = launches[0].nbytes, launches[0].ops
+    r = {"us_per_call": round(t * 1e6, 3), "GBps": round(nbytes / t / 1e9, 1),
+         "hbm_frac": round(nbytes / t / HBM_PEAK, 4), "bytes_per_call": nbytes,
+         "distinct_copies": len(launches)}
+    if ops:
+        r["TOPS"] = round(ops / t / 1e12, 2)
+        r["int8_peak_frac"] = round(ops / t / INT8_PEAK, 5)
+    del g
+    return r
+
+
+def config_suite(torch, lib, seed: int) -> dict:
+    from opentars_amd import ops
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 1)
+    res = {}
+
+    def w8(M, N, K, name):
+        x = torch.randn((M, K), device="cuda", generator=gen)
+        q, s = ops.quant_rows(x)
+        y = torch.empty((M, N), device="cuda")
+        holds = []
+
+        def make(i):
+            W, sc = rand_int8(torch, gen, N, K), rand_scales(torch, gen, N)
+            holds.append((W, sc))
+            return w8_launch(lib, q, s, W, sc, y, name)
+        ls = rotated(torch, make, N * K)
+        r = measure_config(torch, ls)
+        r.update(M=M, N=N, K=K)
+        del ls, holds
+        torch.cuda.empty_cache()
+        return r
+
+    res["c1_gemv_qwen3_gate_M1_K1024_N3072"] = w8(1, 3072, 1024, "c1")
+    res["lm_head_M1_K1024_N151936"] = w8(1, QWEN3_VOCAB, 1024, "lm_head")
+    for split in ((3456, 3456), (4096, 2816)):
+        x = torch.randn((1, 6912), device="cuda", generator=gen)
+        q, s = ops.quant_rows(x)
+        y = torch.empty((1, 1152), device="cuda")
+        holds = []
+
+        def make(i):
+            bl = [rand_int8(torch, gen, 1152, k) for k in split]
+            sc = rand_scales(torch, gen, 1152)
+            holds.append((bl, sc))
+            return ksplit_launch(lib, q, s, bl, sc, y, "c2")
+        ls = rotated(torch, make, 1152 * 6912)
+        r = measure_config(torch, ls)
+        r.update(M=1, N=1152, K=6912, blocks=list(split))
+        res[f"c2_gemma3_down_ksplit_{split[0]}+{split[1]}"] = r
+        log(f"c2 {split}: {r['us_per_call']} us")
+        del ls, holds
+    for M in (4, 256):
+        for K, N in ((1024, 3072), (3072, 1024)):
+            res[f"c4_prefill_M{M}_K{K}_N{N}"] = w8(M, N, K, "c4")
+            log(f"c4 M={M} K={K} N={N}: {res[f'c4_prefill_M{M}_K{K}_N{N}']['us_per_call']} us")
+    for K, N in ((1536, 12288), (6144, 1536)):
+        x = torch.randn((1, K), device="cuda", generator=gen)
+        y = torch.empty((1, N), device="cuda")
+        holds = []
+
+        def make(i):
+            Wp = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device="cuda", generator=gen)
+            ws = (torch.rand((N, K // 128), device="cuda", generator=gen) * 9e-3 + 1e-3).half()
+            holds.append((Wp, ws))
+            return w4_launch(lib, x, Wp, ws, y, "c5")
+        ls = rotated(torch, make, N * K // 2)
+        r = measure_config(torch, ls)
+        r.update(M=1, N=N, K=K)
+        res[f"c5_w4a16_M1_K{K}_N{N}"] = r
+        log(f"c5 K={K} N={N}: {r['us_per_call']} us")
+        del ls, holds
+        torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(launches, target_s: float) -> dict:
+    """The numpy oracle (the golden path's own algorithm: the per-token quantizer, int64 matmul and
+    the elementwise fp32 epilogue) over the decode-step launches in model order, on this host's CPU,
+    single-threaded, until about target_s seconds of compute have passed. Same bytes/s unit."""
+    from oracle import golden as G
+    from oracle import numerics as F
+
+    host = {}
+
+    def operands(i, l):
+        if i not in host:             # device -> host copies happen outside the timed calls
+            host[i] = {k: v.cpu().numpy() for k, v in l.operands.items()}
+        return host[i]
+
+    elapsed, done_bytes, calls = 0.0, 0, 0
+    while elapsed < target_s:
+        for i, l in enumerate(launches):
+            o = operands(i, l)
+            t = time.perf_counter()
+            if l.kind == "quant_rows":
+                F.quant_rows(o["x"])
+            else:
+                G.gemm_rowcol(o["q"], o["s"], o["W"], o["scol"])
+            elapsed += time.perf_counter() - t
+            done_bytes += l.nbytes
+            calls += 1
+            if elapsed >= target_s:
+                break
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    steps = done_bytes / sum(l.nbytes for l in launches)
+    return {"value": round(done_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle over {calls} launches of the decode step in model order "
+                      f"({steps:.2f} steps, {elapsed:.1f} s of compute)",
+            "cpu_model": cpu, "os_cpu_count": os.cpu_count(),
+            "threads_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS")}}
+
+
+# ------------------------------------------------------------------------------ main
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build's path is single-GPU (output-channel sharding over "
+              "several GPUs is described in DESIGN.md but not run); use --gpus 1", file=sys.stderr)
+        return 2
+    os.environ.setdefault("OMP_NUM_THREADS", "1")
+    import numpy as np
+    import torch
+    import opentars_amd
+
+    lib = opentars_amd.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    log("building the decode-step workload")
+    launches, keep = decode_set(torch, lib, args.seed)
+    step_bytes = sum(l.nbytes for l in launches)
+    weight_bytes = sum(l.args[10] * l.args[11] for l in launches if l.kind == "gemm_w8a8")
+    graph = capture(torch, launches)
+    torch.cuda.synchronize()
+
+    log(f"captured {len(launches)} launches; timing {args.steps} steps")
+    # the timed region: W warmup steps, then exactly K steps between synchronizations
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    step_s = e0.elapsed_time(e1) / 1e3 / args.steps
+
+    log(f"step {step_s * 1e6:.1f} us; per-launch event pass")
+    # per-kernel durations (HIP events around each launch, model order) -> roofline of the dominant kernel
+    times = per_launch_times(torch, launches, passes=3)
+    fam = {}
+    for i, l in enumerate(launches):
+        f = fam.setdefault(kernel_family(l), {"launches_per_step": 0, "bytes_per_step": 0, "s_per_step": 0.0})
+        f["launches_per_step"] += 1
+        f["bytes_per_step"] += l.nbytes
+        f["s_per_step"] += float(np.mean(times[i]))
+    dom_name = max(fam, key=lambda k: fam[k]["s_per_step"])
+    dom = fam[dom_name]
+    avg_bytes = dom["bytes_per_step"] / dom["launches_per_step"]
+    avg_s = dom["s_per_step"] / dom["launches_per_step"]
+    kernels = {k: {"launches_per_step": v["launches_per_step"],
+                   "avg_bytes_per_launch": round(v["bytes_per_step"] / v["launches_per_step"]),
+                   "avg_us_per_launch": round(v["s_per_step"] / v["launches_per_step"] * 1e6, 3),
+                   "GBps": round(v["bytes_per_step"] / v["s_per_step"] / 1e9, 1),
+                   "hbm_frac": round(v["bytes_per_step"] / v["s_per_step"] / HBM_PEAK, 4)}
+               for k, v in fam.items()}
+    head_i = next(i for i, l in enumerate(launches) if l.name == "lm_head")
+    head_s = float(np.mean(times[head_i]))
+    lm_head = {"us": round(head_s * 1e6, 2), "GBps": round(launches[head_i].nbytes / head_s / 1e9, 1),
+               "hbm_frac": round(launches[head_i].nbytes / head_s / HBM_PEAK, 4)}
+
+    # bit-exact spot check of one projection of the timed data against the oracle
+    from oracle import golden as G
+    l0 = next(l for l in launches if l.name == "L0.q_proj")
+    o = {k: v.cpu().numpy() for k, v in l0.operands.items()}
+    want = G.gemm_rowcol(o["q"], o["s"], o["W"], o["scol"])
+    spot = bool(np.array_equal(o["y"].view(np.uint32), want.view(np.uint32)))
+
+    # device copy ceiling for context
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(big)
+    for _ in range(2):
+        dst.copy_(big)
+    torch.cuda.synchronize()
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(5):
+        dst.copy_(big)
+    c1.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * (1 << 30) * 5 / (c0.elapsed_time(c1) / 1e3) / 1e9
+    del big, dst
+    torch.cuda.empty_cache()
+
+    log("per-config measurements")
+    configs = {} if args.no_configs else config_suite(torch, lib, args.seed)
+    log("cpu baseline")
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(launches, args.cpu_seconds)
+
+    value = step_bytes / step_s / 1e9
+    line = {
+        "metric": "W8A8 GEMV HBM GB/s, Qwen3-0.6B decode-step linear set (M=1), bit-exact",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / 11.71, 1),
+        "dtype": "int8",
+        "data": "synthetic (seeded random int8 weights, per-channel fp32 scales, N(0,1) activations)",
+        "config": {"workload": "qwen3-0.6b decode-step W8A8 linear set, M=1: 28 layers x (q,k,v,o,gate,up,down) "
+                               "+ lm_head 1024x151936, with per-token quantizers",
+                   "launches_per_step": len(launches), "weight_bytes": weight_bytes,
+                   "algorithmic_bytes_per_step": step_bytes, "graph": True},
+        "hbm_frac": round(value * 1e9 / HBM_PEAK, 4),
+        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(avg_bytes / avg_s / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(avg_bytes / avg_s / HBM_PEAK, 4),
+                     "traffic": None, "avg_bytes_per_launch": round(avg_bytes), "avg_us_per_launch": round(avg_s * 1e6, 3)},
+        "lm_head": lm_head,
+        "kernels": kernels,
+        "device_copy_GBps": round(copy_gbps, 1),
+        "bit_exact_spot_check": spot,
+        "cpu_baseline": cpu,
+        "configs": configs,
+        "wall_s_timed": round(t_wall, 3),
+    }
+    if args.detail:
+        Path(args.detail).write_text(json.dumps(line, indent=1))
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
