@@ -88,6 +88,19 @@ def w8_launch(lib, q, s, W, scol, y, name=""):
                   dict(q=q, s=s, W=W, scol=scol, y=y))
 
 
+def fused_launch(lib, x, mats, name=""):
+    """One tars_quant_gemm_w8a8 call: x quantized in registers, feeding mats [(W, scol, y), ...]."""
+    from opentars_amd import _lib
+    M, K = x.shape
+    descs = (_lib.W8A8Out * len(mats))(*[_lib.W8A8Out(W.data_ptr(), sc.data_ptr(), None, y.data_ptr(),
+                                                      y.stride(0) * 4, W.shape[0], 0, 0, 0) for W, sc, y in mats])
+    nbytes = 4 * M * K + sum(W.shape[0] * K + 4 * W.shape[0] + 4 * M * W.shape[0] for W, _, _ in mats)
+    ops = sum(2 * M * W.shape[0] * K for W, _, _ in mats)
+    return Launch("quant_gemm_w8a8", lib.tars_quant_gemm_w8a8,
+                  (x.data_ptr(), x.stride(0) * 4, None, 0, None, M, K, descs, len(mats)),
+                  nbytes, ops, name, dict(x=x, mats=mats, descs=descs))
+
+
 def ksplit_launch(lib, q, s, blocks, scol, y, name=""):
     M = q.shape[0]
     N = blocks[0].shape[0]
@@ -122,11 +135,14 @@ def rand_scales(torch, gen, n):
 
 
 def decode_set(torch, lib, seed: int):
-    """The Qwen3-0.6B decode-step launches in model order, with their device buffers."""
+    """The Qwen3-0.6B decode-step linear set in model order. Returns (fused, unfused, buffers):
+    fused = one quantize+GEMV launch per shared quantization (q/k/v, o, gate/up, down, head), the
+    way the library runs a layer; unfused = the golden model's own descriptor sequence (ROW_QUANT,
+    then one GEMM per projection), used for the CPU baseline and as a comparison."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     H, Q, KV, FF = QWEN3_H, QWEN3_Q, QWEN3_KV, QWEN3_FF
-    keep, launches = [], []
+    keep, fused, unfused = [], [], []
 
     def act(k):
         x = torch.randn((1, k), device="cuda", generator=gen, dtype=torch.float32)
@@ -140,30 +156,21 @@ def decode_set(torch, lib, seed: int):
         keep.extend([W, sc, y])
         return W, sc, y
 
-    for layer in range(QWEN3_LAYERS):
-        x, q, s = act(H)
-        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_attn_in"))
-        for nm, n in (("q", Q), ("k", KV), ("v", KV)):
-            W, sc, y = lin(n, H)
-            launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.{nm}_proj"))
-        x, q, s = act(Q)
-        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_attn_out"))
-        W, sc, y = lin(H, Q)
-        launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.o_proj"))
-        x, q, s = act(H)
-        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_mlp_in"))
-        for nm in ("gate", "up"):
-            W, sc, y = lin(FF, H)
-            launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.{nm}_proj"))
-        x, q, s = act(FF)
-        launches.append(quant_launch(lib, x, q, s, f"L{layer}.quant_mlp_mid"))
-        W, sc, y = lin(H, FF)
-        launches.append(w8_launch(lib, q, s, W, sc, y, f"L{layer}.down_proj"))
-    x, q, s = act(H)
-    launches.append(quant_launch(lib, x, q, s, "head.quant"))
-    W, sc, y = lin(QWEN3_VOCAB, H)
-    launches.append(w8_launch(lib, q, s, W, sc, y, "lm_head"))
-    return launches, keep
+    def group(tag, k, projs):
+        x, q, s = act(k)
+        mats = [lin(n, k) for _, n in projs]
+        fused.append(fused_launch(lib, x, mats, tag))
+        unfused.append(quant_launch(lib, x, q, s, tag + ".quant"))
+        for (nm, _), (W, sc, y) in zip(projs, mats):
+            unfused.append(w8_launch(lib, q, s, W, sc, y, nm))
+
+    for L in range(QWEN3_LAYERS):
+        group(f"L{L}.qkv", H, [(f"L{L}.q_proj", Q), (f"L{L}.k_proj", KV), (f"L{L}.v_proj", KV)])
+        group(f"L{L}.o", Q, [(f"L{L}.o_proj", H)])
+        group(f"L{L}.gate_up", H, [(f"L{L}.gate_proj", FF), (f"L{L}.up_proj", FF)])
+        group(f"L{L}.down", FF, [(f"L{L}.down_proj", H)])
+    group("head", H, [("lm_head", QWEN3_VOCAB)])
+    return fused, unfused, keep
 
 
 def capture(torch, launches):
@@ -198,34 +205,68 @@ def time_graph(torch, g, reps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
-def per_launch_times(torch, launches, passes: int = 3):
-    """HIP-event duration of every launch (eager, in model order, so caches are as cold as in the
-    step): returns {index: [seconds, ...]}."""
-    out = {i: [] for i in range(len(launches))}
-    s = torch.cuda.current_stream().cuda_stream
-    for _ in range(passes):
-        evs = []
-        for l in launches:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            l(s)
-            b.record()
-            evs.append((a, b))
-        torch.cuda.synchronize()
-        for i, (a, b) in enumerate(evs):
-            out[i].append(a.elapsed_time(b) / 1e3)
-    return out
+def rows_per_wave(rows: int) -> int:
+    """The library's rows-per-wave rule (gemv_w8a8.hip, rows_per_wave)."""
+    return 1 if rows < 16384 else 2 if rows < 32768 else 4 if rows < 65536 else 8
 
 
-def kernel_family(l: Launch) -> str:
-    """Which HIP kernel instance a launch runs (mirrors the dispatch in the library)."""
-    if l.kind != "gemm_w8a8":
+def kernel_instance(l: Launch) -> str:
+    """The HIP kernel instance a launch runs, named as rocprofv3 names it (mirrors the dispatch in
+    gemv_w8a8.hip for the M = 1 W8A8 paths)."""
+    if l.kind == "quant_gemm_w8a8":
+        K = l.args[6]
+        rows = sum(d.N for d in l.operands["descs"])
+        name = "quant_gemv_w8a8_kernel"
+    elif l.kind == "gemm_w8a8" and l.args[9] == 1:
+        K, rows, name = l.args[11], l.args[10], "gemv_w8a8_kernel"
+    else:
         return l.kind
-    M, N, K = l.args[9], l.args[10], l.args[11]
-    if M == 1:
-        c = K // 16
-        return f"gemv_w8a8<K={K}>" if c <= 64 * 8 else "gemv_w8a8<any K>"
-    return "gemm_w8a8_mfma"
+    c = K // 16
+    if c <= 32:
+        lanes = 8 if c <= 8 else 16 if c <= 16 else 32
+        return f"{name}<{lanes}, 1, 8>"
+    cpl = -(-c // 64)
+    u = rows_per_wave(rows)
+    if cpl > 8:
+        return f"{name}<64, 0, {1 if u == 1 else 4}>"
+    u = min(u, {1: 8, 2: 4, 3: 2, 4: 2}.get(cpl, 1))
+    return f"{name}<64, {cpl}, {u}>"
+
+
+def instance_times(torch, step_graph, launches, reps: int = 5) -> dict:
+    """Average launch duration of every kernel instance in the step, from HIP events around a
+    graph of that instance's launches (step order, same buffers). Before each timed replay the full
+    step and then the largest other instance are replayed, so at least ~300 MB (more than the
+    256 MB MALL) stream between two uses of any weight and every timed launch starts cold."""
+    fams = {}
+    for l in launches:
+        fams.setdefault(kernel_instance(l), []).append(l)
+    # (an instance with few launches per step, like the head, carries the graph replay's fixed
+    # overhead in its figure; bench's per-config measurements time such kernels over many launches)
+    graphs = {name: capture(torch, ls) for name, ls in fams.items()}
+    size = {name: sum(l.nbytes for l in ls) for name, ls in fams.items()}
+    out = {}
+    for name, ls in fams.items():
+        others = [k for k in fams if k != name]
+        flush = graphs[max(others, key=lambda k: size[k])] if others else None
+        total = 0.0
+        for _ in range(reps):
+            step_graph.replay()
+            if flush is not None:
+                flush.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graphs[name].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            total += e0.elapsed_time(e1) / 1e3
+        avg_s = total / (reps * len(ls))
+        out[name] = {"launches_per_step": len(ls), "avg_bytes_per_launch": round(size[name] / len(ls)),
+                     "avg_us_per_launch": round(avg_s * 1e6, 3), "s_per_step": avg_s * len(ls),
+                     "GBps": round(size[name] / (avg_s * len(ls)) / 1e9, 1),
+                     "hbm_frac": round(size[name] / (avg_s * len(ls)) / HBM_PEAK, 4)}
+    del graphs
+    return out
 
 
 # ------------------------------------------------------------------------------ single configs
@@ -275,6 +316,19 @@ def config_suite(torch, lib, seed: int) -> dict:
 
     res["c1_gemv_qwen3_gate_M1_K1024_N3072"] = w8(1, 3072, 1024, "c1")
     res["lm_head_M1_K1024_N151936"] = w8(1, QWEN3_VOCAB, 1024, "lm_head")
+    # the head as the decode step runs it: the quantizer fused in, 4 distinct weight copies
+    x = torch.randn((1, 1024), device="cuda", generator=gen)
+    y = torch.empty((1, QWEN3_VOCAB), device="cuda")
+    holds = []
+
+    def make_head(i):
+        W, sc = rand_int8(torch, gen, QWEN3_VOCAB, 1024), rand_scales(torch, gen, QWEN3_VOCAB)
+        holds.append((W, sc))
+        return fused_launch(lib, x, [(W, sc, y)], "head")
+    ls = rotated(torch, make_head, QWEN3_VOCAB * 1024)
+    res["lm_head_fused_quant_M1_K1024_N151936"] = dict(measure_config(torch, ls), M=1, N=QWEN3_VOCAB, K=1024)
+    del ls, holds
+    torch.cuda.empty_cache()
     for split in ((3456, 3456), (4096, 2816)):
         x = torch.randn((1, 6912), device="cuda", generator=gen)
         q, s = ops.quant_rows(x)
@@ -382,9 +436,9 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
 
     log("building the decode-step workload")
-    launches, keep = decode_set(torch, lib, args.seed)
+    launches, unfused, keep = decode_set(torch, lib, args.seed)
     step_bytes = sum(l.nbytes for l in launches)
-    weight_bytes = sum(l.args[10] * l.args[11] for l in launches if l.kind == "gemm_w8a8")
+    weight_bytes = sum(l.args[10] * l.args[11] for l in unfused if l.kind == "gemm_w8a8")
     graph = capture(torch, launches)
     torch.cuda.synchronize()
 
@@ -403,36 +457,31 @@ def main() -> int:
     t_wall = time.perf_counter() - t_wall
     step_s = e0.elapsed_time(e1) / 1e3 / args.steps
 
-    log(f"step {step_s * 1e6:.1f} us; per-launch event pass")
-    # per-kernel durations (HIP events around each launch, model order) -> roofline of the dominant kernel
-    times = per_launch_times(torch, launches, passes=3)
-    fam = {}
-    for i, l in enumerate(launches):
-        f = fam.setdefault(kernel_family(l), {"launches_per_step": 0, "bytes_per_step": 0, "s_per_step": 0.0})
-        f["launches_per_step"] += 1
-        f["bytes_per_step"] += l.nbytes
-        f["s_per_step"] += float(np.mean(times[i]))
-    dom_name = max(fam, key=lambda k: fam[k]["s_per_step"])
-    dom = fam[dom_name]
-    avg_bytes = dom["bytes_per_step"] / dom["launches_per_step"]
-    avg_s = dom["s_per_step"] / dom["launches_per_step"]
-    kernels = {k: {"launches_per_step": v["launches_per_step"],
-                   "avg_bytes_per_launch": round(v["bytes_per_step"] / v["launches_per_step"]),
-                   "avg_us_per_launch": round(v["s_per_step"] / v["launches_per_step"] * 1e6, 3),
-                   "GBps": round(v["bytes_per_step"] / v["s_per_step"] / 1e9, 1),
-                   "hbm_frac": round(v["bytes_per_step"] / v["s_per_step"] / HBM_PEAK, 4)}
-               for k, v in fam.items()}
-    head_i = next(i for i, l in enumerate(launches) if l.name == "lm_head")
-    head_s = float(np.mean(times[head_i]))
-    lm_head = {"us": round(head_s * 1e6, 2), "GBps": round(launches[head_i].nbytes / head_s / 1e9, 1),
-               "hbm_frac": round(launches[head_i].nbytes / head_s / HBM_PEAK, 4)}
+    log(f"step {step_s * 1e6:.1f} us; per-instance timing")
+    kernels = instance_times(torch, graph, launches)
+    dom_name = max(kernels, key=lambda k: kernels[k]["s_per_step"])
+    dom = kernels[dom_name]
+    for v in kernels.values():
+        v.pop("s_per_step")
+    traffic = None
+    tfile = ROOT / "profiles" / "decode_step_traffic.json"
+    if tfile.exists():
+        entry = json.loads(tfile.read_text()).get("instances", {}).get(dom_name)
+        if entry and entry.get("algorithmic_bytes") == dom["avg_bytes_per_launch"]:
+            traffic = entry["traffic_bytes"]
 
-    # bit-exact spot check of one projection of the timed data against the oracle
+    # bit-exact spot check of layer 0's q/k/v outputs of the timed data against the oracle
     from oracle import golden as G
-    l0 = next(l for l in launches if l.name == "L0.q_proj")
-    o = {k: v.cpu().numpy() for k, v in l0.operands.items()}
-    want = G.gemm_rowcol(o["q"], o["s"], o["W"], o["scol"])
-    spot = bool(np.array_equal(o["y"].view(np.uint32), want.view(np.uint32)))
+    from oracle import numerics as F
+    l0 = next(l for l in launches if l.name == "L0.qkv")
+    xq, xs = F.quant_rows(l0.operands["x"].cpu().numpy())
+    spot = all(np.array_equal(y.cpu().numpy().view(np.uint32),
+                              G.gemm_rowcol(xq, xs, W.cpu().numpy(), sc.cpu().numpy()).view(np.uint32))
+               for W, sc, y in l0.operands["mats"])
+    # the golden model's unfused sequence (ROW_QUANT + one GEMM per projection), for comparison
+    g_unf = capture(torch, unfused)
+    unfused_s = time_graph(torch, g_unf, max(3, args.steps // 4), warmup=3)
+    del g_unf
 
     # device copy ceiling for context
     big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
@@ -454,7 +503,7 @@ def main() -> int:
     configs = {} if args.no_configs else config_suite(torch, lib, args.seed)
     log("cpu baseline")
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(launches, args.cpu_seconds)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(unfused, args.cpu_seconds)
 
     value = step_bytes / step_s / 1e9
     line = {
@@ -471,14 +520,20 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic (seeded random int8 weights, per-channel fp32 scales, N(0,1) activations)",
         "config": {"workload": "qwen3-0.6b decode-step W8A8 linear set, M=1: 28 layers x (q,k,v,o,gate,up,down) "
-                               "+ lm_head 1024x151936, with per-token quantizers",
+                               "+ lm_head 1024x151936, each with its per-token quantizer fused in",
                    "launches_per_step": len(launches), "weight_bytes": weight_bytes,
                    "algorithmic_bytes_per_step": step_bytes, "graph": True},
+        "unfused_golden_sequence": {"launches_per_step": len(unfused), "ms_per_step": round(unfused_s * 1e3, 4),
+                                    "GBps": round(sum(l.nbytes for l in unfused) / unfused_s / 1e9, 1)},
         "hbm_frac": round(value * 1e9 / HBM_PEAK, 4),
-        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(avg_bytes / avg_s / 1e9, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(avg_bytes / avg_s / HBM_PEAK, 4),
-                     "traffic": None, "avg_bytes_per_launch": round(avg_bytes), "avg_us_per_launch": round(avg_s * 1e6, 3)},
-        "lm_head": lm_head,
+        "roofline": {"bound": "hbm", "kernel": dom_name,
+                     "achieved": round(dom["avg_bytes_per_launch"] / dom["avg_us_per_launch"] / 1e3, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(dom["avg_bytes_per_launch"] / dom["avg_us_per_launch"] / 1e3 / (HBM_PEAK / 1e9), 4),
+                     "traffic": traffic, "traffic_source": "profiles/decode_step_traffic.json (rocprofv3 --pmc)",
+                     "avg_bytes_per_launch": dom["avg_bytes_per_launch"],
+                     "avg_us_per_launch": dom["avg_us_per_launch"]},
+        "lm_head": {k: configs.get(k) for k in ("lm_head_M1_K1024_N151936", "lm_head_fused_quant_M1_K1024_N151936")},
         "kernels": kernels,
         "device_copy_GBps": round(copy_gbps, 1),
         "bit_exact_spot_check": spot,

@@ -80,6 +80,35 @@ int tars_gemm_w8a8(const int8_t* A, int64_t lda, const float* srow,
                    void* Y, int64_t ldy, int32_t M, int32_t N, int32_t K,
                    int32_t act, int32_t out, uint32_t out_scale_bits, void* stream);
 
+/* One weight matrix fed by a shared quantized activation (tars_quant_gemm_w8a8). */
+typedef struct tars_w8a8_out {
+  const int8_t* W;          /* int8 [N, K] dense row-major, 16-byte aligned */
+  const float* scol;        /* fp32 [N] per-channel scales */
+  const float* bias;        /* fp32 [N] or NULL */
+  void* Y;                  /* [M, N] of the output format, row stride ldy bytes */
+  int64_t ldy;
+  int32_t N;
+  int32_t act;
+  int32_t out;
+  uint32_t out_scale_bits;
+} tars_w8a8_out;
+
+/*
+ * Fused per-token quantization + W8A8 GEMV/GEMM for up to 4 weight matrices sharing it:
+ *   (q, s) = quant_rows(x);  Y_i = convert_i(act_i(((i2f(q W_i^T) * s) * scol_i) + bias_i))
+ * Replaces one ROW_QUANT descriptor and the QM_ROWCOL GEMM descriptors that read its output, as
+ * QwenLowering emits them for q/k/v and gate/up (tars_mini/llm.py:711-731, 620-623; the
+ * descriptors at tars_mini/golden.py:369-372 and 326-349). Bit-identical to quant_rows followed
+ * by tars_gemm_w8a8 per matrix.
+ *   x  fp32 [M, K] (stride lda);  q/ldq/s: optional outputs (both NULL or both given) receiving
+ *   the quantized rows and row scales exactly as tars_quant_rows writes them.
+ *   outs: HOST array of nouts (1..4) descriptors. Rules: those of tars_quant_rows and
+ *   tars_gemm_w8a8 (per matrix, scol per channel); no output may overlap an input or another output.
+ */
+int tars_quant_gemm_w8a8(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s,
+                         int32_t M, int32_t K, const tars_w8a8_out* outs, int32_t nouts,
+                         void* stream);
+
 /*
  * W8A8 with K split into blocks that share one quantized activation row block and one
  * per-channel scale vector: block i covers columns [c_i, c_i + K_i) of A (c_0 = 0) with its own

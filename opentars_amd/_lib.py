@@ -16,12 +16,21 @@ OK, E_FIELD, E_ALIGN, E_RANGE, E_OVERLAP, E_ARG, E_DEVICE = 0, -6, -7, -8, -9, -
 STATUS_NAMES = {OK: "OK", E_FIELD: "E_FIELD", E_ALIGN: "E_ALIGN", E_RANGE: "E_RANGE",
                 E_OVERLAP: "E_OVERLAP", E_ARG: "E_ARG", E_DEVICE: "E_DEVICE"}
 
+class W8A8Out(ctypes.Structure):
+    """tars_w8a8_out: one weight matrix fed by a shared quantized activation."""
+    _fields_ = [("W", c_void_p), ("scol", c_void_p), ("bias", c_void_p), ("Y", c_void_p),
+                ("ldy", c_int64), ("N", c_int32), ("act", c_int32), ("out", c_int32),
+                ("out_scale_bits", c_uint32)]
+
+
 # Every exported entry point: name -> (restype, argtypes)
 SIGNATURES = {
     "tars_quant_rows": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p]),
     "tars_gemm_w8a8": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
                                c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_uint32,
                                c_void_p]),
+    "tars_quant_gemm_w8a8": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_int32,
+                                     ctypes.POINTER(W8A8Out), c_int32, c_void_p]),
     "tars_gemm_w8a8_ksplit": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
                                       c_void_p, c_int64, c_int32, c_int32, c_void_p]),
     "tars_align_w4": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_int64, c_void_p, c_int64, c_int32,

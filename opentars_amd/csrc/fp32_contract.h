@@ -63,6 +63,14 @@ __device__ __forceinline__ float add_to_exponent(float y, int e) {
 
 // 1/x: seed from the magic constant, three correction-form Newton steps, exponent surgery
 // (numerics.py:153-168).
+//
+// Inside the Newton steps the contract's flush/canonicalize wrappers are identities, so the raw
+// round-to-nearest-even operations give the same bits with a much shorter dependent chain:
+// m is in [1, 2) and the seed bits^-1(0x7EF311C7 - bits(m)) is in [0.47, 0.96], so every
+// m * y is a positive normal in [0.47, 1.9]; e = 1 - m * y is exactly 0 or a multiple of 2^-25
+// (both operands are), hence 0 or normal; y * e is 0 or at least 2^-26 in magnitude; and
+// y + y * e = y * (2 - m * y) stays positive and above 0.04. No subnormal, infinity or NaN can
+// arise, and each step is still one rounded operation (never fused: -ffp-contract=off).
 __device__ __forceinline__ float recip_f(float x) {
   const uint32_t xb = fbits(ftz(x));
   const uint32_t sgn = xb & kSign, mag = xb & 0x7FFFFFFFu;
@@ -74,8 +82,8 @@ __device__ __forceinline__ float recip_f(float x) {
   float y = ffrom(kRecipSeed - mb);
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    const float err = fadd(ffrom(kOne), fneg(fmul(m, y)));
-    y = fadd(y, fmul(y, err));
+    const float err = __fadd_rn(1.0f, -__fmul_rn(m, y));
+    y = __fadd_rn(y, __fmul_rn(y, err));
   }
   return ffrom(fbits(add_to_exponent(y, 127 - static_cast<int>(mag >> 23))) | sgn);
 }
@@ -161,6 +169,15 @@ __device__ __forceinline__ int8_t q8(float x, float inv) {
   return static_cast<int8_t>(static_cast<int>(y));
 }
 
+// q8 with an already flushed multiplier (inv from fmul). The product's output flush only turns a
+// subnormal into a zero, whose rint is the same integer 0, and canonicalization only rewrites NaN
+// payloads, which map to 0 anyway; so only the input flush of x remains.
+__device__ __forceinline__ int q8_flushed_inv(float x, float inv) {
+  float y = __fmul_rn(ftz(x), inv);
+  y = is_nan(y) ? 0.0f : rintf(y);
+  return static_cast<int>(fminf(fmaxf(y, -127.0f), 127.0f));
+}
+
 // numerics.py:270-275: FTZ, round-to-nearest-even to the top 16 bits, NaN -> 0x7FC0
 __device__ __forceinline__ uint16_t to_bf16_bits(float x) {
   const uint32_t b = fbits(ftz(x));
@@ -204,12 +221,39 @@ struct RowColEpilogue {
   float out_scale;
 
   __device__ __forceinline__ float value(int32_t acc, int m, int n) const {
+    return value_sr(acc, srow ? srow[m] : 0.0f, srow != nullptr, n);
+  }
+
+  // The same with the row scale given by value (a quantizer fused into the GEMV).
+  __device__ __forceinline__ float value_sr(int32_t acc, float sr, bool has_sr, int n) const {
     float y = i2f(acc);
-    if (srow) y = fmul(y, srow[m]);
+    if (has_sr) y = fmul(y, sr);
     y = fmul(y, scol[scol_per_tensor ? 0 : n]);
     if (bias) y = fadd(y, bias[n]);
     return act_fn(y, act);
   }
 };
+
+// Per-token quantizer pieces shared by the quant_rows kernel and the fused quantize + GEMV
+// kernels (numerics.py:383-390).
+__device__ __forceinline__ uint32_t abs_bits_ftz(float v) {
+  const uint32_t b = fbits(v) & 0x7FFFFFFFu;
+  return b < 0x00800000u ? 0u : b;  // ftz then |.|: a subnormal counts as +0
+}
+
+// amax encoding (an unsigned max of |x| encodings; any NaN encoding wins) -> (inv, s)
+__device__ __forceinline__ void quant_scales(uint32_t amax_bits, float& inv, float& s) {
+  const float amax = ffrom(amax_bits > kExpo ? kCanonNaN : amax_bits);
+  inv = fmul(ffrom(kQ127), recip_f(amax));
+  s = fmul(amax, ffrom(kInv127));
+}
+
+// Four q8 bytes packed little-endian; inv must come from fmul (flushed), as quant_scales gives it.
+__device__ __forceinline__ uint32_t q8x4(float a, float b, float c, float d, float inv) {
+  return (static_cast<uint32_t>(q8_flushed_inv(a, inv)) & 0xFFu) |
+         ((static_cast<uint32_t>(q8_flushed_inv(b, inv)) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(q8_flushed_inv(c, inv)) & 0xFFu) << 16) |
+         ((static_cast<uint32_t>(q8_flushed_inv(d, inv)) & 0xFFu) << 24);
+}
 
 }  // namespace tars

@@ -6,7 +6,7 @@
 // Each lane keeps its activation chunks in registers (the activation row is tiny and shared by
 // all rows), issues the loads of U rows back to back so U * CPL 16-byte loads are in flight, and
 // accumulates with the packed signed 8-bit dot product (v_dot4, 4 MACs per instruction) into
-// exact int32 sums. The L partial sums of a row are combined with cross-lane xor shuffles (exact
+// exact int32 sums. The L partial sums of a row are combined with DPP lane permutes (exact
 // integer adds, so the order is free), and lane `u` of the group runs the fp32 epilogue for row u.
 //
 // Roofline: HBM. Algorithmic bytes per row: K (weights) + 4 (scale) + 4 (output) (+4 bias).
@@ -28,13 +28,6 @@ __device__ __forceinline__ int dot16(v4i w, v4i x, int acc) {
   acc = __builtin_amdgcn_sdot4(w.z, x.z, acc, false);
   acc = __builtin_amdgcn_sdot4(w.w, x.w, acc, false);
   return acc;
-}
-
-template <int L>
-__device__ __forceinline__ int group_sum(int v) {
-#pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
 }
 
 // CPL > 0: exactly CPL chunks per lane with the activations held in registers (K <= 128 * L).
@@ -155,6 +148,140 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_kernel(KSplitArgs a
   }
 }
 
+// ---- fused per-token quantizer + grouped GEMV ----
+// Each workgroup quantizes the activation row once: its 256 threads read the fp32 row in float4s
+// (a single pass over 4K bytes, mostly L2 hits after the first workgroup), the row maximum meets
+// through wave shuffles and 4 LDS words, every thread runs the fixed recip_f sequence, and the
+// q8 bytes land in LDS where each lane picks up the 16-byte chunks its dot products need. The
+// weight loads are issued before any of this, so the quantizer runs under their HBM latency.
+// Workgroup 0 also stores the quantized row and its scale (the ROW_QUANT outputs the golden
+// model writes).
+template <int L, int CPL, int U>
+__global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs a) {
+  extern __shared__ __align__(16) int8_t qsh[];  // the quantized row, K bytes
+  __shared__ uint32_t wave_max[kWaves];
+  constexpr int kSlots = 64 / L;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int slot = lane / L;
+  const int sub = lane % L;
+  const int m = blockIdx.y;
+  const int C = a.K >> 4;
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGroups; ++i)
+    if (i < a.ngroups && static_cast<int>(blockIdx.x) >= a.block_start[i]) g = i;
+  const int8_t* W = a.g[0].W;
+  int N = a.g[0].N;
+#pragma unroll
+  for (int i = 1; i < kMaxGroups; ++i)
+    if (g == i) {
+      W = a.g[i].W;
+      N = a.g[i].N;
+    }
+  const int lb = static_cast<int>(blockIdx.x) - a.block_start[g];
+  const int n0 = (lb * (kWaves * kSlots) + wave * kSlots + slot) * U;
+  const v4i zero = {0, 0, 0, 0};
+
+  // 1. the weight stream starts first
+  v4i wv[U][CPL > 0 ? CPL : 1];
+  if constexpr (CPL > 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int n = n0 + u;
+      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * a.K);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = sub + j * L;
+        wv[u][j] = (n < N && c < C) ? load_stream(wrow + c) : zero;
+      }
+    }
+  }
+
+  // 2. the workgroup quantizes row m into LDS
+  const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(a.x) + m * a.lda);
+  const int K4 = a.K >> 2;
+  uint32_t mx = 0;
+  for (int i = threadIdx.x; i < K4; i += kThreads) {
+    const float4 v = xrow[i];
+    mx = max(mx, max(max(abs_bits_ftz(v.x), abs_bits_ftz(v.y)), max(abs_bits_ftz(v.z), abs_bits_ftz(v.w))));
+  }
+  mx = group_max<64>(mx);
+  if (lane == 0) wave_max[wave] = mx;
+  __syncthreads();
+  mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
+  float inv, sr;
+  quant_scales(mx, inv, sr);
+  const bool store_q = a.q != nullptr && blockIdx.x == 0;
+  for (int i = threadIdx.x; i < K4; i += kThreads) {
+    const float4 v = xrow[i];
+    const uint32_t b = q8x4(v.x, v.y, v.z, v.w, inv);
+    reinterpret_cast<uint32_t*>(qsh)[i] = b;
+    if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
+  }
+  if (store_q && threadIdx.x == 0) a.s[m] = sr;
+  __syncthreads();
+
+  // 3. exact int32 dot products
+  int acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = 0;
+  const v4i* xq = reinterpret_cast<const v4i*>(qsh);
+  if constexpr (CPL > 0) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = sub + j * L;
+      const v4i xv = c < C ? xq[c] : zero;
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] = dot16(wv[u][j], xv, acc[u]);
+    }
+  } else {
+    for (int c = sub; c < C; c += L) {
+      v4i w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int n = n0 + u;
+        w[u] = n < N ? load_stream(reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * a.K) + c) : zero;
+      }
+      const v4i xv = xq[c];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] = dot16(w[u], xv, acc[u]);
+    }
+  }
+
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = group_sum<L>(acc[u]);
+  int mine = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (sub == u) mine = acc[u];
+  const int n = n0 + sub;
+  if (sub < U && n < N) {
+    RowColEpilogue epi = a.g[0].epi;
+    void* Y = a.g[0].Y;
+    int64_t ldy = a.g[0].ldy;
+#pragma unroll
+    for (int i = 1; i < kMaxGroups; ++i)
+      if (g == i) {
+        epi = a.g[i].epi;
+        Y = a.g[i].Y;
+        ldy = a.g[i].ldy;
+      }
+    const float y = epi.value_sr(mine, sr, true, n);
+    store_out(Y, m * ldy, n, epi.out, y, epi.out_scale);
+  }
+}
+
+// Rows per wave: one row keeps small matrices spread over every CU (their time is latency, not
+// bandwidth); more rows per wave amortize the per-wave work once the grid is far larger than the
+// chip (the vocabulary-sized head).
+int rows_per_wave(int64_t rows) {
+  if (rows < 16384) return 1;
+  if (rows < 32768) return 2;
+  if (rows < 65536) return 4;
+  return 8;
+}
+
 template <int L, int CPL, int U>
 hipError_t go(const W8A8Args& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
@@ -163,31 +290,76 @@ hipError_t go(const W8A8Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-}  // namespace
+template <int L, int CPL, int U>
+hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
+  constexpr int rows_per_block = kWaves * (64 / L) * U;
+  int blocks = 0;
+  for (int i = 0; i < a.ngroups; ++i) {
+    a.block_start[i] = blocks;
+    blocks += (a.g[i].N + rows_per_block - 1) / rows_per_block;
+  }
+  for (int i = a.ngroups; i <= kMaxGroups; ++i) a.block_start[i] = blocks;
+  const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
+  hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U>), dim3(blocks, a.M), dim3(kThreads), lds, s, a);
+  return hipGetLastError();
+}
 
-hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s) {
-  const int C = a.K / 16;
-  if (C <= 8) return go<8, 1, 8>(a, s);
-  if (C <= 16) return go<16, 1, 8>(a, s);
-  if (C <= 32) return go<32, 1, 8>(a, s);
+// Kernel instance for (K, rows): lanes per row L, 16-byte chunks per lane CPL, rows per wave U.
+template <class Args, template <int, int, int> class Go>
+hipError_t dispatch(Args& a, int K, int64_t rows, hipStream_t s) {
+  const int C = K / 16;
+  const int u = rows_per_wave(rows);
+  if (C <= 8) return Go<8, 1, 8>::run(a, s);
+  if (C <= 16) return Go<16, 1, 8>::run(a, s);
+  if (C <= 32) return Go<32, 1, 8>::run(a, s);
   switch ((C + 63) / 64) {
-    case 1: return go<64, 1, 8>(a, s);
-    case 2: return go<64, 2, 4>(a, s);
-    case 3: return go<64, 3, 2>(a, s);
-    case 4: return go<64, 4, 2>(a, s);
-    case 5: return go<64, 5, 1>(a, s);
-    case 6: return go<64, 6, 1>(a, s);
-    case 7: return go<64, 7, 1>(a, s);
-    case 8: return go<64, 8, 1>(a, s);
-    default: return go<64, 0, 4>(a, s);
+    case 1:
+      return u == 1 ? Go<64, 1, 1>::run(a, s) : u == 2 ? Go<64, 1, 2>::run(a, s)
+           : u == 4 ? Go<64, 1, 4>::run(a, s) : Go<64, 1, 8>::run(a, s);
+    case 2:
+      return u == 1 ? Go<64, 2, 1>::run(a, s) : u == 2 ? Go<64, 2, 2>::run(a, s) : Go<64, 2, 4>::run(a, s);
+    case 3: return u == 1 ? Go<64, 3, 1>::run(a, s) : Go<64, 3, 2>::run(a, s);
+    case 4: return u == 1 ? Go<64, 4, 1>::run(a, s) : Go<64, 4, 2>::run(a, s);
+    case 5: return Go<64, 5, 1>::run(a, s);
+    case 6: return Go<64, 6, 1>::run(a, s);
+    case 7: return Go<64, 7, 1>::run(a, s);
+    case 8: return Go<64, 8, 1>::run(a, s);
+    default: return u == 1 ? Go<64, 0, 1>::run(a, s) : Go<64, 0, 4>::run(a, s);
   }
 }
 
+template <int L, int CPL, int U>
+struct GoPlain {
+  static hipError_t run(const W8A8Args& a, hipStream_t s) { return go<L, CPL, U>(a, s); }
+};
+template <int L, int CPL, int U>
+struct GoFused {
+  static hipError_t run(QuantGemvArgs& a, hipStream_t s) { return go_fused<L, CPL, U>(a, s); }
+};
+
+}  // namespace
+
+hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s) {
+  return dispatch<const W8A8Args, GoPlain>(a, a.K, a.N, s);
+}
+
+hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
+  int64_t rows = 0;
+  for (int i = 0; i < a.ngroups; ++i) rows += a.g[i].N;
+  return dispatch<QuantGemvArgs, GoFused>(a, a.K, rows, s);
+}
+
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s) {
-  constexpr int U = 4;
-  constexpr int rows_per_block = kWaves * U;
+  const int u = rows_per_wave(a.N);
+  const int rows_per_block = kWaves * u;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block, a.M);
-  hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<U>), grid, dim3(kThreads), 0, s, a);
+  if (u == 1) {
+    hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<1>), grid, dim3(kThreads), 0, s, a);
+  } else if (u == 2) {
+    hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<2>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<4>), dim3((a.N + kWaves * 4 - 1) / (kWaves * 4), a.M), dim3(kThreads), 0, s, a);
+  }
   return hipGetLastError();
 }
 

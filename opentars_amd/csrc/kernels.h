@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "fp32_contract.h"
+#include "wave_reduce.h"
 
 namespace tars {
 
@@ -69,8 +70,32 @@ struct W4Args {
   int M, N, K;
 };
 
+// Fused per-token quantizer + grouped W8A8 GEMV: the activation rows are quantized in registers by
+// every wave and feed up to kMaxGroups weight matrices (q/k/v, gate/up) in one launch.
+constexpr int kMaxGroups = 4;
+struct GemvGroup {
+  const int8_t* W;       // [N, K] dense
+  RowColEpilogue epi;    // srow unused: the row scale comes from the fused quantizer
+  void* Y;
+  int64_t ldy;
+  int N;
+};
+
+struct QuantGemvArgs {
+  const float* x;        // [M, K] fp32 rows at stride lda bytes
+  int64_t lda;
+  int8_t* q;             // optional: the quantized rows (stride ldq) and row scales, as quant_rows
+  int64_t ldq;
+  float* s;
+  int M, K;
+  GemvGroup g[kMaxGroups];
+  int ngroups;
+  int block_start[kMaxGroups + 1];  // first workgroup of each group along grid x
+};
+
 hipError_t launch_quant_rows(const QuantArgs& a, hipStream_t s);
 hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s);
+hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s);
 hipError_t launch_gemm_w8a8_mfma(const W8A8Args& a, hipStream_t s);
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s);
 hipError_t launch_gemm_w8a8_ksplit_mfma(const KSplitArgs& a, hipStream_t s);

@@ -12,11 +12,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ uint32_t abs_bits(float v) {
-  const uint32_t b = fbits(v) & 0x7FFFFFFFu;
-  return b < 0x00800000u ? 0u : b;  // ftz then |.|: a subnormal counts as +0
-}
-
 __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
   const int m = blockIdx.x;
   const float4* row = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(a.x) + m * a.lda);
@@ -26,11 +21,10 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float4 v = row[4 * c + j];
-      mx = max(mx, max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
+      mx = max(mx, max(max(abs_bits_ftz(v.x), abs_bits_ftz(v.y)), max(abs_bits_ftz(v.z), abs_bits_ftz(v.w))));
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off)));
+  mx = group_max<64>(mx);
   __shared__ uint32_t wave_max[kThreads / 64];
   __shared__ float inv_shared;
   if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mx;
@@ -39,9 +33,10 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
     uint32_t t = wave_max[0];
 #pragma unroll
     for (int w = 1; w < kThreads / 64; ++w) t = max(t, wave_max[w]);
-    const float amax = ffrom(t > kExpo ? kCanonNaN : t);
-    inv_shared = fmul(ffrom(kQ127), recip_f(amax));
-    a.s[m] = fmul(amax, ffrom(kInv127));
+    float inv, sr;
+    quant_scales(t, inv, sr);
+    inv_shared = inv;
+    a.s[m] = sr;
   }
   __syncthreads();
   const float inv = inv_shared;
@@ -51,10 +46,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float4 v = row[4 * c + j];
-      packed[j] = (static_cast<uint32_t>(static_cast<uint8_t>(q8(v.x, inv)))) |
-                  (static_cast<uint32_t>(static_cast<uint8_t>(q8(v.y, inv))) << 8) |
-                  (static_cast<uint32_t>(static_cast<uint8_t>(q8(v.z, inv))) << 16) |
-                  (static_cast<uint32_t>(static_cast<uint8_t>(q8(v.w, inv))) << 24);
+      packed[j] = q8x4(v.x, v.y, v.z, v.w, inv);
     }
     qrow[c] = make_int4(static_cast<int>(packed[0]), static_cast<int>(packed[1]),
                         static_cast<int>(packed[2]), static_cast<int>(packed[3]));

@@ -6,7 +6,7 @@
 // threads, fully coalesced), and the four threads of a group are four consecutive lanes.
 //
 // Alignment is fused into the GEMV prologue: each thread aligns the 32 activations of its chunk;
-// the group's exponent maximum and NaN/inf flags meet through two xor shuffles; each mantissa
+// the group's exponent maximum and NaN/inf flags meet through two quad lane permutes; each mantissa
 // (an int16 in [-16384, 16384]) is rounded to nearest-even exactly as the reference does.
 //
 // Exact int16 x int4 dots on v_dot4 (signed 8-bit): a mantissa a is split as a = 256 * ah + al with
@@ -71,10 +71,10 @@ __device__ __forceinline__ void align_chunk(const uint32_t xb[32], int mant[32],
     emax = max(emax, e);
     if (e == 255) flags |= (xb[i] & kMant) ? 1 : 2;
   }
-  emax = max(emax, __shfl_xor(emax, 1));
-  emax = max(emax, __shfl_xor(emax, 2));
-  flags |= __shfl_xor(flags, 1);
-  flags |= __shfl_xor(flags, 2);
+  emax = max(emax, lane_xor1(emax));
+  emax = max(emax, lane_xor2(emax));
+  flags |= lane_xor1(flags);
+  flags |= lane_xor2(flags);
   const bool grp_nan = flags & 1;
   const bool grp_inf = (flags & 2) && !grp_nan;
   const int e_eff = max(emax, 14);
@@ -214,8 +214,8 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     int d16 = chunk_dot16(wv[u], act);
-    d16 += __shfl_xor(d16, 1);
-    d16 += __shfl_xor(d16, 2);
+    d16 += lane_xor1(d16);
+    d16 += lane_xor2(d16);
     const int n = nbase + u * R + r;
     if (live && (cc & 3) == 0 && n < a.N) {
       const float ws = from_fp16_bits(a.ws[static_cast<size_t>(n) * G + g]);
@@ -231,8 +231,8 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
   const int slot_c = has_row ? slot : 0;
   float acc = 0.0f;
   for (int gg = bank; gg < G; gg += 4) acc = fadd(acc, terms[slot_c][gg]);
-  const float pair = fadd(acc, __shfl_xor(acc, 1));  // bank 0: b0 + b1, bank 2: b2 + b3
-  const float other = __shfl_xor(pair, 2);
+  const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
+  const float other = lane_xor2(pair);
   const int u = slot_c / R, rr = slot_c - u * R;
   const int n = nbase + u * R + rr;
   if (has_row && bank == 0 && n < a.N) {

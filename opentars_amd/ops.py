@@ -157,6 +157,48 @@ def gemm_rowcol(q, srow, W, scol, bias=None, act: int = ACT_NONE, out: int = OUT
     return _finish(npm, y)
 
 
+def quant_gemm_rowcol(x, mats: Sequence, return_q: bool = False):
+    """Fused per-token quantization + W8A8 for up to 4 matrices sharing it (q/k/v, gate/up):
+    each entry of `mats` is (W, scol) or (W, scol, bias, act, out, out_scale). Returns the list of
+    outputs (and (q, s) first when return_q). Bit-identical to quant_rows + gemm_rowcol per matrix
+    (llm.py:711-731: one ROW_QUANT feeding several QM_ROWCOL GEMMs)."""
+    flat = [x] + [a for m in mats for a in m[:3]]
+    npm = _numpy_mode(*flat)
+    xt = _to_dev(x, torch.float32)
+    if xt.dtype != torch.float32 or xt.dim() != 2:
+        raise ValueError("x must be fp32 [M, K]")
+    M, K = xt.shape
+    if not 1 <= len(mats) <= 4:
+        raise ValueError("1 to 4 matrices")
+    descs, ys, keep = (_lib.W8A8Out * len(mats))(), [], []
+    for i, m in enumerate(mats):
+        W, scol = m[0], m[1]
+        bias = m[2] if len(m) > 2 else None
+        act = m[3] if len(m) > 3 else ACT_NONE
+        out = m[4] if len(m) > 4 else OUT_FP32
+        osc = m[5] if len(m) > 5 else None
+        Wt, st = _to_dev(W, torch.int8), _to_dev(scol, torch.float32)
+        bt = None if bias is None else _to_dev(bias, torch.float32)
+        N = Wt.shape[0]
+        if Wt.dim() != 2 or Wt.shape[1] != K or not Wt.is_contiguous():
+            raise ValueError("W must be a dense [N, K] int8 matrix")
+        _vec(st, N, "scol")
+        if bt is not None:
+            _vec(bt, N, "bias")
+        y = torch.empty((M, N), dtype=_out_dtype(out), device=xt.device)
+        keep += [Wt, st, bt]
+        ys.append(y)
+        descs[i] = _lib.W8A8Out(Wt.data_ptr(), st.data_ptr(), _ptr(bt), y.data_ptr(), _ld(y), N, act, out,
+                                _f32_bits(osc) if out == OUT_INT8 else 0)
+    q = torch.empty((M, K), dtype=torch.int8, device=xt.device) if return_q else None
+    s = torch.empty((M,), dtype=torch.float32, device=xt.device) if return_q else None
+    _check(_lib.lib().tars_quant_gemm_w8a8(xt.data_ptr(), _ld(xt), _ptr(q), K if q is not None else 0, _ptr(s),
+                                           M, K, descs, len(mats), _stream()))
+    res = ([q, s] if return_q else []) + ys
+    out_ = _finish(npm, *res)
+    return list(out_) if isinstance(out_, tuple) else [out_]
+
+
 def gemm_rowcol_ksplit(q, srow, blocks: Sequence, scol, y: torch.Tensor | None = None):
     """K split into blocks W_i [N, K_i] over consecutive column ranges of q, sharing srow and scol:
     per-block W8A8 partials in fp32, added in block order (llm.py:627-635, golden.py:411-412)."""
@@ -240,5 +282,5 @@ def set_w8a8_path(path: str) -> str:
     return {v: k for k, v in codes.items()}[prev]
 
 
-__all__ = ["TarsError", "ContractError", "quant_rows", "gemm_rowcol", "gemm_rowcol_ksplit",
+__all__ = ["TarsError", "ContractError", "quant_rows", "gemm_rowcol", "quant_gemm_rowcol", "gemm_rowcol_ksplit",
            "align_w4_groups", "gemm_w4", "set_w8a8_path", "ESIZE"]

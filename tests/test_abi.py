@@ -154,3 +154,30 @@ def test_codegen_has_no_fused_or_packed_fp32(tmp_path):
     assert not forbidden, sorted(set(forbidden))
     assert "scratch_" not in dis
     assert "v_mfma_i32_16x16x64_i8" in dis and "v_dot4" in dis
+
+
+def test_fused_validation():
+    lib = _lib.lib()
+    W8 = _lib.W8A8Out
+
+    def call(outs, K=1024, q=None, s=None, x=P, lda=0):
+        arr = (W8 * len(outs))(*outs)
+        rc = lib.tars_quant_gemm_w8a8(x, lda, q, 0, s, 1, K, arr, len(outs), None)
+        assert rc != _lib.OK
+        return rc
+
+    good = W8(P + 2 * MB, P + 3 * MB, None, P + 4 * MB, 0, 64, 0, 0, 0)
+    assert call([good], K=1000) == _lib.E_ALIGN
+    assert call([W8(P + 2 * MB, P + 3 * MB, None, P + 4 * MB, 0, 40, 0, 0, 0)]) == _lib.E_ALIGN
+    assert call([W8(P + 2 * MB, P + 3 * MB, None, P + 4 * MB, 0, 64, 9, 0, 0)]) == _lib.E_FIELD
+    assert call([good], q=P + 8 * MB) == _lib.E_ARG                      # q without s
+    assert call([good, good]) == _lib.E_OVERLAP                           # two outputs on one buffer
+    assert call([W8(P + 2 * MB, P + 3 * MB, None, P + 2 * MB + 64, 0, 64, 0, 0, 0)]) == _lib.E_OVERLAP
+    assert call([good], q=P + 16, s=P + 8 * MB) == _lib.E_OVERLAP       # q over x
+    assert call([good] * 5) == _lib.E_ARG
+    assert ctypes_sizeof_desc() == 56
+
+
+def ctypes_sizeof_desc() -> int:
+    import ctypes
+    return ctypes.sizeof(_lib.W8A8Out)

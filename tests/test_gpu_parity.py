@@ -337,3 +337,63 @@ def test_align_w4_groups(bf16):
     q, s = ops.align_w4_groups(cuda(xin), x_is_bf16=bf16)
     wq, ws = F.align_w4_groups(F.bf16_bits_to_f32(xin) if bf16 else x)
     assert same(host(q), wq) and same(host(s), ws)
+
+
+# ------------------------------------------------------------------------------ fused quantize + GEMV
+def fused_case(rng, M, K, Ns, edge_rows=False):
+    x = (rng.normal(0, 1, (M, K)) * np.exp2(rng.integers(-40, 40, (M, 1)))).astype(f32)
+    if edge_rows and M >= 3:
+        x[1] = 0.0                          # zero row: q = 0, s = 0
+        x[2, K // 3] = np.inf               # inf row: inv = 0, s = inf -> NaN outputs
+        if M >= 4:
+            x[3, 1] = np.nan
+    mats = []
+    for i, N in enumerate(Ns):
+        W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+        sc = rng.uniform(1e-3, 1e-2, N).astype(f32)
+        b = rng.normal(0, 1, N).astype(f32) if i % 2 else None
+        act, out = [(ACT_NONE, OUT_FP32), (ACT_SILU, OUT_FP32), (ACT_GELU, OUT_BF16), (ACT_RELU, OUT_INT8)][i % 4]
+        mats.append((W, sc, b, act, out, f32(3.0) if out == OUT_INT8 else None))
+    return x, mats
+
+
+@pytest.mark.parametrize("K", [16, 48, 496, 1024, 2048, 3072, 4112, 6912, 9216])
+@pytest.mark.parametrize("M", [1, 4])
+def test_fused_quant_gemm_matches_separate_ops(K, M):
+    rng = np.random.default_rng(K * 10 + M)
+    ngroups = {16: 2, 48: 4, 496: 3, 1024: 3, 2048: 1, 3072: 2, 4112: 4, 6912: 2, 9216: 3}[K]
+    x, mats = fused_case(rng, M, K, [48, 96, 32, 160][:ngroups], edge_rows=True)
+    outs = ops.quant_gemm_rowcol(cuda(x), [(cuda(W), cuda(sc), None if b is None else cuda(b), a, o, osc)
+                                           for W, sc, b, a, o, osc in mats], return_q=True)
+    q, s = F.quant_rows(x)
+    assert same(host(outs[0]), q) and same(host(outs[1]), s)
+    for (W, sc, b, a, o, osc), y in zip(mats, outs[2:]):
+        want = G.gemm_rowcol(q, s, W, sc, b, act=a, out=o, out_scale=osc)
+        assert same(host(y), want), mismatch(host(y), want)
+
+
+def test_fused_qwen3_layer_groups_full_size():
+    """q/k/v (2048 + 1024 + 1024 rows) and gate/up (2 x 3072 rows) at K = 1024, and the head."""
+    rng = np.random.default_rng(123)
+    for Ns in ([2048, 1024, 1024], [3072, 3072], [151936]):
+        x = rng.normal(0, 1, (1, 1024)).astype(f32)
+        Ws = [rng.integers(-127, 128, (N, 1024), dtype=np.int8) for N in Ns]
+        scs = [rng.uniform(1e-3, 1e-2, N).astype(f32) for N in Ns]
+        outs = ops.quant_gemm_rowcol(cuda(x), [(cuda(W), cuda(sc)) for W, sc in zip(Ws, scs)])
+        q, s = F.quant_rows(x)
+        for W, sc, y in zip(Ws, scs, outs):
+            want = oracle_rowcol_blocked(q, s, W, sc, rows=37984)
+            assert same(host(y), want), (Ns, mismatch(host(y), want))
+
+
+def test_fused_refuses_aliased_outputs():
+    rng = np.random.default_rng(5)
+    x = cuda(rng.normal(0, 1, (1, 64)).astype(f32))
+    W = cuda(rng.integers(-128, 128, (32, 64), dtype=np.int8))
+    sc = cuda(np.ones(32, f32))
+    y = torch.zeros((1, 32), device="cuda")
+    descs = (ops._lib.W8A8Out * 2)(ops._lib.W8A8Out(W.data_ptr(), sc.data_ptr(), None, y.data_ptr(), 128, 32, 0, 0, 0),
+                                   ops._lib.W8A8Out(W.data_ptr(), sc.data_ptr(), None, y.data_ptr(), 128, 32, 0, 0, 0))
+    rc = ops._lib.lib().tars_quant_gemm_w8a8(x.data_ptr(), 256, None, 0, None, 1, 64, descs, 2, None)
+    assert rc == ops._lib.E_OVERLAP
+    assert (host(y) == 0).all()
