@@ -9,8 +9,9 @@ seeded random int8 with per-channel fp32 scales (~596 MB of weights per step), r
 before timing. A step is captured once as a HIP graph (the C ABI validates every call at capture)
 and replayed; `value` = algorithmic HBM bytes of the step / step time.
 
-Also reported (in "configs"): every BASELINE workload as us/call, GB/s and roofline fraction (and
-TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight copies so the 256 MB
+Also reported (in "configs"): each single-GPU workload of the path (Qwen3-0.6B decode shapes, the
+lm_head, the K-split projections, M = 4 / 256 prefill, W4A16 group-128) as us/call, GB/s and
+roofline fraction (and TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight copies so the 256 MB
 MALL cannot serve it; per-kernel durations from HIP events around each launch of the decode step;
 and the CPU baseline (the numpy oracle, single core) on a bounded sample of the same workload.
 
@@ -420,8 +421,8 @@ def cpu_baseline(launches, target_s: float) -> dict:
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build's path is single-GPU (output-channel sharding over "
-              "several GPUs is described in DESIGN.md but not run); use --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the matrix path runs on a single GPU here (sharding the "
+              "output channels over several GPUs is not implemented); use --gpus 1", file=sys.stderr)
         return 2
     os.environ.setdefault("OMP_NUM_THREADS", "1")
     import numpy as np

@@ -185,16 +185,14 @@ __device__ __forceinline__ uint16_t to_bf16_bits(float x) {
   return static_cast<uint16_t>((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
-// numerics.py:21-23: binary16 bits -> fp32, exact for subnormals, canonical NaN
+// numerics.py:21-23: binary16 bits -> fp32, exact for subnormals, canonical NaN (branch-free)
 __device__ __forceinline__ float from_fp16_bits(uint32_t h) {
   const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, f = h & 0x3FFu;
-  if (e == 31) return ffrom(f ? kCanonNaN : (s | kExpo));
-  if (e == 0) {
-    // f * 2^-24: exact (f < 2^10, the product is a normal fp32)
-    const float v = static_cast<float>(f) * 5.9604644775390625e-08f;
-    return ffrom(fbits(v) | s);
-  }
-  return ffrom(s | ((e + 112u) << 23) | (f << 13));
+  // f * 2^-24 is exact (f < 2^10, the product is a normal fp32)
+  const uint32_t sub = fbits(static_cast<float>(f) * 5.9604644775390625e-08f) | s;
+  const uint32_t normal = s | ((e + 112u) << 23) | (f << 13);
+  const uint32_t special = f ? kCanonNaN : (s | kExpo);
+  return ffrom(e == 31 ? special : (e == 0 ? sub : normal));
 }
 
 // Stores one epilogue result in the output format (golden.py:273-280).
@@ -226,10 +224,21 @@ struct RowColEpilogue {
 
   // The same with the row scale given by value (a quantizer fused into the GEMV).
   __device__ __forceinline__ float value_sr(int32_t acc, float sr, bool has_sr, int n) const {
+    return apply(acc, sr, has_sr, scol[scol_per_tensor ? 0 : n], bias ? bias[n] : 0.0f);
+  }
+
+  // The epilogue's operands, fetched early so their latency hides under the weights. Every load
+  // is unconditional (an absent operand reads scol[0], a valid address, and is ignored): a load
+  // behind a branch would make the compiler drain every outstanding load where the paths join.
+  __device__ __forceinline__ float load_scol(int n) const { return scol[scol_per_tensor ? 0 : n]; }
+  __device__ __forceinline__ float load_bias(int n) const { return *(bias ? bias + n : scol); }
+  __device__ __forceinline__ float load_srow(int m) const { return *(srow ? srow + m : scol); }
+
+  __device__ __forceinline__ float apply(int32_t acc, float sr, bool has_sr, float sc, float b) const {
     float y = i2f(acc);
     if (has_sr) y = fmul(y, sr);
-    y = fmul(y, scol[scol_per_tensor ? 0 : n]);
-    if (bias) y = fadd(y, bias[n]);
+    y = fmul(y, sc);
+    if (bias) y = fadd(y, b);
     return act_fn(y, act);
   }
 };

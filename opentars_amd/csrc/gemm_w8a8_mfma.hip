@@ -64,6 +64,12 @@ __global__ __launch_bounds__(64 * KW) void mfma_skinny_kernel(MfmaArgs a) {
   const int li = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16;
   float chain[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // epilogue operands of this lane's column and rows, fetched before the weight stream
+  const float sc = a.epi.load_scol(n0 + li);
+  const float bi = a.epi.load_bias(n0 + li);
+  float sr[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sr[v] = a.epi.load_srow(min(lg * 4 + v, a.M - 1));
 
   for (int sgi = 0; sgi < a.nseg; ++sgi) {
     const Seg sg = a.seg[sgi];
@@ -81,22 +87,29 @@ __global__ __launch_bounds__(64 * KW) void mfma_skinny_kernel(MfmaArgs a) {
 
     const int s0 = (steps * wave) / KW, s1 = (steps * (wave + 1)) / KW;
     const int8_t* wrow = sg.W + static_cast<int64_t>(n0 + li) * sg.K + lg * 16;
-    const int8_t* arow = smem + li * ldsrow + lg * 16;
     const bool a_live = li < a.M;
+    const int8_t* arow = smem + (a_live ? li : 0) * ldsrow + lg * 16;  // dead rows read row 0, zeroed below
     v4i acc = zero;
     int s = s0;
     for (; s + 4 <= s1; s += 4) {
       v4i b[4], x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = ((s + j) * 64 + lg * 16 < sg.K) ? load_stream(wrow + (s + j) * 64) : zero;
+      for (int j = 0; j < 4; ++j)
+        b[j] = load_stream_pred(reinterpret_cast<const v4i*>(wrow + (s + j) * 64), reinterpret_cast<const v4i*>(sg.W),
+                                (s + j) * 64 + lg * 16 < sg.K, zero);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = a_live ? *reinterpret_cast<const v4i*>(arow + (s + j) * 64) : zero;
+      for (int j = 0; j < 4; ++j) {
+        const v4i t = *reinterpret_cast<const v4i*>(arow + (s + j) * 64);
+        x[j] = a_live ? t : zero;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc = mfma(x[j], b[j], acc);
     }
     for (; s < s1; ++s) {
-      const v4i b = (s * 64 + lg * 16 < sg.K) ? load_stream(wrow + s * 64) : zero;
-      const v4i x = a_live ? *reinterpret_cast<const v4i*>(arow + s * 64) : zero;
+      const v4i b = load_stream_pred(reinterpret_cast<const v4i*>(wrow + s * 64), reinterpret_cast<const v4i*>(sg.W),
+                                     s * 64 + lg * 16 < sg.K, zero);
+      const v4i t = *reinterpret_cast<const v4i*>(arow + s * 64);
+      const v4i x = a_live ? t : zero;
       acc = mfma(x, b, acc);
     }
     if (KW > 1) {
@@ -111,7 +124,7 @@ __global__ __launch_bounds__(64 * KW) void mfma_skinny_kernel(MfmaArgs a) {
       for (int v = 0; v < 4; ++v) {
         const int m = lg * 4 + v;
         if (m < a.M) {
-          const float y = a.epi.value(acc[v], m, n);
+          const float y = a.epi.apply(acc[v], sr[v], a.epi.srow != nullptr, sc, bi);
           if (a.ksplit) {
             chain[v] = sgi == 0 ? y : fadd(chain[v], y);
           } else {
@@ -150,6 +163,18 @@ __global__ __launch_bounds__(256) void mfma_tiled_kernel(MfmaArgs a) {
   const int li = lane & 15, lg = lane >> 4;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   float chain[TM][TN][4];
+  // epilogue operands of this lane's columns and rows, fetched before the K loop
+  float sc[TN], bi[TN], sr[TM][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = min(n0 + (wn * TN + j) * 16 + li, a.N - 1);
+    sc[j] = a.epi.load_scol(n);
+    bi[j] = a.epi.load_bias(n);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sr[i][v] = a.epi.load_srow(min(m0 + (wm * TM + i) * 16 + lg * 4 + v, a.M - 1));
 
   for (int sgi = 0; sgi < a.nseg; ++sgi) {
     const Seg sg = a.seg[sgi];
@@ -165,13 +190,14 @@ __global__ __launch_bounds__(256) void mfma_tiled_kernel(MfmaArgs a) {
 #pragma unroll
       for (int t = 0; t < ACH; ++t) {
         const int i = threadIdx.x + t * 256, r = i >> 3, k = kt * kBK + (i & 7) * 16;
-        ra[t] = (m0 + r < a.M && k < sg.K)
-                    ? *reinterpret_cast<const v4i*>(a.A + (m0 + r) * a.lda + sg.koff + k) : zero;
+        ra[t] = load_pred(reinterpret_cast<const v4i*>(a.A + (m0 + r) * a.lda + sg.koff + k),
+                          reinterpret_cast<const v4i*>(a.A), m0 + r < a.M && k < sg.K, zero);
       }
 #pragma unroll
       for (int t = 0; t < WCH; ++t) {
         const int i = threadIdx.x + t * 256, r = i >> 3, k = kt * kBK + (i & 7) * 16;
-        rw[t] = (n0 + r < a.N && k < sg.K) ? load_stream(sg.W + static_cast<int64_t>(n0 + r) * sg.K + k) : zero;
+        rw[t] = load_stream_pred(reinterpret_cast<const v4i*>(sg.W + static_cast<int64_t>(n0 + r) * sg.K + k),
+                                 reinterpret_cast<const v4i*>(sg.W), n0 + r < a.N && k < sg.K, zero);
       }
     };
     fetch(0);
@@ -214,7 +240,7 @@ __global__ __launch_bounds__(256) void mfma_tiled_kernel(MfmaArgs a) {
         for (int v = 0; v < 4; ++v) {
           const int m = m0 + (wm * TM + i) * 16 + lg * 4 + v;
           if (m < a.M && n < a.N) {
-            const float y = a.epi.value(acc[i][j][v], m, n);
+            const float y = a.epi.apply(acc[i][j][v], sr[i][v], a.epi.srow != nullptr, sc[j], bi[j]);
             if (a.ksplit) {
               chain[i][j][v] = sgi == 0 ? y : fadd(chain[i][j][v], y);
             } else {

@@ -48,14 +48,22 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   int acc[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) acc[u] = 0;
+  // this lane's epilogue row (lane `sub` finishes row n0 + sub) and its operands
+  const int ne = n0 + sub;
+  const bool epi_lane = sub < U && ne < a.N;
+  const int nc = epi_lane ? ne : 0;
+  float sr = 0.0f, sc = 0.0f, bi = 0.0f;
 
   if constexpr (CPL > 0) {
+    // issue order: activations, weights, then the epilogue operands
     v4i xv[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = sub + j * L;
-      xv[j] = c < C ? xrow[c] : zero;
+      xv[j] = load_pred(xrow + c, xrow, c < C, zero);
     }
+    issue_fence();
+    const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
     v4i wv[U][CPL];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -64,21 +72,31 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        wv[u][j] = (n < a.N && c < C) ? load_stream(wrow + c) : zero;
+        wv[u][j] = load_stream_pred(wrow + c, wbase, n < a.N && c < C, zero);
       }
     }
+    issue_fence();
+    sc = a.epi.load_scol(nc);
+    bi = a.epi.load_bias(nc);
+    sr = a.epi.load_srow(m);
+    issue_fence();
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[u] = dot16(wv[u][j], xv[j], acc[u]);
   } else {
+    sc = a.epi.load_scol(nc);
+    bi = a.epi.load_bias(nc);
+    sr = a.epi.load_srow(m);
+    const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
     for (int c = sub; c < C; c += L) {
       const v4i xv = xrow[c];
       v4i wv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int n = n0 + u;
-        wv[u] = n < a.N ? load_stream(reinterpret_cast<const v4i*>(a.W + static_cast<int64_t>(n) * a.K) + c) : zero;
+        wv[u] = load_stream_pred(reinterpret_cast<const v4i*>(a.W + static_cast<int64_t>(n) * a.K) + c, wbase,
+                                 n < a.N, zero);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) acc[u] = dot16(wv[u], xv, acc[u]);
@@ -93,10 +111,9 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
 #pragma unroll
   for (int u = 0; u < U; ++u)
     if (sub == u) mine = acc[u];
-  const int n = n0 + sub;
-  if (sub < U && n < a.N) {
-    const float y = a.epi.value(mine, m, n);
-    store_out(a.Y, m * a.ldy, n, a.epi.out, y, a.epi.out_scale);
+  if (epi_lane) {
+    const float y = a.epi.apply(mine, sr, a.epi.srow != nullptr, sc, bi);
+    store_out(a.Y, m * a.ldy, ne, a.epi.out, y, a.epi.out_scale);
   }
 }
 
@@ -107,8 +124,11 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_kernel(KSplitArgs a
   const int wave = threadIdx.x >> 6;
   const int m = blockIdx.y;
   const int n0 = (blockIdx.x * kWaves + wave) * U;
-  const float sr = a.srow ? a.srow[m] : 1.0f;
+  const float sr = *(a.srow ? a.srow + m : a.scol);  // unconditional (see fp32_contract.h)
   const v4i zero = {0, 0, 0, 0};
+  float sc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) sc[u] = a.scol[min(n0 + u, a.N - 1)];  // fetched before the stream
   float y[U];
   for (int b = 0; b < a.nblocks; ++b) {
     const int C = a.K[b] >> 4;
@@ -122,7 +142,8 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_kernel(KSplitArgs a
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int n = n0 + u;
-        wv[u] = n < a.N ? load_stream(reinterpret_cast<const v4i*>(a.W[b] + static_cast<int64_t>(n) * a.K[b]) + c) : zero;
+        wv[u] = load_stream_pred(reinterpret_cast<const v4i*>(a.W[b] + static_cast<int64_t>(n) * a.K[b]) + c,
+                                 reinterpret_cast<const v4i*>(a.W[b]), n < a.N, zero);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) acc[u] = dot16(wv[u], xv, acc[u]);
@@ -133,8 +154,7 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_kernel(KSplitArgs a
       // the block's partial: the full W8A8 epilogue without bias or activation
       float part = i2f(s);
       if (a.srow) part = fmul(part, sr);
-      const int n = min(n0 + u, a.N - 1);
-      part = fmul(part, a.scol[n]);
+      part = fmul(part, sc[u]);
       y[u] = b == 0 ? part : fadd(y[u], part);
     }
   }
@@ -183,7 +203,20 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   const int n0 = (lb * (kWaves * kSlots) + wave * kSlots + slot) * U;
   const v4i zero = {0, 0, 0, 0};
 
-  // 1. the weight stream starts first
+  // Issue order matters: vmcnt counts loads in order, so the fp32 activations go first (the
+  // quantizer waits on them alone), then the weights, then the epilogue operands.
+  constexpr int XV = CPL > 0 ? (L == 64 ? CPL : 1) : 1;  // float4s of the row per thread (K <= 1024 XV)
+  const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(a.x) + m * a.lda);
+  const int K4 = a.K >> 2;
+  float4 xr[XV];
+  if constexpr (CPL > 0) {
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      xr[j] = load_pred(xrow + i, xrow, i < K4, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
+    }
+  }
+  issue_fence();
   v4i wv[U][CPL > 0 ? CPL : 1];
   if constexpr (CPL > 0) {
 #pragma unroll
@@ -193,18 +226,38 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        wv[u][j] = (n < N && c < C) ? load_stream(wrow + c) : zero;
+        wv[u][j] = load_stream_pred(wrow + c, reinterpret_cast<const v4i*>(W), n < N && c < C, zero);
       }
     }
   }
+  RowColEpilogue epi = a.g[0].epi;
+  void* Yout = a.g[0].Y;
+  int64_t ldy = a.g[0].ldy;
+#pragma unroll
+  for (int i = 1; i < kMaxGroups; ++i)
+    if (g == i) {
+      epi = a.g[i].epi;
+      Yout = a.g[i].Y;
+      ldy = a.g[i].ldy;
+    }
+  const int ne = n0 + sub;
+  const bool epi_lane = sub < U && ne < N;
+  issue_fence();
+  const float sc = epi.load_scol(epi_lane ? ne : 0);
+  const float bi = epi.load_bias(epi_lane ? ne : 0);
+  issue_fence();
 
-  // 2. the workgroup quantizes row m into LDS
-  const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(a.x) + m * a.lda);
-  const int K4 = a.K >> 2;
+  // the workgroup quantizes row m into LDS
   uint32_t mx = 0;
-  for (int i = threadIdx.x; i < K4; i += kThreads) {
-    const float4 v = xrow[i];
-    mx = max(mx, max(max(abs_bits_ftz(v.x), abs_bits_ftz(v.y)), max(abs_bits_ftz(v.z), abs_bits_ftz(v.w))));
+  if constexpr (CPL > 0) {
+#pragma unroll
+    for (int j = 0; j < XV; ++j)
+      mx = max(mx, max(max(abs_bits_ftz(xr[j].x), abs_bits_ftz(xr[j].y)), max(abs_bits_ftz(xr[j].z), abs_bits_ftz(xr[j].w))));
+  } else {
+    for (int i = threadIdx.x; i < K4; i += kThreads) {
+      const float4 v = xrow[i];
+      mx = max(mx, max(max(abs_bits_ftz(v.x), abs_bits_ftz(v.y)), max(abs_bits_ftz(v.z), abs_bits_ftz(v.w))));
+    }
   }
   mx = group_max<64>(mx);
   if (lane == 0) wave_max[wave] = mx;
@@ -213,11 +266,23 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   float inv, sr;
   quant_scales(mx, inv, sr);
   const bool store_q = a.q != nullptr && blockIdx.x == 0;
-  for (int i = threadIdx.x; i < K4; i += kThreads) {
-    const float4 v = xrow[i];
-    const uint32_t b = q8x4(v.x, v.y, v.z, v.w, inv);
-    reinterpret_cast<uint32_t*>(qsh)[i] = b;
-    if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
+  if constexpr (CPL > 0) {
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      if (i < K4) {
+        const uint32_t b = q8x4(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv);
+        reinterpret_cast<uint32_t*>(qsh)[i] = b;
+        if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < K4; i += kThreads) {
+      const float4 v = xrow[i];
+      const uint32_t b = q8x4(v.x, v.y, v.z, v.w, inv);
+      reinterpret_cast<uint32_t*>(qsh)[i] = b;
+      if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
+    }
   }
   if (store_q && threadIdx.x == 0) a.s[m] = sr;
   __syncthreads();
@@ -241,7 +306,8 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int n = n0 + u;
-        w[u] = n < N ? load_stream(reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * a.K) + c) : zero;
+        w[u] = load_stream_pred(reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * a.K) + c,
+                                reinterpret_cast<const v4i*>(W), n < N, zero);
       }
       const v4i xv = xq[c];
 #pragma unroll
@@ -255,20 +321,9 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 #pragma unroll
   for (int u = 0; u < U; ++u)
     if (sub == u) mine = acc[u];
-  const int n = n0 + sub;
-  if (sub < U && n < N) {
-    RowColEpilogue epi = a.g[0].epi;
-    void* Y = a.g[0].Y;
-    int64_t ldy = a.g[0].ldy;
-#pragma unroll
-    for (int i = 1; i < kMaxGroups; ++i)
-      if (g == i) {
-        epi = a.g[i].epi;
-        Y = a.g[i].Y;
-        ldy = a.g[i].ldy;
-      }
-    const float y = epi.value_sr(mine, sr, true, n);
-    store_out(Y, m * ldy, n, epi.out, y, epi.out_scale);
+  if (epi_lane) {
+    const float y = epi.apply(mine, sr, true, sc, bi);
+    store_out(Yout, m * ldy, ne, epi.out, y, epi.out_scale);
   }
 }
 

@@ -10,6 +10,26 @@
 
 namespace tars {
 
+// Predicated loads without branches. A load behind a branch makes the compiler's wait-counter
+// bookkeeping assume either path where they join, so waiting for one early load (the activations)
+// would also wait for every later one (the weight stream). These helpers always issue the load, on
+// a valid fallback address when the predicate is false, and select the value afterwards.
+template <class T>
+__device__ __forceinline__ T load_pred(const T* p, const T* safe, bool pred, T zero) {
+  const T v = *(pred ? p : safe);
+  return pred ? v : zero;
+}
+template <class T>
+__device__ __forceinline__ T load_stream_pred(const T* p, const T* safe, bool pred, T zero) {
+  const T v = __builtin_nontemporal_load(pred ? p : safe);
+  return pred ? v : zero;
+}
+
+// Keeps the machine scheduler from moving instructions across this point. Used between groups of
+// loads whose issue order matters for the wait counters (activations before weights before
+// epilogue operands).
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 struct W8A8Args {
   const int8_t* A;  // [M, K] rows at stride lda bytes
   int64_t lda;

@@ -57,49 +57,64 @@ __device__ __forceinline__ void load_chunk_bits(const void* x, int64_t lda, int 
     }
   }
 #pragma unroll
-  for (int i = 0; i < 32; ++i)
-    if ((xb[i] & kExpo) == 0) xb[i] &= kSign;  // ftz
+  for (int i = 0; i < 32; ++i) xb[i] = (xb[i] & kExpo) ? xb[i] : (xb[i] & kSign);  // ftz
 }
 
-// Aligns one chunk within its group of 4 consecutive lanes (every lane of the wave must call it).
-// Outputs the signed mantissas and the group's fp32 scale encoding.
-__device__ __forceinline__ void align_chunk(const uint32_t xb[32], int mant[32], uint32_t& scale_bits) {
+// Aligns NE elements held by each of GL consecutive lanes that together form one 128-wide group
+// (NE * GL == 128; every lane of the wave must call it, dead lanes on shadow data). Outputs the
+// signed mantissas and the group's fp32 scale encoding. Straight-line selects, no per-element
+// branches: the shift is clamped to 31, and a shift of 25 or more then rounds to 0 by itself (the
+// 24-bit significand is below the half-way point), as the reference requires.
+template <int NE, int GL>
+__device__ __forceinline__ void align_elems(const uint32_t* xb, int* mant, uint32_t& scale_bits) {
+  static_assert(NE * GL == kGroup, "a group is 128 elements");
   int emax = 0, flags = 0;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
+  for (int i = 0; i < NE; ++i) {
     const int e = (xb[i] >> 23) & 0xFF;
     emax = max(emax, e);
-    if (e == 255) flags |= (xb[i] & kMant) ? 1 : 2;
+    flags |= e == 255 ? ((xb[i] & kMant) ? 1 : 2) : 0;
   }
-  emax = max(emax, lane_xor1(emax));
-  emax = max(emax, lane_xor2(emax));
-  flags |= lane_xor1(flags);
-  flags |= lane_xor2(flags);
+  emax = group_reduce<GL>(emax, OpMaxU{});
+  flags = group_reduce<GL>(flags, OpOr{});
   const bool grp_nan = flags & 1;
-  const bool grp_inf = (flags & 2) && !grp_nan;
+  const bool grp_inf = ((flags & 2) != 0) & !grp_nan;
   const int e_eff = max(emax, 14);
+  // Round-to-nearest-even right shift as (sig + 2^(sh-1) - 1 + lsb) >> sh (equal to the reference's
+  // kept/dropped/half rule for every 24-bit significand and shift; checked exhaustively on the CPU).
+  // Inputs are flushed, so exponent 0 means a zero: its significand is taken as 0 and rounds to 0.
+  if (__builtin_amdgcn_ballot_w64(flags != 0) == 0) {
+    // no NaN or infinity anywhere in this wave (the usual case)
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const uint32_t b = xb[i];
-    const int e = (b >> 23) & 0xFF;
-    const uint32_t frac = b & kMant;
-    const int sh = 10 + e_eff - e;  // >= 10
-    int mag = 0;
-    if (e != 0 && e != 255 && sh < 25) {
-      const uint32_t sig = frac | (1u << 23);
-      const uint32_t kept = sig >> sh;
-      const uint32_t dropped = sig & ((1u << sh) - 1u);
-      const uint32_t half = 1u << (sh - 1);
-      mag = static_cast<int>(kept + ((dropped > half || (dropped == half && (kept & 1u))) ? 1u : 0u));
+    for (int i = 0; i < NE; ++i) {
+      const uint32_t b = xb[i];
+      const int e = (b >> 23) & 0xFF;
+      const uint32_t sig = e ? ((b & kMant) | (1u << 23)) : 0u;
+      const uint32_t sh = static_cast<uint32_t>(min(10 + e_eff - e, 31));  // >= 10
+      const int mag = static_cast<int>((sig + ((1u << (sh - 1u)) - 1u) + ((sig >> sh) & 1u)) >> sh);
+      mant[i] = (b & kSign) ? -mag : mag;
     }
-    if (grp_inf && e == 255 && frac == 0) mag = 16384;
-    if (grp_nan) mag = 0;
-    mant[i] = (b & kSign) ? -mag : mag;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const uint32_t b = xb[i];
+      const int e = (b >> 23) & 0xFF;
+      const uint32_t frac = b & kMant;
+      const uint32_t sig = ((e != 0) & (e != 255)) ? (frac | (1u << 23)) : 0u;
+      const uint32_t sh = static_cast<uint32_t>(min(10 + e_eff - e, 31));
+      int mag = static_cast<int>((sig + ((1u << (sh - 1u)) - 1u) + ((sig >> sh) & 1u)) >> sh);
+      mag = (grp_inf & (e == 255) & (frac == 0)) ? 16384 : mag;
+      mag = grp_nan ? 0 : mag;
+      mant[i] = (b & kSign) ? -mag : mag;
+    }
   }
   uint32_t sb = emax == 0 ? 0u : static_cast<uint32_t>(e_eff - 13) << 23;
-  if (grp_inf) sb = kExpo;
-  if (grp_nan) sb = kCanonNaN;
-  scale_bits = sb;
+  sb = grp_inf ? kExpo : sb;
+  scale_bits = grp_nan ? kCanonNaN : sb;
+}
+
+__device__ __forceinline__ void align_chunk(const uint32_t xb[32], int mant[32], uint32_t& scale_bits) {
+  align_elems<32, 4>(xb, mant, scale_bits);
 }
 
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
@@ -177,9 +192,20 @@ __global__ __launch_bounds__(kThreads) void align_w4_kernel(AlignArgs a) {
 }
 
 // ---------------------------------------------------------------------------- GEMV
-// U: rows each thread streams per pass. R = 256 / C rows share a workgroup pass (C = K / 32).
-template <int U>
+// U: rows each thread streams. R = 256 / C rows share a workgroup pass (C = K / 32 chunks per row).
+//
+// 1. Each thread issues its weight loads (U rows x 16 bytes) first.
+// 2. The workgroup aligns activation row m once, cooperatively: 8 consecutive lanes own one
+//    128-wide group (16 elements each), meet their exponent maximum and NaN/inf flags in an 8-lane
+//    DPP reduction, and write the split signed byte planes of their mantissas to LDS in the layout
+//    the dot product reads (per 32-element chunk: lo_even, lo_odd, hi_even, hi_odd, 4 dwords each),
+//    plus the group scale.
+// 3. Each thread reads its chunk's 64 bytes, forms the exact dots, the four lanes of a group add
+//    theirs (quad permutes), the group leader writes the fp32 term to LDS, and four threads per row
+//    run the bank chains.
+template <int U, bool BF16>
 __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
+  extern __shared__ __align__(16) uint32_t act_lds[];  // C * 16 dwords of byte planes, then G scales
   __shared__ float terms[64][65];
   const int C = a.K / 32;
   const int G = a.K / kGroup;
@@ -193,24 +219,118 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
   const int cc = live ? c : 0;
   const int g = cc >> 2;
 
-  uint32_t xb[32];
-  load_chunk_bits(a.x, a.lda, a.bf16, m, cc, xb);
-  int mant[32];
-  uint32_t xs_bits;
-  align_chunk(xb, mant, xs_bits);
-  const ActBytes act = split_bytes(mant);
-  const float xs = ffrom(xs_bits);
-
   const int nbase = blockIdx.x * rows_per_block;
   const size_t row_bytes = static_cast<size_t>(a.K / 2);
+
+  // Issue order matters: vmcnt counts loads in order, so the activation loads go first (the
+  // alignment waits on them alone), then the weights, then the group scales the epilogue needs.
+  // Lane i of the 8 * G alignment lanes owns elements [16 i, 16 i + 16) of row m; K <= 8192 means
+  // at most two passes of 256 lanes.
+  const char* xrow = static_cast<const char*>(a.x) + m * a.lda;
+  const int npass = (8 * G + kThreads - 1) / kThreads;
+  uint32_t xb[2][16];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    // pass 1 exists only for K > 4096; when it does not, its loads read shadow data (always
+    // issued, never branched around: see load_pred) and the results are never used
+    const int i = p * kThreads + tid;
+    const int ii = i < 8 * G ? i : (i & 7);  // dead lanes shadow group 0 (whole 8-lane groups)
+    if constexpr (BF16) {
+      const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * ii);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const v4u v = src[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xb[p][8 * q + 2 * j] = v[j] << 16;
+          xb[p][8 * q + 2 * j + 1] = v[j] & 0xFFFF0000u;
+        }
+      }
+    } else {
+      const v4u* src = reinterpret_cast<const v4u*>(xrow + 64 * ii);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const v4u v = src[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xb[p][4 * q + j] = v[j];
+      }
+    }
+  }
+  issue_fence();
   v4u wv[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int n = nbase + u * R + r;
-    wv[u] = (live && n < a.N)
-                ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(a.Wp + n * row_bytes) + cc)
-                : v4u{0u, 0u, 0u, 0u};
+    wv[u] = load_stream_pred(reinterpret_cast<const v4u*>(a.Wp + n * row_bytes) + cc,
+                             reinterpret_cast<const v4u*>(a.Wp), live && n < a.N, v4u{0u, 0u, 0u, 0u});
   }
+  issue_fence();
+  uint32_t wsb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int n = min(nbase + u * R + r, a.N - 1);
+    wsb[u] = a.ws[static_cast<size_t>(n) * G + g];
+  }
+  // this thread's epilogue row (four threads per row run the bank chains) and its bias, fetched
+  // unconditionally from a valid address
+  const int slot = tid >> 2;
+  const int bank = tid & 3;
+  const bool has_row = slot < rows_per_block;
+  const int slot_c = has_row ? slot : 0;
+  const int ue = slot_c / R, re = slot_c - ue * R;
+  const int ne = nbase + ue * R + re;
+  const float bias_v = *(a.bias ? a.bias + min(ne, a.N - 1) : reinterpret_cast<const float*>(a.ws));
+  issue_fence();
+
+  // cooperative alignment of row m into LDS byte planes
+  float* xs_lds = reinterpret_cast<float*>(act_lds + C * 16);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    if (p < npass) {
+      const int i = p * kThreads + tid;
+      const bool valid = i < 8 * G;
+      const int ii = valid ? i : (i & 7);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xb[p][j] = (xb[p][j] & kExpo) ? xb[p][j] : (xb[p][j] & kSign);  // ftz
+      int mant[16];
+      uint32_t sb;
+      align_elems<16, 8>(xb[p], mant, sb);
+      if (valid) {
+        int lo[16], hi[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          lo[j] = static_cast<int8_t>(mant[j] & 0xFF);
+          hi[j] = (mant[j] - lo[j]) >> 8;
+        }
+        const int chunk = ii >> 1, half = ii & 1;
+        uint32_t* dst = act_lds + chunk * 16 + 2 * half;
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          dst[0 + d] = pack4(lo[8 * d], lo[8 * d + 2], lo[8 * d + 4], lo[8 * d + 6]);
+          dst[4 + d] = pack4(lo[8 * d + 1], lo[8 * d + 3], lo[8 * d + 5], lo[8 * d + 7]);
+          dst[8 + d] = pack4(hi[8 * d], hi[8 * d + 2], hi[8 * d + 4], hi[8 * d + 6]);
+          dst[12 + d] = pack4(hi[8 * d + 1], hi[8 * d + 3], hi[8 * d + 5], hi[8 * d + 7]);
+        }
+        if ((ii & 7) == 0) xs_lds[ii >> 3] = ffrom(sb);
+      }
+    }
+  }
+  __syncthreads();
+
+  ActBytes act;
+  {
+    const v4u* src = reinterpret_cast<const v4u*>(act_lds + cc * 16);
+    const v4u le = src[0], lo = src[1], he = src[2], ho = src[3];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      act.lo_even[d] = le[d];
+      act.lo_odd[d] = lo[d];
+      act.hi_even[d] = he[d];
+      act.hi_odd[d] = ho[d];
+    }
+  }
+  const float xs = xs_lds[g];
+
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     int d16 = chunk_dot16(wv[u], act);
@@ -218,28 +338,21 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
     d16 += lane_xor2(d16);
     const int n = nbase + u * R + r;
     if (live && (cc & 3) == 0 && n < a.N) {
-      const float ws = from_fp16_bits(a.ws[static_cast<size_t>(n) * G + g]);
-      terms[u * R + r][g] = fmul(fmul(i2f(d16 >> 4), ws), xs);
+      terms[u * R + r][g] = fmul(fmul(i2f(d16 >> 4), from_fp16_bits(wsb[u])), xs);
     }
   }
   __syncthreads();
 
   // four bank chains per row, then (b0 + b1) + (b2 + b3)
-  const int slot = tid >> 2;
-  const int bank = tid & 3;
-  const bool has_row = slot < rows_per_block;
-  const int slot_c = has_row ? slot : 0;
   float acc = 0.0f;
   for (int gg = bank; gg < G; gg += 4) acc = fadd(acc, terms[slot_c][gg]);
   const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
   const float other = lane_xor2(pair);
-  const int u = slot_c / R, rr = slot_c - u * R;
-  const int n = nbase + u * R + rr;
-  if (has_row && bank == 0 && n < a.N) {
+  if (has_row && bank == 0 && ne < a.N) {
     float y = fadd(pair, other);
-    if (a.bias) y = fadd(y, a.bias[n]);
+    if (a.bias) y = fadd(y, bias_v);
     y = act_fn(y, a.act);
-    store_out(a.Y, m * a.ldy, n, a.out, y, a.out_scale);
+    store_out(a.Y, m * a.ldy, ne, a.out, y, a.out_scale);
   }
 }
 
@@ -249,7 +362,12 @@ hipError_t go_w4(const W4Args& a, hipStream_t s) {
   const int R = kThreads / C;
   const int rows = R * U;
   const dim3 grid((a.N + rows - 1) / rows, a.M);
-  hipLaunchKernelGGL(gemv_w4a16_kernel<U>, grid, dim3(kThreads), 0, s, a);
+  const size_t lds = static_cast<size_t>(C) * 64 + static_cast<size_t>(a.K / kGroup) * 4;
+  if (a.bf16) {
+    hipLaunchKernelGGL((gemv_w4a16_kernel<U, true>), grid, dim3(kThreads), lds, s, a);
+  } else {
+    hipLaunchKernelGGL((gemv_w4a16_kernel<U, false>), grid, dim3(kThreads), lds, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -263,9 +381,12 @@ hipError_t launch_align_w4(const AlignArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
-  // rows per block R * U must not exceed the 64 LDS term rows
+  // Rows per block R * U must not exceed the 64 LDS term rows. Long rows (R <= 2, K >= 4096)
+  // take 8 rows per thread so the activation row is read and aligned once per 8 * R weight rows;
+  // shorter rows take 4, which keeps >= 600 workgroups at N = 12288 (measured on MI355X:
+  // K=6144 N=1536 8.0 us at U=8 vs 10.2 at U=4; K=1536 N=12288 8.7 us at U=4 vs 9.3 at U=8).
   const int R = kThreads / (a.K / 32);
-  if (R * 8 <= 64 && R > 1) return go_w4<8>(a, s);
+  if (R <= 2) return go_w4<8>(a, s);
   if (R * 4 <= 64) return go_w4<4>(a, s);
   if (R * 2 <= 64) return go_w4<2>(a, s);
   return go_w4<1>(a, s);

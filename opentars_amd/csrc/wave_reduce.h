@@ -31,6 +31,10 @@ struct OpMaxU {
   }
 };
 
+struct OpOr {
+  __device__ __forceinline__ int operator()(int a, int b) const { return a | b; }
+};
+
 template <int L, class Op>
 __device__ __forceinline__ int group_reduce(int v, Op op) {
   static_assert(L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "group of 4..64 lanes");

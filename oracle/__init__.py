@@ -1,7 +1,7 @@
 """CPU oracle for the quantized matrix path -- TEST INFRASTRUCTURE ONLY.
 
 A plain numpy restatement of the openTARS golden model's arithmetic for the W8A8 / W4A16 matrix
-path (tars_mini/numerics.py, tars_mini/golden.py). It is the checker the HIP kernels are compared
+path (tars_mini/numerics.py, tars_mini/golden.py). It is the reference the HIP kernels are compared
 against, bit for bit, and the timed CPU baseline in the benchmark. Only the test suite, the smoke
 check and the benchmark's CPU-baseline leg may import it; the product package never does.
 

@@ -50,3 +50,18 @@ def test_q8_with_flushed_multiplier():
             y = np.where(np.isnan(y), f32(0), np.rint(y))
             lean = np.clip(y, -127, 127).astype(np.int8)
         assert (lean == F.q8(x, inv)).all(), inv
+
+
+def test_rne_shift_by_add_equals_the_reference_rounding():
+    """The aligner's round-to-nearest-even right shift of a 24-bit significand, written as
+    (sig + 2^(sh-1) - 1 + ((sig >> sh) & 1)) >> sh, equals the reference's kept/dropped/half rule
+    (numerics.py:80-89) for every significand and every shift 10..31 (exhaustive)."""
+    sig = (np.arange(1 << 23, dtype=np.int64) | (1 << 23))
+    for sh in range(10, 32):
+        kept = sig >> sh
+        dropped = sig & ((1 << sh) - 1)
+        half = 1 << (sh - 1)
+        ref = kept + ((dropped > half) | ((dropped == half) & ((kept & 1) == 1)))
+        fast = (sig + (half - 1) + ((sig >> sh) & 1)) >> sh
+        assert (ref == fast).all(), sh
+        assert fast.max() <= (1 << 14) or sh < 10  # mantissas stay within 16384 for sh >= 10
