@@ -208,6 +208,25 @@ __device__ __forceinline__ void store_out(void* Y, int64_t byte_row, int n, int 
   }
 }
 
+// store_out for four consecutive columns n .. n + 3 in one vector store (n % 4 == 0; rows and
+// the output base are 16-byte aligned, so the 16/8/4-byte store is naturally aligned).
+__device__ __forceinline__ void store_out4(void* Y, int64_t byte_row, int n, int out, const float (&y)[4],
+                                           float out_scale) {
+  char* row = static_cast<char*>(Y) + byte_row;
+  if (out == 0) {
+    *reinterpret_cast<float4*>(row + 4 * n) = make_float4(ftz(y[0]), ftz(y[1]), ftz(y[2]), ftz(y[3]));
+  } else if (out == 1) {
+    *reinterpret_cast<uint2*>(row + 2 * n) =
+        make_uint2(to_bf16_bits(y[0]) | static_cast<uint32_t>(to_bf16_bits(y[1])) << 16,
+                   to_bf16_bits(y[2]) | static_cast<uint32_t>(to_bf16_bits(y[3])) << 16);
+  } else {
+    uint32_t v = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v |= static_cast<uint32_t>(static_cast<uint8_t>(q8(y[q], out_scale))) << (8 * q);
+    *reinterpret_cast<uint32_t*>(row + n) = v;
+  }
+}
+
 // The W8A8 epilogue after the exact integer sum (golden.py:340-349).
 struct RowColEpilogue {
   const float* srow;   // nullptr: no row scale (QM_CHANNEL / QM_TENSOR)

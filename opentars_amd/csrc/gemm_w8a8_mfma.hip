@@ -1,25 +1,23 @@
 // W8A8 GEMM on INT8 MFMA (tars_mini/golden.py:326-349 for prefill rows, M >= 2).
 //
 // v_mfma_i32_16x16x64_i8 computes a 16x16 int32 tile over 64 k per instruction. Lane l supplies
-// 16 bytes of A row (l % 16) and 16 bytes of B column (l % 16) at k = 16 * (l / 16) .. + 15 of
-// the step; both operands use the same lane -> k map, so each dot product is the exact sum over
-// all 64 k whatever the hardware's internal k order. Lane l receives D[4 * (l / 16) + v][l % 16],
-// v = 0..3. Integer accumulation is exact, so K may be split across waves and summed in any order.
+// 16 bytes of A row (l % 16) and 16 bytes of B column (l % 16); lane l receives
+// D[4 * (l / 16) + v][l % 16], v = 0..3. Which 16 bytes of K a lane supplies is free as long as A
+// and B use the same map: each dot product is then the exact sum over the instruction's 64 k.
+// Integer accumulation is exact, so K may be split across waves and summed in any order.
 //
-// Two kernels:
-//  * skinny (M <= 16, K <= 4096 per block): the decode/prefill chunk (M = 4). The activation rows
-//    are staged once in LDS (every wave and every column tile reuses them); weights have no reuse
-//    at this M, so each wave streams its 16 weight rows straight into B fragments (16 contiguous
-//    bytes per lane, 4 steps in flight). A workgroup owns 16 output columns and its waves split
-//    the K steps; partial int32 tiles meet in LDS.
-//  * tiled (any M): BM x BN tiles, 128-byte K tiles of A and W staged through padded LDS rows
-//    (16 bytes of padding keep ds_read_b128 conflict-free), the next K tile prefetched into
-//    registers while the current one feeds the MFMAs; 2 x 2 waves, each BM/2 x BN/2.
-// Both run the golden fp32 epilogue per element (or, for a K split, the partial and the in-order
-// fp32 adds across blocks).
+// One kernel family (mfma_direct_kernel<TM, TN, KW, D>): a workgroup owns a 16 TM x 16 TN output
+// tile and KW waves that split its K range; every wave loads its share of all 16 (TM + TN) rows
+// straight into MFMA operand registers (no LDS staging: at these sizes the operands have no reuse
+// inside a workgroup once K is split across its waves), and the int32 partial tiles meet in LDS
+// for the golden fp32 epilogue (or, for a K split, the per-block epilogue and the in-order fp32
+// adds across blocks). Measured on MI355X against the earlier LDS-staged 64 x 64 tiles with one
+// K tile in flight: M=256 K=1024 N=3072 19.2 -> 10.2 us, M=256 K=3072 N=1024 40.0 -> 10.6 us,
+// M=4 K=3072 N=1024 6.6 -> 5.9 us, bit-identical outputs.
 //
-// Roofline: at M = 4 HBM (every weight byte read once); at M = 256 still HBM on this chip's
-// ~625 op/B ridge, with INT8 MFMA utilisation reported beside it.
+// Roofline: at M = 4 HBM (every weight byte read once); at M = 256 the int32 MFMA work is small
+// (1.6 GOP) and the kernel is bound by operand traffic from L2 (the 32 x 32 tiles re-read A and W
+// 8 and 96 times), with INT8 MFMA utilisation reported beside it.
 #include "kernels.h"
 
 namespace tars {
@@ -45,253 +43,176 @@ struct MfmaArgs {
   int M, N;
 };
 
-__device__ __forceinline__ v4i load_stream(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
-}
-
 __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// ------------------------------------------------------------------------------------ skinny
-template <int KW>
-__global__ __launch_bounds__(64 * KW) void mfma_skinny_kernel(MfmaArgs a) {
-  extern __shared__ __align__(16) int8_t smem[];
-  __shared__ v4i red[KW > 1 ? KW - 1 : 1][64];
+// ------------------------------------------------------------------------------------ direct
+// MFMA operands loaded straight from global memory into registers, no LDS staging. A 128-byte K
+// chunk of a 16-row tile is read as 32 contiguous bytes per lane: lane l takes row l % 16, bytes
+// 32 * (l / 16) .. + 31 of the chunk; the first 16 bytes feed the chunk's first MFMA and the last
+// 16 its second. A and W use the same byte -> (instruction, lane) map, so the two MFMAs together
+// add every k of the chunk exactly once. The KW waves of a workgroup split the chunks (each wave
+// reads its own K range of all BM + BN rows once, the next chunk in flight while the current one
+// feeds the MFMAs); the int32 partial tiles meet in LDS, where each thread then owns 4 consecutive
+// columns of one row for the epilogue and a 4-wide store.
+template <int TM, int TN, int KW, int D, bool STREAM_W>
+__global__ __launch_bounds__(64 * KW) void mfma_direct_kernel(MfmaArgs a) {
+  constexpr int BM = 16 * TM, BN = 16 * TN;
+  constexpr int LDR = BN + 4;             // int32 pitch of a reduction row
+  constexpr int NT = 64 * KW;
+  constexpr int SLOTS = BM * BN / 4;      // 4-column groups of the tile
+  constexpr int PER = (SLOTS + NT - 1) / NT;
+  extern __shared__ __align__(16) int32_t red[];  // [KW][BM][LDR]
   const v4i zero = {0, 0, 0, 0};
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  float chain[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  // epilogue operands of this lane's column and rows, fetched before the weight stream
-  const float sc = a.epi.load_scol(n0 + li);
-  const float bi = a.epi.load_bias(n0 + li);
-  float sr[4];
+  // Tile order: the hardware deals workgroup ids round-robin over the 8 XCDs (id % 8). With the
+  // grid a multiple of 8, XCD x gets the contiguous tile range [x * G / 8, (x + 1) * G / 8), M
+  // tiles fastest, so each XCD's L2 holds 1/8 of the weight rows instead of all of them.
+  const int mt = gridDim.y, G = gridDim.x * gridDim.y;
+  const int b = blockIdx.y * gridDim.x + blockIdx.x;
+  const int t = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  const int m0 = (t % mt) * BM, n0 = (t / mt) * BN;
+
+  // epilogue slots of this thread and their operands, fetched before the K loop
+  float sc[PER][4], bi[PER][4], sr[PER], chain[PER][4];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) sr[v] = a.epi.load_srow(min(lg * 4 + v, a.M - 1));
+  for (int p = 0; p < PER; ++p) {
+    const int slot = min(static_cast<int>(threadIdx.x) + p * NT, SLOTS - 1);
+    const int row = slot / (BN / 4), col = (slot % (BN / 4)) * 4;
+    sr[p] = a.epi.load_srow(min(m0 + row, a.M - 1));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = min(n0 + col + q, a.N - 1);
+      sc[p][q] = a.epi.load_scol(n);
+      bi[p][q] = a.epi.load_bias(n);
+      chain[p][q] = 0.0f;
+    }
+  }
 
   for (int sgi = 0; sgi < a.nseg; ++sgi) {
     const Seg sg = a.seg[sgi];
-    const int steps = (sg.K + 63) >> 6;
-    const int ldsrow = steps * 64 + 16;
-    const int cpr = steps * 4;  // 16-byte chunks per staged row
-    __syncthreads();            // the previous block's readers are done with smem / red
-    for (int i = threadIdx.x; i < a.M * cpr; i += 64 * KW) {
-      const int r = i / cpr, c = i - r * cpr;
-      v4i v = zero;
-      if (c * 16 < sg.K) v = *reinterpret_cast<const v4i*>(a.A + r * a.lda + sg.koff + c * 16);
-      *reinterpret_cast<v4i*>(smem + r * ldsrow + c * 16) = v;
+    const int chunks = (sg.K + 127) >> 7;
+    const int c0 = (chunks * wave) / KW, c1 = (chunks * (wave + 1)) / KW;
+    const int8_t* arow[TM];
+    const int8_t* wrow[TN];
+    bool alive[TM], wlive[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = m0 + 16 * i + li;
+      alive[i] = r < a.M;
+      arow[i] = a.A + static_cast<int64_t>(alive[i] ? r : 0) * a.lda + sg.koff + 32 * lg;
     }
-    __syncthreads();
-
-    const int s0 = (steps * wave) / KW, s1 = (steps * (wave + 1)) / KW;
-    const int8_t* wrow = sg.W + static_cast<int64_t>(n0 + li) * sg.K + lg * 16;
-    const bool a_live = li < a.M;
-    const int8_t* arow = smem + (a_live ? li : 0) * ldsrow + lg * 16;  // dead rows read row 0, zeroed below
-    v4i acc = zero;
-    int s = s0;
-    for (; s + 4 <= s1; s += 4) {
-      v4i b[4], x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = load_stream_pred(reinterpret_cast<const v4i*>(wrow + (s + j) * 64), reinterpret_cast<const v4i*>(sg.W),
-                                (s + j) * 64 + lg * 16 < sg.K, zero);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4i t = *reinterpret_cast<const v4i*>(arow + (s + j) * 64);
-        x[j] = a_live ? t : zero;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma(x[j], b[j], acc);
+    for (int j = 0; j < TN; ++j) {
+      const int r = n0 + 16 * j + li;
+      wlive[j] = r < a.N;
+      wrow[j] = sg.W + static_cast<int64_t>(wlive[j] ? r : 0) * sg.K + 32 * lg;
     }
-    for (; s < s1; ++s) {
-      const v4i b = load_stream_pred(reinterpret_cast<const v4i*>(wrow + s * 64), reinterpret_cast<const v4i*>(sg.W),
-                                     s * 64 + lg * 16 < sg.K, zero);
-      const v4i t = *reinterpret_cast<const v4i*>(arow + s * 64);
-      const v4i x = a_live ? t : zero;
-      acc = mfma(x, b, acc);
-    }
-    if (KW > 1) {
-      if (wave > 0) red[wave - 1][lane] = acc;
-      __syncthreads();
-    }
-    if (wave == 0) {
+    // Loads of chunk c (all lanes of a wave take the same branch-free path; a dead piece reads
+    // the block's first 16 bytes and is replaced by zeros). Weights are streamed past the caches
+    // only when no other workgroup reads the same rows (a single M tile).
+    auto fetch = [&](int c, bool live, v4i (&fa)[TM][2], v4i (&fw)[TN][2]) {
+      const int k = c * 128 + 32 * lg;
 #pragma unroll
-      for (int w = 1; w < KW; ++w) acc += red[w - 1][lane];
-      const int n = n0 + li;
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = lg * 4 + v;
-        if (m < a.M) {
-          const float y = a.epi.apply(acc[v], sr[v], a.epi.srow != nullptr, sc, bi);
-          if (a.ksplit) {
-            chain[v] = sgi == 0 ? y : fadd(chain[v], y);
-          } else {
-            store_out(a.Y, m * a.ldy, n, a.epi.out, y, a.epi.out_scale);
-          }
+        for (int h = 0; h < 2; ++h)
+          fa[i][h] = load_pred(reinterpret_cast<const v4i*>(arow[i] + c * 128 + 16 * h),
+                               reinterpret_cast<const v4i*>(a.A), live && alive[i] && k + 16 * h < sg.K, zero);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const v4i* p = reinterpret_cast<const v4i*>(wrow[j] + c * 128 + 16 * h);
+          const bool ok = live && wlive[j] && k + 16 * h < sg.K;
+          fw[j][h] = STREAM_W ? load_stream_pred(p, reinterpret_cast<const v4i*>(sg.W), ok, zero)
+                              : load_pred(p, reinterpret_cast<const v4i*>(sg.W), ok, zero);
         }
-      }
-    }
-  }
-  if (a.ksplit && wave == 0) {
-    const int n = n0 + li;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int m = lg * 4 + v;
-      if (m < a.M) reinterpret_cast<float*>(static_cast<char*>(a.Y) + m * a.ldy)[n] = ftz(chain[v]);
-    }
-  }
-}
-
-// ------------------------------------------------------------------------------------ tiled
-constexpr int kBK = 128;          // bytes of K per LDS tile (two MFMA steps)
-constexpr int kLdr = kBK + 16;    // padded LDS row
-
-template <int BM, int BN>
-__global__ __launch_bounds__(256) void mfma_tiled_kernel(MfmaArgs a) {
-  constexpr int TM = BM / 32, TN = BN / 32;           // 16x16 tiles per wave (2 x 2 waves)
-  constexpr int ACH = BM * (kBK / 16) / 256;           // A chunks per thread per K tile
-  constexpr int WCH = BN * (kBK / 16) / 256;
-  static_assert(ACH >= 1 && WCH >= 1, "tile too small for 256 threads");
-  __shared__ __align__(16) int8_t As[BM * kLdr];
-  __shared__ __align__(16) int8_t Ws[BN * kLdr];
-  const v4i zero = {0, 0, 0, 0};
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int li = lane & 15, lg = lane >> 4;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  float chain[TM][TN][4];
-  // epilogue operands of this lane's columns and rows, fetched before the K loop
-  float sc[TN], bi[TN], sr[TM][4];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = min(n0 + (wn * TN + j) * 16 + li, a.N - 1);
-    sc[j] = a.epi.load_scol(n);
-    bi[j] = a.epi.load_bias(n);
-  }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) sr[i][v] = a.epi.load_srow(min(m0 + (wm * TM + i) * 16 + lg * 4 + v, a.M - 1));
-
-  for (int sgi = 0; sgi < a.nseg; ++sgi) {
-    const Seg sg = a.seg[sgi];
-    const int ktiles = (sg.K + kBK - 1) / kBK;
+    };
     v4i acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = zero;
-
-    v4i ra[ACH], rw[WCH];
-    auto fetch = [&](int kt) {
+    // D chunks in flight per wave: a batch of D chunk loads is issued, then its 2 * D MFMA steps.
+    for (int c = c0; c < c1; c += D) {
+      v4i fa[D][TM][2], fw[D][TN][2];
 #pragma unroll
-      for (int t = 0; t < ACH; ++t) {
-        const int i = threadIdx.x + t * 256, r = i >> 3, k = kt * kBK + (i & 7) * 16;
-        ra[t] = load_pred(reinterpret_cast<const v4i*>(a.A + (m0 + r) * a.lda + sg.koff + k),
-                          reinterpret_cast<const v4i*>(a.A), m0 + r < a.M && k < sg.K, zero);
-      }
+      for (int d = 0; d < D; ++d) fetch(c + d, c + d < c1, fa[d], fw[d]);
+      issue_fence();
 #pragma unroll
-      for (int t = 0; t < WCH; ++t) {
-        const int i = threadIdx.x + t * 256, r = i >> 3, k = kt * kBK + (i & 7) * 16;
-        rw[t] = load_stream_pred(reinterpret_cast<const v4i*>(sg.W + static_cast<int64_t>(n0 + r) * sg.K + k),
-                                 reinterpret_cast<const v4i*>(sg.W), n0 + r < a.N && k < sg.K, zero);
-      }
-    };
-    fetch(0);
-    for (int kt = 0; kt < ktiles; ++kt) {
-      __syncthreads();
+      for (int d = 0; d < D; ++d)
 #pragma unroll
-      for (int t = 0; t < ACH; ++t) {
-        const int i = threadIdx.x + t * 256;
-        *reinterpret_cast<v4i*>(As + (i >> 3) * kLdr + (i & 7) * 16) = ra[t];
-      }
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int t = 0; t < WCH; ++t) {
-        const int i = threadIdx.x + t * 256;
-        *reinterpret_cast<v4i*>(Ws + (i >> 3) * kLdr + (i & 7) * 16) = rw[t];
-      }
-      __syncthreads();
-      if (kt + 1 < ktiles) fetch(kt + 1);
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int s = 0; s < kBK / 64; ++s) {
-        v4i af[TM], bf[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af[i] = *reinterpret_cast<const v4i*>(As + ((wm * TM + i) * 16 + li) * kLdr + s * 64 + lg * 16);
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bf[j] = *reinterpret_cast<const v4i*>(Ws + ((wn * TN + j) * 16 + li) * kLdr + s * 64 + lg * 16);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma(af[i], bf[j], acc[i][j]);
-      }
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma(fa[d][i][h], fw[d][j][h], acc[i][j]);
     }
 
+    if (sgi > 0) __syncthreads();  // the previous block's epilogue has read red
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + (wn * TN + j) * 16 + li;
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = m0 + (wm * TM + i) * 16 + lg * 4 + v;
-          if (m < a.M && n < a.N) {
-            const float y = a.epi.apply(acc[i][j][v], sr[i][v], a.epi.srow != nullptr, sc[j], bi[j]);
-            if (a.ksplit) {
-              chain[i][j][v] = sgi == 0 ? y : fadd(chain[i][j][v], y);
-            } else {
-              store_out(a.Y, m * a.ldy, n, a.epi.out, y, a.epi.out_scale);
-            }
-          }
+        for (int v = 0; v < 4; ++v) red[(wave * BM + 16 * i + 4 * lg + v) * LDR + 16 * j + li] = acc[i][j][v];
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int slot = static_cast<int>(threadIdx.x) + p * NT;
+      const int row = slot / (BN / 4), col = (slot % (BN / 4)) * 4;
+      if (SLOTS % NT == 0 || slot < SLOTS) {
+        v4i sum = *reinterpret_cast<const v4i*>(red + row * LDR + col);
+#pragma unroll
+        for (int w = 1; w < KW; ++w) sum += *reinterpret_cast<const v4i*>(red + (w * BM + row) * LDR + col);
+        const int m = m0 + row, n = n0 + col;
+        float y[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          y[q] = a.epi.apply(sum[q], sr[p], a.epi.srow != nullptr, sc[p][q], bi[p][q]);
+          if (a.ksplit) chain[p][q] = sgi == 0 ? y[q] : fadd(chain[p][q], y[q]);
         }
+        if (!a.ksplit && m < a.M && n < a.N) store_out4(a.Y, m * a.ldy, n, a.epi.out, y, a.epi.out_scale);
       }
+    }
   }
   if (a.ksplit) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + (wn * TN + j) * 16 + li;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = m0 + (wm * TM + i) * 16 + lg * 4 + v;
-          if (m < a.M && n < a.N)
-            reinterpret_cast<float*>(static_cast<char*>(a.Y) + m * a.ldy)[n] = ftz(chain[i][j][v]);
-        }
-      }
+    for (int p = 0; p < PER; ++p) {
+      const int slot = static_cast<int>(threadIdx.x) + p * NT;
+      const int row = slot / (BN / 4), col = (slot % (BN / 4)) * 4;
+      const int m = m0 + row, n = n0 + col;
+      if ((SLOTS % NT == 0 || slot < SLOTS) && m < a.M && n < a.N)
+        *reinterpret_cast<float4*>(static_cast<char*>(a.Y) + m * a.ldy + 4 * n) =
+            make_float4(ftz(chain[p][0]), ftz(chain[p][1]), ftz(chain[p][2]), ftz(chain[p][3]));
+    }
   }
 }
 
-// ------------------------------------------------------------------------------------ dispatch
-constexpr int kSkinnyMaxM = 16;
-constexpr int kSkinnyMaxK = 4096;
-
-hipError_t run(const MfmaArgs& a, hipStream_t s) {
-  int kmax = 0;
-  for (int i = 0; i < a.nseg; ++i) kmax = a.seg[i].K > kmax ? a.seg[i].K : kmax;
-  if (a.M <= kSkinnyMaxM && kmax <= kSkinnyMaxK) {
-    const int steps = (kmax + 63) / 64;
-    const size_t lds = static_cast<size_t>(a.M) * (steps * 64 + 16);
-    const dim3 grid(a.N / 16);
-    if (steps >= 32) {
-      hipLaunchKernelGGL(mfma_skinny_kernel<8>, grid, dim3(512), lds, s, a);
-    } else {
-      hipLaunchKernelGGL(mfma_skinny_kernel<4>, grid, dim3(256), lds, s, a);
-    }
-    return hipGetLastError();
-  }
-  if (a.M <= 32) {
-    const dim3 grid((a.N + 63) / 64, (a.M + 31) / 32);
-    hipLaunchKernelGGL((mfma_tiled_kernel<32, 64>), grid, dim3(256), 0, s, a);
+template <int TM, int TN, int KW, int D>
+hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
+  const dim3 grid((a.N + 16 * TN - 1) / (16 * TN), (a.M + 16 * TM - 1) / (16 * TM));
+  const size_t lds = static_cast<size_t>(KW) * 16 * TM * (16 * TN + 4) * 4;
+  if (grid.y == 1) {
+    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, true>), grid, dim3(64 * KW), lds, s, a);
   } else {
-    const dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
-    hipLaunchKernelGGL((mfma_tiled_kernel<64, 64>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, false>), grid, dim3(64 * KW), lds, s, a);
   }
   return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------ dispatch
+// Chunk rows (M <= 16): one 16-column tile per workgroup and 8 waves over K (the weights have no
+// reuse, so the most workgroups and the most weight bytes in flight). Prompt rows: 32 x 32 tiles
+// and 4 waves over K, one chunk in flight per wave (the fastest of the measured
+// 16/32/64-row x 16/32/64-column tiles, 2/4/8/16 waves and 1-4 chunk depths at M = 256).
+hipError_t run(const MfmaArgs& a, hipStream_t s) {
+  if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
+  return go_direct<2, 2, 4, 1>(a, s);
 }
 
 }  // namespace

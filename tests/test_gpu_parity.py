@@ -2,6 +2,7 @@
 reference golden model wrote itself. Needs a gfx950 GPU."""
 from __future__ import annotations
 
+import zlib
 from pathlib import Path
 
 import numpy as np
@@ -126,7 +127,7 @@ def test_gemv_every_k_shape(K):
 def test_epilogue_matrix(path, qm, bias, act, out):
     """Every scale mode x bias x activation/format (the reference's GEMV test grid), with a huge
     scale (inf products), a zero activation chunk, and random int8 including -128."""
-    rng = np.random.default_rng(hash((path, qm, bias, act, out)) & 0xFFFF)
+    rng = np.random.default_rng(zlib.crc32(repr((path, qm, bias, act, out)).encode()))
     M, N, K = (1 if path == "gemv" else 3), 48, 16 * int(rng.integers(1, 40))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     A[:, 16:32] = 0
@@ -245,6 +246,39 @@ def test_ksplit_both_paths_agree():
             ops.set_w8a8_path(prev)
     want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
     assert same(outs[0], want) and same(outs[1], want)
+
+
+@pytest.mark.parametrize("M", [17, 45])
+def test_ksplit_prompt_tiles(M):
+    """The K split on the prompt-row MFMA tiles (M > 16), with a ragged last row and column tile."""
+    x, q, s, W, scol, _ = w8_inputs(M + 77, M, 208, 6912)
+    blocks = [np.ascontiguousarray(W[:, :4096]), np.ascontiguousarray(W[:, 4096:])]
+    y = ops.gemm_rowcol_ksplit(cuda(q), cuda(s), [cuda(b) for b in blocks], cuda(scol))
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
+@pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
+                                     (ACT_GELU, OUT_FP32), (ACT_SOFTPLUS, OUT_BF16)])
+def test_epilogue_matrix_prompt_tiles(qm, act, out):
+    """The prompt-row MFMA tiles (M > 16) through every scale mode and output format with a bias,
+    a ragged last row and column tile (M = 45, N = 80), a huge scale and int8 -128."""
+    rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, "prompt")).encode()))
+    M, N, K = 45, 80, 16 * int(rng.integers(1, 90))
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
+    sc[N // 3] = 3e30
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32)
+    osc = f32(5.0) if out == OUT_INT8 else None
+    y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc), cuda(b),
+                        act=act, out=out, out_scale=osc)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), mismatch(host(y), want)
 
 
 # ------------------------------------------------------------------------------ prefill GEMM (config 4)
