@@ -347,10 +347,19 @@ def config_suite(torch, lib, seed: int) -> dict:
         res[f"c2_gemma3_down_ksplit_{split[0]}+{split[1]}"] = r
         log(f"c2 {split}: {r['us_per_call']} us")
         del ls, holds
-    for M in (4, 256):
+    # the automatic kernel family (GEMV rows for M = 4, INT8 MFMA for M = 256), and the MFMA family
+    # forced at M = 4 beside it
+    for M, path in ((4, 0), (4, 2), (256, 0)):
         for K, N in ((1024, 3072), (3072, 1024)):
-            res[f"c4_prefill_M{M}_K{K}_N{N}"] = w8(M, N, K, "c4")
-            log(f"c4 M={M} K={K} N={N}: {res[f'c4_prefill_M{M}_K{K}_N{N}']['us_per_call']} us")
+            prev = lib.tars_set_w8a8_path(path)
+            try:
+                r = w8(M, N, K, "c4")
+            finally:
+                lib.tars_set_w8a8_path(prev)
+            r["family"] = "mfma" if path == 2 or M > 16 else "gemv_rows"
+            key = f"c4_prefill_M{M}_K{K}_N{N}" + ("_mfma" if path == 2 else "")
+            res[key] = r
+            log(f"{key}: {r['us_per_call']} us ({r['family']})")
     for K, N in ((1536, 12288), (6144, 1536)):
         x = torch.randn((1, K), device="cuda", generator=gen)
         y = torch.empty((1, N), device="cuda")

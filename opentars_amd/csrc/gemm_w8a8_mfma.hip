@@ -56,10 +56,14 @@ __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
 // reads its own K range of all BM + BN rows once, the next chunk in flight while the current one
 // feeds the MFMAs); the int32 partial tiles meet in LDS, where each thread then owns 4 consecutive
 // columns of one row for the epilogue and a 4-wide store.
+// int32 pitch of a reduction row: 4 words of padding (spreads the 4 row groups of an MFMA tile
+// over the banks) unless that would push the tile past 64 KiB of LDS.
+constexpr int red_pitch(int kw, int bm, int bn) { return kw * bm * (bn + 4) * 4 <= 65536 ? bn + 4 : bn; }
+
 template <int TM, int TN, int KW, int D, bool STREAM_W>
 __global__ __launch_bounds__(64 * KW) void mfma_direct_kernel(MfmaArgs a) {
   constexpr int BM = 16 * TM, BN = 16 * TN;
-  constexpr int LDR = BN + 4;             // int32 pitch of a reduction row
+  constexpr int LDR = red_pitch(KW, BM, BN);
   constexpr int NT = 64 * KW;
   constexpr int SLOTS = BM * BN / 4;      // 4-column groups of the tile
   constexpr int PER = (SLOTS + NT - 1) / NT;
@@ -76,21 +80,30 @@ __global__ __launch_bounds__(64 * KW) void mfma_direct_kernel(MfmaArgs a) {
   const int t = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
   const int m0 = (t % mt) * BM, n0 = (t / mt) * BN;
 
-  // epilogue slots of this thread and their operands, fetched before the K loop
-  float sc[PER][4], bi[PER][4], sr[PER], chain[PER][4];
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
+  // Epilogue operands of this thread's slots (row scale, 4 column scales, 4 biases), fetched
+  // before the K loop when a thread owns at most two slots, else when the slot is stored.
+  constexpr bool PRE = PER <= 2;
+  constexpr int PP = PRE ? PER : 1;
+  auto operands = [&](int p, float& sr, float (&sc)[4], float (&bi)[4]) {
     const int slot = min(static_cast<int>(threadIdx.x) + p * NT, SLOTS - 1);
     const int row = slot / (BN / 4), col = (slot % (BN / 4)) * 4;
-    sr[p] = a.epi.load_srow(min(m0 + row, a.M - 1));
+    sr = a.epi.load_srow(min(m0 + row, a.M - 1));
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int n = min(n0 + col + q, a.N - 1);
-      sc[p][q] = a.epi.load_scol(n);
-      bi[p][q] = a.epi.load_bias(n);
-      chain[p][q] = 0.0f;
+      sc[q] = a.epi.load_scol(n);
+      bi[q] = a.epi.load_bias(n);
     }
+  };
+  float psr[PP], psc[PP][4], pbi[PP][4], chain[PER][4];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) operands(p, psr[p], psc[p], pbi[p]);
   }
+#pragma unroll
+  for (int p = 0; p < PER; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) chain[p][q] = 0.0f;
 
   for (int sgi = 0; sgi < a.nseg; ++sgi) {
     const Seg sg = a.seg[sgi];
@@ -170,10 +183,21 @@ __global__ __launch_bounds__(64 * KW) void mfma_direct_kernel(MfmaArgs a) {
 #pragma unroll
         for (int w = 1; w < KW; ++w) sum += *reinterpret_cast<const v4i*>(red + (w * BM + row) * LDR + col);
         const int m = m0 + row, n = n0 + col;
+        float sr, sc[4], bi[4];
+        if constexpr (PRE) {
+          sr = psr[p];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            sc[q] = psc[p][q];
+            bi[q] = pbi[p][q];
+          }
+        } else {
+          operands(p, sr, sc, bi);
+        }
         float y[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          y[q] = a.epi.apply(sum[q], sr[p], a.epi.srow != nullptr, sc[p][q], bi[p][q]);
+          y[q] = a.epi.apply(sum[q], sr, a.epi.srow != nullptr, sc[q], bi[q]);
           if (a.ksplit) chain[p][q] = sgi == 0 ? y[q] : fadd(chain[p][q], y[q]);
         }
         if (!a.ksplit && m < a.M && n < a.N) store_out4(a.Y, m * a.ldy, n, a.epi.out, y, a.epi.out_scale);
@@ -195,12 +219,15 @@ __global__ __launch_bounds__(64 * KW) void mfma_direct_kernel(MfmaArgs a) {
 
 template <int TM, int TN, int KW, int D>
 hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
-  const dim3 grid((a.N + 16 * TN - 1) / (16 * TN), (a.M + 16 * TM - 1) / (16 * TM));
-  const size_t lds = static_cast<size_t>(KW) * 16 * TM * (16 * TN + 4) * 4;
+  constexpr int BM = 16 * TM, BN = 16 * TN;
+  const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+  static_assert(KW * BM * red_pitch(KW, BM, BN) * 4 <= 65536, "reduction tile exceeds 64 KiB of LDS");
+  const size_t lds = static_cast<size_t>(KW) * BM * red_pitch(KW, BM, BN) * 4;
+  const dim3 block(64 * KW);
   if (grid.y == 1) {
-    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, true>), grid, dim3(64 * KW), lds, s, a);
+    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, true>), grid, block, lds, s, a);
   } else {
-    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, false>), grid, dim3(64 * KW), lds, s, a);
+    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, false>), grid, block, lds, s, a);
   }
   return hipGetLastError();
 }
@@ -208,8 +235,9 @@ hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
 // ------------------------------------------------------------------------------------ dispatch
 // Chunk rows (M <= 16): one 16-column tile per workgroup and 8 waves over K (the weights have no
 // reuse, so the most workgroups and the most weight bytes in flight). Prompt rows: 32 x 32 tiles
-// and 4 waves over K, one chunk in flight per wave (the fastest of the measured
-// 16/32/64-row x 16/32/64-column tiles, 2/4/8/16 waves and 1-4 chunk depths at M = 256).
+// and 4 waves over K, one chunk in flight per wave (the fastest of the measured 16/32/64-row x
+// 16/32/64-column tiles, 2/4/8/16 waves over K, 1-4 chunk depths, and 2 x 2 / 4 x 2 waves sharing
+// a 64 x 64 / 128 x 64 tile's operands through L1, at M = 256 and M = 1024).
 hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
   return go_direct<2, 2, 4, 1>(a, s);

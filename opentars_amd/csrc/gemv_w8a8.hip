@@ -32,35 +32,46 @@ __device__ __forceinline__ int dot16(v4i w, v4i x, int acc) {
 
 // CPL > 0: exactly CPL chunks per lane with the activations held in registers (K <= 128 * L).
 // CPL == 0: any K, chunks walked in a loop with the activation chunk re-read from cache.
-template <int L, int CPL, int U>
+// MR activation rows per block (prefill chunks, M <= 8): every weight chunk loaded feeds the
+// dot products of all MR rows, so the weights are read once per MR rows (MR * U <= L).
+template <int L, int CPL, int U, int MR>
 __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
+  static_assert(MR == 1 || CPL > 0, "several activation rows need the register-held activations");
+  static_assert(MR * U <= L, "one epilogue lane per (row, weight row)");
   constexpr int kSlots = 64 / L;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slot = lane / L;
   const int sub = lane % L;
-  const int m = blockIdx.y;
+  const int m0 = blockIdx.y * MR;
   const int C = a.K >> 4;
   const int n0 = (blockIdx.x * (kWaves * kSlots) + wave * kSlots + slot) * U;
-  const v4i* xrow = reinterpret_cast<const v4i*>(a.A + m * a.lda);
   const v4i zero = {0, 0, 0, 0};
 
-  int acc[U];
+  int acc[MR][U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) acc[u] = 0;
-  // this lane's epilogue row (lane `sub` finishes row n0 + sub) and its operands
-  const int ne = n0 + sub;
-  const bool epi_lane = sub < U && ne < a.N;
-  const int nc = epi_lane ? ne : 0;
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[r][u] = 0;
+  // this lane's epilogue element (lane `sub` finishes activation row m0 + sub / U of weight row
+  // n0 + sub % U) and its operands
+  const int ne = n0 + sub % U, me = m0 + sub / U;
+  const bool epi_lane = sub < MR * U && ne < a.N && (MR == 1 || me < a.M);  // MR = 1: grid.y == M
+  const int nc = epi_lane ? ne : 0, mc = epi_lane ? me : 0;
   float sr = 0.0f, sc = 0.0f, bi = 0.0f;
 
   if constexpr (CPL > 0) {
     // issue order: activations, weights, then the epilogue operands
-    v4i xv[CPL];
+    v4i xv[MR][CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = sub + j * L;
-      xv[j] = load_pred(xrow + c, xrow, c < C, zero);
+    for (int r = 0; r < MR; ++r) {
+      const bool live = MR == 1 || m0 + r < a.M;
+      const v4i* xrow = reinterpret_cast<const v4i*>(a.A + (live ? m0 + r : 0) * a.lda);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = sub + j * L;
+        xv[r][j] = load_pred(xrow + c, xrow, live && c < C, zero);
+      }
     }
     issue_fence();
     const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
@@ -78,16 +89,19 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
     issue_fence();
     sc = a.epi.load_scol(nc);
     bi = a.epi.load_bias(nc);
-    sr = a.epi.load_srow(m);
+    sr = a.epi.load_srow(mc);
     issue_fence();
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[u] = dot16(wv[u][j], xv[j], acc[u]);
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc[r][u] = dot16(wv[u][j], xv[r][j], acc[r][u]);
   } else {
     sc = a.epi.load_scol(nc);
     bi = a.epi.load_bias(nc);
-    sr = a.epi.load_srow(m);
+    sr = a.epi.load_srow(mc);
+    const v4i* xrow = reinterpret_cast<const v4i*>(a.A + m0 * a.lda);
     const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
     for (int c = sub; c < C; c += L) {
       const v4i xv = xrow[c];
@@ -99,21 +113,25 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
                                  n < a.N, zero);
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) acc[u] = dot16(wv[u], xv, acc[u]);
+      for (int u = 0; u < U; ++u) acc[0][u] = dot16(wv[u], xv, acc[0][u]);
     }
   }
 
 #pragma unroll
-  for (int u = 0; u < U; ++u) acc[u] = group_sum<L>(acc[u]);
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[r][u] = group_sum<L>(acc[r][u]);
 
-  // lane `sub` of the group finishes row n0 + sub (U <= L)
+  // lane `sub` of the group finishes element (sub / U, sub % U)
   int mine = 0;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (sub == u) mine = acc[u];
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (sub == r * U + u) mine = acc[r][u];
   if (epi_lane) {
     const float y = a.epi.apply(mine, sr, a.epi.srow != nullptr, sc, bi);
-    store_out(a.Y, m * a.ldy, ne, a.epi.out, y, a.epi.out_scale);
+    store_out(a.Y, me * a.ldy, ne, a.epi.out, y, a.epi.out_scale);
   }
 }
 
@@ -340,8 +358,18 @@ int rows_per_wave(int64_t rows) {
 template <int L, int CPL, int U>
 hipError_t go(const W8A8Args& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
-  const dim3 grid((a.N + rows_per_block - 1) / rows_per_block, a.M);
-  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U>), grid, dim3(kThreads), 0, s, a);
+  const unsigned nb = (a.N + rows_per_block - 1) / rows_per_block;
+  if constexpr (CPL > 0 && 4 * U <= L) {
+    if (a.M >= 3) {
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 4>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a);
+      return hipGetLastError();
+    }
+    if (a.M == 2) {
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 2>), dim3(nb, 1), dim3(kThreads), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 1>), dim3(nb, a.M), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

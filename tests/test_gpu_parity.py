@@ -119,16 +119,17 @@ def test_gemv_every_k_shape(K):
     assert same(host(y), G.gemm_rowcol(q, s, W, scol))
 
 
-@pytest.mark.parametrize("path", ["gemv", "mfma"])
+@pytest.mark.parametrize("path,M", [("gemv", 1), ("gemv", 3), ("mfma", 3)])
 @pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
                                      (ACT_SOFTPLUS, OUT_INT8), (ACT_GELU, OUT_FP32)])
-def test_epilogue_matrix(path, qm, bias, act, out):
+def test_epilogue_matrix(path, M, qm, bias, act, out):
     """Every scale mode x bias x activation/format (the reference's GEMV test grid), with a huge
-    scale (inf products), a zero activation chunk, and random int8 including -128."""
-    rng = np.random.default_rng(zlib.crc32(repr((path, qm, bias, act, out)).encode()))
-    M, N, K = (1 if path == "gemv" else 3), 48, 16 * int(rng.integers(1, 40))
+    scale (inf products), a zero activation chunk, and random int8 including -128; the GEMV family
+    at M = 1 and with several activation rows per block (M = 3), and the MFMA family."""
+    rng = np.random.default_rng(zlib.crc32(repr((path, M, qm, bias, act, out)).encode()))
+    N, K = 48, 16 * int(rng.integers(1, 40))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     A[:, 16:32] = 0
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
@@ -185,7 +186,7 @@ def test_lm_head_full_size():
 def test_strided_rows_and_untouched_gaps():
     """Strided A and Y rows give the dense result and leave the gaps untouched (test_golden.py:261-289)."""
     rng = np.random.default_rng(21)
-    for path, M in (("gemv", 1), ("gemv", 3), ("mfma", 3), ("mfma", 40)):
+    for path, M in (("gemv", 1), ("gemv", 2), ("gemv", 3), ("gemv", 6), ("mfma", 3), ("mfma", 40)):
         N, K = 64, 272
         A = rng.integers(-128, 128, (M, K), dtype=np.int8)
         W = rng.integers(-128, 128, (N, K), dtype=np.int8)
@@ -282,13 +283,19 @@ def test_epilogue_matrix_prompt_tiles(qm, act, out):
 
 
 # ------------------------------------------------------------------------------ prefill GEMM (config 4)
+@pytest.mark.parametrize("path", ["auto", "gemv", "mfma"])
 @pytest.mark.parametrize("M", [4, 256])
 @pytest.mark.parametrize("K,N", [(1024, 3072), (3072, 1024)])
-def test_c4_prefill_gemm(M, K, N):
+def test_c4_prefill_gemm(path, M, K, N):
+    """Config 4 on both kernel families and the automatic choice."""
     x, q, s, W, scol, _ = w8_inputs(M * 7 + K, M, N, K)
     qg, sg = ops.quant_rows(cuda(x))
     assert same(host(qg), q) and same(host(sg), s)
-    y = ops.gemm_rowcol(qg, sg, cuda(W), cuda(scol))
+    prev = ops.set_w8a8_path(path)
+    try:
+        y = ops.gemm_rowcol(qg, sg, cuda(W), cuda(scol))
+    finally:
+        ops.set_w8a8_path(prev)
     want = G.gemm_rowcol(q, s, W, scol)
     assert same(host(y), want), mismatch(host(y), want)
 
@@ -298,7 +305,28 @@ def test_c4_prefill_gemm(M, K, N):
 def test_mfma_ragged_m_and_k(M, K):
     x, q, s, W, scol, rng = w8_inputs(M * 1000 + K, M, 80, K)
     b = rng.normal(0, 1, 80).astype(f32)
-    y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol), cuda(b), act=ACT_SILU)
+    prev = ops.set_w8a8_path("mfma")
+    try:
+        y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol), cuda(b), act=ACT_SILU)
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol(q, s, W, scol, b, act=ACT_SILU)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 7, 9, 16])
+@pytest.mark.parametrize("K,N", [(64, 80), (496, 4112), (1040, 80), (4992, 80), (8192, 48), (9216, 32)])
+def test_gemv_rows_ragged(M, K, N):
+    """The GEMV family with 2 or 4 activation rows per block (and the loop form past K = 8192):
+    ragged last row block, every lane-group width, rows per wave 1/2 (N = 4112 has a partial
+    block), bias and SiLU."""
+    x, q, s, W, scol, rng = w8_inputs(M * 7919 + K + N, M, N, K)
+    b = rng.normal(0, 1, N).astype(f32)
+    prev = ops.set_w8a8_path("gemv")
+    try:
+        y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol), cuda(b), act=ACT_SILU)
+    finally:
+        ops.set_w8a8_path(prev)
     want = G.gemm_rowcol(q, s, W, scol, b, act=ACT_SILU)
     assert same(host(y), want), mismatch(host(y), want)
 
