@@ -163,6 +163,57 @@ const char* tars_last_error(void);
  */
 int tars_set_w8a8_path(int path);
 
+/* ---------------------------------------------------------------- descriptor queue executor
+ * Replaces tars_mini/golden.py:450-492 (Machine.run_queue) for a DDR image that lives in device
+ * memory; the descriptor layout, CRC and check order are contract.py:14-38,154-181 and
+ * golden.py:59-169 (validate), :172-258 (strides, segments, extra_out), :260-267 and :440-448
+ * (overlap rules).
+ */
+
+/* The end state of a queue run (golden.py:23-30 Status) plus the hand-off flag. */
+typedef struct tars_queue_status {
+  int32_t done;     /* 1: all n descriptors ran */
+  int32_t err_code; /* the contract's ERR_CODE: 0 OK, 1 E_MAGIC, 2 E_VERSION, 3 E_CRC, 4 E_VALID,
+                       5 E_OPCODE, 6 E_FIELD, 7 E_ALIGN, 8 E_RANGE */
+  int32_t op_idx;   /* the descriptor that stopped the queue (CUR_OP_IDX); n when done */
+  int32_t host_op;  /* 1: stopped at a valid descriptor this library does not run on the GPU
+                       (ops other than the W8A8 / W4A16 GEMM and ROW_QUANT, or an image address
+                       that misses the kernels' 16 / 128-byte alignment); nothing of it ran */
+} tars_queue_status;
+
+/*
+ * Runs the n descriptors at image + queue_addr, in order, on `stream`. `image` is the device
+ * address of the DDR image (image_len bytes); every descriptor address is an offset into it. The
+ * descriptors are read from the image (the call waits for the stream's earlier work to do so)
+ * and checked on the host in the contract's order; the GPU-run ones are enqueued on `stream` and
+ * have not necessarily finished when the call returns. Returns TARS_OK with *st describing the
+ * outcome (a contract error stops the queue at its descriptor, keeping earlier writes), or
+ * TARS_E_OVERLAP when a descriptor's output overlaps one of its inputs (the golden's
+ * ContractError; st->op_idx names it, nothing of it ran), TARS_E_ARG, or TARS_E_DEVICE.
+ * core_id: the executing core's id (CORE_ID must match); gemv_only: the KV260 profile (a conv or
+ * a GEMM with K > 4096 is E_OPCODE), golden.py:48-50.
+ */
+int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int32_t n,
+                   int32_t core_id, int32_t gemv_only, tars_queue_status* st, void* stream);
+
+/*
+ * The full check of one 64-byte descriptor (host memory) against an image of image_len bytes:
+ * *err_code = its ERR_CODE (E_RANGE included, golden.py:462-468); *gpu (if not NULL) = 1 when
+ * it is valid and tars_run_queue would run it on the GPU. Returns TARS_E_OVERLAP for a valid
+ * descriptor whose output overlaps an input (golden.py:473-479), else TARS_OK. Host only.
+ */
+int tars_check_descriptor(const uint8_t* desc, uint64_t image_len, int32_t core_id,
+                          int32_t gemv_only, int32_t* err_code, int32_t* gpu);
+
+/* The 23 fields of a 64-byte descriptor in layout order (MAGIC, VERSION, CORE_ID, HDR_RSV,
+ * OPCODE, CTRL, GROUP_SIZE, EPI, BASE_ADDR, A_OFF, W_OFF, Y_OFF, SCALE_OFF, BIAS_OFF, M, N, K,
+ * LDA16, OUT_SCALE, CRC32, VALID, LDY16, DEP_SIG), contract.py:170-172. Host only. */
+int tars_decode_descriptor(const uint8_t* desc, uint64_t* fields);
+
+/* The CRC-32 a descriptor's CRC32 field must hold: zlib's crc32 over the 64 bytes with bytes
+ * 4..7 read as zero (contract.py:154-181). Host only. */
+uint32_t tars_descriptor_crc(const uint8_t* desc);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,7 +6,7 @@ there is no CPU fallback anywhere in the package.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_char_p, c_int, c_int32, c_int64, c_uint32, c_void_p
+from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libopentars_amd.so"
@@ -16,11 +16,17 @@ OK, E_FIELD, E_ALIGN, E_RANGE, E_OVERLAP, E_ARG, E_DEVICE = 0, -6, -7, -8, -9, -
 STATUS_NAMES = {OK: "OK", E_FIELD: "E_FIELD", E_ALIGN: "E_ALIGN", E_RANGE: "E_RANGE",
                 E_OVERLAP: "E_OVERLAP", E_ARG: "E_ARG", E_DEVICE: "E_DEVICE"}
 
+
 class W8A8Out(ctypes.Structure):
     """tars_w8a8_out: one weight matrix fed by a shared quantized activation."""
     _fields_ = [("W", c_void_p), ("scol", c_void_p), ("bias", c_void_p), ("Y", c_void_p),
                 ("ldy", c_int64), ("N", c_int32), ("act", c_int32), ("out", c_int32),
                 ("out_scale_bits", c_uint32)]
+
+
+class QueueStatus(ctypes.Structure):
+    """tars_queue_status: the end state of a descriptor-queue run."""
+    _fields_ = [("done", c_int32), ("err_code", c_int32), ("op_idx", c_int32), ("host_op", c_int32)]
 
 
 # Every exported entry point: name -> (restype, argtypes)
@@ -40,6 +46,11 @@ SIGNATURES = {
     "tars_version": (c_char_p, []),
     "tars_last_error": (c_char_p, []),
     "tars_set_w8a8_path": (c_int, [c_int]),
+    "tars_run_queue": (c_int, [c_void_p, c_uint64, c_uint64, c_int32, c_int32, c_int32, POINTER(QueueStatus),
+                               c_void_p]),
+    "tars_check_descriptor": (c_int, [c_char_p, c_uint64, c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
+    "tars_decode_descriptor": (c_int, [c_char_p, POINTER(c_uint64)]),
+    "tars_descriptor_crc": (c_uint32, [c_char_p]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -99,6 +99,11 @@ float f32_of(uint32_t b) {
 
 }  // namespace
 
+namespace tars {
+// The calling thread's last-error text, shared by every entry point of the library.
+void set_last_error(const std::string& what) { g_last_error = what; }
+}  // namespace tars
+
 extern "C" {
 
 const char* tars_version(void) { return "opentars_amd 0.1.0 gfx950"; }

@@ -1,0 +1,534 @@
+// Descriptor-queue executor over a DDR image held in device memory (tars_mini/golden.py:450-492
+// run_queue, with golden.py:59-169 validate, :172-258 strides / segments / extra_out and
+// :260-267 / :440-448 the overlap rules; tars_mini/contract.py:14-38 the 512-bit layout and
+// :154-181 encode / decode / CRC).
+//
+// Host side: the descriptors are read from the image once (one device-to-host copy), decoded,
+// CRC-checked and validated in the contract's order, their byte segments range- and overlap-
+// checked; every descriptor the GPU runs (W8A8 GEMM in QM_TENSOR / QM_CHANNEL / QM_ROWCOL, the
+// W4A16 group GEMM, ROW_QUANT) is then enqueued on the caller's stream with pointers into the
+// image, in queue order, so each one sees every earlier write (stream order). The queue stops at
+// the first invalid descriptor (its ERR_CODE and index, earlier writes kept), at an output that
+// overlaps an input (the golden's ContractError), or at a valid descriptor of another kind, which
+// is handed back to the caller (host_op = 1). A descriptor whose output lands on a later
+// descriptor of the same queue makes the executor wait for it and re-read the rest of the queue.
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/opentars_amd.h"
+
+namespace {
+
+typedef unsigned __int128 u128;
+
+// ---------------------------------------------------------------------------- descriptor fields
+// Field order and (low bit, width) of the 512-bit descriptor, byte i holding bits 8i+7..8i.
+enum Field {
+  F_MAGIC, F_VERSION, F_CORE_ID, F_HDR_RSV, F_OPCODE, F_CTRL, F_GROUP_SIZE, F_EPI, F_BASE_ADDR,
+  F_A_OFF, F_W_OFF, F_Y_OFF, F_SCALE_OFF, F_BIAS_OFF, F_M, F_N, F_K, F_LDA16, F_OUT_SCALE,
+  F_CRC32, F_VALID, F_LDY16, F_DEP_SIG, kFields
+};
+struct BitRange {
+  int lo, width;
+};
+constexpr BitRange kBits[kFields] = {
+    {496, 16}, {480, 16}, {472, 8},  {448, 24}, {432, 16}, {416, 16}, {400, 16}, {384, 16},
+    {320, 64}, {288, 32}, {256, 32}, {224, 32}, {192, 32}, {160, 32}, {144, 16}, {128, 16},
+    {112, 16}, {96, 16},  {64, 32},  {32, 32},  {31, 1},   {16, 15},  {0, 16}};
+
+constexpr uint32_t kMagic = 0xAA55, kVersion = 0x0002;
+constexpr uint64_t kDescBytes = 64;
+enum Op { OP_CONV = 1, OP_GEMM = 2, OP_RELU = 3, OP_ROW = 4, OP_CONV_ACT = 5, OP_ELT = 6, OP_ROPE = 7, OP_FDOT = 8 };
+enum Qm { QM_NONE = 0, QM_TENSOR = 1, QM_CHANNEL = 2, QM_ROWCOL = 3 };  // QM_ROWCOL doubles as the W4 group mode
+enum Dt { DT_BF16 = 0, DT_INT8 = 1, DT_INT4 = 2, DT_FP8 = 3, DT_FP32 = 4 };
+enum Out { OUT_FP32 = 0, OUT_BF16 = 1, OUT_INT8 = 2, OUT_FP16 = 3 };
+enum RowFn { ROW_SOFTMAX = 0, ROW_LAYERNORM = 1, ROW_RMSNORM = 2, ROW_L2NORM = 3, ROW_QUANT = 4 };
+enum EltOp { ELT_MUL = 0, ELT_ADD = 1, ELT_MULADD = 2, ELT_SUB = 3 };
+enum Bcast { BM_DENSE = 0, BM_ROW = 1, BM_COL = 2, BM_SCALAR = 3 };
+constexpr uint64_t kStateFp16 = 1u << 3;
+constexpr uint64_t kW4Group = 128;
+enum Err { E_OK = 0, E_MAGIC, E_VERSION, E_CRC, E_VALID, E_OPCODE, E_FIELD, E_ALIGN, E_RANGE };
+
+struct Desc {
+  uint64_t f[kFields];
+  uint64_t operator[](Field i) const { return f[i]; }
+};
+
+uint64_t field_bits(const uint8_t* raw, BitRange r) {
+  u128 acc = 0;
+  const int b0 = r.lo / 8, b1 = (r.lo + r.width - 1) / 8;
+  for (int b = b1; b >= b0; --b) acc = (acc << 8) | raw[b];
+  acc >>= (r.lo % 8);
+  const u128 mask = (r.width >= 64) ? ~static_cast<u128>(0) >> 64 : ((static_cast<u128>(1) << r.width) - 1);
+  return static_cast<uint64_t>(acc & mask);
+}
+
+Desc decode(const uint8_t* raw) {
+  Desc d;
+  for (int i = 0; i < kFields; ++i) d.f[i] = field_bits(raw, kBits[i]);
+  return d;
+}
+
+// CRC-32/ISO-HDLC (reflected polynomial 0xEDB88320, initial and final xor 0xFFFFFFFF), the zlib
+// crc32, over the 64 bytes with the CRC field (bytes 4..7) read as zero.
+uint32_t crc32_desc(const uint8_t* raw) {
+  static uint32_t table[256];
+  static bool ready = false;
+  if (!ready) {
+    for (uint32_t i = 0; i < 256; ++i) {
+      uint32_t c = i;
+      for (int k = 0; k < 8; ++k) c = (c & 1) ? 0xEDB88320u ^ (c >> 1) : c >> 1;
+      table[i] = c;
+    }
+    ready = true;
+  }
+  uint32_t c = 0xFFFFFFFFu;
+  for (uint64_t i = 0; i < kDescBytes; ++i) {
+    const uint8_t byte = (i >= 4 && i < 8) ? 0 : raw[i];
+    c = table[(c ^ byte) & 0xFF] ^ (c >> 8);
+  }
+  return c ^ 0xFFFFFFFFu;
+}
+
+// ---------------------------------------------------------------------------- derived values
+uint32_t act_code(uint64_t epi) { return static_cast<uint32_t>((epi & 3) | ((epi >> 5) & 1) << 2); }
+uint32_t out_code(uint64_t epi) { return static_cast<uint32_t>((epi >> 2) & 3); }
+bool has_bias(uint64_t epi) { return (epi >> 4) & 1; }
+uint64_t out_esize(uint32_t out) { return out == OUT_FP32 ? 4 : out == OUT_INT8 ? 1 : 2; }
+bool is_conv(uint64_t op) { return op == OP_CONV || op == OP_CONV_ACT; }
+bool is_v04(uint64_t op) { return op == OP_ELT || op == OP_ROPE || op == OP_FDOT; }
+bool is_w4(const Desc& d) {
+  return d[F_OPCODE] == OP_GEMM && (d[F_CTRL] & 7) == QM_ROWCOL && ((d[F_CTRL] >> 8) & 15) == DT_INT4;
+}
+
+int64_t floor_div(int64_t a, int64_t b) {
+  int64_t q = a / b;
+  if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+  return q;
+}
+
+// Implicit-GEMM geometry of a conv descriptor: HDR_RSV = H[23:12] | KH[11:8] | KW[7:4] |
+// (STRIDE-1)[3:2] | PAD[1:0], GROUP_SIZE = W (contract.py:58-72).
+struct ConvGeom {
+  int64_t H, W, KH, KW, S, P, Cin, OH, OW;
+};
+ConvGeom conv_geom(const Desc& d) {
+  const uint64_t g = d[F_HDR_RSV];
+  ConvGeom c;
+  c.H = static_cast<int64_t>(g >> 12);
+  c.KH = static_cast<int64_t>((g >> 8) & 15);
+  c.KW = static_cast<int64_t>((g >> 4) & 15);
+  c.S = static_cast<int64_t>((g >> 2) & 3) + 1;
+  c.P = static_cast<int64_t>(g & 3);
+  c.W = static_cast<int64_t>(d[F_GROUP_SIZE]);
+  c.Cin = (c.KH && c.KW) ? static_cast<int64_t>(d[F_K]) / (c.KH * c.KW) : 0;
+  c.OH = floor_div(c.H + 2 * c.P - c.KH, c.S) + 1;
+  c.OW = floor_div(c.W + 2 * c.P - c.KW, c.S) + 1;
+  return c;
+}
+
+struct Strides {
+  uint64_t lda, ldy, arow, yrow;
+};
+Strides strides(const Desc& d) {
+  const uint64_t op = d[F_OPCODE], N = d[F_N], K = d[F_K];
+  uint64_t arow;
+  if (is_w4(d)) {
+    arow = (((d[F_CTRL] >> 4) & 15) == DT_FP32 ? 4 : 2) * K;
+  } else if (op == OP_GEMM) {
+    arow = K;
+  } else if (is_conv(op)) {
+    arow = static_cast<uint64_t>(conv_geom(d).Cin);
+  } else if (op == OP_FDOT) {
+    arow = 4 * K;
+  } else {
+    arow = ((op == OP_ELT && (d[F_HDR_RSV] & kStateFp16)) ? 2 : 4) * N;
+  }
+  const uint64_t yrow = N * out_esize(out_code(d[F_EPI]));
+  return {d[F_LDA16] ? 16 * d[F_LDA16] : arow, d[F_LDY16] ? 16 * d[F_LDY16] : yrow, arow, yrow};
+}
+
+// (row stride, row bytes) of the second operand of ELT (dense B) and FDOT.
+std::pair<uint64_t, uint64_t> b_stride(const Desc& d) {
+  uint64_t brow;
+  if (d[F_OPCODE] == OP_FDOT) {
+    brow = ((d[F_HDR_RSV] & kStateFp16) ? 2 : 4) * ((d[F_CTRL] & 1) ? d[F_N] : d[F_K]);
+  } else {
+    brow = (d[F_HDR_RSV] & 3) == BM_DENSE ? 4 * d[F_N] : 0;
+  }
+  return {d[F_GROUP_SIZE] ? 16 * d[F_GROUP_SIZE] : brow, brow};
+}
+
+// ---------------------------------------------------------------------------- validation
+// The contract's checks in its order; the first failing class wins (golden.py:59-169).
+int field_rules(const Desc& d, int core_id) {
+  const uint64_t op = d[F_OPCODE], c = d[F_CTRL], e = d[F_EPI];
+  const uint64_t qmode = c & 7, sym = (c >> 3) & 1, adt = (c >> 4) & 15, wdt = (c >> 8) & 15, fus = (c >> 12) & 1;
+  const uint32_t act = act_code(e), out = out_code(e);
+  const bool bias = has_bias(e), conv = is_conv(op), w4 = is_w4(d);
+  const uint64_t hdr = d[F_HDR_RSV];
+  const bool hdr_ok = conv || (op == OP_GEMM && qmode == QM_ROWCOL && !w4) || (op == OP_ELT && hdr < 16) ||
+                      (op == OP_FDOT && (c & 1) && hdr == kStateFp16);
+  const bool grp_ok = conv || is_v04(op) || w4;
+  if (d[F_CORE_ID] != static_cast<uint64_t>(core_id) || d[F_DEP_SIG] || (hdr && !hdr_ok) ||
+      (d[F_GROUP_SIZE] && !grp_ok))
+    return E_FIELD;
+  if ((c >> 13) || (e >> 6) || (out == OUT_FP16 && op != OP_ELT)) return E_FIELD;
+  if (out != OUT_INT8 && d[F_OUT_SCALE]) return E_FIELD;
+  if (op == OP_GEMM || conv) {
+    if (w4) {
+      if (sym != 1 || (adt != DT_FP32 && adt != DT_BF16) || hdr != 0 || d[F_GROUP_SIZE] != kW4Group) return E_FIELD;
+    } else if ((qmode != QM_TENSOR && qmode != QM_CHANNEL && qmode != QM_ROWCOL) || sym != 1 || adt != DT_INT8 ||
+               wdt != DT_INT8 || (conv && qmode == QM_ROWCOL)) {
+      return E_FIELD;
+    }
+    if ((act != 0) != (fus == 1)) return E_FIELD;
+    if (op == OP_CONV_ACT && act == 0) return E_FIELD;
+    if (conv) {
+      const ConvGeom g = conv_geom(d);
+      if (!(g.H && g.W && g.KH && g.KW) || g.OH < 1 || g.OW < 1 || static_cast<int64_t>(d[F_M]) != g.OH * g.OW)
+        return E_FIELD;
+    }
+  } else if (op == OP_RELU) {
+    if (c != 0 || bias || d[F_K] || d[F_W_OFF] || d[F_SCALE_OFF] || d[F_BIAS_OFF] || act == 0) return E_FIELD;
+  } else if (op == OP_ROW) {
+    const uint64_t fn = c & 7;
+    if ((c >> 3) || fn > ROW_QUANT || act != 0 || (d[F_K] && fn != ROW_SOFTMAX)) return E_FIELD;
+    if (fn == ROW_SOFTMAX && (bias || d[F_W_OFF] || d[F_SCALE_OFF] || d[F_BIAS_OFF])) return E_FIELD;
+    if (fn == ROW_QUANT && (bias || d[F_W_OFF] || d[F_BIAS_OFF] || out != OUT_INT8 || d[F_OUT_SCALE]))
+      return E_FIELD;
+    if (!bias && d[F_BIAS_OFF]) return E_FIELD;
+  } else if (op == OP_ELT) {
+    const uint64_t eop = c & 3;
+    if ((c >> 2) || d[F_K] || d[F_SCALE_OFF] || bias != (eop == ELT_MULADD) ||
+        (eop == ELT_MULADD && out != OUT_FP32 && out != OUT_FP16) || (!bias && d[F_BIAS_OFF]))
+      return E_FIELD;
+  } else if (op == OP_ROPE) {
+    if (c || act != 0 || bias || d[F_SCALE_OFF] || d[F_BIAS_OFF] || d[F_GROUP_SIZE] == 0) return E_FIELD;
+  } else {  // OP_FDOT
+    if ((c >> 1) || act != 0 || bias || d[F_SCALE_OFF] || d[F_BIAS_OFF]) return E_FIELD;
+  }
+  return E_OK;
+}
+
+int align_rules(const Desc& d) {
+  const uint64_t op = d[F_OPCODE], M = d[F_M], N = d[F_N], K = d[F_K];
+  const bool conv = is_conv(op), gemm = op == OP_GEMM || conv;
+  if (M == 0 || N == 0 || N % 16 || ((gemm || op == OP_FDOT) && (K == 0 || K % 16))) return E_ALIGN;
+  if (is_w4(d) && (K < 2 * kW4Group || K % (2 * kW4Group) || K > 64 * kW4Group || d[F_W_OFF] % 128)) return E_ALIGN;
+  if (op == OP_ROPE && (K == 0 || K % 32 || K > N)) return E_ALIGN;
+  if (conv) {
+    const ConvGeom g = conv_geom(d);
+    if (K % static_cast<uint64_t>(g.KH * g.KW) || g.Cin % 16) return E_ALIGN;
+  }
+  const Field offs[5] = {F_A_OFF, F_Y_OFF, F_SCALE_OFF, F_BIAS_OFF, F_W_OFF};
+  const int noffs = op == OP_ROW ? 4 : 5;
+  for (int i = 0; i < noffs; ++i) {
+    const uint64_t bm = d[F_HDR_RSV] & 3;
+    const uint64_t al = (offs[i] == F_W_OFF && op == OP_ELT && (bm == BM_COL || bm == BM_SCALAR)) ? 4 : 16;
+    if (d[offs[i]] % al) return E_ALIGN;
+  }
+  const Strides s = strides(d);
+  if (s.lda < s.arow || s.ldy < s.yrow) return E_ALIGN;
+  if (op == OP_ELT || op == OP_FDOT) {
+    const auto b = b_stride(d);
+    if (b.first < b.second) return E_ALIGN;
+  }
+  return E_OK;
+}
+
+int validate(const uint8_t* raw, const Desc& d, int core_id, bool gemv_only) {
+  if (d[F_MAGIC] != kMagic) return E_MAGIC;
+  if (d[F_VERSION] != kVersion) return E_VERSION;
+  if (crc32_desc(raw) != d[F_CRC32]) return E_CRC;
+  if (d[F_VALID] != 1) return E_VALID;
+  const uint64_t op = d[F_OPCODE];
+  if (op < OP_CONV || op > OP_FDOT) return E_OPCODE;
+  if (gemv_only && (is_conv(op) || (op == OP_GEMM && d[F_K] > 4096))) return E_OPCODE;
+  if (int e = field_rules(d, core_id)) return e;
+  return align_rules(d);
+}
+
+// ---------------------------------------------------------------------------- byte segments
+struct Seg {
+  u128 lo, hi;  // [lo, hi) in image bytes
+};
+using Segs = std::vector<Seg>;
+
+Segs strided(u128 base, uint64_t ld, uint64_t nrows, uint64_t row_bytes) {
+  Segs v;
+  v.reserve(nrows);
+  for (uint64_t r = 0; r < nrows; ++r) v.push_back({base + static_cast<u128>(r) * ld, base + static_cast<u128>(r) * ld + row_bytes});
+  return v;
+}
+
+// The tensors a valid descriptor reads (each a list of segments) and the rows it writes
+// (ascending and disjoint since ldy >= row bytes), as in golden.py:183-248.
+void segments(const Desc& d, std::vector<Segs>& reads, Segs& y) {
+  const u128 B = d[F_BASE_ADDR];
+  const uint64_t M = d[F_M], N = d[F_N], K = d[F_K], op = d[F_OPCODE];
+  const Strides s = strides(d);
+  reads.clear();
+  y = strided(B + d[F_Y_OFF], s.ldy, M, s.yrow);
+  if (is_v04(op)) {
+    if (op == OP_ELT && ((d[F_HDR_RSV] >> 2) & 1)) {
+      reads.push_back({{B + d[F_A_OFF], B + d[F_A_OFF] + s.arow}});
+    } else {
+      reads.push_back(strided(B + d[F_A_OFF], s.lda, M, s.arow));
+    }
+    const u128 w0 = B + d[F_W_OFF];
+    if (op == OP_ELT) {
+      const uint64_t bm = d[F_HDR_RSV] & 3;
+      if (bm == BM_DENSE) {
+        reads.push_back(strided(w0, b_stride(d).first, M, 4 * N));
+      } else {
+        const uint64_t nb = bm == BM_ROW ? 4 * N : bm == BM_COL ? 4 * M : 4;
+        reads.push_back({{w0, w0 + nb}});
+      }
+      if ((d[F_CTRL] & 3) == ELT_MULADD) reads.push_back(strided(B + d[F_BIAS_OFF], s.ldy, M, s.yrow));
+    } else if (op == OP_ROPE) {
+      const uint64_t tab_rows = (M - 1) / d[F_GROUP_SIZE] + 1;
+      reads.push_back({{w0, w0 + static_cast<u128>(4 * K) * tab_rows}});
+    } else {
+      const auto b = b_stride(d);
+      reads.push_back(strided(w0, b.first, (d[F_CTRL] & 1) ? K : N, b.second));
+    }
+    return;
+  }
+  if (is_conv(op)) {
+    const ConvGeom g = conv_geom(d);
+    const uint64_t npx = static_cast<uint64_t>(g.H * g.W);
+    const u128 a0 = B + d[F_A_OFF];
+    if (s.lda == s.arow) {
+      reads.push_back({{a0, a0 + static_cast<u128>(npx) * s.arow}});
+    } else {
+      reads.push_back(strided(a0, s.lda, npx, s.arow));
+    }
+  } else {
+    reads.push_back(strided(B + d[F_A_OFF], s.lda, M, s.arow));
+  }
+  if (op == OP_GEMM || is_conv(op)) {
+    const bool w4 = is_w4(d);
+    const uint64_t ns = (d[F_CTRL] & 7) == QM_TENSOR ? 1 : N;
+    reads.push_back({{B + d[F_W_OFF], B + d[F_W_OFF] + static_cast<u128>(N) * K / (w4 ? 2 : 1)}});
+    reads.push_back({{B + d[F_SCALE_OFF], B + d[F_SCALE_OFF] + (w4 ? static_cast<u128>(2 * N) * (K / kW4Group) : static_cast<u128>(4 * ns))}});
+    if (has_bias(d[F_EPI])) reads.push_back({{B + d[F_BIAS_OFF], B + d[F_BIAS_OFF] + 4 * N}});
+    if ((d[F_CTRL] & 7) == QM_ROWCOL && !w4) {
+      const u128 r0 = B + static_cast<u128>(16) * d[F_HDR_RSV];
+      reads.push_back({{r0, r0 + 4 * M}});
+    }
+  } else if (op == OP_ROW) {
+    const uint64_t fn = d[F_CTRL] & 7;
+    if (fn == ROW_LAYERNORM || fn == ROW_RMSNORM || fn == ROW_L2NORM) {
+      reads.push_back({{B + d[F_SCALE_OFF], B + d[F_SCALE_OFF] + 4 * N}});
+      if (has_bias(d[F_EPI])) reads.push_back({{B + d[F_BIAS_OFF], B + d[F_BIAS_OFF] + 4 * N}});
+    }
+  }
+}
+
+// ROW_QUANT's second output, the row scales (golden.py:250-256).
+Segs extra_out(const Desc& d) {
+  if (d[F_OPCODE] == OP_ROW && (d[F_CTRL] & 7) == ROW_QUANT) {
+    const u128 a = static_cast<u128>(d[F_BASE_ADDR]) + d[F_SCALE_OFF];
+    return {{a, a + 4 * d[F_M]}};
+  }
+  return {};
+}
+
+// Whether any segment intersects any output row (outputs ascending and disjoint).
+bool overlaps(const Segs& segs, const Segs& y) {
+  for (const Seg& s : segs) {
+    auto it = std::upper_bound(y.begin(), y.end(), s.lo, [](u128 lo, const Seg& o) { return lo < o.hi; });
+    if (it != y.end() && it->lo < s.hi) return true;
+  }
+  return false;
+}
+
+// ELT may read its own output rows in place: A (read 0) or C (read 2), fp32/fp16 (golden.py:440-448).
+bool in_place(const Desc& d, size_t i) {
+  const uint32_t out = out_code(d[F_EPI]);
+  if (d[F_OPCODE] != OP_ELT || (out != OUT_FP32 && out != OUT_FP16)) return false;
+  const Strides s = strides(d);
+  if (i == 0) {
+    const uint32_t afmt = (d[F_HDR_RSV] & kStateFp16) ? OUT_FP16 : OUT_FP32;
+    return afmt == out && !((d[F_HDR_RSV] >> 2) & 1) && d[F_A_OFF] == d[F_Y_OFF] && s.lda == s.ldy;
+  }
+  return i == 2 && d[F_BIAS_OFF] == d[F_Y_OFF];
+}
+
+u128 max_hi(const Segs& v) {
+  u128 m = 0;
+  for (const Seg& s : v) m = std::max(m, s.hi);
+  return m;
+}
+
+// The full check of one descriptor: contract code (E_RANGE against an image of `len` bytes
+// included) or TARS_E_OVERLAP for an output that overlaps an input.
+struct Checked {
+  int err;       // contract ERR_CODE
+  bool overlap;  // valid, but an output overlaps an input (the golden's ContractError)
+  Desc d;
+  std::vector<Segs> reads;
+  Segs y, extra;
+};
+
+Checked check(const uint8_t* raw, uint64_t len, int core_id, bool gemv_only) {
+  Checked c{};
+  c.d = decode(raw);
+  c.err = validate(raw, c.d, core_id, gemv_only);
+  if (c.err != E_OK) return c;
+  segments(c.d, c.reads, c.y);
+  c.extra = extra_out(c.d);
+  u128 hi = std::max(max_hi(c.y), max_hi(c.extra));
+  for (const Segs& s : c.reads) hi = std::max(hi, max_hi(s));
+  if (hi > static_cast<u128>(len)) {
+    c.err = E_RANGE;
+    return c;
+  }
+  for (size_t j = 0; j < c.reads.size(); ++j) {
+    if (overlaps(c.reads[j], c.y) && !in_place(c.d, j)) c.overlap = true;
+    if (!c.extra.empty() && overlaps(c.reads[j], c.extra)) c.overlap = true;
+  }
+  if (!c.extra.empty() && overlaps(c.extra, c.y)) c.overlap = true;
+  return c;
+}
+
+// Whether this library runs the descriptor on the GPU: W8A8 GEMM (QM_TENSOR / QM_CHANNEL /
+// QM_ROWCOL), the W4A16 group GEMM, ROW_QUANT.
+bool gpu_kind(const Desc& d) {
+  const uint64_t op = d[F_OPCODE];
+  if (op == OP_GEMM) return true;  // a valid GEMM is one of the W8A8 modes or W4A16
+  return op == OP_ROW && (d[F_CTRL] & 7) == ROW_QUANT;
+}
+
+// Enqueues a valid, GPU-kind descriptor with pointers into the image; returns a TARS_ status.
+// `needs_host` is set instead when the image addresses miss the kernels' alignment (a base
+// address that is not a multiple of 16, or W4 weights off a 128-byte boundary).
+int launch(uint8_t* image, const Desc& d, hipStream_t stream, bool& needs_host) {
+  uint8_t* B = image + d[F_BASE_ADDR];
+  const Strides s = strides(d);
+  const int M = static_cast<int>(d[F_M]), N = static_cast<int>(d[F_N]), K = static_cast<int>(d[F_K]);
+  const uint32_t act = act_code(d[F_EPI]), out = out_code(d[F_EPI]);
+  const uintptr_t b = reinterpret_cast<uintptr_t>(B);
+  needs_host = b % 16 != 0 || (is_w4(d) && (b + d[F_W_OFF]) % 128 != 0);
+  if (needs_host) return TARS_OK;
+  if (d[F_OPCODE] == OP_ROW) {
+    return tars_quant_rows(reinterpret_cast<const float*>(B + d[F_A_OFF]), static_cast<int64_t>(s.lda),
+                           reinterpret_cast<int8_t*>(B + d[F_Y_OFF]), static_cast<int64_t>(s.ldy),
+                           reinterpret_cast<float*>(B + d[F_SCALE_OFF]), M, N, stream);
+  }
+  const float* bias = has_bias(d[F_EPI]) ? reinterpret_cast<const float*>(B + d[F_BIAS_OFF]) : nullptr;
+  const uint32_t osc = static_cast<uint32_t>(d[F_OUT_SCALE]);
+  if (is_w4(d)) {
+    const int adt = ((d[F_CTRL] >> 4) & 15) == DT_FP32 ? TARS_DT_FP32 : TARS_DT_BF16;
+    return tars_gemm_w4a16(B + d[F_A_OFF], static_cast<int64_t>(s.lda), adt, B + d[F_W_OFF],
+                           reinterpret_cast<const uint16_t*>(B + d[F_SCALE_OFF]), bias, B + d[F_Y_OFF],
+                           static_cast<int64_t>(s.ldy), M, N, K, static_cast<int>(act), static_cast<int>(out), osc, stream);
+  }
+  const uint64_t qmode = d[F_CTRL] & 7;
+  const float* srow = qmode == QM_ROWCOL ? reinterpret_cast<const float*>(B + 16 * d[F_HDR_RSV]) : nullptr;
+  return tars_gemm_w8a8(reinterpret_cast<const int8_t*>(B + d[F_A_OFF]), static_cast<int64_t>(s.lda), srow,
+                        reinterpret_cast<const int8_t*>(B + d[F_W_OFF]), reinterpret_cast<const float*>(B + d[F_SCALE_OFF]),
+                        qmode == QM_TENSOR ? 1 : N, bias, B + d[F_Y_OFF], static_cast<int64_t>(s.ldy), M, N, K,
+                        static_cast<int>(act), static_cast<int>(out), osc, stream);
+}
+
+}  // namespace
+
+namespace tars {
+void set_last_error(const std::string& what);
+}  // namespace tars
+
+namespace {
+
+int queue_fail(int code, const std::string& what) {
+  tars::set_last_error(what);
+  return code;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tars_check_descriptor(const uint8_t* desc, uint64_t image_len, int32_t core_id, int32_t gemv_only,
+                          int32_t* err_code, int32_t* gpu) {
+  tars::set_last_error("");
+  if (!desc || !err_code) return queue_fail(TARS_E_ARG, "NULL descriptor or err_code");
+  const Checked c = check(desc, image_len, core_id, gemv_only != 0);
+  *err_code = c.err;
+  if (gpu) *gpu = (c.err == E_OK && !c.overlap && gpu_kind(c.d)) ? 1 : 0;
+  if (c.err == E_OK && c.overlap) return queue_fail(TARS_E_OVERLAP, "an output overlaps an input");
+  return TARS_OK;
+}
+
+int tars_decode_descriptor(const uint8_t* desc, uint64_t* fields) {
+  if (!desc || !fields) return TARS_E_ARG;
+  const Desc d = decode(desc);
+  for (int i = 0; i < kFields; ++i) fields[i] = d.f[i];
+  return TARS_OK;
+}
+
+uint32_t tars_descriptor_crc(const uint8_t* desc) { return desc ? crc32_desc(desc) : 0u; }
+
+int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int32_t n, int32_t core_id,
+                   int32_t gemv_only, tars_queue_status* st, void* stream) {
+  tars::set_last_error("");
+  if (!image || !st || n < 0) return queue_fail(TARS_E_ARG, "NULL image or status, or n < 0");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  *st = tars_queue_status{0, E_OK, 0, 0};
+  // the descriptors that lie inside the image, read after the stream's earlier work
+  const u128 q_end = static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) * static_cast<uint64_t>(n);
+  const uint64_t in_image = queue_addr >= image_len ? 0
+                            : static_cast<uint64_t>(std::min<u128>(q_end, image_len) - queue_addr) / kDescBytes;
+  std::vector<uint8_t> q(static_cast<size_t>(in_image) * kDescBytes);
+  auto reread = [&](uint64_t from) -> int {
+    if (from >= in_image) return TARS_OK;
+    const size_t off = static_cast<size_t>(from * kDescBytes);
+    if (hipMemcpyAsync(q.data() + off, image + queue_addr + off, q.size() - off, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+      return queue_fail(TARS_E_DEVICE, "reading the queue from the image failed");
+    return TARS_OK;
+  };
+  if (int rc = reread(0)) return rc;
+  for (int32_t i = 0; i < n; ++i) {
+    st->op_idx = i;
+    if (static_cast<uint64_t>(i) >= in_image) {  // the descriptor itself lies past the image
+      st->err_code = E_RANGE;
+      return TARS_OK;
+    }
+    const uint8_t* raw = q.data() + static_cast<size_t>(i) * kDescBytes;
+    const Checked c = check(raw, image_len, core_id, gemv_only != 0);
+    if (c.err != E_OK) {
+      st->err_code = c.err;
+      return TARS_OK;
+    }
+    if (c.overlap) return queue_fail(TARS_E_OVERLAP, "descriptor " + std::to_string(i) + ": an output overlaps an input");
+    if (!gpu_kind(c.d)) {
+      st->host_op = 1;
+      return TARS_OK;
+    }
+    bool needs_host = false;
+    if (int rc = launch(image, c.d, s, needs_host)) {
+      return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+    }
+    if (needs_host) {
+      st->host_op = 1;
+      return TARS_OK;
+    }
+    // an output written over a later descriptor of this queue: wait for it and read them again
+    const u128 later = static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(i) + 1);
+    const Segs rest = {{later, q_end}};
+    if (later < q_end && (overlaps(rest, c.y) || (!c.extra.empty() && overlaps(rest, c.extra)))) {
+      if (int rc = reread(static_cast<uint64_t>(i) + 1)) return rc;
+    }
+  }
+  st->done = 1;
+  st->op_idx = n;
+  return TARS_OK;
+}
+
+}  // extern "C"

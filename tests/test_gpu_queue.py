@@ -1,0 +1,321 @@
+"""The descriptor-queue executor on the GPU (opentars_amd.queue over tars_run_queue) against the
+oracle's queue walk: whole DDR images byte for byte and end statuses, on random programs of
+ROW_QUANT, W8A8 GEMM (QM_TENSOR / QM_CHANNEL / QM_ROWCOL, every epilogue and output format,
+strided rows) and W4A16 GEMM, with errors, host hand-offs and overlaps. Needs a gfx950 GPU."""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import queue as Q
+from opentars_amd import queue as NQ
+from opentars_amd.ops import ContractError
+
+pytestmark = pytest.mark.gpu
+
+IMAGE = 1 << 21
+QADDR = 0x1F0000
+
+
+class Program:
+    """A DDR image under construction: data regions allocated upward from 0x1000, descriptors
+    collected in order."""
+
+    def __init__(self, seed: int, image: int = IMAGE):
+        self.rng = np.random.default_rng(seed)
+        self.ddr = bytearray(image)
+        self.top = 0x1000
+        self.descs: list[bytes] = []
+
+    def alloc(self, nbytes: int, align: int = 16) -> int:
+        a = (self.top + align - 1) // align * align
+        self.top = a + nbytes + 16 * int(self.rng.integers(0, 3))
+        assert self.top < QADDR
+        return a
+
+    def put(self, data: bytes, align: int = 16) -> int:
+        a = self.alloc(len(data), align)
+        self.ddr[a:a + len(data)] = data
+        return a
+
+    def add(self, **f) -> None:
+        self.descs.append(Q.encode({"MAGIC": Q.MAGIC, "VERSION": Q.VERSION, "VALID": 1, **f}))
+
+    def image(self) -> bytearray:
+        img = bytearray(self.ddr)
+        for i, d in enumerate(self.descs):
+            img[QADDR + 64 * i:QADDR + 64 * (i + 1)] = d
+        return img
+
+
+def stride_fields(p: Program, m: int, row: int):
+    """A row region of m rows; sometimes strided (LDA16 / LDY16 given), sometimes dense."""
+    extra = int(p.rng.integers(0, 3))
+    ld = row + 16 * extra
+    return p.alloc(ld * m), (ld // 16 if extra else 0)
+
+
+def add_quant(p: Program, M: int, K: int):
+    x = (p.rng.normal(0, 1, (M, K)) * np.exp2(p.rng.integers(-8, 8, (M, 1)))).astype("<f4")
+    a, lda16 = stride_fields(p, M, 4 * K)
+    ld = 16 * lda16 if lda16 else 4 * K
+    for m in range(M):
+        p.ddr[a + m * ld:a + m * ld + 4 * K] = x[m].tobytes()
+    y, ldy16 = stride_fields(p, M, K)
+    s = p.alloc(4 * M)
+    p.add(OPCODE=Q.OP_ROW, CTRL=Q.ROW_QUANT, EPI=Q.epi(out=Q.OUT_INT8), A_OFF=a, Y_OFF=y, SCALE_OFF=s, M=M, N=K,
+          LDA16=lda16, LDY16=ldy16)
+    return y, (16 * ldy16 if ldy16 else K), s
+
+
+def add_w8(p: Program, M: int, N: int, K: int, qmode: int, a=None, lda=None, srow=None, act=None, out=None,
+           bias=None):
+    rng = p.rng
+    if a is None:
+        A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+        a, lda16 = stride_fields(p, M, K)
+        ld = 16 * lda16 if lda16 else K
+        for m in range(M):
+            p.ddr[a + m * ld:a + m * ld + K] = A[m].tobytes()
+    else:
+        lda16 = 0 if lda == K else lda // 16
+    w = p.put(rng.integers(-128, 128, (N, K), dtype=np.int8).tobytes())
+    ns = 1 if qmode == Q.QM_TENSOR else N
+    sc = rng.uniform(1e-4, 2e-2, ns).astype("<f4")
+    if rng.integers(0, 8) == 0:
+        sc[0] = 3e30
+    s = p.put(sc.tobytes())
+    act = int(rng.integers(0, 8)) if act is None else act
+    out = int(rng.choice([Q.OUT_FP32, Q.OUT_BF16, Q.OUT_INT8])) if out is None else out
+    bias = int(rng.integers(0, 2)) if bias is None else bias
+    b = p.put(rng.normal(0, 2, N).astype("<f4").tobytes()) if bias else 0
+    y, ldy16 = stride_fields(p, M, N * Q.ESIZE[out])
+    hdr = 0
+    if qmode == Q.QM_ROWCOL:
+        if srow is None:
+            srow = p.put(rng.uniform(0.1, 2.0, M).astype("<f4").tobytes())
+        hdr = srow // 16
+    osc = struct.unpack("<I", struct.pack("<f", float(rng.uniform(0.5, 8.0))))[0] if out == Q.OUT_INT8 else 0
+    p.add(OPCODE=Q.OP_GEMM, CTRL=Q.ctrl(qmode, fusion=int(act != 0)), EPI=Q.epi(act, out, bias), A_OFF=a, W_OFF=w,
+          SCALE_OFF=s, BIAS_OFF=b, Y_OFF=y, HDR_RSV=hdr, M=M, N=N, K=K, LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
+    return y
+
+
+def add_w4(p: Program, M: int, N: int, K: int):
+    rng = p.rng
+    bf16 = bool(rng.integers(0, 2))
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    if bf16:
+        xb = (x.view(np.uint32) >> 16).astype("<u2")
+        a, lda16 = stride_fields(p, M, 2 * K)
+        ld = 16 * lda16 if lda16 else 2 * K
+        for m in range(M):
+            p.ddr[a + m * ld:a + m * ld + 2 * K] = xb[m].tobytes()
+    else:
+        a, lda16 = stride_fields(p, M, 4 * K)
+        ld = 16 * lda16 if lda16 else 4 * K
+        for m in range(M):
+            p.ddr[a + m * ld:a + m * ld + 4 * K] = x[m].astype("<f4").tobytes()
+    w = p.put(rng.integers(0, 256, (N, K // 2), dtype=np.uint8).tobytes(), align=128)
+    ws = (rng.uniform(1e-3, 1e-2, (N, K // 128)).astype(np.float16)).view("<u2")
+    s = p.put(ws.tobytes())
+    act = int(rng.integers(0, 8))
+    out = int(rng.choice([Q.OUT_FP32, Q.OUT_BF16, Q.OUT_INT8]))
+    bias = int(rng.integers(0, 2))
+    b = p.put(rng.normal(0, 1, N).astype("<f4").tobytes()) if bias else 0
+    y, ldy16 = stride_fields(p, M, N * Q.ESIZE[out])
+    osc = struct.unpack("<I", struct.pack("<f", 4.0))[0] if out == Q.OUT_INT8 else 0
+    p.add(OPCODE=Q.OP_GEMM, CTRL=Q.ctrl(Q.QM_GROUP, a_dtype=Q.DT_BF16 if bf16 else Q.DT_FP32, w_dtype=Q.DT_INT4,
+                                        fusion=int(act != 0)),
+          EPI=Q.epi(act, out, bias), GROUP_SIZE=128, A_OFF=a, W_OFF=w, SCALE_OFF=s, BIAS_OFF=b, Y_OFF=y, M=M, N=N,
+          K=K, LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
+
+
+def random_program(seed: int) -> Program:
+    p = Program(seed)
+    rng = p.rng
+    for _ in range(int(rng.integers(4, 9))):
+        kind = int(rng.integers(0, 4))
+        M = int(rng.choice([1, 2, 4, 5, 17, 40]))
+        if kind == 0:                                   # ROW_QUANT feeding a QM_ROWCOL GEMM (RAW)
+            K = 16 * int(rng.integers(1, 40))
+            q, ldq, s = add_quant(p, M, K)
+            add_w8(p, M, 16 * int(rng.integers(1, 12)), K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s)
+        elif kind == 1:
+            add_w8(p, M, 16 * int(rng.integers(1, 12)), 16 * int(rng.integers(1, 40)),
+                   int(rng.choice([Q.QM_TENSOR, Q.QM_CHANNEL, Q.QM_ROWCOL])))
+        elif kind == 2:
+            add_w4(p, min(M, 5), 16 * int(rng.integers(1, 8)), 256 * int(rng.integers(1, 5)))
+        else:
+            add_quant(p, M, 16 * int(rng.integers(1, 60)))
+    return p
+
+
+def both(img: bytearray, n: int, **kw):
+    o = Q.Machine(img, **kw)
+    ost = o.run_queue(QADDR, n)
+    g = NQ.Machine(img, **kw)
+    gst = g.run_queue(QADDR, n)
+    return (o, ost), (g, gst)
+
+
+def same_status(a, b) -> bool:
+    return (bool(a.done), a.err_code, a.op_idx, bool(a.host_op)) == (bool(b.done), b.err_code, b.op_idx, bool(b.host_op))
+
+
+def first_diff(a: bytes, b: bytes) -> int:
+    x = np.frombuffer(a, np.uint8) != np.frombuffer(b, np.uint8)
+    return int(np.argmax(x)) if x.any() else -1
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_programs_match_the_oracle(seed):
+    p = random_program(seed)
+    (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
+def test_worked_example_on_the_gpu():
+    rng = np.random.default_rng(2026)
+    M, N, K = 2, 16, 32
+    ddr = bytearray(1 << 16)
+    ddr[0x100:0x140] = rng.integers(-128, 128, (M, K), dtype=np.int8).tobytes()
+    ddr[0x200:0x400] = rng.integers(-128, 128, (N, K), dtype=np.int8).tobytes()
+    ddr[0x600:0x640] = (rng.uniform(0.5, 2.0, N) / 4096).astype("<f4").tobytes()
+    ddr[0x700:0x740] = rng.uniform(-8, 8, N).astype("<f4").tobytes()
+    ddr[0x8000:0x8040] = bytes.fromhex("000000807FC4843700000000000020001000020000070000000600000010000000020000"
+                                       "000100000000000000000000150000001A11020000000000020055AA")
+    m = NQ.Machine(ddr)
+    assert m.run_queue(0x8000, 1).done
+    assert struct.unpack("<H", m.read(0x1002, 2))[0] == 0x3F16
+
+
+@pytest.mark.parametrize("bad,code", [("MAGIC", Q.E_MAGIC), ("CRC", Q.E_CRC), ("N", Q.E_ALIGN), ("Y_OFF", Q.E_RANGE)])
+def test_error_mid_queue_keeps_earlier_writes_only(bad, code):
+    p = random_program(50)
+    i = len(p.descs) // 2
+    f = Q.decode(p.descs[i])
+    f.pop("CRC32")
+    if bad == "CRC":
+        p.descs[i] = Q.encode(f, fix_crc=False)
+    else:
+        f[bad] = {"MAGIC": 0x1234, "N": 8, "Y_OFF": IMAGE - 16}[bad]
+        p.descs[i] = Q.encode(f)
+    (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    assert (ost.done, ost.err_code, ost.op_idx) == (False, code, i)
+    assert same_status(ost, gst) and bytes(g.ddr) == bytes(o.ddr)
+
+
+def test_output_overlapping_input_raises_and_writes_nothing_of_it():
+    p = random_program(51)
+    i = len(p.descs) - 1
+    f = Q.decode(p.descs[i])
+    f.pop("CRC32")
+    f["Y_OFF"] = f["A_OFF"]
+    p.descs[i] = Q.encode(f)
+    img = p.image()
+    o = Q.Machine(img)
+    with pytest.raises(Q.ContractError):
+        o.run_queue(QADDR, len(p.descs))
+    g = NQ.Machine(img)
+    with pytest.raises(ContractError):
+        g.run_queue(QADDR, len(p.descs))
+    assert bytes(g.ddr) == bytes(o.ddr)           # descriptors before it ran, it did not
+
+
+def relu_desc(p: Program, src: int, n: int) -> tuple[int, bytes]:
+    y = p.alloc(4 * n)
+    return y, Q.encode({"MAGIC": Q.MAGIC, "VERSION": Q.VERSION, "VALID": 1, "OPCODE": Q.OP_RELU, "EPI": Q.epi(1),
+                        "A_OFF": src, "Y_OFF": y, "M": 1, "N": n})
+
+
+class FakeHost:
+    """A host executor for the test: runs one RELU descriptor (max(x, 0) on fp32 bits, -0 and NaN to
+    +0) in place on the host image."""
+
+    def __init__(self, ddr: bytearray):
+        self.ddr = ddr
+
+    def run_queue(self, addr: int, n: int):
+        d = Q.decode(bytes(self.ddr[addr:addr + 64]))
+        assert n == 1 and d["OPCODE"] == Q.OP_RELU
+        x = np.frombuffer(bytes(self.ddr[d["A_OFF"]:d["A_OFF"] + 4 * d["N"]]), "<f4")
+        y = np.where(x > 0, x, np.float32(0)).astype("<f4")
+        self.ddr[d["Y_OFF"]:d["Y_OFF"] + 4 * d["N"]] = y.tobytes()
+        return Q.Status(True, Q.E_OK, 1)
+
+
+def test_host_hand_off_stops_then_resumes_with_a_host():
+    """A RELU between two GPU descriptors: without a host the queue stops there (host_op); with one
+    it runs on the host copy and the GPU descriptors after it see its output (RAW across the
+    hand-off)."""
+    p = Program(60)
+    y0 = add_w8(p, 1, 32, 64, Q.QM_CHANNEL, act=0, out=Q.OUT_FP32, bias=0)
+    ry, rdesc = relu_desc(p, y0, 32)
+    p.descs.append(rdesc)
+    q, ldq, s = add_quant(p, 1, 32)                   # quantizes the RELU output: A_OFF patched below
+    f = Q.decode(p.descs[-1])
+    f.pop("CRC32")
+    f.update(A_OFF=ry, LDA16=0)
+    p.descs[-1] = Q.encode(f)
+    img = p.image()
+    g = NQ.Machine(img)
+    st = g.run_queue(QADDR, 3)
+    assert (st.done, st.op_idx, st.host_op) == (False, 1, True)
+    # the expected image: the oracle to the RELU, the fake host, then the oracle for the rest
+    o = Q.Machine(img)
+    assert o.run_queue(QADDR, 1).done
+    FakeHost(o.ddr).run_queue(QADDR + 64, 1)
+    assert o.run_queue(QADDR + 128, 1).done
+    g2 = NQ.Machine(img, host=FakeHost)
+    st2 = g2.run_queue(QADDR, 3)
+    assert st2.done and st2.op_idx == 3
+    assert bytes(g2.ddr) == bytes(o.ddr)
+    assert bytes(NQ.run(img, QADDR, 3, host=FakeHost)) == bytes(o.ddr)
+
+
+def test_unaligned_base_goes_to_the_host():
+    """BASE_ADDR 8: legal for the contract, off the kernels' 16-byte alignment -> handed to the host
+    (here the oracle's machine), with the same final image as the oracle's own run."""
+    p = Program(61)
+    add_w8(p, 2, 32, 64, Q.QM_CHANNEL)
+    f = Q.decode(p.descs[0])
+    f.pop("CRC32")
+    f["BASE_ADDR"] = 8
+    p.descs[0] = Q.encode(f)
+    add_w8(p, 3, 48, 32, Q.QM_TENSOR)
+    img = p.image()
+    assert NQ.Machine(img).run_queue(QADDR, 2).host_op
+    o = Q.Machine(img)
+    assert o.run_queue(QADDR, 2).done
+    g = NQ.Machine(img, host=lambda ddr: Q.Machine(ddr))
+    assert g.run_queue(QADDR, 2).done
+    assert bytes(g.ddr) == bytes(o.ddr)
+
+
+def test_a_descriptor_that_overwrites_the_next_one():
+    """ROW_QUANT's int8 output lands on the following descriptor: both executors read the
+    overwritten bytes (which no longer hold a valid descriptor) and stop with the same code."""
+    p = Program(62)
+    add_quant(p, 1, 64)
+    f = Q.decode(p.descs[0])
+    f.pop("CRC32")
+    f.update(Y_OFF=QADDR + 64, LDY16=0)
+    p.descs[0] = Q.encode(f)
+    add_w8(p, 1, 16, 64, Q.QM_CHANNEL)
+    img = p.image()
+    (o, ost), (g, gst) = both(img, 2)
+    assert not ost.done and ost.op_idx == 1 and same_status(ost, gst), (ost, gst)
+    assert bytes(g.ddr) == bytes(o.ddr)
+
+
+def test_gemv_only_profile_refuses_long_k():
+    p = Program(63)
+    add_w8(p, 1, 16, 4112, Q.QM_CHANNEL)
+    (o, ost), (g, gst) = both(p.image(), 1, gemv_only=True)
+    assert (ost.err_code, gst.err_code) == (Q.E_OPCODE, Q.E_OPCODE)
