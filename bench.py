@@ -9,13 +9,15 @@ seeded random int8 with per-channel fp32 scales (~596 MB of weights per step), r
 before timing. A step is captured once as a HIP graph (the C ABI validates every call at capture)
 and replayed; `value` = algorithmic HBM bytes of the step / step time.
 
-Also reported (in "configs"): each single-GPU workload of the path (Qwen3-0.6B decode shapes, the
+Also reported: each single-GPU workload of the path ("configs": Qwen3-0.6B decode shapes, the
 lm_head, the K-split projections, M = 4 / 256 prefill, W4A16 group-128) as us/call, GB/s and
-roofline fraction (and TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight copies so the 256 MB
-MALL cannot serve it; per-kernel durations from HIP events around each launch of the decode step;
-and the CPU baseline (the numpy oracle, single core) on a bounded sample of the same workload.
+roofline fraction (and TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight
+copies so the 256 MB MALL cannot serve it; per-kernel durations from HIP events around each launch
+of the decode step; the same decode step as a 313-descriptor queue through the library's queue
+executor ("queue_executor", host clock, end to end); and the CPU baseline (the numpy oracle, single
+core) on a bounded sample of the same workload, with a bit-exact check of the timed outputs.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-configs] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-configs] [--no-cpu-baseline] [--no-queue]
 """
 from __future__ import annotations
 
@@ -51,6 +53,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config measurements")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-queue", action="store_true", help="skip the descriptor-queue executor measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample length")
     ap.add_argument("--detail", type=str, default="", help="also write the full result JSON here")
     return ap.parse_args()
@@ -172,6 +175,113 @@ def decode_set(torch, lib, seed: int):
         group(f"L{L}.down", FF, [(f"L{L}.down_proj", H)])
     group("head", H, [("lm_head", QWEN3_VOCAB)])
     return fused, unfused, keep
+
+
+def queue_decode_step(torch, lib, seed: int, steps: int, warmup: int) -> dict:
+    """The same decode-step linear set as a descriptor queue in one device-resident DDR image, run
+    through the library's executor (tars_run_queue) the way QwenLowering emits it: per layer
+    ROW_QUANT + q/k/v GEMMs, ROW_QUANT + o, ROW_QUANT + gate/up, ROW_QUANT + down, then ROW_QUANT +
+    the head as 4 blocks of 37984 rows (qwen_ref.py:371-378); 313 descriptors, QM_ROWCOL, fp32 out.
+    Timed end to end per step on the host clock (descriptor checks, launches and GPU work, the host
+    holding its copy of the queue), with the executor's quantizer+GEMM fusion on (113 launches) and
+    off (313 launches)."""
+    from opentars_amd import _lib, contract as C
+    from opentars_amd.queue import encode_descriptor
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 7)
+    H, Qd, KV, FF, V = QWEN3_H, QWEN3_Q, QWEN3_KV, QWEN3_FF, QWEN3_VOCAB
+    small, big = [0], [0]
+
+    def take(region, n, align):
+        a = (region[0] + align - 1) // align * align
+        region[0] = a + n
+        return a
+
+    descs, fills, nbytes = [], [], 0
+
+    def quant(k):
+        x, q, s = take(small, 4 * k, 16), take(small, k, 16), take(small, 16, 16)
+        fills.append(("randn", x, k))
+        descs.append(dict(OPCODE=C.OP_ROW, CTRL=C.ROW_QUANT, EPI=C.epi(out=C.OUT_INT8), A_OFF=x, Y_OFF=q,
+                          SCALE_OFF=s, M=1, N=k))
+        return q, s, 4 * k
+
+    def gemm(q, s, k, n, w=None, sc=None, y=None):
+        w = take(big, n * k, 256) if w is None else w
+        sc = take(small, 4 * n, 16) if sc is None else sc
+        y = take(small, 4 * n, 16) if y is None else y
+        descs.append(dict(OPCODE=C.OP_GEMM, CTRL=C.ctrl(C.QM_ROWCOL), EPI=C.epi(), A_OFF=q, W_OFF=w, SCALE_OFF=sc,
+                          Y_OFF=y, HDR_RSV=s // 16, M=1, N=n, K=k))
+        return w, sc, y, n * k + 4 * n + 4 * n
+
+    for _ in range(QWEN3_LAYERS):
+        for k, projs in ((H, (Qd, KV, KV)), (Qd, (H,)), (H, (FF, FF)), (FF, (H,))):
+            q, s, xb = quant(k)
+            nbytes += xb
+            for n in projs:
+                w, sc, y, b = gemm(q, s, k, n)
+                fills += [("int8", w, n * k), ("scale", sc, n)]
+                nbytes += b
+    q, s, xb = quant(H)
+    nbytes += xb
+    hw, hsc, hy = take(big, V * H, 256), take(small, 4 * V, 16), take(small, 4 * V, 16)
+    fills += [("int8", hw, V * H), ("scale", hsc, V)]
+    rows = V // 4
+    for blk in range(4):
+        nbytes += gemm(q, s, H, rows, hw + blk * rows * H, hsc + 4 * blk * rows, hy + 4 * blk * rows)[3]
+    qaddr = take(small, 64 * len(descs), 64)
+    if small[0] >= 16 * (1 << 24):
+        raise RuntimeError("row scales must lie below 16 * 2^24 bytes (the HDR_RSV field)")
+    base_big = (small[0] + 4095) // 4096 * 4096
+    image = torch.empty(base_big + big[0], dtype=torch.uint8, device="cuda")
+    image[:base_big].zero_()
+    for kind, off, n in fills:
+        off = off + (base_big if kind == "int8" else 0)
+        if kind == "int8":
+            image[off:off + n].view(torch.int8).copy_(
+                torch.randint(-127, 128, (n,), dtype=torch.int8, device="cuda", generator=gen))
+        elif kind == "scale":
+            image[off:off + 4 * n].view(torch.float32).copy_(torch.rand(n, device="cuda", generator=gen) * 9e-3 + 1e-3)
+        else:
+            image[off:off + 4 * n].view(torch.float32).copy_(torch.randn(n, device="cuda", generator=gen))
+    raw = []
+    for d in descs:
+        if d["OPCODE"] == C.OP_GEMM:
+            d = dict(d, W_OFF=d["W_OFF"] + base_big)
+        raw.append(encode_descriptor(dict(MAGIC=C.MAGIC, VERSION=C.VERSION, VALID=1, **d)))
+    host_q = b"".join(raw)
+    image[qaddr:qaddr + len(host_q)].copy_(torch.frombuffer(bytearray(host_q), dtype=torch.uint8).cuda())
+    torch.cuda.synchronize()
+    st = _lib.QueueStatus()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        rc = lib.tars_run_queue(image.data_ptr(), image.numel(), qaddr, len(raw), host_q, 0, 0, ctypes.byref(st),
+                                stream)
+        if rc != 0 or not st.done:
+            raise RuntimeError(f"queue: status {rc} done={st.done} err={st.err_code} op={st.op_idx}: "
+                               f"{_lib.last_error()}")
+
+    res = {"descriptors": len(raw), "image_bytes": int(image.numel()), "algorithmic_bytes_per_step": nbytes}
+    for fusion in (1, 0):
+        prev = lib.tars_set_queue_fusion(fusion)
+        try:
+            for _ in range(warmup):
+                run()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                run()
+            torch.cuda.synchronize()
+            t = (time.perf_counter() - t0) / steps
+        finally:
+            lib.tars_set_queue_fusion(prev)
+        key = "fused" if fusion else "unfused"
+        res[key] = {"launches_per_step": 113 if fusion else len(raw), "ms_per_step": round(t * 1e3, 4),
+                    "GBps": round(nbytes / t / 1e9, 1)}
+    del image
+    torch.cuda.empty_cache()
+    return res
 
 
 def capture(torch, launches):
@@ -381,12 +491,20 @@ def config_suite(torch, lib, seed: int) -> dict:
 
 
 # ------------------------------------------------------------------------------ CPU baseline
-def cpu_baseline(launches, target_s: float) -> dict:
+def cpu_baseline(launches, target_s: float, spot) -> dict:
     """The numpy oracle (the golden path's own algorithm: the per-token quantizer, int64 matmul and
     the elementwise fp32 epilogue) over the decode-step launches in model order, on this host's CPU,
-    single-threaded, until about target_s seconds of compute have passed. Same bytes/s unit."""
+    single-threaded, until about target_s seconds of compute have passed. Same bytes/s unit. Also
+    checks the GPU's timed layer-0 q/k/v outputs (spot = (x, [(W, scol, y), ...])) bit for bit
+    against the oracle's."""
+    import numpy as np
     from oracle import golden as G
     from oracle import numerics as F
+
+    x0, mats0 = spot
+    xq, xs = F.quant_rows(x0)
+    exact = all(np.array_equal(y.view(np.uint32), G.gemm_rowcol(xq, xs, W, sc).view(np.uint32))
+                for W, sc, y in mats0)
 
     host = {}
 
@@ -422,6 +540,7 @@ def cpu_baseline(launches, target_s: float) -> dict:
     return {"value": round(done_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"numpy oracle over {calls} launches of the decode step in model order "
                       f"({steps:.2f} steps, {elapsed:.1f} s of compute)",
+            "bit_exact_spot_check_layer0_qkv": exact,
             "cpu_model": cpu, "os_cpu_count": os.cpu_count(),
             "threads_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS")}}
 
@@ -434,7 +553,6 @@ def main() -> int:
               "output channels over several GPUs is not implemented); use --gpus 1", file=sys.stderr)
         return 2
     os.environ.setdefault("OMP_NUM_THREADS", "1")
-    import numpy as np
     import torch
     import opentars_amd
 
@@ -480,14 +598,9 @@ def main() -> int:
         if entry and entry.get("algorithmic_bytes") == dom["avg_bytes_per_launch"]:
             traffic = entry["traffic_bytes"]
 
-    # bit-exact spot check of layer 0's q/k/v outputs of the timed data against the oracle
-    from oracle import golden as G
-    from oracle import numerics as F
     l0 = next(l for l in launches if l.name == "L0.qkv")
-    xq, xs = F.quant_rows(l0.operands["x"].cpu().numpy())
-    spot = all(np.array_equal(y.cpu().numpy().view(np.uint32),
-                              G.gemm_rowcol(xq, xs, W.cpu().numpy(), sc.cpu().numpy()).view(np.uint32))
-               for W, sc, y in l0.operands["mats"])
+    l0_out = [(W.cpu().numpy(), sc.cpu().numpy(), y.cpu().numpy()) for W, sc, y in l0.operands["mats"]]
+    l0_x = l0.operands["x"].cpu().numpy()
     # the golden model's unfused sequence (ROW_QUANT + one GEMM per projection), for comparison
     g_unf = capture(torch, unfused)
     unfused_s = time_graph(torch, g_unf, max(3, args.steps // 4), warmup=3)
@@ -509,11 +622,12 @@ def main() -> int:
     del big, dst
     torch.cuda.empty_cache()
 
+    log("descriptor-queue executor")
+    queue = None if args.no_queue else queue_decode_step(torch, lib, args.seed, max(3, args.steps // 10), 3)
     log("per-config measurements")
     configs = {} if args.no_configs else config_suite(torch, lib, args.seed)
     log("cpu baseline")
-
-    cpu = None if args.no_cpu_baseline else cpu_baseline(unfused, args.cpu_seconds)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(unfused, args.cpu_seconds, (l0_x, l0_out))
 
     value = step_bytes / step_s / 1e9
     line = {
@@ -546,7 +660,7 @@ def main() -> int:
         "lm_head": {k: configs.get(k) for k in ("lm_head_M1_K1024_N151936", "lm_head_fused_quant_M1_K1024_N151936")},
         "kernels": kernels,
         "device_copy_GBps": round(copy_gbps, 1),
-        "bit_exact_spot_check": spot,
+        "queue_executor": queue,
         "cpu_baseline": cpu,
         "configs": configs,
         "wall_s_timed": round(t_wall, 3),

@@ -71,7 +71,8 @@ int tars_quant_rows(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* 
  *   A     int8 [M, K], row stride lda bytes      W     int8 [N, K] dense row-major
  *   srow  fp32 [M] or NULL                        scol  fp32 [scol_count]
  *   bias  fp32 [N] or NULL                        Y     [M, N] of the output format, stride ldy
- * M == 1 runs the HBM-streaming GEMV (packed int8 dot products); M >= 2 runs INT8 MFMA tiles.
+ * Small M runs the HBM-streaming GEMV family (packed int8 dot products, up to 4 activation rows
+ * per weight read); larger M runs INT8 MFMA tiles (see tars_set_w8a8_path for the rule).
  * Rules: N % 16 == 0, K % 16 == 0, 16 <= K <= 65535, act in 0..7, out in {FP32, BF16, INT8},
  * out_scale_bits == 0 unless out == INT8, 16-byte aligned pointers and strides.
  */
@@ -183,10 +184,13 @@ typedef struct tars_queue_status {
 
 /*
  * Runs the n descriptors at image + queue_addr, in order, on `stream`. `image` is the device
- * address of the DDR image (image_len bytes); every descriptor address is an offset into it. The
- * descriptors are read from the image (the call waits for the stream's earlier work to do so)
- * and checked on the host in the contract's order; the GPU-run ones are enqueued on `stream` and
- * have not necessarily finished when the call returns. Returns TARS_OK with *st describing the
+ * address of the DDR image (image_len bytes); every descriptor address is an offset into it.
+ * host_queue NULL: the descriptors are read from the image (the call waits for the stream's
+ * earlier work to do so); otherwise host_queue is the caller's HOST copy of the same 64 * n bytes
+ * and the call does not wait (a descriptor whose output lands on a later descriptor of the queue
+ * still makes it wait and re-read those from the image). The descriptors are checked on the host
+ * in the contract's order; the GPU-run ones are enqueued on `stream` and have not necessarily
+ * finished when the call returns. Returns TARS_OK with *st describing the
  * outcome (a contract error stops the queue at its descriptor, keeping earlier writes), or
  * TARS_E_OVERLAP when a descriptor's output overlaps one of its inputs (the golden's
  * ContractError; st->op_idx names it, nothing of it ran), TARS_E_ARG, or TARS_E_DEVICE.
@@ -194,7 +198,8 @@ typedef struct tars_queue_status {
  * a GEMM with K > 4096 is E_OPCODE), golden.py:48-50.
  */
 int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int32_t n,
-                   int32_t core_id, int32_t gemv_only, tars_queue_status* st, void* stream);
+                   const uint8_t* host_queue, int32_t core_id, int32_t gemv_only,
+                   tars_queue_status* st, void* stream);
 
 /*
  * The full check of one 64-byte descriptor (host memory) against an image of image_len bytes:
@@ -213,6 +218,17 @@ int tars_decode_descriptor(const uint8_t* desc, uint64_t* fields);
 /* The CRC-32 a descriptor's CRC32 field must hold: zlib's crc32 over the 64 bytes with bytes
  * 4..7 read as zero (contract.py:154-181). Host only. */
 uint32_t tars_descriptor_crc(const uint8_t* desc);
+
+/* Writes the 64-byte descriptor holding the 23 fields (layout order as tars_decode_descriptor);
+ * with fix_crc the CRC32 field is replaced by the descriptor's CRC (contract.py:154-167 encode).
+ * TARS_E_ARG if a value does not fit its field. Host only. */
+int tars_encode_descriptor(const uint64_t* fields, int32_t fix_crc, uint8_t* desc);
+
+/* Peephole fusion in tars_run_queue (benchmark and test control, not part of the reference's
+ * interface): 1 (default) runs a decode-row ROW_QUANT and the QM_ROWCOL GEMMs that read its output
+ * as one fused launch, 0 runs every descriptor on its own. Results are identical either way.
+ * Returns the previous setting. Process-wide. */
+int tars_set_queue_fusion(int on);
 
 #ifdef __cplusplus
 }

@@ -1,4 +1,5 @@
-"""Codes of the openTARS descriptor contract used by the matrix path (tars_mini/contract.py:88-111).
+"""Codes of the openTARS descriptor contract used by the matrix path and the queue executor
+(tars_mini/contract.py:39-133).
 
 The values are the contract's own (they are what a descriptor carries), so they must be equal.
 """
@@ -20,3 +21,20 @@ ERR_NAMES = {E_OK: "OK", E_MAGIC: "E_MAGIC", E_VERSION: "E_VERSION", E_CRC: "E_C
              E_OPCODE: "E_OPCODE", E_FIELD: "E_FIELD", E_ALIGN: "E_ALIGN", E_RANGE: "E_RANGE"}
 K_MAX = 65535
 GEMV_K = 4096        # the KV260 GEMV unit's longest x: the reference splits longer K (llm.py:195)
+
+# descriptor header and opcodes (contract.py:39-57, 74-86)
+MAGIC, VERSION = 0xAA55, 0x0002
+DESC_BYTES = 64
+OP_CONV, OP_GEMM, OP_RELU, OP_ROW, OP_CONV_ACT, OP_ELT, OP_ROPE, OP_FDOT = 1, 2, 3, 4, 5, 6, 7, 8
+ROW_SOFTMAX, ROW_LAYERNORM, ROW_RMSNORM, ROW_L2NORM, ROW_QUANT = 0, 1, 2, 3, 4
+
+
+def ctrl(qmode: int = QM_TENSOR, symmetric: int = 1, a_dtype: int = DT_INT8, w_dtype: int = DT_INT8,
+         fusion: int = 0) -> int:
+    """The CTRL field: qmode[2:0], symmetric[3], a_dtype[7:4], w_dtype[11:8], fusion[12]."""
+    return (qmode & 7) | (symmetric & 1) << 3 | (a_dtype & 15) << 4 | (w_dtype & 15) << 8 | (fusion & 1) << 12
+
+
+def epi(act: int = ACT_NONE, out: int = OUT_FP32, bias: int = 0) -> int:
+    """The EPI field: act[1:0], out[3:2], bias[4], act[2] at bit 5."""
+    return (act & 3) | (out & 3) << 2 | (bias & 1) << 4 | (act >> 2 & 1) << 5

@@ -3,7 +3,8 @@
 // :260-267 / :440-448 the overlap rules; tars_mini/contract.py:14-38 the 512-bit layout and
 // :154-181 encode / decode / CRC).
 //
-// Host side: the descriptors are read from the image once (one device-to-host copy), decoded,
+// Host side: the descriptors are read from the image once (one device-to-host copy; or taken from
+// the caller's host copy of the same bytes), decoded,
 // CRC-checked and validated in the contract's order, their byte segments range- and overlap-
 // checked; every descriptor the GPU runs (W8A8 GEMM in QM_TENSOR / QM_CHANNEL / QM_ROWCOL, the
 // W4A16 group GEMM, ROW_QUANT) is then enqueued on the caller's stream with pointers into the
@@ -12,6 +13,8 @@
 // overlaps an input (the golden's ContractError), or at a valid descriptor of another kind, which
 // is handed back to the caller (host_op = 1). A descriptor whose output lands on a later
 // descriptor of the same queue makes the executor wait for it and re-read the rest of the queue.
+// A decode-row ROW_QUANT and the QM_ROWCOL GEMMs that read it run as one fused launch (peephole
+// fusion, bit-identical to the one-by-one order; see fuse_group).
 #include <algorithm>
 #include <cstring>
 #include <string>
@@ -445,6 +448,74 @@ void set_last_error(const std::string& what);
 
 namespace {
 
+bool g_fusion = true;
+
+u128 addr(const Desc& d, Field off) { return static_cast<u128>(d[F_BASE_ADDR]) + d[off]; }
+
+// Peephole fusion for decode rows: a ROW_QUANT with M = 1 followed by up to 4 QM_ROWCOL W8A8
+// GEMMs (each valid on its own) whose A row is exactly the quantizer's int8 output and whose row
+// scale is its scale runs as one tars_quant_gemm_w8a8 launch, which also writes the quantizer's
+// outputs: bit-identical to running them one by one (the GEMMs read the same int8 values and
+// scale the kernel computes). No fusion when an output of the group lands on a later descriptor
+// of the queue; when the group's outputs overlap each other or any input of the group, the fused
+// call refuses before launching and the descriptors run one by one. `fused` = GEMMs folded in.
+int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
+               int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
+               int& fused) {
+  fused = 0;
+  const Desc& dq = quant.d;
+  if (!g_fusion || dq[F_OPCODE] != OP_ROW || dq[F_M] != 1 || (reinterpret_cast<uintptr_t>(image) + dq[F_BASE_ADDR]) % 16)
+    return TARS_OK;
+  std::vector<Checked> members;
+  for (int32_t j = i + 1; j < n && static_cast<uint64_t>(j) < in_image && members.size() < 4; ++j) {
+    Checked c = check(q.data() + static_cast<size_t>(j) * kDescBytes, image_len, core_id, gemv_only);
+    const Desc& d = c.d;
+    if (c.err != E_OK || c.overlap || d[F_OPCODE] != OP_GEMM || is_w4(d) || (d[F_CTRL] & 7) != QM_ROWCOL ||
+        d[F_M] != 1 || d[F_K] != dq[F_N] || addr(d, F_A_OFF) != addr(dq, F_Y_OFF) ||
+        static_cast<u128>(d[F_BASE_ADDR]) + 16 * static_cast<u128>(d[F_HDR_RSV]) != addr(dq, F_SCALE_OFF) ||
+        (reinterpret_cast<uintptr_t>(image) + d[F_BASE_ADDR]) % 16)
+      break;
+    members.push_back(std::move(c));
+  }
+  if (members.empty()) return TARS_OK;
+  const Segs rest = {{rest_lo, rest_hi}};
+  if (rest_lo < rest_hi) {
+    if (overlaps(rest, quant.y) || overlaps(rest, quant.extra)) return TARS_OK;
+    for (const Checked& c : members)
+      if (overlaps(rest, c.y)) return TARS_OK;
+  }
+  tars_w8a8_out outs[4];
+  for (size_t k = 0; k < members.size(); ++k) {
+    const Desc& d = members[k].d;
+    uint8_t* B = image + d[F_BASE_ADDR];
+    outs[k].W = reinterpret_cast<const int8_t*>(B + d[F_W_OFF]);
+    outs[k].scol = reinterpret_cast<const float*>(B + d[F_SCALE_OFF]);
+    outs[k].bias = has_bias(d[F_EPI]) ? reinterpret_cast<const float*>(B + d[F_BIAS_OFF]) : nullptr;
+    outs[k].Y = B + d[F_Y_OFF];
+    outs[k].ldy = static_cast<int64_t>(strides(d).ldy);
+    outs[k].N = static_cast<int32_t>(d[F_N]);
+    outs[k].act = static_cast<int32_t>(act_code(d[F_EPI]));
+    outs[k].out = static_cast<int32_t>(out_code(d[F_EPI]));
+    outs[k].out_scale_bits = static_cast<uint32_t>(d[F_OUT_SCALE]);
+  }
+  uint8_t* B = image + dq[F_BASE_ADDR];
+  const Strides sq = strides(dq);
+  const int rc = tars_quant_gemm_w8a8(reinterpret_cast<const float*>(B + dq[F_A_OFF]), static_cast<int64_t>(sq.lda),
+                                      reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
+                                      reinterpret_cast<float*>(B + dq[F_SCALE_OFF]), 1, static_cast<int32_t>(dq[F_N]),
+                                      outs, static_cast<int32_t>(members.size()), s);
+  if (rc == TARS_E_OVERLAP) {
+    tars::set_last_error("");
+    return TARS_OK;
+  }
+  if (rc == TARS_OK) fused = static_cast<int>(members.size());
+  return rc;
+}
+
+}  // namespace
+
+namespace {
+
 int queue_fail(int code, const std::string& what) {
   tars::set_last_error(what);
   return code;
@@ -474,8 +545,33 @@ int tars_decode_descriptor(const uint8_t* desc, uint64_t* fields) {
 
 uint32_t tars_descriptor_crc(const uint8_t* desc) { return desc ? crc32_desc(desc) : 0u; }
 
-int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int32_t n, int32_t core_id,
-                   int32_t gemv_only, tars_queue_status* st, void* stream) {
+int tars_encode_descriptor(const uint64_t* fields, int32_t fix_crc, uint8_t* desc) {
+  tars::set_last_error("");
+  if (!fields || !desc) return queue_fail(TARS_E_ARG, "NULL fields or descriptor");
+  uint8_t raw[kDescBytes] = {};
+  for (int i = 0; i < kFields; ++i) {
+    const BitRange r = kBits[i];
+    if (r.width < 64 && (fields[i] >> r.width) != 0)
+      return queue_fail(TARS_E_ARG, "a field value does not fit its width");
+    for (int b = 0; b < r.width; ++b)
+      if ((fields[i] >> b) & 1) raw[(r.lo + b) / 8] |= static_cast<uint8_t>(1u << ((r.lo + b) % 8));
+  }
+  if (fix_crc) {
+    const uint32_t c = crc32_desc(raw);
+    for (int b = 0; b < 4; ++b) raw[4 + b] = static_cast<uint8_t>(c >> (8 * b));
+  }
+  std::memcpy(desc, raw, kDescBytes);
+  return TARS_OK;
+}
+
+int tars_set_queue_fusion(int on) {
+  const int prev = g_fusion ? 1 : 0;
+  g_fusion = on != 0;
+  return prev;
+}
+
+int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int32_t n, const uint8_t* host_queue,
+                   int32_t core_id, int32_t gemv_only, tars_queue_status* st, void* stream) {
   tars::set_last_error("");
   if (!image || !st || n < 0) return queue_fail(TARS_E_ARG, "NULL image or status, or n < 0");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -493,7 +589,11 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       return queue_fail(TARS_E_DEVICE, "reading the queue from the image failed");
     return TARS_OK;
   };
-  if (int rc = reread(0)) return rc;
+  if (host_queue) {
+    if (!q.empty()) std::memcpy(q.data(), host_queue, q.size());
+  } else if (int rc = reread(0)) {
+    return rc;
+  }
   for (int32_t i = 0; i < n; ++i) {
     st->op_idx = i;
     if (static_cast<uint64_t>(i) >= in_image) {  // the descriptor itself lies past the image
@@ -511,6 +611,14 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       st->host_op = 1;
       return TARS_OK;
     }
+    const u128 later = static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(i) + 1);
+    int fused = 0;
+    if (int rc = fuse_group(image, c, q, i, in_image, n, later, q_end, image_len, core_id, gemv_only != 0, s, fused))
+      return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+    if (fused) {
+      i += fused;  // the quantizer and `fused` GEMMs ran as one launch
+      continue;
+    }
     bool needs_host = false;
     if (int rc = launch(image, c.d, s, needs_host)) {
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
@@ -520,7 +628,6 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       return TARS_OK;
     }
     // an output written over a later descriptor of this queue: wait for it and read them again
-    const u128 later = static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(i) + 1);
     const Segs rest = {{later, q_end}};
     if (later < q_end && (overlaps(rest, c.y) || (!c.extra.empty() && overlaps(rest, c.extra)))) {
       if (int rc = reread(static_cast<uint64_t>(i) + 1)) return rc;

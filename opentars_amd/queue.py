@@ -25,11 +25,8 @@ import numpy as np
 import torch
 
 from . import _lib
+from .contract import DESC_BYTES, ERR_NAMES
 from .ops import ContractError, TarsError, _device
-
-ERR_NAMES = {0: "OK", 1: "E_MAGIC", 2: "E_VERSION", 3: "E_CRC", 4: "E_VALID", 5: "E_OPCODE", 6: "E_FIELD",
-             7: "E_ALIGN", 8: "E_RANGE"}
-DESC_BYTES = 64
 
 
 @dataclass
@@ -89,9 +86,9 @@ class Machine:
         self.image[addr:addr + len(data)] = torch.frombuffer(bytearray(data), dtype=torch.uint8).to(self.image.device)
 
     # ------------------------------------------------------------------ the queue
-    def _gpu(self, queue_addr: int, n: int) -> Status:
+    def _gpu(self, queue_addr: int, n: int, descs: bytes | None = None) -> Status:
         st = _lib.QueueStatus()
-        rc = _lib.lib().tars_run_queue(self.image.data_ptr(), self.image.numel(), queue_addr, n, self.core_id,
+        rc = _lib.lib().tars_run_queue(self.image.data_ptr(), self.image.numel(), queue_addr, n, descs, self.core_id,
                                        int(self.gemv_only), ctypes.byref(st), torch.cuda.current_stream().cuda_stream)
         if rc != _lib.OK:
             _raise(rc)
@@ -106,18 +103,21 @@ class Machine:
         self.image.copy_(torch.from_numpy(after.copy()).to(self.image.device))
         return Status(bool(st.done), int(st.err_code), 0)
 
-    def run_queue(self, queue_addr: int, queue_len: int) -> Status:
+    def run_queue(self, queue_addr: int, queue_len: int, descs: bytes | None = None) -> Status:
         """Runs queue_len descriptors at queue_addr in order; the GPU work is stream-ordered on the
         current stream (read the image through .ddr / .read, which synchronize). An output that
-        overlaps an input raises ContractError, as the golden does."""
+        overlaps an input raises ContractError, as the golden does. descs: optionally the caller's
+        host copy of the queue's bytes (then the call does not wait to read them from the image)."""
         base = 0
         while True:
-            st = self._gpu(queue_addr + DESC_BYTES * base, queue_len - base)
+            part = None if descs is None else descs[DESC_BYTES * base:DESC_BYTES * queue_len]
+            st = self._gpu(queue_addr + DESC_BYTES * base, queue_len - base, part)
             st.op_idx += base
             if st.done or not st.host_op or self.host is None:
                 self.status = st
                 return st
             hs = self._on_host(queue_addr + DESC_BYTES * st.op_idx)
+            descs = None                                      # the host step may have rewritten the queue
             if not hs.done:
                 self.status = Status(False, hs.err_code, st.op_idx)
                 return self.status
@@ -164,4 +164,30 @@ def descriptor_crc(desc: bytes) -> int:
     return int(_lib.lib().tars_descriptor_crc(bytes(desc)))
 
 
-__all__ = ["Machine", "Status", "run", "check_descriptor", "decode_descriptor", "descriptor_crc", "ERR_NAMES"]
+FIELDS = ("MAGIC", "VERSION", "CORE_ID", "HDR_RSV", "OPCODE", "CTRL", "GROUP_SIZE", "EPI", "BASE_ADDR", "A_OFF",
+          "W_OFF", "Y_OFF", "SCALE_OFF", "BIAS_OFF", "M", "N", "K", "LDA16", "OUT_SCALE", "CRC32", "VALID", "LDY16",
+          "DEP_SIG")
+
+
+def encode_descriptor(fields: dict, fix_crc: bool = True) -> bytes:
+    """A 64-byte descriptor from field values by name (absent fields are 0), its CRC fixed
+    (contract.py:154-167 encode). Host only."""
+    unknown = set(fields) - set(FIELDS)
+    if unknown:
+        raise ValueError(f"unknown descriptor fields {sorted(unknown)}")
+    vals = (ctypes.c_uint64 * 23)(*[int(fields.get(n, 0)) for n in FIELDS])
+    out = ctypes.create_string_buffer(DESC_BYTES)
+    rc = _lib.lib().tars_encode_descriptor(vals, int(fix_crc), out)
+    if rc != _lib.OK:
+        _raise(rc)
+    return out.raw
+
+
+def set_fusion(on: bool) -> bool:
+    """Peephole fusion of decode-row ROW_QUANT + its QM_ROWCOL GEMMs in run_queue (default on);
+    returns the previous setting."""
+    return bool(_lib.lib().tars_set_queue_fusion(int(on)))
+
+
+__all__ = ["Machine", "Status", "run", "check_descriptor", "decode_descriptor", "descriptor_crc",
+           "encode_descriptor", "set_fusion", "FIELDS", "ERR_NAMES"]

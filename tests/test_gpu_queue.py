@@ -138,7 +138,7 @@ def random_program(seed: int) -> Program:
     p = Program(seed)
     rng = p.rng
     for _ in range(int(rng.integers(4, 9))):
-        kind = int(rng.integers(0, 4))
+        kind = int(rng.integers(0, 5))
         M = int(rng.choice([1, 2, 4, 5, 17, 40]))
         if kind == 0:                                   # ROW_QUANT feeding a QM_ROWCOL GEMM (RAW)
             K = 16 * int(rng.integers(1, 40))
@@ -149,8 +149,13 @@ def random_program(seed: int) -> Program:
                    int(rng.choice([Q.QM_TENSOR, Q.QM_CHANNEL, Q.QM_ROWCOL])))
         elif kind == 2:
             add_w4(p, min(M, 5), 16 * int(rng.integers(1, 8)), 256 * int(rng.integers(1, 5)))
-        else:
+        elif kind == 3:
             add_quant(p, M, 16 * int(rng.integers(1, 60)))
+        else:                                           # a decode row shared by 1-5 GEMMs (fusable)
+            K = 16 * int(rng.integers(1, 80))
+            q, ldq, s = add_quant(p, 1, K)
+            for _ in range(int(rng.integers(1, 6))):
+                add_w8(p, 1, 16 * int(rng.integers(1, 12)), K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s)
     return p
 
 
@@ -171,13 +176,49 @@ def first_diff(a: bytes, b: bytes) -> int:
     return int(np.argmax(x)) if x.any() else -1
 
 
+@pytest.mark.parametrize("fusion", [True, False])
 @pytest.mark.parametrize("seed", range(12))
-def test_random_programs_match_the_oracle(seed):
+def test_random_programs_match_the_oracle(seed, fusion):
+    """With and without the executor's quantizer + GEMM fusion."""
     p = random_program(seed)
-    (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    prev = NQ.set_fusion(fusion)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    finally:
+        NQ.set_fusion(prev)
     assert ost.done and same_status(ost, gst), (ost, gst)
     gd = bytes(g.ddr)
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_host_copy_of_the_queue_gives_the_same_result(seed):
+    p = random_program(200 + seed)
+    img = p.image()
+    o = Q.Machine(img)
+    assert o.run_queue(QADDR, len(p.descs)).done
+    g = NQ.Machine(img)
+    assert g.run_queue(QADDR, len(p.descs), descs=b"".join(p.descs)).done
+    assert bytes(g.ddr) == bytes(o.ddr)
+
+
+def test_fusion_group_with_a_hazard_runs_one_by_one():
+    """A decode row read by three GEMMs where the second GEMM writes over the third's weights: the
+    fused launch would race, so the group runs descriptor by descriptor (the third GEMM then reads
+    the second's output as its weights, as the golden's order has it)."""
+    p = Program(70)
+    K = 64
+    q, ldq, s = add_quant(p, 1, K)
+    add_w8(p, 1, 32, K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s)
+    add_w8(p, 1, 16, K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s, out=Q.OUT_INT8)
+    add_w8(p, 1, 16, K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s)
+    f1, f2 = Q.decode(p.descs[2]), Q.decode(p.descs[3])
+    f1.pop("CRC32")
+    f1.update(Y_OFF=f2["W_OFF"], LDY16=0)              # int8 [1, 16] lands in the third matrix's weights
+    p.descs[2] = Q.encode(f1)
+    (o, ost), (g, gst) = both(p.image(), 4)
+    assert ost.done and same_status(ost, gst)
+    assert bytes(g.ddr) == bytes(o.ddr)
 
 
 def test_worked_example_on_the_gpu():

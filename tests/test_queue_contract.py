@@ -213,6 +213,18 @@ def test_native_decode_and_crc_match_on_random_bytes():
         assert NQ.descriptor_crc(raw) == zlib.crc32(bytes(z)) & 0xFFFFFFFF
 
 
+def test_native_encode_matches_the_oracle():
+    NQ = native()
+    rng = np.random.default_rng(12)
+    for _ in range(500):
+        f = {n: int(rng.integers(0, 1 << min(hi - lo + 1, 63))) for n, (hi, lo) in Q.LAYOUT.items()}
+        fix = bool(rng.integers(0, 2))
+        assert NQ.encode_descriptor(f, fix) == Q.encode(f if not fix else {k: v for k, v in f.items() if k != "CRC32"},
+                                                        fix_crc=fix)
+    with pytest.raises(Exception):
+        NQ.encode_descriptor({"M": 1 << 16})
+
+
 def valid_templates() -> list[dict]:
     """One valid descriptor of each kind the contract knows."""
     b = dict(MAGIC=Q.MAGIC, VERSION=Q.VERSION, VALID=1, A_OFF=0x100, Y_OFF=0x800, W_OFF=0x1000, M=2, N=16)
