@@ -5,9 +5,12 @@
 // group. Thread c of a row owns chunk c (so a row of K/2 bytes is read by K/32 consecutive
 // threads, fully coalesced), and the four threads of a group are four consecutive lanes.
 //
-// Alignment is fused into the GEMV prologue: each thread aligns the 32 activations of its chunk;
-// the group's exponent maximum and NaN/inf flags meet through two quad lane permutes; each mantissa
-// (an int16 in [-16384, 16384]) is rounded to nearest-even exactly as the reference does.
+// Alignment is fused into the GEMV prologue: the workgroup aligns its activation row once,
+// cooperatively (8 lanes per 128-wide group, 16 elements each; the group's exponent maximum meets
+// through DPP lane permutes), into LDS byte planes that every weight row of the workgroup reads.
+// Each mantissa (an int16 in [-16384, 16384]) is rounded to nearest-even exactly as the reference
+// does: for finite groups as rint(x * 2^(140 - e_eff)), otherwise by the integer shift rule with
+// the NaN / infinity cases.
 //
 // Exact int16 x int4 dots on v_dot4 (signed 8-bit): a mantissa a is split as a = 256 * ah + al with
 // al, ah signed bytes (al = the low byte read as signed, ah in [-64, 64]); a weight nibble w is
@@ -61,52 +64,58 @@ __device__ __forceinline__ void load_chunk_bits(const void* x, int64_t lda, int 
 }
 
 // Aligns NE elements held by each of GL consecutive lanes that together form one 128-wide group
-// (NE * GL == 128; every lane of the wave must call it, dead lanes on shadow data). Outputs the
-// signed mantissas and the group's fp32 scale encoding. Straight-line selects, no per-element
-// branches: the shift is clamped to 31, and a shift of 25 or more then rounds to 0 by itself (the
-// 24-bit significand is below the half-way point), as the reference requires.
+// (NE * GL == 128; every lane of the wave must call it, dead lanes on shadow data). Inputs are raw
+// fp32 encodings (not flushed). Outputs the signed mantissas and the group's fp32 scale encoding.
 template <int NE, int GL>
-__device__ __forceinline__ void align_elems(const uint32_t* xb, int* mant, uint32_t& scale_bits) {
+__device__ __forceinline__ void align_elems(const uint32_t* xraw, int* mant, uint32_t& scale_bits) {
   static_assert(NE * GL == kGroup, "a group is 128 elements");
-  int emax = 0, flags = 0;
+  // A subnormal's exponent field is 0 whether or not it is flushed, so emax needs no flush.
+  int emax = 0;
+#pragma unroll
+  for (int i = 0; i < NE; ++i) emax = max(emax, static_cast<int>((xraw[i] >> 23) & 0xFF));
+  emax = group_reduce<GL>(emax, OpMaxU{});
+  const int e_eff = max(emax, 14);
+  if (__builtin_amdgcn_ballot_w64(emax < 16 || emax == 255) == 0) {
+    // Every group of the wave is finite with emax >= 16 (the usual case). For a finite x of
+    // exponent e the reference's mantissa is its significand shifted right by sh = 10 + e_eff - e
+    // with round-to-nearest-even, i.e. rint(sig * 2^-sh) = rint(x * 2^(140 - e_eff)): one exact
+    // power-of-two product (|result| <= 2^14) and v_rndne_f32 (round half to even), the sign
+    // carried through. A product small enough to be subnormal is far below 1/2 and rounds to 0,
+    // and so does an unflushed subnormal input (|x * 2^(140 - e_eff)| < 2^-126 * 2^124), so no
+    // flush is needed. Equal to the shift rule for every significand and shift (exhaustive CPU
+    // check) and on real rows, flushed or not (CPU check against the aligner's restatement).
+    const float p = __uint_as_float(static_cast<uint32_t>(267 - e_eff) << 23);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) mant[i] = static_cast<int>(__builtin_rintf(__uint_as_float(xraw[i]) * p));
+    scale_bits = static_cast<uint32_t>(e_eff - 13) << 23;
+    return;
+  }
+  // Some group of the wave holds a NaN or an infinity, or is all zeros / tiny (emax < 16).
+  uint32_t xb[NE];
+  int flags = 0;
 #pragma unroll
   for (int i = 0; i < NE; ++i) {
+    xb[i] = (xraw[i] & kExpo) ? xraw[i] : (xraw[i] & kSign);  // ftz
     const int e = (xb[i] >> 23) & 0xFF;
-    emax = max(emax, e);
     flags |= e == 255 ? ((xb[i] & kMant) ? 1 : 2) : 0;
   }
-  emax = group_reduce<GL>(emax, OpMaxU{});
   flags = group_reduce<GL>(flags, OpOr{});
   const bool grp_nan = flags & 1;
   const bool grp_inf = ((flags & 2) != 0) & !grp_nan;
-  const int e_eff = max(emax, 14);
-  // Round-to-nearest-even right shift as (sig + 2^(sh-1) - 1 + lsb) >> sh (equal to the reference's
-  // kept/dropped/half rule for every 24-bit significand and shift; checked exhaustively on the CPU).
-  // Inputs are flushed, so exponent 0 means a zero: its significand is taken as 0 and rounds to 0.
-  if (__builtin_amdgcn_ballot_w64(flags != 0) == 0) {
-    // no NaN or infinity anywhere in this wave (the usual case)
+  // Round-to-nearest-even right shift as (sig + 2^(sh-1) - 1 + lsb) >> sh (equal to the
+  // reference's kept/dropped/half rule for every 24-bit significand and shift; checked
+  // exhaustively on the CPU); exponent 0 (a flushed zero) has significand 0.
 #pragma unroll
-    for (int i = 0; i < NE; ++i) {
-      const uint32_t b = xb[i];
-      const int e = (b >> 23) & 0xFF;
-      const uint32_t sig = e ? ((b & kMant) | (1u << 23)) : 0u;
-      const uint32_t sh = static_cast<uint32_t>(min(10 + e_eff - e, 31));  // >= 10
-      const int mag = static_cast<int>((sig + ((1u << (sh - 1u)) - 1u) + ((sig >> sh) & 1u)) >> sh);
-      mant[i] = (b & kSign) ? -mag : mag;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NE; ++i) {
-      const uint32_t b = xb[i];
-      const int e = (b >> 23) & 0xFF;
-      const uint32_t frac = b & kMant;
-      const uint32_t sig = ((e != 0) & (e != 255)) ? (frac | (1u << 23)) : 0u;
-      const uint32_t sh = static_cast<uint32_t>(min(10 + e_eff - e, 31));
-      int mag = static_cast<int>((sig + ((1u << (sh - 1u)) - 1u) + ((sig >> sh) & 1u)) >> sh);
-      mag = (grp_inf & (e == 255) & (frac == 0)) ? 16384 : mag;
-      mag = grp_nan ? 0 : mag;
-      mant[i] = (b & kSign) ? -mag : mag;
-    }
+  for (int i = 0; i < NE; ++i) {
+    const uint32_t b = xb[i];
+    const int e = (b >> 23) & 0xFF;
+    const uint32_t frac = b & kMant;
+    const uint32_t sig = ((e != 0) & (e != 255)) ? (frac | (1u << 23)) : 0u;
+    const uint32_t sh = static_cast<uint32_t>(min(10 + e_eff - e, 31));
+    int mag = static_cast<int>((sig + ((1u << (sh - 1u)) - 1u) + ((sig >> sh) & 1u)) >> sh);
+    mag = (grp_inf & (e == 255) & (frac == 0)) ? 16384 : mag;
+    mag = grp_nan ? 0 : mag;
+    mant[i] = (b & kSign) ? -mag : mag;
   }
   uint32_t sb = emax == 0 ? 0u : static_cast<uint32_t>(e_eff - 13) << 23;
   sb = grp_inf ? kExpo : sb;
@@ -290,8 +299,6 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
       const int i = p * kThreads + tid;
       const bool valid = i < 8 * G;
       const int ii = valid ? i : (i & 7);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) xb[p][j] = (xb[p][j] & kExpo) ? xb[p][j] : (xb[p][j] & kSign);  // ftz
       int mant[16];
       uint32_t sb;
       align_elems<16, 8>(xb[p], mant, sb);

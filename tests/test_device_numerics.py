@@ -65,3 +65,56 @@ def test_rne_shift_by_add_equals_the_reference_rounding():
         fast = (sig + (half - 1) + ((sig >> sh) & 1)) >> sh
         assert (ref == fast).all(), sh
         assert fast.max() <= (1 << 14) or sh < 10  # mantissas stay within 16384 for sh >= 10
+
+
+def test_rne_shift_equals_a_power_of_two_product_rounded_to_even():
+    """The aligner's finite-group fast path computes a mantissa as rint(x * 2^(140 - e_eff)) in
+    fp32 (one exact power-of-two product, then round-half-even): for a 24-bit significand sig of
+    exponent e that is rint(sig * 2^-sh) with sh = 10 + e_eff - e, which equals the reference's
+    kept/dropped/half shift for every significand and every shift 10..40 (exhaustive)."""
+    sig = (np.arange(1 << 23, dtype=np.int64) | (1 << 23))
+    sigf = sig.astype(f32)                                   # exact: sig < 2^24
+    for sh in range(10, 41):
+        s = min(sh, 31)
+        kept = sig >> s
+        dropped = sig & ((1 << s) - 1)
+        half = 1 << (s - 1)
+        ref = np.where(sh >= 25, 0, kept + ((dropped > half) | ((dropped == half) & ((kept & 1) == 1))))
+        fast = np.rint(sigf * f32(2.0 ** -sh)).astype(np.int64)
+        assert (ref == fast).all(), sh
+
+
+def test_aligner_fast_path_matches_the_oracle_on_finite_groups():
+    """The same formula on real activation rows against the oracle's aligner (numerics.py:55-98):
+    groups mixing exponent spreads of 0..250, zeros, signed values, subnormal inputs (flushed),
+    products that fall into the subnormal range, exact ties, and the e_eff = 14 floor."""
+    rng = np.random.default_rng(3)
+    rows = []
+    for spread in (0, 3, 12, 24, 25, 40, 120, 250):
+        for _ in range(20):
+            e = rng.integers(max(1, 200 - spread), 201, 128) if spread < 200 else rng.integers(1, 255, 128)
+            b = (rng.integers(0, 2, 128) << 31) | (e.astype(np.int64) << 23) | rng.integers(0, 1 << 23, 128)
+            v = b.astype(np.uint32).view(f32).copy()
+            v[rng.integers(0, 128, 5)] = 0.0
+            v[rng.integers(0, 128, 3)] = np.uint32(rng.integers(1, 1 << 23)).view(f32)   # subnormal input
+            rows.append(v)
+    small = (rng.integers(0, 1 << 23, (40, 128)) | (rng.integers(1, 20, (40, 128)) << 23)).astype(np.uint32)
+    rows.extend(small.view(f32))                                                       # e_eff = 14 floor
+    ties = (np.float32(2.0) ** rng.integers(-20, 20, (20, 1))) * (rng.integers(0, 64, (20, 128)) + f32(0.5))
+    rows.extend(ties.astype(f32))
+    x = np.stack(rows)
+    q, scales = F.align_w4_groups(x)
+    for flushed in (True, False):
+        xf = (F.ftz(x) if flushed else x).reshape(x.shape[0], -1, 128)
+        e = (xf.view(np.uint32) >> 23) & 0xFF
+        emax = e.max(axis=2)
+        e_eff = np.maximum(emax, 14)
+        p = ((267 - e_eff).astype(np.uint32) << 23).view(f32)[:, :, None]              # 2^(140 - e_eff)
+        with np.errstate(under="ignore"):
+            fast = np.rint(xf * p).astype(np.int64)
+        want = q.astype(np.int64).reshape(fast.shape)
+        # flushed inputs: every finite group; unflushed inputs (the kernel's fast path): groups with
+        # emax >= 16, where a subnormal input times 2^(140 - e_eff) <= 2^124 stays below 1/4
+        sel = np.ones_like(emax, bool) if flushed else emax >= 16
+        assert sel.sum() > 100
+        assert (fast[sel] == want[sel]).all()

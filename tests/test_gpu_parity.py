@@ -387,6 +387,29 @@ def test_w4_shapes_bf16_bias_act(K, M):
     assert same(host(y2), G.gemm_w4(x, Wp, ws, out=OUT_INT8, out_scale=f32(0.25)))
 
 
+@pytest.mark.parametrize("K", [1024, 6144])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_w4_gemm_special_groups(K, bf16):
+    """The GEMV's in-kernel aligner on groups that leave its fast path: all-zero, tiny (largest
+    exponent below 16), subnormal inputs inside normal groups, +-inf, NaN, and the largest finite
+    values, in rows whose other groups are ordinary (so waves of both kinds meet in one launch)."""
+    rng = np.random.default_rng(K + bf16)
+    x, Wp, ws, _ = w4_inputs(K * 3 + bf16, 6, 64, K)
+    g = x.reshape(6, K // 128, 128)
+    g[0, 1] = 0.0                                                  # all-zero group
+    g[0, 2] = rng.normal(0, 1, 128) * np.float32(2.0 ** -115)      # emax < 16
+    g[1, 0, ::7] = np.array([1, 0x80000003, 0x007FFFFF], np.uint32).view(f32).repeat(7)[:19]  # subnormals
+    g[2, 3, 5], g[2, 3, 9] = np.inf, -np.inf                       # infinity group
+    g[3, K // 128 - 1, 17] = np.nan                                # NaN group
+    g[4, 1] = np.float32(3.3e38) * np.sign(rng.normal(0, 1, 128)).astype(f32)
+    g[5] = rng.normal(0, 1, (K // 128, 128)) * np.exp2(rng.integers(-126, 100, (K // 128, 1)))
+    x = g.reshape(6, K).astype(f32)
+    xin = F.to_bf16_bits(x) if bf16 else x
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_align_w4_groups(bf16):
     rng = np.random.default_rng(44)
