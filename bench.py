@@ -316,9 +316,16 @@ def time_graph(torch, g, reps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
-def rows_per_wave(rows: int) -> int:
-    """The library's rows-per-wave rule (gemv_w8a8.hip, rows_per_wave)."""
-    return 1 if rows < 16384 else 2 if rows < 32768 else 4 if rows < 65536 else 8
+def plain_rows_per_wave(rows: int) -> int:
+    """The plain GEMV's rows-per-wave rule (gemv_w8a8.hip, plain_rows_per_wave)."""
+    return 1 if rows < 2048 else 2 if rows < 32768 else 4
+
+
+def fused_rows_per_wave(rows: int, K: int) -> int:
+    """The fused quantize + GEMV rule (gemv_w8a8.hip, fused_rows_per_wave)."""
+    u = 4 if K <= 1024 else 2 if K <= 3072 else 1
+    wgs = -(-rows // (4 * u))
+    return 2 * u if 256 < wgs < 512 and u < 8 else u
 
 
 def kernel_instance(l: Launch) -> str:
@@ -327,21 +334,21 @@ def kernel_instance(l: Launch) -> str:
     if l.kind == "quant_gemm_w8a8":
         K = l.args[6]
         rows = sum(d.N for d in l.operands["descs"])
-        name = "quant_gemv_w8a8_kernel"
+        name, u, tail = "quant_gemv_w8a8_kernel", fused_rows_per_wave(rows, K), ""
     elif l.kind == "gemm_w8a8" and l.args[9] == 1:
-        K, rows, name = l.args[11], l.args[10], "gemv_w8a8_kernel"
+        K, rows = l.args[11], l.args[10]
+        name, u, tail = "gemv_w8a8_kernel", plain_rows_per_wave(rows), ", 1"
     else:
         return l.kind
     c = K // 16
     if c <= 32:
         lanes = 8 if c <= 8 else 16 if c <= 16 else 32
-        return f"{name}<{lanes}, 1, 8>"
+        return f"{name}<{lanes}, 1, 8{tail}>"
     cpl = -(-c // 64)
-    u = rows_per_wave(rows)
     if cpl > 8:
-        return f"{name}<64, 0, {1 if u == 1 else 4}>"
+        return f"{name}<64, 0, {1 if u == 1 else 4}{tail}>"
     u = min(u, {1: 8, 2: 4, 3: 2, 4: 2}.get(cpl, 1))
-    return f"{name}<64, {cpl}, {u}>"
+    return f"{name}<64, {cpl}, {u}{tail}>"
 
 
 def instance_times(torch, step_graph, launches, reps: int = 5) -> dict:

@@ -348,11 +348,34 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 // Rows per wave: one row keeps small matrices spread over every CU (their time is latency, not
 // bandwidth); more rows per wave amortize the per-wave work once the grid is far larger than the
 // chip (the vocabulary-sized head).
-int rows_per_wave(int64_t rows) {
+// Rows per wave (U) of the plain GEMV: 1 below 2048 rows (the grid must reach every CU), 2 below
+// 32768, 4 above (measured on MI355X, K = 1024: N = 4096 3.16 us at U = 2 vs 3.49 at U = 1; the
+// 151936-row head 26.1 us at U = 4 vs 26.6 at U = 8).
+int plain_rows_per_wave(int64_t rows) {
+  if (rows < 2048) return 1;
+  if (rows < 32768) return 2;
+  return 4;
+}
+
+// Rows per wave of the fused quantize + GEMV: every workgroup re-reads and re-quantizes the fp32
+// activation row, so it takes about 16 KB of weights (4 rows of K bytes per wave step): U = 4 for
+// K <= 1024, 2 up to 3072, else 1; doubled when the grid would fill one wave of workgroups and a
+// part of a second (256 < workgroups < 512). Measured on MI355X (K = 1024 unless noted): q/k/v
+// 4096 rows 3.26 us at U = 4 vs 4.34 at U = 1; gate/up 6144 rows 3.87 us at U = 8 vs 4.31 at U = 4
+// and 5.06 at U = 1; o (K = 2048) and down (K = 3072) 1024 rows 3.56 / 3.59 us at U = 2 vs 3.76 /
+// 3.74 at U = 1; the head 26.3 us at U = 4 vs 27.4 at U = 8.
+int fused_rows_per_wave(int64_t rows, int K) {
+  int u = K <= 1024 ? 4 : K <= 3072 ? 2 : 1;
+  const int64_t wgs = (rows + 4 * u - 1) / (4 * u);
+  if (wgs > 256 && wgs < 512 && u < 8) u *= 2;
+  return u;
+}
+
+// Rows per wave of the K-split GEMV.
+int ksplit_rows_per_wave(int64_t rows) {
   if (rows < 16384) return 1;
   if (rows < 32768) return 2;
-  if (rows < 65536) return 4;
-  return 8;
+  return 4;
 }
 
 template <int L, int CPL, int U>
@@ -387,11 +410,11 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Kernel instance for (K, rows): lanes per row L, 16-byte chunks per lane CPL, rows per wave U.
+// Kernel instance for (K, u): lanes per row L, 16-byte chunks per lane CPL, rows per wave U (u,
+// capped by the instances that exist for the chunk count).
 template <class Args, template <int, int, int> class Go>
-hipError_t dispatch(Args& a, int K, int64_t rows, hipStream_t s) {
+hipError_t dispatch(Args& a, int K, int u, hipStream_t s) {
   const int C = K / 16;
-  const int u = rows_per_wave(rows);
   if (C <= 8) return Go<8, 1, 8>::run(a, s);
   if (C <= 16) return Go<16, 1, 8>::run(a, s);
   if (C <= 32) return Go<32, 1, 8>::run(a, s);
@@ -423,17 +446,17 @@ struct GoFused {
 }  // namespace
 
 hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s) {
-  return dispatch<const W8A8Args, GoPlain>(a, a.K, a.N, s);
+  return dispatch<const W8A8Args, GoPlain>(a, a.K, plain_rows_per_wave(a.N), s);
 }
 
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
   int64_t rows = 0;
   for (int i = 0; i < a.ngroups; ++i) rows += a.g[i].N;
-  return dispatch<QuantGemvArgs, GoFused>(a, a.K, rows, s);
+  return dispatch<QuantGemvArgs, GoFused>(a, a.K, fused_rows_per_wave(rows, a.K), s);
 }
 
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s) {
-  const int u = rows_per_wave(a.N);
+  const int u = ksplit_rows_per_wave(a.N);
   const int rows_per_block = kWaves * u;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block, a.M);
   if (u == 1) {
