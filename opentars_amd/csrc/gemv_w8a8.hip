@@ -186,6 +186,97 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_kernel(KSplitArgs a
   }
 }
 
+// K split with every load in flight at once (total K <= 64 * 16 * CPL): the blocks' columns are
+// consecutive, so chunk c of the concatenated row is activation bytes 16c.. and lies in the block b
+// whose chunk range holds it; lane `lane` owns chunks lane, lane + 64, ... of U rows. All activation
+// chunks are issued, then all weight chunks, then the dot products are summed per block (exact
+// int32, each block's sum on its own), reduced across the wave, and the blocks' fp32 partials are
+// added in block order as in gemv_w8a8_ksplit_kernel.
+template <int CPL, int U>
+__global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSplitArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int m = blockIdx.y;
+  const int n0 = (blockIdx.x * kWaves + wave) * U;
+  const v4i zero = {0, 0, 0, 0};
+  int cstart[kMaxBlocks + 1];
+  cstart[0] = 0;
+#pragma unroll
+  for (int b = 0; b < kMaxBlocks; ++b) cstart[b + 1] = cstart[b] + (b < a.nblocks ? a.K[b] >> 4 : 0);
+  const int ctot = cstart[kMaxBlocks];
+  const v4i* xrow = reinterpret_cast<const v4i*>(a.A + m * a.lda);
+  // block of each of this lane's chunks (blocks are few and ascending: a compare chain)
+  int blk[CPL], cin[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = min(lane + 64 * j, ctot - 1);
+    int b = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBlocks; ++i) b += (i < a.nblocks && c >= cstart[i]) ? 1 : 0;
+    blk[j] = b;
+    cin[j] = c;
+  }
+  v4i xv[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) xv[j] = load_pred(xrow + cin[j], xrow, lane + 64 * j < ctot, zero);
+  issue_fence();
+  v4i wv[U][CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int b = blk[j];
+    const int8_t* Wb = a.W[0];
+    int Kb = a.K[0], cb = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBlocks; ++i)
+      if (b == i) {
+        Wb = a.W[i];
+        Kb = a.K[i];
+        cb = cstart[i];
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int n = n0 + u;
+      wv[u][j] = load_stream_pred(reinterpret_cast<const v4i*>(Wb + static_cast<int64_t>(n) * Kb) + (cin[j] - cb),
+                                  reinterpret_cast<const v4i*>(a.W[0]), n < a.N && lane + 64 * j < ctot, zero);
+    }
+  }
+  issue_fence();
+  const float sr = *(a.srow ? a.srow + m : a.scol);  // unconditional (see fp32_contract.h)
+  float sc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) sc[u] = a.scol[min(n0 + u, a.N - 1)];
+  issue_fence();
+  int d[U][CPL];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) d[u][j] = dot16(wv[u][j], xv[j], 0);
+  float y[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) y[u] = 0.0f;
+  for (int b = 0; b < a.nblocks; ++b) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int acc = 0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) acc += blk[j] == b ? d[u][j] : 0;
+      const int s = group_sum<64>(acc);
+      float part = i2f(s);
+      if (a.srow) part = fmul(part, sr);
+      part = fmul(part, sc[u]);
+      y[u] = b == 0 ? part : fadd(y[u], part);
+    }
+  }
+  float mine = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (lane == u) mine = y[u];
+  const int n = n0 + lane;
+  if (lane < U && n < a.N) {
+    reinterpret_cast<float*>(reinterpret_cast<char*>(a.Y) + m * a.ldy)[n] = ftz(mine);
+  }
+}
+
 // ---- fused per-token quantizer + grouped GEMV ----
 // Each workgroup quantizes the activation row once: its 256 threads read the fp32 row in float4s
 // (a single pass over 4K bytes, mostly L2 hits after the first workgroup), the row maximum meets
@@ -371,7 +462,7 @@ int fused_rows_per_wave(int64_t rows, int K) {
   return u;
 }
 
-// Rows per wave of the K-split GEMV.
+// Rows per wave of the K-split loop kernel (total K > 8192).
 int ksplit_rows_per_wave(int64_t rows) {
   if (rows < 16384) return 1;
   if (rows < 32768) return 2;
@@ -455,7 +546,29 @@ hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
   return dispatch<QuantGemvArgs, GoFused>(a, a.K, fused_rows_per_wave(rows, a.K), s);
 }
 
+// One weight row per wave: measured on MI355X at C2 (K = 6912 in 2 or 3 blocks, N = 1152), 5.8-6.0 us
+// against 6.1-7.3 us for the loop kernel; 2 rows per wave or 5-8 waves per workgroup were slower.
+template <int CPL>
+hipError_t go_ksplit_flight(const KSplitArgs& a, hipStream_t s) {
+  const dim3 grid((a.N + kWaves - 1) / kWaves, a.M);
+  hipLaunchKernelGGL((gemv_w8a8_ksplit_flight_kernel<CPL, 1>), grid, dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s) {
+  int ctot = 0;
+  for (int i = 0; i < a.nblocks; ++i) ctot += a.K[i] >> 4;
+  switch ((ctot + 63) / 64) {  // total K <= 8192: every load in flight at once
+    case 1: return go_ksplit_flight<1>(a, s);
+    case 2: return go_ksplit_flight<2>(a, s);
+    case 3: return go_ksplit_flight<3>(a, s);
+    case 4: return go_ksplit_flight<4>(a, s);
+    case 5: return go_ksplit_flight<5>(a, s);
+    case 6: return go_ksplit_flight<6>(a, s);
+    case 7: return go_ksplit_flight<7>(a, s);
+    case 8: return go_ksplit_flight<8>(a, s);
+    default: break;
+  }
   const int u = ksplit_rows_per_wave(a.N);
   const int rows_per_block = kWaves * u;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block, a.M);

@@ -249,6 +249,27 @@ def test_ksplit_both_paths_agree():
     assert same(outs[0], want) and same(outs[1], want)
 
 
+@pytest.mark.parametrize("split", [[16], [16, 32], [48, 1040, 16], [4096, 4096], [4096, 4112], [1024] * 8,
+                                   [2816, 3456, 16], [7168, 1024]])
+@pytest.mark.parametrize("M", [1, 3])
+def test_ksplit_gemv_block_shapes(split, M):
+    """The K-split GEMV family: one to eight blocks, widths that are not multiples of 64, a total of
+    exactly 8192 (all loads in flight) and just above it (the loop kernel), 1 and 3 rows."""
+    K = sum(split)
+    x, q, s, W, scol, _ = w8_inputs(K * 3 + M, M, 80, K)
+    blocks, c0 = [], 0
+    for k in split:
+        blocks.append(np.ascontiguousarray(W[:, c0:c0 + k]))
+        c0 += k
+    prev = ops.set_w8a8_path("gemv")
+    try:
+        y = ops.gemm_rowcol_ksplit(cuda(q), cuda(s), [cuda(b) for b in blocks], cuda(scol))
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("M", [17, 45])
 def test_ksplit_prompt_tiles(M):
     """The K split on the prompt-row MFMA tiles (M > 16), with a ragged last row and column tile."""
