@@ -183,8 +183,9 @@ def queue_decode_step(torch, lib, seed: int, steps: int, warmup: int) -> dict:
     ROW_QUANT + q/k/v GEMMs, ROW_QUANT + o, ROW_QUANT + gate/up, ROW_QUANT + down, then ROW_QUANT +
     the head as 4 blocks of 37984 rows (qwen_ref.py:371-378); 313 descriptors, QM_ROWCOL, fp32 out.
     Timed end to end per step on the host clock (descriptor checks, launches and GPU work, the host
-    holding its copy of the queue), with the executor's quantizer+GEMM fusion on (113 launches) and
-    off (313 launches)."""
+    holding its copy of the queue): with the executor's quantizer+GEMM fusion (113 launches) and its
+    launch plans (a repeated queue replays as one HIP graph), with fusion but every run checked and
+    launched, and with neither (313 launches)."""
     from opentars_amd import _lib, contract as C
     from opentars_amd.queue import encode_descriptor
     gen = torch.Generator(device="cuda")
@@ -263,10 +264,12 @@ def queue_decode_step(torch, lib, seed: int, steps: int, warmup: int) -> dict:
                                f"{_lib.last_error()}")
 
     res = {"descriptors": len(raw), "image_bytes": int(image.numel()), "algorithmic_bytes_per_step": nbytes}
-    for fusion in (1, 0):
-        prev = lib.tars_set_queue_fusion(fusion)
+    # fused + launch plans (the default: from the third run on, one graph launch per step); fused
+    # with every run checked and launched; the golden's one launch per descriptor
+    for key, fusion, graphs in (("fused_plans", 1, 1), ("fused", 1, 0), ("unfused", 0, 0)):
+        prev_f, prev_g = lib.tars_set_queue_fusion(fusion), lib.tars_set_queue_graphs(graphs)
         try:
-            for _ in range(warmup):
+            for _ in range(max(warmup, 3)):
                 run()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -275,8 +278,8 @@ def queue_decode_step(torch, lib, seed: int, steps: int, warmup: int) -> dict:
             torch.cuda.synchronize()
             t = (time.perf_counter() - t0) / steps
         finally:
-            lib.tars_set_queue_fusion(prev)
-        key = "fused" if fusion else "unfused"
+            lib.tars_set_queue_fusion(prev_f)
+            lib.tars_set_queue_graphs(prev_g)
         res[key] = {"launches_per_step": 113 if fusion else len(raw), "ms_per_step": round(t * 1e3, 4),
                     "GBps": round(nbytes / t / 1e9, 1)}
     del image

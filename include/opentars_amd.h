@@ -230,6 +230,13 @@ int tars_encode_descriptor(const uint64_t* fields, int32_t fix_crc, uint8_t* des
  * Returns the previous setting. Process-wide. */
 int tars_set_queue_fusion(int on);
 
+/* Launch plans in tars_run_queue (benchmark and test control): 1 (default) keeps, for up to 8
+ * queues, the launches of a queue that ran to the end without a hand-off or an output over its own
+ * descriptors; when the same descriptor bytes run again on the same image with the same settings,
+ * they are captured once into a HIP graph and every later run is one graph launch. 0 disables
+ * and drops the plans. Results are identical either way. Returns the previous setting. */
+int tars_set_queue_graphs(int on);
+
 #ifdef __cplusplus
 }
 #endif

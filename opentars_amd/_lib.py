@@ -53,6 +53,7 @@ SIGNATURES = {
     "tars_descriptor_crc": (c_uint32, [c_char_p]),
     "tars_encode_descriptor": (c_int, [POINTER(c_uint64), c_int32, c_void_p]),
     "tars_set_queue_fusion": (c_int, [c_int]),
+    "tars_set_queue_graphs": (c_int, [c_int]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -102,6 +102,8 @@ float f32_of(uint32_t b) {
 namespace tars {
 // The calling thread's last-error text, shared by every entry point of the library.
 void set_last_error(const std::string& what) { g_last_error = what; }
+// The W8A8 kernel-family switch (tars_set_w8a8_path).
+int w8a8_path() { return g_w8a8_path; }
 }  // namespace tars
 
 extern "C" {

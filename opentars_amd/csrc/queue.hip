@@ -17,6 +17,7 @@
 // fusion, bit-identical to the one-by-one order; see fuse_group).
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -444,6 +445,7 @@ int launch(uint8_t* image, const Desc& d, hipStream_t stream, bool& needs_host) 
 
 namespace tars {
 void set_last_error(const std::string& what);
+int w8a8_path();
 }  // namespace tars
 
 namespace {
@@ -459,10 +461,35 @@ u128 addr(const Desc& d, Field off) { return static_cast<u128>(d[F_BASE_ADDR]) +
 // scale the kernel computes). No fusion when an output of the group lands on a later descriptor
 // of the queue; when the group's outputs overlap each other or any input of the group, the fused
 // call refuses before launching and the descriptors run one by one. `fused` = GEMMs folded in.
+// One ROW_QUANT (M = 1) and the GEMMs reading its output, as one tars_quant_gemm_w8a8 call.
+int launch_fused(uint8_t* image, const Desc& dq, const std::vector<Desc>& members, hipStream_t s) {
+  tars_w8a8_out outs[4];
+  for (size_t k = 0; k < members.size(); ++k) {
+    const Desc& d = members[k];
+    uint8_t* B = image + d[F_BASE_ADDR];
+    outs[k].W = reinterpret_cast<const int8_t*>(B + d[F_W_OFF]);
+    outs[k].scol = reinterpret_cast<const float*>(B + d[F_SCALE_OFF]);
+    outs[k].bias = has_bias(d[F_EPI]) ? reinterpret_cast<const float*>(B + d[F_BIAS_OFF]) : nullptr;
+    outs[k].Y = B + d[F_Y_OFF];
+    outs[k].ldy = static_cast<int64_t>(strides(d).ldy);
+    outs[k].N = static_cast<int32_t>(d[F_N]);
+    outs[k].act = static_cast<int32_t>(act_code(d[F_EPI]));
+    outs[k].out = static_cast<int32_t>(out_code(d[F_EPI]));
+    outs[k].out_scale_bits = static_cast<uint32_t>(d[F_OUT_SCALE]);
+  }
+  uint8_t* B = image + dq[F_BASE_ADDR];
+  const Strides sq = strides(dq);
+  return tars_quant_gemm_w8a8(reinterpret_cast<const float*>(B + dq[F_A_OFF]), static_cast<int64_t>(sq.lda),
+                              reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
+                              reinterpret_cast<float*>(B + dq[F_SCALE_OFF]), 1, static_cast<int32_t>(dq[F_N]), outs,
+                              static_cast<int32_t>(members.size()), s);
+}
+
 int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
                int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
-               int& fused) {
+               int& fused, std::vector<Desc>& group) {
   fused = 0;
+  group.clear();
   const Desc& dq = quant.d;
   if (!g_fusion || dq[F_OPCODE] != OP_ROW || dq[F_M] != 1 || (reinterpret_cast<uintptr_t>(image) + dq[F_BASE_ADDR]) % 16)
     return TARS_OK;
@@ -484,33 +511,78 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
     for (const Checked& c : members)
       if (overlaps(rest, c.y)) return TARS_OK;
   }
-  tars_w8a8_out outs[4];
-  for (size_t k = 0; k < members.size(); ++k) {
-    const Desc& d = members[k].d;
-    uint8_t* B = image + d[F_BASE_ADDR];
-    outs[k].W = reinterpret_cast<const int8_t*>(B + d[F_W_OFF]);
-    outs[k].scol = reinterpret_cast<const float*>(B + d[F_SCALE_OFF]);
-    outs[k].bias = has_bias(d[F_EPI]) ? reinterpret_cast<const float*>(B + d[F_BIAS_OFF]) : nullptr;
-    outs[k].Y = B + d[F_Y_OFF];
-    outs[k].ldy = static_cast<int64_t>(strides(d).ldy);
-    outs[k].N = static_cast<int32_t>(d[F_N]);
-    outs[k].act = static_cast<int32_t>(act_code(d[F_EPI]));
-    outs[k].out = static_cast<int32_t>(out_code(d[F_EPI]));
-    outs[k].out_scale_bits = static_cast<uint32_t>(d[F_OUT_SCALE]);
-  }
-  uint8_t* B = image + dq[F_BASE_ADDR];
-  const Strides sq = strides(dq);
-  const int rc = tars_quant_gemm_w8a8(reinterpret_cast<const float*>(B + dq[F_A_OFF]), static_cast<int64_t>(sq.lda),
-                                      reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
-                                      reinterpret_cast<float*>(B + dq[F_SCALE_OFF]), 1, static_cast<int32_t>(dq[F_N]),
-                                      outs, static_cast<int32_t>(members.size()), s);
+  for (const Checked& c : members) group.push_back(c.d);
+  const int rc = launch_fused(image, dq, group, s);
   if (rc == TARS_E_OVERLAP) {
     tars::set_last_error("");
+    group.clear();
     return TARS_OK;
   }
   if (rc == TARS_OK) fused = static_cast<int>(members.size());
   return rc;
 }
+
+// ---------------------------------------------------------------------------- launch plans
+// A decode loop runs the same descriptor bytes every token. A queue that ran to the end with no
+// hand-off and no output over its own descriptors leaves a plan (its launches in order, with the
+// decisions the checks made); when the same bytes run again on the same image with the same
+// settings, the plan is captured once into a HIP graph (on a private stream; the plan records no
+// memset) and every later run is one graph launch. The checks that produced the plan depend only
+// on the descriptor bytes, the image address and length, core_id, the profile and the library's
+// switches, which are the cache key.
+struct Step {
+  Desc d;                   // the descriptor (the quantizer of a fused group)
+  std::vector<Desc> group;  // the GEMMs fused with it (empty: a single launch)
+};
+
+struct Plan {
+  uint8_t* image;
+  uint64_t image_len, queue_addr;
+  int32_t n;
+  int core_id, gemv_only, w8a8_path;
+  bool fusion;
+  std::vector<uint8_t> bytes;
+  std::vector<Step> steps;
+  hipGraphExec_t exec = nullptr;
+  uint64_t last_use = 0;
+};
+
+constexpr size_t kMaxPlans = 8;
+std::mutex g_plans_mu;
+std::vector<Plan> g_plans;
+uint64_t g_plan_clock = 0;
+bool g_graphs = true;
+
+int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) {
+  for (const Step& st : steps) {
+    bool needs_host = false;
+    const int rc = st.group.empty() ? launch(image, st.d, s, needs_host) : launch_fused(image, st.d, st.group, s);
+    if (rc != TARS_OK) return rc;
+  }
+  return TARS_OK;
+}
+
+// The graph of a plan's launches (captured on a private default-priority stream).
+int capture(Plan& p) {
+  hipStream_t cs = nullptr;
+  if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return TARS_E_DEVICE;
+  hipGraph_t g = nullptr;
+  int rc = TARS_OK;
+  if (hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    rc = TARS_E_DEVICE;
+  } else {
+    rc = replay_steps(p.image, p.steps, cs);
+    if (hipStreamEndCapture(cs, &g) != hipSuccess && rc == TARS_OK) rc = TARS_E_DEVICE;
+  }
+  if (rc == TARS_OK && hipGraphInstantiate(&p.exec, g, nullptr, nullptr, 0) != hipSuccess) {
+    p.exec = nullptr;
+    rc = TARS_E_DEVICE;
+  }
+  if (g) (void)hipGraphDestroy(g);
+  (void)hipStreamDestroy(cs);
+  return rc;
+}
+
 
 }  // namespace
 
@@ -594,6 +666,30 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
   } else if (int rc = reread(0)) {
     return rc;
   }
+  const int path = tars::w8a8_path();
+  auto same_key = [&](const Plan& p) {
+    return p.image == image && p.image_len == image_len && p.queue_addr == queue_addr && p.n == n &&
+           p.core_id == core_id && p.gemv_only == gemv_only && p.w8a8_path == path && p.fusion == g_fusion &&
+           p.bytes.size() == q.size() && std::memcmp(p.bytes.data(), q.data(), q.size()) == 0;
+  };
+  if (g_graphs) {
+    std::lock_guard<std::mutex> lock(g_plans_mu);
+    for (size_t k = 0; k < g_plans.size(); ++k) {
+      Plan& p = g_plans[k];
+      if (!same_key(p)) continue;
+      if (!p.exec && capture(p) != TARS_OK) {  // no graph for this plan: forget it, run the queue as usual
+        g_plans.erase(g_plans.begin() + static_cast<std::ptrdiff_t>(k));
+        break;
+      }
+      if (hipGraphLaunch(p.exec, s) != hipSuccess) return queue_fail(TARS_E_DEVICE, "graph launch failed");
+      p.last_use = ++g_plan_clock;
+      st->done = 1;
+      st->op_idx = n;
+      return TARS_OK;
+    }
+  }
+  std::vector<Step> steps;
+  bool cacheable = g_graphs && in_image == static_cast<uint64_t>(n);
   for (int32_t i = 0; i < n; ++i) {
     st->op_idx = i;
     if (static_cast<uint64_t>(i) >= in_image) {  // the descriptor itself lies past the image
@@ -613,9 +709,12 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     }
     const u128 later = static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(i) + 1);
     int fused = 0;
-    if (int rc = fuse_group(image, c, q, i, in_image, n, later, q_end, image_len, core_id, gemv_only != 0, s, fused))
+    std::vector<Desc> group;
+    if (int rc = fuse_group(image, c, q, i, in_image, n, later, q_end, image_len, core_id, gemv_only != 0, s, fused,
+                            group))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
+      if (cacheable) steps.push_back(Step{c.d, std::move(group)});
       i += fused;  // the quantizer and `fused` GEMMs ran as one launch
       continue;
     }
@@ -627,15 +726,51 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       st->host_op = 1;
       return TARS_OK;
     }
+    if (cacheable) steps.push_back(Step{c.d, {}});
     // an output written over a later descriptor of this queue: wait for it and read them again
     const Segs rest = {{later, q_end}};
     if (later < q_end && (overlaps(rest, c.y) || (!c.extra.empty() && overlaps(rest, c.extra)))) {
+      cacheable = false;
       if (int rc = reread(static_cast<uint64_t>(i) + 1)) return rc;
     }
   }
   st->done = 1;
   st->op_idx = n;
+  if (cacheable) {
+    std::lock_guard<std::mutex> lock(g_plans_mu);
+    if (g_plans.size() >= kMaxPlans) {
+      auto lru = std::min_element(g_plans.begin(), g_plans.end(),
+                                  [](const Plan& a, const Plan& b) { return a.last_use < b.last_use; });
+      if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
+      g_plans.erase(lru);
+    }
+    Plan p;
+    p.image = image;
+    p.image_len = image_len;
+    p.queue_addr = queue_addr;
+    p.n = n;
+    p.core_id = core_id;
+    p.gemv_only = gemv_only;
+    p.w8a8_path = path;
+    p.fusion = g_fusion;
+    p.bytes = std::move(q);
+    p.steps = std::move(steps);
+    p.last_use = ++g_plan_clock;
+    g_plans.push_back(std::move(p));
+  }
   return TARS_OK;
+}
+
+int tars_set_queue_graphs(int on) {
+  std::lock_guard<std::mutex> lock(g_plans_mu);
+  const int prev = g_graphs ? 1 : 0;
+  g_graphs = on != 0;
+  if (!g_graphs) {
+    for (Plan& p : g_plans)
+      if (p.exec) (void)hipGraphExecDestroy(p.exec);
+    g_plans.clear();
+  }
+  return prev;
 }
 
 }  // extern "C"

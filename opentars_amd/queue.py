@@ -189,5 +189,11 @@ def set_fusion(on: bool) -> bool:
     return bool(_lib.lib().tars_set_queue_fusion(int(on)))
 
 
+def set_graphs(on: bool) -> bool:
+    """Launch plans replayed as HIP graphs for repeated queues in run_queue (default on); returns
+    the previous setting. Turning it off drops the kept plans."""
+    return bool(_lib.lib().tars_set_queue_graphs(int(on)))
+
+
 __all__ = ["Machine", "Status", "run", "check_descriptor", "decode_descriptor", "descriptor_crc",
-           "encode_descriptor", "set_fusion", "FIELDS", "ERR_NAMES"]
+           "encode_descriptor", "set_fusion", "set_graphs", "FIELDS", "ERR_NAMES"]

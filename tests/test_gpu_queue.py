@@ -202,6 +202,31 @@ def test_host_copy_of_the_queue_gives_the_same_result(seed):
     assert bytes(g.ddr) == bytes(o.ddr)
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_repeated_queue_replays_its_plan_on_new_data(seed):
+    """A decode loop's pattern: the same descriptors run again and again while the image's data
+    changes. Run 1 checks and launches (and keeps a plan), run 2 captures the plan as a HIP graph,
+    later runs launch the graph; every run equals the oracle's run on that run's image."""
+    p = random_program(300 + seed)
+    descs = b"".join(p.descs)
+    img = p.image()
+    g = NQ.Machine(img)
+    rng = np.random.default_rng(seed)
+    for rnd in range(4):
+        if rnd:
+            fresh = bytearray(img)
+            fresh[0x1000:p.top] = rng.integers(0, 256, p.top - 0x1000, dtype=np.uint8).tobytes()
+            img = fresh
+            g.write(0, bytes(img[:QADDR]))
+        st = g.run_queue(QADDR, len(p.descs), descs=descs)
+        o = Q.Machine(img)
+        ost = o.run_queue(QADDR, len(p.descs))
+        assert ost.done and st.done, (rnd, ost, st)
+        gd = bytes(g.ddr)
+        assert gd == bytes(o.ddr), f"run {rnd}: first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+        img = bytearray(gd)
+
+
 def test_fusion_group_with_a_hazard_runs_one_by_one():
     """A decode row read by three GEMMs where the second GEMM writes over the third's weights: the
     fused launch would race, so the group runs descriptor by descriptor (the third GEMM then reads
