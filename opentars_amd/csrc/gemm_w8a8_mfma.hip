@@ -6,18 +6,22 @@
 // and B use the same map: each dot product is then the exact sum over the instruction's 64 k.
 // Integer accumulation is exact, so K may be split across waves and summed in any order.
 //
-// One kernel family (mfma_direct_kernel<TM, TN, KW, D>): a workgroup owns a 16 TM x 16 TN output
-// tile and KW waves that split its K range; every wave loads its share of all 16 (TM + TN) rows
-// straight into MFMA operand registers (no LDS staging: at these sizes the operands have no reuse
-// inside a workgroup once K is split across its waves), and the int32 partial tiles meet in LDS
-// for the golden fp32 epilogue (or, for a K split, the per-block epilogue and the in-order fp32
-// adds across blocks). Measured on MI355X against the earlier LDS-staged 64 x 64 tiles with one
-// K tile in flight: M=256 K=1024 N=3072 19.2 -> 10.2 us, M=256 K=3072 N=1024 40.0 -> 10.6 us,
-// M=4 K=3072 N=1024 6.6 -> 5.9 us, bit-identical outputs.
+// Two kernel families:
+//  * mfma_direct_kernel<TM, TN, KW, D>: a workgroup owns a 16 TM x 16 TN output tile and KW waves
+//    that split its K range; every wave loads its share of all 16 (TM + TN) rows straight into
+//    MFMA operand registers, and the int32 partial tiles meet in LDS for the golden fp32 epilogue
+//    (or, for a K split, the per-block epilogue and the in-order fp32 adds across blocks). Used for
+//    chunk rows (M <= 16) and for K blocks that are not a whole number of stages.
+//  * mfma_staged_kernel<BM, BN, WM, WN, KS, S>: prompt rows. The tile's A and W rows are staged
+//    in LDS by direct global -> LDS loads in a ring of S stages of KS bytes of K, every wave of
+//    the workgroup reading the shared operands from LDS (64 x 64 tiles cut the L2 -> CU operand
+//    traffic to half that of 32 x 32 tiles); each wave owns whole 16 x 16 output tiles over the
+//    full K, so there is no cross-wave reduction.
 //
 // Roofline: at M = 4 HBM (every weight byte read once); at M = 256 the int32 MFMA work is small
-// (1.6 GOP) and the kernel is bound by operand traffic from L2 (the 32 x 32 tiles re-read A and W
-// 8 and 96 times), with INT8 MFMA utilisation reported beside it.
+// (1.6 GOP) and the kernels are bound by operand traffic from L2 into the CUs and by the fixed
+// cost of launch, first loads and the fp32 output stores, with INT8 MFMA utilisation reported
+// beside it.
 #include "kernels.h"
 
 namespace tars {
@@ -232,14 +236,183 @@ hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------ staged
+// Prompt-row tiles with the operands staged in LDS by direct global -> LDS loads
+// (global_load_lds_dwordx4: 64 lanes x 16 bytes land in a 1 KiB LDS block in lane order, with no
+// VGPR round trip, so a wave keeps several stages of loads in flight at no register cost).
+//
+// LDS layout of one stage (KS bytes of K): 1 KiB blocks (g, kb), g over the 16-row groups of the
+// tile's BM A rows then its BN W rows, kb over the stage's 64-byte k blocks. Lane l's 16 bytes in
+// a block are row 16 g + l % 16, bytes 64 kb + 16 (l / 16) .. + 15, at offset 16 l: exactly the
+// MFMA operand a lane supplies, so the MFMA reads are one contiguous ds_read_b128 per wave and
+// A and W share the byte -> (instruction, lane) map.
+//
+// S stage slots form a ring: stage st + S - 1 is issued into the slot of stage st - 1 (free since
+// the barrier that ended st - 1), then each wave waits until only its later stages' loads are
+// outstanding (vmcnt counts this wave's own loads), a barrier makes every wave's loads of stage st
+// visible, and the waves run its MFMAs. WM x WN waves each own TI x TJ 16 x 16 output tiles over
+// the full K, so the int32 sums need no reduction; the epilogue runs in MFMA layout (D transposed:
+// W is the MFMA's first operand, so lane l holds 4 consecutive columns of row l % 16) with a 4-wide
+// store. K blocks (a K split) run one after another through the same pipeline, their fp32
+// partials added in block order.
+#define TARS_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// One 1 KiB block: lane l's 16 bytes at src land at dst + 16 l (dst is wave-uniform).
+__device__ __forceinline__ void stage16(const void* src, int8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, TARS_LDS(dst), 16, 0, 0);
+}
+
+// Stage st of this wave's L blocks into its ring slot (st % S).
+template <int L, int NW, int KS, int S>
+__device__ __forceinline__ void issue_stage(int8_t* lds, const int8_t* const (&src)[L], int wave, int st) {
+  int8_t* slot = lds + 1024 * NW * L * (st % S);
+#pragma unroll
+  for (int u = 0; u < L; ++u) stage16(src[u] + static_cast<int64_t>(KS) * st, slot + 1024 * (wave + u * NW));
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int WM, int WN, int KS, int S>
+__global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
+  constexpr int NW = WM * WN, TI = BM / 16 / WM, TJ = BN / 16 / WN, GA = BM / 16, G = (BM + BN) / 16;
+  constexpr int KBS = KS / 64, BLK = G * KBS, L = BLK / NW, SLOT = 1024 * BLK;
+  static_assert(TI >= 1 && TJ >= 1 && BLK % NW == 0 && L * (S - 1) < 64, "stage shape");
+  extern __shared__ __align__(16) int8_t lds[];  // [S][BLK] 1 KiB blocks
+  const v4i zero = {0, 0, 0, 0};
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane & 15, lg = lane >> 4;
+  const int mt = gridDim.y, G8 = gridDim.x * gridDim.y;
+  const int b = blockIdx.y * gridDim.x + blockIdx.x;
+  const int t = (G8 % 8 == 0) ? (b % 8) * (G8 / 8) + b / 8 : b;  // XCD-contiguous tiles, as above
+  const int m0 = (t % mt) * BM, n0 = (t / mt) * BN;
+
+  // Epilogue operands of this lane's outputs: rows (wm TI + i) 16 + li, columns
+  // (wn TJ + j) 16 + 4 lg + v.
+  float sr[TI], sc[TJ][4], bi[TJ][4], chain[TI][TJ][4];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int n = min(n0 + (wn * TJ + j) * 16 + 4 * lg + v, a.N - 1);
+      sc[j][v] = a.epi.load_scol(n);
+      bi[j][v] = a.epi.load_bias(n);
+    }
+#pragma unroll
+  for (int i = 0; i < TI; ++i) sr[i] = a.epi.load_srow(min(m0 + (wm * TI + i) * 16 + li, a.M - 1));
+
+  for (int sgi = 0; sgi < a.nseg; ++sgi) {
+    const Seg sg = a.seg[sgi];
+    const int NS = sg.K / KS;
+    // This lane's source of each block it loads. A row past the matrix is clamped to the last
+    // row: it feeds only outputs that are not stored.
+    const int8_t* src[L];
+#pragma unroll
+    for (int u = 0; u < L; ++u) {
+      const int blk = wave + u * NW, g = blk / KBS, kb = blk % KBS;
+      if (g < GA) {
+        const int r = min(m0 + 16 * g + li, a.M - 1);
+        src[u] = a.A + static_cast<int64_t>(r) * a.lda + sg.koff + 64 * kb + 16 * lg;
+      } else {
+        const int r = min(n0 + 16 * (g - GA) + li, a.N - 1);
+        src[u] = sg.W + static_cast<int64_t>(r) * sg.K + 64 * kb + 16 * lg;
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st)
+      if (st < NS) issue_stage<L, NW, KS, S>(lds, src, wave, st);
+    v4i acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j] = zero;
+    for (int st = 0; st < NS; ++st) {
+      if (st + S - 1 < NS) {
+        issue_stage<L, NW, KS, S>(lds, src, wave, st + S - 1);
+        wait_vmcnt<L * (S - 1)>();
+      } else {
+        const int ahead = NS - 1 - st;  // stages issued after st (fewer than S - 1)
+        if constexpr (S >= 4) {
+          if (ahead == 2) wait_vmcnt<2 * L>();
+        }
+        if constexpr (S >= 3) {
+          if (ahead == 1) wait_vmcnt<L>();
+        }
+        static_assert(S <= 4, "waits above cover at most 2 stages ahead");
+        if (ahead == 0) wait_vmcnt<0>();
+      }
+      __builtin_amdgcn_s_barrier();
+      const int8_t* slot = lds + SLOT * (st % S) + 16 * lane;
+#pragma unroll
+      for (int kb = 0; kb < KBS; ++kb) {
+        v4i fa[TI], fw[TJ];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) fa[i] = *reinterpret_cast<const v4i*>(slot + 1024 * (KBS * (wm * TI + i) + kb));
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          fw[j] = *reinterpret_cast<const v4i*>(slot + 1024 * (KBS * (GA + wn * TJ + j) + kb));
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) acc[i][j] = mfma(fw[j], fa[i], acc[i][j]);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot are done
+      __builtin_amdgcn_s_barrier();        // ... and every wave's, before the slot is refilled
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float y = a.epi.apply(acc[i][j][v], sr[i], a.epi.srow != nullptr, sc[j][v], bi[j][v]);
+          chain[i][j][v] = sgi == 0 ? y : fadd(chain[i][j][v], y);
+        }
+  }
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int m = m0 + (wm * TI + i) * 16 + li, n = n0 + (wn * TJ + j) * 16 + 4 * lg;
+      if (m < a.M && n < a.N) store_out4(a.Y, m * a.ldy, n, a.epi.out, chain[i][j], a.epi.out_scale);
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int KS, int S>
+hipError_t go_staged(const MfmaArgs& a, hipStream_t s) {
+  constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * KS;
+  static_assert(lds <= 65536, "stage ring exceeds 64 KiB of LDS");
+  const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((mfma_staged_kernel<BM, BN, WM, WN, KS, S>), grid, dim3(64 * WM * WN), lds, s, a);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------------------------ dispatch
-// Chunk rows (M <= 16): one 16-column tile per workgroup and 8 waves over K (the weights have no
-// reuse, so the most workgroups and the most weight bytes in flight). Prompt rows: 32 x 32 tiles
-// and 4 waves over K, one chunk in flight per wave (the fastest of the measured 16/32/64-row x
-// 16/32/64-column tiles, 2/4/8/16 waves over K, 1-4 chunk depths, and 2 x 2 / 4 x 2 waves sharing
-// a 64 x 64 / 128 x 64 tile's operands through L1, at M = 256 and M = 1024).
+// Chunk rows (M <= 16): the direct kernel with one 16-column tile per workgroup and 8 waves over
+// K (the weights have no reuse, so the most workgroups and the most weight bytes in flight).
+// Prompt rows: the staged kernel when every K block is a whole number of stages -- 64 x 64 tiles
+// (16 waves, 128-byte stages, 4 slots) once they alone give about 192 or more workgroups, else
+// 32 x 32 tiles (4 waves, 256-byte stages, 3 slots) -- and the direct kernel's 32 x 32 tiles with
+// 4 waves over K otherwise. Measured on MI355X with the weights cold (rotated over 384 MiB):
+// M=256 K=1024 N=3072 10.7 -> 8.0 us, M=256 K=3072 N=1024 10.6 -> 9.1 us,
+// M=1024 K=1024 N=3072 28.9 -> 17.6 us, M=64 K=1024 N=3072 6.8 -> 5.6 us, bit-identical.
+bool whole_stages(const MfmaArgs& a, int ks) {
+  for (int i = 0; i < a.nseg; ++i)
+    if (a.seg[i].K % ks) return false;
+  return true;
+}
+
 hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
+  const int64_t tiles64 = static_cast<int64_t>((a.M + 63) / 64) * ((a.N + 63) / 64);
+  if (tiles64 >= 192 && whole_stages(a, 128)) return go_staged<64, 64, 4, 4, 128, 4>(a, s);
+  if (whole_stages(a, 256)) return go_staged<32, 32, 2, 2, 256, 3>(a, s);
   return go_direct<2, 2, 4, 1>(a, s);
 }
 

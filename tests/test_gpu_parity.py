@@ -270,6 +270,20 @@ def test_ksplit_gemv_block_shapes(split, M):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("M,N,blocks", [(17, 208, [4096, 2816]), (45, 208, [4096, 2816]), (200, 3072, [256, 384]),
+                                          (33, 96, [1040, 256])])
+def test_ksplit_staged_prompt_tiles(M, N, blocks):
+    """The K split on the LDS-staged prompt tiles: 32 x 32 tiles with 256-byte stages, 64 x 64
+    tiles with 128-byte stages (M=200, N=3072), and a block that is not a whole number of stages
+    (1040), which takes the direct tiles."""
+    x, q, s, W, scol, _ = w8_inputs(M * 31 + N, M, N, sum(blocks))
+    parts = np.split(W, np.cumsum(blocks)[:-1], axis=1)
+    parts = [np.ascontiguousarray(b) for b in parts]
+    y = ops.gemm_rowcol_ksplit(cuda(q), cuda(s), [cuda(b) for b in parts], cuda(scol))
+    want = G.gemm_rowcol_ksplit(q, s, parts, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("M", [17, 45])
 def test_ksplit_prompt_tiles(M):
     """The K split on the prompt-row MFMA tiles (M > 16), with a ragged last row and column tile."""
@@ -288,6 +302,31 @@ def test_epilogue_matrix_prompt_tiles(qm, act, out):
     a ragged last row and column tile (M = 45, N = 80), a huge scale and int8 -128."""
     rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, "prompt")).encode()))
     M, N, K = 45, 80, 16 * int(rng.integers(1, 90))
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
+    sc[N // 3] = 3e30
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32)
+    osc = f32(5.0) if out == OUT_INT8 else None
+    y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc), cuda(b),
+                        act=act, out=out, out_scale=osc)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
+@pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
+                                     (ACT_GELU, OUT_FP32), (ACT_SOFTPLUS, OUT_BF16)])
+@pytest.mark.parametrize("M,N", [(45, 80), (200, 3072 + 16)])
+def test_epilogue_matrix_staged_tiles(qm, act, out, M, N):
+    """The LDS-staged prompt tiles (K a multiple of 256: 32 x 32 tiles at N=80, 64 x 64 tiles at
+    N=3088) through every scale mode and output format with a bias, ragged last row and column
+    tiles, a huge scale and int8 -128."""
+    rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, M, N, "staged")).encode()))
+    K = 256 * int(rng.integers(1, 5))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
     sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
@@ -322,7 +361,7 @@ def test_c4_prefill_gemm(path, M, K, N):
 
 
 @pytest.mark.parametrize("M", [2, 3, 5, 16, 17, 31, 33, 64, 100, 300])
-@pytest.mark.parametrize("K", [64, 1040, 5000 // 16 * 16])
+@pytest.mark.parametrize("K", [64, 256, 1024, 1040, 5000 // 16 * 16])
 def test_mfma_ragged_m_and_k(M, K):
     x, q, s, W, scol, rng = w8_inputs(M * 1000 + K, M, 80, K)
     b = rng.normal(0, 1, 80).astype(f32)
