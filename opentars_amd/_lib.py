@@ -54,6 +54,15 @@ SIGNATURES = {
     "tars_encode_descriptor": (c_int, [POINTER(c_uint64), c_int32, c_void_p]),
     "tars_set_queue_fusion": (c_int, [c_int]),
     "tars_set_queue_graphs": (c_int, [c_int]),
+    "tars_row_op": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_uint32, c_int32, c_void_p, c_void_p,
+                            c_int64, c_int32, c_uint32, c_int32, c_int32, c_void_p]),
+    "tars_elt": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32,
+                         c_int32, c_void_p, c_int64, c_int32, c_uint32, c_int32, c_int32, c_void_p]),
+    "tars_rope": (c_int, [c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int64, c_int32, c_uint32, c_int32,
+                          c_int32, c_void_p]),
+    "tars_relu": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_uint32, c_int32, c_int32, c_void_p]),
+    "tars_fdot": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_int32, c_uint32,
+                          c_int32, c_int32, c_int32, c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None

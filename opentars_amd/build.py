@@ -19,7 +19,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libopentars_amd.so"
-SOURCES = ["abi.hip", "queue.hip", "quant_rows.hip", "gemv_w8a8.hip", "gemm_w8a8_mfma.hip", "w4a16.hip"]
+SOURCES = ["abi.hip", "queue.hip", "quant_rows.hip", "gemv_w8a8.hip", "gemm_w8a8_mfma.hip", "w4a16.hip",
+           "rowops.hip"]
 ARCH = "gfx950"
 
 

@@ -72,7 +72,7 @@ bool extent_ok(const void* base, int64_t ld, int64_t nrows, int64_t row_bytes) {
   return end <= static_cast<unsigned __int128>(UINTPTR_MAX);
 }
 
-int esize(int out) { return out == TARS_OUT_FP32 ? 4 : out == TARS_OUT_BF16 ? 2 : 1; }
+int esize(int out) { return out == TARS_OUT_FP32 ? 4 : (out == TARS_OUT_BF16 || out == TARS_OUT_FP16) ? 2 : 1; }
 
 int check_epilogue(int act, int out, uint32_t out_scale_bits) {
   if (act < 0 || act > 7) return fail(TARS_E_FIELD, "act must be 0..7");
@@ -364,6 +364,156 @@ int tars_gemm_w4a16(const void* x, int64_t lda, int32_t a_dtype, const uint8_t* 
   a.N = N;
   a.K = K;
   return launched(tars::launch_gemv_w4a16(a, static_cast<hipStream_t>(stream)));
+}
+
+// ------------------------------------------------------------------ fp32 row / elementwise / dot ops
+// Shared rules: M, N (and K) >= 1; fp32 data 4-byte aligned, fp16 data 2-byte aligned, the output
+// aligned to its element; strides 0 (dense) or multiples of the element size holding a row; act
+// 0..7; out FP32 / BF16 / INT8 (and FP16 for ELT); out_scale only with INT8.
+}  // extern "C"
+
+namespace {
+
+int check_out(int out, uint32_t out_scale_bits, bool fp16_ok) {
+  if (out < 0 || out > 3 || (out == TARS_OUT_FP16 && !fp16_ok))
+    return fail(TARS_E_FIELD, fp16_ok ? "out must be FP32, BF16, INT8 or FP16" : "out must be FP32, BF16 or INT8");
+  if (out != TARS_OUT_INT8 && out_scale_bits != 0) return fail(TARS_E_FIELD, "out_scale is only meaningful for INT8 output");
+  return TARS_OK;
+}
+
+// A row stride: 0 -> dense; else a multiple of the element size holding a row.
+bool stride_ok(int64_t& ld, int64_t row_bytes, int elem) {
+  if (ld == 0) ld = row_bytes;
+  return ld >= row_bytes && ld % elem == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tars_row_op(const float* x, int64_t lda, int32_t fn, const float* gamma, const float* beta, uint32_t eps_bits,
+                int32_t causal_k, const int32_t* valid, void* y, int64_t ldy, int32_t out, uint32_t out_scale_bits,
+                int32_t M, int32_t N, void* stream) {
+  g_last_error.clear();
+  if (!x || !y) return fail(TARS_E_ARG, "NULL pointer");
+  if (fn < TARS_ROW_SOFTMAX || fn > TARS_ROW_L2NORM) return fail(TARS_E_FIELD, "fn must be SOFTMAX, LAYERNORM, RMSNORM or L2NORM");
+  if (int rc = check_out(out, out_scale_bits, false)) return rc;
+  const bool softmax = fn == TARS_ROW_SOFTMAX;
+  if (softmax && (gamma || beta || eps_bits)) return fail(TARS_E_FIELD, "softmax takes no gamma, beta or eps");
+  if (!softmax && (causal_k || valid)) return fail(TARS_E_FIELD, "only softmax is causal");
+  if (!softmax && !gamma) return fail(TARS_E_ARG, "the norms need gamma");
+  if (causal_k < 0) return fail(TARS_E_FIELD, "causal_k must be >= 0");
+  if (M <= 0 || N <= 0) return fail(TARS_E_ALIGN, "M, N >= 1");
+  const int64_t xrow = 4LL * N, yrow = static_cast<int64_t>(N) * esize(out);
+  if (!stride_ok(lda, xrow, 4) || !stride_ok(ldy, yrow, esize(out))) return fail(TARS_E_ALIGN, "strides must hold a row");
+  if (!aligned(x, 4) || !aligned(y, esize(out)) || (gamma && !aligned(gamma, 4)) || (beta && !aligned(beta, 4)) ||
+      (valid && !aligned(valid, 4)))
+    return fail(TARS_E_ALIGN, "pointer alignment");
+  if (!extent_ok(x, lda, M, xrow) || !extent_ok(y, ldy, M, yrow)) return fail(TARS_E_RANGE, "extent overflows");
+  const auto yout = rows(y, ldy, M, yrow);
+  if (overlaps(rows(x, lda, M, xrow), yout) || (gamma && overlaps(one(gamma, xrow), yout)) ||
+      (beta && overlaps(one(beta, xrow), yout)) || (valid && overlaps(one(valid, 4LL * M), yout)))
+    return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::RowArgs a{x, lda, fn, gamma, beta, f32_of(eps_bits), causal_k, valid, y, ldy, out, f32_of(out_scale_bits), M, N};
+  return launched(tars::launch_row(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_elt(const void* A, int64_t lda, int32_t a_fp16, int32_t a_row, const float* B, int64_t ldb, int32_t bmode,
+             const void* C, int64_t ldc, int32_t op, int32_t act, void* Y, int64_t ldy, int32_t out,
+             uint32_t out_scale_bits, int32_t M, int32_t N, void* stream) {
+  g_last_error.clear();
+  if (!A || !B || !Y || (op == TARS_ELT_MULADD && !C)) return fail(TARS_E_ARG, "NULL pointer");
+  if (op < TARS_ELT_MUL || op > TARS_ELT_SUB) return fail(TARS_E_FIELD, "op must be MUL, ADD, MULADD or SUB");
+  if (bmode < TARS_BM_DENSE || bmode > TARS_BM_SCALAR) return fail(TARS_E_FIELD, "bmode must be DENSE, ROW, COL or SCALAR");
+  if (act < 0 || act > 7) return fail(TARS_E_FIELD, "act must be 0..7");
+  if ((a_fp16 != 0 && a_fp16 != 1) || (a_row != 0 && a_row != 1)) return fail(TARS_E_FIELD, "a_fp16 and a_row are 0 or 1");
+  if (int rc = check_out(out, out_scale_bits, true)) return rc;
+  if (op == TARS_ELT_MULADD && out != TARS_OUT_FP32 && out != TARS_OUT_FP16)
+    return fail(TARS_E_FIELD, "MULADD adds C in the output format: out must be FP32 or FP16");
+  if (op != TARS_ELT_MULADD && C) return fail(TARS_E_FIELD, "C is only read by MULADD");
+  if (M <= 0 || N <= 0) return fail(TARS_E_ALIGN, "M, N >= 1");
+  const int ae = a_fp16 ? 2 : 4, ye = esize(out), ce = out == TARS_OUT_FP16 ? 2 : 4;
+  const int64_t arow = static_cast<int64_t>(ae) * N, yrow = static_cast<int64_t>(ye) * N, crow = static_cast<int64_t>(ce) * N;
+  if (!stride_ok(lda, arow, ae) || !stride_ok(ldy, yrow, ye) || (op == TARS_ELT_MULADD && !stride_ok(ldc, crow, ce)) ||
+      (bmode == TARS_BM_DENSE && !stride_ok(ldb, 4LL * N, 4)))
+    return fail(TARS_E_ALIGN, "strides must hold a row");
+  if (!aligned(A, ae) || !aligned(B, 4) || !aligned(Y, ye) || (C && !aligned(C, ce))) return fail(TARS_E_ALIGN, "pointer alignment");
+  const int64_t am = a_row ? 1 : M;
+  const int64_t bbytes = bmode == TARS_BM_ROW ? 4LL * N : bmode == TARS_BM_COL ? 4LL * M : 4;
+  if (!extent_ok(A, lda, am, arow) || !extent_ok(Y, ldy, M, yrow) || (C && !extent_ok(C, ldc, M, crow)) ||
+      (bmode == TARS_BM_DENSE && !extent_ok(B, ldb, M, 4LL * N)))
+    return fail(TARS_E_RANGE, "extent overflows");
+  // In place (golden.py:440-448): Y may be A itself (same format and stride, not a broadcast row)
+  // or C itself (same stride); any other overlap of an input with Y is refused.
+  const bool a_inplace = A == Y && !a_row && lda == ldy &&
+                         (a_fp16 ? out == TARS_OUT_FP16 : out == TARS_OUT_FP32);
+  const bool c_inplace = C && C == Y && ldc == ldy;
+  const auto yout = rows(Y, ldy, M, yrow);
+  if ((!a_inplace && overlaps(rows(A, lda, am, arow), yout)) ||
+      (bmode == TARS_BM_DENSE ? overlaps(rows(B, ldb, M, 4LL * N), yout) : overlaps(one(B, bbytes), yout)) ||
+      (C && !c_inplace && overlaps(rows(C, ldc, M, crow), yout)))
+    return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::EltArgs a{A, lda, a_fp16, a_row, B, ldb, bmode, C, ldc, op, act, Y, ldy, out, f32_of(out_scale_bits), M, N};
+  return launched(tars::launch_elt(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_rope(const float* x, int64_t lda, const float* tab, int32_t rows_per_pos, int32_t rot, void* y, int64_t ldy,
+              int32_t out, uint32_t out_scale_bits, int32_t M, int32_t N, void* stream) {
+  g_last_error.clear();
+  if (!x || !tab || !y) return fail(TARS_E_ARG, "NULL pointer");
+  if (int rc = check_out(out, out_scale_bits, false)) return rc;
+  if (M <= 0 || N <= 0 || rows_per_pos <= 0 || rot <= 0 || rot % 2 || rot > N)
+    return fail(TARS_E_ALIGN, "M, N >= 1; rows_per_pos >= 1; rot even, 2 <= rot <= N");
+  const int64_t xrow = 4LL * N, yrow = static_cast<int64_t>(N) * esize(out);
+  const int64_t tab_bytes = 4LL * rot * ((M - 1) / rows_per_pos + 1);
+  if (!stride_ok(lda, xrow, 4) || !stride_ok(ldy, yrow, esize(out))) return fail(TARS_E_ALIGN, "strides must hold a row");
+  if (!aligned(x, 4) || !aligned(tab, 4) || !aligned(y, esize(out))) return fail(TARS_E_ALIGN, "pointer alignment");
+  if (!extent_ok(x, lda, M, xrow) || !extent_ok(y, ldy, M, yrow) || !extent_ok(tab, tab_bytes, 1, tab_bytes))
+    return fail(TARS_E_RANGE, "extent overflows");
+  const auto yout = rows(y, ldy, M, yrow);
+  if (overlaps(rows(x, lda, M, xrow), yout) || overlaps(one(tab, tab_bytes), yout))
+    return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::RopeArgs a{x, lda, tab, rows_per_pos, rot, y, ldy, out, f32_of(out_scale_bits), M, N};
+  return launched(tars::launch_rope(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_relu(const float* x, int64_t lda, int32_t act, void* y, int64_t ldy, int32_t out, uint32_t out_scale_bits,
+              int32_t M, int32_t N, void* stream) {
+  g_last_error.clear();
+  if (!x || !y) return fail(TARS_E_ARG, "NULL pointer");
+  if (act < 0 || act > 7) return fail(TARS_E_FIELD, "act must be 0..7");
+  if (int rc = check_out(out, out_scale_bits, false)) return rc;
+  if (M <= 0 || N <= 0) return fail(TARS_E_ALIGN, "M, N >= 1");
+  const int64_t xrow = 4LL * N, yrow = static_cast<int64_t>(N) * esize(out);
+  if (!stride_ok(lda, xrow, 4) || !stride_ok(ldy, yrow, esize(out))) return fail(TARS_E_ALIGN, "strides must hold a row");
+  if (!aligned(x, 4) || !aligned(y, esize(out))) return fail(TARS_E_ALIGN, "pointer alignment");
+  if (!extent_ok(x, lda, M, xrow) || !extent_ok(y, ldy, M, yrow)) return fail(TARS_E_RANGE, "extent overflows");
+  if (overlaps(rows(x, lda, M, xrow), rows(y, ldy, M, yrow))) return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::ReluArgs a{x, lda, act, y, ldy, out, f32_of(out_scale_bits), M, N};
+  return launched(tars::launch_relu(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_fdot(const float* A, int64_t lda, const void* B, int64_t ldb, int32_t nn, int32_t b_fp16, void* Y, int64_t ldy,
+              int32_t out, uint32_t out_scale_bits, int32_t M, int32_t N, int32_t K, void* stream) {
+  g_last_error.clear();
+  if (!A || !B || !Y) return fail(TARS_E_ARG, "NULL pointer");
+  if ((nn != 0 && nn != 1) || (b_fp16 != 0 && b_fp16 != 1)) return fail(TARS_E_FIELD, "nn and b_fp16 are 0 or 1");
+  if (b_fp16 && !nn) return fail(TARS_E_FIELD, "an fp16 B is read only by the NN form");
+  if (int rc = check_out(out, out_scale_bits, false)) return rc;
+  if (M <= 0 || N <= 0 || K <= 0) return fail(TARS_E_ALIGN, "M, N, K >= 1");
+  const int be = b_fp16 ? 2 : 4;
+  const int64_t arow = 4LL * K, brow = static_cast<int64_t>(be) * (nn ? N : K), bn = nn ? K : N;
+  const int64_t yrow = static_cast<int64_t>(N) * esize(out);
+  if (!stride_ok(lda, arow, 4) || !stride_ok(ldb, brow, be) || !stride_ok(ldy, yrow, esize(out)))
+    return fail(TARS_E_ALIGN, "strides must hold a row");
+  if (!aligned(A, 4) || !aligned(B, be) || !aligned(Y, esize(out))) return fail(TARS_E_ALIGN, "pointer alignment");
+  if (!extent_ok(A, lda, M, arow) || !extent_ok(B, ldb, bn, brow) || !extent_ok(Y, ldy, M, yrow))
+    return fail(TARS_E_RANGE, "extent overflows");
+  const auto yout = rows(Y, ldy, M, yrow);
+  if (overlaps(rows(A, lda, M, arow), yout) || overlaps(rows(B, ldb, bn, brow), yout))
+    return fail(TARS_E_OVERLAP, "the output overlaps an input");
+  tars::FdotArgs a{A, lda, B, ldb, nn, b_fp16, Y, ldy, out, f32_of(out_scale_bits), M, N, K};
+  return launched(tars::launch_fdot(a, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -195,6 +195,53 @@ __device__ __forceinline__ float from_fp16_bits(uint32_t h) {
   return ffrom(e == 31 ? special : (e == 0 ? sub : normal));
 }
 
+// numerics.py:14-18: fp32 -> binary16 bits, round to nearest even with gradual underflow, signed
+// zero, NaN -> 0x7E00. Integer rounding of the significand for normal results; for results below
+// 2^-14 the exact product x * 2^24 (a power-of-two scaling) rounded to an integer is the subnormal's
+// significand (1024 there is the smallest normal, 0x0400).
+__device__ __forceinline__ uint16_t to_fp16_bits(float x) {
+  const uint32_t b = fbits(x);
+  const uint32_t s = (b >> 16) & 0x8000u, a = b & 0x7FFFFFFFu;
+  if (a > kExpo) return 0x7E00u;
+  if (a >= 0x477FF000u) return static_cast<uint16_t>(s | 0x7C00u);  // 65520 and above round to inf
+  if (a >= 0x38800000u) {                                             // 2^-14 and above: normal
+    const uint32_t mant = a & kMant, rem = mant & 0x1FFFu;
+    uint32_t h = ((((a >> 23) - 112u)) << 10) | (mant >> 13);
+    h += (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ? 1u : 0u;
+    return static_cast<uint16_t>(s | h);
+  }
+  return static_cast<uint16_t>(s | static_cast<uint32_t>(rintf(ffrom(a) * 16777216.0f)));
+}
+
+// 1/sqrt(x) (numerics.py:171-191): E = biased exponent - 127 = 2k + j; m = x with exponent field
+// 127 + j (m in [1, 4)); seed bits(y0) = 0x5F3759DF - (bits(m) >> 1); three correction-form Newton
+// steps y <- y + y * (1/2 + -(1/2 * ((m * y) * y))), each op one rounded contract step; then -k is
+// added to y's exponent field. +-0 -> +-inf, +inf -> +0, negative or NaN -> canonical NaN.
+__device__ __forceinline__ float rsqrt_f(float x) {
+  const uint32_t xb = fbits(ftz(x));
+  const uint32_t mag = xb & 0x7FFFFFFFu;
+  if (mag > kExpo || ((xb & kSign) && mag != 0)) return ffrom(kCanonNaN);
+  if (mag == 0) return ffrom((xb & kSign) | kExpo);
+  if (xb == kExpo) return 0.0f;
+  const int E = static_cast<int>((xb >> 23) & 0xFFu) - 127;
+  const int j = E & 1, k = E >> 1;  // arithmetic shift: floor, so E = 2k + j for E < 0 too
+  const uint32_t mb = (xb & kMant) | (static_cast<uint32_t>(127 + j) << 23);
+  const float m = ffrom(mb), half = ffrom(kHalf);
+  float y = ffrom(0x5F3759DFu - (mb >> 1));
+#pragma unroll
+  for (int i = 0; i < 3; ++i) y = fadd(y, fmul(y, fadd(half, fneg(fmul(half, fmul(fmul(m, y), y))))));
+  return add_to_exponent(y, -k);
+}
+
+// Order key of the contract's fmax (numerics.py:293-303) on a flushed, non-NaN value: unsigned
+// key order is the fp order with -0 below +0, so the key maximum of a set is its fmax (+0 from
+// +0 and -0, -0 only from -0s). NaN is tracked beside the key.
+__device__ __forceinline__ uint32_t fmax_key(float x) {
+  const uint32_t b = fbits(x);
+  return (b & kSign) ? ~b : (b | kSign);
+}
+__device__ __forceinline__ float fmax_from_key(uint32_t k) { return ffrom((k & kSign) ? (k ^ kSign) : ~k); }
+
 // Stores one epilogue result in the output format (golden.py:273-280).
 __device__ __forceinline__ void store_out(void* Y, int64_t byte_row, int n, int out, float y,
                                           float out_scale) {
@@ -203,6 +250,8 @@ __device__ __forceinline__ void store_out(void* Y, int64_t byte_row, int n, int 
     reinterpret_cast<float*>(row)[n] = ftz(y);
   } else if (out == 1) {
     reinterpret_cast<uint16_t*>(row)[n] = to_bf16_bits(y);
+  } else if (out == 3) {
+    reinterpret_cast<uint16_t*>(row)[n] = to_fp16_bits(y);
   } else {
     reinterpret_cast<int8_t*>(row)[n] = q8(y, out_scale);
   }

@@ -113,6 +113,87 @@ struct QuantGemvArgs {
   int block_start[kMaxGroups + 1];  // first workgroup of each group along grid x
 };
 
+// Row functions, elementwise ops, rotary embedding and fp32 dot products (rowops.hip). Row strides
+// are in bytes; fp32 and fp16 elements are read with element loads, so 4- / 2-byte alignment
+// suffices.
+enum RowFn { ROWFN_SOFTMAX = 0, ROWFN_LAYERNORM = 1, ROWFN_RMSNORM = 2, ROWFN_L2NORM = 3 };
+struct RowArgs {
+  const void* x;           // [M, N] fp32 rows
+  int64_t lda;
+  int fn;
+  const float* gamma;      // [N] (norms)
+  const float* beta;       // [N] or nullptr
+  float eps;
+  int causal_k;            // softmax: > 0 -> row m sees min(N, causal_k + m) elements
+  const int32_t* valid;    // softmax: per-row valid counts (overrides causal_k) or nullptr
+  void* y;
+  int64_t ldy;
+  int out;
+  float out_scale;
+  int M, N;
+};
+
+enum EltOp { ELTOP_MUL = 0, ELTOP_ADD = 1, ELTOP_MULADD = 2, ELTOP_SUB = 3 };
+enum BMode { BMODE_DENSE = 0, BMODE_ROW = 1, BMODE_COL = 2, BMODE_SCALAR = 3 };
+struct EltArgs {
+  const void* A;           // fp32 or fp16 rows (a_fp16); a_row: one row broadcast to all M
+  int64_t lda;
+  int a_fp16, a_row;
+  const float* B;          // dense rows at ldb, or N / M / 1 values
+  int64_t ldb;
+  int bmode;
+  const void* C;           // MULADD addend rows, in the output's float format
+  int64_t ldc;
+  int op, act;
+  void* Y;
+  int64_t ldy;
+  int out;
+  float out_scale;
+  int M, N;
+};
+
+struct RopeArgs {
+  const void* x;
+  int64_t lda;
+  const float* tab;        // rows of [cos(0..rot/2-1), sin(0..rot/2-1)]
+  int rows_per_pos, rot;
+  void* y;
+  int64_t ldy;
+  int out;
+  float out_scale;
+  int M, N;
+};
+
+struct ReluArgs {
+  const void* x;
+  int64_t lda;
+  int act;
+  void* y;
+  int64_t ldy;
+  int out;
+  float out_scale;
+  int M, N;
+};
+
+struct FdotArgs {
+  const void* A;           // [M, K] fp32
+  int64_t lda;
+  const void* B;           // NT: [N, K] fp32; NN: [K, N] fp32 or fp16 (b_fp16)
+  int64_t ldb;
+  int nn, b_fp16;
+  void* Y;
+  int64_t ldy;
+  int out;
+  float out_scale;
+  int M, N, K;
+};
+
+hipError_t launch_row(const RowArgs& a, hipStream_t s);
+hipError_t launch_elt(const EltArgs& a, hipStream_t s);
+hipError_t launch_rope(const RopeArgs& a, hipStream_t s);
+hipError_t launch_relu(const ReluArgs& a, hipStream_t s);
+hipError_t launch_fdot(const FdotArgs& a, hipStream_t s);
+
 hipError_t launch_quant_rows(const QuantArgs& a, hipStream_t s);
 hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s);
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s);

@@ -403,11 +403,8 @@ Checked check(const uint8_t* raw, uint64_t len, int core_id, bool gemv_only) {
 
 // Whether this library runs the descriptor on the GPU: W8A8 GEMM (QM_TENSOR / QM_CHANNEL /
 // QM_ROWCOL), the W4A16 group GEMM, ROW_QUANT.
-bool gpu_kind(const Desc& d) {
-  const uint64_t op = d[F_OPCODE];
-  if (op == OP_GEMM) return true;  // a valid GEMM is one of the W8A8 modes or W4A16
-  return op == OP_ROW && (d[F_CTRL] & 7) == ROW_QUANT;
-}
+// Every valid descriptor but a convolution runs on the GPU.
+bool gpu_kind(const Desc& d) { return d[F_OPCODE] != OP_CONV && d[F_OPCODE] != OP_CONV_ACT; }
 
 // Enqueues a valid, GPU-kind descriptor with pointers into the image; returns a TARS_ status.
 // `needs_host` is set instead when the image addresses miss the kernels' alignment (a base
@@ -420,13 +417,41 @@ int launch(uint8_t* image, const Desc& d, hipStream_t stream, bool& needs_host) 
   const uintptr_t b = reinterpret_cast<uintptr_t>(B);
   needs_host = b % 16 != 0 || (is_w4(d) && (b + d[F_W_OFF]) % 128 != 0);
   if (needs_host) return TARS_OK;
-  if (d[F_OPCODE] == OP_ROW) {
-    return tars_quant_rows(reinterpret_cast<const float*>(B + d[F_A_OFF]), static_cast<int64_t>(s.lda),
-                           reinterpret_cast<int8_t*>(B + d[F_Y_OFF]), static_cast<int64_t>(s.ldy),
-                           reinterpret_cast<float*>(B + d[F_SCALE_OFF]), M, N, stream);
-  }
   const float* bias = has_bias(d[F_EPI]) ? reinterpret_cast<const float*>(B + d[F_BIAS_OFF]) : nullptr;
   const uint32_t osc = static_cast<uint32_t>(d[F_OUT_SCALE]);
+  const uint64_t op = d[F_OPCODE];
+  const auto f32p = [&](Field off) { return reinterpret_cast<const float*>(B + d[off]); };
+  const int64_t lda = static_cast<int64_t>(s.lda), ldy = static_cast<int64_t>(s.ldy);
+  if (op == OP_ROW) {  // golden.py:358-380
+    const uint64_t fn = d[F_CTRL] & 7;
+    if (fn == ROW_QUANT)
+      return tars_quant_rows(f32p(F_A_OFF), lda, reinterpret_cast<int8_t*>(B + d[F_Y_OFF]), ldy,
+                             reinterpret_cast<float*>(B + d[F_SCALE_OFF]), M, N, stream);
+    if (fn == ROW_SOFTMAX)
+      return tars_row_op(f32p(F_A_OFF), lda, TARS_ROW_SOFTMAX, nullptr, nullptr, 0, K, nullptr, B + d[F_Y_OFF], ldy,
+                         static_cast<int>(out), osc, M, N, stream);
+    return tars_row_op(f32p(F_A_OFF), lda, static_cast<int32_t>(fn), f32p(F_SCALE_OFF), bias,
+                       static_cast<uint32_t>(d[F_W_OFF]), 0, nullptr, B + d[F_Y_OFF], ldy, static_cast<int>(out), osc, M,
+                       N, stream);
+  }
+  if (op == OP_RELU)  // golden.py:351-356
+    return tars_relu(f32p(F_A_OFF), lda, static_cast<int>(act), B + d[F_Y_OFF], ldy, static_cast<int>(out), osc, M, N,
+                     stream);
+  if (op == OP_ELT) {  // golden.py:393-418
+    const uint64_t hr = d[F_HDR_RSV], eop = d[F_CTRL] & 3, bm = hr & 3;
+    return tars_elt(B + d[F_A_OFF], lda, (hr & kStateFp16) ? 1 : 0, static_cast<int32_t>((hr >> 2) & 1), f32p(F_W_OFF),
+                    bm == BM_DENSE ? static_cast<int64_t>(b_stride(d).first) : 0, static_cast<int32_t>(bm),
+                    eop == ELT_MULADD ? B + d[F_BIAS_OFF] : nullptr, eop == ELT_MULADD ? ldy : 0,
+                    static_cast<int32_t>(eop), static_cast<int>(act), B + d[F_Y_OFF], ldy, static_cast<int>(out), osc, M,
+                    N, stream);
+  }
+  if (op == OP_ROPE)  // golden.py:420-424
+    return tars_rope(f32p(F_A_OFF), lda, f32p(F_W_OFF), static_cast<int32_t>(d[F_GROUP_SIZE]), K, B + d[F_Y_OFF], ldy,
+                     static_cast<int>(out), osc, M, N, stream);
+  if (op == OP_FDOT)  // golden.py:426-436
+    return tars_fdot(f32p(F_A_OFF), lda, B + d[F_W_OFF], static_cast<int64_t>(b_stride(d).first),
+                     static_cast<int32_t>(d[F_CTRL] & 1), (d[F_HDR_RSV] & kStateFp16) ? 1 : 0, B + d[F_Y_OFF], ldy,
+                     static_cast<int>(out), osc, M, N, K, stream);
   if (is_w4(d)) {
     const int adt = ((d[F_CTRL] >> 4) & 15) == DT_FP32 ? TARS_DT_FP32 : TARS_DT_BF16;
     return tars_gemm_w4a16(B + d[F_A_OFF], static_cast<int64_t>(s.lda), adt, B + d[F_W_OFF],

@@ -8,6 +8,13 @@ bit-identical to the golden model (tars_mini/golden.py, tars_mini/numerics.py):
   gemm_rowcol_ksplit(q, srow, Ws, scol)  lin_k blocks + ELT_ADD chain   llm.py:303-321, 627-635
   align_w4_groups(x)                     numerics.align_w4_groups       numerics.py:55-98
   gemm_w4(x, Wp, ws, ...)                Machine._gemm_w4               golden.py:295-324
+  softmax_rows(x) / softmax_rows_causal  Machine._row (ROW_SOFTMAX)     numerics.py:328-333, 362-371
+  layernorm_rows / rmsnorm_rows /        Machine._row (norms)           numerics.py:341-358, 374-380
+    l2norm_rows(x, gamma, beta, eps)
+  relu(x, act)                           Machine._relu                  golden.py:351-356
+  elt(op, a, b, ...)                     Machine._elt                   golden.py:393-418
+  rope_rows(x, tab, rows_per_pos, rot)   Machine._rope                  numerics.py:412-424
+  fdot_nt(a, b) / fdot_nn(a, b)          Machine._fdot                  numerics.py:393-409
 
 Inputs are torch tensors on the GPU (results stay there, stream-ordered on the current stream),
 or numpy arrays (copied in; results come back as numpy after a synchronize, which is what
@@ -23,7 +30,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .contract import (ACT_NONE, DT_BF16, DT_FP32, ESIZE, OUT_BF16, OUT_FP32, OUT_INT8, W4_GROUP)
+from .contract import (ACT_NONE, DT_BF16, DT_FP32, ESIZE, OUT_BF16, OUT_FP16, OUT_FP32, OUT_INT8, W4_GROUP)
 
 
 class TarsError(RuntimeError):
@@ -98,7 +105,8 @@ def _numpy_mode(*args) -> bool:
 
 
 def _out_dtype(out: int) -> torch.dtype:
-    return {OUT_FP32: torch.float32, OUT_BF16: torch.bfloat16, OUT_INT8: torch.int8}.get(out, torch.uint8)
+    return {OUT_FP32: torch.float32, OUT_BF16: torch.bfloat16, OUT_INT8: torch.int8,
+            OUT_FP16: torch.int16}.get(out, torch.uint8)
 
 
 def _f32_bits(v) -> int:
@@ -113,6 +121,8 @@ def _finish(numpy_mode: bool, *ts: torch.Tensor):
     for t in ts:
         if t.dtype == torch.bfloat16:
             outs.append(t.view(torch.int16).cpu().numpy().view(np.uint16))
+        elif t.dtype == torch.int16:                       # binary16 bits
+            outs.append(t.cpu().numpy().view(np.uint16))
         else:
             outs.append(t.cpu().numpy())
     return tuple(outs) if len(outs) > 1 else outs[0]
@@ -274,6 +284,158 @@ def gemm_w4(x, Wp, ws, bias=None, act: int = ACT_NONE, out: int = OUT_FP32, out_
     return _finish(npm, y)
 
 
+# ---------------------------------------------------------------- fp32 row / elementwise / dot ops
+ROW_SOFTMAX, ROW_LAYERNORM, ROW_RMSNORM, ROW_L2NORM = 0, 1, 2, 3
+ELT_MUL, ELT_ADD, ELT_MULADD, ELT_SUB = 0, 1, 2, 3
+BM_DENSE, BM_ROW, BM_COL, BM_SCALAR = 0, 1, 2, 3
+
+
+def _f32_rows(x, what: str) -> torch.Tensor:
+    t = _to_dev(x)
+    if t.dtype != torch.float32 or t.dim() != 2:
+        raise ValueError(f"{what} must be fp32 [M, N]")
+    return t
+
+
+def _half_rows(x, what: str) -> torch.Tensor:
+    """binary16 rows as int16 bits (numpy uint16 / torch float16 or int16)."""
+    t = _to_dev(x)
+    if t.dtype == torch.float16:
+        t = t.view(torch.int16)
+    if t.dtype != torch.int16 or t.dim() != 2:
+        raise ValueError(f"{what} must be binary16 [rows, cols]")
+    return t
+
+
+def _out(y, M: int, N: int, out: int, like: torch.Tensor) -> torch.Tensor:
+    return torch.empty((M, N), dtype=_out_dtype(out), device=like.device) if y is None else y
+
+
+def _row_op(x, fn: int, gamma=None, beta=None, eps=0.0, causal_k: int = 0, valid=None, out: int = OUT_FP32,
+            out_scale=None, y=None):
+    npm = _numpy_mode(x, gamma, beta, valid)
+    xt = _f32_rows(x, "x")
+    M, N = xt.shape
+    gt = None if gamma is None else _vec(_to_dev(gamma, torch.float32), N, "gamma")
+    bt = None if beta is None else _vec(_to_dev(beta, torch.float32), N, "beta")
+    vt = None if valid is None else _vec(_to_dev(np.asarray(valid, np.int32) if not isinstance(valid, torch.Tensor)
+                                                 else valid, torch.int32), M, "valid")
+    y = _out(y, M, N, out, xt)
+    eb = _f32_bits(eps) if fn != ROW_SOFTMAX else 0
+    osb = _f32_bits(out_scale) if out == OUT_INT8 else 0
+    _check(_lib.lib().tars_row_op(xt.data_ptr(), _ld(xt), fn, _ptr(gt), _ptr(bt), eb, causal_k, _ptr(vt),
+                                  y.data_ptr(), _ld(y), out, osb, M, N, _stream()))
+    return _finish(npm, y)
+
+
+def softmax_rows(x, out: int = OUT_FP32, out_scale=None, y=None, causal_k: int = 0):
+    """mx = row max; e = exp(x + -mx); y = e * recip(sum16(e)) (numerics.py:328-333). causal_k > 0:
+    row m sees its first min(N, causal_k + m) elements (the ROW_SOFTMAX descriptor's K rule,
+    golden.py:366-367)."""
+    return _row_op(x, ROW_SOFTMAX, causal_k=causal_k, out=out, out_scale=out_scale, y=y)
+
+
+def softmax_rows_causal(x, valid, out: int = OUT_FP32, out_scale=None, y=None):
+    """Softmax over the first valid[m] (1..N) elements of row m; the rest +0 (numerics.py:362-371)."""
+    return _row_op(x, ROW_SOFTMAX, valid=valid, out=out, out_scale=out_scale, y=y)
+
+
+def layernorm_rows(x, gamma, beta, eps, out: int = OUT_FP32, out_scale=None, y=None):
+    """numerics.py:341-350."""
+    return _row_op(x, ROW_LAYERNORM, gamma, beta, eps, out=out, out_scale=out_scale, y=y)
+
+
+def rmsnorm_rows(x, gamma, beta, eps, out: int = OUT_FP32, out_scale=None, y=None):
+    """numerics.py:353-358."""
+    return _row_op(x, ROW_RMSNORM, gamma, beta, eps, out=out, out_scale=out_scale, y=y)
+
+
+def l2norm_rows(x, gamma, beta, eps, out: int = OUT_FP32, out_scale=None, y=None):
+    """numerics.py:374-380."""
+    return _row_op(x, ROW_L2NORM, gamma, beta, eps, out=out, out_scale=out_scale, y=y)
+
+
+def relu(x, act: int, out: int = OUT_FP32, out_scale=None, y=None):
+    """act(x) converted to the output format (golden.py:351-356)."""
+    npm = _numpy_mode(x)
+    xt = _f32_rows(x, "x")
+    M, N = xt.shape
+    y = _out(y, M, N, out, xt)
+    osb = _f32_bits(out_scale) if out == OUT_INT8 else 0
+    _check(_lib.lib().tars_relu(xt.data_ptr(), _ld(xt), act, y.data_ptr(), _ld(y), out, osb, M, N, _stream()))
+    return _finish(npm, y)
+
+
+def elt(op: int, a, b, bmode: int = BM_DENSE, c=None, act: int = ACT_NONE, out: int = OUT_FP32, out_scale=None,
+        y=None, a_fp16: bool = False, a_row: bool = False, shape: tuple | None = None):
+    """y = act(a) * b | act(a) + b | act(a) + -b | c + act(a) * b (golden.py:393-418). a: fp32
+    [M, N] (a_fp16: binary16 bits; a_row: one row [1, N] for every m); b: fp32 [M, N] (DENSE) or a
+    vector of N (ROW), M (COL) or 1 (SCALAR) values; c: MULADD's addend [M, N] in the output's
+    float format; y may be a or c itself (in place). shape=(M, N) when a is a broadcast row."""
+    npm = _numpy_mode(a, b, c)
+    at = _half_rows(a, "a") if a_fp16 else _f32_rows(a, "a")
+    M, N = shape if shape is not None else at.shape
+    bt = _to_dev(b, torch.float32)
+    if bmode == BM_DENSE:
+        if bt.dim() != 2:
+            raise ValueError("a dense b must be [M, N]")
+        ldb = _ld(bt)
+    else:
+        bt = bt.reshape(-1)
+        ldb = 0
+    ct = None
+    if c is not None:
+        ct = _half_rows(c, "c") if out == OUT_FP16 else _f32_rows(c, "c")
+    y = _out(y, M, N, out, at)
+    osb = _f32_bits(out_scale) if out == OUT_INT8 else 0
+    _check(_lib.lib().tars_elt(at.data_ptr(), _ld(at), int(a_fp16), int(a_row), bt.data_ptr(), ldb, bmode,
+                               _ptr(ct), 0 if ct is None else _ld(ct), op, act, y.data_ptr(), _ld(y), out, osb, M, N,
+                               _stream()))
+    return _finish(npm, y)
+
+
+def rope_rows(x, tab, rows_per_pos: int, rot: int, out: int = OUT_FP32, out_scale=None, y=None):
+    """Rotary embedding of the first rot elements of each row, table row m // rows_per_pos
+    (numerics.py:412-424)."""
+    npm = _numpy_mode(x, tab)
+    xt = _f32_rows(x, "x")
+    tt = _f32_rows(tab, "tab")
+    M, N = xt.shape
+    if tt.shape[1] != rot or not tt.is_contiguous() or tt.shape[0] < (M - 1) // rows_per_pos + 1:
+        raise ValueError("tab must be a dense [positions, rot] fp32 table covering every row")
+    y = _out(y, M, N, out, xt)
+    osb = _f32_bits(out_scale) if out == OUT_INT8 else 0
+    _check(_lib.lib().tars_rope(xt.data_ptr(), _ld(xt), tt.data_ptr(), rows_per_pos, rot, y.data_ptr(), _ld(y), out,
+                                osb, M, N, _stream()))
+    return _finish(npm, y)
+
+
+def _fdot(a, b, nn: bool, b_fp16: bool, out: int, out_scale, y):
+    npm = _numpy_mode(a, b)
+    at = _f32_rows(a, "a")
+    bt = _half_rows(b, "b") if b_fp16 else _f32_rows(b, "b")
+    M, K = at.shape
+    N = bt.shape[1] if nn else bt.shape[0]
+    if (bt.shape[0] if nn else bt.shape[1]) != K:
+        raise ValueError("a and b disagree on K")
+    y = _out(y, M, N, out, at)
+    osb = _f32_bits(out_scale) if out == OUT_INT8 else 0
+    _check(_lib.lib().tars_fdot(at.data_ptr(), _ld(at), bt.data_ptr(), _ld(bt), int(nn), int(b_fp16), y.data_ptr(),
+                                _ld(y), out, osb, M, N, K, _stream()))
+    return _finish(npm, y)
+
+
+def fdot_nt(a, b, out: int = OUT_FP32, out_scale=None, y=None):
+    """y[m][n] = sum16 over k of a[m][k] * b[n][k] (numerics.py:393-399)."""
+    return _fdot(a, b, False, False, out, out_scale, y)
+
+
+def fdot_nn(a, b, b_fp16: bool = False, out: int = OUT_FP32, out_scale=None, y=None):
+    """y[m][n] = ((+0 + a[m][0] b[0][n]) + a[m][1] b[1][n]) + ... (numerics.py:402-409); b may be
+    binary16 bits (the fp16 KV state)."""
+    return _fdot(a, b, True, b_fp16, out, out_scale, y)
+
+
 def set_w8a8_path(path: str) -> str:
     """'auto' | 'gemv' | 'mfma': which W8A8 kernel family runs for M >= 2 (and M = 1). Returns the
     previous setting."""
@@ -283,4 +445,7 @@ def set_w8a8_path(path: str) -> str:
 
 
 __all__ = ["TarsError", "ContractError", "quant_rows", "gemm_rowcol", "quant_gemm_rowcol", "gemm_rowcol_ksplit",
-           "align_w4_groups", "gemm_w4", "set_w8a8_path", "ESIZE"]
+           "align_w4_groups", "gemm_w4", "set_w8a8_path", "ESIZE", "softmax_rows", "softmax_rows_causal",
+           "layernorm_rows", "rmsnorm_rows", "l2norm_rows", "relu", "elt", "rope_rows", "fdot_nt", "fdot_nn",
+           "ROW_SOFTMAX", "ROW_LAYERNORM", "ROW_RMSNORM", "ROW_L2NORM", "ELT_MUL", "ELT_ADD", "ELT_MULADD",
+           "ELT_SUB", "BM_DENSE", "BM_ROW", "BM_COL", "BM_SCALAR"]

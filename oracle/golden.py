@@ -5,7 +5,7 @@ Op-level forms of the descriptor semantics the HIP kernels reproduce bit for bit
   gemm_rowcol_ksplit the K-block split and its in-order fp32 adds      llm.py:303-321, 627-635,
                                                                        golden.py:393-418 (ELT_ADD)
   gemm_w4            OP_GEMM W4A16 (QM_GROUP + INT4 weights)           golden.py:295-324
-  convert            output conversion (fp32 / bf16 / int8)            golden.py:273-280
+  convert            output conversion (fp32 / bf16 / int8 / fp16)     golden.py:273-280
 plus the host weight quantizers (compiler.py:47-85).
 """
 from __future__ import annotations
@@ -24,14 +24,16 @@ def int_dot(a: np.ndarray, w: np.ndarray) -> np.ndarray:
 
 def convert(y: np.ndarray, out: int, out_scale: np.float32 | None = None) -> np.ndarray:
     """fp32 results -> stored elements (golden.py:273-280): fp32 flushed; bf16 bits (RNE, NaN
-    0x7FC0); int8 q8(y, OUT_SCALE)."""
+    0x7FC0); int8 q8(y, OUT_SCALE); fp16 bits (RNE with gradual underflow, NaN 0x7E00)."""
     if out == OUT_FP32:
         return F.ftz(y)
     if out == OUT_BF16:
         return F.to_bf16_bits(y)
     if out == OUT_INT8:
         return F.q8(y, np.float32(out_scale))
-    raise ValueError(f"output format {out} is not a GEMM output")
+    if out == OUT_FP16:
+        return F.to_fp16_bits(y)
+    raise ValueError(f"output format {out}")
 
 
 def epilogue_rowcol(acc: np.ndarray, srow, scol, bias=None, act: int = F.ACT_NONE) -> np.ndarray:

@@ -7,10 +7,11 @@
   Machine.run_queue                   in-order execution and end status    golden.py:450-492
 
 The executor here runs the descriptors the GPU library runs (OP_GEMM: W8A8 in QM_TENSOR /
-QM_CHANNEL / QM_ROWCOL and W4A16; OP_ROW ROW_QUANT) through the oracle's arithmetic, and stops at
-any other valid descriptor with `host_op` set, exactly as the GPU executor hands such descriptors
-back. It is the reference the GPU queue executor is compared with, byte for byte and status for
-status; only the tests may import it.
+QM_CHANNEL / QM_ROWCOL and W4A16; OP_ROW: softmax, causal softmax, LayerNorm, RMSNorm, L2Norm and
+ROW_QUANT; OP_RELU; OP_ELT; OP_ROPE; OP_FDOT) through the oracle's arithmetic, and stops at a
+valid convolution descriptor with `host_op` set, exactly as the GPU executor hands such
+descriptors back. It is the reference the GPU queue executor is compared with, byte for byte and
+status for status; only the tests may import it.
 
 Pinning: the layout, codec and CRC by the contract document's worked example (descriptor bytes
 and CRC 0x3784C47F, tests/test_contract.py:12-14,47-84) and the reference's round-trip and bit-flip
@@ -31,6 +32,7 @@ import numpy as np
 
 from . import golden as G
 from . import numerics as F
+from . import rowops as R
 
 LAYOUT = {
     "MAGIC": (511, 496), "VERSION": (495, 480), "CORE_ID": (479, 472), "HDR_RSV": (471, 448),
@@ -346,7 +348,8 @@ def check(raw: bytes, ddr_len: int, core_id: int = 0, gemv_only: bool = False):
 
 
 def gpu_kind(d: dict) -> bool:
-    return d["OPCODE"] == OP_GEMM or (d["OPCODE"] == OP_ROW and d["CTRL"] & 7 == ROW_QUANT)
+    """Every opcode but the convolutions runs on the GPU."""
+    return d["OPCODE"] not in CONV_OPS
 
 
 @dataclass
@@ -358,8 +361,8 @@ class Status:
 
 
 class Machine:
-    """A DDR byte image and the in-order queue walk of golden.py:450-492 for the GEMM and
-    ROW_QUANT descriptors (other valid descriptors stop the queue with host_op)."""
+    """A DDR byte image and the in-order queue walk of golden.py:450-492 for every descriptor but
+    the convolutions (a valid conv descriptor stops the queue with host_op)."""
 
     def __init__(self, ddr, core_id: int = 0, gemv_only: bool = False):
         self.ddr = bytearray(ddr)
@@ -377,10 +380,13 @@ class Machine:
         lda = strides(d)[0]
         act, out, osc = act_of(e), e >> 2 & 3, np.frombuffer(struct.pack("<I", d["OUT_SCALE"]), "<f4")[0]
         bias = np.frombuffer(self.read(B + d["BIAS_OFF"], 4 * N), "<f4") if e >> 4 & 1 else None
-        if d["OPCODE"] == OP_ROW:                                       # ROW_QUANT, golden.py:369-372
+        op = d["OPCODE"]
+        if op == OP_ROW and d["CTRL"] & 7 == ROW_QUANT:                 # golden.py:369-372
             q, s = F.quant_rows(self._rows(B + d["A_OFF"], lda, M, 4 * N, "<f4"))
             return q.view(np.uint8).reshape(M, -1), (B + d["SCALE_OFF"], F.ftz(s).astype("<f4").tobytes())
-        if is_w4(d):                                                     # golden.py:295-324
+        if op in (OP_RELU, OP_ROW, OP_ELT, OP_ROPE, OP_FDOT):
+            y = self._rowop(d, lda)
+        elif is_w4(d):                                                     # golden.py:295-324
             bf16 = d["CTRL"] >> 4 & 15 == DT_BF16
             x = self._rows(B + d["A_OFF"], lda, M, (2 if bf16 else 4) * K, "<u2" if bf16 else "<f4")
             wp = np.frombuffer(self.read(B + d["W_OFF"], N * K // 2), np.uint8).reshape(N, K // 2)
@@ -393,8 +399,62 @@ class Machine:
             sc = np.frombuffer(self.read(B + d["SCALE_OFF"], 4 * (1 if qm == QM_TENSOR else N)), "<f4")
             sr = np.frombuffer(self.read(B + 16 * d["HDR_RSV"], 4 * M), "<f4") if qm == QM_ROWCOL else None
             y = G.gemm_rowcol(a, sr, w, sc, bias, act, out, osc)
-        dt = {OUT_FP32: "<f4", OUT_BF16: "<u2", OUT_INT8: np.int8}[out]
+        dt = {OUT_FP32: "<f4", OUT_BF16: "<u2", OUT_INT8: np.int8, OUT_FP16: "<u2"}[out]
         return np.ascontiguousarray(y.astype(dt)).view(np.uint8).reshape(M, -1), None
+
+    def _f32rows(self, addr: int, ld: int, m: int, n: int, half: bool = False) -> np.ndarray:
+        if half:
+            return F.from_fp16_bits(self._rows(addr, ld, m, 2 * n, "<u2"))
+        return self._rows(addr, ld, m, 4 * n, "<f4").astype(np.float32)
+
+    def _rowop(self, d: dict, lda: int) -> np.ndarray:
+        """RELU, the row functions, ELT, ROPE and FDOT (golden.py:351-436), converted to the output
+        format."""
+        B, M, N, K, e = d["BASE_ADDR"], d["M"], d["N"], d["K"], d["EPI"]
+        act, out = act_of(e), e >> 2 & 3
+        osc = np.frombuffer(struct.pack("<I", d["OUT_SCALE"]), "<f4")[0]
+        op = d["OPCODE"]
+        if op == OP_RELU:                                                # golden.py:351-356
+            y = F.act_fn(self._f32rows(B + d["A_OFF"], lda, M, N), act)
+        elif op == OP_ROW:                                               # golden.py:358-380
+            x = self._f32rows(B + d["A_OFF"], lda, M, N)
+            fn = d["CTRL"] & 7
+            if fn == ROW_SOFTMAX and K:
+                y = R.softmax_rows_causal(x, np.minimum(N, K + np.arange(M)))
+            elif fn == ROW_SOFTMAX:
+                y = R.softmax_rows(x)
+            else:
+                g = np.frombuffer(self.read(B + d["SCALE_OFF"], 4 * N), "<f4").astype(np.float32)
+                b = np.frombuffer(self.read(B + d["BIAS_OFF"], 4 * N), "<f4").astype(np.float32) if e >> 4 & 1 else None
+                eps = np.frombuffer(struct.pack("<I", d["W_OFF"]), "<f4")[0]
+                f = {ROW_LAYERNORM: R.layernorm_rows, ROW_RMSNORM: R.rmsnorm_rows, ROW_L2NORM: R.l2norm_rows}[fn]
+                y = f(x, g, b, eps)
+        elif op == OP_ELT:                                               # golden.py:393-418
+            ldy = strides(d)[1]
+            hr = d["HDR_RSV"]
+            a = self._f32rows(B + d["A_OFF"], 0 if hr >> 2 & 1 else lda, M, N, bool(hr & STATE_FP16))
+            bm = hr & 3
+            if bm == BM_DENSE:
+                bv = self._f32rows(B + d["W_OFF"], bstride(d)[0], M, N)
+            else:
+                cnt = {BM_ROW: N, BM_COL: M, BM_SCALAR: 1}[bm]
+                bv = np.frombuffer(self.read(B + d["W_OFF"], 4 * cnt), "<f4").astype(np.float32)
+            eop = d["CTRL"] & 3
+            c = self._f32rows(B + d["BIAS_OFF"], ldy, M, N, out == OUT_FP16) if eop == R.ELT_MULADD else None
+            y = R.elt(eop, a, R.broadcast_b(bv, bm, M, N), c, act)
+        elif op == OP_ROPE:                                              # golden.py:420-424
+            G_, Rr = d["GROUP_SIZE"], K
+            x = self._f32rows(B + d["A_OFF"], lda, M, N)
+            tab = self._f32rows(B + d["W_OFF"], 4 * Rr, (M - 1) // G_ + 1, Rr)
+            y = R.rope_rows(x, tab, G_, Rr)
+        else:                                                            # OP_FDOT, golden.py:426-436
+            a = self._f32rows(B + d["A_OFF"], lda, M, K)
+            ldb = bstride(d)[0]
+            if d["CTRL"] & 1:
+                y = R.fdot_nn(a, self._f32rows(B + d["W_OFF"], ldb, K, N, bool(d["HDR_RSV"] & STATE_FP16)))
+            else:
+                y = R.fdot_nt(a, self._f32rows(B + d["W_OFF"], ldb, N, K))
+        return G.convert(y, out, osc)
 
     def run_queue(self, queue_addr: int, n: int) -> Status:
         for i in range(n):

@@ -1,7 +1,9 @@
 """The descriptor-queue executor on the GPU (opentars_amd.queue over tars_run_queue) against the
 oracle's queue walk: whole DDR images byte for byte and end statuses, on random programs of
 ROW_QUANT, W8A8 GEMM (QM_TENSOR / QM_CHANNEL / QM_ROWCOL, every epilogue and output format,
-strided rows) and W4A16 GEMM, with errors, host hand-offs and overlaps. Needs a gfx950 GPU."""
+strided rows), W4A16 GEMM, the row functions (softmax, causal softmax, LayerNorm, RMSNorm,
+L2Norm), RELU, ELT (every op and broadcast, fp16 states, in place), RoPE and FDOT (NT, NN, fp16 B),
+with errors, host hand-offs (a convolution) and overlaps. Needs a gfx950 GPU."""
 from __future__ import annotations
 
 import struct
@@ -134,11 +136,138 @@ def add_w4(p: Program, M: int, N: int, K: int):
           K=K, LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
 
 
+def f32bits(v: float) -> int:
+    return struct.unpack("<I", struct.pack("<f", float(v)))[0]
+
+
+def put_rows(p: Program, x: np.ndarray, row_bytes: int):
+    """fp32 or uint16 rows [M, n] in a (sometimes strided) region; returns (offset, ld16)."""
+    a, ld16 = stride_fields(p, x.shape[0], row_bytes)
+    ld = 16 * ld16 if ld16 else row_bytes
+    for m in range(x.shape[0]):
+        p.ddr[a + m * ld:a + m * ld + row_bytes] = x[m].tobytes()
+    return a, ld16
+
+
+def rand_rows(p: Program, M: int, N: int) -> np.ndarray:
+    x = (p.rng.normal(0, 1, (M, N)) * np.exp2(p.rng.integers(-4, 5, (M, 1)))).astype("<f4")
+    if p.rng.integers(0, 6) == 0:
+        x[int(p.rng.integers(0, M)), int(p.rng.integers(0, N))] = [np.inf, -np.inf, np.nan, 0.0, 1e-40][
+            int(p.rng.integers(0, 5))]
+    return x
+
+
+def out_fields(p: Program, M: int, N: int, outs=(Q.OUT_FP32, Q.OUT_BF16, Q.OUT_INT8)):
+    out = int(p.rng.choice(outs))
+    y, ldy16 = stride_fields(p, M, N * Q.ESIZE[out])
+    osc = f32bits(p.rng.uniform(0.5, 8.0)) if out == Q.OUT_INT8 else 0
+    return out, y, ldy16, osc
+
+
+def add_row(p: Program, M: int, N: int):
+    rng = p.rng
+    fn = int(rng.choice([Q.ROW_SOFTMAX, Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM]))
+    a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    out, y, ldy16, osc = out_fields(p, M, N)
+    f = dict(OPCODE=Q.OP_ROW, CTRL=fn, A_OFF=a, Y_OFF=y, M=M, N=N, LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
+    if fn == Q.ROW_SOFTMAX:
+        f.update(EPI=Q.epi(out=out), K=int(rng.integers(1, N + 1)) if rng.integers(0, 2) else 0)
+    else:
+        bias = int(rng.integers(0, 2))
+        g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
+        b = p.put(rng.normal(0, 0.1, N).astype("<f4").tobytes()) if bias else 0
+        eps = float(rng.choice([1e-6, 1e-5, 0.0]))
+        f.update(EPI=Q.epi(out=out, bias=bias), SCALE_OFF=g, BIAS_OFF=b, W_OFF=f32bits(eps))
+    p.add(**f)
+    return y
+
+
+def add_relu(p: Program, M: int, N: int, src=None, lda16=0):
+    if src is None:
+        src, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    out, y, ldy16, osc = out_fields(p, M, N)
+    p.add(OPCODE=Q.OP_RELU, EPI=Q.epi(int(p.rng.integers(1, 8)), out), A_OFF=src, Y_OFF=y, M=M, N=N, LDA16=lda16,
+          LDY16=ldy16, OUT_SCALE=osc)
+
+
+def add_elt(p: Program, M: int, N: int):
+    rng = p.rng
+    op = int(rng.integers(0, 4))
+    bm = int(rng.integers(0, 4))
+    fp16 = bool(rng.integers(0, 3) == 0)
+    arow = bool(rng.integers(0, 4) == 0)
+    outs = (Q.OUT_FP32, Q.OUT_FP16) if op == Q.ELT_MULADD else (Q.OUT_FP32, Q.OUT_BF16, Q.OUT_INT8, Q.OUT_FP16)
+    out = int(rng.choice(outs))
+    A = rand_rows(p, 1 if arow else M, N)
+    if fp16:
+        with np.errstate(over="ignore"):
+            A = A.astype(np.float16).view("<u2")
+    inplace = not arow and rng.integers(0, 3) == 0 and (out == (Q.OUT_FP16 if fp16 else Q.OUT_FP32))
+    arb = (2 if fp16 else 4) * N
+    a, lda16 = put_rows(p, A, arb)
+    if bm == Q.BM_DENSE:
+        w, gs = put_rows(p, rand_rows(p, M, N), 4 * N)
+    else:
+        cnt = {Q.BM_ROW: N, Q.BM_COL: M, Q.BM_SCALAR: 1}[bm]
+        w = p.put(rng.normal(0, 1, cnt).astype("<f4").tobytes(), align=16 if bm == Q.BM_ROW else 4)
+        gs = 0
+    if inplace:
+        y, ldy16 = a, lda16
+    else:
+        y, ldy16 = stride_fields(p, M, N * Q.ESIZE[out])
+    c = 0
+    if op == Q.ELT_MULADD:
+        C = rand_rows(p, M, N)
+        crow = C.astype(np.float16).view("<u2") if out == Q.OUT_FP16 else C
+        if not inplace and rng.integers(0, 2):
+            c = y                                   # C is the output itself
+            ld = 16 * ldy16 if ldy16 else N * Q.ESIZE[out]
+            for m in range(M):
+                p.ddr[y + m * ld:y + m * ld + N * Q.ESIZE[out]] = crow[m].tobytes()
+        else:
+            y_ld = 16 * ldy16 if ldy16 else N * Q.ESIZE[out]
+            c = p.alloc(y_ld * M)
+            for m in range(M):
+                p.ddr[c + m * y_ld:c + m * y_ld + N * Q.ESIZE[out]] = crow[m].tobytes()
+    osc = f32bits(rng.uniform(0.5, 8.0)) if out == Q.OUT_INT8 else 0
+    hdr = bm | (4 if arow else 0) | (Q.STATE_FP16 if fp16 else 0)
+    p.add(OPCODE=Q.OP_ELT, CTRL=op, EPI=Q.epi(int(rng.integers(0, 8)), out, int(op == Q.ELT_MULADD)), HDR_RSV=hdr,
+          A_OFF=a, W_OFF=w, BIAS_OFF=c, Y_OFF=y, M=M, N=N, LDA16=lda16, LDY16=ldy16, GROUP_SIZE=gs, OUT_SCALE=osc)
+
+
+def add_rope(p: Program, M: int, N: int):
+    rng = p.rng
+    R = 32 * int(rng.integers(1, N // 32 + 1))
+    G = int(rng.integers(1, 4))
+    a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    rows = (M - 1) // G + 1
+    fr = (np.arange(rows, dtype=np.float32)[:, None] * rng.uniform(0.01, 1.0, R // 2).astype(np.float32)[None, :])
+    t = p.put(np.concatenate([np.cos(fr), np.sin(fr)], 1).astype("<f4").tobytes())
+    out, y, ldy16, osc = out_fields(p, M, N)
+    p.add(OPCODE=Q.OP_ROPE, EPI=Q.epi(out=out), A_OFF=a, W_OFF=t, Y_OFF=y, M=M, N=N, K=R, GROUP_SIZE=G,
+          LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
+
+
+def add_fdot(p: Program, M: int, N: int, K: int):
+    rng = p.rng
+    nn = int(rng.integers(0, 2))
+    fp16 = bool(nn and rng.integers(0, 2))
+    a, lda16 = put_rows(p, rand_rows(p, M, K), 4 * K)
+    Bm = rand_rows(p, K, N) if nn else rand_rows(p, N, K)
+    if fp16:
+        with np.errstate(over="ignore"):
+            Bm = Bm.astype(np.float16).view("<u2")
+    w, gs = put_rows(p, Bm, Bm.shape[1] * Bm.dtype.itemsize)
+    out, y, ldy16, osc = out_fields(p, M, N)
+    p.add(OPCODE=Q.OP_FDOT, CTRL=nn, HDR_RSV=Q.STATE_FP16 if fp16 else 0, EPI=Q.epi(out=out), A_OFF=a, W_OFF=w,
+          Y_OFF=y, M=M, N=N, K=K, GROUP_SIZE=gs, LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
+
+
 def random_program(seed: int) -> Program:
     p = Program(seed)
     rng = p.rng
     for _ in range(int(rng.integers(4, 9))):
-        kind = int(rng.integers(0, 5))
+        kind = int(rng.integers(0, 10))
         M = int(rng.choice([1, 2, 4, 5, 17, 40]))
         if kind == 0:                                   # ROW_QUANT feeding a QM_ROWCOL GEMM (RAW)
             K = 16 * int(rng.integers(1, 40))
@@ -151,11 +280,23 @@ def random_program(seed: int) -> Program:
             add_w4(p, min(M, 5), 16 * int(rng.integers(1, 8)), 256 * int(rng.integers(1, 5)))
         elif kind == 3:
             add_quant(p, M, 16 * int(rng.integers(1, 60)))
-        else:                                           # a decode row shared by 1-5 GEMMs (fusable)
+        elif kind == 4:                                 # a decode row shared by 1-5 GEMMs (fusable)
             K = 16 * int(rng.integers(1, 80))
             q, ldq, s = add_quant(p, 1, K)
             for _ in range(int(rng.integers(1, 6))):
                 add_w8(p, 1, 16 * int(rng.integers(1, 12)), K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s)
+        elif kind == 5:
+            add_row(p, M, 16 * int(rng.integers(1, 70)))
+        elif kind == 6:                                 # a GEMM's fp32 output through an activation (RAW)
+            N = 16 * int(rng.integers(1, 12))
+            y = add_w8(p, M, N, 16 * int(rng.integers(1, 20)), Q.QM_CHANNEL, out=Q.OUT_FP32)
+            add_relu(p, M, N, src=y, lda16=0)
+        elif kind == 7:
+            add_elt(p, M, 16 * int(rng.integers(1, 20)))
+        elif kind == 8:
+            add_rope(p, M, 32 * int(rng.integers(1, 6)))
+        else:
+            add_fdot(p, M, 16 * int(rng.integers(1, 12)), 16 * int(rng.integers(1, 20)))
     return p
 
 
@@ -294,46 +435,53 @@ def test_output_overlapping_input_raises_and_writes_nothing_of_it():
     assert bytes(g.ddr) == bytes(o.ddr)           # descriptors before it ran, it did not
 
 
-def relu_desc(p: Program, src: int, n: int) -> tuple[int, bytes]:
-    y = p.alloc(4 * n)
-    return y, Q.encode({"MAGIC": Q.MAGIC, "VERSION": Q.VERSION, "VALID": 1, "OPCODE": Q.OP_RELU, "EPI": Q.epi(1),
-                        "A_OFF": src, "Y_OFF": y, "M": 1, "N": n})
+def conv_desc(p: Program) -> tuple[int, bytes]:
+    """A valid 3x3 convolution (4x4 input, pad 1, 16 -> 16 channels): the one descriptor kind the
+    executor hands to the host. Its output rows are [16, 16] fp32."""
+    a = p.put(p.rng.integers(-128, 128, (16, 16), dtype=np.int8).tobytes())
+    w = p.put(p.rng.integers(-128, 128, (16, 9 * 16), dtype=np.int8).tobytes())
+    s = p.put(np.full(16, 1e-3, "<f4").tobytes())
+    y = p.alloc(4 * 16 * 16)
+    return y, Q.encode({"MAGIC": Q.MAGIC, "VERSION": Q.VERSION, "VALID": 1, "OPCODE": Q.OP_CONV,
+                        "CTRL": Q.ctrl(Q.QM_CHANNEL), "EPI": Q.epi(), "A_OFF": a, "W_OFF": w, "SCALE_OFF": s,
+                        "Y_OFF": y, "M": 16, "N": 16, "K": 9 * 16, "GROUP_SIZE": 4,
+                        "HDR_RSV": (4 << 12) | (3 << 8) | (3 << 4) | 1})
 
 
 class FakeHost:
-    """A host executor for the test: runs one RELU descriptor (max(x, 0) on fp32 bits, -0 and NaN to
-    +0) in place on the host image."""
+    """A host executor for the test: runs one convolution descriptor by writing a fixed fp32
+    pattern (y[i] = (i - 128) / 8) to its output rows on the host image -- a stand-in for the host's
+    own convolution, enough to follow the data across the hand-off."""
 
     def __init__(self, ddr: bytearray):
         self.ddr = ddr
 
     def run_queue(self, addr: int, n: int):
         d = Q.decode(bytes(self.ddr[addr:addr + 64]))
-        assert n == 1 and d["OPCODE"] == Q.OP_RELU
-        x = np.frombuffer(bytes(self.ddr[d["A_OFF"]:d["A_OFF"] + 4 * d["N"]]), "<f4")
-        y = np.where(x > 0, x, np.float32(0)).astype("<f4")
-        self.ddr[d["Y_OFF"]:d["Y_OFF"] + 4 * d["N"]] = y.tobytes()
+        assert n == 1 and d["OPCODE"] == Q.OP_CONV
+        y = ((np.arange(d["M"] * d["N"], dtype=np.float32) - 128) / 8).astype("<f4")
+        self.ddr[d["Y_OFF"]:d["Y_OFF"] + y.nbytes] = y.tobytes()
         return Q.Status(True, Q.E_OK, 1)
 
 
 def test_host_hand_off_stops_then_resumes_with_a_host():
-    """A RELU between two GPU descriptors: without a host the queue stops there (host_op); with one
-    it runs on the host copy and the GPU descriptors after it see its output (RAW across the
-    hand-off)."""
+    """A convolution between two GPU descriptors: without a host the queue stops there (host_op);
+    with one it runs on the host copy and the GPU descriptors after it see its output (RAW across
+    the hand-off)."""
     p = Program(60)
-    y0 = add_w8(p, 1, 32, 64, Q.QM_CHANNEL, act=0, out=Q.OUT_FP32, bias=0)
-    ry, rdesc = relu_desc(p, y0, 32)
-    p.descs.append(rdesc)
-    q, ldq, s = add_quant(p, 1, 32)                   # quantizes the RELU output: A_OFF patched below
+    add_w8(p, 1, 32, 64, Q.QM_CHANNEL, act=0, out=Q.OUT_FP32, bias=0)
+    cy, cdesc = conv_desc(p)
+    p.descs.append(cdesc)
+    add_quant(p, 16, 16)                              # quantizes the conv output: A_OFF patched below
     f = Q.decode(p.descs[-1])
     f.pop("CRC32")
-    f.update(A_OFF=ry, LDA16=0)
+    f.update(A_OFF=cy, LDA16=0)
     p.descs[-1] = Q.encode(f)
     img = p.image()
     g = NQ.Machine(img)
     st = g.run_queue(QADDR, 3)
     assert (st.done, st.op_idx, st.host_op) == (False, 1, True)
-    # the expected image: the oracle to the RELU, the fake host, then the oracle for the rest
+    # the expected image: the oracle to the conv, the fake host, then the oracle for the rest
     o = Q.Machine(img)
     assert o.run_queue(QADDR, 1).done
     FakeHost(o.ddr).run_queue(QADDR + 64, 1)

@@ -177,11 +177,28 @@ def test_row_quant_then_rowcol_gemm_chain():
     assert m.read(0x5000, 4 * M * N) == G.gemm_rowcol(q, s, W, sc).astype("<f4").tobytes()
 
 
-def test_other_opcodes_stop_with_host_op():
-    relu = dict(MAGIC=Q.MAGIC, VERSION=Q.VERSION, OPCODE=Q.OP_RELU, M=1, N=16, VALID=1, EPI=Q.epi(1),
-                A_OFF=0x800, Y_OFF=0xA00)
-    st, m = run(base_image(), Q.encode(GEMM), Q.encode(relu), Q.encode(GEMM))
+def test_convolutions_stop_with_host_op():
+    """A valid convolution is the one descriptor kind the executor leaves to the host: the queue
+    stops there with host_op, keeping the earlier writes."""
+    conv = dict(MAGIC=Q.MAGIC, VERSION=Q.VERSION, VALID=1, OPCODE=Q.OP_CONV, CTRL=Q.ctrl(Q.QM_CHANNEL),
+                EPI=Q.epi(), A_OFF=0x100, W_OFF=0x200, SCALE_OFF=0x400, Y_OFF=0x3000, M=16, N=16, K=9 * 16,
+                HDR_RSV=(4 << 12) | (3 << 8) | (3 << 4) | 1, GROUP_SIZE=4)
+    assert Q.check(Q.encode(conv), 1 << 14)[0] == Q.E_OK
+    st, m = run(base_image(), Q.encode(GEMM), Q.encode(conv), Q.encode(GEMM))
     assert (st.done, st.err_code, st.op_idx, st.host_op) == (False, Q.E_OK, 1, True)
+    assert m.read(0x800, 64) != bytes(64)
+
+
+def test_relu_descriptor_runs():
+    """OP_RELU (golden.py:351-356): act on fp32 rows, converted to the output format."""
+    ddr = base_image()
+    x = np.linspace(-3, 3, 32, dtype=np.float32)
+    ddr[0x1000:0x1080] = x.tobytes()
+    relu = dict(MAGIC=Q.MAGIC, VERSION=Q.VERSION, OPCODE=Q.OP_RELU, M=2, N=16, VALID=1, EPI=Q.epi(1, out=Q.OUT_BF16),
+                A_OFF=0x1000, Y_OFF=0x1200)
+    st, m = run(ddr, Q.encode(relu))
+    assert st.done
+    assert m.read(0x1200, 64) == F.to_bf16_bits(F.relu_plain(x)).astype("<u2").tobytes()
 
 
 # ------------------------------------------------------------------------------ the native checker
