@@ -497,7 +497,62 @@ def config_suite(torch, lib, seed: int) -> dict:
         log(f"c5 K={K} N={N}: {r['us_per_call']} us")
         del ls, holds
         torch.cuda.empty_cache()
+    res["attention_decode_qwen3_t250"] = attention_decode(torch, lib, gen)
+    log(f"attention t=250: {res['attention_decode_qwen3_t250']['op_by_op']['us_per_layer']} us per layer")
     return res
+
+
+QWEN3_HEADS, QWEN3_KV_HEADS, QWEN3_HEAD_DIM, QWEN3_LAYERS = 16, 8, 128, 28
+
+
+def attention_layers(torch, lib, gen, t0: int):
+    """Decode attention of one token at position t0 for every Qwen3-0.6B layer, as the reference
+    lowers it (tars_mini/llm.py:736-746): per query head, FDOT_NT of the rotated q row with the
+    head's K cache rows (scores over pad16(t0 + 1) keys), the causal softmax with t0 + 1 valid keys,
+    and FDOT_NN of the probabilities with the V cache rows. fp32 caches of pad16(t0 + 1) rows per
+    layer; each layer its own caches. Returns ([launches of layer l], bytes read per layer)."""
+    nh, nkv, hd = QWEN3_HEADS, QWEN3_KV_HEADS, QWEN3_HEAD_DIM
+    nk = (t0 + 1 + 15) // 16 * 16
+    layers, keep = [], []
+    for _ in range(QWEN3_LAYERS):
+        kc = torch.randn((nk, nkv * hd), device="cuda", generator=gen)
+        vc = torch.randn((nk, nkv * hd), device="cuda", generator=gen)
+        q = torch.randn((1, nh * hd), device="cuda", generator=gen) * 0.1
+        sc = torch.empty((1, nk), device="cuda")
+        pr = torch.empty((1, nk), device="cuda")
+        att = torch.empty((1, nh * hd), device="cuda")
+        keep.append((kc, vc, q, sc, pr, att))
+        ls = []
+        for hh in range(nh):
+            kv = hh // (nh // nkv)
+            ls.append(Launch("fdot_nt", lib.tars_fdot,
+                             (q.data_ptr() + 4 * hh * hd, 4 * nh * hd, kc.data_ptr() + 4 * kv * hd, 4 * nkv * hd, 0, 0,
+                              sc.data_ptr(), 4 * nk, 0, 0, 1, nk, hd), 0, 0, f"h{hh}.scores", {}))
+            ls.append(Launch("softmax", lib.tars_row_op,
+                             (sc.data_ptr(), 4 * nk, 0, None, None, 0, t0 + 1, None, pr.data_ptr(), 4 * nk, 0, 0, 1, nk),
+                             0, 0, f"h{hh}.softmax", {}))
+            ls.append(Launch("fdot_nn", lib.tars_fdot,
+                             (pr.data_ptr(), 4 * nk, vc.data_ptr() + 4 * kv * hd, 4 * nkv * hd, 1, 0,
+                              att.data_ptr() + 4 * hh * hd, 4 * nh * hd, 0, 0, 1, hd, nk), 0, 0, f"h{hh}.pv", {}))
+        layers.append(ls)
+    return layers, keep, 2 * nk * nkv * hd * 4
+
+
+def attention_decode(torch, lib, gen, t0: int = 250) -> dict:
+    """The decode attention of one token at t=250 over all 28 layers, op by op (48 launches per
+    layer), timed as one graph per token: us per layer and per token."""
+    layers, keep, nbytes = attention_layers(torch, lib, gen, t0)
+    launches = [l for ls in layers for l in ls]
+    g = capture(torch, launches)
+    t = time_graph(torch, g, reps=20, warmup=3)
+    del g
+    r = {"op_by_op": {"launches_per_layer": len(layers[0]), "us_per_layer": round(t / len(layers) * 1e6, 2),
+                      "us_per_token": round(t * 1e6, 1), "GBps": round(nbytes * len(layers) / t / 1e9, 1)},
+         "t0": t0, "heads": QWEN3_HEADS, "kv_heads": QWEN3_KV_HEADS, "head_dim": QWEN3_HEAD_DIM,
+         "layers": QWEN3_LAYERS, "cache_bytes_per_layer": nbytes}
+    del layers, keep, launches
+    torch.cuda.empty_cache()
+    return r
 
 
 # ------------------------------------------------------------------------------ CPU baseline

@@ -26,12 +26,25 @@ __device__ __forceinline__ float fdpp_xor2(float v) { return __int_as_float(dpp<
 __device__ __forceinline__ float fdpp_half(float v) { return __int_as_float(dpp<kDppRowHalfMirror>(__float_as_int(v))); }
 __device__ __forceinline__ float fdpp_mirror(float v) { return __int_as_float(dpp<kDppRowMirror>(__float_as_int(v))); }
 
-// The pairwise fold of a 16-lane group's partial sums (every lane receives the row sum).
+// One step of a summation chain over flushed values: the contract's fadd without its input
+// flushes (identities here) and without the per-step NaN canonicalization. NaN is absorbing in a
+// sum (NaN + x is NaN for every x), so a chain's result is NaN exactly when the contract's
+// step-by-step chain's is, and every other step is the same rounded, flushed value; the chain's
+// result is canonicalized once at its end (chain_end). The flush tests the value class (+-
+// subnormal) in one compare.
+__device__ __forceinline__ float fadd_chain(float acc, float p) {
+  const float r = __fadd_rn(acc, p);
+  return __builtin_amdgcn_class(r, 0x90) ? ffrom(fbits(r) & kSign) : r;
+}
+__device__ __forceinline__ float chain_end(float acc) { return canon(acc); }
+
+// The pairwise fold of a 16-lane group's partial chain sums (every lane receives the row sum,
+// canonicalized).
 __device__ __forceinline__ float fold16(float v) {
-  v = fadd(v, fdpp_xor1(v));
-  v = fadd(v, fdpp_xor2(v));
-  v = fadd(v, fdpp_half(v));
-  return fadd(v, fdpp_mirror(v));
+  v = fadd_chain(v, fdpp_xor1(v));
+  v = fadd_chain(v, fdpp_xor2(v));
+  v = fadd_chain(v, fdpp_half(v));
+  return chain_end(fadd_chain(v, fdpp_mirror(v)));
 }
 
 __device__ __forceinline__ const float* frow(const void* base, int64_t ld, int m) {
@@ -39,7 +52,120 @@ __device__ __forceinline__ const float* frow(const void* base, int64_t ld, int m
 }
 
 // ------------------------------------------------------------------------------ row functions
-// One 16-lane group per row (golden.py:358-380; numerics.py:328-380).
+// A lane's elements of a row arrive in blocks of kChunk (elements l, l + 16, ... of the block),
+// loaded together before the block's dependent chain runs, and the next block is loaded while the
+// current one is consumed: one memory round trip per 16 * kChunk elements instead of one per
+// element.
+constexpr int kChunk = 16;
+
+struct RowBlock {
+  float v[kChunk];
+};
+
+__device__ __forceinline__ void load_block(RowBlock& b, const float* x, int j0, int l, int n) {
+#pragma unroll
+  for (int u = 0; u < kChunk; ++u) {
+    const int j = j0 + l + 16 * u;
+    b.v[u] = load_pred(x + j, x, j < n, 0.0f);
+  }
+}
+
+// Runs f(j, value) over this lane's elements j = l, l + 16, ... < n, in order.
+template <class Fn>
+__device__ __forceinline__ void for_lane(const float* x, int l, int n, Fn&& f) {
+  RowBlock cur, nxt;
+  load_block(cur, x, 0, l, n);
+  for (int j0 = 0; j0 < n; j0 += 16 * kChunk) {
+    if (j0 + 16 * kChunk < n) load_block(nxt, x, j0 + 16 * kChunk, l, n);
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int j = j0 + l + 16 * u;
+      if (j < n) f(j, cur.v[u]);
+    }
+    cur = nxt;
+  }
+}
+
+// The 16-lane chains of sum16 over v[0..n) in LDS, of the values (SQUARE: of fmul(v, v)): lane l
+// of the first 16 threads adds element l, l + 16, ... in order from +0, then the pairwise fold;
+// every thread of the workgroup receives the sum through LDS. v must hold contract results.
+template <bool SQUARE>
+__device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) {
+  __syncthreads();  // v complete
+  if (threadIdx.x < 16) {
+    const int l = threadIdx.x;
+    float acc = 0.0f;
+    int j0 = 0;
+    for (; j0 + 16 * 8 <= n; j0 += 16 * 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = SQUARE ? fmul(v[j0 + l + 16 * u], v[j0 + l + 16 * u]) : v[j0 + l + 16 * u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = fadd_chain(acc, t[u]);
+    }
+    for (int j = j0 + l; j < n; j += 16) acc = fadd_chain(acc, SQUARE ? fmul(v[j], v[j]) : v[j]);
+    acc = fold16(acc);
+    if (l == 0) *bcast = acc;
+  }
+  __syncthreads();
+  return *bcast;
+}
+
+// Rows up to kLdsRow elements: one workgroup per row, the row staged in LDS; the elementwise work
+// (exp, differences, squares, outputs) spread over all 256 threads, only the fixed-order sums on
+// 16 lanes (golden.py:358-380; numerics.py:328-380).
+constexpr int kLdsRow = 12288;
+
+__global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
+  __shared__ float v[kLdsRow];
+  __shared__ uint32_t red[kRowThreads / 64 + 1];
+  __shared__ float bcast;
+  const int m = blockIdx.x;
+  const float* x = frow(a.x, a.lda, m);
+  const int N = a.N, t = threadIdx.x;
+  const int64_t yrow = m * a.ldy;
+  for (int j = t; j < N; j += kRowThreads) v[j] = ftz(x[j]);
+  if (a.fn == ROWFN_SOFTMAX) {
+    const int V = a.valid ? min(max(a.valid[m], 1), N) : (a.causal_k > 0 ? min(N, a.causal_k + m) : N);
+    __syncthreads();
+    uint32_t key = 0;
+    int nan = 0;
+    for (int j = t; j < V; j += kRowThreads) {
+      if (is_nan(v[j])) nan = 1;
+      else key = max(key, fmax_key(v[j]));
+    }
+    key = static_cast<uint32_t>(group_reduce<64>(static_cast<int>(key), OpMaxU{}));
+    nan = group_reduce<64>(nan, OpOr{});
+    if ((t & 63) == 0) red[t >> 6] = nan ? 0xFFFFFFFFu : key;  // NaN: a key no value has
+    __syncthreads();
+    uint32_t k = 0;
+#pragma unroll
+    for (int w = 0; w < kRowThreads / 64; ++w) k = max(k, red[w]);
+    const float nmx = fneg(k == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k));
+    __syncthreads();  // every thread has read red before v is rewritten
+    for (int j = t; j < N; j += kRowThreads) v[j] = j < V ? exp_f(fadd(v[j], nmx)) : 0.0f;
+    const float r = recip_f(lds_sum16<false>(v, N, &bcast));
+    for (int j = t; j < N; j += kRowThreads) store_out(a.y, yrow, j, a.out, fmul(v[j], r), a.out_scale);
+    return;
+  }
+  const float kinv = recip_f(i2f(N));
+  float rs;
+  if (a.fn == ROWFN_LAYERNORM) {
+    const float nmean = fneg(fmul(lds_sum16<false>(v, N, &bcast), kinv));
+    for (int j = t; j < N; j += kRowThreads) v[j] = fadd(v[j], nmean);  // d = x + -mean
+    rs = rsqrt_f(fadd(fmul(lds_sum16<true>(v, N, &bcast), kinv), a.eps));
+  } else {
+    const float ss = lds_sum16<true>(v, N, &bcast);
+    rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, a.eps));
+  }
+  for (int j = t; j < N; j += kRowThreads) {
+    float y = fmul(fmul(v[j], rs), a.gamma[j]);
+    if (a.beta) y = fadd(y, a.beta[j]);
+    store_out(a.y, yrow, j, a.out, y, a.out_scale);
+  }
+}
+
+// Longer rows: one 16-lane group per row, the lane's elements streamed in blocks.
 __global__ __launch_bounds__(kRowThreads) void row_kernel(RowArgs a) {
   const int m = blockIdx.x * (kRowThreads / 16) + static_cast<int>(threadIdx.x >> 4);
   const int l = threadIdx.x & 15;
@@ -51,19 +177,20 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(RowArgs a) {
     const int V = a.valid ? min(max(a.valid[m], 1), N) : (a.causal_k > 0 ? min(N, a.causal_k + m) : N);
     uint32_t key = 0;
     int nan = 0;
-    for (int j = l; j < V; j += 16) {
-      const float v = ftz(x[j]);
+    for_lane(x, l, V, [&](int, float xv) {
+      const float v = ftz(xv);
       if (is_nan(v)) nan = 1;
       else key = max(key, fmax_key(v));
-    }
+    });
     key = static_cast<uint32_t>(group_reduce<16>(static_cast<int>(key), OpMaxU{}));
     nan = group_reduce<16>(nan, OpOr{});
     const float nmx = fneg(nan ? ffrom(kCanonNaN) : fmax_from_key(key));
     float acc = 0.0f;
-    for (int j = l; j < N; j += 16) acc = fadd(acc, j < V ? exp_f(fadd(x[j], nmx)) : 0.0f);
+    for_lane(x, l, N, [&](int j, float xv) { acc = fadd(acc, j < V ? exp_f(fadd(xv, nmx)) : 0.0f); });
     const float r = recip_f(fold16(acc));
-    for (int j = l; j < N; j += 16)
-      store_out(a.y, yrow, j, a.out, fmul(j < V ? exp_f(fadd(x[j], nmx)) : 0.0f, r), a.out_scale);
+    for_lane(x, l, N, [&](int j, float xv) {
+      store_out(a.y, yrow, j, a.out, fmul(j < V ? exp_f(fadd(xv, nmx)) : 0.0f, r), a.out_scale);
+    });
     return;
   }
   float rs;
@@ -71,26 +198,27 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(RowArgs a) {
   const float k = recip_f(i2f(N));
   if (a.fn == ROWFN_LAYERNORM) {
     float acc = 0.0f;
-    for (int j = l; j < N; j += 16) acc = fadd(acc, x[j]);
+    for_lane(x, l, N, [&](int, float xv) { acc = fadd(acc, xv); });
     nmean = fneg(fmul(fold16(acc), k));
     float acc2 = 0.0f;
-    for (int j = l; j < N; j += 16) {
-      const float d = fadd(x[j], nmean);
+    for_lane(x, l, N, [&](int, float xv) {
+      const float d = fadd(xv, nmean);
       acc2 = fadd(acc2, fmul(d, d));
-    }
+    });
     rs = rsqrt_f(fadd(fmul(fold16(acc2), k), a.eps));
   } else {
     float acc = 0.0f;
-    for (int j = l; j < N; j += 16) acc = fadd(acc, fmul(x[j], x[j]));
+    for_lane(x, l, N, [&](int, float xv) { acc = fadd(acc, fmul(xv, xv)); });
     const float ss = fold16(acc);
     rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, k) : ss, a.eps));
   }
-  for (int j = l; j < N; j += 16) {
-    const float d = a.fn == ROWFN_LAYERNORM ? fadd(x[j], nmean) : ftz(x[j]);
+  const bool ln = a.fn == ROWFN_LAYERNORM;
+  for_lane(x, l, N, [&](int j, float xv) {
+    const float d = ln ? fadd(xv, nmean) : ftz(xv);
     float y = fmul(fmul(d, rs), a.gamma[j]);
     if (a.beta) y = fadd(y, a.beta[j]);
     store_out(a.y, yrow, j, a.out, y, a.out_scale);
-  }
+  });
 }
 
 // ------------------------------------------------------------------------------ elementwise
@@ -149,7 +277,23 @@ __global__ __launch_bounds__(256) void relu_kernel(ReluArgs a) {
 }
 
 // ------------------------------------------------------------------------------ fp32 dots
-// numerics.py:393-399: y[m][n] = sum16_k a[m][k] * b[n][k]; one 16-lane group per output.
+// numerics.py:393-399: y[m][n] = sum16_k a[m][k] * b[n][k]; one 16-lane group per output. Lane l's
+// chain (k = l, l + 16, ...) consumes blocks of kNtChunk products whose loads were issued one block
+// ahead.
+constexpr int kNtChunk = 8;
+
+struct NtBlock {
+  float a[kNtChunk], b[kNtChunk];
+  __device__ __forceinline__ void load(const float* ar, const float* br, int k0, int l, int K) {
+#pragma unroll
+    for (int u = 0; u < kNtChunk; ++u) {
+      const int k = k0 + l + 16 * u;
+      a[u] = load_pred(ar + k, ar, k < K, 0.0f);
+      b[u] = load_pred(br + k, br, k < K, 0.0f);
+    }
+  }
+};
+
 __global__ __launch_bounds__(256) void fdot_nt_kernel(FdotArgs a) {
   const int n = blockIdx.x * 16 + static_cast<int>(threadIdx.x >> 4);
   const int l = threadIdx.x & 15;
@@ -158,38 +302,102 @@ __global__ __launch_bounds__(256) void fdot_nt_kernel(FdotArgs a) {
   for (int m = blockIdx.y; m < a.M; m += gridDim.y) {
     const float* ar = frow(a.A, a.lda, m);
     float acc = 0.0f;
-    int k = l;
-    for (; k + 48 < a.K; k += 64) {  // four chain steps with their loads issued together
-      const float p0 = fmul(ar[k], br[k]), p1 = fmul(ar[k + 16], br[k + 16]);
-      const float p2 = fmul(ar[k + 32], br[k + 32]), p3 = fmul(ar[k + 48], br[k + 48]);
-      acc = fadd(fadd(fadd(fadd(acc, p0), p1), p2), p3);
+    NtBlock cur, nxt;
+    cur.load(ar, br, 0, l, a.K);
+    for (int k0 = 0; k0 < a.K; k0 += 16 * kNtChunk) {
+      if (k0 + 16 * kNtChunk < a.K) nxt.load(ar, br, k0 + 16 * kNtChunk, l, a.K);
+#pragma unroll
+      for (int u = 0; u < kNtChunk; ++u)
+        if (k0 + l + 16 * u < a.K) acc = fadd_chain(acc, fmul(cur.a[u], cur.b[u]));
+      cur = nxt;
     }
-    for (; k < a.K; k += 16) acc = fadd(acc, fmul(ar[k], br[k]));
     const float y = fold16(acc);
     if (l == 0) store_out(a.Y, m * a.ldy, n, a.out, y, a.out_scale);
   }
 }
 
-// numerics.py:402-409: y[m][n] = ((+0 + a[m][0] b[0][n]) + a[m][1] b[1][n]) + ...; one lane per
-// output, columns n across the lanes (b rows read coalesced; a[m][k] is the same for the wave's
-// lanes of one m).
+// numerics.py:402-409: y[m][n] = ((+0 + a[m][0] b[0][n]) + a[m][1] b[1][n]) + ...: one sequential
+// k chain per output. A workgroup owns 128 columns; all 256 threads stage B in LDS in blocks of
+// kNnRows rows (fp16 widened to fp32 on the way), the next block's global loads in flight while
+// the 128 chain threads consume the current one from LDS.
+constexpr int kNnCols = 128, kNnRows = 56;
+constexpr int kNnPer = kNnRows * kNnCols / 4 / 256;  // 4-element groups per thread per block (7)
+static_assert(kNnRows * kNnCols / 4 % 256 == 0 && kNnRows <= 256, "block shape");
+
+template <bool HALF>
+struct NnStage {
+  float4 r[kNnPer];
+  float a;
+  __device__ __forceinline__ void load(const FdotArgs& f, const float* ar, int k0, int c0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kNnPer; ++u) {
+      const int e = t + 256 * u, row = e / (kNnCols / 4), c = c0 + 4 * (e % (kNnCols / 4));
+      const int k = k0 + row;
+      const bool ok = k < f.K && c < f.N;  // N % 4 == 0 is not required: a partial group is zero-filled
+      const char* rowp = static_cast<const char*>(f.B) + static_cast<int64_t>(ok ? k : 0) * f.ldb;
+      if constexpr (HALF) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(rowp);
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (ok && c + q < f.N) ? from_fp16_bits(h[c + q]) : 0.0f;
+        r[u] = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        const float* x = reinterpret_cast<const float*>(rowp);
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (ok && c + q < f.N) ? x[c + q] : 0.0f;
+        r[u] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+    a = (t < kNnRows && k0 + t < f.K) ? ar[k0 + t] : 0.0f;
+  }
+  __device__ __forceinline__ void store(float (*lb)[kNnCols], float* la) const {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kNnPer; ++u) {
+      const int e = t + 256 * u;
+      *reinterpret_cast<float4*>(&lb[e / (kNnCols / 4)][4 * (e % (kNnCols / 4))]) = r[u];
+    }
+    if (t < kNnRows) la[t] = a;
+  }
+};
+
 template <bool HALF>
 __global__ __launch_bounds__(256) void fdot_nn_kernel(FdotArgs a) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= a.N) return;
+  __shared__ __align__(16) float lb[2][kNnRows][kNnCols];
+  __shared__ float la[2][kNnRows];
+  const int c0 = blockIdx.x * kNnCols, t = threadIdx.x;
+  const int n = c0 + t;
+  const int nb = (a.K + kNnRows - 1) / kNnRows;
   for (int m = blockIdx.y; m < a.M; m += gridDim.y) {
     const float* ar = frow(a.A, a.lda, m);
+    NnStage<HALF> st;
+    st.load(a, ar, 0, c0);
+    __syncthreads();  // the previous row's chains are done with the buffers
+    st.store(lb[0], la[0]);
+    __syncthreads();
     float acc = 0.0f;
-    int k = 0;
-    for (; k + 8 <= a.K; k += 8) {
-      float p[8];
+    for (int b = 0; b < nb; ++b) {
+      if (b + 1 < nb) st.load(a, ar, (b + 1) * kNnRows, c0);
+      if (t < kNnCols) {
+        const int rows = min(kNnRows, a.K - b * kNnRows);
+        const float(*cb)[kNnCols] = lb[b & 1];
+        const float* ca = la[b & 1];
+        int kk = 0;
+        for (; kk + 8 <= rows; kk += 8) {
+          float p[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) p[u] = fmul(ar[k + u], load_f(a.B, a.ldb, k + u, n, HALF));
+          for (int u = 0; u < 8; ++u) p[u] = fmul(ca[kk + u], cb[kk + u][t]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc = fadd(acc, p[u]);
+          for (int u = 0; u < 8; ++u) acc = fadd_chain(acc, p[u]);
+        }
+        for (; kk < rows; ++kk) acc = fadd_chain(acc, fmul(ca[kk], cb[kk][t]));
+      }
+      if (b + 1 < nb) st.store(lb[(b + 1) & 1], la[(b + 1) & 1]);
+      __syncthreads();
     }
-    for (; k < a.K; ++k) acc = fadd(acc, fmul(ar[k], load_f(a.B, a.ldb, k, n, HALF)));
-    store_out(a.Y, m * a.ldy, n, a.out, acc, a.out_scale);
+    if (t < kNnCols && n < a.N) store_out(a.Y, m * a.ldy, n, a.out, chain_end(acc), a.out_scale);
   }
 }
 
@@ -201,7 +409,10 @@ dim3 row_grid(int M, int N, int per) {
 }  // namespace
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(row_kernel, dim3((a.M + 15) / 16), dim3(kRowThreads), 0, s, a);
+  if (a.N <= kLdsRow)
+    hipLaunchKernelGGL(row_lds_kernel, dim3(a.M), dim3(kRowThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(row_kernel, dim3((a.M + 15) / 16), dim3(kRowThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -224,9 +435,9 @@ hipError_t launch_fdot(const FdotArgs& a, hipStream_t s) {
   if (!a.nn) {
     hipLaunchKernelGGL(fdot_nt_kernel, row_grid(a.M, a.N, 16), dim3(256), 0, s, a);
   } else if (a.b_fp16) {
-    hipLaunchKernelGGL(fdot_nn_kernel<true>, row_grid(a.M, a.N, 256), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(fdot_nn_kernel<true>, row_grid(a.M, a.N, kNnCols), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL(fdot_nn_kernel<false>, row_grid(a.M, a.N, 256), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(fdot_nn_kernel<false>, row_grid(a.M, a.N, kNnCols), dim3(256), 0, s, a);
   }
   return hipGetLastError();
 }

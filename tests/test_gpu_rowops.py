@@ -70,7 +70,7 @@ def test_softmax_causal_reference_vectors(name):
 
 @pytest.mark.parametrize("out", OUTS)
 @pytest.mark.parametrize("M,N,k", [(1, 16, 0), (7, 80, 0), (16, 250, 0), (33, 512, 0), (16, 256, 5), (9, 96, 90),
-                                   (3, 4096, 0)])
+                                   (3, 4096, 0), (2, 12288, 0), (2, 13000, 7000)])
 def test_softmax_seeded(M, N, k, out):
     x = rows_with_specials(M * 7 + N, M, N, scale=4.0)
     osc = f32(3.0) if out == OUT_INT8 else None
@@ -95,7 +95,7 @@ def test_norm_reference_vectors(name, fn):
 
 @pytest.mark.parametrize("fn", ["ln", "rms", "l2"])
 @pytest.mark.parametrize("out", OUTS)
-@pytest.mark.parametrize("M,N", [(1, 1024), (6, 48), (40, 2560), (2, 10)])
+@pytest.mark.parametrize("M,N", [(1, 1024), (6, 48), (40, 2560), (2, 10), (2, 16400)])
 def test_norms_seeded(fn, out, M, N):
     rng = np.random.default_rng(zlib.crc32(repr((fn, out, M, N)).encode()))
     x = rows_with_specials(M + N, M, N)
