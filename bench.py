@@ -539,8 +539,11 @@ def attention_layers(torch, lib, gen, t0: int):
 
 
 def attention_decode(torch, lib, gen, t0: int = 250) -> dict:
-    """The decode attention of one token at t=250 over all 28 layers, op by op (48 launches per
-    layer), timed as one graph per token: us per layer and per token."""
+    """The decode attention of one token at t=250 over all 28 layers (16 query heads, 8 KV heads,
+    head dim 128, fp32 caches of pad16(t0 + 1) rows): op by op through the C ABI (48 launches per
+    layer, one graph per token), and as the reference's descriptor queue (1344 descriptors) through
+    the executor, whose attention fusion runs each layer's 16 head triples as one launch; us per
+    layer and per token."""
     layers, keep, nbytes = attention_layers(torch, lib, gen, t0)
     launches = [l for ls in layers for l in ls]
     g = capture(torch, launches)
@@ -552,7 +555,74 @@ def attention_decode(torch, lib, gen, t0: int = 250) -> dict:
          "layers": QWEN3_LAYERS, "cache_bytes_per_layer": nbytes}
     del layers, keep, launches
     torch.cuda.empty_cache()
+    r["executor"] = attention_queue(torch, lib, gen, t0)
     return r
+
+
+def attention_queue(torch, lib, gen, t0: int) -> dict:
+    """The same attention as descriptors in one device DDR image (per layer and head: FDOT_NT into
+    the shared scores, causal ROW_SOFTMAX into the shared probabilities, FDOT_NN into the head's
+    output columns, tars_mini/llm.py:736-746), run through tars_run_queue; host clock per token."""
+    from opentars_amd import _lib, contract as C
+    from opentars_amd.queue import encode_descriptor
+    nh, nkv, hd = QWEN3_HEADS, QWEN3_KV_HEADS, QWEN3_HEAD_DIM
+    nk = (t0 + 1 + 15) // 16 * 16
+    top = [0]
+
+    def take(n):
+        a = (top[0] + 255) // 256 * 256
+        top[0] = a + n
+        return a
+
+    descs, fills = [], []
+    for _ in range(QWEN3_LAYERS):
+        q, kc, vc = take(4 * nh * hd), take(4 * nk * nkv * hd), take(4 * nk * nkv * hd)
+        sc, pr, att = take(4 * nk), take(4 * nk), take(4 * nh * hd)
+        fills += [(q, nh * hd, 0.1), (kc, nk * nkv * hd, 1.0), (vc, nk * nkv * hd, 1.0)]
+        for h in range(nh):
+            kv = h // (nh // nkv)
+            descs.append(dict(OPCODE=C.OP_FDOT, EPI=C.epi(), A_OFF=q + 4 * h * hd, W_OFF=kc + 4 * kv * hd, Y_OFF=sc,
+                              M=1, N=nk, K=hd, GROUP_SIZE=4 * nkv * hd // 16))
+            descs.append(dict(OPCODE=C.OP_ROW, CTRL=C.ROW_SOFTMAX, EPI=C.epi(), A_OFF=sc, Y_OFF=pr, M=1, N=nk, K=t0 + 1))
+            descs.append(dict(OPCODE=C.OP_FDOT, CTRL=1, EPI=C.epi(), A_OFF=pr, W_OFF=vc + 4 * kv * hd,
+                              Y_OFF=att + 4 * h * hd, M=1, N=hd, K=nk, GROUP_SIZE=4 * nkv * hd // 16))
+    qaddr = take(64 * len(descs))
+    image = torch.zeros(top[0], dtype=torch.uint8, device="cuda")
+    for off, n, sd in fills:
+        image[off:off + 4 * n].view(torch.float32).copy_(torch.randn(n, device="cuda", generator=gen) * sd)
+    host_q = b"".join(encode_descriptor(dict(MAGIC=C.MAGIC, VERSION=C.VERSION, VALID=1, **d)) for d in descs)
+    image[qaddr:qaddr + len(host_q)].copy_(torch.frombuffer(bytearray(host_q), dtype=torch.uint8).cuda())
+    torch.cuda.synchronize()
+    st = _lib.QueueStatus()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        rc = lib.tars_run_queue(image.data_ptr(), image.numel(), qaddr, len(descs), host_q, 0, 0, ctypes.byref(st),
+                                stream)
+        if rc != 0 or not st.done:
+            raise RuntimeError(f"attention queue: status {rc} done={st.done} err={st.err_code} op={st.op_idx}: "
+                               f"{_lib.last_error()}")
+
+    res = {"descriptors": len(descs)}
+    for key, fusion, graphs, reps in (("fused_plans", 1, 1, 20), ("fused", 1, 0, 10), ("unfused_plans", 0, 1, 5)):
+        prev_f, prev_g = lib.tars_set_queue_fusion(fusion), lib.tars_set_queue_graphs(graphs)
+        try:
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            t_start = time.perf_counter()
+            for _ in range(reps):
+                run()
+            torch.cuda.synchronize()
+            t = (time.perf_counter() - t_start) / reps
+        finally:
+            lib.tars_set_queue_fusion(prev_f)
+            lib.tars_set_queue_graphs(prev_g)
+        res[key] = {"launches_per_token": QWEN3_LAYERS if fusion else len(descs), "us_per_token": round(t * 1e6, 1),
+                    "us_per_layer": round(t / QWEN3_LAYERS * 1e6, 2)}
+    del image
+    torch.cuda.empty_cache()
+    return res
 
 
 # ------------------------------------------------------------------------------ CPU baseline

@@ -255,26 +255,12 @@ hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
 // W is the MFMA's first operand, so lane l holds 4 consecutive columns of row l % 16) with a 4-wide
 // store. K blocks (a K split) run one after another through the same pipeline, their fp32
 // partials added in block order.
-#define TARS_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-// One 1 KiB block: lane l's 16 bytes at src land at dst + 16 l (dst is wave-uniform).
-__device__ __forceinline__ void stage16(const void* src, int8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, TARS_LDS(dst), 16, 0, 0);
-}
-
 // Stage st of this wave's L blocks into its ring slot (st % S).
 template <int L, int NW, int KS, int S>
 __device__ __forceinline__ void issue_stage(int8_t* lds, const int8_t* const (&src)[L], int wave, int st) {
   int8_t* slot = lds + 1024 * NW * L * (st % S);
 #pragma unroll
   for (int u = 0; u < L; ++u) stage16(src[u] + static_cast<int64_t>(KS) * st, slot + 1024 * (wave + u * NW));
-}
-
-// s_waitcnt vmcnt(N) with the other counters left alone.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 template <int BM, int BN, int WM, int WN, int KS, int S>

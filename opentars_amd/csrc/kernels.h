@@ -25,6 +25,22 @@ __device__ __forceinline__ T load_stream_pred(const T* p, const T* safe, bool pr
   return pred ? v : zero;
 }
 
+// Direct global -> LDS loads (global_load_lds_dwordx4): 64 lanes x 16 bytes land in a 1 KiB LDS
+// block in lane order with no VGPR round trip (lane l's bytes at dst + 16 l; dst is wave-uniform).
+// The loads count in vmcnt like any other vector load; wait_vmcnt<N> waits until at most N of this
+// wave's vector loads are outstanding.
+#define TARS_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+__device__ __forceinline__ void stage16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, TARS_LDS(dst), 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Keeps the machine scheduler from moving instructions across this point. Used between groups of
 // loads whose issue order matters for the wait counters (activations before weights before
 // epilogue operands).
@@ -187,6 +203,28 @@ struct FdotArgs {
   float out_scale;
   int M, N, K;
 };
+
+// Decode attention of up to kAttnMaxHeads query heads in one launch, the fusion of the reference's
+// per-head FDOT_NT (scores) -> ROW_SOFTMAX (causal) -> FDOT_NN (P V) triple
+// (tars_mini/llm.py:736-746), bit-identical to running the three ops per head in order: every
+// head's scores, probabilities and outputs are the golden's, and the scores and probabilities of
+// the last head are written to sc / pr (the buffers all heads share).
+constexpr int kAttnMaxHeads = 32, kAttnMaxKeys = 4080;  // 4080 keys: the scores row and the V ring fit 64 KiB of LDS
+struct AttnArgs {
+  const float* q[kAttnMaxHeads];   // head h: query rows [M, hd] at ldq
+  const float* k[kAttnMaxHeads];   // K rows [nk, hd] at ldk (fp32)
+  const void* v[kAttnMaxHeads];    // V rows [nk, hd] at ldv (fp32, or fp16 when v_fp16)
+  void* att[kAttnMaxHeads];        // output rows [M, hd] at ldatt, format out
+  int64_t ldq, ldk, ldv, ldatt;
+  float* sc;                       // [M, nk] at ldsc: the last head's scores (fp32)
+  int64_t ldsc;
+  float* pr;                       // [M, nk] at ldpr: the last head's probabilities (fp32)
+  int64_t ldpr;
+  int heads, M, nk, hd, causal_k, v_fp16, out;
+  float out_scale;
+};
+bool attention_supported(int hd, int nk);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s);
 hipError_t launch_elt(const EltArgs& a, hipStream_t s);

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/opentars_amd.h"
+#include "kernels.h"
 
 namespace {
 
@@ -547,6 +548,151 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
   return rc;
 }
 
+// Attention fusion: a run of per-head triples FDOT_NT (scores) -> ROW_SOFTMAX -> FDOT_NN (P V), the
+// reference's decode/prefill attention lowering (tars_mini/llm.py:736-746), runs as one launch of
+// the fused attention kernel, all heads at once. Each triple must read its softmax input from the
+// NT output and its NN input from the softmax output, every head the same shapes and the same
+// score / probability buffers; no head may read (q, K, V) what any head writes, and the heads'
+// outputs must not overlap each other or the rest of the queue. The heads then do not interact, so
+// running them concurrently (the last head writing the shared buffers) leaves the image exactly as
+// the triples run one after another.
+struct AttnHead {
+  Desc nt, sm, nn;
+};
+
+Segs merged(std::vector<Seg> v) {
+  std::sort(v.begin(), v.end(), [](const Seg& a, const Seg& b) { return a.lo < b.lo; });
+  Segs out;
+  for (const Seg& x : v) {
+    if (!out.empty() && x.lo <= out.back().hi) out.back().hi = std::max(out.back().hi, x.hi);
+    else out.push_back(x);
+  }
+  return out;
+}
+
+bool pairwise_disjoint(std::vector<Seg> v) {
+  std::sort(v.begin(), v.end(), [](const Seg& a, const Seg& b) { return a.lo < b.lo; });
+  for (size_t i = 1; i < v.size(); ++i)
+    if (v[i].lo < v[i - 1].hi) return false;
+  return true;
+}
+
+tars::AttnArgs attention_args(uint8_t* image, const std::vector<AttnHead>& heads) {
+  tars::AttnArgs a{};
+  const Desc& nt0 = heads[0].nt;
+  const Desc& sm0 = heads[0].sm;
+  const Desc& nn0 = heads[0].nn;
+  for (size_t h = 0; h < heads.size(); ++h) {
+    const Desc& nt = heads[h].nt;
+    const Desc& nn = heads[h].nn;
+    a.q[h] = reinterpret_cast<const float*>(image + nt[F_BASE_ADDR] + nt[F_A_OFF]);
+    a.k[h] = reinterpret_cast<const float*>(image + nt[F_BASE_ADDR] + nt[F_W_OFF]);
+    a.v[h] = image + nn[F_BASE_ADDR] + nn[F_W_OFF];
+    a.att[h] = image + nn[F_BASE_ADDR] + nn[F_Y_OFF];
+  }
+  a.ldq = static_cast<int64_t>(strides(nt0).lda);
+  a.ldk = static_cast<int64_t>(b_stride(nt0).first);
+  a.ldv = static_cast<int64_t>(b_stride(nn0).first);
+  a.ldatt = static_cast<int64_t>(strides(nn0).ldy);
+  a.sc = reinterpret_cast<float*>(image + nt0[F_BASE_ADDR] + nt0[F_Y_OFF]);
+  a.ldsc = static_cast<int64_t>(strides(nt0).ldy);
+  a.pr = reinterpret_cast<float*>(image + sm0[F_BASE_ADDR] + sm0[F_Y_OFF]);
+  a.ldpr = static_cast<int64_t>(strides(sm0).ldy);
+  a.heads = static_cast<int>(heads.size());
+  a.M = static_cast<int>(nt0[F_M]);
+  a.nk = static_cast<int>(nt0[F_N]);
+  a.hd = static_cast<int>(nt0[F_K]);
+  a.causal_k = static_cast<int>(sm0[F_K]);
+  a.v_fp16 = (nn0[F_HDR_RSV] & kStateFp16) ? 1 : 0;
+  a.out = static_cast<int>(out_code(nn0[F_EPI]));
+  const uint32_t osc = static_cast<uint32_t>(nn0[F_OUT_SCALE]);
+  std::memcpy(&a.out_scale, &osc, 4);
+  return a;
+}
+
+int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, hipStream_t s) {
+  const tars::AttnArgs a = attention_args(image, heads);
+  const hipError_t e = tars::launch_attention(a, s);
+  if (e != hipSuccess) {
+    tars::set_last_error(std::string("HIP launch failed: ") + hipGetErrorString(e));
+    return TARS_E_DEVICE;
+  }
+  return TARS_OK;
+}
+
+// Whether descriptors (nt, sm, nn) form one head's triple the fused kernel runs.
+bool attention_triple(const Checked& nt, const Checked& sm, const Checked& nn, uintptr_t image) {
+  const Desc& a = nt.d;
+  const Desc& b = sm.d;
+  const Desc& c = nn.d;
+  for (const Checked* x : {&nt, &sm, &nn})
+    if (x->err != E_OK || x->overlap || (image + x->d[F_BASE_ADDR]) % 16) return false;
+  if (a[F_OPCODE] != OP_FDOT || (a[F_CTRL] & 1) || out_code(a[F_EPI]) != OUT_FP32) return false;
+  if (b[F_OPCODE] != OP_ROW || (b[F_CTRL] & 7) != ROW_SOFTMAX || out_code(b[F_EPI]) != OUT_FP32) return false;
+  if (c[F_OPCODE] != OP_FDOT || !(c[F_CTRL] & 1)) return false;
+  if (!tars::attention_supported(static_cast<int>(a[F_K]), static_cast<int>(a[F_N]))) return false;
+  const uint64_t M = a[F_M], nk = a[F_N], hd = a[F_K];
+  if (b[F_M] != M || b[F_N] != nk || c[F_M] != M || c[F_K] != nk || c[F_N] != hd) return false;
+  if (addr(b, F_A_OFF) != addr(a, F_Y_OFF) || strides(b).lda != strides(a).ldy) return false;
+  if (addr(c, F_A_OFF) != addr(b, F_Y_OFF) || strides(c).lda != strides(b).ldy) return false;
+  return true;
+}
+
+int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
+                   int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
+                   int& fused, std::vector<AttnHead>& group) {
+  fused = 0;
+  group.clear();
+  if (!g_fusion || first.d[F_OPCODE] != OP_FDOT || (first.d[F_CTRL] & 1)) return TARS_OK;
+  const uintptr_t img = reinterpret_cast<uintptr_t>(image);
+  std::vector<Seg> ins, outs, atts;
+  Segs sc_y, pr_y;
+  for (int32_t j = i; j + 2 < n && static_cast<uint64_t>(j + 2) < in_image &&
+                      group.size() < static_cast<size_t>(tars::kAttnMaxHeads);
+       j += 3) {
+    const Checked nt = j == i ? first : check(q.data() + static_cast<size_t>(j) * kDescBytes, image_len, core_id, gemv_only);
+    const Checked sm = check(q.data() + static_cast<size_t>(j + 1) * kDescBytes, image_len, core_id, gemv_only);
+    const Checked nn = check(q.data() + static_cast<size_t>(j + 2) * kDescBytes, image_len, core_id, gemv_only);
+    if (!attention_triple(nt, sm, nn, img)) break;
+    if (!group.empty()) {  // the same shapes, formats and shared buffers as the first head
+      const AttnHead& h0 = group[0];
+      if (nt.d[F_M] != h0.nt[F_M] || nt.d[F_N] != h0.nt[F_N] || nt.d[F_K] != h0.nt[F_K] ||
+          sm.d[F_K] != h0.sm[F_K] || addr(nt.d, F_Y_OFF) != addr(h0.nt, F_Y_OFF) ||
+          strides(nt.d).ldy != strides(h0.nt).ldy || addr(sm.d, F_Y_OFF) != addr(h0.sm, F_Y_OFF) ||
+          strides(sm.d).ldy != strides(h0.sm).ldy || strides(nt.d).lda != strides(h0.nt).lda ||
+          b_stride(nt.d).first != b_stride(h0.nt).first || b_stride(nn.d).first != b_stride(h0.nn).first ||
+          strides(nn.d).ldy != strides(h0.nn).ldy || nn.d[F_HDR_RSV] != h0.nn[F_HDR_RSV] ||
+          nn.d[F_EPI] != h0.nn[F_EPI] || nn.d[F_OUT_SCALE] != h0.nn[F_OUT_SCALE])
+        break;
+    } else {
+      sc_y = nt.y;
+      pr_y = sm.y;
+    }
+    for (const Segs& r : nt.reads) ins.insert(ins.end(), r.begin(), r.end());  // q and K
+    const Desc& c = nn.d;
+    const Segs vrows = strided(addr(c, F_W_OFF), b_stride(c).first, c[F_K], b_stride(c).second);
+    ins.insert(ins.end(), vrows.begin(), vrows.end());
+    atts.insert(atts.end(), nn.y.begin(), nn.y.end());
+    group.push_back(AttnHead{nt.d, sm.d, nn.d});
+  }
+  if (group.empty()) return TARS_OK;
+  outs = atts;
+  outs.insert(outs.end(), sc_y.begin(), sc_y.end());
+  outs.insert(outs.end(), pr_y.begin(), pr_y.end());
+  std::vector<Seg> sp = sc_y;
+  sp.insert(sp.end(), pr_y.begin(), pr_y.end());
+  sp.insert(sp.end(), atts.begin(), atts.end());
+  const Segs all_out = merged(outs);
+  if (!pairwise_disjoint(sp) || overlaps(merged(ins), all_out) ||
+      (rest_lo < rest_hi && overlaps(Segs{{rest_lo, rest_hi}}, all_out))) {
+    group.clear();
+    return TARS_OK;
+  }
+  const int rc = launch_attention_group(image, group, s);
+  if (rc == TARS_OK) fused = static_cast<int>(group.size());
+  return rc;
+}
+
 // ---------------------------------------------------------------------------- launch plans
 // A decode loop runs the same descriptor bytes every token. A queue that ran to the end with no
 // hand-off and no output over its own descriptors leaves a plan (its launches in order, with the
@@ -558,6 +704,7 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
 struct Step {
   Desc d;                   // the descriptor (the quantizer of a fused group)
   std::vector<Desc> group;  // the GEMMs fused with it (empty: a single launch)
+  std::vector<AttnHead> attn;  // or: the heads of a fused attention launch
 };
 
 struct Plan {
@@ -581,7 +728,9 @@ bool g_graphs = true;
 int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) {
   for (const Step& st : steps) {
     bool needs_host = false;
-    const int rc = st.group.empty() ? launch(image, st.d, s, needs_host) : launch_fused(image, st.d, st.group, s);
+    const int rc = !st.attn.empty()   ? launch_attention_group(image, st.attn, s)
+                   : st.group.empty() ? launch(image, st.d, s, needs_host)
+                                      : launch_fused(image, st.d, st.group, s);
     if (rc != TARS_OK) return rc;
   }
   return TARS_OK;
@@ -739,8 +888,17 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
                             group))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
-      if (cacheable) steps.push_back(Step{c.d, std::move(group)});
+      if (cacheable) steps.push_back(Step{c.d, std::move(group), {}});
       i += fused;  // the quantizer and `fused` GEMMs ran as one launch
+      continue;
+    }
+    std::vector<AttnHead> heads;
+    if (int rc = fuse_attention(image, c, q, i, in_image, n, static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) *
+                                (static_cast<uint64_t>(i) + 3), q_end, image_len, core_id, gemv_only != 0, s, fused, heads))
+      return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+    if (fused) {
+      if (cacheable) steps.push_back(Step{c.d, {}, std::move(heads)});
+      i += 3 * fused - 1;  // `fused` heads of three descriptors ran as one launch
       continue;
     }
     bool needs_host = false;
@@ -751,7 +909,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       st->host_op = 1;
       return TARS_OK;
     }
-    if (cacheable) steps.push_back(Step{c.d, {}});
+    if (cacheable) steps.push_back(Step{c.d, {}, {}});
     // an output written over a later descriptor of this queue: wait for it and read them again
     const Segs rest = {{later, q_end}};
     if (later < q_end && (overlaps(rest, c.y) || (!c.extra.empty() && overlaps(rest, c.extra)))) {

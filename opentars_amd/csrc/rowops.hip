@@ -401,6 +401,143 @@ __global__ __launch_bounds__(256) void fdot_nn_kernel(FdotArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------ fused decode attention
+// One workgroup per query head: (1) the scores s[j] = sum16_k q[k] K[j][k] for every key (16-lane
+// groups, kAttnKeysInFlight keys per group with their K rows loaded together and their chains
+// interleaved), kept in LDS; (2) the causal softmax over them in place (as row_lds_kernel); (3) the
+// P V chains over V staged in LDS by direct global -> LDS loads in a ring of kAttnSlots stages.
+// Each step is the contract's, in the same order as the three separate ops, so every value is the
+// same bit for bit; the last head also writes its scores and probabilities where the reference's
+// ops leave them.
+constexpr int kAttnKeysInFlight = 8, kAttnSlots = 3, kAttnStageBytes = 16384;
+
+template <int HD, bool VHALF>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  constexpr int U = HD / 16;                                  // elements per lane of a key row
+  constexpr int ES = VHALF ? 2 : 4;
+  constexpr int ROWB = HD * ES;                               // bytes of one V row
+  constexpr int SR = kAttnStageBytes / ROWB;                  // V rows per stage
+  constexpr int IPS = kAttnStageBytes / 1024;                 // 1 KiB loads per stage (16)
+  constexpr int L = IPS / 4;                                  // per wave (4)
+  static_assert(ROWB <= 1024 && 1024 % ROWB == 0 && IPS % 4 == 0, "attention shape");
+  __shared__ float sp[kAttnMaxKeys];
+  __shared__ __align__(16) int8_t ring[kAttnSlots * kAttnStageBytes];
+  __shared__ uint32_t red[4];
+  __shared__ float bcast;
+  const int h = blockIdx.x, t = threadIdx.x, g = t >> 4, l = t & 15, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const bool last = h == a.heads - 1;
+  const int nk = a.nk;
+  const int NS = (nk + SR - 1) / SR;
+  for (int m = 0; m < a.M; ++m) {
+    // (1) scores
+    const float* qr = frow(a.q[h], a.ldq, m);
+    float qv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) qv[u] = qr[l + 16 * u];
+    for (int j0 = g; j0 < nk; j0 += 16 * kAttnKeysInFlight) {
+      float kv[kAttnKeysInFlight][U];
+#pragma unroll
+      for (int c = 0; c < kAttnKeysInFlight; ++c) {
+        const int j = min(j0 + 16 * c, nk - 1);  // clamped: a key past the end is computed and dropped
+        const float* kr = frow(a.k[h], a.ldk, j);
+#pragma unroll
+        for (int u = 0; u < U; ++u) kv[c][u] = kr[l + 16 * u];
+      }
+      float acc[kAttnKeysInFlight];
+#pragma unroll
+      for (int c = 0; c < kAttnKeysInFlight; ++c) acc[c] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int c = 0; c < kAttnKeysInFlight; ++c) acc[c] = fadd_chain(acc[c], fmul(qv[u], kv[c][u]));
+#pragma unroll
+      for (int c = 0; c < kAttnKeysInFlight; ++c) {
+        const float sv = fold16(acc[c]);
+        const int j = j0 + 16 * c;
+        if (l == 0 && j < nk) {
+          sp[j] = sv;
+          if (last && a.sc) store_out(a.sc, m * a.ldsc, j, 0, sv, 0.0f);
+        }
+      }
+    }
+    // (2) causal softmax in place
+    const int V = a.causal_k > 0 ? min(nk, a.causal_k + m) : nk;
+    __syncthreads();
+    uint32_t key = 0;
+    int nan = 0;
+    for (int j = t; j < V; j += 256) {
+      if (is_nan(sp[j])) nan = 1;
+      else key = max(key, fmax_key(sp[j]));
+    }
+    key = static_cast<uint32_t>(group_reduce<64>(static_cast<int>(key), OpMaxU{}));
+    nan = group_reduce<64>(nan, OpOr{});
+    if (lane == 0) red[t >> 6] = nan ? 0xFFFFFFFFu : key;
+    __syncthreads();
+    const uint32_t k4 = max(max(red[0], red[1]), max(red[2], red[3]));
+    const float nmx = fneg(k4 == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k4));
+    __syncthreads();
+    for (int j = t; j < nk; j += 256) sp[j] = j < V ? exp_f(fadd(sp[j], nmx)) : 0.0f;
+    const float r = recip_f(lds_sum16<false>(sp, nk, &bcast));
+    for (int j = t; j < nk; j += 256) {
+      const float p = fmul(sp[j], r);
+      sp[j] = p;
+      if (last && a.pr) store_out(a.pr, m * a.ldpr, j, 0, p, 0.0f);
+    }
+    wait_vmcnt<0>();  // no earlier vector memory operation outstanding before the ring's counts
+    __syncthreads();
+    // (3) P V over the V ring
+    const char* vbase = static_cast<const char*>(a.v[h]);
+    auto issue = [&](int st) __device__ {
+      int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
+#pragma unroll
+      for (int u = 0; u < L; ++u) {
+        const int i = wave + 4 * u;
+        const int byte = i * 1024 + lane * 16;
+        const int row = min(st * SR + byte / ROWB, nk - 1);
+        stage16(vbase + static_cast<int64_t>(row) * a.ldv + byte % ROWB, slot + i * 1024);
+      }
+    };
+#pragma unroll
+    for (int st = 0; st < kAttnSlots - 1; ++st)
+      if (st < NS) issue(st);
+    float acc = 0.0f;
+    for (int st = 0; st < NS; ++st) {
+      if (st + kAttnSlots - 1 < NS) {
+        issue(st + kAttnSlots - 1);
+        wait_vmcnt<L * (kAttnSlots - 1)>();
+      } else if (st + 1 < NS) {
+        wait_vmcnt<L>();  // one later stage issued (kAttnSlots == 3)
+      } else {
+        wait_vmcnt<0>();
+      }
+      __builtin_amdgcn_s_barrier();
+      if (t < HD) {
+        const int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
+        const float* ps = sp + st * SR;
+        const int rows = min(SR, nk - st * SR);
+        auto vval = [&](int rr) {
+          return VHALF ? from_fp16_bits(reinterpret_cast<const uint16_t*>(slot + rr * ROWB)[t])
+                       : reinterpret_cast<const float*>(slot + rr * ROWB)[t];
+        };
+        int rr = 0;
+        for (; rr + 8 <= rows; rr += 8) {  // the block's LDS reads and products first, then its chain steps
+          float pv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) pv[u] = fmul(ps[rr + u], vval(rr + u));
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc = fadd_chain(acc, pv[u]);
+        }
+        for (; rr < rows; ++rr) acc = fadd_chain(acc, fmul(ps[rr], vval(rr)));
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot are done
+      __builtin_amdgcn_s_barrier();
+    }
+    if (t < HD) store_out(a.att[h], m * a.ldatt, t, a.out, chain_end(acc), a.out_scale);
+    __syncthreads();  // sp and the ring are free for the next row
+  }
+}
+
 // Columns over grid x (per / threads each), rows over grid y with a stride loop past 65535 rows.
 dim3 row_grid(int M, int N, int per) {
   return dim3(static_cast<unsigned>((N + per - 1) / per), static_cast<unsigned>(M < 65535 ? M : 65535));
@@ -438,6 +575,29 @@ hipError_t launch_fdot(const FdotArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(fdot_nn_kernel<true>, row_grid(a.M, a.N, kNnCols), dim3(256), 0, s, a);
   } else {
     hipLaunchKernelGGL(fdot_nn_kernel<false>, row_grid(a.M, a.N, kNnCols), dim3(256), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tars
+
+namespace tars {
+
+bool attention_supported(int hd, int nk) {
+  return (hd == 64 || hd == 128 || hd == 256) && nk >= 1 && nk <= kAttnMaxKeys;
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+  const dim3 grid(a.heads), block(256);
+  if (a.hd == 64) {
+    if (a.v_fp16) hipLaunchKernelGGL((attn_kernel<64, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<64, false>), grid, block, 0, s, a);
+  } else if (a.hd == 128) {
+    if (a.v_fp16) hipLaunchKernelGGL((attn_kernel<128, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<128, false>), grid, block, 0, s, a);
+  } else {
+    if (a.v_fp16) hipLaunchKernelGGL((attn_kernel<256, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<256, false>), grid, block, 0, s, a);
   }
   return hipGetLastError();
 }

@@ -26,16 +26,17 @@ class Program:
     """A DDR image under construction: data regions allocated upward from 0x1000, descriptors
     collected in order."""
 
-    def __init__(self, seed: int, image: int = IMAGE):
+    def __init__(self, seed: int, image: int = IMAGE, qaddr: int = QADDR):
         self.rng = np.random.default_rng(seed)
         self.ddr = bytearray(image)
+        self.qaddr = qaddr
         self.top = 0x1000
         self.descs: list[bytes] = []
 
     def alloc(self, nbytes: int, align: int = 16) -> int:
         a = (self.top + align - 1) // align * align
         self.top = a + nbytes + 16 * int(self.rng.integers(0, 3))
-        assert self.top < QADDR
+        assert self.top < self.qaddr
         return a
 
     def put(self, data: bytes, align: int = 16) -> int:
@@ -49,7 +50,7 @@ class Program:
     def image(self) -> bytearray:
         img = bytearray(self.ddr)
         for i, d in enumerate(self.descs):
-            img[QADDR + 64 * i:QADDR + 64 * (i + 1)] = d
+            img[self.qaddr + 64 * i:self.qaddr + 64 * (i + 1)] = d
         return img
 
 
@@ -300,11 +301,11 @@ def random_program(seed: int) -> Program:
     return p
 
 
-def both(img: bytearray, n: int, **kw):
+def both(img: bytearray, n: int, qaddr: int = QADDR, **kw):
     o = Q.Machine(img, **kw)
-    ost = o.run_queue(QADDR, n)
+    ost = o.run_queue(qaddr, n)
     g = NQ.Machine(img, **kw)
-    gst = g.run_queue(QADDR, n)
+    gst = g.run_queue(qaddr, n)
     return (o, ost), (g, gst)
 
 
@@ -533,3 +534,87 @@ def test_gemv_only_profile_refuses_long_k():
     add_w8(p, 1, 16, 4112, Q.QM_CHANNEL)
     (o, ost), (g, gst) = both(p.image(), 1, gemv_only=True)
     assert (ost.err_code, gst.err_code) == (Q.E_OPCODE, Q.E_OPCODE)
+
+
+# ------------------------------------------------------------------------------ fused attention
+ATT_IMAGE, ATT_QADDR = 1 << 24, (1 << 24) - 0x10000
+
+
+def attention_program(seed: int, heads: int, kv_heads: int, hd: int, M: int, t0: int, v_fp16: bool,
+                      out: int = Q.OUT_FP32, hazard: bool = False) -> Program:
+    """One layer's attention as the reference lowers it (tars_mini/llm.py:736-746): per query head an
+    FDOT_NT of its q rows with its KV head's K rows into the shared score buffer, the causal softmax
+    (t0 + 1 valid keys for the first row) into the shared probability buffer, and an FDOT_NN with the
+    V rows into the head's output columns. hazard: the last head's q rows are the first head's
+    output, so the heads cannot run concurrently."""
+    p = Program(seed, image=ATT_IMAGE, qaddr=ATT_QADDR)
+    rng = p.rng
+    nk = (t0 + M + 15) // 16 * 16
+    qrow = 4 * heads * hd
+    q = p.put((rng.normal(0, 0.3, (M, heads * hd))).astype("<f4").tobytes())
+    kc = p.put(rng.normal(0, 1, (nk, kv_heads * hd)).astype("<f4").tobytes())
+    vv = rng.normal(0, 1, (nk, kv_heads * hd)).astype(np.float32)
+    vc = p.put(vv.astype(np.float16).view("<u2").tobytes() if v_fp16 else vv.astype("<f4").tobytes())
+    ves = 2 if v_fp16 else 4
+    sc = p.alloc(4 * M * nk)
+    pr = p.alloc(4 * M * nk)
+    arow = heads * hd * Q.ESIZE[out]
+    att = p.alloc(M * arow)
+    osc = f32bits(4.0) if out == Q.OUT_INT8 else 0
+    for h in range(heads):
+        kv = h // (heads // kv_heads)
+        dep = hazard and h == heads - 1
+        p.add(OPCODE=Q.OP_FDOT, CTRL=0, EPI=Q.epi(), A_OFF=att if dep else q + 4 * h * hd, W_OFF=kc + 4 * kv * hd,
+              Y_OFF=sc, M=M, N=nk, K=hd, LDA16=(arow if dep else qrow) // 16, GROUP_SIZE=4 * kv_heads * hd // 16)
+        p.add(OPCODE=Q.OP_ROW, CTRL=Q.ROW_SOFTMAX, EPI=Q.epi(), A_OFF=sc, Y_OFF=pr, M=M, N=nk, K=t0 + 1)
+        p.add(OPCODE=Q.OP_FDOT, CTRL=1, HDR_RSV=Q.STATE_FP16 if v_fp16 else 0, EPI=Q.epi(out=out), A_OFF=pr,
+              W_OFF=vc + ves * kv * hd, Y_OFF=att + Q.ESIZE[out] * h * hd, M=M, N=hd, K=nk,
+              GROUP_SIZE=ves * kv_heads * hd // 16, LDY16=arow // 16, OUT_SCALE=osc)
+    return p
+
+
+@pytest.mark.parametrize("fusion", [True, False])
+@pytest.mark.parametrize("heads,kv_heads,hd,M,t0,v_fp16,out", [
+    (16, 8, 128, 1, 250, False, Q.OUT_FP32),      # Qwen3-0.6B decode
+    (4, 1, 256, 1, 37, True, Q.OUT_FP32),         # head dim 256, fp16 V state
+    (8, 4, 64, 3, 100, False, Q.OUT_BF16),        # a 3-token chunk, bf16 out
+    (2, 2, 128, 2, 0, False, Q.OUT_INT8),         # the first position
+    (2, 1, 128, 1, 4100, False, Q.OUT_FP32),      # past the fused kernel's 4080 keys: unfused
+])
+def test_attention_layer_matches_the_oracle(fusion, heads, kv_heads, hd, M, t0, v_fp16, out):
+    p = attention_program(heads * 1000 + t0, heads, kv_heads, hd, M, t0, v_fp16, out)
+    prev = NQ.set_fusion(fusion)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs), ATT_QADDR)
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
+def test_attention_heads_that_depend_on_each_other_run_in_order():
+    """The last head reads the first head's output as its q rows: not concurrent, so not fused as
+    one group; the image still equals the oracle's in-order run."""
+    p = attention_program(7, 4, 2, 64, 1, 30, False, hazard=True)
+    (o, ost), (g, gst) = both(p.image(), len(p.descs), ATT_QADDR)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    assert bytes(g.ddr) == bytes(o.ddr)
+
+
+def test_attention_plan_replays_with_new_cache_data():
+    """The fused attention inside a launch plan: the same queue run again on changed q / K / V bytes."""
+    p = attention_program(11, 16, 8, 128, 1, 60, False)
+    img = p.image()
+    g = NQ.Machine(img)
+    rng = np.random.default_rng(3)
+    for rep in range(3):
+        if rep:
+            new = rng.normal(0, 1, 0x40000).astype("<f4").tobytes()
+            img[0x1000:0x1000 + len(new)] = new
+            g.write(0x1000, new)
+        gst = g.run_queue(ATT_QADDR, len(p.descs))
+        o = Q.Machine(img)
+        ost = o.run_queue(ATT_QADDR, len(p.descs))
+        assert ost.done and gst.done
+        assert bytes(g.ddr) == bytes(o.ddr), f"replay {rep}: first differing byte at {first_diff(bytes(g.ddr), bytes(o.ddr)):#x}"
