@@ -181,3 +181,51 @@ def test_fused_validation():
 def ctypes_sizeof_desc() -> int:
     import ctypes
     return ctypes.sizeof(_lib.W8A8Out)
+
+
+def test_rowop_validation():
+    """tars_row_op / tars_elt / tars_rope / tars_relu / tars_fdot refuse bad arguments with the
+    contract's codes before any launch (every call below is invalid)."""
+    lib = _lib.lib()
+    E = _lib
+    X, Y, G = P, P + 8 * MB, P + 16 * MB
+    row = lambda **k: lib.tars_row_op(*[k.get(n, d) for n, d in (
+        ("x", X), ("lda", 0), ("fn", 0), ("gamma", None), ("beta", None), ("eps", 0), ("ck", 0), ("valid", None),
+        ("y", Y), ("ldy", 0), ("out", 0), ("osc", 0), ("M", 2), ("N", 16))], None)
+    assert row(fn=4) == E.E_FIELD                                   # ROW_QUANT has its own entry point
+    assert row(fn=2) == E.E_ARG                                     # a norm needs gamma
+    assert row(gamma=G) == E.E_FIELD                                # softmax takes no gamma
+    assert row(fn=2, gamma=G, ck=3) == E.E_FIELD                    # only softmax is causal
+    assert row(out=3) == E.E_FIELD                                  # FP16 is an ELT output only
+    assert row(osc=0x40000000) == E.E_FIELD                         # out_scale without INT8
+    assert row(ldy=60) == E.E_ALIGN                                 # a stride shorter than a row
+    assert row(x=X + 2) == E.E_ALIGN                                # fp32 data 4-byte aligned
+    assert row(y=X + 32) == E.E_OVERLAP                             # y over x
+    assert row(x=None) == E.E_ARG
+    elt = lambda **k: lib.tars_elt(*[k.get(n, d) for n, d in (
+        ("A", X), ("lda", 0), ("a16", 0), ("arow", 0), ("B", G), ("ldb", 0), ("bm", 0), ("C", None), ("ldc", 0),
+        ("op", 0), ("act", 0), ("Y", Y), ("ldy", 0), ("out", 0), ("osc", 0), ("M", 4), ("N", 16))], None)
+    assert elt(op=4) == E.E_FIELD
+    assert elt(bm=4) == E.E_FIELD
+    assert elt(op=2) == E.E_ARG                                     # MULADD needs C
+    assert elt(op=2, C=P + 24 * MB, out=1) == E.E_FIELD             # MULADD adds in fp32 / fp16 only
+    assert elt(C=P + 24 * MB) == E.E_FIELD                          # C only for MULADD
+    assert elt(Y=X, a16=1, out=0) == E.E_OVERLAP                    # in place needs the same format
+    assert elt(Y=X + 16) == E.E_OVERLAP                             # a partial overlap
+    assert elt(Y=G) == E.E_OVERLAP                                  # over B
+    rope = lambda **k: lib.tars_rope(*[k.get(n, d) for n, d in (
+        ("x", X), ("lda", 0), ("tab", G), ("G", 2), ("rot", 16), ("y", Y), ("ldy", 0), ("out", 0), ("osc", 0),
+        ("M", 4), ("N", 16))], None)
+    assert rope(rot=15) == E.E_ALIGN
+    assert rope(rot=32) == E.E_ALIGN                                # rot past the row
+    assert rope(G=0) == E.E_ALIGN
+    assert rope(y=G + 8) == E.E_OVERLAP                             # over the table
+    assert lib.tars_relu(X, 0, 9, Y, 0, 0, 0, 2, 16, None) == E.E_FIELD          # act code 9
+    fdot = lambda **k: lib.tars_fdot(*[k.get(n, d) for n, d in (
+        ("A", X), ("lda", 0), ("B", G), ("ldb", 0), ("nn", 0), ("b16", 0), ("Y", Y), ("ldy", 0), ("out", 0),
+        ("osc", 0), ("M", 2), ("N", 16), ("K", 64))], None)
+    assert fdot(b16=1) == E.E_FIELD                                 # fp16 B only in the NN form
+    assert fdot(nn=2) == E.E_FIELD
+    assert fdot(K=0) == E.E_ALIGN
+    assert fdot(ldb=128) == E.E_ALIGN                               # NT rows of 64 fp32 are 256 bytes
+    assert fdot(Y=G + 64) == E.E_OVERLAP
