@@ -14,8 +14,11 @@ lm_head, the K-split projections, M = 4 / 256 prefill, W4A16 group-128) as us/ca
 roofline fraction (and TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight
 copies so the 256 MB MALL cannot serve it; per-kernel durations from HIP events around each launch
 of the decode step; the same decode step as a 313-descriptor queue through the library's queue
-executor ("queue_executor", host clock, end to end); and the CPU baseline (the numpy oracle, single
-core) on a bounded sample of the same workload, with a bit-exact check of the timed outputs.
+executor ("queue_executor", host clock, end to end); a whole Qwen3-0.6B decode step at position 250
+(norms, quantizers, every linear, q/k norms, RoPE, the attention, residual adds, SiLU * up and the
+head: 1910 descriptors) through the same executor ("queue_whole_decode_step_t250"); and the CPU
+baseline (the numpy oracle, single core) on a bounded sample of the same workload, with a bit-exact
+check of the timed outputs.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-configs] [--no-cpu-baseline] [--no-queue]
 """
@@ -29,6 +32,8 @@ import platform
 import sys
 import time
 from pathlib import Path
+
+import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -282,6 +287,196 @@ def queue_decode_step(torch, lib, seed: int, steps: int, warmup: int) -> dict:
             lib.tars_set_queue_graphs(prev_g)
         res[key] = {"launches_per_step": 113 if fusion else len(raw), "ms_per_step": round(t * 1e3, 4),
                     "GBps": round(nbytes / t / 1e9, 1)}
+    del image
+    torch.cuda.empty_cache()
+    return res
+
+
+class DecodeQueue:
+    """A Qwen3-style decode step (one token at position t0) as the descriptor queue the reference's
+    lowering emits for it (tars_mini/llm.py:705-767 attention block, :614-640 MLP, 330-338
+    linears, 94-108 norm/quant/softmax): per layer RMSNorm -> ROW_QUANT -> q/k/v GEMMs (v straight
+    into the V cache row t0) -> per-head RMSNorm + RoPE of q and k (k into the K cache row) -> per
+    head FDOT_NT / causal softmax / FDOT_NN -> ROW_QUANT -> o GEMM -> residual ELT_ADD -> RMSNorm ->
+    ROW_QUANT -> gate (SiLU) / up GEMMs -> ELT_MUL in place -> ROW_QUANT -> down GEMM -> residual;
+    then the final RMSNorm, ROW_QUANT and the head in 4 blocks. Synthetic weights (int8 with
+    per-channel scales, norms near 1), KV caches holding t0 earlier positions. `small` data first
+    (row scales must lie below 16 * 2^24 bytes), weights after."""
+
+    def __init__(self, layers=28, H=1024, heads=16, kv_heads=8, hd=128, ff=3072, vocab=151936, t0=250,
+                 head_blocks=4):
+        from opentars_amd import contract as C
+        self.C = C
+        self.descs, self.fills = [], []
+        self.small, self.big = [0], [0]
+        nk = (t0 + 1 + 15) // 16 * 16
+        take_s = lambda n: self._take(self.small, n, 256)
+        take_b = lambda n: self._take(self.big, n, 256)
+        tab = take_s(4 * hd * (t0 + 1))
+        self.fills.append(("rope", tab, (t0 + 1, hd)))
+        x = take_s(4 * H)
+        self.fills.append(("randn", x, H, 1.0))
+        self.weight_bytes = 0
+        for _ in range(layers):
+            kc, vc = take_s(4 * nk * kv_heads * hd), take_s(4 * nk * kv_heads * hd)
+            self.fills += [("randn", kc, nk * kv_heads * hd, 1.0), ("randn", vc, nk * kv_heads * hd, 1.0)]
+            h = self.norm(x, H, 1, take_s)
+            qh, sh = self.quant(h, H, take_s)
+            q = self.gemm(qh, sh, H, heads * hd, take_s, take_b)
+            k = self.gemm(qh, sh, H, kv_heads * hd, take_s, take_b)
+            self.gemm(qh, sh, H, kv_heads * hd, take_s, take_b, y=vc + 4 * t0 * kv_heads * hd)
+            qn = self.norm(q, hd, heads, take_s)
+            qr = take_s(4 * heads * hd)
+            self.add(OPCODE=C.OP_ROPE, EPI=C.epi(), A_OFF=qn, W_OFF=tab + 4 * hd * t0, Y_OFF=qr, M=heads, N=hd, K=hd,
+                     GROUP_SIZE=heads)
+            kn = self.norm(k, hd, kv_heads, take_s)
+            self.add(OPCODE=C.OP_ROPE, EPI=C.epi(), A_OFF=kn, W_OFF=tab + 4 * hd * t0,
+                     Y_OFF=kc + 4 * t0 * kv_heads * hd, M=kv_heads, N=hd, K=hd, GROUP_SIZE=kv_heads)
+            sc, pr, att = take_s(4 * nk), take_s(4 * nk), take_s(4 * heads * hd)
+            for hh in range(heads):
+                kv = hh // (heads // kv_heads)
+                self.add(OPCODE=C.OP_FDOT, EPI=C.epi(), A_OFF=qr + 4 * hh * hd, W_OFF=kc + 4 * kv * hd, Y_OFF=sc,
+                         M=1, N=nk, K=hd, GROUP_SIZE=4 * kv_heads * hd // 16)
+                self.add(OPCODE=C.OP_ROW, CTRL=C.ROW_SOFTMAX, EPI=C.epi(), A_OFF=sc, Y_OFF=pr, M=1, N=nk, K=t0 + 1)
+                self.add(OPCODE=C.OP_FDOT, CTRL=1, EPI=C.epi(), A_OFF=pr, W_OFF=vc + 4 * kv * hd,
+                         Y_OFF=att + 4 * hh * hd, M=1, N=hd, K=nk, GROUP_SIZE=4 * kv_heads * hd // 16)
+            qa, sa = self.quant(att, heads * hd, take_s)
+            o = self.gemm(qa, sa, heads * hd, H, take_s, take_b)
+            x1 = take_s(4 * H)
+            self.add(OPCODE=C.OP_ELT, CTRL=C.ELT_ADD, EPI=C.epi(), A_OFF=x, W_OFF=o, Y_OFF=x1, M=1, N=H)
+            h2 = self.norm(x1, H, 1, take_s)
+            q2, s2 = self.quant(h2, H, take_s)
+            g = self.gemm(q2, s2, H, ff, take_s, take_b, act=C.ACT_SILU)
+            u = self.gemm(q2, s2, H, ff, take_s, take_b)
+            self.add(OPCODE=C.OP_ELT, CTRL=C.ELT_MUL, EPI=C.epi(), A_OFF=g, W_OFF=u, Y_OFF=g, M=1, N=ff)
+            q3, s3 = self.quant(g, ff, take_s)
+            d = self.gemm(q3, s3, ff, H, take_s, take_b)
+            x = take_s(4 * H)
+            self.add(OPCODE=C.OP_ELT, CTRL=C.ELT_ADD, EPI=C.epi(), A_OFF=x1, W_OFF=d, Y_OFF=x, M=1, N=H)
+        hf = self.norm(x, H, 1, take_s)
+        qf, sf = self.quant(hf, H, take_s)
+        hw, hsc, hy = take_b(vocab * H), take_s(4 * vocab), take_s(4 * vocab)
+        self.fills += [("int8", hw, vocab * H), ("scale", hsc, vocab)]
+        self.weight_bytes += vocab * H
+        rows = vocab // head_blocks
+        for blk in range(head_blocks):
+            self.add(OPCODE=C.OP_GEMM, CTRL=C.ctrl(C.QM_ROWCOL), EPI=C.epi(), A_OFF=qf, W_OFF=hw + blk * rows * H,
+                     SCALE_OFF=hsc + 4 * blk * rows, Y_OFF=hy + 4 * blk * rows, HDR_RSV=sf // 16, M=1, N=rows, K=H)
+        self.logits, self.vocab = hy, vocab
+        self.qaddr = take_s(64 * len(self.descs))
+        if self.small[0] >= 16 * (1 << 24):
+            raise RuntimeError("row scales must lie below 16 * 2^24 bytes (the HDR_RSV field)")
+        self.base_big = (self.small[0] + 4095) // 4096 * 4096
+        self.size = self.base_big + self.big[0]
+
+    @staticmethod
+    def _take(region, n, align):
+        a = (region[0] + align - 1) // align * align
+        region[0] = a + n
+        return a
+
+    def add(self, **f):
+        self.descs.append(dict(MAGIC=self.C.MAGIC, VERSION=self.C.VERSION, VALID=1, **f))
+
+    def norm(self, x, n, rows, take_s):
+        g = take_s(4 * n)
+        self.fills.append(("gamma", g, n))
+        y = take_s(4 * n * rows)
+        self.add(OPCODE=self.C.OP_ROW, CTRL=self.C.ROW_RMSNORM, EPI=self.C.epi(), A_OFF=x, SCALE_OFF=g,
+                 W_OFF=int(np.float32(1e-6).view(np.uint32)), Y_OFF=y, M=rows, N=n)
+        return y
+
+    def quant(self, x, k, take_s):
+        q, s = take_s(k), take_s(16)
+        self.add(OPCODE=self.C.OP_ROW, CTRL=self.C.ROW_QUANT, EPI=self.C.epi(out=self.C.OUT_INT8), A_OFF=x, Y_OFF=q,
+                 SCALE_OFF=s, M=1, N=k)
+        return q, s
+
+    def gemm(self, q, s, k, n, take_s, take_b, act=0, y=None):
+        C = self.C
+        w, sc = take_b(n * k), take_s(4 * n)
+        y = take_s(4 * n) if y is None else y
+        self.fills += [("int8", w, n * k), ("scale", sc, n)]
+        self.weight_bytes += n * k
+        self.add(OPCODE=C.OP_GEMM, CTRL=C.ctrl(C.QM_ROWCOL, fusion=int(act != 0)), EPI=C.epi(act), A_OFF=q, W_OFF=w,
+                 SCALE_OFF=sc, Y_OFF=y, HDR_RSV=s // 16, M=1, N=n, K=k)
+        return y
+
+    def raw(self) -> bytes:
+        """The encoded queue, weight offsets moved past the small region."""
+        from opentars_amd.queue import encode_descriptor
+        out = []
+        for d in self.descs:
+            if d["OPCODE"] == self.C.OP_GEMM:
+                d = dict(d, W_OFF=d["W_OFF"] + self.base_big)
+            out.append(encode_descriptor(d))
+        return b"".join(out)
+
+    def fill(self, put):
+        """put(kind, offset, count, extra) for every region (weights at base_big + offset)."""
+        for f in self.fills:
+            kind, off = f[0], f[1]
+            put(kind, off + (self.base_big if kind == "int8" else 0), *f[2:])
+
+
+def full_decode_step(torch, lib, seed: int, t0: int = 250, steps: int = 20) -> dict:
+    """A whole Qwen3-0.6B decode step at t=250 as one descriptor queue (1910 descriptors) in one
+    device image, through the executor with its fusions and launch plans: ms per token."""
+    from opentars_amd import _lib
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 11)
+    dq = DecodeQueue(t0=t0)
+    image = torch.zeros(dq.size, dtype=torch.uint8, device="cuda")
+
+    def put(kind, off, n, extra=None):
+        if kind == "int8":
+            image[off:off + n].view(torch.int8).copy_(torch.randint(-127, 128, (n,), dtype=torch.int8, device="cuda",
+                                                                    generator=gen))
+        elif kind == "scale":
+            image[off:off + 4 * n].view(torch.float32).copy_(torch.rand(n, device="cuda", generator=gen) * 9e-3 + 1e-3)
+        elif kind == "gamma":
+            image[off:off + 4 * n].view(torch.float32).copy_(1 + 0.1 * torch.randn(n, device="cuda", generator=gen))
+        elif kind == "rope":
+            rows, hd = n
+            pos = torch.arange(rows, device="cuda", dtype=torch.float32)[:, None]
+            inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device="cuda", dtype=torch.float32) / hd))
+            fr = pos * inv[None, :]
+            image[off:off + 4 * rows * hd].view(torch.float32).copy_(torch.cat([fr.cos(), fr.sin()], 1).reshape(-1))
+        else:
+            image[off:off + 4 * n].view(torch.float32).copy_(torch.randn(n, device="cuda", generator=gen) * extra)
+
+    dq.fill(put)
+    host_q = dq.raw()
+    image[dq.qaddr:dq.qaddr + len(host_q)].copy_(torch.frombuffer(bytearray(host_q), dtype=torch.uint8).cuda())
+    torch.cuda.synchronize()
+    st = _lib.QueueStatus()
+    stream = torch.cuda.current_stream().cuda_stream
+    n = len(dq.descs)
+
+    def run():
+        rc = lib.tars_run_queue(image.data_ptr(), image.numel(), dq.qaddr, n, host_q, 0, 0, ctypes.byref(st), stream)
+        if rc != 0 or not st.done:
+            raise RuntimeError(f"decode queue: status {rc} done={st.done} err={st.err_code} op={st.op_idx}: "
+                               f"{_lib.last_error()}")
+
+    res = {"descriptors": n, "t0": t0, "weight_bytes": dq.weight_bytes}
+    for key, fusion, graphs, reps in (("fused_plans", 1, 1, steps), ("fused", 1, 0, 3)):
+        prev_f, prev_g = lib.tars_set_queue_fusion(fusion), lib.tars_set_queue_graphs(graphs)
+        try:
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            t_start = time.perf_counter()
+            for _ in range(reps):
+                run()
+            torch.cuda.synchronize()
+            t = (time.perf_counter() - t_start) / reps
+        finally:
+            lib.tars_set_queue_fusion(prev_f)
+            lib.tars_set_queue_graphs(prev_g)
+        res[key] = {"ms_per_token": round(t * 1e3, 3), "tokens_per_s": round(1 / t, 1)}
+    logits = image[dq.logits:dq.logits + 4 * dq.vocab].view(torch.float32)
+    res["logits_finite"] = bool(torch.isfinite(logits).all().item())
     del image
     torch.cuda.empty_cache()
     return res
@@ -759,6 +954,8 @@ def main() -> int:
 
     log("descriptor-queue executor")
     queue = None if args.no_queue else queue_decode_step(torch, lib, args.seed, max(3, args.steps // 10), 3)
+    log("whole decode step through the executor")
+    full = None if args.no_queue else full_decode_step(torch, lib, args.seed)
     log("per-config measurements")
     configs = {} if args.no_configs else config_suite(torch, lib, args.seed)
     log("cpu baseline")
@@ -796,6 +993,7 @@ def main() -> int:
         "kernels": kernels,
         "device_copy_GBps": round(copy_gbps, 1),
         "queue_executor": queue,
+        "queue_whole_decode_step_t250": full,
         "cpu_baseline": cpu,
         "configs": configs,
         "wall_s_timed": round(t_wall, 3),

@@ -27,6 +27,12 @@ MAGIC, VERSION = 0xAA55, 0x0002
 DESC_BYTES = 64
 OP_CONV, OP_GEMM, OP_RELU, OP_ROW, OP_CONV_ACT, OP_ELT, OP_ROPE, OP_FDOT = 1, 2, 3, 4, 5, 6, 7, 8
 ROW_SOFTMAX, ROW_LAYERNORM, ROW_RMSNORM, ROW_L2NORM, ROW_QUANT = 0, 1, 2, 3, 4
+# ELT op (CTRL[1:0]), B / A broadcast (HDR_RSV[1:0] / HDR_RSV[2]), fp16 state (HDR_RSV[3]) and FDOT
+# layout (CTRL[0]) of the row-engine opcodes (contract.py:63-72, 102-104)
+ELT_MUL, ELT_ADD, ELT_MULADD, ELT_SUB = 0, 1, 2, 3
+BM_DENSE, BM_ROW, BM_COL, BM_SCALAR = 0, 1, 2, 3
+FDOT_NT, FDOT_NN = 0, 1
+STATE_FP16 = 1 << 3
 
 
 def ctrl(qmode: int = QM_TENSOR, symmetric: int = 1, a_dtype: int = DT_INT8, w_dtype: int = DT_INT8,

@@ -259,16 +259,54 @@ int validate(const uint8_t* raw, const Desc& d, int core_id, bool gemv_only) {
 }
 
 // ---------------------------------------------------------------------------- byte segments
-struct Seg {
-  u128 lo, hi;  // [lo, hi) in image bytes
+// A tensor's bytes in closed form: `rows` rows of `rb` bytes, `ld` apart, i.e. the segments
+// [base + r ld, base + r ld + rb) for r < rows. A K or V cache of thousands of rows is one entry,
+// and whether two tensors share a byte is answered without listing their rows.
+struct Span {
+  u128 base, ld, rb;
+  uint64_t rows;
+  bool empty() const { return rows == 0 || rb == 0; }
+  u128 lo() const { return base; }
+  u128 hi() const { return empty() ? base : base + ld * (rows - 1) + rb; }
 };
-using Segs = std::vector<Seg>;
+using Segs = std::vector<Span>;
+
+Span interval(u128 lo, u128 hi) { return hi > lo ? Span{lo, hi - lo, hi - lo, 1} : Span{lo, 1, 0, 0}; }
+
+// Rows that touch or overlap (ld <= row bytes) are one interval, their union.
+Span strided_span(u128 base, uint64_t ld, uint64_t nrows, uint64_t row_bytes) {
+  if (nrows == 0 || row_bytes == 0) return Span{base, 1, 0, 0};
+  if (nrows == 1 || ld <= row_bytes) return interval(base, base + static_cast<u128>(ld) * (nrows - 1) + row_bytes);
+  return Span{base, ld, row_bytes, nrows};
+}
 
 Segs strided(u128 base, uint64_t ld, uint64_t nrows, uint64_t row_bytes) {
-  Segs v;
-  v.reserve(nrows);
-  for (uint64_t r = 0; r < nrows; ++r) v.push_back({base + static_cast<u128>(r) * ld, base + static_cast<u128>(r) * ld + row_bytes});
-  return v;
+  return {strided_span(base, ld, nrows, row_bytes)};
+}
+
+// Whether [lo, hi) meets a row of s: the rows from the first that ends past lo to the last that
+// starts before hi.
+bool meets(const Span& s, u128 lo, u128 hi) {
+  if (s.empty() || lo >= hi || hi <= s.lo() || lo >= s.hi()) return false;
+  if (s.rows == 1) return true;
+  const u128 r0 = lo < s.base + s.rb ? 0 : (lo - s.base - s.rb) / s.ld + 1;
+  const u128 r1 = std::min<u128>(s.rows - 1, (hi - 1 - s.base) / s.ld);
+  return r0 <= r1;
+}
+
+// Whether any row of a meets any row of b: the rows of the span with fewer rows, from the first
+// that ends past the other's start, each tested in closed form.
+bool meets(const Span& a, const Span& b) {
+  if (a.empty() || b.empty() || a.hi() <= b.lo() || b.hi() <= a.lo()) return false;
+  const Span& x = a.rows <= b.rows ? a : b;
+  const Span& y = a.rows <= b.rows ? b : a;
+  const u128 r0 = x.base + x.rb > y.lo() ? 0 : (y.lo() - x.base - x.rb) / x.ld + 1;
+  for (u128 r = r0; r < x.rows; ++r) {
+    const u128 lo = x.base + x.ld * r;
+    if (lo >= y.hi()) break;
+    if (meets(y, lo, lo + x.rb)) return true;
+  }
+  return false;
 }
 
 // The tensors a valid descriptor reads (each a list of segments) and the rows it writes
@@ -281,7 +319,7 @@ void segments(const Desc& d, std::vector<Segs>& reads, Segs& y) {
   y = strided(B + d[F_Y_OFF], s.ldy, M, s.yrow);
   if (is_v04(op)) {
     if (op == OP_ELT && ((d[F_HDR_RSV] >> 2) & 1)) {
-      reads.push_back({{B + d[F_A_OFF], B + d[F_A_OFF] + s.arow}});
+      reads.push_back({interval(B + d[F_A_OFF], B + d[F_A_OFF] + s.arow)});
     } else {
       reads.push_back(strided(B + d[F_A_OFF], s.lda, M, s.arow));
     }
@@ -292,12 +330,12 @@ void segments(const Desc& d, std::vector<Segs>& reads, Segs& y) {
         reads.push_back(strided(w0, b_stride(d).first, M, 4 * N));
       } else {
         const uint64_t nb = bm == BM_ROW ? 4 * N : bm == BM_COL ? 4 * M : 4;
-        reads.push_back({{w0, w0 + nb}});
+        reads.push_back({interval(w0, w0 + nb)});
       }
       if ((d[F_CTRL] & 3) == ELT_MULADD) reads.push_back(strided(B + d[F_BIAS_OFF], s.ldy, M, s.yrow));
     } else if (op == OP_ROPE) {
       const uint64_t tab_rows = (M - 1) / d[F_GROUP_SIZE] + 1;
-      reads.push_back({{w0, w0 + static_cast<u128>(4 * K) * tab_rows}});
+      reads.push_back({interval(w0, w0 + static_cast<u128>(4 * K) * tab_rows)});
     } else {
       const auto b = b_stride(d);
       reads.push_back(strided(w0, b.first, (d[F_CTRL] & 1) ? K : N, b.second));
@@ -309,7 +347,7 @@ void segments(const Desc& d, std::vector<Segs>& reads, Segs& y) {
     const uint64_t npx = static_cast<uint64_t>(g.H * g.W);
     const u128 a0 = B + d[F_A_OFF];
     if (s.lda == s.arow) {
-      reads.push_back({{a0, a0 + static_cast<u128>(npx) * s.arow}});
+      reads.push_back({interval(a0, a0 + static_cast<u128>(npx) * s.arow)});
     } else {
       reads.push_back(strided(a0, s.lda, npx, s.arow));
     }
@@ -319,18 +357,19 @@ void segments(const Desc& d, std::vector<Segs>& reads, Segs& y) {
   if (op == OP_GEMM || is_conv(op)) {
     const bool w4 = is_w4(d);
     const uint64_t ns = (d[F_CTRL] & 7) == QM_TENSOR ? 1 : N;
-    reads.push_back({{B + d[F_W_OFF], B + d[F_W_OFF] + static_cast<u128>(N) * K / (w4 ? 2 : 1)}});
-    reads.push_back({{B + d[F_SCALE_OFF], B + d[F_SCALE_OFF] + (w4 ? static_cast<u128>(2 * N) * (K / kW4Group) : static_cast<u128>(4 * ns))}});
-    if (has_bias(d[F_EPI])) reads.push_back({{B + d[F_BIAS_OFF], B + d[F_BIAS_OFF] + 4 * N}});
+    reads.push_back({interval(B + d[F_W_OFF], B + d[F_W_OFF] + static_cast<u128>(N) * K / (w4 ? 2 : 1))});
+    reads.push_back({interval(B + d[F_SCALE_OFF],
+                              B + d[F_SCALE_OFF] + (w4 ? static_cast<u128>(2 * N) * (K / kW4Group) : static_cast<u128>(4 * ns)))});
+    if (has_bias(d[F_EPI])) reads.push_back({interval(B + d[F_BIAS_OFF], B + d[F_BIAS_OFF] + 4 * N)});
     if ((d[F_CTRL] & 7) == QM_ROWCOL && !w4) {
       const u128 r0 = B + static_cast<u128>(16) * d[F_HDR_RSV];
-      reads.push_back({{r0, r0 + 4 * M}});
+      reads.push_back({interval(r0, r0 + 4 * M)});
     }
   } else if (op == OP_ROW) {
     const uint64_t fn = d[F_CTRL] & 7;
     if (fn == ROW_LAYERNORM || fn == ROW_RMSNORM || fn == ROW_L2NORM) {
-      reads.push_back({{B + d[F_SCALE_OFF], B + d[F_SCALE_OFF] + 4 * N}});
-      if (has_bias(d[F_EPI])) reads.push_back({{B + d[F_BIAS_OFF], B + d[F_BIAS_OFF] + 4 * N}});
+      reads.push_back({interval(B + d[F_SCALE_OFF], B + d[F_SCALE_OFF] + 4 * N)});
+      if (has_bias(d[F_EPI])) reads.push_back({interval(B + d[F_BIAS_OFF], B + d[F_BIAS_OFF] + 4 * N)});
     }
   }
 }
@@ -339,17 +378,16 @@ void segments(const Desc& d, std::vector<Segs>& reads, Segs& y) {
 Segs extra_out(const Desc& d) {
   if (d[F_OPCODE] == OP_ROW && (d[F_CTRL] & 7) == ROW_QUANT) {
     const u128 a = static_cast<u128>(d[F_BASE_ADDR]) + d[F_SCALE_OFF];
-    return {{a, a + 4 * d[F_M]}};
+    return {interval(a, a + 4 * d[F_M])};
   }
   return {};
 }
 
-// Whether any segment intersects any output row (outputs ascending and disjoint).
-bool overlaps(const Segs& segs, const Segs& y) {
-  for (const Seg& s : segs) {
-    auto it = std::upper_bound(y.begin(), y.end(), s.lo, [](u128 lo, const Seg& o) { return lo < o.hi; });
-    if (it != y.end() && it->lo < s.hi) return true;
-  }
+// Whether any row of any tensor in a meets any row of any tensor in b.
+bool overlaps(const Segs& a, const Segs& b) {
+  for (const Span& x : a)
+    for (const Span& y : b)
+      if (meets(x, y)) return true;
   return false;
 }
 
@@ -367,7 +405,7 @@ bool in_place(const Desc& d, size_t i) {
 
 u128 max_hi(const Segs& v) {
   u128 m = 0;
-  for (const Seg& s : v) m = std::max(m, s.hi);
+  for (const Span& s : v) m = std::max(m, s.hi());
   return m;
 }
 
@@ -531,7 +569,7 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
     members.push_back(std::move(c));
   }
   if (members.empty()) return TARS_OK;
-  const Segs rest = {{rest_lo, rest_hi}};
+  const Segs rest = {interval(rest_lo, rest_hi)};
   if (rest_lo < rest_hi) {
     if (overlaps(rest, quant.y) || overlaps(rest, quant.extra)) return TARS_OK;
     for (const Checked& c : members)
@@ -560,20 +598,10 @@ struct AttnHead {
   Desc nt, sm, nn;
 };
 
-Segs merged(std::vector<Seg> v) {
-  std::sort(v.begin(), v.end(), [](const Seg& a, const Seg& b) { return a.lo < b.lo; });
-  Segs out;
-  for (const Seg& x : v) {
-    if (!out.empty() && x.lo <= out.back().hi) out.back().hi = std::max(out.back().hi, x.hi);
-    else out.push_back(x);
-  }
-  return out;
-}
-
-bool pairwise_disjoint(std::vector<Seg> v) {
-  std::sort(v.begin(), v.end(), [](const Seg& a, const Seg& b) { return a.lo < b.lo; });
-  for (size_t i = 1; i < v.size(); ++i)
-    if (v[i].lo < v[i - 1].hi) return false;
+bool pairwise_disjoint(const Segs& v) {
+  for (size_t i = 0; i < v.size(); ++i)
+    for (size_t j = i + 1; j < v.size(); ++j)
+      if (meets(v[i], v[j])) return false;
   return true;
 }
 
@@ -645,8 +673,7 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
   group.clear();
   if (!g_fusion || first.d[F_OPCODE] != OP_FDOT || (first.d[F_CTRL] & 1)) return TARS_OK;
   const uintptr_t img = reinterpret_cast<uintptr_t>(image);
-  std::vector<Seg> ins, outs, atts;
-  Segs sc_y, pr_y;
+  Segs ins, atts, sc_y, pr_y;
   for (int32_t j = i; j + 2 < n && static_cast<uint64_t>(j + 2) < in_image &&
                       group.size() < static_cast<size_t>(tars::kAttnMaxHeads);
        j += 3) {
@@ -670,21 +697,15 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
     }
     for (const Segs& r : nt.reads) ins.insert(ins.end(), r.begin(), r.end());  // q and K
     const Desc& c = nn.d;
-    const Segs vrows = strided(addr(c, F_W_OFF), b_stride(c).first, c[F_K], b_stride(c).second);
-    ins.insert(ins.end(), vrows.begin(), vrows.end());
+    ins.push_back(strided_span(addr(c, F_W_OFF), b_stride(c).first, c[F_K], b_stride(c).second));
     atts.insert(atts.end(), nn.y.begin(), nn.y.end());
     group.push_back(AttnHead{nt.d, sm.d, nn.d});
   }
   if (group.empty()) return TARS_OK;
-  outs = atts;
-  outs.insert(outs.end(), sc_y.begin(), sc_y.end());
+  Segs outs = sc_y;
   outs.insert(outs.end(), pr_y.begin(), pr_y.end());
-  std::vector<Seg> sp = sc_y;
-  sp.insert(sp.end(), pr_y.begin(), pr_y.end());
-  sp.insert(sp.end(), atts.begin(), atts.end());
-  const Segs all_out = merged(outs);
-  if (!pairwise_disjoint(sp) || overlaps(merged(ins), all_out) ||
-      (rest_lo < rest_hi && overlaps(Segs{{rest_lo, rest_hi}}, all_out))) {
+  outs.insert(outs.end(), atts.begin(), atts.end());
+  if (!pairwise_disjoint(outs) || overlaps(ins, outs) || (rest_lo < rest_hi && overlaps(Segs{interval(rest_lo, rest_hi)}, outs))) {
     group.clear();
     return TARS_OK;
   }
@@ -911,7 +932,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     }
     if (cacheable) steps.push_back(Step{c.d, {}, {}});
     // an output written over a later descriptor of this queue: wait for it and read them again
-    const Segs rest = {{later, q_end}};
+    const Segs rest = {interval(later, q_end)};
     if (later < q_end && (overlaps(rest, c.y) || (!c.extra.empty() && overlaps(rest, c.extra)))) {
       cacheable = false;
       if (int rc = reread(static_cast<uint64_t>(i) + 1)) return rc;

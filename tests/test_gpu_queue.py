@@ -618,3 +618,58 @@ def test_attention_plan_replays_with_new_cache_data():
         ost = o.run_queue(ATT_QADDR, len(p.descs))
         assert ost.done and gst.done
         assert bytes(g.ddr) == bytes(o.ddr), f"replay {rep}: first differing byte at {first_diff(bytes(g.ddr), bytes(o.ddr)):#x}"
+
+
+def decode_step_image(seed: int, **shape):
+    """A whole decode step of a small Qwen3-style model (bench.DecodeQueue, the reference's lowering
+    of one token: tars_mini/llm.py:614-640, 705-767) in a host image with seeded data."""
+    from bench import DecodeQueue
+    dq = DecodeQueue(**shape)
+    rng = np.random.default_rng(seed)
+    img = bytearray(dq.size)
+
+    def put(kind, off, n, extra=None):
+        if kind == "int8":
+            b = rng.integers(-127, 128, n, dtype=np.int8).tobytes()
+        elif kind == "scale":
+            b = (rng.random(n) * 9e-3 + 1e-3).astype("<f4").tobytes()
+        elif kind == "gamma":
+            b = (1 + 0.1 * rng.normal(0, 1, n)).astype("<f4").tobytes()
+        elif kind == "rope":
+            rows, hd = n
+            fr = np.arange(rows, dtype=np.float32)[:, None] * (
+                1.0 / (1e6 ** (np.arange(0, hd, 2, dtype=np.float32) / hd)))[None, :]
+            b = np.concatenate([np.cos(fr), np.sin(fr)], 1).astype("<f4").tobytes()
+        else:
+            b = (rng.normal(0, 1, n) * extra).astype("<f4").tobytes()
+        img[off:off + len(b)] = b
+
+    dq.fill(put)
+    q = dq.raw()
+    img[dq.qaddr:dq.qaddr + len(q)] = q
+    return dq, img
+
+
+@pytest.mark.parametrize("fusion", [True, False])
+def test_whole_decode_step_matches_the_oracle(fusion):
+    """Every opcode of a decode step in one queue (RMSNorm, ROW_QUANT + q/k/v GEMMs, q/k norms per
+    head, RoPE into the K cache, V straight into the cache, the attention triples, o, residual
+    ELT_ADD, SiLU gate * up in place, down, final norm and a 4-block head): the image byte for byte,
+    on the first run and on two plan replays."""
+    dq, img = decode_step_image(5, layers=2, H=256, heads=4, kv_heads=2, hd=64, ff=512, vocab=1024, t0=40)
+    n = len(dq.descs)
+    o = Q.Machine(img)
+    ost = o.run_queue(dq.qaddr, n)
+    assert ost.done, ost
+    prev = NQ.set_fusion(fusion)
+    try:
+        g = NQ.Machine(img)
+        for rep in range(3):
+            gst = g.run_queue(dq.qaddr, n)
+            assert same_status(ost, gst), (rep, ost, gst)
+            gd = bytes(g.ddr)
+            assert gd == bytes(o.ddr), f"run {rep}: first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+    finally:
+        NQ.set_fusion(prev)
+    logits = np.frombuffer(bytes(o.ddr[dq.logits:dq.logits + 4 * dq.vocab]), "<f4")
+    assert np.isfinite(logits).all() and np.abs(logits).max() > 0

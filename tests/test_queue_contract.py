@@ -316,3 +316,49 @@ def test_native_validation_matches_the_oracle_on_mutations(seed):
         assert got == (want_err, want_gpu), (f, got, want_err)
         counts[want_err] += 1
     assert (counts > 0).sum() >= 6, counts           # the fuzz reaches most error classes
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_overlap_of_strided_rows_matches_the_oracle(seed):
+    """Outputs and inputs with row strides, packed into a few KiB so that their rows interleave,
+    touch and partly overlap: the executor's closed-form row test refuses exactly the descriptors
+    whose rows the oracle finds sharing a byte (golden.py:195-256, 440-448)."""
+    NQ = native()
+    rng = np.random.default_rng(700 + seed)
+    refused = accepted = 0
+    for _ in range(3000):
+        kind = int(rng.integers(0, 4))
+        M, N, K = int(rng.integers(1, 9)), 16 * int(rng.integers(1, 5)), 16 * int(rng.integers(1, 5))
+        f = dict(MAGIC=Q.MAGIC, VERSION=Q.VERSION, VALID=1, M=M, N=N,
+                 A_OFF=16 * int(rng.integers(0, 256)), W_OFF=16 * int(rng.integers(0, 256)),
+                 Y_OFF=16 * int(rng.integers(0, 256)))
+        if kind == 0:    # FDOT NT / NN with strided A, B and Y
+            nn = int(rng.integers(0, 2))
+            f.update(OPCODE=Q.OP_FDOT, CTRL=nn, K=K, LDA16=(4 * K) // 16 + int(rng.integers(0, 9)),
+                     GROUP_SIZE=(4 * (N if nn else K)) // 16 + int(rng.integers(0, 9)),
+                     LDY16=(4 * N) // 16 + int(rng.integers(0, 9)))
+        elif kind == 1:  # ELT with a dense strided B, sometimes in place
+            f.update(OPCODE=Q.OP_ELT, CTRL=int(rng.choice([Q.ELT_MUL, Q.ELT_ADD, Q.ELT_SUB])), LDA16=(4 * N) // 16 + int(rng.integers(0, 5)),
+                     GROUP_SIZE=(4 * N) // 16 + int(rng.integers(0, 5)), LDY16=(4 * N) // 16 + int(rng.integers(0, 5)))
+            if rng.integers(0, 4) == 0:
+                f.update(Y_OFF=f["A_OFF"], LDY16=f["LDA16"])
+        elif kind == 2:  # row function with strided rows and its gamma
+            f.update(OPCODE=Q.OP_ROW, CTRL=Q.ROW_RMSNORM, SCALE_OFF=16 * int(rng.integers(0, 256)), W_OFF=0x3A83126F,
+                     LDA16=(4 * N) // 16 + int(rng.integers(0, 9)), LDY16=(4 * N) // 16 + int(rng.integers(0, 9)))
+        else:            # ROPE reading a table, strided rows
+            f.update(OPCODE=Q.OP_ROPE, K=32, GROUP_SIZE=int(rng.integers(1, 4)), N=max(N, 32),
+                     LDA16=(4 * max(N, 32)) // 16 + int(rng.integers(0, 9)),
+                     LDY16=(4 * max(N, 32)) // 16 + int(rng.integers(0, 9)))
+        raw = Q.encode(f)
+        try:
+            want = Q.check(raw, 1 << 16)
+        except Q.ContractError:
+            with pytest.raises(Exception) as ei:
+                NQ.check_descriptor(raw, 1 << 16)
+            assert "overlap" in str(ei.value), f
+            refused += 1
+            continue
+        assert want[0] == Q.E_OK, f
+        assert NQ.check_descriptor(raw, 1 << 16)[0] == Q.E_OK, f
+        accepted += 1
+    assert refused > 300 and accepted > 300, (refused, accepted)
