@@ -3,16 +3,16 @@
 `Machine(ddr)` holds the DDR byte image in device memory and runs descriptor queues on it through
 the C ABI's tars_run_queue (include/opentars_amd.h), the replacement of tars_mini/golden.py:41-62
 (Machine: ddr, read, write) and :450-492 (run_queue -> Status). Descriptors are validated in the
-contract's order on the host; OP_GEMM (W8A8 QM_TENSOR / QM_CHANNEL / QM_ROWCOL and W4A16) and
-ROW_QUANT run on the GPU, in queue order, bit-identical to the golden model.
+contract's order on the host; every kind but a convolution runs on the GPU, in queue order,
+bit-identical to the golden model: OP_GEMM (W8A8 QM_TENSOR / QM_CHANNEL / QM_ROWCOL and W4A16),
+the row functions (ROW_QUANT, softmax, the norms), RELU, ELT, ROPE and FDOT.
 
-A valid descriptor of any other kind (norms, softmax, RoPE, FDOT, ELT, RELU, conv) is not run
-here. Without a `host` the queue stops there and the returned Status has host_op set. With a
-`host` -- a factory taking a host bytearray and returning an object with a `ddr` image and a
-run_queue(addr, 1) that executes one descriptor on it, e.g. the reference's own
-`tars_mini.golden.Machine` -- the
-image is copied to the host, that descriptor runs there, the image is copied back and the GPU
-queue resumes. `run(ddr, q, n, host)` is the `run(ddr, q, n) -> bytes` seam of
+A valid convolution (OP_CONV, OP_CONV_ACT) is not run here. Without a `host` the queue stops there
+and the returned Status has host_op set. With a `host` -- a factory taking a host bytearray and
+returning an object with a `ddr` image and a run_queue(addr, 1) that executes one descriptor on it,
+e.g. the reference's own `tars_mini.golden.Machine` -- the image is copied to the host, that
+descriptor runs there, the image is copied back and the GPU queue resumes. The language-model
+lowering emits no convolutions. `run(ddr, q, n, host)` is the `run(ddr, q, n) -> bytes` seam of
 QwenLowering.generate (tars_mini/llm.py:815-836).
 """
 from __future__ import annotations

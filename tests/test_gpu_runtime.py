@@ -1,0 +1,119 @@
+"""The export loader and runtime on the GPU (opentars_amd.runtime): the small Qwen3 export of
+tests/golden/export_small.npz (the reference's lowering) run by Model, and by the reference-style
+device interface GpuDevice, reproduces the logits the reference's runtime recorded on its golden
+backend, bit for bit (the SHA-256 of every step's fp32 logits), token by token and in prefill
+chunks. Needs a gfx950 GPU."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from export_fixture import expected, sha, unpack
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def export_dir(tmp_path_factory):
+    return unpack(tmp_path_factory.mktemp("export"))
+
+
+def check_case(model, exp):
+    model.new_conversation()
+    for s in exp["steps"]:
+        lg = model.step(s["token"])
+        assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} step {s['pos']}"
+    model.new_conversation()
+    lg = model.prefill(exp["ids"], chunked=True)
+    first = exp["prefill"][0]
+    assert (int(np.argmax(lg)), sha(lg)) == (first["argmax"], first["sha256"]), f"{exp['name']} prefill"
+    for s in exp["prefill"][1:]:
+        lg = model.step(s["token"])
+        assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} after prefill {s['pos']}"
+
+
+def test_model_reproduces_the_reference_runtime(export_dir):
+    from opentars_amd.runtime import Model
+    model = Model(export_dir, log=None)
+    for exp in expected(export_dir):
+        check_case(model, exp)
+
+
+def test_prefill_without_chunks_and_queue_parts(export_dir, tmp_path):
+    """Every prompt token a step (chunked=False), and queues run in parts of 29 descriptors
+    through the queue region (a manifest with a smaller queue_cap): the same bits."""
+    from opentars_amd.runtime import Model
+    d = unpack(tmp_path)
+    m = json.loads((d / "manifest.json").read_text())
+    m["queue_cap"] = 29
+    (d / "manifest.json").write_text(json.dumps(m))
+    model = Model(d, log=None)
+    exp = expected(export_dir)[0]
+    lg = model.prefill(exp["ids"], chunked=False)
+    assert sha(lg) == exp["steps"][len(exp["ids"]) - 1]["sha256"]
+    check_case(model, exp)
+
+
+def test_context_overflow_and_a_wrong_image_size(export_dir, tmp_path):
+    from opentars_amd.runtime import Model
+    model = Model(export_dir, log=None)
+    model.pos = model.T - 1
+    with pytest.raises(OverflowError):
+        model.prefill([1, 2])
+    d = unpack(tmp_path)
+    with open(d / "image.bin", "ab") as f:
+        f.write(b"\0" * 16)
+    with pytest.raises(RuntimeError, match="the manifest says"):
+        Model(d, log=None)
+
+
+class DeviceDriver:
+    """The reference runtime's use of a board device (tars_board.Qwen: the image into dev.mem,
+    to_dev; per token the embedding row and the queue into dev.mem, to_dev, run, from_dev of the
+    logits), over GpuDevice."""
+
+    def __init__(self, dev, d):
+        self.dev, self.m = dev, json.loads((d / "manifest.json").read_text())
+        img = np.fromfile(d / "image.bin", np.uint8)
+        dev.mem[:img.size] = img
+        dev.mem[img.size:] = 0
+        dev.to_dev(0, dev.mem.size)
+        self.state0 = dev.mem[:self.m["state_end"]].copy()
+        self.embed = np.fromfile(d / "embed_bf16.bin", np.uint16).reshape(self.m["vocab"], self.m["hidden"])
+        self.queues = np.fromfile(d / "queues.bin", np.uint8)
+        self.pos = 0
+
+    def new_conversation(self):
+        self.dev.mem[:self.m["state_end"]] = self.state0
+        self.dev.to_dev(0, self.m["state_end"])
+        self.pos = 0
+
+    def step(self, tok):
+        m, dev = self.m, self.dev
+        a = m["x0_off"] + self.pos * m["x0_ld"]
+        x = (self.embed[tok].astype(np.uint32) << 16).view(np.float32)
+        dev.mem[a:a + 4 * m["hidden"]] = np.frombuffer(x.tobytes(), np.uint8)
+        dev.to_dev(a, 4 * m["hidden"])
+        off, n = m["queue_index"][self.pos]
+        q = m["qbase"]
+        dev.mem[q:q + 64 * n] = self.queues[off:off + 64 * n]
+        dev.to_dev(q, 64 * n)
+        done, err, op, _ = dev.run(q, n)
+        assert done and not err, (err, op)
+        self.pos += 1
+        lo = m["logits_off"]
+        dev.from_dev(lo, 4 * m["vocab"])
+        return dev.mem[lo:lo + 4 * m["vocab"]].view(np.float32).copy()
+
+
+def test_gpu_device_under_the_reference_runtime_calls(export_dir):
+    from opentars_amd.runtime import GpuDevice
+    m = json.loads((export_dir / "manifest.json").read_text())
+    drv = DeviceDriver(GpuDevice(mem_bytes=m["mem_bytes"]), export_dir)
+    for exp in expected(export_dir):
+        drv.new_conversation()
+        for s in exp["steps"]:
+            lg = drv.step(s["token"])
+            assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} step {s['pos']}"

@@ -1,0 +1,114 @@
+"""The oracle's descriptor-queue walk over a whole board export: the small Qwen3 export of
+tests/golden/export_small.npz run token by token and in prefill chunks reproduces, bit for bit,
+the logits the reference's runtime recorded on its golden backend (the SHA-256 of every step's
+fp32 logits, tools/export_kv260.py:320-347). This pins the oracle's row, elementwise, RoPE, FDOT,
+quantizer and GEMM steps together, in the order the reference's lowering emits them."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from oracle import queue as Q
+from export_fixture import expected, sha, unpack
+
+
+class OracleBoard:
+    """A minimal board runtime over the oracle (the steps of tars_board.Qwen: embedding rows into
+    x0, the position's queue into the queue region, the run, the logits)."""
+
+    def __init__(self, d):
+        m = self.m = json.loads((d / "manifest.json").read_text())
+        img = (d / "image.bin").read_bytes()
+        assert len(img) == m["image_bytes"]
+        self.ddr = bytearray(max(len(img), m["mem_bytes"]))
+        self.ddr[:len(img)] = img
+        self.state0 = bytes(self.ddr[:m["state_end"]])
+        self.embed = np.fromfile(d / "embed_bf16.bin", np.uint16).reshape(m["vocab"], m["hidden"])
+        self.queues = (d / "queues.bin").read_bytes()
+        self.chunks = {int(n): ((d / f"queues_c{n}.bin").read_bytes(), {t0: (o, k) for t0, o, k in idx})
+                       for n, idx in m["chunks"].items()}
+        self.pos = 0
+
+    def new_conversation(self):
+        self.ddr[:self.m["state_end"]] = self.state0
+        self.pos = 0
+
+    def _put(self, t, tokens):
+        m = self.m
+        for i, tok in enumerate(tokens):
+            x = (self.embed[tok].astype(np.uint32) << 16).view(np.float32)
+            a = m["x0_off"] + (t + i) * m["x0_ld"]
+            self.ddr[a:a + 4 * m["hidden"]] = x.tobytes()
+
+    def _run(self, queues, off, n):
+        q, cap = self.m["qbase"], self.m["queue_cap"]
+        for s in range(0, n, cap):
+            k = min(cap, n - s)
+            self.ddr[q:q + 64 * k] = queues[off + 64 * s:off + 64 * (s + k)]
+            mach = Q.Machine(self.ddr)
+            st = mach.run_queue(q, k)
+            assert st.done and st.err_code == 0, st
+            self.ddr = mach.ddr
+
+    def logits(self):
+        lo = self.m["logits_off"]
+        return np.frombuffer(bytes(self.ddr[lo:lo + 4 * self.m["vocab"]]), np.float32).copy()
+
+    def step(self, tok):
+        self._put(self.pos, [tok])
+        off, n = self.m["queue_index"][self.pos]
+        self._run(self.queues, off, n)
+        self.pos += 1
+        return self.logits()
+
+    def prefill(self, tokens):
+        i = 0
+        while i < len(tokens):
+            n = next((n for n in sorted(self.chunks, reverse=True)
+                      if i + n <= len(tokens) and self.pos in self.chunks[n][1]), 1)
+            if n == 1:
+                self.step(tokens[i])
+            else:
+                self._put(self.pos, tokens[i:i + n])
+                qs, idx = self.chunks[n]
+                off, k = idx[self.pos]
+                self._run(qs, off, k)
+                self.pos += n
+            i += n
+        return self.logits()
+
+
+@pytest.fixture(scope="module")
+def export_dir(tmp_path_factory):
+    return unpack(tmp_path_factory.mktemp("export"))
+
+
+@pytest.mark.parametrize("case", [0, 1])
+def test_oracle_reproduces_the_reference_runtime_on_an_export(export_dir, case):
+    exp = expected(export_dir)[case]
+    b = OracleBoard(export_dir)
+    b.new_conversation()
+    for s in exp["steps"]:
+        lg = b.step(s["token"])
+        assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} step {s['pos']}"
+    b.new_conversation()
+    lg = b.prefill(exp["ids"])
+    first = exp["prefill"][0]
+    assert (int(np.argmax(lg)), sha(lg)) == (first["argmax"], first["sha256"])
+    for s in exp["prefill"][1:]:
+        lg = b.step(s["token"])
+        assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} after prefill {s['pos']}"
+
+
+def test_runtime_needs_a_gpu(export_dir):
+    """No CPU fallback: without a GPU the loader refuses to start."""
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from opentars_amd.runtime import GpuDevice, Model
+    with pytest.raises(RuntimeError, match="needs a ROCm GPU"):
+        Model(export_dir, log=None)
+    with pytest.raises(RuntimeError, match="needs a ROCm GPU"):
+        GpuDevice(1 << 20)
