@@ -1,5 +1,5 @@
-"""The small board export of tests/golden/export_small.npz (written by make_export_fixture.py from
-the reference's lowering and runtime) unpacked into a directory, and the results recorded on it."""
+"""The small board exports of tests/golden/export_*.npz (written by make_export_fixture.py from the
+reference's lowering and runtime) unpacked into a directory, and the results recorded on them."""
 from __future__ import annotations
 
 import hashlib
@@ -8,12 +8,13 @@ from pathlib import Path
 
 import numpy as np
 
-NPZ = Path(__file__).resolve().parent / "golden" / "export_small.npz"
+GOLDEN = Path(__file__).resolve().parent / "golden"
+KINDS = {"qwen3": "export_small.npz", "qwen35_mtp": "export_qwen35_mtp.npz", "gemma4": "export_gemma4.npz"}
 
 
-def unpack(dst: Path) -> Path:
+def unpack(dst: Path, kind: str = "qwen3") -> Path:
     """The export's files into dst; returns dst."""
-    with np.load(NPZ) as z:
+    with np.load(GOLDEN / KINDS[kind]) as z:
         for name in z.files:
             (dst / name).write_bytes(z[name].tobytes())
     return dst

@@ -1,8 +1,9 @@
-"""The export loader and runtime on the GPU (opentars_amd.runtime): the small Qwen3 export of
-tests/golden/export_small.npz (the reference's lowering) run by Model, and by the reference-style
-device interface GpuDevice, reproduces the logits the reference's runtime recorded on its golden
-backend, bit for bit (the SHA-256 of every step's fp32 logits), token by token and in prefill
-chunks. Needs a gfx950 GPU."""
+"""The export loader and runtime on the GPU (opentars_amd.runtime): the small Qwen3, Qwen3.5
+(DeltaNet, MTP head) and Gemma 4 (per-layer embeddings, scaled input embedding) exports of
+tests/golden/export_*.npz (the reference's lowering) run by Model, and by the reference-style
+device interface GpuDevice, reproduce the logits the reference's runtime recorded on its golden
+backend, bit for bit (the SHA-256 of every step's fp32 logits), token by token, in prefill chunks
+and in speculative rounds. Needs a gfx950 GPU."""
 from __future__ import annotations
 
 import json
@@ -10,7 +11,7 @@ import json
 import numpy as np
 import pytest
 
-from export_fixture import expected, sha, unpack
+from export_fixture import KINDS, expected, sha, unpack
 
 pytestmark = pytest.mark.gpu
 
@@ -18,6 +19,11 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def export_dir(tmp_path_factory):
     return unpack(tmp_path_factory.mktemp("export"))
+
+
+@pytest.fixture(scope="module", params=list(KINDS))
+def any_export(request, tmp_path_factory):
+    return unpack(tmp_path_factory.mktemp(request.param), request.param)
 
 
 def check_case(model, exp):
@@ -34,11 +40,37 @@ def check_case(model, exp):
         assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} after prefill {s['pos']}"
 
 
-def test_model_reproduces_the_reference_runtime(export_dir):
+def test_model_reproduces_the_reference_runtime(any_export):
     from opentars_amd.runtime import Model
-    model = Model(export_dir, log=None)
-    for exp in expected(export_dir):
+    model = Model(any_export, log=None)
+    for exp in expected(any_export):
         check_case(model, exp)
+
+
+def test_speculative_rounds_reproduce_the_reference_runtime(tmp_path):
+    """The MTP export: prefill, the first draft, verify rounds on both state copies (hits and
+    misses), the swap back; the same tokens and verify rows as the reference's runtime."""
+    from opentars_amd.runtime import Model
+    d = unpack(tmp_path, "qwen35_mtp")
+    model = Model(d, log=None)
+    for exp in expected(d):
+        spec = exp["spec"]
+        model.new_conversation()
+        lg = model.prefill(exp["ids"], chunked=True)
+        cur = model.begin_spec(lg)
+        toks = [cur]
+        assert cur == spec["first"]
+        for r in spec["rounds"]:
+            assert model.can_spec()
+            assert model.draft == r["draft"]
+            new, rows = model.spec_round(cur)
+            assert (model.pos, new, sha(rows)) == (r["pos"], r["new"], r["rows_sha256"]), r
+            toks += new
+            cur = new[-1]
+        model.end_spec()
+        assert toks == spec["tokens"]
+        greedy = [s["argmax"] for s in exp["steps"][len(exp["ids"]) - 1:]]
+        assert toks[:len(greedy)] == greedy[:len(toks)]       # the tokens of plain greedy decoding
 
 
 def test_prefill_without_chunks_and_queue_parts(export_dir, tmp_path):

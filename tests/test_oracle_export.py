@@ -1,8 +1,9 @@
-"""The oracle's descriptor-queue walk over a whole board export: the small Qwen3 export of
-tests/golden/export_small.npz run token by token and in prefill chunks reproduces, bit for bit,
-the logits the reference's runtime recorded on its golden backend (the SHA-256 of every step's
-fp32 logits, tools/export_kv260.py:320-347). This pins the oracle's row, elementwise, RoPE, FDOT,
-quantizer and GEMM steps together, in the order the reference's lowering emits them."""
+"""The oracle's descriptor-queue walk over whole board exports: the small Qwen3, Qwen3.5 (DeltaNet
+and full attention) and Gemma 4 (sliding / full attention, shared KV, per-layer embeddings)
+exports of tests/golden/export_*.npz run token by token and in prefill chunks reproduce, bit for
+bit, the logits the reference's runtime recorded on its golden backend (the SHA-256 of every
+step's fp32 logits, tools/export_kv260.py:320-347). This pins the oracle's row, elementwise, RoPE,
+FDOT, quantizer and GEMM steps together, in the orders the reference's lowering emits them."""
 from __future__ import annotations
 
 import json
@@ -11,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import queue as Q
-from export_fixture import expected, sha, unpack
+from export_fixture import KINDS, expected, sha, unpack
 
 
 class OracleBoard:
@@ -26,6 +27,8 @@ class OracleBoard:
         self.ddr[:len(img)] = img
         self.state0 = bytes(self.ddr[:m["state_end"]])
         self.embed = np.fromfile(d / "embed_bf16.bin", np.uint16).reshape(m["vocab"], m["hidden"])
+        self.ple = np.fromfile(d / "ple_bf16.bin", np.uint16).reshape(m["vocab"], m["ple_cols"]) \
+            if m.get("ple_cols") else None
         self.queues = (d / "queues.bin").read_bytes()
         self.chunks = {int(n): ((d / f"queues_c{n}.bin").read_bytes(), {t0: (o, k) for t0, o, k in idx})
                        for n, idx in m["chunks"].items()}
@@ -39,8 +42,14 @@ class OracleBoard:
         m = self.m
         for i, tok in enumerate(tokens):
             x = (self.embed[tok].astype(np.uint32) << 16).view(np.float32)
+            if m["embed_scale"] is not None:
+                x = x * np.float32(m["embed_scale"])
             a = m["x0_off"] + (t + i) * m["x0_ld"]
-            self.ddr[a:a + 4 * m["hidden"]] = x.tobytes()
+            self.ddr[a:a + 4 * m["hidden"]] = x.astype(np.float32).tobytes()
+            if self.ple is not None:
+                p = (self.ple[tok].astype(np.uint32) << 16).view(np.float32) * np.float32(m["ple_scale"])
+                a = m["ple0_off"] + (t + i) * m["ple0_ld"]
+                self.ddr[a:a + 4 * m["ple_cols"]] = p.astype(np.float32).tobytes()
 
     def _run(self, queues, off, n):
         q, cap = self.m["qbase"], self.m["queue_cap"]
@@ -80,9 +89,9 @@ class OracleBoard:
         return self.logits()
 
 
-@pytest.fixture(scope="module")
-def export_dir(tmp_path_factory):
-    return unpack(tmp_path_factory.mktemp("export"))
+@pytest.fixture(scope="module", params=list(KINDS))
+def export_dir(request, tmp_path_factory):
+    return unpack(tmp_path_factory.mktemp(request.param), request.param)
 
 
 @pytest.mark.parametrize("case", [0, 1])
