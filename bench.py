@@ -516,14 +516,16 @@ def time_graph(torch, g, reps: int, warmup: int) -> float:
 
 def plain_rows_per_wave(rows: int) -> int:
     """The plain GEMV's rows-per-wave rule (gemv_w8a8.hip, plain_rows_per_wave)."""
-    return 1 if rows < 2048 else 2 if rows < 32768 else 4
+    return 1 if rows < 32768 else 4
 
 
 def fused_rows_per_wave(rows: int, K: int) -> int:
     """The fused quantize + GEMV rule (gemv_w8a8.hip, fused_rows_per_wave)."""
-    u = 4 if K <= 1024 else 2 if K <= 3072 else 1
+    u = 1
+    while u < 4 and rows // (4 * 2 * u) >= 256:
+        u *= 2
     wgs = -(-rows // (4 * u))
-    return 2 * u if 256 < wgs < 512 and u < 8 else u
+    return 2 * u if 256 < wgs < 512 else u
 
 
 def kernel_instance(l: Launch) -> str:

@@ -9,6 +9,17 @@
 // exact int32 sums. The L partial sums of a row are combined with DPP lane permutes (exact
 // integer adds, so the order is free), and lane `u` of the group runs the fp32 epilogue for row u.
 //
+// Latency rules (each measured on MI355X; together 3.02 -> 2.4 us at K = 1024, N = 3072):
+//  * every global load of a lane is issued back to back, activations first, then the epilogue
+//    operands, then the weights, with only address arithmetic in between; values are masked after
+//    the whole batch is in flight (a select placed between two loads makes the compiler wait for
+//    the first before issuing the second, and an epilogue load issued after the weights waits for
+//    them);
+//  * the scalar epilogue fields (output pointer, formats) are pinned in SGPRs right after the
+//    batch, so their kernel-argument load overlaps the weight stream instead of following it;
+//  * workgroup b of n takes row block xcd_block(b, n): the workgroups of one XCD own consecutive
+//    rows, so each 128-byte line of the output is written from one XCD's L2.
+//
 // Roofline: HBM. Algorithmic bytes per row: K (weights) + 4 (scale) + 4 (output) (+4 bias).
 #include "kernels.h"
 
@@ -45,7 +56,8 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   const int sub = lane % L;
   const int m0 = blockIdx.y * MR;
   const int C = a.K >> 4;
-  const int n0 = (blockIdx.x * (kWaves * kSlots) + wave * kSlots + slot) * U;
+  const int bx = xcd_block(blockIdx.x, gridDim.x);
+  const int n0 = (bx * (kWaves * kSlots) + wave * kSlots + slot) * U;
   const v4i zero = {0, 0, 0, 0};
 
   int acc[MR][U];
@@ -61,7 +73,9 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   float sr = 0.0f, sc = 0.0f, bi = 0.0f;
 
   if constexpr (CPL > 0) {
-    // issue order: activations, weights, then the epilogue operands
+    // one batch of loads: activations, epilogue operands, weights (rows past N and chunks past K
+    // read the matrix start; a chunk past K is zeroed on the activation side, which zeroes its
+    // products, and rows past N are never stored)
     v4i xv[MR][CPL];
 #pragma unroll
     for (int r = 0; r < MR; ++r) {
@@ -70,10 +84,12 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        xv[r][j] = load_pred(xrow + c, xrow, live && c < C, zero);
+        xv[r][j] = *(c < C ? xrow + c : xrow);
       }
     }
-    issue_fence();
+    sc = a.epi.load_scol(nc);
+    bi = a.epi.load_bias(nc);
+    sr = a.epi.load_srow(mc);
     const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
     v4i wv[U][CPL];
 #pragma unroll
@@ -83,14 +99,19 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        wv[u][j] = load_stream_pred(wrow + c, wbase, n < a.N && c < C, zero);
+        wv[u][j] = __builtin_nontemporal_load(n < a.N && c < C ? wrow + c : wbase);
       }
     }
     issue_fence();
-    sc = a.epi.load_scol(nc);
-    bi = a.epi.load_bias(nc);
-    sr = a.epi.load_srow(mc);
-    issue_fence();
+    pin_sgpr(a.Y);
+    pin_sgpr(a.ldy);
+    pin_sgpr(a.epi.act);
+    pin_sgpr(a.epi.out);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      if (sub + j * L >= C)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) xv[r][j] = zero;
 #pragma unroll
     for (int r = 0; r < MR; ++r)
 #pragma unroll
@@ -197,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSpli
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m = blockIdx.y;
-  const int n0 = (blockIdx.x * kWaves + wave) * U;
+  const int n0 = (xcd_block(blockIdx.x, gridDim.x) * kWaves + wave) * U;
   const v4i zero = {0, 0, 0, 0};
   int cstart[kMaxBlocks + 1];
   cstart[0] = 0;
@@ -282,50 +303,52 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSpli
 // (a single pass over 4K bytes, mostly L2 hits after the first workgroup), the row maximum meets
 // through wave shuffles and 4 LDS words, every thread runs the fixed recip_f sequence, and the
 // q8 bytes land in LDS where each lane picks up the 16-byte chunks its dot products need. The
-// weight loads are issued before any of this, so the quantizer runs under their HBM latency.
-// Workgroup 0 also stores the quantized row and its scale (the ROW_QUANT outputs the golden
-// model writes).
+// weight loads are issued with the activations, so the quantizer runs under their HBM latency.
+// Weight matrix g of the launch is grid z = g (its fields are read at a fixed kernel-argument
+// offset, with no dependent load before the weight stream); a matrix with fewer row blocks than
+// the grid's x extent leaves the excess workgroups idle. The first workgroup of matrix 0 also
+// stores the quantized row and its scale (the ROW_QUANT outputs the golden model writes).
 template <int L, int CPL, int U>
 __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs a) {
   extern __shared__ __align__(16) int8_t qsh[];  // the quantized row, K bytes
   __shared__ uint32_t wave_max[kWaves];
   constexpr int kSlots = 64 / L;
+  constexpr int kRows = kWaves * kSlots * U;  // weight rows per workgroup
+  const GemvGroup& gr = a.g[blockIdx.z];
+  // every kernel argument the load batch needs, in one scalar round trip
+  __asm__ volatile("" : : "s"(a.x), "s"(a.lda), "s"(a.K), "s"(gr.W), "s"(gr.N), "s"(gr.epi.scol),
+                   "s"(gr.epi.bias), "s"(gr.epi.scol_per_tensor));
+  const int N = gr.N;
+  const int nblk = (N + kRows - 1) / kRows;
+  if (static_cast<int>(blockIdx.x) >= nblk) return;  // a matrix with fewer row blocks than the grid
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slot = lane / L;
   const int sub = lane % L;
   const int m = blockIdx.y;
   const int C = a.K >> 4;
-  int g = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxGroups; ++i)
-    if (i < a.ngroups && static_cast<int>(blockIdx.x) >= a.block_start[i]) g = i;
-  const int8_t* W = a.g[0].W;
-  int N = a.g[0].N;
-#pragma unroll
-  for (int i = 1; i < kMaxGroups; ++i)
-    if (g == i) {
-      W = a.g[i].W;
-      N = a.g[i].N;
-    }
-  const int lb = static_cast<int>(blockIdx.x) - a.block_start[g];
-  const int n0 = (lb * (kWaves * kSlots) + wave * kSlots + slot) * U;
+  const int K4 = a.K >> 2;
+  const int n0 = (xcd_block(blockIdx.x, nblk) * (kWaves * kSlots) + wave * kSlots + slot) * U;
   const v4i zero = {0, 0, 0, 0};
+  const int8_t* W = gr.W;
 
-  // Issue order matters: vmcnt counts loads in order, so the fp32 activations go first (the
-  // quantizer waits on them alone), then the weights, then the epilogue operands.
+  // one batch of loads: the fp32 activations (the quantizer waits on them alone), the epilogue
+  // operands, the weights (rows past N and chunks past K read the matrix start: rows past N are
+  // never stored and a chunk past K meets a zero activation chunk)
   constexpr int XV = CPL > 0 ? (L == 64 ? CPL : 1) : 1;  // float4s of the row per thread (K <= 1024 XV)
   const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(a.x) + m * a.lda);
-  const int K4 = a.K >> 2;
   float4 xr[XV];
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       const int i = threadIdx.x + j * kThreads;
-      xr[j] = load_pred(xrow + i, xrow, i < K4, make_float4(0.0f, 0.0f, 0.0f, 0.0f));
+      xr[j] = *(i < K4 ? xrow + i : xrow);
     }
   }
-  issue_fence();
+  const int ne = n0 + sub;
+  const bool epi_lane = sub < U && ne < N;
+  const float sc = gr.epi.load_scol(epi_lane ? ne : 0);
+  const float bi = gr.epi.load_bias(epi_lane ? ne : 0);
   v4i wv[U][CPL > 0 ? CPL : 1];
   if constexpr (CPL > 0) {
 #pragma unroll
@@ -335,33 +358,24 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        wv[u][j] = load_stream_pred(wrow + c, reinterpret_cast<const v4i*>(W), n < N && c < C, zero);
+        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : reinterpret_cast<const v4i*>(W));
       }
     }
   }
-  RowColEpilogue epi = a.g[0].epi;
-  void* Yout = a.g[0].Y;
-  int64_t ldy = a.g[0].ldy;
-#pragma unroll
-  for (int i = 1; i < kMaxGroups; ++i)
-    if (g == i) {
-      epi = a.g[i].epi;
-      Yout = a.g[i].Y;
-      ldy = a.g[i].ldy;
-    }
-  const int ne = n0 + sub;
-  const bool epi_lane = sub < U && ne < N;
   issue_fence();
-  const float sc = epi.load_scol(epi_lane ? ne : 0);
-  const float bi = epi.load_bias(epi_lane ? ne : 0);
-  issue_fence();
+  pin_sgpr(gr.Y);
+  pin_sgpr(gr.ldy);
+  pin_sgpr(gr.epi.act);
+  pin_sgpr(gr.epi.out);
 
   // the workgroup quantizes row m into LDS
   uint32_t mx = 0;
   if constexpr (CPL > 0) {
 #pragma unroll
-    for (int j = 0; j < XV; ++j)
+    for (int j = 0; j < XV; ++j) {
+      if (threadIdx.x + j * kThreads >= K4) xr[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       mx = max(mx, max(max(abs_bits_ftz(xr[j].x), abs_bits_ftz(xr[j].y)), max(abs_bits_ftz(xr[j].z), abs_bits_ftz(xr[j].w))));
+    }
   } else {
     for (int i = threadIdx.x; i < K4; i += kThreads) {
       const float4 v = xrow[i];
@@ -374,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
   float inv, sr;
   quant_scales(mx, inv, sr);
-  const bool store_q = a.q != nullptr && blockIdx.x == 0;
+  const bool store_q = a.q != nullptr && blockIdx.x == 0 && blockIdx.z == 0;
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
@@ -396,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   if (store_q && threadIdx.x == 0) a.s[m] = sr;
   __syncthreads();
 
-  // 3. exact int32 dot products
+  // exact int32 dot products
   int acc[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) acc[u] = 0;
@@ -405,7 +419,8 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = sub + j * L;
-      const v4i xv = c < C ? xq[c] : zero;
+      const v4i xl = xq[c < C ? c : 0];
+      const v4i xv = c < C ? xl : zero;
 #pragma unroll
       for (int u = 0; u < U; ++u) acc[u] = dot16(wv[u][j], xv, acc[u]);
     }
@@ -431,34 +446,29 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   for (int u = 0; u < U; ++u)
     if (sub == u) mine = acc[u];
   if (epi_lane) {
-    const float y = epi.apply(mine, sr, true, sc, bi);
-    store_out(Yout, m * ldy, ne, epi.out, y, epi.out_scale);
+    const float y = gr.epi.apply(mine, sr, true, sc, bi);
+    store_out(gr.Y, m * gr.ldy, ne, gr.epi.out, y, gr.epi.out_scale);
   }
 }
 
-// Rows per wave: one row keeps small matrices spread over every CU (their time is latency, not
-// bandwidth); more rows per wave amortize the per-wave work once the grid is far larger than the
-// chip (the vocabulary-sized head).
-// Rows per wave (U) of the plain GEMV: 1 below 2048 rows (the grid must reach every CU), 2 below
-// 32768, 4 above (measured on MI355X, K = 1024: N = 4096 3.16 us at U = 2 vs 3.49 at U = 1; the
-// 151936-row head 26.1 us at U = 4 vs 26.6 at U = 8).
-int plain_rows_per_wave(int64_t rows) {
-  if (rows < 2048) return 1;
-  if (rows < 32768) return 2;
-  return 4;
-}
+// Rows per wave (measured on MI355X with the kernels above, weights cold). A launch wants at least
+// 256 workgroups (one per CU); below that, more rows per wave only lengthen each wave's chain.
+// Plain GEMV: 1 row per wave below 32768 rows (K = 1024, N = 3072: 2.76 us at U = 1, 2.78 at 2,
+// 3.04 at 4; M = 4 rows of activations: 3.30 us at U = 1 vs 3.66 at 2), 4 above (the head).
+int plain_rows_per_wave(int64_t rows) { return rows < 32768 ? 1 : 4; }
 
-// Rows per wave of the fused quantize + GEMV: every workgroup re-reads and re-quantizes the fp32
-// activation row, so it takes about 16 KB of weights (4 rows of K bytes per wave step): U = 4 for
-// K <= 1024, 2 up to 3072, else 1; doubled when the grid would fill one wave of workgroups and a
-// part of a second (256 < workgroups < 512). Measured on MI355X (K = 1024 unless noted): q/k/v
-// 4096 rows 3.26 us at U = 4 vs 4.34 at U = 1; gate/up 6144 rows 3.87 us at U = 8 vs 4.31 at U = 4
-// and 5.06 at U = 1; o (K = 2048) and down (K = 3072) 1024 rows 3.56 / 3.59 us at U = 2 vs 3.76 /
-// 3.74 at U = 1; the head 26.3 us at U = 4 vs 27.4 at U = 8.
+// Fused quantize + GEMV: every workgroup re-quantizes the activation row, so U is the largest of
+// 1, 2, 4 that still leaves >= 256 workgroups, doubled when the grid would fill one wave of
+// workgroups and part of a second (256 < workgroups < 512). Measured: q/k/v (4096 rows, K = 1024)
+// 3.15 us at U = 4 (3.59 at 2, 3.43 at 8); gate/up (6144 rows) 3.65 us at U = 8 (3.72 at 4);
+// o (K = 2048) and down (K = 3072), 1024 rows, 2.85 / 3.11 us at U = 1 (3.10 / 3.38 at 2); the
+// head (151936 rows) 25.5 us at U = 4 (26.7 at 8).
 int fused_rows_per_wave(int64_t rows, int K) {
-  int u = K <= 1024 ? 4 : K <= 3072 ? 2 : 1;
-  const int64_t wgs = (rows + 4 * u - 1) / (4 * u);
-  if (wgs > 256 && wgs < 512 && u < 8) u *= 2;
+  (void)K;
+  int u = 1;
+  while (u < 4 && rows / (kWaves * 2 * u) >= 256) u *= 2;
+  const int64_t wgs = (rows + kWaves * u - 1) / (kWaves * u);
+  if (wgs > 256 && wgs < 512) u *= 2;
   return u;
 }
 
@@ -487,17 +497,52 @@ hipError_t go(const W8A8Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Output element size of an epilogue format (fp32, bf16, int8, fp16).
+int out_bytes(int out) { return out == 0 ? 4 : out == 2 ? 1 : 2; }
+
+int gcd(int a, int b) {
+  while (b) {
+    const int t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// Matrix pieces as grid z: matrices of unequal height are cut into pieces of their greatest
+// common height when that gives at most kMaxPieces pieces (q/k/v: 2048 + 1024 + 1024 rows ->
+// four pieces of 1024), so every z slice has the same number of workgroups and none idles; other
+// shapes run one slice per matrix, the shorter ones leaving workgroups idle.
 template <int L, int CPL, int U>
 hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
-  int blocks = 0;
+  int h = 0, rows = 0;
   for (int i = 0; i < a.ngroups; ++i) {
-    a.block_start[i] = blocks;
-    blocks += (a.g[i].N + rows_per_block - 1) / rows_per_block;
+    h = gcd(h, a.g[i].N);
+    rows += a.g[i].N;
   }
-  for (int i = a.ngroups; i <= kMaxGroups; ++i) a.block_start[i] = blocks;
+  if (a.ngroups > 1 && rows / h <= kMaxPieces) {
+    GemvGroup pieces[kMaxPieces];
+    int np = 0;
+    for (int i = 0; i < a.ngroups; ++i) {
+      const GemvGroup& gi = a.g[i];
+      for (int r = 0; r < gi.N; r += h) {
+        GemvGroup p = gi;
+        p.W = gi.W + static_cast<int64_t>(r) * a.K;
+        if (!gi.epi.scol_per_tensor) p.epi.scol = gi.epi.scol + r;
+        if (gi.epi.bias) p.epi.bias = gi.epi.bias + r;
+        p.Y = static_cast<char*>(gi.Y) + static_cast<int64_t>(r) * out_bytes(gi.epi.out);
+        p.N = h;
+        pieces[np++] = p;
+      }
+    }
+    for (int i = 0; i < np; ++i) a.g[i] = pieces[i];
+    a.ngroups = np;
+  }
+  int blocks = 0;
+  for (int i = 0; i < a.ngroups; ++i) blocks = max(blocks, (a.g[i].N + rows_per_block - 1) / rows_per_block);
   const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
-  hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U>), dim3(blocks, a.M), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U>), dim3(blocks, a.M, a.ngroups), dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
 

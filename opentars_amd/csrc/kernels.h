@@ -41,6 +41,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Forces a uniform value (a kernel argument) into SGPRs at this point, so its scalar load is issued
+// here, beside the vector loads already in flight, rather than at its first use.
+template <class T>
+__device__ __forceinline__ void pin_sgpr(const T& v) {
+  __asm__ volatile("" : : "s"(v));
+}
+
+// Workgroup ids are dealt round-robin over the 8 XCDs (id % 8). Block index of workgroup x of n
+// such that the workgroups of one XCD take consecutive blocks: the blocks' outputs then share
+// cache lines inside one XCD's L2 instead of across XCDs. A bijection on [0, n).
+__device__ __forceinline__ int xcd_block(int x, int n) {
+  const int r = x & 7, k = x >> 3, per = n >> 3, rem = n & 7;
+  return r * per + min(r, rem) + k;
+}
+
 // Keeps the machine scheduler from moving instructions across this point. Used between groups of
 // loads whose issue order matters for the wait counters (activations before weights before
 // epilogue operands).
@@ -108,7 +123,8 @@ struct W4Args {
 
 // Fused per-token quantizer + grouped W8A8 GEMV: the activation rows are quantized in registers by
 // every wave and feed up to kMaxGroups weight matrices (q/k/v, gate/up) in one launch.
-constexpr int kMaxGroups = 4;
+constexpr int kMaxGroups = 4;   // matrices per call
+constexpr int kMaxPieces = 8;   // equal row pieces they may be cut into (one grid z slice each)
 struct GemvGroup {
   const int8_t* W;       // [N, K] dense
   RowColEpilogue epi;    // srow unused: the row scale comes from the fused quantizer
@@ -124,9 +140,8 @@ struct QuantGemvArgs {
   int64_t ldq;
   float* s;
   int M, K;
-  GemvGroup g[kMaxGroups];
-  int ngroups;
-  int block_start[kMaxGroups + 1];  // first workgroup of each group along grid x
+  GemvGroup g[kMaxPieces];
+  int ngroups;  // matrix (piece) g runs as grid z = g
 };
 
 // Row functions, elementwise ops, rotary embedding and fp32 dot products (rowops.hip). Row strides

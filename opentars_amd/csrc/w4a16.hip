@@ -2,11 +2,12 @@
 // (tars_mini/golden.py:295-324).
 //
 // Work unit: a 16-byte chunk of a packed weight row = 32 int4 weights = a quarter of a 128-wide
-// group. Thread c of a row owns chunk c (so a row of K/2 bytes is read by K/32 consecutive
-// threads, fully coalesced), and the four threads of a group are four consecutive lanes.
+// group. A wave owns whole rows; lane l streams chunks l, l + 64, ... of each (every load
+// instruction reads 1 KiB of a row, fully coalesced), so a group's four chunks sit on four
+// consecutive lanes.
 //
 // Alignment is fused into the GEMV prologue: the workgroup aligns its activation row once,
-// cooperatively (8 lanes per 128-wide group, 16 elements each; the group's exponent maximum meets
+// cooperatively (16 lanes per 128-wide group, 8 elements each; the group's exponent maximum meets
 // through DPP lane permutes), into LDS byte planes that every weight row of the workgroup reads.
 // Each mantissa (an int16 in [-16384, 16384]) is rounded to nearest-even exactly as the reference
 // does: for finite groups as rint(x * 2^(140 - e_eff)), otherwise by the integer shift rule with
@@ -19,9 +20,10 @@
 // final arithmetic shift by 4 is exact. The packed byte holds the even k in its low nibble and the
 // odd k in its high nibble, so the activations are kept as even/odd byte lanes.
 //
-// The per-group fp32 terms (i2f(dot) * ws) * xs go to LDS; four threads per row then run the four
-// bank chains (group g goes to bank g % 4, added in g order from +0) and combine
-// (b0 + b1) + (b2 + b3) before bias, activation and conversion.
+// The per-group fp32 terms (i2f(dot) * ws) * xs go to the wave's own LDS rows; four lanes per
+// row then run the four bank chains (group g goes to bank g % 4, added in g order from +0) and
+// combine (b0 + b1) + (b2 + b3) before bias, activation and conversion. The only workgroup
+// barrier is the one after the alignment.
 //
 // Roofline: HBM. Algorithmic bytes per row: K/2 (weights) + K/64 (fp16 scales) + 4 (output).
 #include "kernels.h"
@@ -201,133 +203,123 @@ __global__ __launch_bounds__(kThreads) void align_w4_kernel(AlignArgs a) {
 }
 
 // ---------------------------------------------------------------------------- GEMV
-// U: rows each thread streams. R = 256 / C rows share a workgroup pass (C = K / 32 chunks per row).
+// One wave owns U whole weight rows: lane l streams chunks l, l + 64, ... (CPL per lane) of each
+// row, so a group's four chunks sit on four consecutive lanes and everything after the activation
+// alignment (the group sums, the terms and the four bank chains) stays inside the wave.
 //
-// 1. Each thread issues its weight loads (U rows x 16 bytes) first.
-// 2. The workgroup aligns activation row m once, cooperatively: 8 consecutive lanes own one
-//    128-wide group (16 elements each), meet their exponent maximum and NaN/inf flags in an 8-lane
-//    DPP reduction, and write the split signed byte planes of their mantissas to LDS in the layout
-//    the dot product reads (per 32-element chunk: lo_even, lo_odd, hi_even, hi_odd, 4 dwords each),
-//    plus the group scale.
-// 3. Each thread reads its chunk's 64 bytes, forms the exact dots, the four lanes of a group add
-//    theirs (quad permutes), the group leader writes the fp32 term to LDS, and four threads per row
-//    run the bank chains.
-template <int U, bool BF16>
+// 1. Loads are issued activations first (the aligner waits on them alone), then the U * CPL weight
+//    chunks, then the group scales and the bias.
+// 2. The workgroup aligns activation row m once: aligner thread t (t < K / 8, CPL passes of 256)
+//    owns elements [8 t, 8 t + 8), 16 consecutive threads form one 128-wide group and meet their
+//    exponent maximum and flags by DPP. The split signed bytes go to LDS plane-major (plane q =
+//    lo_even, lo_odd, hi_even, hi_odd; dword t of each plane), the group scale beside them.
+// 3. After the one workgroup barrier each lane reads its chunks' 64 bytes, forms the exact dots,
+//    adds its group's four lanes (quad permutes), and the group's first lane writes the fp32 term
+//    (i2f(dot) * ws) * xs into the wave's own LDS rows.
+// 4. Lane 4 u + b runs bank b's chain of row u (groups b, b + 4, ... in order from +0, every term
+//    read up front so only the fadds are sequential), and the quad folds (b0 + b1) + (b2 + b3).
+constexpr int kWaves = kThreads / 64;
+constexpr int kTermStride = 65;  // LDS floats per term row (G <= 64), padded against bank conflicts
+
+template <int CPL, int U, bool BF16>
 __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
-  extern __shared__ __align__(16) uint32_t act_lds[];  // C * 16 dwords of byte planes, then G scales
-  __shared__ float terms[64][65];
-  const int C = a.K / 32;
-  const int G = a.K / kGroup;
-  const int R = kThreads / C;
-  const int rows_per_block = R * U;
-  const int m = blockIdx.y;
+  static_assert(CPL >= 1 && CPL <= 4 && U >= 1 && 4 * U <= 64, "K <= 8192; one chain quad per row");
+  extern __shared__ __align__(16) uint32_t planes[];  // 4 planes of 4C dwords, then G scale encodings
+  __shared__ float terms[kWaves][U][kTermStride];
+  const int C = a.K >> 5;
+  const int G = a.K >> 7;
+  const int A = a.K >> 3;  // aligner threads (8 elements each)
   const int tid = threadIdx.x;
-  const int r = tid / C;
-  const int c = tid - r * C;
-  const bool live = r < R;
-  const int cc = live ? c : 0;
-  const int g = cc >> 2;
-
-  const int nbase = blockIdx.x * rows_per_block;
-  const size_t row_bytes = static_cast<size_t>(a.K / 2);
-
-  // Issue order matters: vmcnt counts loads in order, so the activation loads go first (the
-  // alignment waits on them alone), then the weights, then the group scales the epilogue needs.
-  // Lane i of the 8 * G alignment lanes owns elements [16 i, 16 i + 16) of row m; K <= 8192 means
-  // at most two passes of 256 lanes.
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int m = blockIdx.y;
+  const int n0 = (blockIdx.x * kWaves + wave) * U;
+  const int64_t row_bytes = a.K >> 1;
   const char* xrow = static_cast<const char*>(a.x) + m * a.lda;
-  const int npass = (8 * G + kThreads - 1) / kThreads;
-  uint32_t xb[2][16];
+
+  // 1. activations (dead aligner threads shadow the first group's lanes: whole 16-lane groups)
+  uint32_t xb[CPL][8];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    // pass 1 exists only for K > 4096; when it does not, its loads read shadow data (always
-    // issued, never branched around: see load_pred) and the results are never used
-    const int i = p * kThreads + tid;
-    const int ii = i < 8 * G ? i : (i & 7);  // dead lanes shadow group 0 (whole 8-lane groups)
+  for (int p = 0; p < CPL; ++p) {
+    const int t = p * kThreads + tid;
+    const int tt = t < A ? t : (t & 15);
     if constexpr (BF16) {
-      const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * ii);
+      const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * tt);
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const v4u v = src[q];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          xb[p][8 * q + 2 * j] = v[j] << 16;
-          xb[p][8 * q + 2 * j + 1] = v[j] & 0xFFFF0000u;
-        }
+      for (int j = 0; j < 4; ++j) {
+        xb[p][2 * j] = v[j] << 16;
+        xb[p][2 * j + 1] = v[j] & 0xFFFF0000u;
       }
     } else {
-      const v4u* src = reinterpret_cast<const v4u*>(xrow + 64 * ii);
+      const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * tt);
+      const v4u v0 = src[0], v1 = src[1];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const v4u v = src[q];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xb[p][4 * q + j] = v[j];
+      for (int j = 0; j < 4; ++j) {
+        xb[p][j] = v0[j];
+        xb[p][4 + j] = v1[j];
       }
     }
   }
   issue_fence();
-  v4u wv[U];
+  v4u wv[U][CPL];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int n = nbase + u * R + r;
-    wv[u] = load_stream_pred(reinterpret_cast<const v4u*>(a.Wp + n * row_bytes) + cc,
-                             reinterpret_cast<const v4u*>(a.Wp), live && n < a.N, v4u{0u, 0u, 0u, 0u});
+    const int n = n0 + u;
+    const v4u* wrow = reinterpret_cast<const v4u*>(a.Wp + n * row_bytes);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      wv[u][j] = load_stream_pred(wrow + c, reinterpret_cast<const v4u*>(a.Wp), n < a.N && c < C,
+                                  v4u{0u, 0u, 0u, 0u});
+    }
   }
   issue_fence();
-  uint32_t wsb[U];
+  uint32_t wsb[U][CPL];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int n = min(nbase + u * R + r, a.N - 1);
-    wsb[u] = a.ws[static_cast<size_t>(n) * G + g];
+    const int n = min(n0 + u, a.N - 1);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) wsb[u][j] = a.ws[static_cast<int64_t>(n) * G + min((lane + 64 * j) >> 2, G - 1)];
   }
-  // this thread's epilogue row (four threads per row run the bank chains) and its bias, fetched
-  // unconditionally from a valid address
-  const int slot = tid >> 2;
-  const int bank = tid & 3;
-  const bool has_row = slot < rows_per_block;
-  const int slot_c = has_row ? slot : 0;
-  const int ue = slot_c / R, re = slot_c - ue * R;
-  const int ne = nbase + ue * R + re;
+  const int ue = lane >> 2, bank = lane & 3;  // this lane's chain: bank `bank` of row n0 + ue
+  const int ne = n0 + (ue < U ? ue : 0);
   const float bias_v = *(a.bias ? a.bias + min(ne, a.N - 1) : reinterpret_cast<const float*>(a.ws));
   issue_fence();
 
-  // cooperative alignment of row m into LDS byte planes
-  float* xs_lds = reinterpret_cast<float*>(act_lds + C * 16);
+  // 2. cooperative alignment into the LDS planes
+  float* xs_lds = reinterpret_cast<float*>(planes + 16 * C);
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    if (p < npass) {
-      const int i = p * kThreads + tid;
-      const bool valid = i < 8 * G;
-      const int ii = valid ? i : (i & 7);
-      int mant[16];
-      uint32_t sb;
-      align_elems<16, 8>(xb[p], mant, sb);
-      if (valid) {
-        int lo[16], hi[16];
+  for (int p = 0; p < CPL; ++p) {
+    const int t = p * kThreads + tid;
+    int mant[8];
+    uint32_t sb;
+    align_elems<8, 16>(xb[p], mant, sb);
+    if (t < A) {
+      int lo[8], hi[8];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          lo[j] = static_cast<int8_t>(mant[j] & 0xFF);
-          hi[j] = (mant[j] - lo[j]) >> 8;
-        }
-        const int chunk = ii >> 1, half = ii & 1;
-        uint32_t* dst = act_lds + chunk * 16 + 2 * half;
-#pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          dst[0 + d] = pack4(lo[8 * d], lo[8 * d + 2], lo[8 * d + 4], lo[8 * d + 6]);
-          dst[4 + d] = pack4(lo[8 * d + 1], lo[8 * d + 3], lo[8 * d + 5], lo[8 * d + 7]);
-          dst[8 + d] = pack4(hi[8 * d], hi[8 * d + 2], hi[8 * d + 4], hi[8 * d + 6]);
-          dst[12 + d] = pack4(hi[8 * d + 1], hi[8 * d + 3], hi[8 * d + 5], hi[8 * d + 7]);
-        }
-        if ((ii & 7) == 0) xs_lds[ii >> 3] = ffrom(sb);
+      for (int j = 0; j < 8; ++j) {
+        lo[j] = static_cast<int8_t>(mant[j] & 0xFF);
+        hi[j] = (mant[j] - lo[j]) >> 8;
       }
+      planes[t] = pack4(lo[0], lo[2], lo[4], lo[6]);
+      planes[4 * C + t] = pack4(lo[1], lo[3], lo[5], lo[7]);
+      planes[8 * C + t] = pack4(hi[0], hi[2], hi[4], hi[6]);
+      planes[12 * C + t] = pack4(hi[1], hi[3], hi[5], hi[7]);
+      if ((t & 15) == 0) xs_lds[t >> 4] = ffrom(sb);
     }
   }
   __syncthreads();
 
-  ActBytes act;
-  {
-    const v4u* src = reinterpret_cast<const v4u*>(act_lds + cc * 16);
-    const v4u le = src[0], lo = src[1], he = src[2], ho = src[3];
+  // 3. dots and group terms
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    const int cc = c < C ? c : 0;
+    ActBytes act;
+    const v4u le = *reinterpret_cast<const v4u*>(planes + 4 * cc);
+    const v4u lo = *reinterpret_cast<const v4u*>(planes + 4 * C + 4 * cc);
+    const v4u he = *reinterpret_cast<const v4u*>(planes + 8 * C + 4 * cc);
+    const v4u ho = *reinterpret_cast<const v4u*>(planes + 12 * C + 4 * cc);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       act.lo_even[d] = le[d];
@@ -335,47 +327,60 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
       act.hi_even[d] = he[d];
       act.hi_odd[d] = ho[d];
     }
-  }
-  const float xs = xs_lds[g];
-
+    const float xs = xs_lds[cc >> 2];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    int d16 = chunk_dot16(wv[u], act);
-    d16 += lane_xor1(d16);
-    d16 += lane_xor2(d16);
-    const int n = nbase + u * R + r;
-    if (live && (cc & 3) == 0 && n < a.N) {
-      terms[u * R + r][g] = fmul(fmul(i2f(d16 >> 4), from_fp16_bits(wsb[u])), xs);
+    for (int u = 0; u < U; ++u) {
+      int d16 = chunk_dot16(wv[u][j], act);
+      d16 += lane_xor1(d16);
+      d16 += lane_xor2(d16);
+      if ((lane & 3) == 0 && c < C && n0 + u < a.N)
+        terms[wave][u][c >> 2] = fmul(fmul(i2f(d16 >> 4), from_fp16_bits(wsb[u][j])), xs);
     }
   }
-  __syncthreads();
+  // the terms were written by other lanes of this wave: order the LDS accesses (no block barrier)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // four bank chains per row, then (b0 + b1) + (b2 + b3)
+  // 4. four bank chains per row, then (b0 + b1) + (b2 + b3)
+  const float* trow = terms[wave][ue < U ? ue : 0];
+  float tv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tv[i] = trow[bank + 4 * i];  // index <= 63 < kTermStride
   float acc = 0.0f;
-  for (int gg = bank; gg < G; gg += 4) acc = fadd(acc, terms[slot_c][gg]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (bank + 4 * i < G) acc = fadd(acc, tv[i]);
   const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
   const float other = lane_xor2(pair);
-  if (has_row && bank == 0 && ne < a.N) {
+  if (bank == 0 && ue < U && n0 + ue < a.N) {
     float y = fadd(pair, other);
     if (a.bias) y = fadd(y, bias_v);
     y = act_fn(y, a.act);
-    store_out(a.Y, m * a.ldy, ne, a.out, y, a.out_scale);
+    store_out(a.Y, m * a.ldy, n0 + ue, a.out, y, a.out_scale);
   }
 }
 
-template <int U>
+template <int CPL, int U>
 hipError_t go_w4(const W4Args& a, hipStream_t s) {
-  const int C = a.K / 32;
-  const int R = kThreads / C;
-  const int rows = R * U;
-  const dim3 grid((a.N + rows - 1) / rows, a.M);
-  const size_t lds = static_cast<size_t>(C) * 64 + static_cast<size_t>(a.K / kGroup) * 4;
+  const dim3 grid((a.N + kWaves * U - 1) / (kWaves * U), a.M);
+  const size_t lds = static_cast<size_t>(a.K / 32) * 64 + static_cast<size_t>(a.K / kGroup) * 4;
   if (a.bf16) {
-    hipLaunchKernelGGL((gemv_w4a16_kernel<U, true>), grid, dim3(kThreads), lds, s, a);
+    hipLaunchKernelGGL((gemv_w4a16_kernel<CPL, U, true>), grid, dim3(kThreads), lds, s, a);
   } else {
-    hipLaunchKernelGGL((gemv_w4a16_kernel<U, false>), grid, dim3(kThreads), lds, s, a);
+    hipLaunchKernelGGL((gemv_w4a16_kernel<CPL, U, false>), grid, dim3(kThreads), lds, s, a);
   }
   return hipGetLastError();
+}
+
+template <int CPL>
+hipError_t go_w4_rows(const W4Args& a, int u, hipStream_t s) {
+  switch (u) {
+    case 1: return go_w4<CPL, 1>(a, s);
+    case 2: return go_w4<CPL, 2>(a, s);
+    case 4: return go_w4<CPL, 4>(a, s);
+    default: return go_w4<CPL, 8>(a, s);
+  }
 }
 
 }  // namespace
@@ -387,16 +392,25 @@ hipError_t launch_align_w4(const AlignArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Rows per wave: every workgroup aligns the whole activation row, so U trades that repeated work
+// (workgroups x K elements) against workgroups in flight: the smallest U in {1, 2, 4, 8} that keeps
+// the repeated alignment within 1.5M elements. Measured on MI355X: K = 1536, N = 12288 6.59 us at
+// U = 4 (7.01 at U = 2, 7.55 at U = 8); K = 6144, N = 1536 5.53 us at U = 2 (5.81 at U = 1, 7.51
+// at U = 4).
+static int w4_rows_per_wave(int64_t N, int K) {
+  int u = 1;
+  while (u < 8 && (N + kWaves * u - 1) / (kWaves * u) * K > 3 * (1 << 19)) u *= 2;
+  return u;
+}
+
 hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
-  // Rows per block R * U must not exceed the 64 LDS term rows. Long rows (R <= 2, K >= 4096)
-  // take 8 rows per thread so the activation row is read and aligned once per 8 * R weight rows;
-  // shorter rows take 4, which keeps >= 600 workgroups at N = 12288 (measured on MI355X:
-  // K=6144 N=1536 8.0 us at U=8 vs 10.2 at U=4; K=1536 N=12288 8.7 us at U=4 vs 9.3 at U=8).
-  const int R = kThreads / (a.K / 32);
-  if (R <= 2) return go_w4<8>(a, s);
-  if (R * 4 <= 64) return go_w4<4>(a, s);
-  if (R * 2 <= 64) return go_w4<2>(a, s);
-  return go_w4<1>(a, s);
+  const int u = w4_rows_per_wave(a.N, a.K);
+  switch ((a.K / 32 + 63) / 64) {  // chunks per lane
+    case 1: return go_w4_rows<1>(a, u, s);
+    case 2: return go_w4_rows<2>(a, u, s);
+    case 3: return go_w4_rows<3>(a, u, s);
+    default: return go_w4_rows<4>(a, u, s);
+  }
 }
 
 }  // namespace tars
