@@ -534,12 +534,16 @@ def kernel_instance(l: Launch) -> str:
     if l.kind == "quant_gemm_w8a8":
         K = l.args[6]
         rows = sum(d.N for d in l.operands["descs"])
+        simple = all(not d.bias and d.act == 0 and d.out == 0 for d in l.operands["descs"])
         name, u, tail = "quant_gemv_w8a8_kernel", fused_rows_per_wave(rows, K), ""
     elif l.kind == "gemm_w8a8" and l.args[9] == 1:
         K, rows = l.args[11], l.args[10]
+        simple = l.args[2] is not None and l.args[6] is None and l.args[12] == 0 and l.args[13] == 0
         name, u, tail = "gemv_w8a8_kernel", plain_rows_per_wave(rows), ", 1"
     else:
         return l.kind
+    # the epilogue instance: true for QM_ROWCOL with fp32 output and no bias or activation
+    tail += ", true" if simple else ", false"
     c = K // 16
     if c <= 32:
         lanes = 8 if c <= 8 else 16 if c <= 16 else 32

@@ -178,6 +178,19 @@ __device__ __forceinline__ int q8_flushed_inv(float x, float inv) {
   return static_cast<int>(fminf(fmaxf(y, -127.0f), 127.0f));
 }
 
+// q8 for a row whose maximum amax = max |ftz(x)| is finite and at least 2^-118 (every row but
+// all-tiny, all-zero, infinity and NaN rows): the row holds no NaN or infinity, a normal x is its
+// own flush, and a subnormal x gives |x * inv| < 2^-126 * 127 * 2^118 * (1 + 2^-22) < 1/2, which
+// rounds to the 0 its flush gives; so q8 is rint(x * inv) clamped, with no flush or NaN test
+// (checked on the CPU: every subnormal at the smallest maxima, random rows across the range).
+constexpr uint32_t kQ8FastMin = 0x04800000u;  // 2^-118
+__device__ __forceinline__ bool q8_fast_row(uint32_t amax_bits) {
+  return amax_bits >= kQ8FastMin && amax_bits < kExpo;
+}
+__device__ __forceinline__ int q8_fast(float x, float inv) {
+  return static_cast<int>(fminf(fmaxf(__builtin_rintf(__fmul_rn(x, inv)), -127.0f), 127.0f));
+}
+
 // numerics.py:270-275: FTZ, round-to-nearest-even to the top 16 bits, NaN -> 0x7FC0
 __device__ __forceinline__ uint16_t to_bf16_bits(float x) {
   const uint32_t b = fbits(ftz(x));
@@ -331,6 +344,12 @@ __device__ __forceinline__ uint32_t q8x4(float a, float b, float c, float d, flo
          ((static_cast<uint32_t>(q8_flushed_inv(b, inv)) & 0xFFu) << 8) |
          ((static_cast<uint32_t>(q8_flushed_inv(c, inv)) & 0xFFu) << 16) |
          ((static_cast<uint32_t>(q8_flushed_inv(d, inv)) & 0xFFu) << 24);
+}
+
+// Four fast-path q8 bytes packed little-endian (a row for which q8_fast_row holds).
+__device__ __forceinline__ uint32_t q8x4_fast(float a, float b, float c, float d, float inv) {
+  return (static_cast<uint32_t>(q8_fast(a, inv)) & 0xFFu) | ((static_cast<uint32_t>(q8_fast(b, inv)) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(q8_fast(c, inv)) & 0xFFu) << 16) | ((static_cast<uint32_t>(q8_fast(d, inv)) & 0xFFu) << 24);
 }
 
 }  // namespace tars

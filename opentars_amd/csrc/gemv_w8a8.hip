@@ -45,7 +45,20 @@ __device__ __forceinline__ int dot16(v4i w, v4i x, int acc) {
 // CPL == 0: any K, chunks walked in a loop with the activation chunk re-read from cache.
 // MR activation rows per block (prefill chunks, M <= 8): every weight chunk loaded feeds the
 // dot products of all MR rows, so the weights are read once per MR rows (MR * U <= L).
-template <int L, int CPL, int U, int MR>
+// The epilogue of QM_ROWCOL with fp32 output and neither bias nor activation (the decode-step
+// linears and the lm_head): the golden's steps fmul(fmul(i2f(acc), srow), scol) and the output
+// flush, with the general epilogue's code (every activation and output format) compiled out, which
+// a cold launch otherwise fetches (measured: 0.05 - 0.2 us per launch).
+__device__ __forceinline__ float simple_epilogue(int acc, float sr, float sc) {
+  return ftz(fmul(fmul(i2f(acc), sr), sc));
+}
+
+// Whether an epilogue is that simple one (plain GEMV: it also needs a row scale).
+bool simple_epi(const RowColEpilogue& e, bool need_srow) {
+  return (!need_srow || e.srow != nullptr) && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0;
+}
+
+template <int L, int CPL, int U, int MR, bool SIMPLE>
 __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   static_assert(MR == 1 || CPL > 0, "several activation rows need the register-held activations");
   static_assert(MR * U <= L, "one epilogue lane per (row, weight row)");
@@ -151,8 +164,12 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
     for (int u = 0; u < U; ++u)
       if (sub == r * U + u) mine = acc[r][u];
   if (epi_lane) {
-    const float y = a.epi.apply(mine, sr, a.epi.srow != nullptr, sc, bi);
-    store_out(a.Y, me * a.ldy, ne, a.epi.out, y, a.epi.out_scale);
+    if constexpr (SIMPLE) {
+      reinterpret_cast<float*>(static_cast<char*>(a.Y) + me * a.ldy)[ne] = simple_epilogue(mine, sr, sc);
+    } else {
+      const float y = a.epi.apply(mine, sr, a.epi.srow != nullptr, sc, bi);
+      store_out(a.Y, me * a.ldy, ne, a.epi.out, y, a.epi.out_scale);
+    }
   }
 }
 
@@ -302,13 +319,15 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSpli
 // Each workgroup quantizes the activation row once: its 256 threads read the fp32 row in float4s
 // (a single pass over 4K bytes, mostly L2 hits after the first workgroup), the row maximum meets
 // through wave shuffles and 4 LDS words, every thread runs the fixed recip_f sequence, and the
-// q8 bytes land in LDS where each lane picks up the 16-byte chunks its dot products need. The
-// weight loads are issued with the activations, so the quantizer runs under their HBM latency.
+// q8 bytes land in LDS where each lane picks up the 16-byte chunks its dot products need; rows
+// whose maximum allows it take q8's fast form (q8_fast_row). The weight loads are issued with the
+// activations, so the quantizer runs under their HBM latency. (A wave-local quantizer, each lane
+// packing its own chunk in registers with no LDS or barrier, measured the same.)
 // Weight matrix g of the launch is grid z = g (its fields are read at a fixed kernel-argument
 // offset, with no dependent load before the weight stream); a matrix with fewer row blocks than
 // the grid's x extent leaves the excess workgroups idle. The first workgroup of matrix 0 also
 // stores the quantized row and its scale (the ROW_QUANT outputs the golden model writes).
-template <int L, int CPL, int U>
+template <int L, int CPL, int U, bool SIMPLE>
 __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs a) {
   extern __shared__ __align__(16) int8_t qsh[];  // the quantized row, K bytes
   __shared__ uint32_t wave_max[kWaves];
@@ -370,6 +389,8 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 
   // the workgroup quantizes row m into LDS
   uint32_t mx = 0;
+  float inv, sr;
+  const bool store_q = a.q != nullptr && blockIdx.x == 0 && blockIdx.z == 0;
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
@@ -386,15 +407,15 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   if (lane == 0) wave_max[wave] = mx;
   __syncthreads();
   mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
-  float inv, sr;
   quant_scales(mx, inv, sr);
-  const bool store_q = a.q != nullptr && blockIdx.x == 0 && blockIdx.z == 0;
+  const bool fast = q8_fast_row(mx);
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       const int i = threadIdx.x + j * kThreads;
       if (i < K4) {
-        const uint32_t b = q8x4(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv);
+        const uint32_t b = fast ? q8x4_fast(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv)
+                                : q8x4(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv);
         reinterpret_cast<uint32_t*>(qsh)[i] = b;
         if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
       }
@@ -446,8 +467,12 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
   for (int u = 0; u < U; ++u)
     if (sub == u) mine = acc[u];
   if (epi_lane) {
-    const float y = gr.epi.apply(mine, sr, true, sc, bi);
-    store_out(gr.Y, m * gr.ldy, ne, gr.epi.out, y, gr.epi.out_scale);
+    if constexpr (SIMPLE) {
+      reinterpret_cast<float*>(static_cast<char*>(gr.Y) + m * gr.ldy)[ne] = simple_epilogue(mine, sr, sc);
+    } else {
+      const float y = gr.epi.apply(mine, sr, true, sc, bi);
+      store_out(gr.Y, m * gr.ldy, ne, gr.epi.out, y, gr.epi.out_scale);
+    }
   }
 }
 
@@ -479,21 +504,21 @@ int ksplit_rows_per_wave(int64_t rows) {
   return 4;
 }
 
-template <int L, int CPL, int U>
+template <int L, int CPL, int U, bool SIMPLE>
 hipError_t go(const W8A8Args& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
   const unsigned nb = (a.N + rows_per_block - 1) / rows_per_block;
   if constexpr (CPL > 0 && 4 * U <= L) {
     if (a.M >= 3) {
-      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 4>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 4, SIMPLE>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a);
       return hipGetLastError();
     }
     if (a.M == 2) {
-      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 2>), dim3(nb, 1), dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 2, SIMPLE>), dim3(nb, 1), dim3(kThreads), 0, s, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 1>), dim3(nb, a.M), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 1, SIMPLE>), dim3(nb, a.M), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -513,7 +538,7 @@ int gcd(int a, int b) {
 // common height when that gives at most kMaxPieces pieces (q/k/v: 2048 + 1024 + 1024 rows ->
 // four pieces of 1024), so every z slice has the same number of workgroups and none idles; other
 // shapes run one slice per matrix, the shorter ones leaving workgroups idle.
-template <int L, int CPL, int U>
+template <int L, int CPL, int U, bool SIMPLE>
 hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
   int h = 0, rows = 0;
@@ -542,7 +567,7 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   int blocks = 0;
   for (int i = 0; i < a.ngroups; ++i) blocks = max(blocks, (a.g[i].N + rows_per_block - 1) / rows_per_block);
   const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
-  hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U>), dim3(blocks, a.M, a.ngroups), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE>), dim3(blocks, a.M, a.ngroups), dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
 
@@ -572,11 +597,17 @@ hipError_t dispatch(Args& a, int K, int u, hipStream_t s) {
 
 template <int L, int CPL, int U>
 struct GoPlain {
-  static hipError_t run(const W8A8Args& a, hipStream_t s) { return go<L, CPL, U>(a, s); }
+  static hipError_t run(const W8A8Args& a, hipStream_t s) {
+    return simple_epi(a.epi, true) ? go<L, CPL, U, true>(a, s) : go<L, CPL, U, false>(a, s);
+  }
 };
 template <int L, int CPL, int U>
 struct GoFused {
-  static hipError_t run(QuantGemvArgs& a, hipStream_t s) { return go_fused<L, CPL, U>(a, s); }
+  static hipError_t run(QuantGemvArgs& a, hipStream_t s) {
+    bool simple = true;
+    for (int i = 0; i < a.ngroups; ++i) simple = simple && simple_epi(a.g[i].epi, false);
+    return simple ? go_fused<L, CPL, U, true>(a, s) : go_fused<L, CPL, U, false>(a, s);
+  }
 };
 
 }  // namespace

@@ -118,3 +118,39 @@ def test_aligner_fast_path_matches_the_oracle_on_finite_groups():
         sel = np.ones_like(emax, bool) if flushed else emax >= 16
         assert sel.sum() > 100
         assert (fast[sel] == want[sel]).all()
+
+
+def test_q8_fast_path_for_rows_with_a_normal_maximum():
+    """A quantizer row whose maximum amax = max |ftz(x)| is finite and at least 2^-118 skips q8's
+    input flush and NaN test: with inv = fmul(127, recip_f(amax)), q8(x, inv) equals
+    clamp(rint(x * inv), -127, 127) on the unflushed x. Such a row holds no NaN or infinity, a normal
+    x is its own flush, and a subnormal x (|x| < 2^-126) gives |x * inv| < 2^-126 * 127 * 2^118 *
+    (1 + 2^-22) < 1/2, which rounds to the 0 its flush gives. Exhaustive over every subnormal at the
+    smallest maxima; random rows (extremes, exact ties, tiny normals) across the whole range."""
+    rng = np.random.default_rng(7)
+    edge = np.array([0x04800000, 0x04800001, 0x04800007, 0x04FFFFFF, 0x05000000], np.uint32).view(f32)
+    sub = np.arange(1, 1 << 23, dtype=np.uint32)
+    sub = np.concatenate([sub, sub | np.uint32(0x80000000)]).view(f32)       # every nonzero subnormal
+    for amax in edge:
+        inv = F.fmul(F.Q127, F.recip_f(np.array([amax], f32)))[0]
+        with np.errstate(all="ignore"):
+            fast = np.clip(np.rint(sub * inv), -127, 127)
+        assert (fast == 0).all(), amax
+        assert (F.q8(sub, inv) == 0).all()
+    # random maxima over every exponent from 2^-118 to the largest finite value
+    mb = np.concatenate([(rng.integers(9, 255, 400, dtype=np.uint32) << 23) | rng.integers(0, 1 << 23, 400, dtype=np.uint32),
+                         np.array([0x04800000, 0x7F7FFFFF, 0x3F800000, 0x42FE0000], np.uint32)])
+    for amax in mb.view(f32):
+        inv = F.fmul(F.Q127, F.recip_f(np.array([amax], f32)))[0]
+        u = rng.uniform(-1, 1, 4000).astype(f32)
+        x = np.concatenate([
+            (u * amax).astype(f32),                                          # inside [-amax, amax]
+            np.array([amax, -amax, 0.0, -0.0], f32),
+            ((rng.integers(-127, 127, 200) + f32(0.5)) / inv).astype(f32),   # near the q8 ties
+            sub[rng.integers(0, sub.size, 200)],                              # subnormal inputs
+            (np.uint32(0x00800000) + rng.integers(0, 1 << 20, 100, dtype=np.uint32)).view(f32),  # tiny normals
+        ])
+        x = x[np.abs(F.ftz(x)) <= amax]
+        with np.errstate(all="ignore"):
+            fast = np.clip(np.rint(x * inv), -127, 127).astype(np.int8)
+        assert (fast == F.q8(x, inv)).all(), amax
