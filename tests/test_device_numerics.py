@@ -143,10 +143,12 @@ def test_q8_fast_path_for_rows_with_a_normal_maximum():
     for amax in mb.view(f32):
         inv = F.fmul(F.Q127, F.recip_f(np.array([amax], f32)))[0]
         u = rng.uniform(-1, 1, 4000).astype(f32)
+        with np.errstate(divide="ignore"):           # inv is 0 for the largest maxima (q8 is then 0)
+            ties = ((rng.integers(-127, 127, 200) + f32(0.5)) / inv).astype(f32)
         x = np.concatenate([
             (u * amax).astype(f32),                                          # inside [-amax, amax]
             np.array([amax, -amax, 0.0, -0.0], f32),
-            ((rng.integers(-127, 127, 200) + f32(0.5)) / inv).astype(f32),   # near the q8 ties
+            ties,                                                             # near the q8 ties
             sub[rng.integers(0, sub.size, 200)],                              # subnormal inputs
             (np.uint32(0x00800000) + rng.integers(0, 1 << 20, 100, dtype=np.uint32)).view(f32),  # tiny normals
         ])
