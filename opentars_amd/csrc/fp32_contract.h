@@ -35,6 +35,18 @@ __device__ __forceinline__ float canon(float x) { return is_nan(x) ? ffrom(kCano
 __device__ __forceinline__ float fmul(float a, float b) { return canon(ftz(__fmul_rn(ftz(a), ftz(b)))); }
 __device__ __forceinline__ float fadd(float a, float b) { return canon(ftz(__fadd_rn(ftz(a), ftz(b)))); }
 
+// One step of a summation chain over flushed values: the contract's fadd without its input
+// flushes (identities here) and without the per-step NaN canonicalization. NaN is absorbing in a
+// sum (NaN + x is NaN for every x), so a chain's result is NaN exactly when the contract's
+// step-by-step chain's is, and every other step is the same rounded, flushed value; the chain's
+// result is canonicalized once at its end (chain_end). The flush tests the value class (+-
+// subnormal) in one compare.
+__device__ __forceinline__ float fadd_chain(float acc, float p) {
+  const float r = __fadd_rn(acc, p);
+  return __builtin_amdgcn_class(r, 0x90) ? ffrom(fbits(r) & kSign) : r;
+}
+__device__ __forceinline__ float chain_end(float acc) { return canon(acc); }
+
 // numerics.py:50-52: int32 -> fp32 round-to-nearest-even (v_cvt_f32_i32)
 __device__ __forceinline__ float i2f(int32_t i) { return static_cast<float>(i); }
 

@@ -26,18 +26,6 @@ __device__ __forceinline__ float fdpp_xor2(float v) { return __int_as_float(dpp<
 __device__ __forceinline__ float fdpp_half(float v) { return __int_as_float(dpp<kDppRowHalfMirror>(__float_as_int(v))); }
 __device__ __forceinline__ float fdpp_mirror(float v) { return __int_as_float(dpp<kDppRowMirror>(__float_as_int(v))); }
 
-// One step of a summation chain over flushed values: the contract's fadd without its input
-// flushes (identities here) and without the per-step NaN canonicalization. NaN is absorbing in a
-// sum (NaN + x is NaN for every x), so a chain's result is NaN exactly when the contract's
-// step-by-step chain's is, and every other step is the same rounded, flushed value; the chain's
-// result is canonicalized once at its end (chain_end). The flush tests the value class (+-
-// subnormal) in one compare.
-__device__ __forceinline__ float fadd_chain(float acc, float p) {
-  const float r = __fadd_rn(acc, p);
-  return __builtin_amdgcn_class(r, 0x90) ? ffrom(fbits(r) & kSign) : r;
-}
-__device__ __forceinline__ float chain_end(float acc) { return canon(acc); }
-
 // The pairwise fold of a 16-lane group's partial chain sums (every lane receives the row sum,
 // canonicalized).
 __device__ __forceinline__ float fold16(float v) {
