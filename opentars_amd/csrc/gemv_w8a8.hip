@@ -224,18 +224,22 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_kernel(KSplitArgs a
   }
 }
 
-// K split with every load in flight at once (total K <= 64 * 16 * CPL): the blocks' columns are
-// consecutive, so chunk c of the concatenated row is activation bytes 16c.. and lies in the block b
-// whose chunk range holds it; lane `lane` owns chunks lane, lane + 64, ... of U rows. All activation
-// chunks are issued, then all weight chunks, then the dot products are summed per block (exact
-// int32, each block's sum on its own), reduced across the wave, and the blocks' fp32 partials are
-// added in block order as in gemv_w8a8_ksplit_kernel.
-template <int CPL, int U>
-__global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSplitArgs a) {
+// K split with each row's chunks spread over WPR waves of the workgroup (4 / WPR rows per
+// workgroup): wave part p of a row takes the 1 KiB slices p, p + WPR, ... of the concatenated row
+// (lane l: chunk 64 (p + WPR j) + l, CPL of them), so a launch has WPR times the workgroups of one
+// wave per row and each lane keeps only CPL loads in flight. Per block, a wave's exact int32 sum
+// meets the row's other parts in LDS after one barrier (integer adds, order-free), then lane 0 of
+// part 0 forms each block's partial (i2f(acc) * srow) * scol and adds them in block order.
+template <int CPL, int WPR>
+__global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_rows_kernel(KSplitArgs a) {
+  constexpr int kRowsPerWg = kWaves / WPR;
+  __shared__ int part_sum[kWaves][kMaxBlocks];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int rs = wave / WPR, kp = wave % WPR;
   const int m = blockIdx.y;
-  const int n0 = (xcd_block(blockIdx.x, gridDim.x) * kWaves + wave) * U;
+  const int n = xcd_block(blockIdx.x, gridDim.x) * kRowsPerWg + rs;
+  const int nc = min(n, a.N - 1);
   const v4i zero = {0, 0, 0, 0};
   int cstart[kMaxBlocks + 1];
   cstart[0] = 0;
@@ -243,22 +247,24 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSpli
   for (int b = 0; b < kMaxBlocks; ++b) cstart[b + 1] = cstart[b] + (b < a.nblocks ? a.K[b] >> 4 : 0);
   const int ctot = cstart[kMaxBlocks];
   const v4i* xrow = reinterpret_cast<const v4i*>(a.A + m * a.lda);
-  // block of each of this lane's chunks (blocks are few and ascending: a compare chain)
   int blk[CPL], cin[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = min(lane + 64 * j, ctot - 1);
+    const int c = min(64 * (kp + WPR * j) + lane, ctot - 1);
     int b = 0;
 #pragma unroll
     for (int i = 1; i < kMaxBlocks; ++i) b += (i < a.nblocks && c >= cstart[i]) ? 1 : 0;
     blk[j] = b;
     cin[j] = c;
   }
+  // one batch of loads: activations, epilogue operands, weights (every address in bounds: chunks
+  // past the row re-read its last chunk and are zeroed on the activation side after the batch)
   v4i xv[CPL];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) xv[j] = load_pred(xrow + cin[j], xrow, lane + 64 * j < ctot, zero);
-  issue_fence();
-  v4i wv[U][CPL];
+  for (int j = 0; j < CPL; ++j) xv[j] = xrow[cin[j]];
+  const float sr = *(a.srow ? a.srow + m : a.scol);  // unconditional (see fp32_contract.h)
+  const float sc = a.scol[nc];
+  v4i wv[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int b = blk[j];
@@ -271,47 +277,35 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_flight_kernel(KSpli
         Kb = a.K[i];
         cb = cstart[i];
       }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int n = n0 + u;
-      wv[u][j] = load_stream_pred(reinterpret_cast<const v4i*>(Wb + static_cast<int64_t>(n) * Kb) + (cin[j] - cb),
-                                  reinterpret_cast<const v4i*>(a.W[0]), n < a.N && lane + 64 * j < ctot, zero);
-    }
+    wv[j] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(Wb + static_cast<int64_t>(nc) * Kb) + (cin[j] - cb));
   }
   issue_fence();
-  const float sr = *(a.srow ? a.srow + m : a.scol);  // unconditional (see fp32_contract.h)
-  float sc[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) sc[u] = a.scol[min(n0 + u, a.N - 1)];
-  issue_fence();
-  int d[U][CPL];
+  for (int j = 0; j < CPL; ++j)
+    if (64 * (kp + WPR * j) + lane >= ctot) xv[j] = zero;
+  int d[CPL];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) d[u][j] = dot16(wv[u][j], xv[j], 0);
-  float y[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) y[u] = 0.0f;
+  for (int j = 0; j < CPL; ++j) d[j] = dot16(wv[j], xv[j], 0);
   for (int b = 0; b < a.nblocks; ++b) {
+    int acc = 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int acc = 0;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) acc += blk[j] == b ? d[u][j] : 0;
-      const int s = group_sum<64>(acc);
-      float part = i2f(s);
-      if (a.srow) part = fmul(part, sr);
-      part = fmul(part, sc[u]);
-      y[u] = b == 0 ? part : fadd(y[u], part);
-    }
+    for (int j = 0; j < CPL; ++j) acc += blk[j] == b ? d[j] : 0;
+    acc = group_sum<64>(acc);
+    if (lane == 0) part_sum[wave][b] = acc;
   }
-  float mine = 0.0f;
+  __syncthreads();
+  if (kp == 0 && lane == 0 && n < a.N) {
+    float y = 0.0f;
+    for (int b = 0; b < a.nblocks; ++b) {
+      int s = 0;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (lane == u) mine = y[u];
-  const int n = n0 + lane;
-  if (lane < U && n < a.N) {
-    reinterpret_cast<float*>(reinterpret_cast<char*>(a.Y) + m * a.ldy)[n] = ftz(mine);
+      for (int p = 0; p < WPR; ++p) s += part_sum[rs * WPR + p][b];
+      float pb = i2f(s);
+      if (a.srow) pb = fmul(pb, sr);
+      pb = fmul(pb, sc);
+      y = b == 0 ? pb : fadd(y, pb);
+    }
+    reinterpret_cast<float*>(reinterpret_cast<char*>(a.Y) + m * a.ldy)[n] = ftz(y);
   }
 }
 
@@ -622,29 +616,21 @@ hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
   return dispatch<QuantGemvArgs, GoFused>(a, a.K, fused_rows_per_wave(rows, a.K), s);
 }
 
-// One weight row per wave: measured on MI355X at C2 (K = 6912 in 2 or 3 blocks, N = 1152), 5.8-6.0 us
-// against 6.1-7.3 us for the loop kernel; 2 rows per wave or 5-8 waves per workgroup were slower.
-template <int CPL>
-hipError_t go_ksplit_flight(const KSplitArgs& a, hipStream_t s) {
-  const dim3 grid((a.N + kWaves - 1) / kWaves, a.M);
-  hipLaunchKernelGGL((gemv_w8a8_ksplit_flight_kernel<CPL, 1>), grid, dim3(kThreads), 0, s, a);
+// K split up to a total K of 8192: four waves per row (measured on MI355X at C2, K = 6912 in two
+// blocks, N = 1152: 4.65 us, against 5.7 us for two waves per row and for one wave per row with
+// every chunk of the row in flight).
+template <int CPL, int WPR>
+hipError_t go_ksplit_rows(const KSplitArgs& a, hipStream_t s) {
+  constexpr int rows = kWaves / WPR;
+  const dim3 grid((a.N + rows - 1) / rows, a.M);
+  hipLaunchKernelGGL((gemv_w8a8_ksplit_rows_kernel<CPL, WPR>), grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s) {
   int ctot = 0;
   for (int i = 0; i < a.nblocks; ++i) ctot += a.K[i] >> 4;
-  switch ((ctot + 63) / 64) {  // total K <= 8192: every load in flight at once
-    case 1: return go_ksplit_flight<1>(a, s);
-    case 2: return go_ksplit_flight<2>(a, s);
-    case 3: return go_ksplit_flight<3>(a, s);
-    case 4: return go_ksplit_flight<4>(a, s);
-    case 5: return go_ksplit_flight<5>(a, s);
-    case 6: return go_ksplit_flight<6>(a, s);
-    case 7: return go_ksplit_flight<7>(a, s);
-    case 8: return go_ksplit_flight<8>(a, s);
-    default: break;
-  }
+  if (ctot <= 512) return ctot <= 256 ? go_ksplit_rows<1, 4>(a, s) : go_ksplit_rows<2, 4>(a, s);
   const int u = ksplit_rows_per_wave(a.N);
   const int rows_per_block = kWaves * u;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block, a.M);
