@@ -556,10 +556,12 @@ def kernel_instance(l: Launch) -> str:
 
 
 def instance_times(torch, step_graph, launches, reps: int = 5) -> dict:
-    """Average launch duration of every kernel instance in the step, from HIP events around a
-    graph of that instance's launches (step order, same buffers). Before each timed replay the full
-    step and then the largest other instance are replayed, so at least ~300 MB (more than the
-    256 MB MALL) stream between two uses of any weight and every timed launch starts cold."""
+    """Average launch duration of every kernel instance in the step: HIP events around a graph of
+    that instance's launches from the step (same buffers, step order), i.e. the time each launch
+    adds to a dependent chain. Before each timed replay the full step and then the largest other
+    instance are replayed, so at least ~300 MB (more than the 256 MB MALL) stream between two uses
+    of any weight and every timed launch starts cold. (Events around one launch at a time cannot
+    time it: the event packets alone add several microseconds.)"""
     fams = {}
     for l in launches:
         fams.setdefault(kernel_instance(l), []).append(l)
