@@ -517,6 +517,22 @@ def test_fused_quant_gemm_matches_separate_ops(K, M):
         assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("Ns", [[64, 32, 32], [48, 96], [128, 64, 32, 32], [96, 32, 160, 32]])
+@pytest.mark.parametrize("K,M", [(1024, 1), (2048, 4), (16, 1)])
+def test_fused_equal_row_pieces(Ns, K, M):
+    """Matrices of unequal height cut into equal row pieces (their greatest common height, at most 8
+    pieces; one grid slice each): every piece's weights, scales, bias and output rows are offset
+    from its matrix's, for every output format and with biases and activations."""
+    rng = np.random.default_rng(sum(Ns) + K + M)
+    x, mats = fused_case(rng, M, K, Ns, edge_rows=True)
+    outs = ops.quant_gemm_rowcol(cuda(x), [(cuda(W), cuda(sc), None if b is None else cuda(b), a, o, osc)
+                                           for W, sc, b, a, o, osc in mats])
+    q, s = F.quant_rows(x)
+    for (W, sc, b, a, o, osc), y in zip(mats, outs):
+        want = G.gemm_rowcol(q, s, W, sc, b, act=a, out=o, out_scale=osc)
+        assert same(host(y), want), (Ns, mismatch(host(y), want))
+
+
 def test_fused_qwen3_layer_groups_full_size():
     """q/k/v (2048 + 1024 + 1024 rows) and gate/up (2 x 3072 rows) at K = 1024, and the head."""
     rng = np.random.default_rng(123)
