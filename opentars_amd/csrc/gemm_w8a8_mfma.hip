@@ -263,12 +263,16 @@ __device__ __forceinline__ void issue_stage(int8_t* lds, const int8_t* const (&s
   for (int u = 0; u < L; ++u) stage16(src[u] + static_cast<int64_t>(KS) * st, slot + 1024 * (wave + u * NW));
 }
 
-template <int BM, int BN, int WM, int WN, int KS, int S>
+template <int BM, int BN, int WM, int WN, int KS, int S, bool SIMPLE>
 __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
   constexpr int NW = WM * WN, TI = BM / 16 / WM, TJ = BN / 16 / WN, GA = BM / 16, G = (BM + BN) / 16;
   constexpr int KBS = KS / 64, BLK = G * KBS, L = BLK / NW, SLOT = 1024 * BLK;
   static_assert(TI >= 1 && TJ >= 1 && BLK % NW == 0 && L * (S - 1) < 64, "stage shape");
   extern __shared__ __align__(16) int8_t lds[];  // [S][BLK] 1 KiB blocks
+  // every kernel argument the first stages need (with the grid size), in one scalar round trip
+  __asm__ volatile("" : : "s"(a.A), "s"(a.lda), "s"(a.nseg), "s"(a.seg[0].W), "s"(a.seg[0].K), "s"(a.seg[0].koff),
+                   "s"(a.M), "s"(a.N), "s"(a.epi.scol), "s"(a.epi.srow), "s"(a.epi.bias), "s"(a.epi.scol_per_tensor),
+                   "s"(gridDim.x), "s"(gridDim.y));
   const v4i zero = {0, 0, 0, 0};
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -280,21 +284,11 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
   const int m0 = (t % mt) * BM, n0 = (t / mt) * BN;
 
   // Epilogue operands of this lane's outputs: rows (wm TI + i) 16 + li, columns
-  // (wn TJ + j) 16 + 4 lg + v.
+  // (wn TJ + j) 16 + 4 lg + v; loaded once the first stages are in flight.
   float sr[TI], sc[TJ][4], bi[TJ][4], chain[TI][TJ][4];
-#pragma unroll
-  for (int j = 0; j < TJ; ++j)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int n = min(n0 + (wn * TJ + j) * 16 + 4 * lg + v, a.N - 1);
-      sc[j][v] = a.epi.load_scol(n);
-      bi[j][v] = a.epi.load_bias(n);
-    }
-#pragma unroll
-  for (int i = 0; i < TI; ++i) sr[i] = a.epi.load_srow(min(m0 + (wm * TI + i) * 16 + li, a.M - 1));
 
   for (int sgi = 0; sgi < a.nseg; ++sgi) {
-    const Seg sg = a.seg[sgi];
+    const Seg sg = sgi == 0 ? a.seg[0] : a.seg[sgi];  // the first block's fields are already loaded
     const int NS = sg.K / KS;
     // This lane's source of each block it loads. A row past the matrix is clamped to the last
     // row: it feeds only outputs that are not stored.
@@ -313,6 +307,18 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
 #pragma unroll
     for (int st = 0; st < S - 1; ++st)
       if (st < NS) issue_stage<L, NW, KS, S>(lds, src, wave, st);
+    if (sgi == 0) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int n = min(n0 + (wn * TJ + j) * 16 + 4 * lg + v, a.N - 1);
+          sc[j][v] = a.epi.load_scol(n);
+          bi[j][v] = a.epi.load_bias(n);
+        }
+#pragma unroll
+      for (int i = 0; i < TI; ++i) sr[i] = a.epi.load_srow(min(m0 + (wm * TI + i) * 16 + li, a.M - 1));
+    }
     v4i acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -357,7 +363,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float y = a.epi.apply(acc[i][j][v], sr[i], a.epi.srow != nullptr, sc[j][v], bi[j][v]);
+          const float y = SIMPLE ? fmul(fmul(i2f(acc[i][j][v]), sr[i]), sc[j][v])
+                                 : a.epi.apply(acc[i][j][v], sr[i], a.epi.srow != nullptr, sc[j][v], bi[j][v]);
           chain[i][j][v] = sgi == 0 ? y : fadd(chain[i][j][v], y);
         }
   }
@@ -366,7 +373,14 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int m = m0 + (wm * TI + i) * 16 + li, n = n0 + (wn * TJ + j) * 16 + 4 * lg;
-      if (m < a.M && n < a.N) store_out4(a.Y, m * a.ldy, n, a.epi.out, chain[i][j], a.epi.out_scale);
+      if (m < a.M && n < a.N) {
+        if constexpr (SIMPLE) {
+          *reinterpret_cast<float4*>(static_cast<char*>(a.Y) + m * a.ldy + 4 * n) =
+              make_float4(ftz(chain[i][j][0]), ftz(chain[i][j][1]), ftz(chain[i][j][2]), ftz(chain[i][j][3]));
+        } else {
+          store_out4(a.Y, m * a.ldy, n, a.epi.out, chain[i][j], a.epi.out_scale);
+        }
+      }
     }
 }
 
@@ -375,7 +389,13 @@ hipError_t go_staged(const MfmaArgs& a, hipStream_t s) {
   constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * KS;
   static_assert(lds <= 65536, "stage ring exceeds 64 KiB of LDS");
   const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((mfma_staged_kernel<BM, BN, WM, WN, KS, S>), grid, dim3(64 * WM * WN), lds, s, a);
+  // QM_ROWCOL with fp32 output and neither bias nor activation (every K split): the general
+  // epilogue's code compiled out, as in the GEMV kernels
+  const RowColEpilogue& e = a.epi;
+  if (e.srow && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0)
+    hipLaunchKernelGGL((mfma_staged_kernel<BM, BN, WM, WN, KS, S, true>), grid, dim3(64 * WM * WN), lds, s, a);
+  else
+    hipLaunchKernelGGL((mfma_staged_kernel<BM, BN, WM, WN, KS, S, false>), grid, dim3(64 * WM * WN), lds, s, a);
   return hipGetLastError();
 }
 
