@@ -104,15 +104,45 @@ __device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) 
 // 16 lanes (golden.py:358-380; numerics.py:328-380).
 constexpr int kLdsRow = 12288;
 
+// Elements per thread per pass of row_lds_kernel's staging and output loops: every global load of
+// a pass is issued before any of its values is used (one memory round trip per pass, not per
+// element); rows up to kRowThreads * kRowE elements take one pass.
+constexpr int kRowE = 8;
+
 __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
   __shared__ float v[kLdsRow];
   __shared__ uint32_t red[kRowThreads / 64 + 1];
   __shared__ float bcast;
+  // every kernel argument the first loads need, in one scalar round trip
+  __asm__ volatile("" : : "s"(a.x), "s"(a.lda), "s"(a.N), "s"(a.fn), "s"(a.gamma), "s"(a.beta));
   const int m = blockIdx.x;
   const float* x = frow(a.x, a.lda, m);
   const int N = a.N, t = threadIdx.x;
   const int64_t yrow = m * a.ldy;
-  for (int j = t; j < N; j += kRowThreads) v[j] = ftz(x[j]);
+  const bool norm = a.fn != ROWFN_SOFTMAX;
+  // the row into LDS; the first pass's gamma and beta (norms) are fetched with it
+  float g0[kRowE], b0[kRowE];
+  for (int j0 = 0; j0 < N; j0 += kRowThreads * kRowE) {
+    float xv[kRowE];
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      const int j = j0 + t + u * kRowThreads;
+      xv[u] = *(j < N ? x + j : x);
+    }
+    if (j0 == 0) {
+#pragma unroll
+      for (int u = 0; u < kRowE; ++u) {
+        const int j = t + u * kRowThreads;
+        g0[u] = *(norm && j < N ? a.gamma + j : x);
+        b0[u] = *(norm && a.beta && j < N ? a.beta + j : x);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      const int j = j0 + t + u * kRowThreads;
+      if (j < N) v[j] = ftz(xv[u]);
+    }
+  }
   if (a.fn == ROWFN_SOFTMAX) {
     const int V = a.valid ? min(max(a.valid[m], 1), N) : (a.causal_k > 0 ? min(N, a.causal_k + m) : N);
     __syncthreads();
@@ -146,10 +176,23 @@ __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
     const float ss = lds_sum16<true>(v, N, &bcast);
     rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, a.eps));
   }
-  for (int j = t; j < N; j += kRowThreads) {
-    float y = fmul(fmul(v[j], rs), a.gamma[j]);
-    if (a.beta) y = fadd(y, a.beta[j]);
-    store_out(a.y, yrow, j, a.out, y, a.out_scale);
+  for (int j0 = 0; j0 < N; j0 += kRowThreads * kRowE) {
+    float gv[kRowE], bv[kRowE];
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      const int j = j0 + t + u * kRowThreads;
+      gv[u] = j0 == 0 ? g0[u] : *(j < N ? a.gamma + j : a.gamma);
+      bv[u] = j0 == 0 ? b0[u] : *(a.beta && j < N ? a.beta + j : a.gamma);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      const int j = j0 + t + u * kRowThreads;
+      if (j < N) {
+        float y = fmul(fmul(v[j], rs), gv[u]);
+        if (a.beta) y = fadd(y, bv[u]);
+        store_out(a.y, yrow, j, a.out, y, a.out_scale);
+      }
+    }
   }
 }
 
@@ -252,6 +295,49 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     else if (n < a.rot) y = fadd(fmul(x[n], t[n - h]), fmul(x[n - h], t[n]));
     else y = ftz(x[n]);
     store_out(a.y, m * a.ldy, n, a.out, y, a.out_scale);
+  }
+}
+
+// ELT on dense fp32 rows with an fp32 output and the activation fixed at compile time (a decode
+// step's residual adds and gated products): every kernel argument in one scalar round trip and each
+// thread's two loads in one batch. Same steps as elt_kernel; in place is as safe.
+template <int OP, int ACT>
+__global__ __launch_bounds__(256) void elt_fast_kernel(EltArgs a) {
+  __asm__ volatile("" : : "s"(a.A), "s"(a.lda), "s"(a.B), "s"(a.ldb), "s"(a.Y), "s"(a.ldy), "s"(a.M), "s"(a.N));
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= a.N) return;
+  for (int m = blockIdx.y; m < a.M; m += gridDim.y) {
+    const float x = frow(a.A, a.lda, m)[n];
+    const float b = frow(a.B, a.ldb, m)[n];
+    const float av = act_fn(x, ACT);
+    float y;
+    if constexpr (OP == ELTOP_MUL) y = fmul(av, b);
+    else if constexpr (OP == ELTOP_ADD) y = fadd(av, b);
+    else y = fadd(av, fneg(ftz(b)));
+    reinterpret_cast<float*>(static_cast<char*>(a.Y) + m * a.ldy)[n] = ftz(y);
+  }
+}
+
+// RoPE with an fp32 output: the element, its rotation partner and both table entries in one batch
+// of loads (partner and table indices chosen without branches), then rope_kernel's steps.
+__global__ __launch_bounds__(256) void rope_fast_kernel(RopeArgs a) {
+  __asm__ volatile("" : : "s"(a.x), "s"(a.lda), "s"(a.tab), "s"(a.rows_per_pos), "s"(a.rot), "s"(a.y), "s"(a.ldy),
+                   "s"(a.M), "s"(a.N));
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= a.N) return;
+  const int h = a.rot / 2;
+  const bool lo = n < h, rotated = n < a.rot;
+  const int p = lo ? n + h : rotated ? n - h : n;   // rotation partner
+  const int c = lo ? n : rotated ? n - h : 0;       // cos index; the sin is at h + c
+  for (int m = blockIdx.y; m < a.M; m += gridDim.y) {
+    const float* x = frow(a.x, a.lda, m);
+    const float* t = a.tab + static_cast<int64_t>(static_cast<unsigned>(m) / static_cast<unsigned>(a.rows_per_pos)) * a.rot;
+    const float xn = x[n], xp = x[p], tc = t[c], ts = t[h + c];
+    float y;
+    if (lo) y = fadd(fmul(xn, tc), fneg(fmul(xp, ts)));
+    else if (rotated) y = fadd(fmul(xn, tc), fmul(xp, ts));
+    else y = ftz(xn);
+    reinterpret_cast<float*>(static_cast<char*>(a.y) + m * a.ldy)[n] = ftz(y);
   }
 }
 
@@ -541,13 +627,34 @@ hipError_t launch_row(const RowArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int OP>
+bool elt_fast(const EltArgs& a, hipStream_t s) {
+  const dim3 g = row_grid(a.M, a.N, 256);
+  switch (a.act) {
+    case 0: hipLaunchKernelGGL((elt_fast_kernel<OP, 0>), g, dim3(256), 0, s, a); return true;
+    case 3: hipLaunchKernelGGL((elt_fast_kernel<OP, 3>), g, dim3(256), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((elt_fast_kernel<OP, 4>), g, dim3(256), 0, s, a); return true;
+    default: return false;
+  }
+}
+
 hipError_t launch_elt(const EltArgs& a, hipStream_t s) {
+  // dense fp32 operands, fp32 output, no activation / GELU / SiLU: the one-batch instances
+  if (!a.a_fp16 && !a.a_row && a.bmode == BMODE_DENSE && a.out == 0) {
+    if (a.op == ELTOP_MUL && elt_fast<ELTOP_MUL>(a, s)) return hipGetLastError();
+    if (a.op == ELTOP_ADD && elt_fast<ELTOP_ADD>(a, s)) return hipGetLastError();
+    if (a.op == ELTOP_SUB && elt_fast<ELTOP_SUB>(a, s)) return hipGetLastError();
+  }
   hipLaunchKernelGGL(elt_kernel, row_grid(a.M, a.N, 256), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_rope(const RopeArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(rope_kernel, row_grid(a.M, a.N, 256), dim3(256), 0, s, a);
+  if (a.out == 0) {
+    hipLaunchKernelGGL(rope_fast_kernel, row_grid(a.M, a.N, 256), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(rope_kernel, row_grid(a.M, a.N, 256), dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 
