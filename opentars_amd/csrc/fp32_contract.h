@@ -43,9 +43,22 @@ __device__ __forceinline__ float fadd(float a, float b) { return canon(ftz(__fad
 // subnormal) in one compare.
 __device__ __forceinline__ float fadd_chain(float acc, float p) {
   const float r = __fadd_rn(acc, p);
-  return __builtin_amdgcn_class(r, 0x90) ? ffrom(fbits(r) & kSign) : r;
+  return __builtin_amdgcn_classf(r, 0x90) ? ffrom(fbits(r) & kSign) : r;
 }
 __device__ __forceinline__ float chain_end(float acc) { return canon(acc); }
+
+// A chain run with plain rounded operations (no flushes) equals the contract's chain, up to NaN
+// payloads that chain_end canonicalizes, whenever none of its inputs, products and partial sums is
+// subnormal: every flush is then an identity. Such a chain keeps the minimum of sub_key over those
+// values, off its dependent path in vector registers, and is recomputed with the flushes when the
+// minimum is below kSubKeyNormal. sub_key(x) = (bits << 1) - 1 as unsigned drops the sign: +-0 wraps
+// to the largest key, a subnormal maps to [0, 2^24 - 2], every normal, infinite or NaN x to at
+// least 2^24 - 1 (one shift-add per value, one three-way minimum per two values).
+constexpr uint32_t kSubKeyNormal = 0x00FFFFFFu;
+__device__ __forceinline__ uint32_t sub_key(float x) { return (fbits(x) << 1) - 1u; }
+__device__ __forceinline__ uint32_t min_key(uint32_t m, float a, float b) {
+  return min(m, min(sub_key(a), sub_key(b)));
+}
 
 // numerics.py:50-52: int32 -> fp32 round-to-nearest-even (v_cvt_f32_i32)
 __device__ __forceinline__ float i2f(int32_t i) { return static_cast<float>(i); }

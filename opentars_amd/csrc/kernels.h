@@ -41,6 +41,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Waits until at most L * ahead of this wave's vector loads are outstanding: a ring of stages of L
+// loads each, `ahead` (uniform, 0..A) of them issued after the one about to be read.
+template <int L, int A>
+__device__ __forceinline__ void wait_stages_ahead(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vmcnt<L * A>();
+      return;
+    }
+    wait_stages_ahead<L, A - 1>(ahead);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 // Forces a uniform value (a kernel argument) into SGPRs at this point, so its scalar load is issued
 // here, beside the vector loads already in flight, rather than at its first use.
 template <class T>

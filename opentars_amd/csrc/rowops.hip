@@ -14,6 +14,8 @@
 //    per output with the k loop unrolled and its loads issued ahead.
 // Everything else is elementwise. All of these ops are latency-bound at decode sizes (a few
 // thousand elements, tens of dependent steps per lane).
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace tars {
@@ -477,24 +479,104 @@ __global__ __launch_bounds__(256) void fdot_nn_kernel(FdotArgs a) {
 
 // ------------------------------------------------------------------------------ fused decode attention
 // One workgroup per query head: (1) the scores s[j] = sum16_k q[k] K[j][k] for every key (16-lane
-// groups, kAttnKeysInFlight keys per group with their K rows loaded together and their chains
+// groups, 16 keys per group (8 at head size 256 or up to 128 keys, 4 up to 64) with their K rows loaded together and their chains
 // interleaved), kept in LDS; (2) the causal softmax over them in place (as row_lds_kernel); (3) the
-// P V chains over V staged in LDS by direct global -> LDS loads in a ring of kAttnSlots stages.
+// P V chains over V staged in LDS by direct global -> LDS loads in a ring of kAttnSlots stages,
+// the first kAttnSlots - 1 of them issued before the scores so that they land while (1) and (2) run.
 // Each step is the contract's, in the same order as the three separate ops, so every value is the
 // same bit for bit; the last head also writes its scores and probabilities where the reference's
 // ops leave them.
-constexpr int kAttnKeysInFlight = 8, kAttnSlots = 3, kAttnStageBytes = 16384;
+constexpr int kAttnSlots = 6, kAttnStageBytes = 8192;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(TARS_LDS(p)));
+}
+
+// Eight V values of one column (rows at va + u * ROWB, 4- or 2-byte elements) and the eight
+// probabilities at pa, read from LDS in one sequence that waits for its own reads. Written as
+// assembly so that the compiler, which cannot tell the V ring's direct global -> LDS loads apart,
+// adds no wait for every one of them in flight before an LDS read; the ring's stage waits order it.
+template <int ROWB, bool VHALF>
+__device__ __forceinline__ void ring_read8(uint32_t va, uint32_t pa, uint32_t (&v)[8], float (&p)[8]) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 p0, p1;
+#define TARS_R(op)                                                                                        \
+  asm volatile(op " %0, %10\n\t" op " %1, %10 offset:%12\n\t" op " %2, %10 offset:%13\n\t"              \
+               op " %3, %10 offset:%14\n\t" op " %4, %10 offset:%15\n\t" op " %5, %10 offset:%16\n\t"  \
+               op " %6, %10 offset:%17\n\t" op " %7, %10 offset:%18\n\t"                              \
+               "ds_read_b128 %8, %11\n\tds_read_b128 %9, %11 offset:16\n\ts_waitcnt lgkmcnt(0)"        \
+               : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), \
+                 "=&v"(v[7]), "=&v"(p0), "=&v"(p1)                                                        \
+               : "v"(va), "v"(pa), "i"(ROWB), "i"(2 * ROWB), "i"(3 * ROWB), "i"(4 * ROWB), "i"(5 * ROWB),   \
+                 "i"(6 * ROWB), "i"(7 * ROWB)                                                             \
+               : "memory")
+  if constexpr (VHALF) TARS_R("ds_read_u16");
+  else TARS_R("ds_read_b32");
+#undef TARS_R
+  p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
+  p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
+}
+
+// The scores of query row m of head h: 16-lane group g takes keys g, g + 16, ..., KF of them per
+// pass with their K rows loaded together and their chains interleaved. The chains run unflushed
+// (qv is flushed) and are checked; a pass is recomputed with the contract's flushes when a key
+// element, a product or a partial sum is subnormal.
+template <int U, int KF>
+__device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int g, int l, bool last,
+                                            const float (&qv)[U], float* sp) {
+  const int nk = a.nk;
+  for (int j0 = g; j0 < nk; j0 += 16 * KF) {
+    float kv[KF][U];
+#pragma unroll
+    for (int c = 0; c < KF; ++c) {
+      const int j = min(j0 + 16 * c, nk - 1);  // clamped: a key past the end is computed and dropped
+      const float* kr = frow(a.k[h], a.ldk, j);
+#pragma unroll
+      for (int u = 0; u < U; ++u) kv[c][u] = kr[l + 16 * u];
+    }
+    float acc[KF];
+    uint32_t mk = ~0u;
+#pragma unroll
+    for (int c = 0; c < KF; ++c) acc[c] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int c = 0; c < KF; ++c) {
+        const float pr = __fmul_rn(qv[u], kv[c][u]);
+        acc[c] = __fadd_rn(acc[c], pr);
+        mk = min_key(min_key(mk, kv[c][u], pr), acc[c], acc[c]);
+      }
+    if (__builtin_expect(mk < kSubKeyNormal, 0)) {
+#pragma unroll
+      for (int c = 0; c < KF; ++c) acc[c] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int c = 0; c < KF; ++c) acc[c] = fadd_chain(acc[c], fmul(qv[u], kv[c][u]));
+    }
+#pragma unroll
+    for (int c = 0; c < KF; ++c) {
+      const float sv = fold16(acc[c]);
+      const int j = j0 + 16 * c;
+      if (l == 0 && j < nk) {
+        sp[j] = sv;
+        if (last && a.sc) store_out(a.sc, m * a.ldsc, j, 0, sv, 0.0f);
+      }
+    }
+  }
+}
 
 template <int HD, bool VHALF>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   constexpr int U = HD / 16;                                  // elements per lane of a key row
+  constexpr int KF = HD <= 128 ? 16 : 8;                      // keys in flight per 16-lane group (4 up to 64 keys, 8 up to 128)
   constexpr int ES = VHALF ? 2 : 4;
   constexpr int ROWB = HD * ES;                               // bytes of one V row
   constexpr int SR = kAttnStageBytes / ROWB;                  // V rows per stage
   constexpr int IPS = kAttnStageBytes / 1024;                 // 1 KiB loads per stage (16)
   constexpr int L = IPS / 4;                                  // per wave (4)
   static_assert(ROWB <= 1024 && 1024 % ROWB == 0 && IPS % 4 == 0, "attention shape");
-  __shared__ float sp[kAttnMaxKeys];
+  __shared__ __align__(16) float sp[kAttnMaxKeys];
   __shared__ __align__(16) int8_t ring[kAttnSlots * kAttnStageBytes];
   __shared__ uint32_t red[4];
   __shared__ float bcast;
@@ -503,38 +585,30 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const bool last = h == a.heads - 1;
   const int nk = a.nk;
   const int NS = (nk + SR - 1) / SR;
+  const char* vbase = static_cast<const char*>(a.v[h]);
+  auto issue = [&](int st) {
+    int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
+#pragma unroll
+    for (int u = 0; u < L; ++u) {
+      const int i = wave + 4 * u;
+      const int byte = i * 1024 + lane * 16;
+      const int row = min(st * SR + byte / ROWB, nk - 1);
+      stage16(vbase + static_cast<int64_t>(row) * a.ldv + byte % ROWB, slot + i * 1024);
+    }
+  };
   for (int m = 0; m < a.M; ++m) {
+    // the V ring's first stages stream in while the scores and the softmax run (V depends on neither)
+#pragma unroll
+    for (int st = 0; st < kAttnSlots - 1; ++st)
+      if (st < NS) issue(st);
     // (1) scores
     const float* qr = frow(a.q[h], a.ldq, m);
     float qv[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) qv[u] = qr[l + 16 * u];
-    for (int j0 = g; j0 < nk; j0 += 16 * kAttnKeysInFlight) {
-      float kv[kAttnKeysInFlight][U];
-#pragma unroll
-      for (int c = 0; c < kAttnKeysInFlight; ++c) {
-        const int j = min(j0 + 16 * c, nk - 1);  // clamped: a key past the end is computed and dropped
-        const float* kr = frow(a.k[h], a.ldk, j);
-#pragma unroll
-        for (int u = 0; u < U; ++u) kv[c][u] = kr[l + 16 * u];
-      }
-      float acc[kAttnKeysInFlight];
-#pragma unroll
-      for (int c = 0; c < kAttnKeysInFlight; ++c) acc[c] = 0.0f;
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int c = 0; c < kAttnKeysInFlight; ++c) acc[c] = fadd_chain(acc[c], fmul(qv[u], kv[c][u]));
-#pragma unroll
-      for (int c = 0; c < kAttnKeysInFlight; ++c) {
-        const float sv = fold16(acc[c]);
-        const int j = j0 + 16 * c;
-        if (l == 0 && j < nk) {
-          sp[j] = sv;
-          if (last && a.sc) store_out(a.sc, m * a.ldsc, j, 0, sv, 0.0f);
-        }
-      }
-    }
+    for (int u = 0; u < U; ++u) qv[u] = ftz(qr[l + 16 * u]);
+    if (nk <= 64) attn_scores<U, 4>(a, h, m, g, l, last, qv, sp);
+    else if (nk <= 128) attn_scores<U, 8>(a, h, m, g, l, last, qv, sp);
+    else attn_scores<U, KF>(a, h, m, g, l, last, qv, sp);
     // (2) causal softmax in place
     const int V = a.causal_k > 0 ? min(nk, a.causal_k + m) : nk;
     __syncthreads();
@@ -553,38 +627,23 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __syncthreads();
     for (int j = t; j < nk; j += 256) sp[j] = j < V ? exp_f(fadd(sp[j], nmx)) : 0.0f;
     const float r = recip_f(lds_sum16<false>(sp, nk, &bcast));
+    int above1 = 0;  // a probability above 1 or NaN
     for (int j = t; j < nk; j += 256) {
       const float p = fmul(sp[j], r);
       sp[j] = p;
+      above1 |= !(p <= 1.0f);
       if (last && a.pr) store_out(a.pr, m * a.ldpr, j, 0, p, 0.0f);
     }
-    wait_vmcnt<0>();  // no earlier vector memory operation outstanding before the ring's counts
-    __syncthreads();
-    // (3) P V over the V ring
-    const char* vbase = static_cast<const char*>(a.v[h]);
-    auto issue = [&](int st) __device__ {
-      int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
-#pragma unroll
-      for (int u = 0; u < L; ++u) {
-        const int i = wave + 4 * u;
-        const int byte = i * 1024 + lane * 16;
-        const int row = min(st * SR + byte / ROWB, nk - 1);
-        stage16(vbase + static_cast<int64_t>(row) * a.ldv + byte % ROWB, slot + i * 1024);
-      }
-    };
-#pragma unroll
-    for (int st = 0; st < kAttnSlots - 1; ++st)
-      if (st < NS) issue(st);
+    wait_vmcnt<0>();  // the first V stages have landed; nothing else outstanding before the ring's counts
+    // V elements need their own test only when fp32 and some probability is above 1 or NaN: with
+    // every p <= 1, a subnormal V element gives |p v| < 2^-126, a subnormal product (tested) or
+    // the zero of sign(p) ^ sign(v) that its flush gives too.
+    const bool vtest = __syncthreads_or(above1) && !VHALF;
+    // (3) P V over the V ring (its first kAttnSlots - 1 stages were issued before the scores)
     float acc = 0.0f;
     for (int st = 0; st < NS; ++st) {
-      if (st + kAttnSlots - 1 < NS) {
-        issue(st + kAttnSlots - 1);
-        wait_vmcnt<L * (kAttnSlots - 1)>();
-      } else if (st + 1 < NS) {
-        wait_vmcnt<L>();  // one later stage issued (kAttnSlots == 3)
-      } else {
-        wait_vmcnt<0>();
-      }
+      if (st + kAttnSlots - 1 < NS) issue(st + kAttnSlots - 1);
+      wait_stages_ahead<L, kAttnSlots - 1>(min(NS - 1 - st, kAttnSlots - 1));
       __builtin_amdgcn_s_barrier();
       if (t < HD) {
         const int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
@@ -594,15 +653,41 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
           return VHALF ? from_fp16_bits(reinterpret_cast<const uint16_t*>(slot + rr * ROWB)[t])
                        : reinterpret_cast<const float*>(slot + rr * ROWB)[t];
         };
+        // The stage's chain steps unflushed, checked (a probability is an fmul output: flushed,
+        // so only V (when vtest), the products and the partial sums are tested); recomputed from
+        // the stage's first value with the contract's flushes when any is subnormal.
+        const float acc0 = acc;
+        uint32_t mk = ~0u;
         int rr = 0;
-        for (; rr + 8 <= rows; rr += 8) {  // the block's LDS reads and products first, then its chain steps
-          float pv[8];
+        auto blocks = [&](auto vt) {
+          for (; rr + 8 <= rows; rr += 8) {  // the block's LDS reads and products first, then its chain steps
+            uint32_t vb[8];
+            float pb[8], pv[8];
+            ring_read8<ROWB, VHALF>(lds_addr(slot + rr * ROWB + ES * t), lds_addr(ps + rr), vb, pb);
 #pragma unroll
-          for (int u = 0; u < 8; ++u) pv[u] = fmul(ps[rr + u], vval(rr + u));
+            for (int u = 0; u < 8; ++u) {
+              const float v = VHALF ? from_fp16_bits(vb[u]) : __uint_as_float(vb[u]);
+              pv[u] = __fmul_rn(pb[u], v);
+              if constexpr (decltype(vt)::value) mk = min_key(mk, v, v);
+            }
+            float sums[8];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) acc = fadd_chain(acc, pv[u]);
+            for (int u = 0; u < 8; ++u) sums[u] = acc = __fadd_rn(acc, pv[u]);
+#pragma unroll
+            for (int u = 0; u < 8; u += 2) mk = min_key(min_key(mk, pv[u], pv[u + 1]), sums[u], sums[u + 1]);
+          }
+        };
+        if (vtest) blocks(std::true_type{});
+        else blocks(std::false_type{});
+        for (; rr < rows; ++rr) {
+          const float v = vval(rr), pr = __fmul_rn(ps[rr], v);
+          acc = __fadd_rn(acc, pr);
+          mk = min_key(min_key(mk, v, pr), acc, acc);
         }
-        for (; rr < rows; ++rr) acc = fadd_chain(acc, fmul(ps[rr], vval(rr)));
+        if (__builtin_expect(mk < kSubKeyNormal, 0)) {
+          acc = acc0;
+          for (rr = 0; rr < rows; ++rr) acc = fadd_chain(acc, fmul(ps[rr], vval(rr)));
+        }
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot are done
       __builtin_amdgcn_s_barrier();

@@ -540,20 +540,45 @@ def test_gemv_only_profile_refuses_long_k():
 ATT_IMAGE, ATT_QADDR = 1 << 24, (1 << 24) - 0x10000
 
 
+def plant_attention_specials(rng, q, kc, vv, kv_heads, hd, v_fp16):
+    """Values whose flushes change a result: subnormal K and V elements, K and V columns of tiny
+    normals (their products with q or with a probability are subnormal), an infinite q element
+    against a subnormal K element (the flushed product is NaN, the unflushed one infinite), and two
+    equal K rows whose V values cancel to a subnormal partial sum (2^-100 (1 - (1 - 2^-23)) p)."""
+    nk = kc.shape[0]
+    sub = lambda n: (rng.integers(1, 1 << 23, n, dtype=np.uint32) | (rng.integers(0, 2, n, dtype=np.uint32) << 31)).view(np.float32)
+    for kv in range(kv_heads):
+        c0 = kv * hd
+        kc[rng.integers(0, nk, 6), c0 + rng.integers(0, hd, 6)] = sub(6)
+        kc[:, c0 + 9] = rng.normal(0, 1, nk).astype(np.float32) * np.float32(2.0 ** -70)
+        q[:, c0 + 9] = np.float32(2.0 ** -60)
+        if not v_fp16:
+            vv[rng.integers(0, nk, 6), c0 + rng.integers(0, hd, 6)] = sub(6)
+            vv[:, c0 + 5] = rng.normal(0, 1, nk).astype(np.float32) * np.float32(2.0 ** -124)
+            vv[0, c0 + 3], vv[1, c0 + 3] = np.float32(2.0 ** -100), -np.float32(2.0 ** -100) * np.float32(1 - 2.0 ** -23)
+        kc[1, c0:c0 + hd] = kc[0, c0:c0 + hd]
+    q[0, 7] = np.inf
+    kc[nk // 2, 7] = sub(1)[0]
+
+
 def attention_program(seed: int, heads: int, kv_heads: int, hd: int, M: int, t0: int, v_fp16: bool,
-                      out: int = Q.OUT_FP32, hazard: bool = False) -> Program:
+                      out: int = Q.OUT_FP32, hazard: bool = False, specials: bool = False) -> Program:
     """One layer's attention as the reference lowers it (tars_mini/llm.py:736-746): per query head an
     FDOT_NT of its q rows with its KV head's K rows into the shared score buffer, the causal softmax
     (t0 + 1 valid keys for the first row) into the shared probability buffer, and an FDOT_NN with the
     V rows into the head's output columns. hazard: the last head's q rows are the first head's
-    output, so the heads cannot run concurrently."""
+    output, so the heads cannot run concurrently. specials: plant_attention_specials."""
     p = Program(seed, image=ATT_IMAGE, qaddr=ATT_QADDR)
     rng = p.rng
     nk = (t0 + M + 15) // 16 * 16
     qrow = 4 * heads * hd
-    q = p.put((rng.normal(0, 0.3, (M, heads * hd))).astype("<f4").tobytes())
-    kc = p.put(rng.normal(0, 1, (nk, kv_heads * hd)).astype("<f4").tobytes())
+    qv = rng.normal(0, 0.3, (M, heads * hd)).astype(np.float32)
+    kv_ = rng.normal(0, 1, (nk, kv_heads * hd)).astype(np.float32)
     vv = rng.normal(0, 1, (nk, kv_heads * hd)).astype(np.float32)
+    if specials:
+        plant_attention_specials(rng, qv, kv_, vv, kv_heads, hd, v_fp16)
+    q = p.put(qv.astype("<f4").tobytes())
+    kc = p.put(kv_.astype("<f4").tobytes())
     vc = p.put(vv.astype(np.float16).view("<u2").tobytes() if v_fp16 else vv.astype("<f4").tobytes())
     ves = 2 if v_fp16 else 4
     sc = p.alloc(4 * M * nk)
@@ -579,6 +604,7 @@ def attention_program(seed: int, heads: int, kv_heads: int, hd: int, M: int, t0:
     (4, 1, 256, 1, 37, True, Q.OUT_FP32),         # head dim 256, fp16 V state
     (8, 4, 64, 3, 100, False, Q.OUT_BF16),        # a 3-token chunk, bf16 out
     (2, 2, 128, 2, 0, False, Q.OUT_INT8),         # the first position
+    (2, 1, 64, 2, 2000, True, Q.OUT_FP32),        # 32 V stages per row, two query rows
     (2, 1, 128, 1, 4100, False, Q.OUT_FP32),      # past the fused kernel's 4080 keys: unfused
 ])
 def test_attention_layer_matches_the_oracle(fusion, heads, kv_heads, hd, M, t0, v_fp16, out):
@@ -588,6 +614,22 @@ def test_attention_layer_matches_the_oracle(fusion, heads, kv_heads, hd, M, t0, 
         (o, ost), (g, gst) = both(p.image(), len(p.descs), ATT_QADDR)
     finally:
         NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,M,t0,v_fp16", [
+    (4, 2, 128, 1, 250, False),
+    (4, 2, 128, 2, 40, False),
+    (2, 1, 64, 1, 300, True),
+    (2, 1, 256, 1, 20, False),
+])
+def test_attention_with_values_the_flushes_change(heads, kv_heads, hd, M, t0, v_fp16):
+    """The fused kernel's chains run unflushed and are recomputed with the flushes when an input,
+    product or partial sum is subnormal: planted values that take that path match the oracle."""
+    p = attention_program(heads * 77 + t0, heads, kv_heads, hd, M, t0, v_fp16, specials=True)
+    (o, ost), (g, gst) = both(p.image(), len(p.descs), ATT_QADDR)
     assert ost.done and same_status(ost, gst), (ost, gst)
     gd = bytes(g.ddr)
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
