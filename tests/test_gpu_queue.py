@@ -31,6 +31,7 @@ class Program:
         self.ddr = bytearray(image)
         self.qaddr = qaddr
         self.top = 0x1000
+        self.row_scale = 1.0   # rand_rows' values are multiplied by this
         self.descs: list[bytes] = []
 
     def alloc(self, nbytes: int, align: int = 16) -> int:
@@ -151,7 +152,7 @@ def put_rows(p: Program, x: np.ndarray, row_bytes: int):
 
 
 def rand_rows(p: Program, M: int, N: int) -> np.ndarray:
-    x = (p.rng.normal(0, 1, (M, N)) * np.exp2(p.rng.integers(-4, 5, (M, 1)))).astype("<f4")
+    x = (p.rng.normal(0, 1, (M, N)) * np.exp2(p.rng.integers(-4, 5, (M, 1))) * p.row_scale).astype("<f4")
     if p.rng.integers(0, 6) == 0:
         x[int(p.rng.integers(0, M)), int(p.rng.integers(0, N))] = [np.inf, -np.inf, np.nan, 0.0, 1e-40][
             int(p.rng.integers(0, 5))]
@@ -165,9 +166,9 @@ def out_fields(p: Program, M: int, N: int, outs=(Q.OUT_FP32, Q.OUT_BF16, Q.OUT_I
     return out, y, ldy16, osc
 
 
-def add_row(p: Program, M: int, N: int):
+def add_row(p: Program, M: int, N: int, fn: int | None = None):
     rng = p.rng
-    fn = int(rng.choice([Q.ROW_SOFTMAX, Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM]))
+    fn = int(rng.choice([Q.ROW_SOFTMAX, Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM])) if fn is None else fn
     a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
     out, y, ldy16, osc = out_fields(p, M, N)
     f = dict(OPCODE=Q.OP_ROW, CTRL=fn, A_OFF=a, Y_OFF=y, M=M, N=N, LDA16=lda16, LDY16=ldy16, OUT_SCALE=osc)
@@ -323,6 +324,83 @@ def first_diff(a: bytes, b: bytes) -> int:
 def test_random_programs_match_the_oracle(seed, fusion):
     """With and without the executor's quantizer + GEMM fusion."""
     p = random_program(seed)
+    prev = NQ.set_fusion(fusion)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
+def cancelling_rows(rng, M: int, N: int, stride: int) -> np.ndarray:
+    """Rows near 2^-115 whose summation chains (elements c, c + stride, ...) pass through a
+    subnormal partial sum: per chain the first two elements are a near 2^-112 and -(a - s) with
+    s = k 2^-133 (|k| < 100; exact, as s is a multiple of a's ulp), whose sum is exactly the
+    subnormal s, and the third is near 2^-115, so a step that keeps s instead of flushing it changes
+    the sum."""
+    x = (rng.normal(0, 1, (M, N)) * 2.0 ** -115).astype(np.float32)
+    for c in range(min(stride, N - 2 * stride)):
+        a = ((1 + rng.random(M)) * 2.0 ** -112 * rng.choice([-1, 1], M)).astype(np.float32)
+        sv = (rng.integers(1, 100, M) * rng.choice([-1, 1], M) * 2.0 ** -133).astype(np.float32)
+        x[:, c], x[:, c + stride] = a, -(a - sv)
+        assert (np.abs(x[:, c] + x[:, c + stride]) < np.float32(2.0 ** -126)).all()
+    return x
+
+
+def add_w4_cancelling(p: Program, M: int, N: int, K: int):
+    """A W4A16 GEMM whose fp32 bank 0 (groups 0, 4, 8, ...) passes through a subnormal sum: group 4
+    holds group 0's activations (near 2^-108, element 5 at 2^-115) and group 0's weights negated
+    except element 5, which differs by 1; with every group scale 2^-20 the two terms (near 2^-122)
+    are exact and add to the subnormal +-aq_5 2^-20 xs (near 2^-135); group 8's term follows it."""
+    rng = p.rng
+    assert K >= 9 * 128
+    x = (rng.normal(0, 1, (M, K)) * 2.0 ** -108).astype(np.float32)
+    x[:, 5] = np.float32(2.0 ** -115)
+    x[:, 512:640] = x[:, 0:128]
+    w = rng.integers(-7, 8, (N, K)).astype(np.int64)
+    w[:, 512:640] = -w[:, 0:128]
+    w[:, 512 + 5] += np.where(w[:, 512 + 5] < 7, 1, -1)
+    nib = (w & 15).astype(np.uint8)
+    wp = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    a, lda16 = put_rows(p, x, 4 * K)
+    wo = p.put(wp.tobytes(), align=128)
+    s = p.put(np.full((N, K // 128), 0x0010, "<u2").tobytes())      # binary16 2^-20
+    y, ldy16 = stride_fields(p, M, 4 * N)
+    p.add(OPCODE=Q.OP_GEMM, CTRL=Q.ctrl(Q.QM_GROUP, a_dtype=Q.DT_FP32, w_dtype=Q.DT_INT4), EPI=Q.epi(),
+          GROUP_SIZE=128, A_OFF=a, W_OFF=wo, SCALE_OFF=s, Y_OFF=y, M=M, N=N, K=K, LDA16=lda16, LDY16=ldy16)
+
+
+@pytest.mark.parametrize("seed", range(3))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_chains_whose_partial_sums_are_subnormal(seed, fusion):
+    """Summation chains whose steps' flushes decide the result (cancelling_rows): LayerNorm's
+    16-lane row sums, FDOT NT's 16-lane chains and their fold (B is 1.0 on the cancelling columns,
+    so the products are the row's elements), FDOT NN's sequential chains, and the W4A16 banks of
+    add_w4_cancelling; the images equal the oracle's."""
+    p = Program(7000 + seed)
+    rng = p.rng
+    for M, N in ((1, 1024), (3, 4096), (2, 208)):
+        a, lda16 = put_rows(p, cancelling_rows(rng, M, N, 16), 4 * N)
+        y, ldy16 = stride_fields(p, M, 4 * N)
+        g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
+        p.add(OPCODE=Q.OP_ROW, CTRL=Q.ROW_LAYERNORM, EPI=Q.epi(), A_OFF=a, Y_OFF=y, SCALE_OFF=g, M=M, N=N,
+              LDA16=lda16, LDY16=ldy16, W_OFF=f32bits(1e-30))
+    for nn, M, N, K in ((0, 1, 64, 128), (0, 2, 48, 256), (1, 1, 128, 1008), (1, 3, 48, 64)):
+        A = cancelling_rows(rng, M, K, 1 if nn else 16)
+        a, lda16 = put_rows(p, A, 4 * K)
+        B = (rng.normal(0, 1, (K, N) if nn else (N, K)) * 0.5).astype(np.float32)
+        if nn:
+            B[:3] = 1.0
+        else:
+            B[:, :48] = 1.0
+        w, gs = put_rows(p, B, 4 * B.shape[1])
+        y, ldy16 = stride_fields(p, M, 4 * N)
+        p.add(OPCODE=Q.OP_FDOT, CTRL=nn, EPI=Q.epi(), A_OFF=a, W_OFF=w, Y_OFF=y, M=M, N=N, K=K, GROUP_SIZE=gs,
+              LDA16=lda16, LDY16=ldy16)
+    for M, N, K in ((1, 256, 1280), (2, 64, 1536), (4, 32, 1280)):
+        add_w4_cancelling(p, M, N, K)
     prev = NQ.set_fusion(fusion)
     try:
         (o, ost), (g, gst) = both(p.image(), len(p.descs))
