@@ -343,16 +343,27 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // 4. four bank chains per row (at most G / 4 <= K / 512 <= 4 CPL steps; the terms are flushed
-  //    fmul results, so the steps are fadd_chain's), then (b0 + b1) + (b2 + b3)
+  //    fmul results, so the steps are fadd_chain's, run unflushed and checked: recomputed with the
+  //    flushes when a partial sum is subnormal), then (b0 + b1) + (b2 + b3)
   constexpr int kSteps = 4 * CPL;
   const float* trow = terms[wave][ue < U ? ue : 0];
   float tv[kSteps];
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) tv[i] = trow[bank + 4 * i];  // index <= 16 CPL - 1 < kTermStride
   float acc = 0.0f;
+  uint32_t mk = ~0u;
 #pragma unroll
   for (int i = 0; i < kSteps; ++i)
-    if (bank + 4 * i < G) acc = fadd_chain(acc, tv[i]);
+    if (bank + 4 * i < G) {
+      acc = __fadd_rn(acc, tv[i]);
+      mk = min(mk, sub_key(acc));
+    }
+  if (__builtin_expect(mk < kSubKeyNormal, 0)) {
+    acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i)
+      if (bank + 4 * i < G) acc = fadd_chain(acc, tv[i]);
+  }
   acc = chain_end(acc);
   const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
   const float other = lane_xor2(pair);
