@@ -84,16 +84,32 @@ __device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) 
   __syncthreads();  // v complete
   if (threadIdx.x < 16) {
     const int l = threadIdx.x;
-    float acc = 0.0f;
-    int j0 = 0;
-    for (; j0 + 16 * 8 <= n; j0 += 16 * 8) {
-      float t[8];
+    // the chain unflushed with its partial sums checked (its terms are flushed contract results),
+    // then with the flushes when one was subnormal
+    auto chain = [&](auto flushed) {
+      float acc = 0.0f;
+      uint32_t mk = ~0u;
+      auto step = [&](float t) {
+        if constexpr (decltype(flushed)::value) {
+          acc = fadd_chain(acc, t);
+        } else {
+          acc = __fadd_rn(acc, t);
+          mk = min(mk, sub_key(acc));
+        }
+      };
+      int j0 = 0;
+      for (; j0 + 16 * 8 <= n; j0 += 16 * 8) {
+        float t[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = SQUARE ? fmul(v[j0 + l + 16 * u], v[j0 + l + 16 * u]) : v[j0 + l + 16 * u];
+        for (int u = 0; u < 8; ++u) t[u] = SQUARE ? fmul(v[j0 + l + 16 * u], v[j0 + l + 16 * u]) : v[j0 + l + 16 * u];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc = fadd_chain(acc, t[u]);
-    }
-    for (int j = j0 + l; j < n; j += 16) acc = fadd_chain(acc, SQUARE ? fmul(v[j], v[j]) : v[j]);
+        for (int u = 0; u < 8; ++u) step(t[u]);
+      }
+      for (int j = j0 + l; j < n; j += 16) step(SQUARE ? fmul(v[j], v[j]) : v[j]);
+      return mk < kSubKeyNormal ? ffrom(kCanonNaN) : acc;  // NaN marks "recompute" (a NaN sum recomputes too)
+    };
+    float acc = chain(std::false_type{});
+    if (__builtin_expect(is_nan(acc), 0)) acc = chain(std::true_type{});
     acc = fold16(acc);
     if (l == 0) *bcast = acc;
   }
