@@ -138,6 +138,51 @@ __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
   const int N = a.N, t = threadIdx.x;
   const int64_t yrow = m * a.ldy;
   const bool norm = a.fn != ROWFN_SOFTMAX;
+  if (norm && N <= kRowThreads * kRowE) {
+    // A norm whose row fits one pass: each thread keeps its elements (and then the LayerNorm
+    // differences) in registers, and all threads write the terms of each sum (x, or the squares)
+    // to LDS, so the 16-lane chains only add. The same values in the same order as below.
+    float xv[kRowE], gv[kRowE], bv[kRowE];
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      const int j = t + u * kRowThreads;
+      xv[u] = *(j < N ? x + j : x);
+      gv[u] = *(j < N ? a.gamma + j : x);
+      bv[u] = *(a.beta && j < N ? a.beta + j : x);
+    }
+    const float kinv = recip_f(i2f(N));
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) xv[u] = ftz(xv[u]);
+    float rs;
+    if (a.fn == ROWFN_LAYERNORM) {
+#pragma unroll
+      for (int u = 0; u < kRowE; ++u)
+        if (t + u * kRowThreads < N) v[t + u * kRowThreads] = xv[u];
+      const float nmean = fneg(fmul(lds_sum16<false>(v, N, &bcast), kinv));
+#pragma unroll
+      for (int u = 0; u < kRowE; ++u) {
+        xv[u] = fadd(xv[u], nmean);  // d = x + -mean
+        if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
+      }
+      rs = rsqrt_f(fadd(fmul(lds_sum16<false>(v, N, &bcast), kinv), a.eps));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kRowE; ++u)
+        if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
+      const float ss = lds_sum16<false>(v, N, &bcast);
+      rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, a.eps));
+    }
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      const int j = t + u * kRowThreads;
+      if (j < N) {
+        float y = fmul(fmul(xv[u], rs), gv[u]);
+        if (a.beta) y = fadd(y, bv[u]);
+        store_out(a.y, yrow, j, a.out, y, a.out_scale);
+      }
+    }
+    return;
+  }
   // the row into LDS; the first pass's gamma and beta (norms) are fetched with it
   float g0[kRowE], b0[kRowE];
   for (int j0 = 0; j0 < N; j0 += kRowThreads * kRowE) {
