@@ -553,35 +553,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(TARS_LDS(p)));
 }
 
-// Eight V values of one column (rows at va + u * ROWB, 4- or 2-byte elements) and the eight
-// probabilities at pa, read from LDS in one sequence that waits for its own reads. Written as
-// assembly so that the compiler, which cannot tell the V ring's direct global -> LDS loads apart,
-// adds no wait for every one of them in flight before an LDS read; the ring's stage waits order it.
-template <int ROWB, bool VHALF>
-__device__ __forceinline__ void ring_read8(uint32_t va, uint32_t pa, uint32_t (&v)[8], float (&p)[8]) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 p0, p1;
-#define TARS_R(op)                                                                                        \
-  asm volatile(op " %0, %10\n\t" op " %1, %10 offset:%12\n\t" op " %2, %10 offset:%13\n\t"              \
-               op " %3, %10 offset:%14\n\t" op " %4, %10 offset:%15\n\t" op " %5, %10 offset:%16\n\t"  \
-               op " %6, %10 offset:%17\n\t" op " %7, %10 offset:%18\n\t"                              \
-               "ds_read_b128 %8, %11\n\tds_read_b128 %9, %11 offset:16\n\ts_waitcnt lgkmcnt(0)"        \
-               : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), \
-                 "=&v"(v[7]), "=&v"(p0), "=&v"(p1)                                                        \
-               : "v"(va), "v"(pa), "i"(ROWB), "i"(2 * ROWB), "i"(3 * ROWB), "i"(4 * ROWB), "i"(5 * ROWB),   \
-                 "i"(6 * ROWB), "i"(7 * ROWB)                                                             \
-               : "memory")
-  if constexpr (VHALF) TARS_R("ds_read_u16");
-  else TARS_R("ds_read_b32");
-#undef TARS_R
-  p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
-  p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
+// One direct global -> LDS load of the V ring (global_load_lds_dwordx4; dst is the wave-uniform LDS
+// address of the 1 KiB block), written as assembly that sets M0 itself. The compiler does not see
+// it as a write to LDS, so it adds no wait for every such load in flight before a later LDS read
+// (which it does for the builtin, not knowing which bytes it writes); the ring's stage waits and
+// barriers order the ring instead. No other code in the kernel keeps a value in M0.
+__device__ __forceinline__ void ring_load16(const void* src, uint32_t dst) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(dst) : "memory");
 }
 
-// The scores of query row m of head h: 16-lane group g takes keys g, g + 16, ..., KF of them per
-// pass with their K rows loaded together and their chains interleaved. The chains run unflushed
-// (qv is flushed) and are checked; a pass is recomputed with the contract's flushes when a key
-// element, a product or a partial sum is subnormal.
 template <int U, int KF>
 __device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int g, int l, bool last,
                                             const float (&qv)[U], float* sp) {
@@ -654,7 +634,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       const int i = wave + 4 * u;
       const int byte = i * 1024 + lane * 16;
       const int row = min(st * SR + byte / ROWB, nk - 1);
-      stage16(vbase + static_cast<int64_t>(row) * a.ldv + byte % ROWB, slot + i * 1024);
+      ring_load16(vbase + static_cast<int64_t>(row) * a.ldv + byte % ROWB,
+                  __builtin_amdgcn_readfirstlane(lds_addr(slot + i * 1024)));
     }
   };
   for (int m = 0; m < a.M; ++m) {
@@ -706,6 +687,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       if (st + kAttnSlots - 1 < NS) issue(st + kAttnSlots - 1);
       wait_stages_ahead<L, kAttnSlots - 1>(min(NS - 1 - st, kAttnSlots - 1));
       __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the slot's reads stay after the barrier
       if (t < HD) {
         const int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
         const float* ps = sp + st * SR;
@@ -721,21 +703,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         uint32_t mk = ~0u;
         int rr = 0;
         auto blocks = [&](auto vt) {
-          for (; rr + 8 <= rows; rr += 8) {  // the block's LDS reads and products first, then its chain steps
-            uint32_t vb[8];
-            float pb[8], pv[8];
-            ring_read8<ROWB, VHALF>(lds_addr(slot + rr * ROWB + ES * t), lds_addr(ps + rr), vb, pb);
+          constexpr int RB = SR < 16 ? SR : 16;
+          for (; rr + RB <= rows; rr += RB) {  // the block's LDS reads and products first, then its chain steps
+            float pv[RB], sums[RB];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const float v = VHALF ? from_fp16_bits(vb[u]) : __uint_as_float(vb[u]);
-              pv[u] = __fmul_rn(pb[u], v);
+            for (int u = 0; u < RB; ++u) {
+              const float v = vval(rr + u);
+              pv[u] = __fmul_rn(ps[rr + u], v);
               if constexpr (decltype(vt)::value) mk = min_key(mk, v, v);
             }
-            float sums[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) sums[u] = acc = __fadd_rn(acc, pv[u]);
+            for (int u = 0; u < RB; ++u) sums[u] = acc = __fadd_rn(acc, pv[u]);
 #pragma unroll
-            for (int u = 0; u < 8; u += 2) mk = min_key(min_key(mk, pv[u], pv[u + 1]), sums[u], sums[u + 1]);
+            for (int u = 0; u < RB; u += 2) mk = min_key(min_key(mk, pv[u], pv[u + 1]), sums[u], sums[u + 1]);
           }
         };
         if (vtest) blocks(std::true_type{});
