@@ -257,6 +257,10 @@ bool attention_supported(int hd, int nk);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s);
+// An ELT ADD (dense fp32 rows, fp32 output, no activation) and the LayerNorm / RMSNorm / L2Norm of
+// its output in one launch: the ELT's output is written, then normalized as launch_row would.
+bool add_norm_supported(int M, int N);
+hipError_t launch_add_norm(const EltArgs& e, const RowArgs& r, hipStream_t s);
 hipError_t launch_elt(const EltArgs& a, hipStream_t s);
 hipError_t launch_rope(const RopeArgs& a, hipStream_t s);
 hipError_t launch_relu(const ReluArgs& a, hipStream_t s);

@@ -714,6 +714,91 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
   return rc;
 }
 
+// A residual ELT ADD followed by the norm of its output (a decoder's add -> RMSNorm pairs) runs as
+// one launch (tars::launch_add_norm), bit-identical to the two in order. Taken when the ELT is dense
+// fp32 with an fp32 output, no activation and no fp16 state, the next descriptor is a LayerNorm /
+// RMSNorm / L2Norm whose input rows are exactly the ELT's output rows, the rows fit the kernel, the
+// ELT runs in place or apart from its A rows, and no output of the pair lands on the ELT's B rows,
+// gamma, beta, the other output, the norm's input, or a later descriptor.
+int launch_add_norm_pair(uint8_t* image, const Desc& d, const Desc& rd, hipStream_t s) {
+  uint8_t* B = image + d[F_BASE_ADDR];
+  uint8_t* RB = image + rd[F_BASE_ADDR];
+  const int M = static_cast<int>(d[F_M]), N = static_cast<int>(d[F_N]);
+  const auto f32_bits = [](uint64_t v) {
+    const uint32_t b = static_cast<uint32_t>(v);
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+  };
+  tars::EltArgs e{};
+  e.A = B + d[F_A_OFF];
+  e.lda = static_cast<int64_t>(strides(d).lda);
+  e.B = reinterpret_cast<const float*>(B + d[F_W_OFF]);
+  e.ldb = static_cast<int64_t>(b_stride(d).first);
+  e.bmode = BM_DENSE;
+  e.op = tars::ELTOP_ADD;
+  e.Y = B + d[F_Y_OFF];
+  e.ldy = static_cast<int64_t>(strides(d).ldy);
+  e.M = M;
+  e.N = N;
+  tars::RowArgs r{};
+  r.x = RB + rd[F_A_OFF];
+  r.lda = static_cast<int64_t>(strides(rd).lda);
+  r.fn = static_cast<int>(rd[F_CTRL] & 7);
+  r.gamma = reinterpret_cast<const float*>(RB + rd[F_SCALE_OFF]);
+  r.beta = has_bias(rd[F_EPI]) ? reinterpret_cast<const float*>(RB + rd[F_BIAS_OFF]) : nullptr;
+  r.eps = f32_bits(rd[F_W_OFF]);
+  r.y = RB + rd[F_Y_OFF];
+  r.ldy = static_cast<int64_t>(strides(rd).ldy);
+  r.out = static_cast<int>(out_code(rd[F_EPI]));
+  r.out_scale = f32_bits(rd[F_OUT_SCALE]);
+  r.M = M;
+  r.N = N;
+  const hipError_t err = tars::launch_add_norm(e, r, s);
+  if (err != hipSuccess) {
+    tars::set_last_error(std::string("HIP launch failed: ") + hipGetErrorString(err));
+    return TARS_E_DEVICE;
+  }
+  return TARS_OK;
+}
+
+int fuse_add_norm(uint8_t* image, const Checked& e, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
+                  int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
+                  int& fused, Desc& norm) {
+  fused = 0;
+  const Desc& d = e.d;
+  if (!g_fusion || d[F_OPCODE] != OP_ELT || (d[F_CTRL] & 3) != ELT_ADD || d[F_HDR_RSV] != 0 ||
+      act_code(d[F_EPI]) != 0 || out_code(d[F_EPI]) != OUT_FP32 || i + 1 >= n || static_cast<uint64_t>(i) + 1 >= in_image)
+    return TARS_OK;
+  const Checked r = check(q.data() + static_cast<size_t>(i + 1) * kDescBytes, image_len, core_id, gemv_only);
+  const Desc& rd = r.d;
+  const uint64_t fn = rd[F_CTRL] & 7;
+  const uintptr_t img = reinterpret_cast<uintptr_t>(image);
+  if (e.err != E_OK || e.overlap || r.err != E_OK || r.overlap || rd[F_OPCODE] != OP_ROW ||
+      (fn != ROW_LAYERNORM && fn != ROW_RMSNORM && fn != ROW_L2NORM) || (img + d[F_BASE_ADDR]) % 16 ||
+      (img + rd[F_BASE_ADDR]) % 16 || rd[F_M] != d[F_M] || rd[F_N] != d[F_N] ||
+      !tars::add_norm_supported(static_cast<int>(d[F_M]), static_cast<int>(d[F_N])) ||
+      addr(rd, F_A_OFF) != addr(d, F_Y_OFF) || strides(rd).lda != strides(d).ldy)
+    return TARS_OK;
+  const uint64_t M = d[F_M], N = d[F_N];
+  const Segs a_rows = strided(addr(d, F_A_OFF), strides(d).lda, M, 4 * N);
+  Segs ins = strided(addr(d, F_W_OFF), b_stride(d).first, M, 4 * N);
+  ins.push_back(interval(addr(rd, F_SCALE_OFF), addr(rd, F_SCALE_OFF) + 4 * N));
+  if (has_bias(rd[F_EPI])) ins.push_back(interval(addr(rd, F_BIAS_OFF), addr(rd, F_BIAS_OFF) + 4 * N));
+  const bool in_place = addr(d, F_Y_OFF) == addr(d, F_A_OFF) && strides(d).ldy == strides(d).lda;
+  Segs outs = e.y;
+  outs.insert(outs.end(), r.y.begin(), r.y.end());
+  if (!pairwise_disjoint(outs) || overlaps(ins, outs) || overlaps(a_rows, r.y) || (!in_place && overlaps(a_rows, e.y)) ||
+      (rest_lo < rest_hi && overlaps(Segs{interval(rest_lo, rest_hi)}, outs)))
+    return TARS_OK;
+  const int rc = launch_add_norm_pair(image, d, rd, s);
+  if (rc == TARS_OK) {
+    fused = 1;
+    norm = rd;
+  }
+  return rc;
+}
+
 // ---------------------------------------------------------------------------- launch plans
 // A decode loop runs the same descriptor bytes every token. A queue that ran to the end with no
 // hand-off and no output over its own descriptors leaves a plan (its launches in order, with the
@@ -726,6 +811,8 @@ struct Step {
   Desc d;                   // the descriptor (the quantizer of a fused group)
   std::vector<Desc> group;  // the GEMMs fused with it (empty: a single launch)
   std::vector<AttnHead> attn;  // or: the heads of a fused attention launch
+  Desc norm{};                 // or (add_norm): the norm fused with the ELT ADD in d
+  bool add_norm = false;
 };
 
 struct Plan {
@@ -749,7 +836,8 @@ bool g_graphs = true;
 int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) {
   for (const Step& st : steps) {
     bool needs_host = false;
-    const int rc = !st.attn.empty()   ? launch_attention_group(image, st.attn, s)
+    const int rc = st.add_norm        ? launch_add_norm_pair(image, st.d, st.norm, s)
+                   : !st.attn.empty() ? launch_attention_group(image, st.attn, s)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
                                       : launch_fused(image, st.d, st.group, s);
     if (rc != TARS_OK) return rc;
@@ -920,6 +1008,20 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     if (fused) {
       if (cacheable) steps.push_back(Step{c.d, {}, std::move(heads)});
       i += 3 * fused - 1;  // `fused` heads of three descriptors ran as one launch
+      continue;
+    }
+    Desc norm{};
+    if (int rc = fuse_add_norm(image, c, q, i, in_image, n, static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) *
+                               (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, norm))
+      return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+    if (fused) {
+      if (cacheable) {
+        Step st2{c.d, {}, {}};
+        st2.norm = norm;
+        st2.add_norm = true;
+        steps.push_back(std::move(st2));
+      }
+      ++i;  // the ELT and its norm ran as one launch
       continue;
     }
     bool needs_host = false;

@@ -127,6 +127,48 @@ constexpr int kLdsRow = 12288;
 // element); rows up to kRowThreads * kRowE elements take one pass.
 constexpr int kRowE = 8;
 
+// A norm whose row fits one pass of kRowThreads * kRowE elements: each thread keeps its elements
+// (and then the LayerNorm differences) in registers, and all threads write the terms of each sum
+// (x, or the squares) to LDS, so the 16-lane chains only add. xv: the thread's raw elements
+// t + u * kRowThreads of row m; gv, bv: gamma and beta there. The same values in the same order as
+// the general path of row_lds_kernel.
+__device__ __forceinline__ void norm_in_regs(const RowArgs& a, int m, float (&xv)[kRowE], const float (&gv)[kRowE],
+                                             const float (&bv)[kRowE], float* v, float* bcast) {
+  const int N = a.N, t = threadIdx.x;
+  const int64_t yrow = m * a.ldy;
+  const float kinv = recip_f(i2f(N));
+#pragma unroll
+  for (int u = 0; u < kRowE; ++u) xv[u] = ftz(xv[u]);
+  float rs;
+  if (a.fn == ROWFN_LAYERNORM) {
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u)
+      if (t + u * kRowThreads < N) v[t + u * kRowThreads] = xv[u];
+    const float nmean = fneg(fmul(lds_sum16<false>(v, N, bcast), kinv));
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u) {
+      xv[u] = fadd(xv[u], nmean);  // d = x + -mean
+      if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
+    }
+    rs = rsqrt_f(fadd(fmul(lds_sum16<false>(v, N, bcast), kinv), a.eps));
+  } else {
+#pragma unroll
+    for (int u = 0; u < kRowE; ++u)
+      if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
+    const float ss = lds_sum16<false>(v, N, bcast);
+    rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, a.eps));
+  }
+#pragma unroll
+  for (int u = 0; u < kRowE; ++u) {
+    const int j = t + u * kRowThreads;
+    if (j < N) {
+      float y = fmul(fmul(xv[u], rs), gv[u]);
+      if (a.beta) y = fadd(y, bv[u]);
+      store_out(a.y, yrow, j, a.out, y, a.out_scale);
+    }
+  }
+}
+
 __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
   __shared__ float v[kLdsRow];
   __shared__ uint32_t red[kRowThreads / 64 + 1];
@@ -139,9 +181,6 @@ __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
   const int64_t yrow = m * a.ldy;
   const bool norm = a.fn != ROWFN_SOFTMAX;
   if (norm && N <= kRowThreads * kRowE) {
-    // A norm whose row fits one pass: each thread keeps its elements (and then the LayerNorm
-    // differences) in registers, and all threads write the terms of each sum (x, or the squares)
-    // to LDS, so the 16-lane chains only add. The same values in the same order as below.
     float xv[kRowE], gv[kRowE], bv[kRowE];
 #pragma unroll
     for (int u = 0; u < kRowE; ++u) {
@@ -150,37 +189,7 @@ __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
       gv[u] = *(j < N ? a.gamma + j : x);
       bv[u] = *(a.beta && j < N ? a.beta + j : x);
     }
-    const float kinv = recip_f(i2f(N));
-#pragma unroll
-    for (int u = 0; u < kRowE; ++u) xv[u] = ftz(xv[u]);
-    float rs;
-    if (a.fn == ROWFN_LAYERNORM) {
-#pragma unroll
-      for (int u = 0; u < kRowE; ++u)
-        if (t + u * kRowThreads < N) v[t + u * kRowThreads] = xv[u];
-      const float nmean = fneg(fmul(lds_sum16<false>(v, N, &bcast), kinv));
-#pragma unroll
-      for (int u = 0; u < kRowE; ++u) {
-        xv[u] = fadd(xv[u], nmean);  // d = x + -mean
-        if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
-      }
-      rs = rsqrt_f(fadd(fmul(lds_sum16<false>(v, N, &bcast), kinv), a.eps));
-    } else {
-#pragma unroll
-      for (int u = 0; u < kRowE; ++u)
-        if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
-      const float ss = lds_sum16<false>(v, N, &bcast);
-      rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, a.eps));
-    }
-#pragma unroll
-    for (int u = 0; u < kRowE; ++u) {
-      const int j = t + u * kRowThreads;
-      if (j < N) {
-        float y = fmul(fmul(xv[u], rs), gv[u]);
-        if (a.beta) y = fadd(y, bv[u]);
-        store_out(a.y, yrow, j, a.out, y, a.out_scale);
-      }
-    }
+    norm_in_regs(a, m, xv, gv, bv, v, &bcast);
     return;
   }
   // the row into LDS; the first pass's gamma and beta (norms) are fetched with it
@@ -257,6 +266,37 @@ __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
       }
     }
   }
+}
+
+// A residual add and the norm that reads it (the executor's fusion of an ELT ADD on dense fp32
+// rows with an fp32 output, no activation, and the LayerNorm / RMSNorm / L2Norm of its output, rows
+// of at most kRowThreads * kRowE elements): each thread adds its elements as elt_fast_kernel does,
+// writes the sums (the ELT's output) and runs the norm on them from registers. In place is as safe
+// as for the ELT alone: each element is read and written by one thread.
+__global__ __launch_bounds__(kRowThreads) void add_norm_kernel(EltArgs e, RowArgs r) {
+  __shared__ float v[kRowThreads * kRowE];
+  __shared__ float bcast;
+  __asm__ volatile("" : : "s"(e.A), "s"(e.lda), "s"(e.B), "s"(e.ldb), "s"(r.gamma), "s"(r.beta), "s"(r.N));
+  const int m = blockIdx.x, t = threadIdx.x, N = r.N;
+  const float* A = frow(e.A, e.lda, m);
+  const float* B = frow(e.B, e.ldb, m);
+  float xa[kRowE], xb[kRowE], gv[kRowE], bv[kRowE];
+#pragma unroll
+  for (int u = 0; u < kRowE; ++u) {
+    const int j = t + u * kRowThreads;
+    xa[u] = *(j < N ? A + j : A);
+    xb[u] = *(j < N ? B + j : B);
+    gv[u] = *(j < N ? r.gamma + j : A);
+    bv[u] = *(r.beta && j < N ? r.beta + j : A);
+  }
+  float* Y = reinterpret_cast<float*>(static_cast<char*>(e.Y) + m * e.ldy);
+#pragma unroll
+  for (int u = 0; u < kRowE; ++u) {
+    const int j = t + u * kRowThreads;
+    xa[u] = ftz(fadd(act_fn(xa[u], 0), xb[u]));
+    if (j < N) Y[j] = xa[u];
+  }
+  norm_in_regs(r, m, xa, gv, bv, v, &bcast);
 }
 
 // Longer rows: one 16-lane group per row, the lane's elements streamed in blocks.
@@ -744,6 +784,13 @@ dim3 row_grid(int M, int N, int per) {
 }
 
 }  // namespace
+
+bool add_norm_supported(int M, int N) { return M >= 1 && M <= 65535 && N >= 1 && N <= kRowThreads * kRowE; }
+
+hipError_t launch_add_norm(const EltArgs& e, const RowArgs& r, hipStream_t s) {
+  hipLaunchKernelGGL(add_norm_kernel, dim3(r.M), dim3(kRowThreads), 0, s, e, r);
+  return hipGetLastError();
+}
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s) {
   if (a.N <= kLdsRow)

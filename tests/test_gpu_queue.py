@@ -411,6 +411,49 @@ def test_chains_whose_partial_sums_are_subnormal(seed, fusion):
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
+def add_residual_norm(p: Program, M: int, N: int, inplace: bool, norm_over_b: bool = False):
+    """A residual ELT ADD of dense fp32 rows (fp32 out, no activation) and a norm of its output, the
+    pair the executor fuses; norm_over_b: the norm writes over the ELT's B rows (fp32), which the
+    executor must not fuse."""
+    rng = p.rng
+    a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    b, ldb16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    y, ldy16 = (a, lda16) if inplace else stride_fields(p, M, 4 * N)
+    p.add(OPCODE=Q.OP_ELT, CTRL=Q.ELT_ADD, EPI=Q.epi(), A_OFF=a, W_OFF=b, Y_OFF=y, M=M, N=N, LDA16=lda16, LDY16=ldy16,
+          GROUP_SIZE=ldb16)
+    fn = int(rng.choice([Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM]))
+    if norm_over_b:
+        out, yo, ldyo16, osc = Q.OUT_FP32, b, ldb16, 0
+    else:
+        out, yo, ldyo16, osc = out_fields(p, M, N)
+    g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
+    bias = int(rng.integers(0, 2))
+    bb = p.put(rng.normal(0, 0.1, N).astype("<f4").tobytes()) if bias else 0
+    p.add(OPCODE=Q.OP_ROW, CTRL=fn, EPI=Q.epi(out=out, bias=bias), A_OFF=y, Y_OFF=yo, SCALE_OFF=g, BIAS_OFF=bb,
+          W_OFF=f32bits(float(rng.choice([1e-6, 1e-5, 0.0]))), M=M, N=N, LDA16=ldy16, LDY16=ldyo16, OUT_SCALE=osc)
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_residual_add_then_norm(seed, fusion):
+    """ELT ADD -> norm pairs, which the executor runs as one launch: in place and apart, every norm,
+    with and without beta, every output format, rows up to the fused kernel's 2048 elements and one
+    block past it (not fused), and a pair whose norm writes over the ELT's B rows (not fused); the
+    images equal the oracle's."""
+    p = Program(8100 + seed)
+    for k, (M, N) in enumerate(((1, 1024), (3, 2048), (2, 224), (1, 2064), (4, 1024))):
+        add_residual_norm(p, M, N, inplace=bool(k % 2))
+    add_residual_norm(p, 1, 1024, inplace=True, norm_over_b=True)
+    prev = NQ.set_fusion(fusion)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 @pytest.mark.parametrize("seed", range(3))
 def test_host_copy_of_the_queue_gives_the_same_result(seed):
     p = random_program(200 + seed)
