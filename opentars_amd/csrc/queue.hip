@@ -720,27 +720,16 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
 // RMSNorm / L2Norm whose input rows are exactly the ELT's output rows, the rows fit the kernel, the
 // ELT runs in place or apart from its A rows, and no output of the pair lands on the ELT's B rows,
 // gamma, beta, the other output, the norm's input, or a later descriptor.
-int launch_add_norm_pair(uint8_t* image, const Desc& d, const Desc& rd, hipStream_t s) {
-  uint8_t* B = image + d[F_BASE_ADDR];
+float f32_bits(uint64_t v) {
+  const uint32_t b = static_cast<uint32_t>(v);
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+
+// The kernel arguments of a LayerNorm / RMSNorm / L2Norm descriptor (as tars_row_op builds them).
+tars::RowArgs norm_args(uint8_t* image, const Desc& rd) {
   uint8_t* RB = image + rd[F_BASE_ADDR];
-  const int M = static_cast<int>(d[F_M]), N = static_cast<int>(d[F_N]);
-  const auto f32_bits = [](uint64_t v) {
-    const uint32_t b = static_cast<uint32_t>(v);
-    float f;
-    std::memcpy(&f, &b, 4);
-    return f;
-  };
-  tars::EltArgs e{};
-  e.A = B + d[F_A_OFF];
-  e.lda = static_cast<int64_t>(strides(d).lda);
-  e.B = reinterpret_cast<const float*>(B + d[F_W_OFF]);
-  e.ldb = static_cast<int64_t>(b_stride(d).first);
-  e.bmode = BM_DENSE;
-  e.op = tars::ELTOP_ADD;
-  e.Y = B + d[F_Y_OFF];
-  e.ldy = static_cast<int64_t>(strides(d).ldy);
-  e.M = M;
-  e.N = N;
   tars::RowArgs r{};
   r.x = RB + rd[F_A_OFF];
   r.lda = static_cast<int64_t>(strides(rd).lda);
@@ -752,9 +741,26 @@ int launch_add_norm_pair(uint8_t* image, const Desc& d, const Desc& rd, hipStrea
   r.ldy = static_cast<int64_t>(strides(rd).ldy);
   r.out = static_cast<int>(out_code(rd[F_EPI]));
   r.out_scale = f32_bits(rd[F_OUT_SCALE]);
-  r.M = M;
-  r.N = N;
-  const hipError_t err = tars::launch_add_norm(e, r, s);
+  r.M = static_cast<int>(rd[F_M]);
+  r.N = static_cast<int>(rd[F_N]);
+  return r;
+}
+
+int launch_add_norm_pair(uint8_t* image, const Desc& d, const Desc& rd, hipStream_t s) {
+  uint8_t* B = image + d[F_BASE_ADDR];
+  const int M = static_cast<int>(d[F_M]), N = static_cast<int>(d[F_N]);
+  tars::EltArgs e{};
+  e.A = B + d[F_A_OFF];
+  e.lda = static_cast<int64_t>(strides(d).lda);
+  e.B = reinterpret_cast<const float*>(B + d[F_W_OFF]);
+  e.ldb = static_cast<int64_t>(b_stride(d).first);
+  e.bmode = BM_DENSE;
+  e.op = tars::ELTOP_ADD;
+  e.Y = B + d[F_Y_OFF];
+  e.ldy = static_cast<int64_t>(strides(d).ldy);
+  e.M = M;
+  e.N = N;
+  const hipError_t err = tars::launch_add_norm(e, norm_args(image, rd), s);
   if (err != hipSuccess) {
     tars::set_last_error(std::string("HIP launch failed: ") + hipGetErrorString(err));
     return TARS_E_DEVICE;
@@ -799,6 +805,66 @@ int fuse_add_norm(uint8_t* image, const Checked& e, const std::vector<uint8_t>& 
   return rc;
 }
 
+// A norm with an fp32 output followed by the RoPE of its output rows (a decoder's q / k norm and
+// rotation) runs as one launch (tars::launch_norm_rope), bit-identical to the two in order. Taken
+// when the RoPE's input rows are exactly the norm's output rows, both write fp32, the rows fit the
+// kernel, and neither output lands on an input of the pair (the norm's rows, gamma, beta, the
+// table), on the other output or on a later descriptor.
+int launch_norm_rope_pair(uint8_t* image, const Desc& rd, const Desc& pd, hipStream_t s) {
+  uint8_t* PB = image + pd[F_BASE_ADDR];
+  tars::RopeArgs p{};
+  p.x = PB + pd[F_A_OFF];
+  p.lda = static_cast<int64_t>(strides(pd).lda);
+  p.tab = reinterpret_cast<const float*>(PB + pd[F_W_OFF]);
+  p.rows_per_pos = static_cast<int>(pd[F_GROUP_SIZE]);
+  p.rot = static_cast<int>(pd[F_K]);
+  p.y = PB + pd[F_Y_OFF];
+  p.ldy = static_cast<int64_t>(strides(pd).ldy);
+  p.M = static_cast<int>(pd[F_M]);
+  p.N = static_cast<int>(pd[F_N]);
+  const hipError_t err = tars::launch_norm_rope(norm_args(image, rd), p, s);
+  if (err != hipSuccess) {
+    tars::set_last_error(std::string("HIP launch failed: ") + hipGetErrorString(err));
+    return TARS_E_DEVICE;
+  }
+  return TARS_OK;
+}
+
+int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
+                   int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
+                   int& fused, Desc& rope) {
+  fused = 0;
+  const Desc& rd = r.d;
+  const uint64_t fn = rd[F_CTRL] & 7;
+  if (!g_fusion || rd[F_OPCODE] != OP_ROW || (fn != ROW_LAYERNORM && fn != ROW_RMSNORM && fn != ROW_L2NORM) ||
+      out_code(rd[F_EPI]) != OUT_FP32 || i + 1 >= n || static_cast<uint64_t>(i) + 1 >= in_image)
+    return TARS_OK;
+  const Checked p = check(q.data() + static_cast<size_t>(i + 1) * kDescBytes, image_len, core_id, gemv_only);
+  const Desc& pd = p.d;
+  const uintptr_t img = reinterpret_cast<uintptr_t>(image);
+  if (r.err != E_OK || r.overlap || p.err != E_OK || p.overlap || pd[F_OPCODE] != OP_ROPE ||
+      out_code(pd[F_EPI]) != OUT_FP32 || (img + rd[F_BASE_ADDR]) % 16 || (img + pd[F_BASE_ADDR]) % 16 ||
+      pd[F_M] != rd[F_M] || pd[F_N] != rd[F_N] ||
+      !tars::add_norm_supported(static_cast<int>(rd[F_M]), static_cast<int>(rd[F_N])) ||
+      addr(pd, F_A_OFF) != addr(rd, F_Y_OFF) || strides(pd).lda != strides(rd).ldy)
+    return TARS_OK;
+  Segs ins;
+  for (const Segs& x : r.reads) ins.insert(ins.end(), x.begin(), x.end());
+  const uint64_t tab_rows = (pd[F_M] - 1) / pd[F_GROUP_SIZE] + 1;
+  ins.push_back(interval(addr(pd, F_W_OFF), addr(pd, F_W_OFF) + static_cast<u128>(4 * pd[F_K]) * tab_rows));
+  Segs outs = r.y;
+  outs.insert(outs.end(), p.y.begin(), p.y.end());
+  if (!pairwise_disjoint(outs) || overlaps(ins, outs) ||
+      (rest_lo < rest_hi && overlaps(Segs{interval(rest_lo, rest_hi)}, outs)))
+    return TARS_OK;
+  const int rc = launch_norm_rope_pair(image, rd, pd, s);
+  if (rc == TARS_OK) {
+    fused = 1;
+    rope = pd;
+  }
+  return rc;
+}
+
 // ---------------------------------------------------------------------------- launch plans
 // A decode loop runs the same descriptor bytes every token. A queue that ran to the end with no
 // hand-off and no output over its own descriptors leaves a plan (its launches in order, with the
@@ -811,8 +877,9 @@ struct Step {
   Desc d;                   // the descriptor (the quantizer of a fused group)
   std::vector<Desc> group;  // the GEMMs fused with it (empty: a single launch)
   std::vector<AttnHead> attn;  // or: the heads of a fused attention launch
-  Desc norm{};                 // or (add_norm): the norm fused with the ELT ADD in d
-  bool add_norm = false;
+  Desc second{};               // or: the second descriptor of a fused pair with d
+  bool add_norm = false;       // d an ELT ADD, second its norm
+  bool norm_rope = false;      // d a norm, second its RoPE
 };
 
 struct Plan {
@@ -836,7 +903,8 @@ bool g_graphs = true;
 int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) {
   for (const Step& st : steps) {
     bool needs_host = false;
-    const int rc = st.add_norm        ? launch_add_norm_pair(image, st.d, st.norm, s)
+    const int rc = st.add_norm        ? launch_add_norm_pair(image, st.d, st.second, s)
+                   : st.norm_rope     ? launch_norm_rope_pair(image, st.d, st.second, s)
                    : !st.attn.empty() ? launch_attention_group(image, st.attn, s)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
                                       : launch_fused(image, st.d, st.group, s);
@@ -1017,11 +1085,25 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     if (fused) {
       if (cacheable) {
         Step st2{c.d, {}, {}};
-        st2.norm = norm;
+        st2.second = norm;
         st2.add_norm = true;
         steps.push_back(std::move(st2));
       }
       ++i;  // the ELT and its norm ran as one launch
+      continue;
+    }
+    Desc rope{};
+    if (int rc = fuse_norm_rope(image, c, q, i, in_image, n, static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) *
+                                (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, rope))
+      return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+    if (fused) {
+      if (cacheable) {
+        Step st2{c.d, {}, {}};
+        st2.second = rope;
+        st2.norm_rope = true;
+        steps.push_back(std::move(st2));
+      }
+      ++i;  // the norm and its RoPE ran as one launch
       continue;
     }
     bool needs_host = false;

@@ -299,6 +299,44 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(EltArgs e, RowArg
   norm_in_regs(r, m, xa, gv, bv, v, &bcast);
 }
 
+// A norm (LayerNorm / RMSNorm / L2Norm, fp32 output) and the RoPE of its output rows (fp32 output;
+// the executor's fusion of a decoder's q / k norm and rotation, rows of at most kRowThreads * kRowE
+// elements): each workgroup normalizes its row as row_lds_kernel does and stores it; after a
+// workgroup barrier, which makes the row's stores visible to the workgroup, it rotates the stored
+// values as rope_fast_kernel does.
+__global__ __launch_bounds__(kRowThreads) void norm_rope_kernel(RowArgs r, RopeArgs p) {
+  __shared__ float v[kRowThreads * kRowE];
+  __shared__ float bcast;
+  __asm__ volatile("" : : "s"(r.x), "s"(r.lda), "s"(r.gamma), "s"(r.beta), "s"(r.N));
+  const int m = blockIdx.x, t = threadIdx.x, N = r.N;
+  const float* x = frow(r.x, r.lda, m);
+  float xv[kRowE], gv[kRowE], bv[kRowE];
+#pragma unroll
+  for (int u = 0; u < kRowE; ++u) {
+    const int j = t + u * kRowThreads;
+    xv[u] = *(j < N ? x + j : x);
+    gv[u] = *(j < N ? r.gamma + j : x);
+    bv[u] = *(r.beta && j < N ? r.beta + j : x);
+  }
+  norm_in_regs(r, m, xv, gv, bv, v, &bcast);
+  __syncthreads();
+  const float* xr = frow(p.x, p.lda, m);
+  const float* tb = p.tab + static_cast<int64_t>(static_cast<unsigned>(m) / static_cast<unsigned>(p.rows_per_pos)) * p.rot;
+  const int h = p.rot / 2;
+  float* y = reinterpret_cast<float*>(static_cast<char*>(p.y) + m * p.ldy);
+  for (int n = t; n < N; n += kRowThreads) {
+    const bool lo = n < h, rotated = n < p.rot;
+    const int q = lo ? n + h : rotated ? n - h : n;  // rotation partner
+    const int c = lo ? n : rotated ? n - h : 0;      // cos index; the sin is at h + c
+    const float xn = xr[n], xp = xr[q], tc = tb[c], ts = tb[h + c];
+    float o;
+    if (lo) o = fadd(fmul(xn, tc), fneg(fmul(xp, ts)));
+    else if (rotated) o = fadd(fmul(xn, tc), fmul(xp, ts));
+    else o = ftz(xn);
+    y[n] = ftz(o);
+  }
+}
+
 // Longer rows: one 16-lane group per row, the lane's elements streamed in blocks.
 __global__ __launch_bounds__(kRowThreads) void row_kernel(RowArgs a) {
   const int m = blockIdx.x * (kRowThreads / 16) + static_cast<int>(threadIdx.x >> 4);
@@ -786,6 +824,11 @@ dim3 row_grid(int M, int N, int per) {
 }  // namespace
 
 bool add_norm_supported(int M, int N) { return M >= 1 && M <= 65535 && N >= 1 && N <= kRowThreads * kRowE; }
+
+hipError_t launch_norm_rope(const RowArgs& r, const RopeArgs& p, hipStream_t s) {
+  hipLaunchKernelGGL(norm_rope_kernel, dim3(r.M), dim3(kRowThreads), 0, s, r, p);
+  return hipGetLastError();
+}
 
 hipError_t launch_add_norm(const EltArgs& e, const RowArgs& r, hipStream_t s) {
   hipLaunchKernelGGL(add_norm_kernel, dim3(r.M), dim3(kRowThreads), 0, s, e, r);

@@ -454,6 +454,48 @@ def test_residual_add_then_norm(seed, fusion):
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
+def add_norm_then_rope(p: Program, M: int, N: int, rot: int, G: int, rope_over_x: bool = False):
+    """A norm with an fp32 output and a RoPE of its output rows (fp32 out), the pair the executor
+    fuses; rope_over_x: the RoPE writes over the norm's input rows, which the executor must not
+    fuse."""
+    rng = p.rng
+    a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    y, ldy16 = stride_fields(p, M, 4 * N)
+    g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
+    bias = int(rng.integers(0, 2))
+    bb = p.put(rng.normal(0, 0.1, N).astype("<f4").tobytes()) if bias else 0
+    fn = int(rng.choice([Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM]))
+    p.add(OPCODE=Q.OP_ROW, CTRL=fn, EPI=Q.epi(bias=bias), A_OFF=a, Y_OFF=y, SCALE_OFF=g, BIAS_OFF=bb,
+          W_OFF=f32bits(1e-6), M=M, N=N, LDA16=lda16, LDY16=ldy16)
+    rows = (M - 1) // G + 1
+    fr = np.arange(rows, dtype=np.float32)[:, None] * rng.uniform(0.01, 1.0, rot // 2).astype(np.float32)[None, :]
+    t = p.put(np.concatenate([np.cos(fr), np.sin(fr)], 1).astype("<f4").tobytes())
+    yr, ldyr16 = (a, lda16) if rope_over_x else stride_fields(p, M, 4 * N)
+    p.add(OPCODE=Q.OP_ROPE, EPI=Q.epi(), A_OFF=y, W_OFF=t, Y_OFF=yr, M=M, N=N, K=rot, GROUP_SIZE=G, LDA16=ldy16,
+          LDY16=ldyr16)
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_norm_then_rope(seed, fusion):
+    """Norm -> RoPE pairs, which the executor runs as one launch: q / k shapes (16 and 8 rows of
+    128, one table row), several table rows, partial rotation, rows up to the fused kernel's 2048
+    elements and one block past it (not fused), and a RoPE over the norm's input (not fused); the
+    images equal the oracle's."""
+    p = Program(8300 + seed)
+    for M, N, rot, G in ((16, 128, 128, 16), (8, 128, 128, 8), (6, 256, 128, 2), (3, 2048, 2048, 1), (2, 2080, 64, 1)):
+        add_norm_then_rope(p, M, N, rot, G)
+    add_norm_then_rope(p, 4, 128, 128, 4, rope_over_x=True)
+    prev = NQ.set_fusion(fusion)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 @pytest.mark.parametrize("seed", range(3))
 def test_host_copy_of_the_queue_gives_the_same_result(seed):
     p = random_program(200 + seed)
