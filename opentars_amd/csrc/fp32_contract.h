@@ -56,6 +56,13 @@ __device__ __forceinline__ float chain_end(float acc) { return canon(acc); }
 // least 2^24 - 1 (one shift-add per value, one three-way minimum per two values).
 constexpr uint32_t kSubKeyNormal = 0x00FFFFFFu;
 __device__ __forceinline__ uint32_t sub_key(float x) { return (fbits(x) << 1) - 1u; }
+// A partial sum of magnitude at least 2^-100 absorbs any subnormal addend s: |s| < 2^-126 is below
+// half an ulp of it (>= 2^-124), so RN(acc + s) = acc, which is what acc + ftz(s) = acc + 0 gives.
+// A chain whose starting value and unflushed partial sums all avoid (0, 2^-100) in magnitude
+// therefore matches the contract without testing its products: a subnormal product added to a
+// zero shows up as a subnormal partial sum. kSubKeyTiny = sub_key(2^-100); a minimum below it
+// (including any subnormal, whose key is smaller still) sends the chain to the flushing recompute.
+constexpr uint32_t kSubKeyTiny = ((27u << 23) << 1) - 1u;
 __device__ __forceinline__ uint32_t min_key(uint32_t m, float a, float b) {
   return min(m, min(sub_key(a), sub_key(b)));
 }

@@ -640,6 +640,11 @@ __device__ __forceinline__ void ring_load16(const void* src, uint32_t dst) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(dst) : "memory");
 }
 
+// The scores of query row m of head h: 16-lane group g takes keys g, g + 16, ..., KF of them per
+// pass with their K rows loaded together and their chains interleaved. The chains run unflushed
+// (qv is flushed) and are checked; a pass is recomputed with the contract's flushes when a key
+// element or a partial sum lies in (0, 2^-100) in magnitude (a subnormal product is then absorbed
+// by its partial sum or shows in it, see kSubKeyTiny).
 template <int U, int KF>
 __device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int g, int l, bool last,
                                             const float (&qv)[U], float* sp) {
@@ -663,9 +668,9 @@ __device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int
       for (int c = 0; c < KF; ++c) {
         const float pr = __fmul_rn(qv[u], kv[c][u]);
         acc[c] = __fadd_rn(acc[c], pr);
-        mk = min_key(min_key(mk, kv[c][u], pr), acc[c], acc[c]);
+        mk = min_key(mk, kv[c][u], acc[c]);
       }
-    if (__builtin_expect(mk < kSubKeyNormal, 0)) {
+    if (__builtin_expect(mk < kSubKeyTiny, 0)) {
 #pragma unroll
       for (int c = 0; c < KF; ++c) acc[c] = 0.0f;
 #pragma unroll
@@ -775,10 +780,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                        : reinterpret_cast<const float*>(slot + rr * ROWB)[t];
         };
         // The stage's chain steps unflushed, checked (a probability is an fmul output: flushed,
-        // so only V (when vtest), the products and the partial sums are tested); recomputed from
-        // the stage's first value with the contract's flushes when any is subnormal.
+        // so only V (when vtest), the stage's first value and the partial sums are tested, the
+        // products' flushes being absorbed, see kSubKeyTiny); recomputed from the stage's first
+        // value with the contract's flushes when one lies in (0, 2^-100) in magnitude.
         const float acc0 = acc;
-        uint32_t mk = ~0u;
+        uint32_t mk = sub_key(acc0);
         int rr = 0;
         auto blocks = [&](auto vt) {
           constexpr int RB = SR < 16 ? SR : 16;
@@ -793,7 +799,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 0; u < RB; ++u) sums[u] = acc = __fadd_rn(acc, pv[u]);
 #pragma unroll
-            for (int u = 0; u < RB; u += 2) mk = min_key(min_key(mk, pv[u], pv[u + 1]), sums[u], sums[u + 1]);
+            for (int u = 0; u < RB; u += 2) mk = min_key(mk, sums[u], sums[u + 1]);
           }
         };
         if (vtest) blocks(std::true_type{});
@@ -801,9 +807,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         for (; rr < rows; ++rr) {
           const float v = vval(rr), pr = __fmul_rn(ps[rr], v);
           acc = __fadd_rn(acc, pr);
-          mk = min_key(min_key(mk, v, pr), acc, acc);
+          mk = min_key(mk, v, acc);
         }
-        if (__builtin_expect(mk < kSubKeyNormal, 0)) {
+        if (__builtin_expect(mk < kSubKeyTiny, 0)) {
           acc = acc0;
           for (rr = 0; rr < rows; ++rr) acc = fadd_chain(acc, fmul(ps[rr], vval(rr)));
         }

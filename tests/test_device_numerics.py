@@ -156,3 +156,28 @@ def test_q8_fast_path_for_rows_with_a_normal_maximum():
         with np.errstate(all="ignore"):
             fast = np.clip(np.rint(x * inv), -127, 127).astype(np.int8)
         assert (fast == F.q8(x, inv)).all(), amax
+
+
+def test_partial_sums_above_2_pow_minus_100_absorb_subnormal_addends():
+    """The attention chains skip their products' flushes when every partial sum avoids (0, 2^-100):
+    RN(acc + s) == acc for every |acc| >= 2^-100 and every subnormal s (random accumulators over
+    every exponent from -100 up, the smallest and largest mantissas at 2^-100, and subnormals at
+    both ends of the range and at random), while just below 2^-100 some do not."""
+    rng = np.random.default_rng(11)
+    sub = np.concatenate([np.array([1, 2, 0x7FFFFF, 0x7FFFFE, 0x400000], np.uint32),
+                          rng.integers(1, 1 << 23, 2000, dtype=np.uint32)])
+    sub = np.concatenate([sub, sub | np.uint32(0x80000000)]).view(f32)
+    accs = np.concatenate([np.array([0x0D800000, 0x0D800001, 0x0DFFFFFF, 0x7F7FFFFF], np.uint32),
+                           (rng.integers(27, 255, 3000, dtype=np.uint32) << 23) | rng.integers(0, 1 << 23, 3000, dtype=np.uint32)])
+    accs = np.concatenate([accs, accs | np.uint32(0x80000000)]).view(f32)
+    assert (np.abs(accs) >= f32(2.0 ** -100)).all()
+    for a in accs:
+        assert (np.float32(a) + sub == a).all(), a
+    below = np.float32(2.0 ** -100) * np.float32(1 - 2.0 ** -24)          # just below 2^-100
+    with np.errstate(all="ignore"):
+        assert ((np.float32(2.0 ** -110) + sub) != np.float32(2.0 ** -110)).any()
+    assert below < np.float32(2.0 ** -100)
+    key = lambda x: ((np.asarray(x, f32).view(np.uint32).astype(np.uint64) << 1) + 0xFFFFFFFF) & 0xFFFFFFFF  # (bits << 1) - 1 mod 2^32
+    tiny = ((27 << 23) << 1) - 1
+    assert key(np.float32(2.0 ** -100)) == tiny and key(below) < tiny and key(np.float32(0)) > tiny
+    assert (key(sub) < tiny).all()
