@@ -24,10 +24,17 @@ check of the timed outputs.
 """
 from __future__ import annotations
 
+import os
+
+# The CPU baseline is a single-core figure: pin every numeric library's thread pool to one thread
+# before numpy (or torch) loads its BLAS / OpenMP runtime.
+for _var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS", "BLIS_NUM_THREADS",
+             "NUMEXPR_NUM_THREADS"):
+    os.environ[_var] = "1"
+
 import argparse
 import ctypes
 import json
-import os
 import platform
 import sys
 import time
@@ -851,36 +858,65 @@ def cpu_baseline(launches, target_s: float, spot) -> dict:
             host[i] = {k: v.cpu().numpy() for k, v in l.operands.items()}
         return host[i]
 
-    elapsed, done_bytes, calls = 0.0, 0, 0
-    while elapsed < target_s:
-        for i, l in enumerate(launches):
-            o = operands(i, l)
-            t = time.perf_counter()
-            if l.kind == "quant_rows":
-                F.quant_rows(o["x"])
-            else:
-                G.gemm_rowcol(o["q"], o["s"], o["W"], o["scol"])
-            elapsed += time.perf_counter() - t
-            done_bytes += l.nbytes
-            calls += 1
-            if elapsed >= target_s:
-                break
-    cpu = platform.processor() or platform.machine()
+    for i, l in enumerate(launches):
+        operands(i, l)
+    # one core: the process is pinned to a single CPU for the timed loop (restored afterwards)
+    mask = os.sched_getaffinity(0)
+    pinned = min(mask)
+    os.sched_setaffinity(0, {pinned})
     try:
-        with open("/proc/cpuinfo") as fh:
-            for line in fh:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
+        elapsed, done_bytes, calls = 0.0, 0, 0
+        while elapsed < target_s:
+            for i, l in enumerate(launches):
+                o = host[i]
+                t = time.perf_counter()
+                if l.kind == "quant_rows":
+                    F.quant_rows(o["x"])
+                else:
+                    G.gemm_rowcol(o["q"], o["s"], o["W"], o["scol"])
+                elapsed += time.perf_counter() - t
+                done_bytes += l.nbytes
+                calls += 1
+                if elapsed >= target_s:
                     break
-    except OSError:
-        pass
+    finally:
+        os.sched_setaffinity(0, mask)
+    cpu = cpu_description()
     steps = done_bytes / sum(l.nbytes for l in launches)
     return {"value": round(done_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"numpy oracle over {calls} launches of the decode step in model order "
                       f"({steps:.2f} steps, {elapsed:.1f} s of compute)",
             "bit_exact_spot_check_layer0_qkv": exact,
-            "cpu_model": cpu, "os_cpu_count": os.cpu_count(),
-            "threads_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS")}}
+            "cpu_model": cpu, "os_cpu_count": os.cpu_count(), "pinned_cpu": pinned,
+            "threads_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS",
+                                                           "MKL_NUM_THREADS")}}
+
+
+def cpu_description() -> dict:
+    """The host CPU as /proc/cpuinfo and lscpu name it (a virtual machine may shorten the model name,
+    so the family / model / stepping numbers are reported too)."""
+    import subprocess
+    info = {"machine": platform.machine()}
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if not line.strip():
+                    break
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k in ("vendor_id", "cpu family", "model", "model name", "stepping", "cpu MHz"):
+                    info[k.replace(" ", "_")] = v.strip()
+    except OSError:
+        pass
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "BIOS Model name", "Socket(s)", "Core(s) per socket"):
+                info["lscpu_" + k.strip().replace(" ", "_").replace("(", "").replace(")", "")] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
 
 
 # ------------------------------------------------------------------------------ main
@@ -890,7 +926,6 @@ def main() -> int:
         print("bench.py measures one GPU: the matrix path runs on a single GPU here (sharding the "
               "output channels over several GPUs is not implemented); use --gpus 1", file=sys.stderr)
         return 2
-    os.environ.setdefault("OMP_NUM_THREADS", "1")
     import torch
     import opentars_amd
 

@@ -19,6 +19,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libopentars_amd.so"
+OBJ = PKG / "_build"
 SOURCES = ["abi.hip", "queue.hip", "quant_rows.hip", "gemv_w8a8.hip", "gemm_w8a8_mfma.hip", "w4a16.hip",
            "rowops.hip"]
 ARCH = "gfx950"
@@ -32,24 +33,41 @@ def hipcc() -> str:
 
 
 def flags() -> list[str]:
-    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             "-Wall", "-Wno-unused-function", "-I", str(PKG.parent / "include")]
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into one shared library next to this file (always rebuilds)."""
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *flags(), *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+_NOISE = "is not a recognized feature for this target"  # the host pass does not know the GPU feature
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in proc.stderr.splitlines() if _NOISE not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source into one shared library next to this file (always rebuilds).
+
+    Each source compiles to its own object in parallel (each carries its own kernels' code
+    objects), then one link step writes the library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    OBJ.mkdir(exist_ok=True)
+    cc = hipcc()
+    objs = [OBJ / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [[cc, *flags(), "-c", str(CSRC / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    jobs = jobs or max(1, min(len(cmds), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)
     return LIB
 
