@@ -220,6 +220,20 @@ int tars_relu(const float* x, int64_t lda, int32_t act, void* y, int64_t ldy, in
               uint32_t out_scale_bits, int32_t M, int32_t N, void* stream);
 
 /*
+ * Token rows of a bf16 embedding table, looked up on the device: dst row i (at dst + i * ldd) =
+ * table row ids[i] widened to fp32 (the 16 bits moved to the top half, exact), times the fp32
+ * scale scale_bits when `scaled` (one multiply, rounded to nearest even, subnormals kept).
+ * Replaces the board runtime's host lookup of the input embedding and Gemma 4's per-layer
+ * embedding rows (deploy/kv260/sw/tars_board.py:298-314, Qwen._put), so a step sends token ids.
+ *   table [rows, cols] at ld_table bytes (>= 2 cols, even); ids: host array of n indexes in
+ *   [0, rows), any n >= 1; dst fp32 at ldd bytes (>= 4 cols, a multiple of 4); dst must not
+ *   overlap the table's extent (its row gaps included).
+ */
+int tars_embed_rows(const uint16_t* table, int64_t ld_table, int64_t rows, int32_t cols,
+                    const int32_t* ids, int32_t n, int32_t scaled, uint32_t scale_bits, float* dst,
+                    int64_t ldd, void* stream);
+
+/*
  * fp32 dot products y[m][n] = sum_k A[m][k] * B(k, n).
  * Replaces Machine._fdot (tars_mini/golden.py:426-436): nn = 0, B [N, K] fp32 (numerics.fdot_nt,
  * the 16-lane sum, numerics.py:393-399); nn = 1, B [K, N] fp32 or binary16 (b_fp16), each output

@@ -21,7 +21,7 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libopentars_amd.so"
 OBJ = PKG / "_build"
 SOURCES = ["abi.hip", "queue.hip", "quant_rows.hip", "gemv_w8a8.hip", "gemm_w8a8_mfma.hip", "w4a16.hip",
-           "rowops.hip"]
+           "rowops.hip", "embed.hip"]
 ARCH = "gfx950"
 
 

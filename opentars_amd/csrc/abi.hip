@@ -516,4 +516,37 @@ int tars_fdot(const float* A, int64_t lda, const void* B, int64_t ldb, int32_t n
   return launched(tars::launch_fdot(a, static_cast<hipStream_t>(stream)));
 }
 
+int tars_embed_rows(const uint16_t* table, int64_t ld_table, int64_t table_rows, int32_t cols, const int32_t* ids,
+                    int32_t n, int32_t scaled, uint32_t scale_bits, float* dst, int64_t ldd, void* stream) {
+  g_last_error.clear();
+  if (!table || !ids || !dst) return fail(TARS_E_ARG, "NULL pointer");
+  if (scaled != 0 && scaled != 1) return fail(TARS_E_FIELD, "scaled is 0 or 1");
+  if (table_rows <= 0 || cols <= 0 || n <= 0) return fail(TARS_E_ALIGN, "rows, cols, n >= 1");
+  if (!stride_ok(ld_table, 2LL * cols, 2) || !stride_ok(ldd, 4LL * cols, 4)) return fail(TARS_E_ALIGN, "strides must hold a row");
+  if (!aligned(table, 2) || !aligned(dst, 4)) return fail(TARS_E_ALIGN, "pointer alignment");
+  for (int32_t i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= table_rows) return fail(TARS_E_RANGE, "a token id lies outside the table");
+  if (!extent_ok(table, ld_table, table_rows, 2LL * cols) || !extent_ok(dst, ldd, n, 4LL * cols))
+    return fail(TARS_E_RANGE, "extent overflows");
+  // the table as one span (its row gaps included): a per-row list would cost a host pass over
+  // every vocabulary row per call
+  if (overlaps(one(table, ld_table * (table_rows - 1) + 2LL * cols), rows(dst, ldd, n, 4LL * cols)))
+    return fail(TARS_E_OVERLAP, "the output overlaps the table");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int32_t i0 = 0; i0 < n; i0 += tars::kEmbedMaxIds) {
+    tars::EmbedArgs a{};
+    a.table = table;
+    a.ld_table = ld_table;
+    a.n = std::min<int32_t>(tars::kEmbedMaxIds, n - i0);
+    a.dst = reinterpret_cast<float*>(reinterpret_cast<char*>(dst) + static_cast<int64_t>(i0) * ldd);
+    a.ldd = ldd;
+    a.cols = cols;
+    a.scaled = scaled;
+    a.scale_bits = scale_bits;
+    for (int32_t j = 0; j < a.n; ++j) a.ids[j] = ids[i0 + j];
+    if (int rc = launched(tars::launch_embed_rows(a, s))) return rc;
+  }
+  return TARS_OK;
+}
+
 }  // extern "C"

@@ -254,6 +254,19 @@ struct AttnArgs {
   float out_scale;
 };
 bool attention_supported(int hd, int nk);
+
+// Embedding rows: dst row i = fp32(table row ids[i]) (times the fp32 scale when scaled).
+constexpr int kEmbedMaxIds = 64;
+struct EmbedArgs {
+  const uint16_t* table;  // bf16 [rows, cols] at ld_table bytes
+  int64_t ld_table;
+  float* dst;             // fp32 [n, cols] at ldd bytes
+  int64_t ldd;
+  int cols, n, scaled;
+  uint32_t scale_bits;
+  int32_t ids[kEmbedMaxIds];
+};
+hipError_t launch_embed_rows(const EmbedArgs& a, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s);

@@ -15,6 +15,7 @@ bit-identical to the golden model (tars_mini/golden.py, tars_mini/numerics.py):
   elt(op, a, b, ...)                     Machine._elt                   golden.py:393-418
   rope_rows(x, tab, rows_per_pos, rot)   Machine._rope                  numerics.py:412-424
   fdot_nt(a, b) / fdot_nn(a, b)          Machine._fdot                  numerics.py:393-409
+  embed_rows(table, ids, scale)          the runtime's embedding lookup tars_board.py:298-314
 
 Inputs are torch tensors on the GPU (results stay there, stream-ordered on the current stream),
 or numpy arrays (copied in; results come back as numpy after a synchronize, which is what
@@ -436,6 +437,33 @@ def fdot_nn(a, b, b_fp16: bool = False, out: int = OUT_FP32, out_scale=None, y=N
     return _fdot(a, b, True, b_fp16, out, out_scale, y)
 
 
+def embed_rows(table, ids, scale=None, y=None):
+    """Rows `ids` of the bf16 table ([rows, cols], uint16 bits; int16 on the device) as fp32, times
+    the fp32 `scale` when given: the board runtime's embedding lookup (tars_board.py:298-314),
+    done on the device. y: optional fp32 [len(ids), cols] output rows (row-strided view allowed)."""
+    nm = _numpy_mode(table)
+    t = _to_dev(table)
+    if t.dim() != 2 or t.element_size() != 2 or t.is_floating_point():
+        raise ValueError("the table is a 2-D array of bf16 bits (uint16 / int16)")
+    ids = np.ascontiguousarray(np.asarray(ids, np.int64).reshape(-1))
+    if ids.size == 0:
+        raise ValueError("no ids")
+    if ids.min() < -(1 << 31) or ids.max() >= (1 << 31):
+        raise ValueError("ids must fit int32")
+    ids32 = ids.astype(np.int32)
+    rows, cols = t.shape
+    if y is None:
+        y = torch.empty((ids.size, cols), dtype=torch.float32, device=t.device)
+    if y.shape != (ids.size, cols) or y.dtype != torch.float32:
+        raise ValueError("y must be fp32 [len(ids), cols]")
+    scaled = scale is not None
+    _check(_lib.lib().tars_embed_rows(t.data_ptr(), _ld(t), rows, cols,
+                                      ids32.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ids32.size,
+                                      int(scaled), _f32_bits(scale) if scaled else 0, y.data_ptr(), _ld(y),
+                                      _stream()))
+    return _finish(nm, y)
+
+
 def set_w8a8_path(path: str) -> str:
     """'auto' | 'gemv' | 'mfma': which W8A8 kernel family runs for M >= 2 (and M = 1). Returns the
     previous setting."""
@@ -445,7 +473,7 @@ def set_w8a8_path(path: str) -> str:
 
 
 __all__ = ["TarsError", "ContractError", "quant_rows", "gemm_rowcol", "quant_gemm_rowcol", "gemm_rowcol_ksplit",
-           "align_w4_groups", "gemm_w4", "set_w8a8_path", "ESIZE", "softmax_rows", "softmax_rows_causal",
+           "align_w4_groups", "gemm_w4", "embed_rows", "set_w8a8_path", "ESIZE", "softmax_rows", "softmax_rows_causal",
            "layernorm_rows", "rmsnorm_rows", "l2norm_rows", "relu", "elt", "rope_rows", "fdot_nt", "fdot_nn",
            "ROW_SOFTMAX", "ROW_LAYERNORM", "ROW_RMSNORM", "ROW_L2NORM", "ELT_MUL", "ELT_ADD", "ELT_MULADD",
            "ELT_SUB", "BM_DENSE", "BM_ROW", "BM_COL", "BM_SCALAR"]

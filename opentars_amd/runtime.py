@@ -1,47 +1,57 @@
-"""Board exports on one MI355X: a device with the board runtime's interface, and the loader and
-model runtime of an export directory.
+"""Board exports on one MI355X: a device with the board runtime's interface, and a model runtime
+of its own design that keeps a whole export resident in HBM.
 
 An export (tools/export_kv260.py:13-32, 141-247) is a directory: image.bin (the DDR image from
-address 0: zeroed states, the queue region, scratch, quantized weights), embed_bf16.bin (the
+address 0: zeroed states, the queue region, scratch, quantized weights), embed_bf16.bin (the input
 embedding table [vocab, hidden] as bf16), ple_bf16.bin (Gemma 4's per-layer embeddings),
 queues.bin (one descriptor queue per token position), queues_c<n>.bin (prefill chunks of n
-tokens), queues_s_*.bin (speculative decoding) and manifest.json (addresses, sizes, the queue
-indexes, tokenizer settings).
+tokens), queues_s_<name>.bin (speculative decoding with an MTP head) and manifest.json.
 
-GpuDevice is a device of the board runtime (deploy/kv260/sw/tars_board.py:4-12: mem, to_dev,
-from_dev, run(q, n) -> (done, err, op_idx, cycles), like Fpga :50-152 and Golden :155-178) whose
-image lives in HBM and whose queues run through the library's executor (tars_run_queue), so the
-reference's runtime (tars_board.Qwen) runs on it as it is.
+GpuDevice is a device of the board runtime's interface (deploy/kv260/sw/tars_board.py:4-12:
+mem, to_dev, from_dev, run(q, n) -> (done, err, op_idx, cycles)) over the library's executor.
 
-Model is that runtime's own counterpart (tars_board.py:212-435: Qwen) with the export resident on
-the GPU: image.bin is read straight into device memory through a pinned staging buffer, the
-initial states stay on the device for new conversations, each position's queue is copied into the
-image's queue region and run by the executor with the host's copy of its bytes, and the logits
-come back. The embedding lookup (bf16 -> fp32, exact; Gemma's fp32 scale) is done on the host from
-the memory-mapped table, as the reference's runtime does, and only the rows cross to the device.
-Every device step is the executor's, bit-identical to the golden model, so each step's logits are
-the bits the reference's runtime gets on its golden backend.
+Model runs an export with everything on the device. What crosses PCIe per step is the token ids
+(kernel arguments of the embedding lookup), the descriptors' host copy the executor decodes (it
+never copies them back), and the logits:
+
+  ExportLayout  the manifest, parsed once into typed fields.
+  QueueStore    every queue file in one HBM buffer, read once at load; each schedule entry (the
+                queue of a position, a prefill chunk, a speculative step) is precomputed as its
+                executor runs: parts of at most queue_cap descriptors, each a device-to-device copy
+                into the image's queue region and one tars_run_queue.
+  TokenRows     the bf16 embedding tables resident in HBM; a token's fp32 input rows are written
+                into the image by tars_embed_rows (the bf16 -> fp32 shift and Gemma's one fp32
+                multiply, as the board runtime computes them on its host, tars_board.py:298-314).
+  Speculation   the state of MTP speculative decoding as one object: which state copy the verify
+                queues read, how far the MTP head has consumed the cache, and its current draft.
+  Model         schedules the entries: a step, a prefill covered greedily by the longest chunk
+                queue the export holds at each position, the MTP rounds. The export's queue
+                protocol (which queue runs at which position, and the verify / accept / reject
+                sequence of a speculative round) is the export's own and is followed as
+                tars_board.Qwen (tars_board.py:212-435) defines it; each step's logits are the bits
+                the reference's runtime gets on its golden backend.
 """
 from __future__ import annotations
 
 import ctypes
 import json
 import time
+from dataclasses import dataclass
 from pathlib import Path
+from typing import Iterable, NamedTuple
 
 import numpy as np
 import torch
 
 from . import _lib
 from .contract import DESC_BYTES, ERR_NAMES
+from .ops import _check, _device
 from .queue import _raise
-from .ops import _device
 
-STAGING = 64 << 20           # pinned staging buffer for reading image.bin
-
-
-def _host_ptr(addr: int) -> ctypes.c_char_p:
-    return ctypes.cast(ctypes.c_void_p(addr), ctypes.c_char_p)
+STAGING = 64 << 20           # pinned staging buffer for reading files into device memory
+# The executor's feature level, in the board firmware's numbering (the W4A16 unit of v4.0, FP16
+# states, images over 1 GB): an export whose min_firmware is above it is refused.
+EXECUTOR_LEVEL = 0x00040001
 
 
 def _run_queue(image: torch.Tensor, q: int, n: int, host_addr: int) -> tuple[int, int, int, int]:
@@ -49,7 +59,8 @@ def _run_queue(image: torch.Tensor, q: int, n: int, host_addr: int) -> tuple[int
     (done, err_code, op_idx, host_op). Raises on a refusal (an output over an input) or a device
     error."""
     st = _lib.QueueStatus()
-    rc = _lib.lib().tars_run_queue(image.data_ptr(), image.numel(), q, n, _host_ptr(host_addr), 0, 0,
+    rc = _lib.lib().tars_run_queue(image.data_ptr(), image.numel(), q, n,
+                                   ctypes.cast(ctypes.c_void_p(host_addr), ctypes.c_char_p), 0, 0,
                                    ctypes.byref(st), torch.cuda.current_stream().cuda_stream)
     if rc != _lib.OK:
         _raise(rc)
@@ -65,9 +76,7 @@ class GpuDevice:
     device image and returns (done, err, op_idx, cycles), cycles 0 (the device keeps no cycle count).
     A descriptor the executor leaves to the host (a convolution: the language-model exports hold
     none) ends the run with done = 0 and err = 0 at its index."""
-    # version: the firmware level whose features the executor covers (the W4A16 unit of v4.0, bit 0,
-    # FP16 states and images over 1 GB): tars_board.Qwen checks an export's min_firmware against it
-    params = dict(backend="mi355x executor", version=0x00040001)
+    params = dict(backend="mi355x executor", version=EXECUTOR_LEVEL)
 
     def __init__(self, mem_bytes: int = 1 << 30):
         dev = _device()
@@ -88,18 +97,16 @@ class GpuDevice:
         return done, err, op, 0
 
 
-def _read_into(path: Path, dst: torch.Tensor, log=None) -> None:
-    """path's bytes into the device tensor dst (exactly its size) through a pinned staging buffer."""
-    size = dst.numel()
-    stage = torch.empty(min(STAGING, max(size, 1)), dtype=torch.uint8, pin_memory=True)
+def _load(path: Path, dst: torch.Tensor, stage: torch.Tensor, log=None) -> None:
+    """The file's bytes into the device tensor dst (exactly its size) through the pinned stage."""
+    size, pos = dst.numel(), 0
     view = memoryview(stage.numpy())
-    pos = 0
     with open(path, "rb") as f:
         while pos < size:
             k = f.readinto(view[:min(stage.numel(), size - pos)])
             if not k:
                 raise IOError(f"short read of {path}")
-            dst[pos:pos + k].copy_(stage[:k])
+            dst[pos:pos + k].copy_(stage[:k])            # synchronous: the stage is free again after it
             pos += k
             if log:
                 log(f"\r  loading {path.name} {pos >> 20} / {size >> 20} MiB", end="")
@@ -107,226 +114,348 @@ def _read_into(path: Path, dst: torch.Tensor, log=None) -> None:
         log("")
 
 
-class Model:
-    """An export directory on one MI355X: the loader and runtime of tars_board.Qwen
-    (tars_board.py:212-435) with the same methods, arguments and errors.
+# ---------------------------------------------------------------------------------- layout
+@dataclass(frozen=True)
+class ExportLayout:
+    """The manifest's fields the runtime uses (tools/export_kv260.py:248-295 writes them)."""
+    positions: int                 # max_tokens
+    hidden: int
+    vocab: int
+    image_bytes: int
+    mem_bytes: int                 # the device image's size (>= image_bytes)
+    state_end: int                 # [0, state_end): the conversation state (KV caches, DeltaNet states)
+    qbase: int                     # the image's queue region
+    queue_cap: int                 # descriptors it holds
+    x0: tuple[int, int]            # input rows: (offset, row stride)
+    ple: tuple[int, int, int] | None   # per-layer embedding rows: (offset, row stride, columns)
+    embed_scale: float | None
+    ple_scale: float | None
+    logits: int                    # logits offset
+    head_blocks: tuple[int, ...]   # the head's row blocks (a verify's rows are dense per block)
+    bos: tuple[int, ...]
+    eos: frozenset
+    turn_end: str
+    chat: tuple[str, str]          # chat template: (prefix, suffix)
+    min_firmware: int
 
-    step(token) -> logits (fp32 [vocab]) of the token at the next position; prefill(tokens,
-    chunked) -> the logits after the last one, in prefill chunks where the export has a queue for
-    the position (every chunk size it holds: the GPU's GEMMs take any number of rows) and single
-    steps elsewhere; new_conversation(); encode(tokenizer, text, chat); the speculative decoding of
-    an export with MTP queues (begin_spec, spec_round, end_spec, can_spec). self.seconds: host
-    wall time of the last step / prefill / speculative round."""
+    @staticmethod
+    def parse(m: dict) -> "ExportLayout":
+        ple_cols = int(m.get("ple_cols", 0))
+        level = int(m.get("min_firmware", 0))
+        if m.get("state_dtype") == "fp16":
+            level = max(level, 0x30400)         # FP16 states need firmware 3.4
+        es = m.get("embed_scale")
+        return ExportLayout(
+            positions=int(m["max_tokens"]), hidden=int(m["hidden"]), vocab=int(m["vocab"]),
+            image_bytes=int(m["image_bytes"]), mem_bytes=max(int(m["image_bytes"]), int(m.get("mem_bytes", 0))),
+            state_end=int(m["state_end"]), qbase=int(m["qbase"]), queue_cap=int(m["queue_cap"]),
+            x0=(int(m["x0_off"]), int(m["x0_ld"])),
+            ple=(int(m["ple0_off"]), int(m["ple0_ld"]), ple_cols) if ple_cols else None,
+            embed_scale=None if es is None else float(es),
+            ple_scale=float(m["ple_scale"]) if ple_cols else None,
+            logits=int(m["logits_off"]), head_blocks=tuple(int(b) for b in m["head_blocks"]),
+            bos=tuple(int(v) for v in m.get("bos_ids", [])), eos=frozenset(int(v) for v in m.get("eos_ids", [])),
+            turn_end=m.get("turn_end", "<|im_end|>\n"),
+            chat=(m.get("chat_prefix", ""), m.get("chat_suffix", "")), min_firmware=level)
+
+
+# ---------------------------------------------------------------------------------- queues
+class Run(NamedTuple):
+    """One tars_run_queue call: `count` descriptors at byte `src` of the store, the first of them
+    descriptor `first` of its schedule entry; `host` is their bytes for the executor to decode."""
+    src: int
+    count: int
+    first: int
+    host: np.ndarray
+
+
+class QueueStore:
+    """The export's queue files in one HBM buffer, and the runs of every schedule entry.
+
+    books: name -> (file name, [(key, byte offset, descriptors), ...]). An entry (name, key)
+    becomes ceil(descriptors / queue_cap) runs (a queue longer than the image's queue region runs
+    in parts; the descriptors keep nothing from one part to the next)."""
+
+    def __init__(self, d: Path, books: dict, cap: int, stage: torch.Tensor, log=None):
+        files = sorted({f for f, _ in books.values()})
+        base, total = {}, 0
+        for f in files:
+            base[f] = total
+            total += ((d / f).stat().st_size + 255) // 256 * 256
+        self.dev = torch.empty(max(total, 1), dtype=torch.uint8, device=_device())
+        host = {}
+        for f in files:
+            size = (d / f).stat().st_size
+            _load(d / f, self.dev[base[f]:base[f] + size], stage, log)
+            host[f] = np.fromfile(d / f, np.uint8)          # read-only bytes for the executor
+        self._runs: dict[tuple[str, int], tuple[Run, ...]] = {}
+        self._keys: dict[str, frozenset] = {}
+        for name, (f, index) in books.items():
+            keys = []
+            for key, off, n in index:
+                off, n = int(off), int(n)
+                self._runs[(name, int(key))] = tuple(
+                    Run(base[f] + off + DESC_BYTES * s, min(cap, n - s), s,
+                        host[f][off + DESC_BYTES * s:off + DESC_BYTES * (s + min(cap, n - s))])
+                    for s in range(0, n, cap))
+                keys.append(int(key))
+            self._keys[name] = frozenset(keys)
+
+    def keys(self, name: str) -> frozenset:
+        return self._keys.get(name, frozenset())
+
+    def runs(self, name: str, key: int) -> tuple[Run, ...]:
+        return self._runs[(name, key)]
+
+
+def cover(start: int, stop: int, sizes_at) -> list[tuple[int, int]]:
+    """Positions [start, stop) as consecutive (position, length) runs: at each position the largest
+    length sizes_at(position) offers that still fits, else 1 (a single step)."""
+    out, t = [], start
+    while t < stop:
+        n = max((s for s in sizes_at(t) if t + s <= stop), default=1)
+        out.append((t, n))
+        t += n
+    return out
+
+
+# ---------------------------------------------------------------------------------- token rows
+class TokenRows:
+    """The input embedding table (and Gemma 4's per-layer embedding table) resident in HBM; write()
+    puts the fp32 rows of token ids into the image's input rows on the device."""
+
+    def __init__(self, d: Path, lay: ExportLayout, stage: torch.Tensor, log=None):
+        self.lay = lay
+        dev = _device()
+        self.embed = torch.empty((lay.vocab, lay.hidden), dtype=torch.int16, device=dev)
+        _load(d / "embed_bf16.bin", self.embed.view(torch.uint8).view(-1), stage, log)
+        self.ple = None
+        if lay.ple is not None:
+            self.ple = torch.empty((lay.vocab, lay.ple[2]), dtype=torch.int16, device=dev)
+            _load(d / "ple_bf16.bin", self.ple.view(torch.uint8).view(-1), stage, log)
+
+    @staticmethod
+    def _gather(table: torch.Tensor, ids: np.ndarray, scale, dst: int, ld: int) -> None:
+        bits = 0 if scale is None else int(np.float32(scale).view(np.uint32))
+        _check(_lib.lib().tars_embed_rows(table.data_ptr(), 2 * table.shape[1], table.shape[0], table.shape[1],
+                                          ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ids.size,
+                                          int(scale is not None), bits, dst, ld,
+                                          torch.cuda.current_stream().cuda_stream))
+
+    def write(self, image: torch.Tensor, pos: int, tokens: Iterable[int]) -> None:
+        ids = np.ascontiguousarray(np.fromiter((int(t) for t in tokens), np.int64), np.int32)
+        if pos + ids.size > self.lay.positions:
+            raise OverflowError(f"context full ({self.lay.positions} tokens)")
+        off, ld = self.lay.x0
+        self._gather(self.embed, ids, self.lay.embed_scale, image.data_ptr() + off + pos * ld, ld)
+        if self.ple is not None:
+            off, ld, _ = self.lay.ple
+            self._gather(self.ple, ids, self.lay.ple_scale, image.data_ptr() + off + pos * ld, ld)
+
+
+# ---------------------------------------------------------------------------------- model
+@dataclass
+class Speculation:
+    """MTP speculative decoding state. parity: which of the two state copies the verify queue of
+    the next round reads (v2p0 / v2p1); an accepted draft leaves its update in the other copy, so
+    parity flips. seen: the positions below it have been consumed by the MTP head. draft: the MTP
+    head's proposal for the token after the current one."""
+    parity: int = 0
+    seen: int = 0
+    draft: int | None = None
+
+
+class Model:
+    """An export directory run on one MI355X, with the board runtime's methods (tars_board.Qwen:
+    step, prefill, new_conversation, encode, begin_spec / spec_round / end_spec / can_spec) and
+    their results and errors.
+
+    step(token) -> logits (fp32 [vocab]) of `token` at the next position; prefill(tokens, chunked)
+    -> the logits after the last token, the positions covered by the longest prefill-chunk queue
+    the export holds at each position (any number of rows runs on the GPU's GEMMs) and single steps
+    elsewhere (bit-identical either way). self.seconds: host wall time of the last call."""
 
     def __init__(self, data: str | Path, log=print):
+        t_start = time.time()
         self.d = Path(data)
-        m = json.loads((self.d / "manifest.json").read_text())
-        self.m = m
-        self.T, self.H, self.vocab = int(m["max_tokens"]), int(m["hidden"]), int(m["vocab"])
-        t = time.time()
+        self.manifest = json.loads((self.d / "manifest.json").read_text())
+        lay = self.lay = ExportLayout.parse(self.manifest)
+        if lay.min_firmware > EXECUTOR_LEVEL:
+            raise RuntimeError(f"export requires firmware >= 0x{lay.min_firmware:08x}; the executor "
+                               f"covers 0x{EXECUTOR_LEVEL:08x}")
+        self.T, self.H, self.vocab = lay.positions, lay.hidden, lay.vocab
         img = self.d / "image.bin"
-        size = img.stat().st_size
-        if size != m["image_bytes"]:
-            raise RuntimeError(f"{img}: {size} bytes, the manifest says {m['image_bytes']}")
-        dev = _device()
-        self.image = torch.empty(max(size, int(m.get("mem_bytes", size))), dtype=torch.uint8, device=dev)
-        _read_into(img, self.image[:size], log)
-        self.image[size:].zero_()
-        self.state_end = int(m["state_end"])
-        st = self.image[:self.state_end]
-        self.state0 = st.clone() if bool(st.any()) else None
-        self.embed = np.memmap(self.d / "embed_bf16.bin", np.uint16, "r", shape=(self.vocab, self.H))
-        self.ple_cols = int(m.get("ple_cols", 0))
-        self.ple = np.memmap(self.d / "ple_bf16.bin", np.uint16, "r", shape=(self.vocab, self.ple_cols)) \
-            if self.ple_cols else None
-        self.ple_scale = np.float32(m["ple_scale"]) if self.ple_cols else None
-        self.qidx = np.asarray(m["queue_index"], np.int64)
-        self.queues = np.memmap(self.d / "queues.bin", np.uint8, "r")
-        self.chunks = {int(n): (np.memmap(self.d / f"queues_c{n}.bin", np.uint8, "r"),
-                                {int(t0): (int(o), int(k)) for t0, o, k in index})
-                       for n, index in m.get("chunks", {}).items() if (self.d / f"queues_c{n}.bin").exists()}
-        self.spec = {n: (np.memmap(self.d / f"queues_s_{n}.bin", np.uint8, "r"),
-                         {int(r): (int(o), int(k)) for r, o, k in index})
-                     for n, index in m.get("spec", {}).items()}
-        s = m.get("embed_scale")
-        self.embed_scale = None if s is None else np.float32(s)
-        self.bos = [int(v) for v in m.get("bos_ids", [])]
-        self.turn_end = m.get("turn_end", "<|im_end|>\n")
-        self.pos, self.par, self.mrow, self.draft = 0, 0, 0, None
+        if img.stat().st_size != lay.image_bytes:
+            raise RuntimeError(f"{img}: {img.stat().st_size} bytes, the manifest says {lay.image_bytes}")
+        stage = torch.empty(STAGING, dtype=torch.uint8, pin_memory=True)
+        self.image = torch.zeros(lay.mem_bytes, dtype=torch.uint8, device=_device())
+        _load(img, self.image[:lay.image_bytes], stage, log)
+        state = self.image[:lay.state_end]
+        self._state0 = state.clone() if bool(state.any()) else None   # None: the state starts zeroed
+
+        m = self.manifest
+        books = {"pos": ("queues.bin", [(t, off, n) for t, (off, n) in enumerate(m["queue_index"])])}
+        for n, index in m.get("chunks", {}).items():
+            if (self.d / f"queues_c{n}.bin").exists():
+                books[f"c{int(n)}"] = (f"queues_c{n}.bin", index)
+        for name, index in m.get("spec", {}).items():
+            books[f"s:{name}"] = (f"queues_s_{name}.bin", index)
+        self.store = QueueStore(self.d, books, lay.queue_cap, stage, log)
+        self.chunk_sizes = sorted(int(k[1:]) for k in books if k[0] == "c")
+        self._chunks_at = {}
+        for n in self.chunk_sizes:
+            for t in self.store.keys(f"c{n}"):
+                self._chunks_at.setdefault(t, []).append(n)
+        self.rows = TokenRows(self.d, lay, stage, log)
+        del stage
+        self.pos = 0
+        self.spec = Speculation()
         self.seconds = 0.0
         torch.cuda.synchronize()
         if log:
-            log(f"  ready in {time.time() - t:.1f} s ({size >> 20} MiB image, {self.T} positions, "
-                f"prefill chunks {sorted(self.chunks) or 'none'})")
+            log(f"  ready in {time.time() - t_start:.1f} s ({lay.image_bytes >> 20} MiB image, {self.T} positions, "
+                f"prefill chunks {self.chunk_sizes or 'none'})")
 
-    # ------------------------------------------------------------------ conversation state
-    def new_conversation(self) -> None:
-        if self.state0 is None:
-            self.image[:self.state_end].zero_()
-        else:
-            self.image[:self.state_end].copy_(self.state0)
-        self.pos, self.par, self.mrow, self.draft = 0, 0, 0, None
-
-    def encode(self, tk, text: str, chat: bool = True) -> list[int]:
-        """Token ids of `text` at the next position: in the export's chat template with `chat` (a
-        later turn closes the model's turn first), the BOS tokens at position 0."""
-        if chat:
-            text = self.m["chat_prefix"] + text + self.m["chat_suffix"]
-            if self.pos:
-                text = self.turn_end + text
-        return (self.bos if self.pos == 0 else []) + list(tk.encode(text, add_special_tokens=False).ids)
-
-    # ------------------------------------------------------------------ device transfers
-    def _write_rows(self, off: int, ld: int, rows: np.ndarray) -> None:
-        rows = np.ascontiguousarray(rows, np.float32)
-        nb = rows.shape[1] * 4
-        src = torch.from_numpy(rows.view(np.uint8).reshape(rows.shape[0], nb))
-        if ld == nb:
-            self.image[off:off + rows.shape[0] * nb].copy_(src.reshape(-1))
-        else:
-            for i in range(rows.shape[0]):
-                self.image[off + i * ld:off + i * ld + nb].copy_(src[i])
-
-    def _put(self, t: int, tokens) -> None:
-        """The embeddings of `tokens` into the input rows t, t + 1, ... (bf16 -> fp32 exactly; Gemma:
-        times the manifest's embed_scale, one fp32 multiply)."""
-        m = self.m
-        if t + len(tokens) > self.T:
-            raise OverflowError(f"context full ({self.T} tokens)")
-        ids = np.asarray(tokens, np.int64)
-        x = (self.embed[ids].astype(np.uint32) << 16).view(np.float32)
-        if self.embed_scale is not None:
-            x = (x * self.embed_scale).astype(np.float32)
-        self._write_rows(int(m["x0_off"]) + t * int(m["x0_ld"]), int(m["x0_ld"]), x)
-        if self.ple is not None:
-            p = ((self.ple[ids].astype(np.uint32) << 16).view(np.float32) * self.ple_scale).astype(np.float32)
-            self._write_rows(int(m["ple0_off"]) + t * int(m["ple0_ld"]), int(m["ple0_ld"]), p)
-
-    def _run(self, queues: np.ndarray, off: int, n: int, what: str) -> None:
-        """n descriptors from queues[off:], through the image's queue region in parts of at most
-        queue_cap descriptors (the descriptors keep nothing from one part to the next)."""
-        q, cap = int(self.m["qbase"]), int(self.m["queue_cap"])
-        for s in range(0, n, cap):
-            k = min(cap, n - s)
-            part = np.array(queues[off + DESC_BYTES * s:off + DESC_BYTES * (s + k)])   # a writable copy
-            self.image[q:q + part.size].copy_(torch.from_numpy(part))
-            done, err, op, host_op = _run_queue(self.image, q, k, part.ctypes.data)
+    # ------------------------------------------------------------------ device work
+    def _execute(self, book: str, key: int, what: str) -> None:
+        """The schedule entry's runs through the executor, in order; raises where the core stops."""
+        q = self.lay.qbase
+        for r in self.store.runs(book, key):
+            nb = DESC_BYTES * r.count
+            self.image[q:q + nb].copy_(self.store.dev[r.src:r.src + nb])
+            done, err, op, host_op = _run_queue(self.image, q, r.count, r.host.ctypes.data)
             if host_op:
-                raise RuntimeError(f"{what}: descriptor {s + op} is a convolution, which this executor leaves "
-                                   f"to a host")
+                raise RuntimeError(f"{what}: descriptor {r.first + op} is a convolution, which this "
+                                   f"executor leaves to a host")
             if not done or err:
-                raise RuntimeError(f"{what}: the core stopped at descriptor {s + op} with error "
+                raise RuntimeError(f"{what}: the core stopped at descriptor {r.first + op} with error "
                                    f"{ERR_NAMES.get(err, err)}")
 
     def _logits(self) -> np.ndarray:
-        lo = int(self.m["logits_off"])
-        return self.image[lo:lo + 4 * self.vocab].cpu().numpy().view(np.float32).copy()
+        lo = self.lay.logits
+        return self.image[lo:lo + 4 * self.vocab].view(torch.float32).cpu().numpy()
 
-    def _rows(self, n: int) -> np.ndarray:
-        """The logits rows [n, vocab] of a verify (each head block holds its n rows densely)."""
-        lo = int(self.m["logits_off"])
-        flat = self.image[lo:lo + 4 * self.vocab * n].cpu().numpy().view(np.float32)
-        out, c0 = np.empty((n, self.vocab), np.float32), 0
-        for b in self.m["head_blocks"]:
-            out[:, c0:c0 + b] = flat[c0 * n:(c0 + b) * n].reshape(n, b)
+    def _verify_rows(self, n: int) -> np.ndarray:
+        """The logits rows [n, vocab] of an n-token verify: each head block holds its n rows
+        densely, one after the other; the blocks are put side by side on the device."""
+        lo = self.lay.logits
+        flat = self.image[lo:lo + 4 * self.vocab * n].view(torch.float32)
+        parts, c0 = [], 0
+        for b in self.lay.head_blocks:
+            parts.append(flat[c0 * n:(c0 + b) * n].view(n, b))
             c0 += b
-        return out
+        return torch.cat(parts, dim=1).cpu().numpy()
+
+    # ------------------------------------------------------------------ conversation
+    def new_conversation(self) -> None:
+        state = self.image[:self.lay.state_end]
+        if self._state0 is None:
+            state.zero_()
+        else:
+            state.copy_(self._state0)
+        self.pos = 0
+        self.spec = Speculation()
+
+    def encode(self, tk, text: str, chat: bool = True) -> list[int]:
+        """Token ids of `text` at the next position: in the export's chat template with `chat`
+        (a turn after the first closes the model's turn first), the BOS tokens at position 0."""
+        if chat:
+            prefix, suffix = self.lay.chat
+            text = (self.lay.turn_end if self.pos else "") + prefix + text + suffix
+        lead = list(self.lay.bos) if self.pos == 0 else []
+        return lead + list(tk.encode(text, add_special_tokens=False).ids)
 
     # ------------------------------------------------------------------ decoding
+    def _timed(self, t0: float, value):
+        self.seconds = time.perf_counter() - t0
+        return value
+
     def step(self, token: int) -> np.ndarray:
         """`token` at the next position; returns the logits (fp32, vocab)."""
         t0 = time.perf_counter()
-        t = self.pos
-        self._put(t, [token])
-        off, n = (int(v) for v in self.qidx[t])
-        self._run(self.queues, off, n, f"position {t}")
+        self.rows.write(self.image, self.pos, [token])
+        self._execute("pos", self.pos, f"position {self.pos}")
         self.pos += 1
-        lg = self._logits()
-        self.seconds = time.perf_counter() - t0
-        return lg
+        return self._timed(t0, self._logits())
 
     def prefill(self, tokens, chunked: bool = True) -> np.ndarray:
-        """`tokens` at the next positions; returns the logits after the last one. chunked: the
-        largest chunk the export has a queue for at each position (bit-identical to one token at a
-        time), single steps elsewhere; chunked=False: every token a step."""
+        """`tokens` at the next positions; returns the logits after the last one. chunked: each
+        position covered by the longest chunk queue the export holds there that fits (bit-identical
+        to single steps); chunked=False: every token a step."""
         tokens = [int(v) for v in tokens]
         if not tokens:
             raise ValueError("no tokens")
-        t_start = time.perf_counter()
-        i, lg = 0, None
-        while i < len(tokens):
-            t = self.pos
-            n = next((n for n in sorted(self.chunks, reverse=True)
-                      if chunked and i + n <= len(tokens) and t in self.chunks[n][1]), 1)
+        t0 = time.perf_counter()
+        start = self.pos
+        if start + len(tokens) > self.T:
+            raise OverflowError(f"context full ({self.T} tokens)")
+        sizes = (lambda t: self._chunks_at.get(t, ())) if chunked else (lambda t: ())
+        for t, n in cover(start, start + len(tokens), sizes):
+            self.rows.write(self.image, t, tokens[t - start:t - start + n])
             if n == 1:
-                lg = self.step(tokens[i])
+                self._execute("pos", t, f"position {t}")
             else:
-                self._put(t, tokens[i:i + n])
-                queues, index = self.chunks[n]
-                off, k = index[t]
-                self._run(queues, off, k, f"positions {t}..{t + n - 1}")
-                self.pos += n
-                lg = None
-            i += n
-        lg = lg if lg is not None else self._logits()
-        self.seconds = time.perf_counter() - t_start
-        return lg
+                self._execute(f"c{n}", t, f"positions {t}..{t + n - 1}")
+            self.pos = t + n
+        return self._timed(t0, self._logits())
 
     # ------------------------------------------------------------------ speculative decoding (MTP exports)
-    def _spec_run(self, name: str, r: int) -> None:
-        queues, index = self.spec[name]
-        off, k = index[r]
-        self._run(queues, off, k, f"{name} at {r}")
+    @property
+    def draft(self) -> int | None:
+        return self.spec.draft
+
+    def _mtp(self, name: str, t: int) -> None:
+        self._execute(f"s:{name}", t, f"{name} at {t}")
+
+    def _redraft(self) -> None:
+        self.spec.seen = self.pos
+        self.spec.draft = int(np.argmax(self._logits()))
 
     def begin_spec(self, lg: np.ndarray) -> int:
-        """After a prefill with logits lg: the first new token (not yet in the cache); the MTP head
-        takes the rows it has not seen and drafts the token after it."""
-        t_start = time.perf_counter()
+        """After a prefill with logits lg: the first new token (written at the next position, not
+        yet run). The MTP head consumes the cache rows it has not seen (in runs of 4 where the
+        export has that queue) and the last one with that token, and drafts the token after it."""
+        t0 = time.perf_counter()
         cur = int(np.argmax(lg))
         t = self.pos
-        self._put(t, [cur])
-        while self.mrow < t - 1:
-            n = 4 if self.mrow + 4 <= t - 1 and self.mrow in self.spec["mp4"][1] else 1
-            self._spec_run(f"mp{n}", self.mrow)
-            self.mrow += n
-        self._spec_run("m1", t - 1)
-        self.mrow = t
-        self.draft = int(np.argmax(self._logits()))
-        self.seconds = time.perf_counter() - t_start
-        return cur
+        self.rows.write(self.image, t, [cur])
+        four = self.store.keys("s:mp4")
+        for r, n in cover(self.spec.seen, t - 1, lambda r: (4,) if r in four else ()):
+            self._mtp(f"mp{n}", r)
+        self._mtp("m1", t - 1)
+        self._redraft()
+        return self._timed(t0, cur)
 
     def can_spec(self) -> bool:
+        """Room for a verify of two tokens and the MTP step after it."""
         return self.pos + 3 <= self.T
 
     def spec_round(self, cur: int) -> tuple[list[int], np.ndarray]:
-        """Verify [cur, draft] at the next position: the new tokens (2 on a hit, 1 on a miss; the last
-        is not yet in the cache) and the verify's logits rows; the tokens of plain greedy decoding."""
-        t_start = time.perf_counter()
-        t, d = self.pos, self.draft
-        self._put(t + 1, [d])
-        self._spec_run(f"v2p{self.par}", t)
-        rows = self._rows(2)
-        x = int(np.argmax(rows[0]))
-        if x == d and x not in self.m["eos_ids"]:
-            y = int(np.argmax(rows[1]))
-            self.par ^= 1
-            self._put(t + 2, [y])
-            self._spec_run("m2", t)
-            self.pos, new = t + 2, [x, y]
-        else:
-            self._put(t + 1, [x])
-            self._spec_run("m1", t)
-            self.pos, new = t + 1, [x]
-        self.mrow = self.pos
-        self.draft = int(np.argmax(self._logits()))
-        self.seconds = time.perf_counter() - t_start
-        return new, rows
+        """Verify [cur, draft] at the next position. Returns the new tokens and the verify's logits
+        rows [2, vocab]: on a hit (the model's own next token is the draft, and not an end token)
+        two tokens, else one; the last is written at its position but not yet run. The tokens are
+        those of plain greedy decoding."""
+        t0 = time.perf_counter()
+        t, sp = self.pos, self.spec
+        self.rows.write(self.image, t + 1, [sp.draft])
+        self._mtp(f"v2p{sp.parity}", t)
+        rows = self._verify_rows(2)
+        best = [int(v) for v in rows.argmax(axis=1)]
+        hit = best[0] == sp.draft and best[0] not in self.lay.eos
+        new = best if hit else best[:1]
+        if hit:
+            sp.parity ^= 1                   # the verify's update of the draft row is the state now
+        self.rows.write(self.image, t + len(new), [new[-1]])
+        self._mtp("m2" if hit else "m1", t)
+        self.pos = t + len(new)
+        self._redraft()
+        return self._timed(t0, (new, rows))
 
     def end_spec(self) -> None:
-        """Back to the plain queues (they use the first state copy)."""
-        if self.par:
-            self._spec_run("swap", 0)
-            self.par = 0
+        """Back to the plain queues, which read the first state copy."""
+        if self.spec.parity:
+            self._mtp("swap", 0)
+            self.spec.parity = 0
 
 
-__all__ = ["GpuDevice", "Model"]
+__all__ = ["GpuDevice", "Model", "ExportLayout", "QueueStore", "TokenRows", "Speculation", "cover"]

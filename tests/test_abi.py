@@ -229,3 +229,28 @@ def test_rowop_validation():
     assert fdot(K=0) == E.E_ALIGN
     assert fdot(ldb=128) == E.E_ALIGN                               # NT rows of 64 fp32 are 256 bytes
     assert fdot(Y=G + 64) == E.E_OVERLAP
+
+
+def test_embed_rows_validation():
+    """tars_embed_rows refuses bad arguments before any launch (every call below is invalid)."""
+    import ctypes
+    lib = _lib.lib()
+    T, D = P, P + 64 * MB
+
+    def call(ids=(1, 2), **k):
+        arr = (ctypes.c_int32 * max(len(ids), 1))(*ids)
+        a = dict(table=T, ldt=0, rows=512, cols=256, n=len(ids), scaled=0, sb=0, dst=D, ldd=0)
+        a.update(k)
+        return lib.tars_embed_rows(a["table"], a["ldt"], a["rows"], a["cols"], arr, a["n"], a["scaled"], a["sb"],
+                                   a["dst"], a["ldd"], None)
+    assert call(table=None) == _lib.E_ARG
+    assert call(scaled=2) == _lib.E_FIELD
+    assert call(n=0) == _lib.E_ALIGN
+    assert call(cols=0) == _lib.E_ALIGN
+    assert call(ldt=256) == _lib.E_ALIGN                            # 256 bf16 are 512 bytes
+    assert call(ldd=1000) == _lib.E_ALIGN                           # 256 fp32 are 1024 bytes
+    assert call(ldd=1030) == _lib.E_ALIGN                           # not a multiple of 4
+    assert call(dst=D + 2) == _lib.E_ALIGN
+    assert call(ids=(1, 512)) == _lib.E_RANGE                       # past the table
+    assert call(ids=(-1,)) == _lib.E_RANGE
+    assert call(dst=T + 100 * 512) == _lib.E_OVERLAP                # rows into the table

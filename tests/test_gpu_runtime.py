@@ -149,3 +149,28 @@ def test_gpu_device_under_the_reference_runtime_calls(export_dir):
         for s in exp["steps"]:
             lg = drv.step(s["token"])
             assert (int(np.argmax(lg)), sha(lg)) == (s["argmax"], s["sha256"]), f"{exp['name']} step {s['pos']}"
+
+
+def test_embed_rows_matches_the_host_lookup():
+    """tars_embed_rows against numpy's bf16 -> fp32 shift and float32 multiply (the board runtime's
+    host lookup, tars_board.py:298-314): random bf16 bits with zeros, infinities, subnormals and
+    products that round into the subnormal range; scaled and unscaled; the 16-byte vector path
+    (256 and 512 columns) and the element path (odd widths, a strided table); more ids than one
+    launch takes; repeated ids."""
+    import torch
+    from opentars_amd import ops
+    rng = np.random.default_rng(11)
+    for rows, cols, ld_extra in ((512, 256, 0), (300, 512, 0), (97, 37, 3), (64, 8, 8)):
+        bits = rng.integers(0, 1 << 16, (rows, cols + ld_extra), dtype=np.uint32).astype(np.uint16)
+        bits = np.where((bits & 0x7F80) == 0x7F80, bits & 0x807F, bits)        # no NaN / inf ...
+        bits[0, :4] = [0x0000, 0x8000, 0x7F80, 0xFF80]                        # ... but zeros and infinities
+        bits[1, :4] = [0x0001, 0x807F, 0x0080, 0x3F80]                        # subnormal, min normal, 1.0
+        table = torch.from_numpy(bits.view(np.int16)).cuda()[:, :cols]
+        ids = rng.integers(0, rows, 150)
+        ids[:3] = [0, 1, 0]
+        ref32 = (bits[:, :cols][ids].astype(np.uint32) << 16).view(np.float32)
+        for scale in (None, 16.0, 11.313708305358887, 3.0e-30):
+            got = ops.embed_rows(table, ids, scale).cpu().numpy()
+            with np.errstate(over="ignore"):
+                want = ref32 if scale is None else (ref32 * np.float32(scale)).astype(np.float32)
+            assert got.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), (rows, cols, scale)
