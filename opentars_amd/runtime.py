@@ -287,8 +287,9 @@ class Model:
         img = self.d / "image.bin"
         if img.stat().st_size != lay.image_bytes:
             raise RuntimeError(f"{img}: {img.stat().st_size} bytes, the manifest says {lay.image_bytes}")
+        dev = _device()                       # raises first when there is no GPU
         stage = torch.empty(STAGING, dtype=torch.uint8, pin_memory=True)
-        self.image = torch.zeros(lay.mem_bytes, dtype=torch.uint8, device=_device())
+        self.image = torch.zeros(lay.mem_bytes, dtype=torch.uint8, device=dev)
         _load(img, self.image[:lay.image_bytes], stage, log)
         state = self.image[:lay.state_end]
         self._state0 = state.clone() if bool(state.any()) else None   # None: the state starts zeroed
