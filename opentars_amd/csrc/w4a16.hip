@@ -2,30 +2,30 @@
 // (tars_mini/golden.py:295-324).
 //
 // Work unit: a 16-byte chunk of a packed weight row = 32 int4 weights = a quarter of a 128-wide
-// group. A wave owns whole rows; lane l streams chunks l, l + 64, ... of each (every load
-// instruction reads 1 KiB of a row, fully coalesced), so a group's four chunks sit on four
-// consecutive lanes.
+// group. A wave owns whole rows; lane l streams chunks l, l + 64, ... of each, so a group's four
+// chunks sit on four consecutive lanes (a quad).
 //
-// Alignment is fused into the GEMV prologue: the workgroup aligns its activation row once,
+// Alignment is fused into the GEMV prologue: the workgroup aligns each activation row once,
 // cooperatively (16 lanes per 128-wide group, 8 elements each; the group's exponent maximum meets
-// through DPP lane permutes), into LDS byte planes that every weight row of the workgroup reads.
-// Each mantissa (an int16 in [-16384, 16384]) is rounded to nearest-even exactly as the reference
-// does: for finite groups as rint(x * 2^(140 - e_eff)), otherwise by the integer shift rule with
-// the NaN / infinity cases.
+// through DPP lane permutes). Each mantissa (an int16 in [-16384, 16384]) is rounded to
+// nearest-even exactly as the reference does: for finite groups as rint(x * 2^(140 - e_eff)),
+// otherwise by the integer shift rule with the NaN / infinity cases.
 //
-// Exact int16 x int4 dots on v_dot4 (signed 8-bit): a mantissa a is split as a = 256 * ah + al with
-// al, ah signed bytes (al = the low byte read as signed, ah in [-64, 64]); a weight nibble w is
-// used as the byte w * 16 (the nibble moved to the byte's top, which sign-extends it). Then
-// 16 * sum(w * a) = 256 * dot4(w16, ah) + dot4(w16, al), exact in int32 (|.| <= 2^28), and the
-// final arithmetic shift by 4 is exact. The packed byte holds the even k in its low nibble and the
-// odd k in its high nibble, so the activations are kept as even/odd byte lanes.
+// Exact int16 x int4 dots on v_dot8_i32_i4: each mantissa is written in balanced base 16 (four
+// signed digits in [-8, 7]); LDS holds one "digit plane" per digit, 8 elements per dword in the
+// packed weights' nibble order, so a weight dword dotted with plane i gives sum w d_i exactly and
+// the chunk's dot is P0 + 16 P1 + 256 P2 + 4096 P3 (16 dot instructions per chunk and row; the
+// former byte split needed 28 instructions).
 //
-// The per-group fp32 terms (i2f(dot) * ws) * xs go to the wave's own LDS rows; four lanes per
-// row then run the four bank chains (group g goes to bank g % 4, added in g order from +0) and
+// The per-group fp32 terms (i2f(dot) * ws) * xs go to the wave's own LDS rows (the quad's four
+// lanes form the terms of four different rows in one instruction stream); four lanes per row
+// then run the four bank chains (group g goes to bank g % 4, added in g order from +0) and
 // combine (b0 + b1) + (b2 + b3) before bias, activation and conversion. The only workgroup
 // barrier is the one after the alignment.
 //
-// Roofline: HBM. Algorithmic bytes per row: K/2 (weights) + K/64 (fp16 scales) + 4 (output).
+// Roofline: HBM. Algorithmic bytes per row: K/2 (weights) + K/64 (fp16 scales) + 4 (output). The
+// kernels also carry VALU work per weight byte (dots, terms, chains) that measured as the larger
+// share of a call at these sizes; see the launcher's notes.
 #include "kernels.h"
 
 namespace tars {
@@ -128,50 +128,6 @@ __device__ __forceinline__ void align_chunk(const uint32_t xb[32], int mant[32],
   align_elems<32, 4>(xb, mant, scale_bits);
 }
 
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
-         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | ((static_cast<uint32_t>(d) & 0xFFu) << 24);
-}
-
-// Splits 32 mantissas into the byte lanes the nibble layout needs: for weight dword d (k = 8d..8d+7
-// of the chunk), even k pair with the low nibbles and odd k with the high nibbles.
-struct ActBytes {
-  uint32_t lo_even[4], lo_odd[4], hi_even[4], hi_odd[4];
-};
-
-__device__ __forceinline__ ActBytes split_bytes(const int mant[32]) {
-  ActBytes r;
-  int lo[32], hi[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    lo[i] = static_cast<int8_t>(mant[i] & 0xFF);
-    hi[i] = (mant[i] - lo[i]) >> 8;
-  }
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    r.lo_even[d] = pack4(lo[8 * d], lo[8 * d + 2], lo[8 * d + 4], lo[8 * d + 6]);
-    r.lo_odd[d] = pack4(lo[8 * d + 1], lo[8 * d + 3], lo[8 * d + 5], lo[8 * d + 7]);
-    r.hi_even[d] = pack4(hi[8 * d], hi[8 * d + 2], hi[8 * d + 4], hi[8 * d + 6]);
-    r.hi_odd[d] = pack4(hi[8 * d + 1], hi[8 * d + 3], hi[8 * d + 5], hi[8 * d + 7]);
-  }
-  return r;
-}
-
-// 16 * (exact dot of the chunk's 32 weights with its 32 mantissas)
-__device__ __forceinline__ int chunk_dot16(v4u w, const ActBytes& x) {
-  int lo = 0, hi = 0;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const int we = static_cast<int>((w[d] << 4) & 0xF0F0F0F0u);
-    const int wo = static_cast<int>(w[d] & 0xF0F0F0F0u);
-    lo = __builtin_amdgcn_sdot4(we, static_cast<int>(x.lo_even[d]), lo, false);
-    lo = __builtin_amdgcn_sdot4(wo, static_cast<int>(x.lo_odd[d]), lo, false);
-    hi = __builtin_amdgcn_sdot4(we, static_cast<int>(x.hi_even[d]), hi, false);
-    hi = __builtin_amdgcn_sdot4(wo, static_cast<int>(x.hi_odd[d]), hi, false);
-  }
-  return hi * 256 + lo;
-}
-
 // ---------------------------------------------------------------------------- align (standalone)
 __global__ __launch_bounds__(kThreads) void align_w4_kernel(AlignArgs a) {
   const int C = a.K / 32;
@@ -203,150 +159,202 @@ __global__ __launch_bounds__(kThreads) void align_w4_kernel(AlignArgs a) {
 }
 
 // ---------------------------------------------------------------------------- GEMV
-// One wave owns U whole weight rows: lane l streams chunks l, l + 64, ... (CPL per lane) of each
-// row, so a group's four chunks sit on four consecutive lanes and everything after the activation
-// alignment (the group sums, the terms and the four bank chains) stays inside the wave.
+// Digit planes. An aligned mantissa a (|a| <= 2^14) is written in balanced base 16,
+// a = d0 + 16 d1 + 256 d2 + 4096 d3 with every digit in [-8, 7]; digit i's nibble (d_i mod 16) is
+// floor((a + c_i) / 16^i) mod 16 with c = {0, 8, 136, 2184}, and the top digit is in [-4, 4]. A
+// plane dword holds one digit of 8 consecutive elements, element e in nibble e: the same nibble
+// order as a packed weight dword (low nibble of byte b = k 2b, high nibble = k 2b + 1). Then
+// v_dot8_i32_i4 of a weight dword with plane i is sum_e w_e d_{i,e} exactly, and the chunk's dot is
+// P0 + 16 P1 + 256 P2 + 4096 P3 (|dot| <= 2^24 per group: exact in int32).
+__device__ __forceinline__ void digit_planes(const int mant[8], uint32_t pl[4]) {
+  constexpr int kC[4] = {0, 8, 136, 2184};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v |= ((static_cast<uint32_t>(mant[e] + kC[i]) >> (4 * i)) & 15u) << (4 * e);
+    pl[i] = v;
+  }
+}
+
+// exact dot of a chunk's 32 weights (4 dwords) with its 32 elements' digit planes
+__device__ __forceinline__ int chunk_dot_digits(v4u w, const v4u x[4]) {
+  int p[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_sdot8(static_cast<int>(w[d]), static_cast<int>(x[i][d]), p[i], false);
+  return p[0] + (p[1] << 4) + (p[2] << 8) + (p[3] << 12);
+}
+
+// A wave owns U consecutive weight rows; lane l streams chunks l, l + 64, ... (CPL per lane) of
+// each, so a 128-wide group's four chunks sit on four consecutive lanes (a quad). A workgroup of
+// NW waves shares one alignment of each of its MR activation rows.
 //
-// 1. Loads are issued activations first (the aligner waits on them alone), then the U * CPL weight
-//    chunks, then the group scales and the bias.
-// 2. The workgroup aligns activation row m once: aligner thread t (t < K / 8, CPL passes of 256)
-//    owns elements [8 t, 8 t + 8), 16 consecutive threads form one 128-wide group and meet their
-//    exponent maximum and flags by DPP. The split signed bytes go to LDS plane-major (plane q =
-//    lo_even, lo_odd, hi_even, hi_odd; dword t of each plane), the group scale beside them.
-// 3. After the one workgroup barrier each lane reads its chunks' 64 bytes, forms the exact dots,
-//    adds its group's four lanes (quad permutes), and the group's first lane writes the fp32 term
-//    (i2f(dot) * ws) * xs into the wave's own LDS rows.
-// 4. Lane 4 u + b runs bank b's chain of row u (groups b, b + 4, ... in order from +0, every term
-//    read up front so only the fadds are sequential), and the quad folds (b0 + b1) + (b2 + b3).
-constexpr int kWaves = kThreads / 64;
+// 1. One batch of loads: the activation rows (only the waves that align them), the wave's fp16
+//    group scales (U * G halves, contiguous: one dword per lane), then the U * CPL weight chunks.
+//    A lane past the row's last chunk re-reads that chunk, a row past N re-reads row N - 1 (the
+//    values are never used): addresses stay inside rows the wave streams anyway (a fixed fallback
+//    address shared by every wave measured as a hot spot).
+// 2. Aligner thread t (t < K / 8) owns elements 8 t .. 8 t + 7 of a row; 16 threads form a
+//    128-wide group (exponent maximum and flags by DPP). Digit planes and the group scale go to LDS.
+//    The only workgroup barrier follows.
+// 3. Per chunk, row and activation row: 16 v_dot8 and the digit combination; the quad adds its
+//    four chunks (DPP). Lane q of the quad forms the terms (i2f(dot) * ws) * xs of the rows
+//    u = q, q + 4, ... into the wave's LDS terms.
+// 4. Lane 4 (m U + u) + b runs bank b's chain of row u, activation row m: groups b, b + 4, ... in
+//    order from +0 (every term read first, the adds unflushed with the subnormal check and redone
+//    with the flushes when a partial sum is subnormal), and the quad folds (b0 + b1) + (b2 + b3).
 constexpr int kTermStride = 65;  // LDS floats per term row (G <= 64), padded against bank conflicts
 
-template <int CPL, int U, bool BF16, bool SIMPLE>
-__global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
-  static_assert(CPL >= 1 && CPL <= 4 && U >= 1 && 4 * U <= 64, "K <= 8192; one chain quad per row");
-  extern __shared__ __align__(16) uint32_t planes[];  // 4 planes of 4C dwords, then G scale encodings
-  __shared__ float terms[kWaves][U][kTermStride];
+template <int NW, int U, int MR, int CPL>
+struct W4Smem {
+  float terms[NW][MR * U][kTermStride];
+  uint32_t ws[NW][U * 32];                             // U rows x G <= 64 halves per wave
+  float xs[MR][64];
+  // then the digit planes: MR rows x 4 planes x 4C dwords (dynamic)
+};
+
+template <int NW, int U, int MR, int CPL, bool BF16, bool SIMPLE>
+__global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
+  static_assert(CPL >= 1 && CPL <= 4 && MR * U * 4 <= 64, "K <= 8192; one chain lane per bank");
+  constexpr int NT = NW * 64;
+  constexpr int AP = (CPL * 256 + NT - 1) / NT;       // aligner passes (K / 8 <= 256 CPL threads)
+  using Smem = W4Smem<NW, U, MR, CPL>;
+  __shared__ Smem sm;
+  extern __shared__ __align__(16) uint32_t planes[];    // [MR][4][4C]
+  // every kernel argument the load batch needs, in one scalar round trip
+  __asm__ volatile("" : : "s"(a.x), "s"(a.lda), "s"(a.Wp), "s"(a.ws), "s"(a.M), "s"(a.N), "s"(a.K));
   const int C = a.K >> 5;
   const int G = a.K >> 7;
-  const int A = a.K >> 3;  // aligner threads (8 elements each)
+  const int A = a.K >> 3;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int m = blockIdx.y;
-  const int n0 = (blockIdx.x * kWaves + wave) * U;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = blockIdx.y * MR;
+  const int n0 = (blockIdx.x * NW + wave) * U;
   const int64_t row_bytes = a.K >> 1;
-  const char* xrow = static_cast<const char*>(a.x) + m * a.lda;
 
-  // 1. activations (dead aligner threads shadow the first group's lanes: whole 16-lane groups)
-  uint32_t xb[CPL][8];
+  // 1. activations (per pass: whole waves only; dead lanes of a live wave shadow group 0)
+  uint32_t xb[MR][AP][8];
 #pragma unroll
-  for (int p = 0; p < CPL; ++p) {
-    const int t = p * kThreads + tid;
-    const int tt = t < A ? t : (t & 15);
-    if constexpr (BF16) {
-      const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * tt);
+  for (int r = 0; r < MR; ++r) {
+    const char* xrow = static_cast<const char*>(a.x) + min(m0 + r, a.M - 1) * a.lda;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xb[p][2 * j] = v[j] << 16;
-        xb[p][2 * j + 1] = v[j] & 0xFFFF0000u;
-      }
-    } else {
-      const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * tt);
-      const v4u v0 = src[0], v1 = src[1];
+    for (int p = 0; p < AP; ++p) {
+      const int t = p * NT + tid;
+      if (p * NT + wave * 64 >= A) continue;                   // wave-uniform
+      const int tt = t < A ? t : (t & 15);
+      if constexpr (BF16) {
+        const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * tt);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xb[p][j] = v0[j];
-        xb[p][4 + j] = v1[j];
+        for (int j = 0; j < 4; ++j) {
+          xb[r][p][2 * j] = v[j] << 16;
+          xb[r][p][2 * j + 1] = v[j] & 0xFFFF0000u;
+        }
+      } else {
+        const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * tt);
+        const v4u v0 = src[0], v1 = src[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xb[r][p][j] = v0[j];
+          xb[r][p][4 + j] = v1[j];
+        }
       }
     }
   }
+  issue_fence();
+  // the wave's group scales: halves [n0 G, (n0 + U) G) as dwords (G is even), clamped at the end
+  const int ws_dw = (U * G) >> 1;
+  const uint32_t* ws32 = reinterpret_cast<const uint32_t*>(a.ws);
+  const int64_t ws_last = (static_cast<int64_t>(a.N) * G >> 1) - 1;
+  constexpr int kWsPer = (U * 32 + 63) / 64;          // dwords per lane: U rows x G <= 64 halves
+  uint32_t wsv[kWsPer];
+#pragma unroll
+  for (int i = 0; i < kWsPer; ++i)
+    wsv[i] = ws32[min(static_cast<int64_t>(n0) * G / 2 + min(lane + 64 * i, ws_dw - 1), ws_last)];
   issue_fence();
   v4u wv[U][CPL];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int n = n0 + u;
-    const v4u* wrow = reinterpret_cast<const v4u*>(a.Wp + n * row_bytes);
+    const v4u* wrow = reinterpret_cast<const v4u*>(a.Wp + min(n0 + u, a.N - 1) * row_bytes);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      wv[u][j] = load_stream_pred(wrow + c, reinterpret_cast<const v4u*>(a.Wp), n < a.N && c < C,
-                                  v4u{0u, 0u, 0u, 0u});
-    }
+    for (int j = 0; j < CPL; ++j) wv[u][j] = __builtin_nontemporal_load(wrow + min(lane + 64 * j, C - 1));
   }
   issue_fence();
-  uint32_t wsb[U][CPL];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int n = min(n0 + u, a.N - 1);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) wsb[u][j] = a.ws[static_cast<int64_t>(n) * G + min((lane + 64 * j) >> 2, G - 1)];
-  }
-  const int ue = lane >> 2, bank = lane & 3;  // this lane's chain: bank `bank` of row n0 + ue
-  const int ne = n0 + (ue < U ? ue : 0);
-  const float bias_v = *(a.bias ? a.bias + min(ne, a.N - 1) : reinterpret_cast<const float*>(a.ws));
-  issue_fence();
+  const int ce = lane >> 2, bank = lane & 3;          // chain lane: (m, u) = (ce / U, ce % U)
+  const int ue = ce % U, me = ce / U;
+  const float bias_v = SIMPLE ? 0.0f : *(a.bias ? a.bias + min(n0 + ue, a.N - 1) : reinterpret_cast<const float*>(a.ws));
 
-  // 2. cooperative alignment into the LDS planes
-  float* xs_lds = reinterpret_cast<float*>(planes + 16 * C);
+  // 2. alignment into LDS digit planes
 #pragma unroll
-  for (int p = 0; p < CPL; ++p) {
-    const int t = p * kThreads + tid;
-    int mant[8];
-    uint32_t sb;
-    align_elems<8, 16>(xb[p], mant, sb);
-    if (t < A) {
-      int lo[8], hi[8];
+  for (int r = 0; r < MR; ++r) {
+    uint32_t* pl = planes + r * 16 * C;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        lo[j] = static_cast<int8_t>(mant[j] & 0xFF);
-        hi[j] = (mant[j] - lo[j]) >> 8;
+    for (int p = 0; p < AP; ++p) {
+      if (p * NT + wave * 64 >= A) continue;                   // wave-uniform
+      const int t = p * NT + tid;
+      int mant[8];
+      uint32_t sb;
+      align_elems<8, 16>(xb[r][p], mant, sb);
+      if (t < A) {
+        uint32_t d[4];
+        digit_planes(mant, d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pl[i * 4 * C + t] = d[i];
+        if ((t & 15) == 0) sm.xs[r][t >> 4] = ffrom(sb);
       }
-      planes[t] = pack4(lo[0], lo[2], lo[4], lo[6]);
-      planes[4 * C + t] = pack4(lo[1], lo[3], lo[5], lo[7]);
-      planes[8 * C + t] = pack4(hi[0], hi[2], hi[4], hi[6]);
-      planes[12 * C + t] = pack4(hi[1], hi[3], hi[5], hi[7]);
-      if ((t & 15) == 0) xs_lds[t >> 4] = ffrom(sb);
     }
   }
+  // the wave's scales into its LDS slot (read back by other lanes of the wave after the barrier)
+#pragma unroll
+  for (int i = 0; i < kWsPer; ++i)
+    if (lane + 64 * i < ws_dw) sm.ws[wave][lane + 64 * i] = wsv[i];
   __syncthreads();
 
-  // 3. dots and group terms
+  // 3. dots and terms
+  const uint16_t* wsh = reinterpret_cast<const uint16_t*>(sm.ws[wave]);
+  const int q = lane & 3;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
     const int cc = c < C ? c : 0;
-    ActBytes act;
-    const v4u le = *reinterpret_cast<const v4u*>(planes + 4 * cc);
-    const v4u lo = *reinterpret_cast<const v4u*>(planes + 4 * C + 4 * cc);
-    const v4u he = *reinterpret_cast<const v4u*>(planes + 8 * C + 4 * cc);
-    const v4u ho = *reinterpret_cast<const v4u*>(planes + 12 * C + 4 * cc);
+    const int g = cc >> 2;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      act.lo_even[d] = le[d];
-      act.lo_odd[d] = lo[d];
-      act.hi_even[d] = he[d];
-      act.hi_odd[d] = ho[d];
-    }
-    const float xs = xs_lds[cc >> 2];
+    for (int r = 0; r < MR; ++r) {
+      v4u x[4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int d16 = chunk_dot16(wv[u][j], act);
-      d16 += lane_xor1(d16);
-      d16 += lane_xor2(d16);
-      if ((lane & 3) == 0 && c < C && n0 + u < a.N)
-        terms[wave][u][c >> 2] = fmul(fmul(i2f(d16 >> 4), from_fp16_bits(wsb[u][j])), xs);
+      for (int i = 0; i < 4; ++i) x[i] = *reinterpret_cast<const v4u*>(planes + r * 16 * C + i * 4 * C + 4 * cc);
+      const float xs = sm.xs[r][g];
+      int dots[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int d = chunk_dot_digits(wv[u][j], x);
+        d += lane_xor1(d);
+        d += lane_xor2(d);
+        dots[u] = d;
+      }
+      // lane q of the quad forms the terms of rows q, q + 4, ... in one instruction stream
+#pragma unroll
+      for (int k = 0; k < (U + 3) / 4; ++k) {
+        const int u = q + 4 * k;
+        int d = dots[4 * k];
+#pragma unroll
+        for (int v = 1; v < 4; ++v)
+          if (4 * k + v < U) d = q == v ? dots[4 * k + v] : d;
+        const float term = fmul(fmul(i2f(d), from_fp16_bits(wsh[min(u, U - 1) * G + g])), xs);
+        if (u < U && c < C && n0 + u < a.N) sm.terms[wave][r * U + u][g] = term;
+      }
     }
   }
-  // the terms were written by other lanes of this wave: order the LDS accesses (no block barrier)
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // 4. four bank chains per row (at most G / 4 <= K / 512 <= 4 CPL steps; the terms are flushed
-  //    fmul results, so the steps are fadd_chain's, run unflushed and checked: recomputed with the
-  //    flushes when a partial sum is subnormal), then (b0 + b1) + (b2 + b3)
+  // 4. bank chains (at most G / 4 <= 4 CPL steps)
   constexpr int kSteps = 4 * CPL;
-  const float* trow = terms[wave][ue < U ? ue : 0];
+  const float* trow = sm.terms[wave][ce < MR * U ? ce : 0];
   float tv[kSteps];
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) tv[i] = trow[bank + 4 * i];  // index <= 16 CPL - 1 < kTermStride
@@ -367,42 +375,32 @@ __global__ __launch_bounds__(kThreads) void gemv_w4a16_kernel(W4Args a) {
   acc = chain_end(acc);
   const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
   const float other = lane_xor2(pair);
-  if (bank == 0 && ue < U && n0 + ue < a.N) {
+  if (bank == 0 && ce < MR * U && n0 + ue < a.N && m0 + me < a.M) {
     float y = fadd(pair, other);
+    const int64_t yrow = static_cast<int64_t>(m0 + me) * a.ldy;
     if constexpr (SIMPLE) {
-      reinterpret_cast<float*>(static_cast<char*>(a.Y) + m * a.ldy)[n0 + ue] = ftz(y);
+      reinterpret_cast<float*>(static_cast<char*>(a.Y) + yrow)[n0 + ue] = ftz(y);
     } else {
       if (a.bias) y = fadd(y, bias_v);
       y = act_fn(y, a.act);
-      store_out(a.Y, m * a.ldy, n0 + ue, a.out, y, a.out_scale);
+      store_out(a.Y, yrow, n0 + ue, a.out, y, a.out_scale);
     }
   }
 }
 
-template <int CPL, int U>
+template <int NW, int U, int MR, int CPL>
 hipError_t go_w4(const W4Args& a, hipStream_t s) {
-  const dim3 grid((a.N + kWaves * U - 1) / (kWaves * U), a.M);
-  const size_t lds = static_cast<size_t>(a.K / 32) * 64 + static_cast<size_t>(a.K / kGroup) * 4;
-  // fp32 output with neither bias nor activation: the epilogue's general code compiled out
+  const dim3 grid((a.N + NW * U - 1) / (NW * U), (a.M + MR - 1) / MR);
+  const size_t lds = static_cast<size_t>(MR) * (a.K / 32) * 64;
   const bool simple = !a.bias && a.act == 0 && a.out == 0;
   if (a.bf16) {
-    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<CPL, U, true, true>), grid, dim3(kThreads), lds, s, a);
-    else hipLaunchKernelGGL((gemv_w4a16_kernel<CPL, U, true, false>), grid, dim3(kThreads), lds, s, a);
+    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, true>), grid, dim3(NW * 64), lds, s, a);
+    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, false>), grid, dim3(NW * 64), lds, s, a);
   } else {
-    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<CPL, U, false, true>), grid, dim3(kThreads), lds, s, a);
-    else hipLaunchKernelGGL((gemv_w4a16_kernel<CPL, U, false, false>), grid, dim3(kThreads), lds, s, a);
+    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, true>), grid, dim3(NW * 64), lds, s, a);
+    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, false>), grid, dim3(NW * 64), lds, s, a);
   }
   return hipGetLastError();
-}
-
-template <int CPL>
-hipError_t go_w4_rows(const W4Args& a, int u, hipStream_t s) {
-  switch (u) {
-    case 1: return go_w4<CPL, 1>(a, s);
-    case 2: return go_w4<CPL, 2>(a, s);
-    case 4: return go_w4<CPL, 4>(a, s);
-    default: return go_w4<CPL, 8>(a, s);
-  }
 }
 
 }  // namespace
@@ -414,25 +412,26 @@ hipError_t launch_align_w4(const AlignArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Rows per wave: every workgroup aligns the whole activation row, so U trades that repeated work
-// (workgroups x K elements) against workgroups in flight: the smallest U in {1, 2, 4, 8} that keeps
-// the repeated alignment within 1.5M elements. Measured on MI355X: K = 1536, N = 12288 6.59 us at
-// U = 4 (7.01 at U = 2, 7.55 at U = 8); K = 6144, N = 1536 5.53 us at U = 2 (5.81 at U = 1, 7.51
-// at U = 4).
-static int w4_rows_per_wave(int64_t N, int K) {
-  int u = 1;
-  while (u < 8 && (N + kWaves * u - 1) / (kWaves * u) * K > 3 * (1 << 19)) u *= 2;
-  return u;
+template <int NW, int U, int MR>
+hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
+  switch (cpl) {
+    case 1: return go_w4<NW, U, MR, 1>(a, s);
+    case 2: return go_w4<NW, U, MR, 2>(a, s);
+    case 3: return go_w4<NW, U, MR, 3>(a, s);
+    default: return go_w4<NW, U, MR, 4>(a, s);
+  }
 }
 
+// Shapes by measurement on MI355X (weights cold, graph replays): one activation row: rows of at
+// most 2048 k (one chunk per lane) 4 rows per wave in 4-wave workgroups (K = 1536, N = 12288:
+// 4.5 us; 3-, 8- and 12-wave workgroups within 0.2 us, 1 or 2 rows per wave 5.4 - 7.5 us); longer
+// rows one row per wave in 8-wave workgroups (K = 6144, N = 1536: 4.1 - 4.6 us; 4 rows per wave
+// 4.9 us, 12-wave workgroups 7.9 us). Prefill chunks: two activation rows per block, 4 rows per
+// wave (M = 4 / 8 at K = 1536, N = 12288: 11.3 / 19.4 us; four rows per block 12.7 / 20.0 us).
 hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
-  const int u = w4_rows_per_wave(a.N, a.K);
-  switch ((a.K / 32 + 63) / 64) {  // chunks per lane
-    case 1: return go_w4_rows<1>(a, u, s);
-    case 2: return go_w4_rows<2>(a, u, s);
-    case 3: return go_w4_rows<3>(a, u, s);
-    default: return go_w4_rows<4>(a, u, s);
-  }
+  const int cpl = (a.K / 32 + 63) / 64;  // chunks per lane
+  if (a.M >= 2) return go_cpl<4, 4, 2>(a, cpl, s);
+  return cpl == 1 ? go_cpl<4, 4, 1>(a, cpl, s) : go_cpl<8, 1, 1>(a, cpl, s);
 }
 
 }  // namespace tars

@@ -181,3 +181,40 @@ def test_partial_sums_above_2_pow_minus_100_absorb_subnormal_addends():
     tiny = ((27 << 23) << 1) - 1
     assert key(np.float32(2.0 ** -100)) == tiny and key(below) < tiny and key(np.float32(0)) > tiny
     assert (key(sub) < tiny).all()
+
+
+def test_balanced_hex_digit_planes_reconstruct_every_mantissa():
+    """The W4A16 GEMV writes each aligned mantissa a (|a| <= 2^14) as four balanced base-16 digits
+    and dots each digit plane with the weight nibbles on v_dot8_i32_i4 (signed 4-bit operands).
+    For every a in [-16384, 16384]: nibble i = floor((a + c_i) / 16^i) mod 16 with c = (0, 8, 136,
+    2184), read back as a signed 4-bit value d_i, satisfies sum 16^i d_i == a; so for any signed
+    4-bit weights w the planes' dots combine to the exact dot, sum_i 16^i sum_e w_e d_ie ==
+    sum_e w_e a_e (checked on random 8-element dwords too, with the kernel's packing order)."""
+    a = np.arange(-16384, 16385, dtype=np.int64)
+    c = (0, 8, 136, 2184)
+    nib = [((a + c[i]) >> (4 * i)) & 15 for i in range(4)]
+    d = [np.where(n >= 8, n - 16, n) for n in nib]                       # sign-extended 4-bit
+    assert all(((di >= -8) & (di <= 7)).all() for di in d)
+    assert (d[0] + 16 * d[1] + 256 * d[2] + 4096 * d[3] == a).all()
+    assert (np.abs(d[3]) <= 4).all()
+
+    def sext4(v):
+        return np.where(v >= 8, v - 16, v)
+
+    def dot8(wd, xd):
+        """v_dot8_i32_i4: the sum over the 8 nibble positions of the signed nibble products."""
+        s = np.zeros(wd.shape, np.int64)
+        for e in range(8):
+            s += sext4((wd >> (4 * e)) & 15) * sext4((xd >> (4 * e)) & 15)
+        return s
+
+    rng = np.random.default_rng(3)
+    w = rng.integers(-8, 8, (4000, 8))
+    x = rng.integers(-16384, 16385, (4000, 8))
+    x[:8] = [[-16384] * 8, [16384] * 8, [16383] * 8, [-16383] * 8, [8] * 8, [-8] * 8, [7] * 8, [-9] * 8]
+    wd = sum((w[:, e] & 15) << (4 * e) for e in range(8))              # low nibble of byte b = k 2b
+    total = np.zeros(4000, np.int64)
+    for i in range(4):
+        xd = sum((((x[:, e] + c[i]) >> (4 * i)) & 15) << (4 * e) for e in range(8))
+        total += dot8(wd, xd) << (4 * i)
+    assert (total == (w * x).sum(axis=1)).all()

@@ -433,6 +433,17 @@ def test_c5_w4a16_gemma4(K, N, seed):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("K,N", [(1536, 12288), (6144, 1536)])
+@pytest.mark.parametrize("M", [2, 4, 5, 8])
+def test_w4a16_prefill_chunks(K, N, M):
+    """W4A16 for prefill chunks (the board's W4 unit serves 1 / 4 / 8 rows): the C5 shapes at
+    M = 2, 4, 8 and a ragged M = 5 (two activation rows per block, the last block half empty)."""
+    x, Wp, ws, _ = w4_inputs(K + 7 * M, M, N, K)
+    y = ops.gemm_w4(cuda(x), cuda(Wp), cuda(ws))
+    want = G.gemm_w4(x, Wp, ws)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("K", [256, 512, 768, 1024, 2048, 4096, 8192])
 @pytest.mark.parametrize("M", [1, 3])
 def test_w4_shapes_bf16_bias_act(K, M):
