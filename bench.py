@@ -68,6 +68,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-queue", action="store_true", help="skip the descriptor-queue executor measurement")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample length")
     ap.add_argument("--detail", type=str, default="", help="also write the full result JSON here")
+    ap.add_argument("--only-configs", action="store_true",
+                    help="run only the per-config measurements and print them (for profiler passes)")
+    ap.add_argument("--config-reps", type=int, default=2000, help="launches timed per config")
     return ap.parse_args()
 
 
@@ -607,7 +610,11 @@ def rotated(torch, make, per_copy_bytes: int):
     return [make(i) for i in range(n)]
 
 
-def measure_config(torch, launches, reps_target: int = 2000) -> dict:
+CONFIG_REPS = 2000
+
+
+def measure_config(torch, launches, reps_target: int | None = None) -> dict:
+    reps_target = reps_target or CONFIG_REPS
     g = capture(torch, launches)
     reps = max(3, reps_target // len(launches))
     t = time_graph(torch, g, reps, warmup=2) / len(launches)
@@ -622,7 +629,7 @@ def measure_config(torch, launches, reps_target: int = 2000) -> dict:
     return r
 
 
-def config_suite(torch, lib, seed: int) -> dict:
+def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
     from opentars_amd import ops
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed + 1)
@@ -707,8 +714,9 @@ def config_suite(torch, lib, seed: int) -> dict:
         log(f"c5 K={K} N={N}: {r['us_per_call']} us")
         del ls, holds
         torch.cuda.empty_cache()
-    res["attention_decode_qwen3_t250"] = attention_decode(torch, lib, gen)
-    log(f"attention t=250: {res['attention_decode_qwen3_t250']['op_by_op']['us_per_layer']} us per layer")
+    if attention:
+        res["attention_decode_qwen3_t250"] = attention_decode(torch, lib, gen)
+        log(f"attention t=250: {res['attention_decode_qwen3_t250']['op_by_op']['us_per_layer']} us per layer")
     return res
 
 
@@ -935,6 +943,21 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     torch.backends.cuda.matmul.allow_tf32 = False
+    global CONFIG_REPS
+    CONFIG_REPS = args.config_reps
+    if args.only_configs:
+        # a 256 MiB device-to-device copy first: the calibration dispatch for profiler byte counters
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        configs = config_suite(torch, lib, args.seed, attention=False)
+        out = {"configs": configs}
+        if args.detail:
+            Path(args.detail).write_text(json.dumps(out, indent=1))
+        print(json.dumps(out), flush=True)
+        return 0
 
     log("building the decode-step workload")
     launches, unfused, keep = decode_set(torch, lib, args.seed)

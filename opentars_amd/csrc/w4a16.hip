@@ -167,13 +167,27 @@ __global__ __launch_bounds__(kThreads) void align_w4_kernel(AlignArgs a) {
 // v_dot8_i32_i4 of a weight dword with plane i is sum_e w_e d_{i,e} exactly, and the chunk's dot is
 // P0 + 16 P1 + 256 P2 + 4096 P3 (|dot| <= 2^24 per group: exact in int32).
 __device__ __forceinline__ void digit_planes(const int mant[8], uint32_t pl[4]) {
-  constexpr int kC[4] = {0, 8, 136, 2184};
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  constexpr unsigned kC[4] = {0, 8, 136, 2184};
+  // elements e and e + 4 as the two 16-bit halves of one register (|a| <= 2^14 and a + c_i fit
+  // in 16 bits, so 16-bit adds give the low 16 bits of a + c_i), then per plane and pair: one
+  // packed add, one packed shift moving nibble i of both halves to nibble positions e and e + 4
+  // of their halves, one masked or into the plane
+  u16x2 pr[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    pr[e] = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(static_cast<uint32_t>(mant[e + 4]),
+                                                           static_cast<uint32_t>(mant[e]), 0x05040100u));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t v = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v |= ((static_cast<uint32_t>(mant[e] + kC[i]) >> (4 * i)) & 15u) << (4 * e);
+    for (int e = 0; e < 4; ++e) {
+      u16x2 q = pr[e] + u16x2{static_cast<unsigned short>(kC[i]), static_cast<unsigned short>(kC[i])};
+      if (e > i) q = q << static_cast<unsigned short>(4 * (e - i));
+      if (e < i) q = q >> static_cast<unsigned short>(4 * (i - e));
+      v |= __builtin_bit_cast(uint32_t, q) & (0x000F000Fu << (4 * e));
+    }
     pl[i] = v;
   }
 }
