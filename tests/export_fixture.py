@@ -9,7 +9,8 @@ from pathlib import Path
 import numpy as np
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-KINDS = {"qwen3": "export_small.npz", "qwen35_mtp": "export_qwen35_mtp.npz", "gemma4": "export_gemma4.npz"}
+KINDS = {"qwen3": "export_small.npz", "qwen35_mtp": "export_qwen35_mtp.npz", "gemma4": "export_gemma4.npz",
+         "gemma3_ksplit": "export_gemma3_ksplit.npz", "gemma4_w4": "export_gemma4_w4.npz"}
 
 
 def unpack(dst: Path, kind: str = "qwen3") -> Path:

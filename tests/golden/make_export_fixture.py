@@ -5,6 +5,11 @@ full-attention layers, the MTP head and the speculative-decoding queues) and exp
 input embedding). Each holds the files tools/export_kv260.py writes (image.bin, embed_bf16.bin,
 ple_bf16.bin, queues.bin, queues_c<n>.bin, queues_s_*.bin, manifest.json) and expected.json.
 
+Two more exports pin the compositions the three above leave open: export_gemma3_ksplit.npz (Gemma 3
+with intermediate 4608, so every down projection is two K blocks added in fp32, llm.py:303-321) and
+export_gemma4_w4.npz (Gemma 4 lowered with wbits=4: every linear a W4A16 GEMM, the double-wide
+down projections as W4 K blocks with their own group scales, llm.py:120-132, 306-313).
+
 The models are the reference's small configurations (qwen_ref.py:43-45, 79-90) with a 512-token
 vocabulary and seeded random weights (qwen_ref.random_weights / random_mtp, the embedding tables
 rounded to bf16 as the export requires). The descriptor queues and DDR images come from the
@@ -15,7 +20,8 @@ step the argmax and the SHA-256 of the fp32 logits, and for the MTP export the t
 rows of speculative rounds. This script imports the reference checkout (read-only, in the build
 container only); the .npz files hold data only and the GPU box never runs this.
 
-    python tests/golden/make_export_fixture.py [qwen3|qwen35_mtp|gemma4 ...] [--ref /path/to/reference]
+    python tests/golden/make_export_fixture.py [qwen3|qwen35_mtp|gemma4|gemma3_ksplit|gemma4_w4 ...] \
+        [--ref /path/to/reference]
 """
 from __future__ import annotations
 
@@ -32,7 +38,8 @@ HERE = Path(__file__).resolve().parent
 T = 40                       # positions
 CHUNKS, ALIGN = (8, 4), 4    # prefill chunk sizes and their start alignment (export_kv260.py:48)
 HPAGE = 2 << 20
-OUT = {"qwen3": "export_small.npz", "qwen35_mtp": "export_qwen35_mtp.npz", "gemma4": "export_gemma4.npz"}
+OUT = {"qwen3": "export_small.npz", "qwen35_mtp": "export_qwen35_mtp.npz", "gemma4": "export_gemma4.npz",
+       "gemma3_ksplit": "export_gemma3_ksplit.npz", "gemma4_w4": "export_gemma4_w4.npz"}
 # token sequences the expected results are recorded on
 PROMPTS = [dict(name="plain", ids=[3, 141, 59, 26, 500, 7, 7, 311, 42, 9, 88, 201, 17], new=8),
            dict(name="short", ids=[1, 2], new=6)]
@@ -57,6 +64,19 @@ def model(kind: str):
         w = Q.random_weights(cfg, seed=2027, embed=True)
         w.update(Q.random_mtp(cfg, seed=5))
         return cfg, w, dict(scratch_bytes=1 << 21, verify_rows=2, mtp=True, queue_cap=4096)
+    if kind == "gemma3_ksplit":
+        # intermediate 4608: every down projection runs as two K blocks [2304, 2304] (as the
+        # reference's Gemma 3 test sets it up, tests/test_v04.py:313-317)
+        cfg = Q.make_config(dict(Q.CFG_G3_SMALL, intermediate_size=4608), ["sliding_attention", "full_attention"],
+                            vocab=512)
+        return cfg, Q.random_weights(cfg, seed=2029, embed=True), dict(scratch_bytes=1 << 22, queue_cap=4096)
+    if kind == "gemma4_w4":
+        # W4A16 linears (llm.py:120-132); intermediate 2304, so the two KV-shared layers' double-wide
+        # MLP (4608) runs its down projection as two W4 K blocks with their own group scales
+        # (llm.py:306-313); per-layer inputs of 256 (a W4 GEMM needs K >= 256, llm.py:123)
+        cfg = Q.make_config(dict(Q.CFG_G4_SMALL, intermediate_size=2304, hidden_size_per_layer_input=256), vocab=512)
+        return cfg, Q.random_weights(cfg, seed=2030, embed=True), dict(scratch_bytes=1 << 22, keep_layers=False,
+                                                                         queue_cap=4096, wbits=4)
     cfg = Q.make_config(Q.CFG_G4_SMALL, vocab=512)
     return cfg, Q.random_weights(cfg, seed=2028, embed=True), dict(scratch_bytes=1 << 22, keep_layers=False,
                                                                      queue_cap=4096)
@@ -93,8 +113,9 @@ def write_export(out: Path, kind: str) -> None:
     chunks = {str(n): emit(low, out / f"queues_c{n}.bin",
                            [(t0, lambda t0=t0, n=n: low.chunk(t0, n)) for t0 in range(0, T - n + 1, ALIGN)])
               for n in CHUNKS}
+    wbits = opts.get("wbits", 8)
     m = dict(model=f"{kind}-small-random", max_tokens=T, hidden=low.H, vocab=low.vocab, state_dtype="fp32",
-             wbits=8, min_firmware=0, keep_layers=low.keep_layers, bos_ids=[], turn_end="<|im_end|>\n",
+             wbits=wbits, min_firmware=0x00040001 if wbits == 4 else 0, keep_layers=low.keep_layers, bos_ids=[], turn_end="<|im_end|>\n",
              embed_scale=float(L.input_embedding(cfg, np.ones((1, 1), np.float32))[0, 0])
              if (low.gemma or low.gemma4) else None,
              image_bytes=len(img), state_end=low.scratch_end, qbase=low.qbase, queue_cap=low.queue_cap,

@@ -121,3 +121,41 @@ def test_runtime_needs_a_gpu(export_dir):
         Model(export_dir, log=None)
     with pytest.raises(RuntimeError, match="needs a ROCm GPU"):
         GpuDevice(1 << 20)
+
+
+def _descs(export_dir, pos):
+    m = json.loads((export_dir / "manifest.json").read_text())
+    off, n = m["queue_index"][pos]
+    raw = (export_dir / "queues.bin").read_bytes()[off:off + 64 * n]
+    return [Q.decode(raw[64 * i:64 * i + 64]) for i in range(n)]
+
+
+def test_ksplit_export_holds_two_block_down_projections(tmp_path):
+    """export_gemma3_ksplit.npz pins the K split end to end: every layer's down projection is two
+    QM_ROWCOL GEMMs over K = 2304 blocks of one quantized row (the same row scale and per-channel
+    scales), their partials added by an fp32 ELT ADD (llm.py:303-321, 627-635)."""
+    d = unpack(tmp_path, "gemma3_ksplit")
+    ds = _descs(d, 5)
+    blocks = [i for i, x in enumerate(ds) if x["OPCODE"] == Q.OP_GEMM and x["K"] == 2304]
+    assert len(blocks) == 2 * 2                                      # two layers, two blocks each
+    for i in blocks[::2]:
+        a, b = ds[i], ds[i + 1]
+        assert b["OPCODE"] == Q.OP_GEMM and b["K"] == 2304 and a["N"] == b["N"] == 256
+        assert a["SCALE_OFF"] == b["SCALE_OFF"] and a["A_OFF"] != b["A_OFF"]       # shared scales, the row's halves
+        adds = [x for x in ds[i + 2:i + 6] if x["OPCODE"] == Q.OP_ELT and x["CTRL"] & 3 == Q.ELT_ADD]
+        assert adds, "the block partials are added by an ELT ADD"
+
+
+def test_w4_export_runs_every_linear_as_w4a16_with_k_blocks(tmp_path):
+    """export_gemma4_w4.npz: every GEMM of a decode step is W4A16 (QM_GROUP, int4 weights), and
+    the KV-shared layers' double-wide down projections (K = 4608) are two W4 K blocks with their
+    own group scales (llm.py:120-132, 306-313)."""
+    d = unpack(tmp_path, "gemma4_w4")
+    ds = _descs(d, 3)
+    gemms = [x for x in ds if x["OPCODE"] == Q.OP_GEMM]
+    assert gemms and all(Q.is_w4(x) for x in gemms)
+    kb = [i for i, x in enumerate(ds) if Q.is_w4(x) and x["K"] == 2304 and x["N"] == 256]
+    pairs = [(ds[i], ds[i + 1]) for i in kb if i + 1 < len(ds) and Q.is_w4(ds[i + 1]) and ds[i + 1]["K"] == 2304]
+    assert len(pairs) >= 2
+    for a, b in pairs:
+        assert a["SCALE_OFF"] != b["SCALE_OFF"] and a["W_OFF"] != b["W_OFF"]         # each block its own scales
