@@ -323,6 +323,13 @@ int tars_encode_descriptor(const uint64_t* fields, int32_t fix_crc, uint8_t* des
  * Returns the previous setting. Process-wide. */
 int tars_set_queue_fusion(int on);
 
+/* Fused launches tars_run_queue has run (diagnostics for tests and benchmarks, not part of the
+ * reference's interface), counted per kind since the last reset: counts[0] decode-row quantizer +
+ * GEMMs, counts[1] attention (per-head FDOT / softmax / FDOT triples), counts[2] residual ELT ADD +
+ * norm, counts[3] norm + RoPE. A replayed launch plan counts its fused launches again. counts
+ * (4 values) may be NULL; reset != 0 zeroes the counts after reading them. Process-wide. */
+int tars_queue_fusion_counts(int64_t* counts, int32_t reset);
+
 /* Launch plans in tars_run_queue (benchmark and test control): 1 (default) keeps, for up to 8
  * queues, the launches of a queue that ran to the end without a hand-off or an output over its own
  * descriptors; when the same descriptor bytes run again on the same image with the same settings,

@@ -16,6 +16,7 @@
 // A decode-row ROW_QUANT and the QM_ROWCOL GEMMs that read it run as one fused launch (peephole
 // fusion, bit-identical to the one-by-one order; see fuse_group).
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -894,6 +895,17 @@ struct Plan {
   uint64_t last_use = 0;
 };
 
+// Fused launches run (diagnostics for tests and benchmarks): quantizer + GEMMs, attention,
+// residual ADD + norm, norm + RoPE; counted when a queue is dispatched and when a plan replays.
+std::atomic<int64_t> g_fused_launches[4];
+
+void count_fused(const std::vector<Step>& steps) {
+  for (const Step& st : steps) {
+    const int k = !st.group.empty() ? 0 : !st.attn.empty() ? 1 : st.add_norm ? 2 : st.norm_rope ? 3 : -1;
+    if (k >= 0) g_fused_launches[k].fetch_add(1, std::memory_order_relaxed);
+  }
+}
+
 constexpr size_t kMaxPlans = 8;
 std::mutex g_plans_mu;
 std::vector<Plan> g_plans;
@@ -1033,6 +1045,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
         break;
       }
       if (hipGraphLaunch(p.exec, s) != hipSuccess) return queue_fail(TARS_E_DEVICE, "graph launch failed");
+      count_fused(p.steps);
       p.last_use = ++g_plan_clock;
       st->done = 1;
       st->op_idx = n;
@@ -1065,6 +1078,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
                             group))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
+      g_fused_launches[0].fetch_add(1, std::memory_order_relaxed);
       if (cacheable) steps.push_back(Step{c.d, std::move(group), {}});
       i += fused;  // the quantizer and `fused` GEMMs ran as one launch
       continue;
@@ -1074,6 +1088,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
                                 (static_cast<uint64_t>(i) + 3), q_end, image_len, core_id, gemv_only != 0, s, fused, heads))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
+      g_fused_launches[1].fetch_add(1, std::memory_order_relaxed);
       if (cacheable) steps.push_back(Step{c.d, {}, std::move(heads)});
       i += 3 * fused - 1;  // `fused` heads of three descriptors ran as one launch
       continue;
@@ -1083,6 +1098,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
                                (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, norm))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
+      g_fused_launches[2].fetch_add(1, std::memory_order_relaxed);
       if (cacheable) {
         Step st2{c.d, {}, {}};
         st2.second = norm;
@@ -1097,6 +1113,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
                                 (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, rope))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
+      g_fused_launches[3].fetch_add(1, std::memory_order_relaxed);
       if (cacheable) {
         Step st2{c.d, {}, {}};
         st2.second = rope;
@@ -1145,6 +1162,14 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     p.steps = std::move(steps);
     p.last_use = ++g_plan_clock;
     g_plans.push_back(std::move(p));
+  }
+  return TARS_OK;
+}
+
+int tars_queue_fusion_counts(int64_t* counts, int32_t reset) {
+  for (int k = 0; k < 4; ++k) {
+    const int64_t v = reset ? g_fused_launches[k].exchange(0) : g_fused_launches[k].load();
+    if (counts) counts[k] = v;
   }
   return TARS_OK;
 }

@@ -189,11 +189,22 @@ def set_fusion(on: bool) -> bool:
     return bool(_lib.lib().tars_set_queue_fusion(int(on)))
 
 
+FUSION_KINDS = ("quant_gemm", "attention", "add_norm", "norm_rope")
+
+
+def fusion_counts(reset: bool = False) -> dict:
+    """Fused launches run_queue has run since the last reset, per kind (FUSION_KINDS); a replayed
+    launch plan counts its fused launches again. Diagnostics for tests and benchmarks."""
+    arr = (ctypes.c_int64 * 4)()
+    _lib.lib().tars_queue_fusion_counts(arr, int(reset))
+    return dict(zip(FUSION_KINDS, (int(v) for v in arr)))
+
+
 def set_graphs(on: bool) -> bool:
     """Launch plans replayed as HIP graphs for repeated queues in run_queue (default on); returns
     the previous setting. Turning it off drops the kept plans."""
     return bool(_lib.lib().tars_set_queue_graphs(int(on)))
 
 
-__all__ = ["Machine", "Status", "run", "check_descriptor", "decode_descriptor", "descriptor_crc",
+__all__ = ["Machine", "Status", "run", "check_descriptor", "decode_descriptor", "descriptor_crc", "fusion_counts",
            "encode_descriptor", "set_fusion", "set_graphs", "FIELDS", "ERR_NAMES"]

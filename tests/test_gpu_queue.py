@@ -411,19 +411,20 @@ def test_chains_whose_partial_sums_are_subnormal(seed, fusion):
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
-def add_residual_norm(p: Program, M: int, N: int, inplace: bool, norm_over_b: bool = False):
+def add_residual_norm(p: Program, M: int, N: int, inplace: bool, norm_over_b: bool = False, shift: int = 0):
     """A residual ELT ADD of dense fp32 rows (fp32 out, no activation) and a norm of its output, the
-    pair the executor fuses; norm_over_b: the norm writes over the ELT's B rows (fp32), which the
-    executor must not fuse."""
+    pair the executor fuses; norm_over_b: the norm writes over the ELT's B rows (fp32), shifted by
+    `shift` rows (shift 1: norm row r lands on B row r + 1, which the fused launch's row r + 1 would
+    read after row r wrote it), which the executor must not fuse."""
     rng = p.rng
     a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
-    b, ldb16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    b, ldb16 = put_rows(p, rand_rows(p, M + shift, N), 4 * N)
     y, ldy16 = (a, lda16) if inplace else stride_fields(p, M, 4 * N)
     p.add(OPCODE=Q.OP_ELT, CTRL=Q.ELT_ADD, EPI=Q.epi(), A_OFF=a, W_OFF=b, Y_OFF=y, M=M, N=N, LDA16=lda16, LDY16=ldy16,
           GROUP_SIZE=ldb16)
     fn = int(rng.choice([Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM]))
     if norm_over_b:
-        out, yo, ldyo16, osc = Q.OUT_FP32, b, ldb16, 0
+        out, yo, ldyo16, osc = Q.OUT_FP32, b + shift * (16 * ldb16 if ldb16 else 4 * N), ldb16, 0
     else:
         out, yo, ldyo16, osc = out_fields(p, M, N)
     g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
@@ -444,22 +445,28 @@ def test_residual_add_then_norm(seed, fusion):
     for k, (M, N) in enumerate(((1, 1024), (3, 2048), (2, 224), (1, 2064), (4, 1024))):
         add_residual_norm(p, M, N, inplace=bool(k % 2))
     add_residual_norm(p, 1, 1024, inplace=True, norm_over_b=True)
+    add_residual_norm(p, 3, 512, inplace=True, norm_over_b=True, shift=1)
+    add_residual_norm(p, 4, 256, inplace=False, norm_over_b=True, shift=1)
     prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
     try:
         (o, ost), (g, gst) = both(p.image(), len(p.descs))
     finally:
         NQ.set_fusion(prev)
     assert ost.done and same_status(ost, gst), (ost, gst)
+    # exactly the four pairs within the fused kernel's row limit and free of hazards ran fused
+    assert NQ.fusion_counts()["add_norm"] == (4 if fusion else 0)
     gd = bytes(g.ddr)
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
-def add_norm_then_rope(p: Program, M: int, N: int, rot: int, G: int, rope_over_x: bool = False):
+def add_norm_then_rope(p: Program, M: int, N: int, rot: int, G: int, rope_over_x: bool = False, shift: int = 0):
     """A norm with an fp32 output and a RoPE of its output rows (fp32 out), the pair the executor
-    fuses; rope_over_x: the RoPE writes over the norm's input rows, which the executor must not
-    fuse."""
+    fuses; rope_over_x: the RoPE writes over the norm's input rows, shifted by `shift` rows (shift
+    1: RoPE row r lands on input row r + 1, which the fused launch's row r + 1 would read after
+    row r wrote it), which the executor must not fuse."""
     rng = p.rng
-    a, lda16 = put_rows(p, rand_rows(p, M, N), 4 * N)
+    a, lda16 = put_rows(p, rand_rows(p, M + shift, N), 4 * N)
     y, ldy16 = stride_fields(p, M, 4 * N)
     g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
     bias = int(rng.integers(0, 2))
@@ -470,7 +477,8 @@ def add_norm_then_rope(p: Program, M: int, N: int, rot: int, G: int, rope_over_x
     rows = (M - 1) // G + 1
     fr = np.arange(rows, dtype=np.float32)[:, None] * rng.uniform(0.01, 1.0, rot // 2).astype(np.float32)[None, :]
     t = p.put(np.concatenate([np.cos(fr), np.sin(fr)], 1).astype("<f4").tobytes())
-    yr, ldyr16 = (a, lda16) if rope_over_x else stride_fields(p, M, 4 * N)
+    yr, ldyr16 = ((a + shift * (16 * lda16 if lda16 else 4 * N), lda16) if rope_over_x
+                  else stride_fields(p, M, 4 * N))
     p.add(OPCODE=Q.OP_ROPE, EPI=Q.epi(), A_OFF=y, W_OFF=t, Y_OFF=yr, M=M, N=N, K=rot, GROUP_SIZE=G, LDA16=ldy16,
           LDY16=ldyr16)
 
@@ -486,12 +494,17 @@ def test_norm_then_rope(seed, fusion):
     for M, N, rot, G in ((16, 128, 128, 16), (8, 128, 128, 8), (6, 256, 128, 2), (3, 2048, 2048, 1), (2, 2080, 64, 1)):
         add_norm_then_rope(p, M, N, rot, G)
     add_norm_then_rope(p, 4, 128, 128, 4, rope_over_x=True)
+    add_norm_then_rope(p, 4, 128, 128, 4, rope_over_x=True, shift=1)
+    add_norm_then_rope(p, 3, 256, 64, 1, rope_over_x=True, shift=1)
     prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
     try:
         (o, ost), (g, gst) = both(p.image(), len(p.descs))
     finally:
         NQ.set_fusion(prev)
     assert ost.done and same_status(ost, gst), (ost, gst)
+    # exactly the four pairs within the fused kernel's row limit and free of hazards ran fused
+    assert NQ.fusion_counts()["norm_rope"] == (4 if fusion else 0)
     gd = bytes(g.ddr)
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
@@ -707,7 +720,11 @@ def plant_attention_specials(rng, q, kc, vv, kv_heads, hd, v_fp16):
     """Values whose flushes change a result: subnormal K and V elements, K and V columns of tiny
     normals (their products with q or with a probability are subnormal), an infinite q element
     against a subnormal K element (the flushed product is NaN, the unflushed one infinite), and two
-    equal K rows whose V values cancel to a subnormal partial sum (2^-100 (1 - (1 - 2^-23)) p)."""
+    equal K rows whose V values cancel to a subnormal partial sum (2^-100 (1 - (1 - 2^-23)) p).
+    The tiny K column 9 is the first step of its 16-lane chain (the chain starts subnormal); the tiny
+    K column 25 is the second step of the same lane's chain and the V column 6 turns tiny halfway
+    down the keys, so there a normal partial sum absorbs the subnormal products (the unflushed fast
+    path's case)."""
     nk = kc.shape[0]
     sub = lambda n: (rng.integers(1, 1 << 23, n, dtype=np.uint32) | (rng.integers(0, 2, n, dtype=np.uint32) << 31)).view(np.float32)
     for kv in range(kv_heads):
@@ -715,9 +732,12 @@ def plant_attention_specials(rng, q, kc, vv, kv_heads, hd, v_fp16):
         kc[rng.integers(0, nk, 6), c0 + rng.integers(0, hd, 6)] = sub(6)
         kc[:, c0 + 9] = rng.normal(0, 1, nk).astype(np.float32) * np.float32(2.0 ** -70)
         q[:, c0 + 9] = np.float32(2.0 ** -60)
+        kc[:, c0 + 25] = rng.normal(0, 1, nk).astype(np.float32) * np.float32(2.0 ** -70)
+        q[:, c0 + 25] = np.float32(2.0 ** -60)
         if not v_fp16:
             vv[rng.integers(0, nk, 6), c0 + rng.integers(0, hd, 6)] = sub(6)
             vv[:, c0 + 5] = rng.normal(0, 1, nk).astype(np.float32) * np.float32(2.0 ** -124)
+            vv[nk // 2:, c0 + 6] = rng.normal(0, 1, nk - nk // 2).astype(np.float32) * np.float32(2.0 ** -124)
             vv[0, c0 + 3], vv[1, c0 + 3] = np.float32(2.0 ** -100), -np.float32(2.0 ** -100) * np.float32(1 - 2.0 ** -23)
         kc[1, c0:c0 + hd] = kc[0, c0:c0 + hd]
     q[0, 7] = np.inf
