@@ -71,6 +71,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--only-configs", action="store_true",
                     help="run only the per-config measurements and print them (for profiler passes)")
     ap.add_argument("--config-reps", type=int, default=2000, help="launches timed per config")
+    ap.add_argument("--pmc-summary", nargs=5, metavar=("FETCH_CSV", "WRITE_CSV", "MFMA_CSV", "VALU_CSV", "DETAIL"),
+                    help="write the per-config counter table from four --only-configs rocprofv3 passes and exit")
+    ap.add_argument("--pmc-out", type=str, default=str(ROOT / "profiles" / "config_traffic.json"))
     return ap.parse_args()
 
 
@@ -629,6 +632,105 @@ def measure_config(torch, launches, reps_target: int | None = None) -> dict:
     return r
 
 
+# ------------------------------------------------------------------------------ profiler counters per config
+CLOCK_HZ = 2.4e9            # MI355X peak engine clock
+SIMDS = 1024                # 256 CUs x 4 SIMDs
+COUNTER_FILE = ROOT / "profiles" / "config_traffic.json"
+# the kernel instance (as rocprofv3 names it) and grid size in work-items that each per-config
+# measurement dispatches, as the library's selection rules pick them
+CONFIG_KERNELS = {
+    "c1_gemv_qwen3_gate_M1_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 1, true>", 196608),
+    "lm_head_M1_K1024_N151936": ("gemv_w8a8_kernel<64, 1, 4, 1, true>", 2430976),
+    "lm_head_fused_quant_M1_K1024_N151936": ("quant_gemv_w8a8_kernel<64, 1, 4, true>", 2430976),
+    "c2_gemma3_down_ksplit_3456+3456": ("gemv_w8a8_ksplit_rows_kernel<2, 4>", 294912),
+    "c2_gemma3_down_ksplit_4096+2816": ("gemv_w8a8_ksplit_rows_kernel<2, 4>", 294912),
+    "c4_prefill_M4_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 4, true>", 196608),
+    "c4_prefill_M4_K3072_N1024": ("gemv_w8a8_kernel<64, 3, 1, 4, true>", 65536),
+    "c4_prefill_M4_K1024_N3072_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 98304),
+    "c4_prefill_M4_K3072_N1024_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 32768),
+    "c4_prefill_M256_K1024_N3072": ("mfma_staged_kernel<64, 64, 4, 4, 128, 4, true>", 196608),
+    "c4_prefill_M256_K3072_N1024": ("mfma_staged_kernel<32, 32, 2, 2, 256, 3, true>", 65536),
+    "c5_w4a16_M1_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 1, 1, false, true>", 196608),
+    "c5_w4a16_M1_K6144_N1536": ("gemv_w4a16_kernel<8, 1, 1, 3, false, true>", 98304),
+    "c5_w4a16_M4_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 2, 1, false, true>", 393216),
+    "c5_w4a16_M4_K6144_N1536": ("gemv_w4a16_kernel<4, 4, 2, 3, false, true>", 49152),
+    "c5_w4a16_M8_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 2, 1, false, true>", 786432),
+    "c5_w4a16_M8_K6144_N1536": ("gemv_w4a16_kernel<4, 4, 2, 3, false, true>", 98304),
+}
+
+
+def pmc_means(path: str) -> dict:
+    """Per (kernel, grid) of a rocprofv3 counter_collection.csv: the dispatch count and the mean
+    per dispatch of each counter (summed over the counter's hardware instances)."""
+    import csv
+    disp = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            d = disp.setdefault(row["Dispatch_Id"], {"kernel": row["Kernel_Name"], "grid": int(row["Grid_Size"]),
+                                                     "c": {}})
+            d["c"][row["Counter_Name"]] = d["c"].get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    agg = {}
+    for d in disp.values():
+        a = agg.setdefault((d["kernel"], d["grid"]), {"n": 0, "sum": {}})
+        a["n"] += 1
+        for c, v in d["c"].items():
+            a["sum"][c] = a["sum"].get(c, 0.0) + v
+    return {k: {"dispatches": a["n"], **{c: v / a["n"] for c, v in a["sum"].items()}} for k, a in agg.items()}
+
+
+def pmc_summary(csvs: list, detail: str, out: str) -> int:
+    """The per-config counter table from four `--only-configs` profiler passes (FETCH_SIZE;
+    WRITE_SIZE; SQ_VALU_MFMA_BUSY_CYCLES + SQ_INSTS_VALU_MFMA_MOPS_I8; SQ_INSTS_VALU) and the
+    first pass's --detail output (algorithmic bytes per config). Byte counters are scaled by what
+    they read for the 256 MiB device copy the pass starts with."""
+    P = [pmc_means(p) for p in csvs]
+    configs = json.loads(Path(detail).read_text())["configs"]
+
+    def find(p, sub, grid):
+        hits = [k for k in p if sub in k[0] and k[1] == grid]
+        if len(hits) != 1:
+            raise SystemExit(f"{len(hits)} kernels match {sub} with grid {grid}")
+        return hits[0]
+    copy = max((k for k in P[0] if "copyBuffer" in k[0]), key=lambda k: P[0][k]["FETCH_SIZE"])
+    fetch_scale = (256 << 20) / (P[0][copy]["FETCH_SIZE"] * 1024)
+    write_scale = (256 << 20) / (P[1][find(P[1], copy[0], copy[1])]["WRITE_SIZE"] * 1024)
+    table = {}
+    for key, (sub, grid) in CONFIG_KERNELS.items():
+        m = [p[find(p, sub, grid)] for p in P]
+        rd, wr = m[0]["FETCH_SIZE"] * 1024 * fetch_scale, m[1]["WRITE_SIZE"] * 1024 * write_scale
+        alg = configs[key]["bytes_per_call"]
+        table[key] = {"kernel": sub, "grid_workitems": grid, "dispatches": m[0]["dispatches"],
+                      "read_bytes": round(rd), "write_bytes": round(wr), "traffic_bytes": round(rd + wr),
+                      "algorithmic_bytes": alg, "traffic_over_algorithmic": round((rd + wr) / alg, 3),
+                      "mfma_busy_cycles_per_simd": round(m[2].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / SIMDS, 1),
+                      "mfma_i8_ops": round(m[2].get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) * 512),
+                      "valu_instructions_per_simd": round(m[3].get("SQ_INSTS_VALU", 0.0) / SIMDS, 1)}
+    Path(out).write_text(json.dumps({"fetch_scale": round(fetch_scale, 5), "write_scale": round(write_scale, 5),
+                                     "calibration": "256 MiB device-to-device copy", "configs": table}, indent=1))
+    print(f"{len(table)} configs; FETCH_SIZE x {fetch_scale:.4f}, WRITE_SIZE x {write_scale:.4f}", flush=True)
+    return 0
+
+
+def attach_counters(res: dict) -> None:
+    """Profiler figures for each measured config whose algorithmic bytes match the table's: HBM
+    traffic per call, and the share of the call (at the measured time and peak clock) that each
+    SIMD's MFMA unit is busy and that its VALU issues (a wave64 VALU instruction holds a SIMD for
+    4 cycles)."""
+    if not COUNTER_FILE.exists():
+        return
+    table = json.loads(COUNTER_FILE.read_text())["configs"]
+    for key, r in res.items():
+        e = table.get(key)
+        if not e or e["algorithmic_bytes"] != r.get("bytes_per_call"):
+            continue
+        cycles = r["us_per_call"] * 1e-6 * CLOCK_HZ
+        r["counters"] = {"kernel": e["kernel"], "traffic_bytes": e["traffic_bytes"],
+                         "traffic_over_algorithmic": e["traffic_over_algorithmic"],
+                         "mfma_busy_frac": round(e["mfma_busy_cycles_per_simd"] / cycles, 4),
+                         "valu_issue_frac": round(4 * e["valu_instructions_per_simd"] / cycles, 4),
+                         "source": "profiles/config_traffic.json (rocprofv3 --pmc)"}
+
+
 def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
     from opentars_amd import ops
     gen = torch.Generator(device="cuda")
@@ -697,9 +799,10 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
             key = f"c4_prefill_M{M}_K{K}_N{N}" + ("_mfma" if path == 2 else "")
             res[key] = r
             log(f"{key}: {r['us_per_call']} us ({r['family']})")
-    for K, N in ((1536, 12288), (6144, 1536)):
-        x = torch.randn((1, K), device="cuda", generator=gen)
-        y = torch.empty((1, N), device="cuda")
+    for M, K, N in ((1, 1536, 12288), (1, 6144, 1536), (4, 1536, 12288), (4, 6144, 1536), (8, 1536, 12288),
+                    (8, 6144, 1536)):
+        x = torch.randn((M, K), device="cuda", generator=gen)
+        y = torch.empty((M, N), device="cuda")
         holds = []
 
         def make(i):
@@ -709,14 +812,15 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
             return w4_launch(lib, x, Wp, ws, y, "c5")
         ls = rotated(torch, make, N * K // 2)
         r = measure_config(torch, ls)
-        r.update(M=1, N=N, K=K)
-        res[f"c5_w4a16_M1_K{K}_N{N}"] = r
-        log(f"c5 K={K} N={N}: {r['us_per_call']} us")
+        r.update(M=M, N=N, K=K)
+        res[f"c5_w4a16_M{M}_K{K}_N{N}"] = r
+        log(f"c5 M={M} K={K} N={N}: {r['us_per_call']} us")
         del ls, holds
         torch.cuda.empty_cache()
     if attention:
         res["attention_decode_qwen3_t250"] = attention_decode(torch, lib, gen)
         log(f"attention t=250: {res['attention_decode_qwen3_t250']['op_by_op']['us_per_layer']} us per layer")
+    attach_counters(res)
     return res
 
 
@@ -930,6 +1034,8 @@ def cpu_description() -> dict:
 # ------------------------------------------------------------------------------ main
 def main() -> int:
     args = parse()
+    if args.pmc_summary:
+        return pmc_summary(args.pmc_summary[:4], args.pmc_summary[4], args.pmc_out)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the matrix path runs on a single GPU here (sharding the "
               "output channels over several GPUs is not implemented); use --gpus 1", file=sys.stderr)

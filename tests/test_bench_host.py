@@ -1,0 +1,95 @@
+"""bench.py's host-side pieces that need no GPU: the per-config profiler table built from
+rocprofv3 counter CSVs (the byte counters scaled by the calibration copy, one table entry per
+measured config), and its attachment to measured configs."""
+from __future__ import annotations
+
+import csv
+import importlib.util
+import json
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="module")
+def bench():
+    spec = importlib.util.spec_from_file_location("bench_under_test", ROOT / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["bench_under_test"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def write_pass(path: Path, counters: dict, per_kernel: dict, copy_value: dict) -> None:
+    """A counter CSV as rocprofv3 writes it: one row per dispatch, counter and hardware instance
+    (here each dispatch's value split over two instances, which the summary must add back)."""
+    cols = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, cols)
+        w.writeheader()
+        did = 0
+        rows = [("__amd_rocclr_copyBuffer", 131072, copy_value)] + [
+            (f"void tars::(anonymous namespace)::{name}(Args)", grid, per_kernel[(name, grid)])
+            for name, grid in per_kernel]
+        for name, grid, vals in rows:
+            for _ in range(3):
+                did += 1
+                for c in counters:
+                    for half in (0.25, 0.75):
+                        w.writerow({"Dispatch_Id": did, "Kernel_Name": name, "Grid_Size": grid,
+                                    "Counter_Name": c, "Counter_Value": vals.get(c, 0.0) * half})
+
+
+def test_pmc_summary_scales_and_attaches(bench, tmp_path, monkeypatch):
+    kernels = sorted(set(bench.CONFIG_KERNELS.values()))
+    fetch = {k: {"FETCH_SIZE": 1000.0 + i} for i, k in enumerate(kernels)}
+    write = {k: {"WRITE_SIZE": 10.0 + i} for i, k in enumerate(kernels)}
+    mfma = {k: {"SQ_VALU_MFMA_BUSY_CYCLES": 1024.0 * 768, "SQ_INSTS_VALU_MFMA_MOPS_I8": 2.0} for k in kernels}
+    valu = {k: {"SQ_INSTS_VALU": 1024.0 * 100} for k in kernels}
+    # the copy of 256 MiB reads FETCH_SIZE = 131072 KiB (64 B units counted as 32) and writes 262144 KiB
+    paths = []
+    for i, (cnt, table, copy) in enumerate((
+            (["FETCH_SIZE"], fetch, {"FETCH_SIZE": 131072.0}),
+            (["WRITE_SIZE"], write, {"WRITE_SIZE": 262144.0}),
+            (["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_I8"], mfma, {}),
+            (["SQ_INSTS_VALU"], valu, {}))):
+        p = tmp_path / f"p{i}.csv"
+        write_pass(p, cnt, table, copy)
+        paths.append(str(p))
+    detail = tmp_path / "detail.json"
+    detail.write_text(json.dumps({"configs": {k: {"bytes_per_call": 2_000_000} for k in bench.CONFIG_KERNELS}}))
+    out = tmp_path / "table.json"
+    assert bench.pmc_summary(paths, str(detail), str(out)) == 0
+    t = json.loads(out.read_text())
+    assert t["fetch_scale"] == 2.0 and t["write_scale"] == 1.0
+    for key, (name, grid) in bench.CONFIG_KERNELS.items():
+        e = t["configs"][key]
+        i = kernels.index((name, grid))
+        assert e["dispatches"] == 3
+        assert e["read_bytes"] == round((1000.0 + i) * 1024 * 2) and e["write_bytes"] == round((10.0 + i) * 1024)
+        assert e["traffic_bytes"] == e["read_bytes"] + e["write_bytes"]
+        assert e["mfma_busy_cycles_per_simd"] == 768 and e["mfma_i8_ops"] == 1024
+        assert e["valu_instructions_per_simd"] == 100
+    monkeypatch.setattr(bench, "COUNTER_FILE", out)
+    key = "c4_prefill_M256_K1024_N3072"
+    res = {key: {"bytes_per_call": 2_000_000, "us_per_call": 1.0},
+           "c1_gemv_qwen3_gate_M1_K1024_N3072": {"bytes_per_call": 123, "us_per_call": 1.0}}
+    bench.attach_counters(res)
+    c = res[key]["counters"]
+    assert c["mfma_busy_frac"] == round(768 / 2400, 4) and c["valu_issue_frac"] == round(400 / 2400, 4)
+    assert "counters" not in res["c1_gemv_qwen3_gate_M1_K1024_N3072"]     # other bytes: a stale entry
+
+
+def test_pmc_summary_refuses_a_missing_kernel(bench, tmp_path):
+    paths = []
+    for i, c in enumerate(("FETCH_SIZE", "WRITE_SIZE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU")):
+        p = tmp_path / f"only_copy{i}.csv"
+        write_pass(p, [c], {}, {c: 131072.0})
+        paths.append(str(p))
+    detail = tmp_path / "detail.json"
+    detail.write_text(json.dumps({"configs": {}}))
+    with pytest.raises(SystemExit, match="0 kernels match"):
+        bench.pmc_summary(paths, str(detail), str(tmp_path / "o.json"))
