@@ -819,7 +819,9 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
         torch.cuda.empty_cache()
     if attention:
         res["attention_decode_qwen3_t250"] = attention_decode(torch, lib, gen)
-        log(f"attention t=250: {res['attention_decode_qwen3_t250']['op_by_op']['us_per_layer']} us per layer")
+        ad = res["attention_decode_qwen3_t250"]
+        log(f"attention t=250: {ad['op_by_op']['us_per_layer']} us per layer op by op, "
+            f"{ad['fused_op']['us_per_layer']} us fused")
     attach_counters(res)
     return res
 
@@ -875,7 +877,26 @@ def attention_decode(torch, lib, gen, t0: int = 250) -> dict:
                       "us_per_token": round(t * 1e6, 1), "GBps": round(nbytes * len(layers) / t / 1e9, 1)},
          "t0": t0, "heads": QWEN3_HEADS, "kv_heads": QWEN3_KV_HEADS, "head_dim": QWEN3_HEAD_DIM,
          "layers": QWEN3_LAYERS, "cache_bytes_per_layer": nbytes}
-    del layers, keep, launches
+    # the fused attention op (tars_attention): one call per layer for its 16 heads over the same
+    # buffers (the split form: a scores launch and a softmax + P V launch)
+    nh, nkv, hd = QWEN3_HEADS, QWEN3_KV_HEADS, QWEN3_HEAD_DIM
+    nk = (t0 + 1 + 15) // 16 * 16
+    ops_l = []
+    for kc, vc, q, sc, pr, att in keep:
+        arr = lambda vals: (ctypes.c_void_p * nh)(*vals)
+        grp = nh // nkv
+        ptrs = (arr([q.data_ptr() + 4 * h * hd for h in range(nh)]), arr([kc.data_ptr() + 4 * (h // grp) * hd for h in range(nh)]),
+                arr([vc.data_ptr() + 4 * (h // grp) * hd for h in range(nh)]), arr([att.data_ptr() + 4 * h * hd for h in range(nh)]))
+        ops_l.append(Launch("attention", lib.tars_attention,
+                            (ptrs[0], 4 * nh * hd, ptrs[1], 4 * nkv * hd, ptrs[2], 4 * nkv * hd, 0, ptrs[3], 4 * nh * hd, 0, 0,
+                             sc.data_ptr(), 4 * nk, pr.data_ptr(), 4 * nk, nh, 1, nk, hd, t0 + 1), nbytes, 0, "attention",
+                            {"ptrs": ptrs}))
+    g = capture(torch, ops_l)
+    t = time_graph(torch, g, reps=50, warmup=3)
+    del g
+    r["fused_op"] = {"calls_per_token": len(ops_l), "us_per_layer": round(t / len(ops_l) * 1e6, 2),
+                     "us_per_token": round(t * 1e6, 1), "GBps": round(nbytes * len(ops_l) / t / 1e9, 1)}
+    del layers, keep, launches, ops_l
     torch.cuda.empty_cache()
     r["executor"] = attention_queue(torch, lib, gen, t0)
     return r
@@ -940,7 +961,8 @@ def attention_queue(torch, lib, gen, t0: int) -> dict:
         finally:
             lib.tars_set_queue_fusion(prev_f)
             lib.tars_set_queue_graphs(prev_g)
-        res[key] = {"launches_per_token": QWEN3_LAYERS if fusion else len(descs), "us_per_token": round(t * 1e6, 1),
+        # a fused layer is one tars_attention launch group: two kernels in the split form
+        res[key] = {"launches_per_token": 2 * QWEN3_LAYERS if fusion else len(descs), "us_per_token": round(t * 1e6, 1),
                     "us_per_layer": round(t / QWEN3_LAYERS * 1e6, 2)}
     del image
     torch.cuda.empty_cache()

@@ -243,6 +243,32 @@ int tars_fdot(const float* A, int64_t lda, const void* B, int64_t ldb, int32_t n
               void* Y, int64_t ldy, int32_t out, uint32_t out_scale_bits, int32_t M, int32_t N,
               int32_t K, void* stream);
 
+/*
+ * Attention of `heads` query heads in one call: per head h the triple the reference lowers
+ * attention to (tars_mini/llm.py:736-746), FDOT_NT of q[h]'s rows with the K rows (the scores,
+ * Machine._fdot, golden.py:426-436), ROW_SOFTMAX with the causal rule (Machine._row,
+ * golden.py:358-380), FDOT_NN of the probabilities with the V rows into att[h]. Every output bit
+ * is what the three ops leave run head after head: att[h] for every head, and the shared score
+ * rows sc and probability rows pr holding the last head's (either may be NULL to skip it).
+ *   q, k, v, att: HOST arrays of `heads` device pointers. q[h] fp32 [M, hd] at ldq; k[h] fp32
+ *   [nk, hd] at ldk; v[h] [nk, hd] at ldv, fp32 or binary16 (v_fp16); att[h] [M, hd] at ldatt
+ *   in format out (FP32, BF16, or INT8 with out_scale_bits); sc, pr fp32 [M, nk] at ldsc / ldpr.
+ *   causal_k > 0: query row m sees its first min(nk, causal_k + m) keys (the descriptor's K
+ *   rule); 0: all nk. hd 64, 128 or 256; 1 <= nk <= 4080; 1 <= heads <= 32; M >= 1; pointers
+ *   and strides (0 = dense) multiples of 16 bytes. No output may overlap another output or any
+ *   head's q, K or V rows (the heads run concurrently): TARS_E_OVERLAP.
+ * Consecutive heads with equal k and v pointers (2 or 4 query heads per K / V head) are run
+ * together. When such a group has at most 4 query rows in all (heads in the group times M) and
+ * the scores fit, the work is split over many workgroups through a 1 MiB device scratch buffer
+ * that the library allocates on the device at its first use there and keeps until the process
+ * ends (calls that overlap in time on one device race on it); otherwise, or while the stream is
+ * capturing a graph before that first use, one workgroup per head. The bits are the same.
+ */
+int tars_attention(const float* const* q, int64_t ldq, const float* const* k, int64_t ldk,
+                   const void* const* v, int64_t ldv, int32_t v_fp16, void* const* att, int64_t ldatt,
+                   int32_t out, uint32_t out_scale_bits, float* sc, int64_t ldsc, float* pr, int64_t ldpr,
+                   int32_t heads, int32_t M, int32_t nk, int32_t hd, int32_t causal_k, void* stream);
+
 /* Library version string ("opentars_amd <semver> gfx950"). Host only, never fails. */
 const char* tars_version(void);
 

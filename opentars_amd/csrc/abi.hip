@@ -387,6 +387,86 @@ bool stride_ok(int64_t& ld, int64_t row_bytes, int elem) {
   return ld >= row_bytes && ld % elem == 0;
 }
 
+// Whether the spans (any order) are pairwise disjoint; sorts them by start.
+bool disjoint(std::vector<Span>& v) {
+  std::sort(v.begin(), v.end(), [](const Span& x, const Span& y) { return x.lo < y.lo; });
+  for (size_t i = 1; i < v.size(); ++i)
+    if (v[i].lo < v[i - 1].hi) return false;
+  return true;
+}
+
+// The checks of tars_attention, in the order of the other entry points (NULLs, fields, shapes and
+// alignment, extents, overlaps), and its kernel arguments.
+int attention_args(const float* const* q, int64_t ldq, const float* const* k, int64_t ldk, const void* const* v,
+                   int64_t ldv, int32_t v_fp16, void* const* att, int64_t ldatt, int32_t out, uint32_t out_scale_bits,
+                   float* sc, int64_t ldsc, float* pr, int64_t ldpr, int32_t heads, int32_t M, int32_t nk, int32_t hd,
+                   int32_t causal_k, tars::AttnArgs& a) {
+  g_last_error.clear();
+  if (!q || !k || !v || !att) return fail(TARS_E_ARG, "NULL pointer array");
+  if (heads < 1 || heads > tars::kAttnMaxHeads) return fail(TARS_E_ARG, "heads must be 1..32");
+  for (int32_t h = 0; h < heads; ++h)
+    if (!q[h] || !k[h] || !v[h] || !att[h]) return fail(TARS_E_ARG, "NULL pointer");
+  if (v_fp16 != 0 && v_fp16 != 1) return fail(TARS_E_FIELD, "v_fp16 is 0 or 1");
+  if (int rc = check_out(out, out_scale_bits, false)) return rc;
+  if (causal_k < 0) return fail(TARS_E_FIELD, "causal_k >= 0");
+  if (M < 1 || nk < 1) return fail(TARS_E_ALIGN, "M, nk >= 1");
+  if (!tars::attention_supported(hd, nk)) return fail(TARS_E_ARG, "head size 64, 128 or 256 and at most 4080 keys");
+  const int ve = v_fp16 ? 2 : 4, oe = esize(out);
+  const int64_t qrow = 4LL * hd, vrow = static_cast<int64_t>(ve) * hd, arow = static_cast<int64_t>(oe) * hd,
+                srow = 4LL * nk;
+  if (!stride_ok(ldq, qrow, 16) || !stride_ok(ldk, qrow, 16) || !stride_ok(ldv, vrow, 16) ||
+      !stride_ok(ldatt, arow, 16) || !stride_ok(ldsc, srow, 16) || !stride_ok(ldpr, srow, 16))
+    return fail(TARS_E_ALIGN, "strides must hold a row and be multiples of 16 bytes");
+  if (!aligned(sc, 16) || !aligned(pr, 16)) return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+  std::vector<Span> ins, outs;
+  for (int32_t h = 0; h < heads; ++h) {
+    if (!aligned(q[h], 16) || !aligned(k[h], 16) || !aligned(v[h], 16) || !aligned(att[h], 16))
+      return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+    if (!extent_ok(q[h], ldq, M, qrow) || !extent_ok(k[h], ldk, nk, qrow) || !extent_ok(v[h], ldv, nk, vrow) ||
+        !extent_ok(att[h], ldatt, M, arow))
+      return fail(TARS_E_RANGE, "extent overflows");
+    auto add = [](std::vector<Span>& to, std::vector<Span> from) { to.insert(to.end(), from.begin(), from.end()); };
+    add(ins, rows(q[h], ldq, M, qrow));
+    if (h == 0 || k[h] != k[h - 1]) add(ins, rows(k[h], ldk, nk, qrow));  // heads sharing K / V: their rows once
+    if (h == 0 || v[h] != v[h - 1]) add(ins, rows(v[h], ldv, nk, vrow));
+    add(outs, rows(att[h], ldatt, M, arow));
+  }
+  if ((sc && !extent_ok(sc, ldsc, M, srow)) || (pr && !extent_ok(pr, ldpr, M, srow)))
+    return fail(TARS_E_RANGE, "extent overflows");
+  if (sc) {
+    const auto r = rows(sc, ldsc, M, srow);
+    outs.insert(outs.end(), r.begin(), r.end());
+  }
+  if (pr) {
+    const auto r = rows(pr, ldpr, M, srow);
+    outs.insert(outs.end(), r.begin(), r.end());
+  }
+  if (!disjoint(outs) || overlaps(ins, outs)) return fail(TARS_E_OVERLAP, "an output overlaps another output or an input");
+  for (int32_t h = 0; h < heads; ++h) {
+    a.q[h] = q[h];
+    a.k[h] = k[h];
+    a.v[h] = v[h];
+    a.att[h] = att[h];
+  }
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.ldv = ldv;
+  a.ldatt = ldatt;
+  a.sc = sc;
+  a.ldsc = ldsc;
+  a.pr = pr;
+  a.ldpr = ldpr;
+  a.heads = heads;
+  a.M = M;
+  a.nk = nk;
+  a.hd = hd;
+  a.causal_k = causal_k;
+  a.v_fp16 = v_fp16;
+  a.out = out;
+  a.out_scale = f32_of(out_scale_bits);
+  return TARS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -514,6 +594,20 @@ int tars_fdot(const float* A, int64_t lda, const void* B, int64_t ldb, int32_t n
     return fail(TARS_E_OVERLAP, "the output overlaps an input");
   tars::FdotArgs a{A, lda, B, ldb, nn, b_fp16, Y, ldy, out, f32_of(out_scale_bits), M, N, K};
   return launched(tars::launch_fdot(a, static_cast<hipStream_t>(stream)));
+}
+
+int tars_attention(const float* const* q, int64_t ldq, const float* const* k, int64_t ldk, const void* const* v,
+                   int64_t ldv, int32_t v_fp16, void* const* att, int64_t ldatt, int32_t out, uint32_t out_scale_bits,
+                   float* sc, int64_t ldsc, float* pr, int64_t ldpr, int32_t heads, int32_t M, int32_t nk, int32_t hd,
+                   int32_t causal_k, void* stream) {
+  tars::AttnArgs a{};
+  if (int rc = attention_args(q, ldq, k, ldk, v, ldv, v_fp16, att, ldatt, out, out_scale_bits, sc, ldsc, pr, ldpr, heads,
+                              M, nk, hd, causal_k, a))
+    return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  a.scratch = tars::attention_workspace(s);
+  a.scratch_floats = a.scratch ? tars::kAttnScratchFloats : 0;
+  return launched(tars::launch_attention(a, s));
 }
 
 int tars_embed_rows(const uint16_t* table, int64_t ld_table, int64_t table_rows, int32_t cols, const int32_t* ids,

@@ -66,6 +66,12 @@ constexpr uint32_t kSubKeyTiny = ((27u << 23) << 1) - 1u;
 __device__ __forceinline__ uint32_t min_key(uint32_t m, float a, float b) {
   return min(m, min(sub_key(a), sub_key(b)));
 }
+// The same test kept as the minimum magnitude (fminf: NaN ignored, one three-way minimum with
+// absolute-value operands per two values): a chain is recomputed when it falls below kTiny. An
+// exact zero also sends it there (the same bits, more time), so this form suits chains whose
+// partial sums are rarely exactly zero.
+constexpr float kTiny = 0x1p-100f;
+__device__ __forceinline__ float min_mag(float m, float a, float b) { return fminf(m, fminf(fabsf(a), fabsf(b))); }
 
 // numerics.py:50-52: int32 -> fp32 round-to-nearest-even (v_cvt_f32_i32)
 __device__ __forceinline__ float i2f(int32_t i) { return static_cast<float>(i); }
@@ -121,21 +127,37 @@ __device__ __forceinline__ float recip_f(float x) {
 }
 
 // e^x (numerics.py:135-150).
+//
+// After the input flush and the NaN test the contract's flush/canonicalize wrappers change no
+// step, so the raw round-to-nearest-even operations give the same bits with a much shorter
+// dependent chain. For finite x (zero or normal): x * log2e is 0 or normal (log2e > 1); n is an
+// integer in [-200, 200]; n * -ln2_hi is 0 or at least 0.69 in magnitude, and exact (ln2_hi has
+// 14 fraction bits); n * -ln2_lo is +-0 or at least 1.4e-6 in magnitude. With n = 0, r = x. Else
+// x + n * -ln2_hi is a multiple of 2^-25 (|x| >= 0.34 then, and n * ln2_hi a multiple of 2^-14),
+// so 0 or normal, and adding n * -ln2_lo (a multiple of 2^-43 below 2^-11 in magnitude) leaves 0
+// or a normal value. For -104 < x < 89 (n unclamped, |r| <= 0.35) every partial value of the
+// polynomial lies in [0.0078, 1.5], and a product p * r is normal except when n = 0 and
+// |x| < 2^-116, where it may be subnormal: the contract flushes it to 0 and adds a coefficient of
+// at least 1/120, whose half ulp (>= 2^-31) the unflushed product cannot reach, so both sums round
+// to that coefficient. Other x take their result from the range tests; on the way their steps
+// stay free of NaN (r and the coefficients are finite unless x is infinite, and then no product
+// pairs an infinity with a zero and no sum pairs opposite infinities). No NaN arises, so the result
+// needs no canonicalization.
 __device__ __forceinline__ float exp_f(float x) {
   x = ftz(x);
   if (is_nan(x)) return ffrom(kCanonNaN);
-  float n = rintf(fmul(x, ffrom(kLog2e)));
+  float n = rintf(__fmul_rn(x, ffrom(kLog2e)));
   n = fminf(fmaxf(n, -200.0f), 200.0f);
-  const float r = fadd(fadd(x, fmul(n, ffrom(kNegLn2Hi))), fmul(n, ffrom(kNegLn2Lo)));
+  const float r = __fadd_rn(__fadd_rn(x, __fmul_rn(n, ffrom(kNegLn2Hi))), __fmul_rn(n, ffrom(kNegLn2Lo)));
   const uint32_t coeffs[6] = {0x3C088889u, 0x3D2AAAABu, 0x3E2AAAABu, 0x3F000000u, 0x3F800000u,
                               0x3F800000u};
   float p = ffrom(0x3AB60B61u);
 #pragma unroll
-  for (int i = 0; i < 6; ++i) p = fadd(fmul(p, r), ffrom(coeffs[i]));
+  for (int i = 0; i < 6; ++i) p = __fadd_rn(__fmul_rn(p, r), ffrom(coeffs[i]));
   float y = add_to_exponent(p, static_cast<int>(n));
   if (x >= ffrom(kExpHi)) y = ffrom(kExpo);
   else if (x <= ffrom(kExpLo)) y = 0.0f;
-  return canon(y);
+  return y;
 }
 
 __device__ __forceinline__ float relu_plain(float x) { return x > 0.0f ? x : 0.0f; }

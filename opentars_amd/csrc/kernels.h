@@ -252,8 +252,25 @@ struct AttnArgs {
   int64_t ldpr;
   int heads, M, nk, hd, causal_k, v_fp16, out;
   float out_scale;
+  // The split form (two launches over many workgroups) when scratch is not null and the shape fits
+  // (attention_split_fits); otherwise one workgroup per head. scratch: device memory of
+  // scratch_floats floats holding the scores of every head and query row between the launches.
+  float* scratch;
+  int64_t scratch_floats;
+  // set by launch_attention for the split kernels: scratch row stride (floats), query heads per
+  // K / V head group, keys per scores workgroup
+  int64_t ld_scratch;
+  int group, keys_per_wg;
 };
 bool attention_supported(int hd, int nk);
+// Split form limits: query rows per head group (heads sharing K / V times M) and probabilities a
+// P V workgroup holds in LDS; output columns per P V workgroup.
+constexpr int kAttnSplitMaxQ = 4, kAttnSplitProbs = 4096, kAttnSplitCols = 32;
+bool attention_split_fits(int heads, int M, int nk, int64_t scratch_floats);
+// The split form's scratch on the current device: kAttnScratchFloats floats allocated at the first
+// call there (not while `s` is capturing a graph) and kept until the process ends; null when none.
+constexpr int64_t kAttnScratchFloats = int64_t{1} << 18;
+float* attention_workspace(hipStream_t s);
 
 // Embedding rows: dst row i = fp32(table row ids[i]) (times the fp32 scale when scaled).
 constexpr int kEmbedMaxIds = 64;

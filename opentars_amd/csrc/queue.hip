@@ -640,7 +640,9 @@ tars::AttnArgs attention_args(uint8_t* image, const std::vector<AttnHead>& heads
 }
 
 int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, hipStream_t s) {
-  const tars::AttnArgs a = attention_args(image, heads);
+  tars::AttnArgs a = attention_args(image, heads);
+  a.scratch = tars::attention_workspace(s);  // the split form's scores, when the device has its scratch
+  a.scratch_floats = a.scratch ? tars::kAttnScratchFloats : 0;
   const hipError_t e = tars::launch_attention(a, s);
   if (e != hipSuccess) {
     tars::set_last_error(std::string("HIP launch failed: ") + hipGetErrorString(e));

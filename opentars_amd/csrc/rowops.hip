@@ -14,6 +14,7 @@
 //    per output with the k loop unrolled and its loads issued ahead.
 // Everything else is elementwise. All of these ops are latency-bound at decode sizes (a few
 // thousand elements, tens of dependent steps per lane).
+#include <mutex>
 #include <type_traits>
 
 #include "kernels.h"
@@ -76,14 +77,16 @@ __device__ __forceinline__ void for_lane(const float* x, int l, int n, Fn&& f) {
   }
 }
 
-// The 16-lane chains of sum16 over v[0..n) in LDS, of the values (SQUARE: of fmul(v, v)): lane l
-// of the first 16 threads adds element l, l + 16, ... in order from +0, then the pairwise fold;
-// every thread of the workgroup receives the sum through LDS. v must hold contract results.
+// The 16-lane chains of sum16 over rows of n values in LDS (row i at v + i * ld), of the values
+// (SQUARE: of fmul(v, v)): lane l of threads 16 i .. 16 i + 15 adds element l, l + 16, ... of row i
+// in order from +0, then the pairwise fold; row i's sum lands in bcast[i] for every thread of the
+// workgroup. v must hold contract results.
 template <bool SQUARE>
-__device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) {
+__device__ __forceinline__ void lds_sum16_rows(const float* v, int ld, int rows, int n, float* bcast) {
   __syncthreads();  // v complete
-  if (threadIdx.x < 16) {
-    const int l = threadIdx.x;
+  if (static_cast<int>(threadIdx.x) < 16 * rows) {
+    const int l = threadIdx.x & 15, i = threadIdx.x >> 4;
+    v += i * ld;
     // the chain unflushed with its partial sums checked (its terms are flushed contract results),
     // then with the flushes when one was subnormal
     auto chain = [&](auto flushed) {
@@ -111,9 +114,15 @@ __device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) 
     float acc = chain(std::false_type{});
     if (__builtin_expect(is_nan(acc), 0)) acc = chain(std::true_type{});
     acc = fold16(acc);
-    if (l == 0) *bcast = acc;
+    if (l == 0) bcast[i] = acc;
   }
   __syncthreads();
+}
+
+// The sum16 of v[0..n) in LDS (as lds_sum16_rows for one row), returned to every thread.
+template <bool SQUARE>
+__device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) {
+  lds_sum16_rows<SQUARE>(v, 0, 1, n, bcast);
   return *bcast;
 }
 
@@ -617,11 +626,20 @@ __global__ __launch_bounds__(256) void fdot_nn_kernel(FdotArgs a) {
 }
 
 // ------------------------------------------------------------------------------ fused decode attention
-// One workgroup per query head: (1) the scores s[j] = sum16_k q[k] K[j][k] for every key (16-lane
-// groups, 16 keys per group (8 at head size 256 or up to 128 keys, 4 up to 64) with their K rows loaded together and their chains
-// interleaved), kept in LDS; (2) the causal softmax over them in place (as row_lds_kernel); (3) the
-// P V chains over V staged in LDS by direct global -> LDS loads in a ring of kAttnSlots stages,
-// the first kAttnSlots - 1 of them issued before the scores so that they land while (1) and (2) run.
+// The per-head triple FDOT_NT (scores) -> ROW_SOFTMAX (causal) -> FDOT_NN (P V) of the reference's
+// attention lowering, in two forms with the same bits:
+//  * one workgroup per query head (attn_kernel): (1) the scores s[j] = sum16_k q[k] K[j][k] for
+//    every key (16-lane groups, 16 keys per group (8 at head size 256 or up to 128 keys, 4 up to
+//    64) with their K rows loaded together and their chains interleaved), kept in LDS; (2) the
+//    causal softmax over them in place (as row_lds_kernel); (3) the P V chains over V staged in LDS
+//    by direct global -> LDS loads in a ring of kAttnSlots stages, the first kAttnSlots - 1 of them
+//    issued before the scores so that they land while (1) and (2) run.
+//  * split over workgroups (attn_split_scores_kernel, then attn_split_pv_kernel): the scores of a
+//    group of query heads that share one K / V head, one chunk of keys per workgroup, into a
+//    scratch row per head and query row; then per 32 output columns a workgroup that recomputes
+//    every query's softmax from those rows (each workgroup the same values) and runs the P V
+//    chains of its columns. One workgroup per head reads all of that head's K and V through one
+//    CU; the split spreads them over many.
 // Each step is the contract's, in the same order as the three separate ops, so every value is the
 // same bit for bit; the last head also writes its scores and probabilities where the reference's
 // ops leave them.
@@ -640,14 +658,46 @@ __device__ __forceinline__ void ring_load16(const void* src, uint32_t dst) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(dst) : "memory");
 }
 
+// The score chains of Q query rows qv against KF keys whose K elements (this lane's U of each row)
+// are in kv, unflushed (qv is flushed) and checked; recomputed with the contract's flushes when a
+// key element or a partial sum lies in (0, 2^-100) in magnitude (a subnormal product is then
+// absorbed by its partial sum or shows in it, see kSubKeyTiny). acc receives the lane's chains.
+template <int U, int KF, int Q>
+__device__ __forceinline__ void score_chains(const float (&qv)[Q][U], const float (&kv)[KF][U], float (&acc)[Q][KF]) {
+  uint32_t mk = ~0u;
+#pragma unroll
+  for (int i = 0; i < Q; ++i)
+#pragma unroll
+    for (int c = 0; c < KF; ++c) acc[i][c] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < Q; ++i)
+#pragma unroll
+      for (int c = 0; c < KF; ++c) {
+        const float pr = __fmul_rn(qv[i][u], kv[c][u]);
+        acc[i][c] = __fadd_rn(acc[i][c], pr);
+        mk = min_key(mk, kv[c][u], acc[i][c]);
+      }
+  if (__builtin_expect(mk < kSubKeyTiny, 0)) {
+#pragma unroll
+    for (int i = 0; i < Q; ++i)
+#pragma unroll
+      for (int c = 0; c < KF; ++c) acc[i][c] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < Q; ++i)
+#pragma unroll
+        for (int c = 0; c < KF; ++c) acc[i][c] = fadd_chain(acc[i][c], fmul(qv[i][u], kv[c][u]));
+  }
+}
+
 // The scores of query row m of head h: 16-lane group g takes keys g, g + 16, ..., KF of them per
-// pass with their K rows loaded together and their chains interleaved. The chains run unflushed
-// (qv is flushed) and are checked; a pass is recomputed with the contract's flushes when a key
-// element or a partial sum lies in (0, 2^-100) in magnitude (a subnormal product is then absorbed
-// by its partial sum or shows in it, see kSubKeyTiny).
+// pass with their K rows loaded together and their chains interleaved.
 template <int U, int KF>
 __device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int g, int l, bool last,
-                                            const float (&qv)[U], float* sp) {
+                                            const float (&qv)[1][U], float* sp) {
   const int nk = a.nk;
   for (int j0 = g; j0 < nk; j0 += 16 * KF) {
     float kv[KF][U];
@@ -658,29 +708,11 @@ __device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int
 #pragma unroll
       for (int u = 0; u < U; ++u) kv[c][u] = kr[l + 16 * u];
     }
-    float acc[KF];
-    uint32_t mk = ~0u;
-#pragma unroll
-    for (int c = 0; c < KF; ++c) acc[c] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int c = 0; c < KF; ++c) {
-        const float pr = __fmul_rn(qv[u], kv[c][u]);
-        acc[c] = __fadd_rn(acc[c], pr);
-        mk = min_key(mk, kv[c][u], acc[c]);
-      }
-    if (__builtin_expect(mk < kSubKeyTiny, 0)) {
-#pragma unroll
-      for (int c = 0; c < KF; ++c) acc[c] = 0.0f;
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int c = 0; c < KF; ++c) acc[c] = fadd_chain(acc[c], fmul(qv[u], kv[c][u]));
-    }
+    float acc[1][KF];
+    score_chains<U, KF, 1>(qv, kv, acc);
 #pragma unroll
     for (int c = 0; c < KF; ++c) {
-      const float sv = fold16(acc[c]);
+      const float sv = fold16(acc[0][c]);
       const int j = j0 + 16 * c;
       if (l == 0 && j < nk) {
         sp[j] = sv;
@@ -688,6 +720,113 @@ __device__ __forceinline__ void attn_scores(const AttnArgs& a, int h, int m, int
       }
     }
   }
+}
+
+// The causal softmax (ROW_SOFTMAX with V of the nk values valid) of sp[0..nk) in place, by the
+// whole workgroup: the fmax over the valid scores (order-free: an unsigned key, NaN beside it),
+// exp_f of each difference (0 past V), the 16-lane sum, recip_f, the products. When pr is not null
+// the probabilities are also stored there (fp32 row at byte offset off). Returns whether one of
+// this thread's probabilities is above 1 or NaN.
+__device__ __forceinline__ int softmax_lds(float* sp, int nk, int V, float* pr, int64_t off, uint32_t* red,
+                                           float* bcast) {
+  const int t = threadIdx.x, lane = t & 63;
+  __syncthreads();  // sp complete
+  uint32_t key = 0;
+  int nan = 0;
+  for (int j = t; j < V; j += 256) {
+    if (is_nan(sp[j])) nan = 1;
+    else key = max(key, fmax_key(sp[j]));
+  }
+  key = static_cast<uint32_t>(group_reduce<64>(static_cast<int>(key), OpMaxU{}));
+  nan = group_reduce<64>(nan, OpOr{});
+  if (lane == 0) red[t >> 6] = nan ? 0xFFFFFFFFu : key;
+  __syncthreads();
+  const uint32_t k4 = max(max(red[0], red[1]), max(red[2], red[3]));
+  const float nmx = fneg(k4 == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k4));
+  __syncthreads();
+  for (int j = t; j < nk; j += 256) sp[j] = j < V ? exp_f(fadd(sp[j], nmx)) : 0.0f;
+  const float r = recip_f(lds_sum16<false>(sp, nk, bcast));
+  int above1 = 0;
+  for (int j = t; j < nk; j += 256) {
+    const float p = fmul(sp[j], r);
+    sp[j] = p;
+    above1 |= !(p <= 1.0f);
+    if (pr) store_out(pr, off, j, 0, p, 0.0f);
+  }
+  return above1;
+}
+
+// One ring stage's P V chain steps for output column d: the stage's rows (ROWB bytes apart in the
+// slot, rows of them) times the probabilities ps[0..rows), added to acc in key order. The steps run
+// unflushed and checked (a probability is an fmul output: flushed, so only V (when vtest), the
+// stage's first value and the partial sums are tested, the products' flushes being absorbed, see
+// kSubKeyTiny); recomputed from the stage's first value with the contract's flushes when one lies
+// in (0, 2^-100) in magnitude.
+template <bool VHALF, int SR, int ROWB>
+__device__ __forceinline__ float pv_stage(float acc, const int8_t* slot, int d, const float* ps, int rows, bool vtest) {
+  auto vval = [&](int rr) {
+    return VHALF ? from_fp16_bits(reinterpret_cast<const uint16_t*>(slot + rr * ROWB)[d])
+                 : reinterpret_cast<const float*>(slot + rr * ROWB)[d];
+  };
+  const float acc0 = acc;
+  float mn = acc0 == 0.0f ? __builtin_inff() : fabsf(acc0);
+  constexpr int RB = SR < 16 ? SR : 16;  // keys per block
+  static_assert(RB % 4 == 0, "probabilities are read 4 at a time");
+  const int nb = rows / RB;
+  int rr = 0;
+  // Blocks of RB keys in two register sets: block b + 1's LDS reads are issued before block b's
+  // products and chain steps, so they are in flight while block b runs.
+  auto blocks = [&](auto vt) {
+    float va[RB], pa[RB], vb[RB], pb[RB];
+    auto load = [&](float (&v)[RB], float (&p)[RB], int b) {
+#pragma unroll
+      for (int u = 0; u < RB; ++u) v[u] = vval(b * RB + u);
+#pragma unroll
+      for (int u = 0; u < RB; u += 4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(ps + b * RB + u);  // 16-byte aligned: SR, RB, ldp multiples of 4
+        p[u] = q4.x;
+        p[u + 1] = q4.y;
+        p[u + 2] = q4.z;
+        p[u + 3] = q4.w;
+      }
+    };
+    auto run = [&](const float (&v)[RB], const float (&p)[RB]) {
+      float pv[RB], sums[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) pv[u] = __fmul_rn(p[u], v[u]);
+      if constexpr (decltype(vt)::value) {
+#pragma unroll
+        for (int u = 0; u < RB; u += 2) mn = min_mag(mn, v[u], v[u + 1]);
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) sums[u] = acc = __fadd_rn(acc, pv[u]);
+#pragma unroll
+      for (int u = 0; u < RB; u += 2) mn = min_mag(mn, sums[u], sums[u + 1]);
+    };
+    // (the read of block b + 2 is unconditional: past the last block it reads the last one again)
+    if (nb > 0) load(va, pa, 0);
+    int b = 0;
+    for (; b + 1 < nb; b += 2) {
+      load(vb, pb, b + 1);
+      run(va, pa);
+      load(va, pa, min(b + 2, nb - 1));
+      run(vb, pb);
+    }
+    if (b < nb) run(va, pa);
+    rr = nb * RB;
+  };
+  if (vtest) blocks(std::true_type{});
+  else blocks(std::false_type{});
+  for (; rr < rows; ++rr) {
+    const float v = vval(rr), pr = __fmul_rn(ps[rr], v);
+    acc = __fadd_rn(acc, pr);
+    mn = min_mag(mn, v, acc);
+  }
+  if (__builtin_expect(mn < kTiny, 0)) {
+    acc = acc0;
+    for (rr = 0; rr < rows; ++rr) acc = fadd_chain(acc, fmul(ps[rr], vval(rr)));
+  }
+  return acc;
 }
 
 template <int HD, bool VHALF>
@@ -728,37 +867,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       if (st < NS) issue(st);
     // (1) scores
     const float* qr = frow(a.q[h], a.ldq, m);
-    float qv[U];
+    float qv[1][U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) qv[u] = ftz(qr[l + 16 * u]);
+    for (int u = 0; u < U; ++u) qv[0][u] = ftz(qr[l + 16 * u]);
     if (nk <= 64) attn_scores<U, 4>(a, h, m, g, l, last, qv, sp);
     else if (nk <= 128) attn_scores<U, 8>(a, h, m, g, l, last, qv, sp);
     else attn_scores<U, KF>(a, h, m, g, l, last, qv, sp);
     // (2) causal softmax in place
     const int V = a.causal_k > 0 ? min(nk, a.causal_k + m) : nk;
-    __syncthreads();
-    uint32_t key = 0;
-    int nan = 0;
-    for (int j = t; j < V; j += 256) {
-      if (is_nan(sp[j])) nan = 1;
-      else key = max(key, fmax_key(sp[j]));
-    }
-    key = static_cast<uint32_t>(group_reduce<64>(static_cast<int>(key), OpMaxU{}));
-    nan = group_reduce<64>(nan, OpOr{});
-    if (lane == 0) red[t >> 6] = nan ? 0xFFFFFFFFu : key;
-    __syncthreads();
-    const uint32_t k4 = max(max(red[0], red[1]), max(red[2], red[3]));
-    const float nmx = fneg(k4 == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k4));
-    __syncthreads();
-    for (int j = t; j < nk; j += 256) sp[j] = j < V ? exp_f(fadd(sp[j], nmx)) : 0.0f;
-    const float r = recip_f(lds_sum16<false>(sp, nk, &bcast));
-    int above1 = 0;  // a probability above 1 or NaN
-    for (int j = t; j < nk; j += 256) {
-      const float p = fmul(sp[j], r);
-      sp[j] = p;
-      above1 |= !(p <= 1.0f);
-      if (last && a.pr) store_out(a.pr, m * a.ldpr, j, 0, p, 0.0f);
-    }
+    const int above1 = softmax_lds(sp, nk, V, last ? a.pr : nullptr, m * a.ldpr, red, &bcast);
     wait_vmcnt<0>();  // the first V stages have landed; nothing else outstanding before the ring's counts
     // V elements need their own test only when fp32 and some probability is above 1 or NaN: with
     // every p <= 1, a subnormal V element gives |p v| < 2^-126, a subnormal product (tested) or
@@ -771,55 +888,191 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       wait_stages_ahead<L, kAttnSlots - 1>(min(NS - 1 - st, kAttnSlots - 1));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the slot's reads stay after the barrier
-      if (t < HD) {
-        const int8_t* slot = ring + kAttnStageBytes * (st % kAttnSlots);
-        const float* ps = sp + st * SR;
-        const int rows = min(SR, nk - st * SR);
-        auto vval = [&](int rr) {
-          return VHALF ? from_fp16_bits(reinterpret_cast<const uint16_t*>(slot + rr * ROWB)[t])
-                       : reinterpret_cast<const float*>(slot + rr * ROWB)[t];
-        };
-        // The stage's chain steps unflushed, checked (a probability is an fmul output: flushed,
-        // so only V (when vtest), the stage's first value and the partial sums are tested, the
-        // products' flushes being absorbed, see kSubKeyTiny); recomputed from the stage's first
-        // value with the contract's flushes when one lies in (0, 2^-100) in magnitude.
-        const float acc0 = acc;
-        uint32_t mk = sub_key(acc0);
-        int rr = 0;
-        auto blocks = [&](auto vt) {
-          constexpr int RB = SR < 16 ? SR : 16;
-          for (; rr + RB <= rows; rr += RB) {  // the block's LDS reads and products first, then its chain steps
-            float pv[RB], sums[RB];
-#pragma unroll
-            for (int u = 0; u < RB; ++u) {
-              const float v = vval(rr + u);
-              pv[u] = __fmul_rn(ps[rr + u], v);
-              if constexpr (decltype(vt)::value) mk = min_key(mk, v, v);
-            }
-#pragma unroll
-            for (int u = 0; u < RB; ++u) sums[u] = acc = __fadd_rn(acc, pv[u]);
-#pragma unroll
-            for (int u = 0; u < RB; u += 2) mk = min_key(mk, sums[u], sums[u + 1]);
-          }
-        };
-        if (vtest) blocks(std::true_type{});
-        else blocks(std::false_type{});
-        for (; rr < rows; ++rr) {
-          const float v = vval(rr), pr = __fmul_rn(ps[rr], v);
-          acc = __fadd_rn(acc, pr);
-          mk = min_key(mk, v, acc);
-        }
-        if (__builtin_expect(mk < kSubKeyTiny, 0)) {
-          acc = acc0;
-          for (rr = 0; rr < rows; ++rr) acc = fadd_chain(acc, fmul(ps[rr], vval(rr)));
-        }
-      }
+      if (t < HD)
+        acc = pv_stage<VHALF, SR, ROWB>(acc, ring + kAttnStageBytes * (st % kAttnSlots), t, sp + st * SR,
+                                        min(SR, nk - st * SR), vtest);
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot are done
       __builtin_amdgcn_s_barrier();
     }
     if (t < HD) store_out(a.att[h], m * a.ldatt, t, a.out, chain_end(acc), a.out_scale);
     __syncthreads();  // sp and the ring are free for the next row
   }
+}
+
+// Split form, first kernel: workgroup (hg, c) computes the scores of the Q = group * M query rows
+// of head group hg (heads hg * group .. + group - 1, which share K and V) for keys
+// [c * keys_per_wg, (c + 1) * keys_per_wg): 16-lane group g takes keys g, g + 16, ... of the chunk,
+// KF at a time, each K row loaded once for all Q queries. Scores go to scratch row h * M + m (and,
+// for the last head, to its score rows).
+template <int HD, int Q>
+__global__ __launch_bounds__(256) void attn_split_scores_kernel(AttnArgs a) {
+  constexpr int U = HD / 16, KF = 2;
+  const int hg = blockIdx.x, t = threadIdx.x, g = t >> 4, l = t & 15;
+  const int G = a.group, M = a.M, nk = a.nk;
+  const int jb = blockIdx.y * a.keys_per_wg, je = min(nk, jb + a.keys_per_wg);
+  float qv[Q][U];
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const float* qr = frow(a.q[hg * G + i / M], a.ldq, i % M);
+#pragma unroll
+    for (int u = 0; u < U; ++u) qv[i][u] = ftz(qr[l + 16 * u]);
+  }
+  const float* kb = a.k[hg * G];
+  for (int j0 = jb + g; j0 < je; j0 += 16 * KF) {
+    float kv[KF][U];
+#pragma unroll
+    for (int c = 0; c < KF; ++c) {
+      const float* kr = frow(kb, a.ldk, min(j0 + 16 * c, nk - 1));  // clamped: computed and dropped
+#pragma unroll
+      for (int u = 0; u < U; ++u) kv[c][u] = kr[l + 16 * u];
+    }
+    float acc[Q][KF];
+    score_chains<U, KF, Q>(qv, kv, acc);
+#pragma unroll
+    for (int i = 0; i < Q; ++i)
+#pragma unroll
+      for (int c = 0; c < KF; ++c) {
+        const float sv = fold16(acc[i][c]);
+        const int j = j0 + 16 * c, h = hg * G + i / M, m = i % M;
+        if (l == 0 && j < je) {
+          a.scratch[(static_cast<int64_t>(h) * M + m) * a.ld_scratch + j] = sv;
+          if (h == a.heads - 1 && a.sc) store_out(a.sc, m * a.ldsc, j, 0, sv, 0.0f);
+        }
+      }
+  }
+}
+
+// The causal softmax (ROW_SOFTMAX) of Q rows of scores in LDS, in place and side by side: row i at
+// sp + i * ldp is query row i % M of its head, with min(nk, causal_k + i % M) valid keys (nk when
+// causal_k is 0). Every step of every row is spread over the whole workgroup, each thread taking
+// the same element of every row together (independent work for the latency of exp_f), and the
+// rows' 16-lane sums run together (lds_sum16_rows); each row's values are softmax_lds's. Rows from
+// pr_first on also go to pr (row i - pr_first at ldpr bytes) when pr is not null. Returns whether
+// one of this thread's probabilities is above 1 or NaN.
+template <int Q>
+__device__ __forceinline__ int softmax_rows_lds(float* sp, int ldp, int M, int nk, int causal_k, int pr_first,
+                                                float* pr, int64_t ldpr, uint32_t (*red)[4], float* bcast) {
+  const int t = threadIdx.x, lane = t & 63;
+  int V[Q];
+#pragma unroll
+  for (int i = 0; i < Q; ++i) V[i] = causal_k > 0 ? min(nk, causal_k + i % M) : nk;
+  __syncthreads();  // the rows are complete
+  uint32_t key[Q];
+  int nan[Q];
+#pragma unroll
+  for (int i = 0; i < Q; ++i) key[i] = 0, nan[i] = 0;
+  for (int j = t; j < nk; j += 256) {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const float x = sp[i * ldp + j];
+      if (j < V[i]) {
+        if (is_nan(x)) nan[i] = 1;
+        else key[i] = max(key[i], fmax_key(x));
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    key[i] = static_cast<uint32_t>(group_reduce<64>(static_cast<int>(key[i]), OpMaxU{}));
+    nan[i] = group_reduce<64>(nan[i], OpOr{});
+    if (lane == 0) red[i][t >> 6] = nan[i] ? 0xFFFFFFFFu : key[i];
+  }
+  __syncthreads();
+  float nmx[Q];
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const uint32_t k4 = max(max(red[i][0], red[i][1]), max(red[i][2], red[i][3]));
+    nmx[i] = fneg(k4 == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k4));
+  }
+  for (int j = t; j < nk; j += 256) {
+    float e[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) e[i] = exp_f(fadd(sp[i * ldp + j], nmx[i]));
+#pragma unroll
+    for (int i = 0; i < Q; ++i) sp[i * ldp + j] = j < V[i] ? e[i] : 0.0f;
+  }
+  lds_sum16_rows<false>(sp, ldp, Q, nk, bcast);
+  float r[Q];
+#pragma unroll
+  for (int i = 0; i < Q; ++i) r[i] = recip_f(bcast[i]);
+  int above1 = 0;
+  for (int j = t; j < nk; j += 256) {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const float p = fmul(sp[i * ldp + j], r[i]);
+      sp[i * ldp + j] = p;
+      above1 |= !(p <= 1.0f);
+      if (pr && i >= pr_first) store_out(pr, (i - pr_first) * ldpr, j, 0, p, 0.0f);
+    }
+  }
+  return above1;
+}
+
+// Split form, second kernel: workgroup (hg, c) loads the scratch scores of the Q = group * M query
+// rows of head group hg (Q consecutive scratch rows) into LDS by direct loads, then issues the
+// first stages of a ring of direct loads of V's columns [32 c, 32 c + 32), runs the Q softmaxes
+// side by side (the same probabilities in every workgroup of the group; workgroup 0 of the last
+// head's group stores that head's), then the P V chains of those columns for every query row,
+// one thread per (query row, column).
+template <int HD, bool VHALF, int Q>
+__global__ __launch_bounds__(256) void attn_split_pv_kernel(AttnArgs a) {
+  constexpr int DS = kAttnSplitCols, ES = VHALF ? 2 : 4;
+  constexpr int ROWB = DS * ES;                      // bytes of a V row's columns (128 / 64)
+  constexpr int LPR = ROWB / 16;                     // lanes per row in a 1 KiB load
+  constexpr int SB = 8192, SR = SB / ROWB;           // rows per stage
+  constexpr int SLOTS = 5, L = SB / 1024 / 4;        // 1 KiB loads per wave per stage (2)
+  static_assert(HD % DS == 0 && 1024 % ROWB == 0 && kAttnSplitProbs % 256 == 0, "split attention shape");
+  __shared__ __align__(16) float sp[kAttnSplitProbs];
+  __shared__ __align__(16) int8_t ring[SLOTS * SB];
+  __shared__ uint32_t red[kAttnSplitMaxQ][4];
+  __shared__ float bcast[kAttnSplitMaxQ];
+  const int hg = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int G = a.group, M = a.M, nk = a.nk;  // G * M == Q
+  const int ldp = static_cast<int>(a.ld_scratch);
+  const int NS = (nk + SR - 1) / SR;
+  const char* vbase = static_cast<const char*>(a.v[hg * G]) + c * ROWB;
+  auto issue = [&](int st) {
+    int8_t* slot = ring + SB * (st % SLOTS);
+#pragma unroll
+    for (int u = 0; u < L; ++u) {
+      const int i = wave + 4 * u;
+      const int row = min(st * SR + i * (1024 / ROWB) + lane / LPR, nk - 1);
+      ring_load16(vbase + static_cast<int64_t>(row) * a.ldv + 16 * (lane % LPR),
+                  __builtin_amdgcn_readfirstlane(lds_addr(slot + i * 1024)));
+    }
+  };
+  // the Q score rows (4 Q ldp bytes, contiguous in the scratch) in 1 KiB blocks; a block's lanes
+  // past the end read the last 16 bytes again (into LDS past the rows, inside sp)
+  const int sbytes = 4 * Q * ldp;
+  const char* sbase = reinterpret_cast<const char*>(a.scratch + static_cast<int64_t>(hg) * Q * a.ld_scratch);
+  for (int b = wave; 1024 * b < sbytes; b += 4)
+    ring_load16(sbase + min(1024 * b + 16 * lane, sbytes - 16), __builtin_amdgcn_readfirstlane(lds_addr(sp + 256 * b)));
+#pragma unroll
+  for (int st = 0; st < SLOTS - 1; ++st)
+    if (st < NS) issue(st);
+  wait_stages_ahead<L, SLOTS - 1>(min(NS, SLOTS - 1));  // this wave's score blocks have landed
+  const int pr_first = hg == gridDim.x - 1 && c == 0 ? (G - 1) * M : Q;
+  const int above1 = softmax_rows_lds<Q>(sp, ldp, M, nk, a.causal_k, pr_first, a.pr, a.ldpr, red, bcast);
+  wait_vmcnt<0>();  // the first V stages have landed; nothing else outstanding before the ring's counts
+  // V elements need their own test only when fp32 and some probability is above 1 or NaN (as in
+  // attn_kernel)
+  const bool vtest = __syncthreads_or(above1) && !VHALF;
+  const int i = t / DS, d = t % DS;
+  const bool active = i < Q;
+  float acc = 0.0f;
+  for (int st = 0; st < NS; ++st) {
+    if (st + SLOTS - 1 < NS) issue(st + SLOTS - 1);
+    wait_stages_ahead<L, SLOTS - 1>(min(NS - 1 - st, SLOTS - 1));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the slot's reads stay after the barrier
+    if (active)
+      acc = pv_stage<VHALF, SR, ROWB>(acc, ring + SB * (st % SLOTS), d, sp + i * ldp + st * SR, min(SR, nk - st * SR),
+                                      vtest);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot are done
+    __builtin_amdgcn_s_barrier();
+  }
+  if (active) store_out(a.att[hg * G + i / M], (i % M) * a.ldatt, c * DS + d, a.out, chain_end(acc), a.out_scale);
 }
 
 // Columns over grid x (per / threads each), rows over grid y with a stride loop past 65535 rows.
@@ -904,8 +1157,82 @@ bool attention_supported(int hd, int nk) {
   return (hd == 64 || hd == 128 || hd == 256) && nk >= 1 && nk <= kAttnMaxKeys;
 }
 
-hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  const dim3 grid(a.heads), block(256);
+namespace {
+
+// Query heads per K / V head for the split form: the largest G in {4, 2} with G * M <= 4 that
+// divides the heads such that every run of G consecutive heads reads the same K and V rows, else 1.
+int query_group(const AttnArgs& a) {
+  for (int G : {4, 2}) {
+    if (a.heads % G || G * a.M > kAttnSplitMaxQ) continue;
+    bool same = true;
+    for (int h = 0; h < a.heads && same; ++h) same = a.k[h] == a.k[h - h % G] && a.v[h] == a.v[h - h % G];
+    if (same) return G;
+  }
+  return 1;
+}
+
+template <int HD, int Q>
+void launch_split_q(const AttnArgs& a, dim3 gs, dim3 gp, hipStream_t s) {
+  hipLaunchKernelGGL((attn_split_scores_kernel<HD, Q>), gs, dim3(256), 0, s, a);
+  if (a.v_fp16) hipLaunchKernelGGL((attn_split_pv_kernel<HD, true, Q>), gp, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((attn_split_pv_kernel<HD, false, Q>), gp, dim3(256), 0, s, a);
+}
+
+template <int HD>
+void launch_split(const AttnArgs& a, hipStream_t s) {
+  const int NG = a.heads / a.group, Q = a.group * a.M;
+  const dim3 gs(NG, (a.nk + a.keys_per_wg - 1) / a.keys_per_wg), gp(NG, HD / kAttnSplitCols);
+  switch (Q) {
+    case 1: launch_split_q<HD, 1>(a, gs, gp, s); break;
+    case 2: launch_split_q<HD, 2>(a, gs, gp, s); break;
+    case 3: launch_split_q<HD, 3>(a, gs, gp, s); break;
+    default: launch_split_q<HD, 4>(a, gs, gp, s); break;
+  }
+}
+
+}  // namespace
+
+float* attention_workspace(hipStream_t s) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static float* ws[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ws[dev]) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, static_cast<size_t>(kAttnScratchFloats) * sizeof(float)) != hipSuccess) {
+      (void)hipGetLastError();  // no scratch: the one-workgroup-per-head form runs instead
+      return nullptr;
+    }
+    ws[dev] = static_cast<float*>(p);
+  }
+  return ws[dev];
+}
+
+bool attention_split_fits(int heads, int M, int nk, int64_t scratch_floats) {
+  const int64_t ld = (nk + 3) / 4 * 4;
+  return M >= 1 && M <= kAttnSplitMaxQ && M * ld <= kAttnSplitProbs && static_cast<int64_t>(heads) * M * ld <= scratch_floats;
+}
+
+hipError_t launch_attention(const AttnArgs& in, hipStream_t s) {
+  const dim3 grid(in.heads), block(256);
+  if (in.scratch && attention_split_fits(in.heads, in.M, in.nk, in.scratch_floats)) {
+    // the split form: scratch rows of the scores, 32 keys per scores workgroup (more past 512 keys,
+    // at most 16 chunks)
+    AttnArgs a = in;
+    a.ld_scratch = (a.nk + 3) / 4 * 4;
+    a.group = query_group(a);
+    while (a.group > 1 && a.group * a.M * a.ld_scratch > kAttnSplitProbs) a.group /= 2;
+    a.keys_per_wg = 32 * ((a.nk + 511) / 512);
+    if (a.hd == 64) launch_split<64>(a, s);
+    else if (a.hd == 128) launch_split<128>(a, s);
+    else launch_split<256>(a, s);
+    return hipGetLastError();
+  }
+  const AttnArgs& a = in;
   if (a.hd == 64) {
     if (a.v_fp16) hipLaunchKernelGGL((attn_kernel<64, true>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<64, false>), grid, block, 0, s, a);

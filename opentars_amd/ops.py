@@ -437,6 +437,39 @@ def fdot_nn(a, b, b_fp16: bool = False, out: int = OUT_FP32, out_scale=None, y=N
     return _fdot(a, b, True, b_fp16, out, out_scale, y)
 
 
+def attention(q, kcache, vcache, heads: int, kv_heads: int, causal_k: int = 0, v_fp16: bool = False,
+              out: int = OUT_FP32, out_scale=None, sc=None, pr=None, att=None):
+    """One layer's attention as the reference lowers it (tars_mini/llm.py:736-746): for every query
+    head h, with K / V head h // (heads // kv_heads), fdot_nt of its q rows with the K rows, the
+    causal softmax (causal_k: the descriptor's K rule; 0 = every key valid), fdot_nn with the V rows
+    into its output columns; sc / pr (fp32 [M, nk], optional) receive the last head's scores and
+    probabilities, as the shared buffers of the three ops do. q fp32 [M, heads * hd]; kcache fp32
+    [nk, kv_heads * hd]; vcache the same, fp32 or binary16 bits (v_fp16). Returns att
+    [M, heads * hd] in format out (or fills the given one)."""
+    npm = _numpy_mode(q, kcache, vcache)
+    qt = _f32_rows(q, "q")
+    kt = _f32_rows(kcache, "kcache")
+    vt = _half_rows(vcache, "vcache") if v_fp16 else _f32_rows(vcache, "vcache")
+    M, nk = qt.shape[0], kt.shape[0]
+    if heads < 1 or kv_heads < 1 or heads % kv_heads or qt.shape[1] % heads:
+        raise ValueError("heads must be a multiple of kv_heads and divide q's columns")
+    hd = qt.shape[1] // heads
+    if kt.shape[1] != kv_heads * hd or vt.shape != (nk, kv_heads * hd):
+        raise ValueError("kcache and vcache must be [nk, kv_heads * hd]")
+    att = _out(att, M, heads * hd, out, qt)
+    ve, oe, grp = (2 if v_fp16 else 4), ESIZE[out], heads // kv_heads
+    arr = lambda vals: (ctypes.c_void_p * heads)(*vals)
+    qp = arr([qt.data_ptr() + 4 * h * hd for h in range(heads)])
+    kp = arr([kt.data_ptr() + 4 * (h // grp) * hd for h in range(heads)])
+    vp = arr([vt.data_ptr() + ve * (h // grp) * hd for h in range(heads)])
+    ap = arr([att.data_ptr() + oe * h * hd for h in range(heads)])
+    osb = _f32_bits(out_scale) if out == OUT_INT8 else 0
+    _check(_lib.lib().tars_attention(qp, _ld(qt), kp, _ld(kt), vp, _ld(vt), int(v_fp16), ap, _ld(att), out, osb,
+                                     _ptr(sc), 0 if sc is None else _ld(sc), _ptr(pr), 0 if pr is None else _ld(pr),
+                                     heads, M, nk, hd, causal_k, _stream()))
+    return _finish(npm, att)
+
+
 def embed_rows(table, ids, scale=None, y=None):
     """Rows `ids` of the bf16 table ([rows, cols], uint16 bits; int16 on the device) as fp32, times
     the fp32 `scale` when given: the board runtime's embedding lookup (tars_board.py:298-314),
@@ -473,7 +506,7 @@ def set_w8a8_path(path: str) -> str:
 
 
 __all__ = ["TarsError", "ContractError", "quant_rows", "gemm_rowcol", "quant_gemm_rowcol", "gemm_rowcol_ksplit",
-           "align_w4_groups", "gemm_w4", "embed_rows", "set_w8a8_path", "ESIZE", "softmax_rows", "softmax_rows_causal",
+           "align_w4_groups", "gemm_w4", "embed_rows", "attention", "set_w8a8_path", "ESIZE", "softmax_rows", "softmax_rows_causal",
            "layernorm_rows", "rmsnorm_rows", "l2norm_rows", "relu", "elt", "rope_rows", "fdot_nt", "fdot_nn",
            "ROW_SOFTMAX", "ROW_LAYERNORM", "ROW_RMSNORM", "ROW_L2NORM", "ELT_MUL", "ELT_ADD", "ELT_MULADD",
            "ELT_SUB", "BM_DENSE", "BM_ROW", "BM_COL", "BM_SCALAR"]

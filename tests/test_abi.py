@@ -254,3 +254,41 @@ def test_embed_rows_validation():
     assert call(ids=(1, 512)) == _lib.E_RANGE                       # past the table
     assert call(ids=(-1,)) == _lib.E_RANGE
     assert call(dst=T + 100 * 512) == _lib.E_OVERLAP                # rows into the table
+
+
+def test_attention_validation():
+    """tars_attention refuses bad arguments before any launch (every call below is invalid)."""
+    import ctypes
+    lib = _lib.lib()
+    Qb, K, V, A, S = P, P + 64 * MB, P + 128 * MB, P + 192 * MB, P + 256 * MB
+
+    def call(heads=4, kv=2, hd=128, nk=256, M=1, q=None, att=None, **k):
+        grp = heads // kv
+        arr = lambda vals: (ctypes.c_void_p * max(heads, 1))(*vals)
+        qp = arr(q if q is not None else [Qb + 4 * h * hd for h in range(heads)])
+        kp = arr([K + 4 * (h // grp) * hd for h in range(heads)])
+        vp = arr([V + 4 * (h // grp) * hd for h in range(heads)])
+        ap = arr(att if att is not None else [A + 4 * h * hd for h in range(heads)])
+        a = dict(ldq=4 * heads * hd, ldk=4 * kv * hd, ldv=4 * kv * hd, v16=0, ldatt=4 * heads * hd, out=0, osc=0,
+                 sc=S, ldsc=0, pr=S + MB, ldpr=0, causal=nk)
+        a.update(k)
+        return lib.tars_attention(qp, a["ldq"], kp, a["ldk"], vp, a["ldv"], a["v16"], ap, a["ldatt"], a["out"],
+                                  a["osc"], a["sc"], a["ldsc"], a["pr"], a["ldpr"], heads, M, nk, hd, a["causal"], None)
+    assert call(q=[None, Qb, Qb, Qb]) == _lib.E_ARG
+    assert call(heads=0, kv=1) == _lib.E_ARG
+    assert call(heads=33, kv=1) == _lib.E_ARG
+    assert call(v16=2) == _lib.E_FIELD
+    assert call(out=3) == _lib.E_FIELD                              # fp16 is no attention output
+    assert call(osc=0x3F800000) == _lib.E_FIELD                     # a scale without INT8 output
+    assert call(causal=-1) == _lib.E_FIELD
+    assert call(M=0) == _lib.E_ALIGN
+    assert call(hd=48) == _lib.E_ARG                                # head sizes 64, 128, 256
+    assert call(nk=4096) == _lib.E_ARG                              # past 4080 keys
+    assert call(ldk=4 * 128 + 4) == _lib.E_ALIGN                    # not a multiple of 16
+    assert call(ldq=256) == _lib.E_ALIGN                            # shorter than a row
+    assert call(sc=S + 8) == _lib.E_ALIGN
+    assert call(att=[A + 4, A + 516, A + 1028, A + 1540]) == _lib.E_ALIGN
+    assert call(att=[A, A, A + 1024, A + 1536]) == _lib.E_OVERLAP   # two heads' outputs
+    assert call(att=[Qb + 4 * 128 * h for h in range(4)]) == _lib.E_OVERLAP   # over the q rows
+    assert call(pr=V) == _lib.E_OVERLAP                             # over the V rows
+    assert call(pr=S) == _lib.E_OVERLAP                             # the score and probability rows

@@ -134,6 +134,17 @@ def test_relu_op(act, out):
     assert same(got, want), mismatch(got, want)
 
 
+@pytest.mark.parametrize("act", [3, 4, 5, 6, 7])
+def test_exp_based_activations_over_a_bit_pattern_sweep(act):
+    """GELU, SiLU, sigmoid, softplus and exp (every one built on exp_f) on every 1024th fp32 bit
+    pattern (both signs, every exponent: zeros, subnormals, normals, infinities, NaNs), bit for bit
+    against the oracle."""
+    x = (np.arange(1 << 22, dtype=np.uint64) << np.uint64(10)).astype(np.uint32).view(f32).reshape(4096, 1024)
+    got = ops.relu(x, act)
+    want = F.act_fn(x, act)
+    assert same(got, want), mismatch(got, want)
+
+
 # ------------------------------------------------------------------------------ ELT
 @pytest.mark.parametrize("op", [R.ELT_MUL, R.ELT_ADD, R.ELT_SUB, R.ELT_MULADD])
 @pytest.mark.parametrize("bm", [R.BM_DENSE, R.BM_ROW, R.BM_COL, R.BM_SCALAR])
