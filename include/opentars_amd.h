@@ -4,7 +4,9 @@
  * C ABI of libopentars_amd.so. Plain pointers and sizes only. Every pointer is a device
  * pointer (hipMalloc'd or a torch CUDA/HIP tensor's data_ptr) except where noted; `stream` is a
  * hipStream_t (NULL = the null stream). Work is enqueued on `stream` and is stream-ordered with
- * whatever else the caller puts there; nothing synchronizes the host. No entry point allocates.
+ * whatever else the caller puts there; nothing synchronizes the host. No entry point allocates,
+ * except that tars_attention and the attention in tars_run_queue allocate one 1 MiB scratch buffer
+ * per device at their first use there (tars_attention_noalloc never does).
  *
  * Every entry point validates its arguments on the host before it launches anything and returns
  * a status. On a non-zero status nothing was launched and nothing was written, mirroring the
@@ -268,6 +270,21 @@ int tars_attention(const float* const* q, int64_t ldq, const float* const* k, in
                    const void* const* v, int64_t ldv, int32_t v_fp16, void* const* att, int64_t ldatt,
                    int32_t out, uint32_t out_scale_bits, float* sc, int64_t ldsc, float* pr, int64_t ldpr,
                    int32_t heads, int32_t M, int32_t nk, int32_t hd, int32_t causal_k, void* stream);
+
+/*
+ * tars_attention without any allocation, for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc); it has no counterpart
+ * in the reference. Same arguments, checks and results as tars_attention; the split form's scores
+ * go to a static device array of 262144 floats (1 MiB) that each GPU holds from the library's load
+ * until the process ends, instead of a workspace the library allocates. heads * M * nk (nk rounded
+ * up to a multiple of 4) above 262144 is refused with TARS_E_RANGE. Every call on a GPU shares that
+ * GPU's array: calls that overlap in time on one GPU race.
+ */
+int tars_attention_noalloc(const float* const* q, int64_t ldq, const float* const* k, int64_t ldk,
+                           const void* const* v, int64_t ldv, int32_t v_fp16, void* const* att,
+                           int64_t ldatt, int32_t out, uint32_t out_scale_bits, float* sc, int64_t ldsc,
+                           float* pr, int64_t ldpr, int32_t heads, int32_t M, int32_t nk, int32_t hd,
+                           int32_t causal_k, void* stream);
 
 /* Library version string ("opentars_amd <semver> gfx950"). Host only, never fails. */
 const char* tars_version(void);

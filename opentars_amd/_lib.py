@@ -69,6 +69,10 @@ SIGNATURES = {
     "tars_attention": (c_int, [POINTER(c_void_p), c_int64, POINTER(c_void_p), c_int64, POINTER(c_void_p), c_int64,
                                c_int32, POINTER(c_void_p), c_int64, c_int32, c_uint32, c_void_p, c_int64, c_void_p,
                                c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p]),
+    "tars_attention_noalloc": (c_int, [POINTER(c_void_p), c_int64, POINTER(c_void_p), c_int64, POINTER(c_void_p),
+                                       c_int64, c_int32, POINTER(c_void_p), c_int64, c_int32, c_uint32, c_void_p,
+                                       c_int64, c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                       c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None

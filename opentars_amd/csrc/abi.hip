@@ -610,6 +610,23 @@ int tars_attention(const float* const* q, int64_t ldq, const float* const* k, in
   return launched(tars::launch_attention(a, s));
 }
 
+int tars_attention_noalloc(const float* const* q, int64_t ldq, const float* const* k, int64_t ldk, const void* const* v,
+                           int64_t ldv, int32_t v_fp16, void* const* att, int64_t ldatt, int32_t out,
+                           uint32_t out_scale_bits, float* sc, int64_t ldsc, float* pr, int64_t ldpr, int32_t heads,
+                           int32_t M, int32_t nk, int32_t hd, int32_t causal_k, void* stream) {
+  tars::AttnArgs a{};
+  if (int rc = attention_args(q, ldq, k, ldk, v, ldv, v_fp16, att, ldatt, out, out_scale_bits, sc, ldsc, pr, ldpr, heads,
+                              M, nk, hd, causal_k, a))
+    return rc;
+  const int64_t need = static_cast<int64_t>(heads) * M * ((nk + 3) / 4 * 4);
+  if (need > tars::kAttnScratchFloats)
+    return fail(TARS_E_RANGE, "heads * M * nk (nk rounded up to 4) exceeds the 262144 floats of the static scratch");
+  a.scratch = tars::attention_static_scratch();
+  if (!a.scratch) return fail(TARS_E_DEVICE, "the static scratch has no device address on this device");
+  a.scratch_floats = tars::kAttnScratchFloats;
+  return launched(tars::launch_attention(a, static_cast<hipStream_t>(stream)));
+}
+
 int tars_embed_rows(const uint16_t* table, int64_t ld_table, int64_t table_rows, int32_t cols, const int32_t* ids,
                     int32_t n, int32_t scaled, uint32_t scale_bits, float* dst, int64_t ldd, void* stream) {
   g_last_error.clear();

@@ -271,6 +271,9 @@ bool attention_split_fits(int heads, int M, int nk, int64_t scratch_floats);
 // call there (not while `s` is capturing a graph) and kept until the process ends; null when none.
 constexpr int64_t kAttnScratchFloats = int64_t{1} << 18;
 float* attention_workspace(hipStream_t s);
+// The same size of scratch as a file-scope device array on the current device (no allocation;
+// its address looked up once per device); null when the lookup fails.
+float* attention_static_scratch();
 
 // Embedding rows: dst row i = fp32(table row ids[i]) (times the fp32 scale when scaled).
 constexpr int kEmbedMaxIds = 64;

@@ -1212,6 +1212,31 @@ float* attention_workspace(hipStream_t s) {
   return ws[dev];
 }
 
+// The scores scratch of tars_attention_noalloc: a file-scope device array (each GPU holds its own
+// copy from module load until the process ends), so that entry point allocates nothing. Host code
+// must not pass `scratch` itself to a kernel (on the host it names a stand-in, not device memory):
+// its device address on each GPU comes from hipGetSymbolAddress, looked up once per device with
+// that device current.
+__device__ __align__(256) float scratch[kAttnScratchFloats];
+
+float* attention_static_scratch() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static float* ptr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    ptr[dev] = static_cast<float*>(p);
+  }
+  return ptr[dev];
+}
+
 bool attention_split_fits(int heads, int M, int nk, int64_t scratch_floats) {
   const int64_t ld = (nk + 3) / 4 * 4;
   return M >= 1 && M <= kAttnSplitMaxQ && M * ld <= kAttnSplitProbs && static_cast<int64_t>(heads) * M * ld <= scratch_floats;
