@@ -71,7 +71,11 @@ __device__ __forceinline__ uint32_t min_key(uint32_t m, float a, float b) {
 // exact zero also sends it there (the same bits, more time), so this form suits chains whose
 // partial sums are rarely exactly zero.
 constexpr float kTiny = 0x1p-100f;
-__device__ __forceinline__ float min_mag(float m, float a, float b) { return fminf(m, fminf(fabsf(a), fabsf(b))); }
+__device__ __forceinline__ float min_mag(float m, float a, float b) {
+  float r;  // one v_min3_f32 with |a| and |b| (fminf would add canonicalizing maxima around it)
+  __asm__("v_min3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
 
 // numerics.py:50-52: int32 -> fp32 round-to-nearest-even (v_cvt_f32_i32)
 __device__ __forceinline__ float i2f(int32_t i) { return static_cast<float>(i); }
