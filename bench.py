@@ -568,18 +568,41 @@ def kernel_instance(l: Launch) -> str:
     return f"{name}<64, {cpl}, {u}{tail}>"
 
 
-def instance_times(torch, step_graph, launches, reps: int = 5) -> dict:
+def replay_fixed_s(torch, lib, busy_graph, reps: int = 10) -> float:
+    """The fixed cost of one graph replay as instance_times times it (events around a single replay
+    queued behind other work): graphs of 1 and of 29 tiny launches (a 16-element quant_rows) timed
+    that way, and the intercept of the line through them (seconds)."""
+    x = torch.randn((1, 16), device="cuda")
+    q = torch.empty((1, 16), dtype=torch.int8, device="cuda")
+    s = torch.empty(4, device="cuda")
+    t = {}
+    for n in (1, 29):
+        g = capture(torch, [quant_launch(lib, x, q, s, "tiny") for _ in range(n)])
+        total = 0.0
+        for _ in range(reps):
+            busy_graph.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            total += e0.elapsed_time(e1) / 1e3
+        t[n] = total / reps
+        del g
+    return max(0.0, t[1] - (t[29] - t[1]) / 28)
+
+
+def instance_times(torch, step_graph, launches, fixed_s: float, reps: int = 5) -> dict:
     """Average launch duration of every kernel instance in the step: HIP events around a graph of
-    that instance's launches from the step (same buffers, step order), i.e. the time each launch
-    adds to a dependent chain. Before each timed replay the full step and then the largest other
-    instance are replayed, so at least ~300 MB (more than the 256 MB MALL) stream between two uses
-    of any weight and every timed launch starts cold. (Events around one launch at a time cannot
-    time it: the event packets alone add several microseconds.)"""
+    that instance's launches from the step (same buffers, step order), less one graph replay's fixed
+    cost (fixed_s, replay_fixed_s), i.e. the time each launch adds to a dependent chain. Before each
+    timed replay the full step and then the largest other instance are replayed, so at least ~300
+    MB (more than the 256 MB MALL) stream between two uses of any weight and every timed launch
+    starts cold. (Events around one launch at a time cannot time it: the event packets alone add
+    several microseconds.)"""
     fams = {}
     for l in launches:
         fams.setdefault(kernel_instance(l), []).append(l)
-    # (an instance with few launches per step, like the head, carries the graph replay's fixed
-    # overhead in its figure; bench's per-config measurements time such kernels over many launches)
     graphs = {name: capture(torch, ls) for name, ls in fams.items()}
     size = {name: sum(l.nbytes for l in ls) for name, ls in fams.items()}
     out = {}
@@ -597,9 +620,11 @@ def instance_times(torch, step_graph, launches, reps: int = 5) -> dict:
             e1.record()
             torch.cuda.synchronize()
             total += e0.elapsed_time(e1) / 1e3
-        avg_s = total / (reps * len(ls))
+        raw_s = total / (reps * len(ls))
+        avg_s = (total / reps - fixed_s) / len(ls)
         out[name] = {"launches_per_step": len(ls), "avg_bytes_per_launch": round(size[name] / len(ls)),
-                     "avg_us_per_launch": round(avg_s * 1e6, 3), "s_per_step": avg_s * len(ls),
+                     "avg_us_per_launch": round(avg_s * 1e6, 3), "avg_us_per_launch_with_replay_cost": round(raw_s * 1e6, 3),
+                     "s_per_step": avg_s * len(ls),
                      "GBps": round(size[name] / (avg_s * len(ls)) / 1e9, 1),
                      "hbm_frac": round(size[name] / (avg_s * len(ls)) / HBM_PEAK, 4)}
     del graphs
@@ -1110,11 +1135,11 @@ def main() -> int:
     step_s = e0.elapsed_time(e1) / 1e3 / args.steps
 
     log(f"step {step_s * 1e6:.1f} us; per-instance timing")
-    kernels = instance_times(torch, graph, launches)
+    fixed_s = replay_fixed_s(torch, lib, graph)
+    kernels = instance_times(torch, graph, launches, fixed_s)
     dom_name = max(kernels, key=lambda k: kernels[k]["s_per_step"])
     dom = kernels[dom_name]
-    for v in kernels.values():
-        v.pop("s_per_step")
+    instances_sum_s = sum(v.pop("s_per_step") for v in kernels.values())
     traffic = None
     tfile = ROOT / "profiles" / "decode_step_traffic.json"
     if tfile.exists():
@@ -1185,6 +1210,10 @@ def main() -> int:
                      "avg_us_per_launch": dom["avg_us_per_launch"]},
         "lm_head": {k: configs.get(k) for k in ("lm_head_M1_K1024_N151936", "lm_head_fused_quant_M1_K1024_N151936")},
         "kernels": kernels,
+        # the instances' per-launch times (each instance timed as its own graph, less one replay's
+        # fixed cost) summed over a step's launches, beside the step itself
+        "kernels_sum_us_per_step": round(instances_sum_s * 1e6, 1),
+        "graph_replay_fixed_us": round(fixed_s * 1e6, 2),
         "device_copy_GBps": round(copy_gbps, 1),
         "queue_executor": queue,
         "queue_whole_decode_step_t250": full,
