@@ -7,6 +7,11 @@ Flags that matter for bit-exactness:
   (no -ffast-math, no -fgpu-flush-denormals-to-zero): fp32 subnormals are preserved by the
                          hardware and flushed explicitly after each step, as the reference does
   -packed-fp32-ops off   scalar fp32 instructions only
+Latency:
+  -amdgpu-kernarg-preload-count=16   leading scalar kernel arguments arrive in SGPRs at wave launch
+                         (a kernel whose first loads need them issues those loads without a
+                         kernel-argument round trip; a compatibility prologue loads them itself
+                         where the firmware does not preload)
 """
 from __future__ import annotations
 
@@ -35,6 +40,7 @@ def hipcc() -> str:
 def flags() -> list[str]:
     return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-mllvm", "-amdgpu-kernarg-preload-count=16",
             "-Wall", "-Wno-unused-function", "-I", str(PKG.parent / "include")]
 
 

@@ -99,9 +99,8 @@ constexpr uint32_t kQ127 = 0x42FE0000u, kInv127 = 0x3C010204u;
 __device__ __forceinline__ float add_to_exponent(float y, int e) {
   const uint32_t yb = fbits(y);
   const int field = static_cast<int>((yb >> 23) & 0xFFu) + e;
-  if (field >= 255) return ffrom(kExpo);
-  if (field <= 0) return 0.0f;
-  return ffrom((static_cast<uint32_t>(field) << 23) | (yb & kMant));
+  const uint32_t r = (static_cast<uint32_t>(field) << 23) | (yb & kMant);
+  return ffrom(field >= 255 ? kExpo : field <= 0 ? 0u : r);
 }
 
 // 1/x: seed from the magic constant, three correction-form Newton steps, exponent surgery
@@ -117,9 +116,6 @@ __device__ __forceinline__ float add_to_exponent(float y, int e) {
 __device__ __forceinline__ float recip_f(float x) {
   const uint32_t xb = fbits(ftz(x));
   const uint32_t sgn = xb & kSign, mag = xb & 0x7FFFFFFFu;
-  if (mag > kExpo) return ffrom(kCanonNaN);
-  if (mag == 0) return ffrom(sgn | kExpo);
-  if (mag == kExpo) return ffrom(sgn);
   const uint32_t mb = (mag & kMant) | (127u << 23);
   const float m = ffrom(mb);
   float y = ffrom(kRecipSeed - mb);
@@ -128,7 +124,10 @@ __device__ __forceinline__ float recip_f(float x) {
     const float err = __fadd_rn(1.0f, -__fmul_rn(m, y));
     y = __fadd_rn(y, __fmul_rn(y, err));
   }
-  return ffrom(fbits(add_to_exponent(y, 127 - static_cast<int>(mag >> 23))) | sgn);
+  const uint32_t r = fbits(add_to_exponent(y, 127 - static_cast<int>(mag >> 23))) | sgn;
+  // the special inputs by selects, so the common path runs straight through (no branches)
+  const uint32_t special = mag > kExpo ? kCanonNaN : mag == 0 ? (sgn | kExpo) : sgn;
+  return ffrom(mag == 0 || mag >= kExpo ? special : r);
 }
 
 // e^x (numerics.py:135-150).
@@ -245,9 +244,6 @@ __device__ __forceinline__ int q8_flushed_inv(float x, float inv) {
 constexpr uint32_t kQ8FastMin = 0x04800000u;  // 2^-118
 __device__ __forceinline__ bool q8_fast_row(uint32_t amax_bits) {
   return amax_bits >= kQ8FastMin && amax_bits < kExpo;
-}
-__device__ __forceinline__ int q8_fast(float x, float inv) {
-  return static_cast<int>(fminf(fmaxf(__builtin_rintf(__fmul_rn(x, inv)), -127.0f), 127.0f));
 }
 
 // numerics.py:270-275: FTZ, round-to-nearest-even to the top 16 bits, NaN -> 0x7FC0
@@ -385,10 +381,20 @@ struct RowColEpilogue {
 
 // Per-token quantizer pieces shared by the quant_rows kernel and the fused quantize + GEMV
 // kernels (numerics.py:383-390).
+//
+// The row maximum of |ftz(x)| as an unsigned maximum of encodings: the maximum of the unflushed
+// |x| encodings, flushed once. A normal, infinite or NaN element dominates every subnormal one, so
+// flushing the subnormals first changes the maximum only when every element is zero or subnormal,
+// and then both give +0.
+__device__ __forceinline__ uint32_t abs_bits(float v) { return fbits(v) & 0x7FFFFFFFu; }
 __device__ __forceinline__ uint32_t abs_bits_ftz(float v) {
-  const uint32_t b = fbits(v) & 0x7FFFFFFFu;
+  const uint32_t b = abs_bits(v);
   return b < 0x00800000u ? 0u : b;  // ftz then |.|: a subnormal counts as +0
 }
+__device__ __forceinline__ uint32_t max_abs_bits4(uint32_t m, float4 v) {
+  return max(max(m, max(abs_bits(v.x), abs_bits(v.y))), max(abs_bits(v.z), abs_bits(v.w)));
+}
+__device__ __forceinline__ uint32_t flush_max_bits(uint32_t m) { return m < 0x00800000u ? 0u : m; }
 
 // amax encoding (an unsigned max of |x| encodings; any NaN encoding wins) -> (inv, s)
 __device__ __forceinline__ void quant_scales(uint32_t amax_bits, float& inv, float& s) {
@@ -405,10 +411,24 @@ __device__ __forceinline__ uint32_t q8x4(float a, float b, float c, float d, flo
          ((static_cast<uint32_t>(q8_flushed_inv(d, inv)) & 0xFFu) << 24);
 }
 
-// Four fast-path q8 bytes packed little-endian (a row for which q8_fast_row holds).
+// Four q8 bytes of a row for which q8_fast_row holds, packed little-endian. q8 is then
+// clamp(rint(x * inv), -127, 127) on the unflushed x (above), and the clamp is the identity:
+// |x * inv| <= amax * inv < 127.5 for every such amax (checked on the CPU for every mantissa of amax;
+// the exponent cancels). t = x * inv is rounded once; adding 1.5 * 2^23 rounds it to an integer in
+// the sum's last mantissa bits (the sum lies in [2^23, 2^24), where the spacing is 1, and ties go
+// to even as rint's do, 1.5 * 2^23 being even), so the low byte of the sum's encoding is
+// rint(t) mod 256, the two's-complement q8 byte; three byte permutes gather the four bytes.
+// A subnormal x gives |t| < 1/2 and the byte 0, as its flush does.
 __device__ __forceinline__ uint32_t q8x4_fast(float a, float b, float c, float d, float inv) {
-  return (static_cast<uint32_t>(q8_fast(a, inv)) & 0xFFu) | ((static_cast<uint32_t>(q8_fast(b, inv)) & 0xFFu) << 8) |
-         ((static_cast<uint32_t>(q8_fast(c, inv)) & 0xFFu) << 16) | ((static_cast<uint32_t>(q8_fast(d, inv)) & 0xFFu) << 24);
+  const float kRound = 12582912.0f;  // 1.5 * 2^23
+  const uint32_t ea = fbits(__fadd_rn(__fmul_rn(a, inv), kRound));
+  const uint32_t eb = fbits(__fadd_rn(__fmul_rn(b, inv), kRound));
+  const uint32_t ec = fbits(__fadd_rn(__fmul_rn(c, inv), kRound));
+  const uint32_t ed = fbits(__fadd_rn(__fmul_rn(d, inv), kRound));
+  // v_perm_b32 (hi, lo, sel): selector byte k picks byte k of lo (0-3) or byte k-4 of hi (4-7); 0x0C is 0
+  const uint32_t ab = __builtin_amdgcn_perm(eb, ea, 0x0C0C0400u);  // [a, b, 0, 0]
+  const uint32_t cd = __builtin_amdgcn_perm(ed, ec, 0x0C0C0400u);  // [c, d, 0, 0]
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);                 // [a, b, c, d]
 }
 
 }  // namespace tars

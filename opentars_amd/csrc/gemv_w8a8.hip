@@ -78,10 +78,16 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   for (int r = 0; r < MR; ++r)
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[r][u] = 0;
-  // this lane's epilogue element (lane `sub` finishes activation row m0 + sub / U of weight row
-  // n0 + sub % U) and its operands
-  const int ne = n0 + sub % U, me = m0 + sub / U;
-  const bool epi_lane = sub < MR * U && ne < a.N && (MR == 1 || me < a.M);  // MR = 1: grid.y == M
+  // this lane's epilogue element (element e = (activation row m0 + e / U, weight row n0 + e % U))
+  // and its operands: a whole-wave row group (L = 64) of up to 8 elements ends its reduction
+  // scattered, element scatter_row(lane) stored by its first lane (wave_sum_scatter); otherwise
+  // lane `sub` finishes element sub
+  constexpr int kE = MR * U;
+  constexpr bool kScatter = L == 64 && (kE == 1 || kE == 2 || kE == 4 || kE == 8);
+  const int e = kScatter ? scatter_row<kScatter ? kE : 1>(lane) : sub;
+  const int ne = n0 + e % U, me = m0 + e / U;
+  const bool owner = kScatter ? scatter_owner<kScatter ? kE : 1>(lane) : sub < kE;
+  const bool epi_lane = owner && ne < a.N && (MR == 1 || me < a.M);  // MR = 1: grid.y == M
   const int nc = epi_lane ? ne : 0, mc = epi_lane ? me : 0;
   float sr = 0.0f, sc = 0.0f, bi = 0.0f;
 
@@ -151,18 +157,25 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
     }
   }
 
-#pragma unroll
-  for (int r = 0; r < MR; ++r)
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc[r][u] = group_sum<L>(acc[r][u]);
-
-  // lane `sub` of the group finishes element (sub / U, sub % U)
   int mine = 0;
+  if constexpr (kScatter) {
+    int flat[kE];
 #pragma unroll
-  for (int r = 0; r < MR; ++r)
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (sub == r * U + u) mine = acc[r][u];
+      for (int u = 0; u < U; ++u) flat[r * U + u] = acc[r][u];
+    mine = wave_sum_scatter<kE>(flat);
+  } else {
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[r][u] = group_sum<L>(acc[r][u]);
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (sub == r * U + u) mine = acc[r][u];
+  }
   if (epi_lane) {
     if constexpr (SIMPLE) {
       reinterpret_cast<float*>(static_cast<char*>(a.Y) + me * a.ldy)[ne] = simple_epilogue(mine, sr, sc);
@@ -315,41 +328,62 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_rows_kernel(KSplitA
 // through wave shuffles and 4 LDS words, every thread runs the fixed recip_f sequence, and the
 // q8 bytes land in LDS where each lane picks up the 16-byte chunks its dot products need; rows
 // whose maximum allows it take q8's fast form (q8_fast_row). The weight loads are issued with the
-// activations, so the quantizer runs under their HBM latency. (A wave-local quantizer, each lane
-// packing its own chunk in registers with no LDS or barrier, measured the same.)
-// Weight matrix g of the launch is grid z = g (its fields are read at a fixed kernel-argument
-// offset, with no dependent load before the weight stream); a matrix with fewer row blocks than
-// the grid's x extent leaves the excess workgroups idle. The first workgroup of matrix 0 also
-// stores the quantized row and its scale (the ROW_QUANT outputs the golden model writes).
+// activations, so the quantizer runs under their HBM latency.
+// A launch carries up to four weight matrices (pieces) of one height N, matrix z as grid z. What
+// a wave needs before its loads (x, lda, the four matrix pointers, K, N) comes first among the
+// kernel arguments as scalars: the library is built with kernel-argument preloading, so gfx950
+// places these in SGPRs at wave launch and the activation and weight streams are issued without
+// waiting for a kernel-argument load (measured 0.13 us per launch on a dependent chain). The rest
+// (epilogue operands, outputs, the optional quantized-row outputs) is read from `a` after the
+// streams are issued. The first workgroup of matrix 0 also stores the quantized row and its scale
+// (the ROW_QUANT outputs the golden model writes).
+// A field of the kernel-argument segment read as a volatile scalar load: issued where it stands
+// (not sunk to its first use), so its latency overlaps the streams already in flight.
+typedef const __attribute__((address_space(4))) char* KArg;
+template <class T>
+__device__ __forceinline__ T kload(KArg p) {
+  return *reinterpret_cast<const volatile __attribute__((address_space(4))) T*>(p);
+}
+
+// The kernel's arguments as laid out in the kernel-argument segment (natural alignment, in order).
+struct QuantGemvKernargs {
+  const float* x;
+  int64_t lda;
+  const int8_t* W[4];
+  int K, N;
+  QuantGemvArgs a;
+};
+constexpr size_t kQuantGemvArgsOffset = offsetof(QuantGemvKernargs, a);
+static_assert(kQuantGemvArgsOffset == 56, "the preloaded scalars take 56 bytes before the argument block");
+
 template <int L, int CPL, int U, bool SIMPLE>
-__global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs a) {
+__global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* x, int64_t lda, const int8_t* W0,
+                                                                   const int8_t* W1, const int8_t* W2,
+                                                                   const int8_t* W3, int K, int N, QuantGemvArgs a) {
   extern __shared__ __align__(16) int8_t qsh[];  // the quantized row, K bytes
   __shared__ uint32_t wave_max[kWaves];
   constexpr int kSlots = 64 / L;
   constexpr int kRows = kWaves * kSlots * U;  // weight rows per workgroup
-  const GemvGroup& gr = a.g[blockIdx.z];
-  // every kernel argument the load batch needs, in one scalar round trip
-  __asm__ volatile("" : : "s"(a.x), "s"(a.lda), "s"(a.K), "s"(gr.W), "s"(gr.N), "s"(gr.epi.scol),
-                   "s"(gr.epi.bias), "s"(gr.epi.scol_per_tensor));
-  const int N = gr.N;
-  const int nblk = (N + kRows - 1) / kRows;
-  if (static_cast<int>(blockIdx.x) >= nblk) return;  // a matrix with fewer row blocks than the grid
+  const int z = blockIdx.z;
+  const int8_t* W = z == 0 ? W0 : z == 1 ? W1 : z == 2 ? W2 : W3;
+  const GemvGroup& gr = a.g[z];
+  const int nblk = (N + kRows - 1) / kRows;  // the grid's x extent
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slot = lane / L;
   const int sub = lane % L;
   const int m = blockIdx.y;
-  const int C = a.K >> 4;
-  const int K4 = a.K >> 2;
+  const int C = K >> 4;
+  const int K4 = K >> 2;
   const int n0 = (xcd_block(blockIdx.x, nblk) * (kWaves * kSlots) + wave * kSlots + slot) * U;
   const v4i zero = {0, 0, 0, 0};
-  const int8_t* W = gr.W;
 
-  // one batch of loads: the fp32 activations (the quantizer waits on them alone), the epilogue
-  // operands, the weights (rows past N and chunks past K read the matrix start: rows past N are
-  // never stored and a chunk past K meets a zero activation chunk)
+  // one batch of loads: the fp32 activations (the quantizer waits on them alone), the weights
+  // (rows past N and chunks past K read the matrix start: rows past N are never stored and a
+  // chunk past K meets a zero activation chunk), then the epilogue operands, whose addresses come
+  // from the kernel-argument load
   constexpr int XV = CPL > 0 ? (L == 64 ? CPL : 1) : 1;  // float4s of the row per thread (K <= 1024 XV)
-  const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(a.x) + m * a.lda);
+  const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(x) + m * lda);
   float4 xr[XV];
   if constexpr (CPL > 0) {
 #pragma unroll
@@ -358,16 +392,12 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
       xr[j] = *(i < K4 ? xrow + i : xrow);
     }
   }
-  const int ne = n0 + sub;
-  const bool epi_lane = sub < U && ne < N;
-  const float sc = gr.epi.load_scol(epi_lane ? ne : 0);
-  const float bi = gr.epi.load_bias(epi_lane ? ne : 0);
   v4i wv[U][CPL > 0 ? CPL : 1];
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int n = n0 + u;
-      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * a.K);
+      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
@@ -375,51 +405,76 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
       }
     }
   }
-  issue_fence();
-  pin_sgpr(gr.Y);
-  pin_sgpr(gr.ldy);
-  pin_sgpr(gr.epi.act);
-  pin_sgpr(gr.epi.out);
+  issue_fence();  // nothing that waits for the kernel-argument load moves above the streams
+  // a whole-wave row (L = 64) ends its reduction scattered: the lane that stores row u is the
+  // first lane holding u's total (wave_sum_scatter)
+  const int ne = n0 + (L == 64 ? scatter_row<U>(lane) : sub);
+  const bool epi_lane = (L == 64 ? scatter_owner<U>(lane) : sub < U) && ne < N;
+  // the epilogue operands' addresses from the kernel arguments: read here, through the
+  // kernel-argument segment (volatile: the loads stay here instead of sinking to their use), and
+  // waited for only after the row maximum
+  KArg ka = (KArg)__builtin_amdgcn_kernarg_segment_ptr() + kQuantGemvArgsOffset;
+  KArg kg = ka + offsetof(QuantGemvArgs, g) + z * sizeof(GemvGroup) + offsetof(GemvGroup, epi);
+  const float* const scol = kload<const float*>(kg + offsetof(RowColEpilogue, scol));
+  const int per_tensor = kload<int>(kg + offsetof(RowColEpilogue, scol_per_tensor));
+  const float* const bias = SIMPLE ? nullptr : kload<const float*>(kg + offsetof(RowColEpilogue, bias));
+  int8_t* const qout = kload<int8_t*>(ka + offsetof(QuantGemvArgs, q));  // the optional ROW_QUANT outputs
+  const int64_t ldq = kload<int64_t>(ka + offsetof(QuantGemvArgs, ldq));
+  float sc, bi;
 
   // the workgroup quantizes row m into LDS
   uint32_t mx = 0;
   float inv, sr;
-  const bool store_q = a.q != nullptr && blockIdx.x == 0 && blockIdx.z == 0;
+  const bool store_q = qout != nullptr && blockIdx.x == 0 && blockIdx.z == 0;
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       if (threadIdx.x + j * kThreads >= K4) xr[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      mx = max(mx, max(max(abs_bits_ftz(xr[j].x), abs_bits_ftz(xr[j].y)), max(abs_bits_ftz(xr[j].z), abs_bits_ftz(xr[j].w))));
+      mx = max_abs_bits4(mx, xr[j]);
     }
   } else {
-    for (int i = threadIdx.x; i < K4; i += kThreads) {
-      const float4 v = xrow[i];
-      mx = max(mx, max(max(abs_bits_ftz(v.x), abs_bits_ftz(v.y)), max(abs_bits_ftz(v.z), abs_bits_ftz(v.w))));
-    }
+    for (int i = threadIdx.x; i < K4; i += kThreads) mx = max_abs_bits4(mx, xrow[i]);
   }
   mx = group_max<64>(mx);
   if (lane == 0) wave_max[wave] = mx;
+  // the epilogue operands, once the activations are in (their addresses wait for the
+  // kernel-argument load, which is then long done)
+  sc = scol[per_tensor || !epi_lane ? 0 : ne];
+  bi = *(bias ? bias + (epi_lane ? ne : 0) : scol);
   __syncthreads();
-  mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
+  // the row maximum is uniform: one scalar value, and a branch (not a select) between the q8 forms
+  mx = flush_max_bits(__builtin_amdgcn_readfirstlane(max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]))));
   quant_scales(mx, inv, sr);
-  const bool fast = q8_fast_row(mx);
+  uint32_t* qw = reinterpret_cast<uint32_t*>(qsh);
+  uint32_t* qg = reinterpret_cast<uint32_t*>(qout + m * ldq);
   if constexpr (CPL > 0) {
+    if (q8_fast_row(mx)) {
 #pragma unroll
-    for (int j = 0; j < XV; ++j) {
-      const int i = threadIdx.x + j * kThreads;
-      if (i < K4) {
-        const uint32_t b = fast ? q8x4_fast(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv)
-                                : q8x4(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv);
-        reinterpret_cast<uint32_t*>(qsh)[i] = b;
-        if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
+      for (int j = 0; j < XV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        const uint32_t b = q8x4_fast(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv);
+        if (i < K4) {
+          qw[i] = b;
+          if (store_q) qg[i] = b;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < XV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        const uint32_t b = q8x4(xr[j].x, xr[j].y, xr[j].z, xr[j].w, inv);
+        if (i < K4) {
+          qw[i] = b;
+          if (store_q) qg[i] = b;
+        }
       }
     }
   } else {
     for (int i = threadIdx.x; i < K4; i += kThreads) {
       const float4 v = xrow[i];
       const uint32_t b = q8x4(v.x, v.y, v.z, v.w, inv);
-      reinterpret_cast<uint32_t*>(qsh)[i] = b;
-      if (store_q) reinterpret_cast<uint32_t*>(a.q + m * a.ldq)[i] = b;
+      qw[i] = b;
+      if (store_q) qg[i] = b;
     }
   }
   if (store_q && threadIdx.x == 0) a.s[m] = sr;
@@ -445,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int n = n0 + u;
-        w[u] = load_stream_pred(reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * a.K) + c,
+        w[u] = load_stream_pred(reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K) + c,
                                 reinterpret_cast<const v4i*>(W), n < N, zero);
       }
       const v4i xv = xq[c];
@@ -454,12 +509,16 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(QuantGemvArgs
     }
   }
 
-#pragma unroll
-  for (int u = 0; u < U; ++u) acc[u] = group_sum<L>(acc[u]);
   int mine = 0;
+  if constexpr (L == 64) {
+    mine = wave_sum_scatter<U>(acc);
+  } else {
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (sub == u) mine = acc[u];
+    for (int u = 0; u < U; ++u) acc[u] = group_sum<L>(acc[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (sub == u) mine = acc[u];
+  }
   if (epi_lane) {
     if constexpr (SIMPLE) {
       reinterpret_cast<float*>(static_cast<char*>(gr.Y) + m * gr.ldy)[ne] = simple_epilogue(mine, sr, sc);
@@ -530,8 +589,9 @@ int gcd(int a, int b) {
 
 // Matrix pieces as grid z: matrices of unequal height are cut into pieces of their greatest
 // common height when that gives at most kMaxPieces pieces (q/k/v: 2048 + 1024 + 1024 rows ->
-// four pieces of 1024), so every z slice has the same number of workgroups and none idles; other
-// shapes run one slice per matrix, the shorter ones leaving workgroups idle.
+// four pieces of 1024), so every z slice has the same number of workgroups. Each launch takes up
+// to four consecutive pieces of one height (the kernel's preloaded arguments hold four matrix
+// pointers and one N); other shapes take more than one launch.
 template <int L, int CPL, int U, bool SIMPLE>
 hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
@@ -558,11 +618,30 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
     for (int i = 0; i < np; ++i) a.g[i] = pieces[i];
     a.ngroups = np;
   }
-  int blocks = 0;
-  for (int i = 0; i < a.ngroups; ++i) blocks = max(blocks, (a.g[i].N + rows_per_block - 1) / rows_per_block);
+  // launches of up to four consecutive matrices (pieces) of one height; only the first stores the
+  // quantized rows (outputs never overlap x, so every launch reads the same row)
   const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
-  hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE>), dim3(blocks, a.M, a.ngroups), dim3(kThreads), lds, s, a);
-  return hipGetLastError();
+  QuantGemvArgs b = a;
+  for (int first = 0; first < a.ngroups;) {
+    int n = 1;
+    while (first + n < a.ngroups && n < 4 && a.g[first + n].N == a.g[first].N) ++n;
+    for (int i = 0; i < n; ++i) b.g[i] = a.g[first + i];
+    b.ngroups = n;
+    if (first > 0) {
+      b.q = nullptr;
+      b.s = nullptr;
+    }
+    const int N = b.g[0].N;
+    const int8_t* Wz[4];
+    for (int i = 0; i < 4; ++i) Wz[i] = b.g[i < n ? i : 0].W;
+    const unsigned blocks = (N + rows_per_block - 1) / rows_per_block;
+    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE>), dim3(blocks, a.M, n), dim3(kThreads), lds, s,
+                       a.x, a.lda, Wz[0], Wz[1], Wz[2], Wz[3], a.K, N, b);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    first += n;
+  }
+  return hipSuccess;
 }
 
 // Kernel instance for (K, u): lanes per row L, 16-byte chunks per lane CPL, rows per wave U (u,

@@ -1,10 +1,11 @@
 // Per-token INT8 quantizer (tars_mini/numerics.py:383-390, ROW_QUANT at tars_mini/golden.py:369-372).
 //
-// One workgroup per row. Pass 1 takes the row maximum of |ftz(x)|. The reference's fmax is
-// order-free (numerics.py:293-303), and on non-negative encodings it is exactly an unsigned
-// integer max in which every NaN encoding (> 0x7F800000) wins, so the reduction is a plain
-// wave/LDS max over bit patterns. Lane 0 then runs the fixed recip_f sequence once; pass 2
-// quantizes with q8 and writes 16 bytes per lane. HBM-bound: 4 bytes read and 1 written per element.
+// One workgroup per row. Pass 1 takes the row maximum of |ftz(x)|: the maximum of the |x|
+// encodings, flushed once. The reference's fmax is order-free (numerics.py:293-303), and on
+// non-negative encodings it is exactly an unsigned integer max in which every NaN encoding
+// (> 0x7F800000) wins, so the reduction is a plain wave/LDS max over bit patterns. Lane 0 then runs
+// the fixed recip_f sequence once; pass 2 quantizes with q8 and writes 16 bytes per lane.
+// HBM-bound: 4 bytes read and 1 written per element.
 #include "kernels.h"
 
 namespace tars {
@@ -20,8 +21,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
   for (int c = threadIdx.x; c < chunks; c += kThreads) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float4 v = row[4 * c + j];
-      mx = max(mx, max(max(abs_bits_ftz(v.x), abs_bits_ftz(v.y)), max(abs_bits_ftz(v.z), abs_bits_ftz(v.w))));
+      mx = max_abs_bits4(mx, row[4 * c + j]);
     }
   }
   mx = group_max<64>(mx);
@@ -33,6 +33,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
     uint32_t t = wave_max[0];
 #pragma unroll
     for (int w = 1; w < kThreads / 64; ++w) t = max(t, wave_max[w]);
+    t = flush_max_bits(t);
     float inv, sr;
     quant_scales(t, inv, sr);
     inv_shared = inv;

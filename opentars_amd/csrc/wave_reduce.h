@@ -61,6 +61,65 @@ __device__ __forceinline__ uint32_t group_max(uint32_t v) {
   return static_cast<uint32_t>(group_reduce<L>(static_cast<int>(v), OpMaxU{}));
 }
 
+// ---- wave-wide sums of U values per lane, scattered over the lanes ----
+// v_permlane32_swap(A, B) exchanges lanes 32-63 of A with lanes 0-31 of B, so afterwards A + B holds
+// in lanes 0-31 the sum of A's lanes l and l ^ 32 and in lanes 32-63 the same sum of B's:
+// one instruction and one add halve the number of values per lane (a reduce-scatter step, no
+// selects). v_permlane16_swap does the same across the 16-lane rows (lane bit 4).
+__device__ __forceinline__ int swap32_sum(int a, int b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  return static_cast<int>(r[0]) + static_cast<int>(r[1]);
+}
+__device__ __forceinline__ int swap16_sum(int a, int b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  return static_cast<int>(r[0]) + static_cast<int>(r[1]);
+}
+constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+
+// Every lane ends with the total over the wave's 64 lanes of one of its U (1, 2, 4 or 8) values,
+// value scatter_row<U>(lane); exact int32 sums, so the order of the adds does not matter.
+// U = 8: the pairs (v0, v1), (v2, v3), ... are halved across lane bit 5, the results across bit 4,
+// then once more between lanes l and l ^ 1 (DPP with selects); the lane bits left are summed in full.
+template <int U>
+__device__ __forceinline__ int wave_sum_scatter(const int (&v)[U]) {
+  static_assert(U == 1 || U == 2 || U == 4 || U == 8, "1, 2, 4 or 8 values per lane");
+  if constexpr (U == 1) {
+    const int t = group_sum<16>(v[0]);
+    const int h = swap16_sum(t, t);
+    return swap32_sum(h, h);
+  } else if constexpr (U == 2) {
+    const int t = group_sum<16>(swap32_sum(v[0], v[1]));
+    return swap16_sum(t, t);
+  } else if constexpr (U == 4) {
+    return group_sum<16>(swap16_sum(swap32_sum(v[0], v[1]), swap32_sum(v[2], v[3])));
+  } else {
+    const int t0 = swap16_sum(swap32_sum(v[0], v[1]), swap32_sum(v[2], v[3]));
+    const int t1 = swap16_sum(swap32_sum(v[4], v[5]), swap32_sum(v[6], v[7]));
+    const bool odd = threadIdx.x & 1;
+    int u = (odd ? t1 : t0) + dpp<kDppQuadXor1>(odd ? t0 : t1);
+    u += dpp<kDppQuadXor2>(u);
+    u += dpp<kDppRowRor4>(u);
+    return u + dpp<kDppRowRor8>(u);
+  }
+}
+// The value whose total lane `lane` holds after wave_sum_scatter<U>, and whether the lane is the
+// first (lowest) lane holding that value's total.
+template <int U>
+__device__ __forceinline__ int scatter_row(int lane) {
+  const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
+  if constexpr (U == 1) return 0;
+  else if constexpr (U == 2) return b5;
+  else if constexpr (U == 4) return 2 * b4 + b5;
+  else return 4 * (lane & 1) + 2 * b4 + b5;
+}
+template <int U>
+__device__ __forceinline__ bool scatter_owner(int lane) {
+  if constexpr (U == 1) return lane == 0;
+  else if constexpr (U == 2) return (lane & 31) == 0;
+  else if constexpr (U == 4) return (lane & 15) == 0;
+  else return (lane & 14) == 0;
+}
+
 // Lane i receives lane (i ^ 1) / (i ^ 2)'s value (within its quad).
 __device__ __forceinline__ int lane_xor1(int v) { return dpp<kDppQuadXor1>(v); }
 __device__ __forceinline__ int lane_xor2(int v) { return dpp<kDppQuadXor2>(v); }

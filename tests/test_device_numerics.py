@@ -155,7 +155,52 @@ def test_q8_fast_path_for_rows_with_a_normal_maximum():
         x = x[np.abs(F.ftz(x)) <= amax]
         with np.errstate(all="ignore"):
             fast = np.clip(np.rint(x * inv), -127, 127).astype(np.int8)
+            byte = rounding_constant_byte(x * inv)        # the kernels' form: no clamp
         assert (fast == F.q8(x, inv)).all(), amax
+        assert (byte == F.q8(x, inv)).all(), amax
+
+
+ROUND_C = f32(1.5 * 2.0 ** 23)
+
+
+def rounding_constant_byte(t):
+    """The fast q8 byte as the kernels form it: the low byte of the encoding of t + 1.5 * 2^23."""
+    return ((t.astype(f32) + ROUND_C).view(np.uint32) & np.uint32(0xFF)).astype(np.uint8).view(np.int8)
+
+
+def test_q8_fast_rows_need_no_clamp():
+    """On a row for which the fast path holds, |x * inv| <= amax * inv < 127.5, so clamping
+    rint(x * inv) to [-127, 127] never changes it. amax * inv depends only on amax's mantissa m
+    (recip_f and the product by 127 scale exactly with a power of two while the results stay normal;
+    a flushed subnormal result makes inv 0): exhaustive over all 2^23 mantissas, plus random maxima
+    over every fast-path exponent, including those where inv underflows to 0."""
+    m = (np.arange(1 << 23, dtype=np.uint32) | np.uint32(127 << 23)).view(f32)
+    p = m * F.fmul(F.Q127, F.recip_f(m))
+    assert p.max() < f32(127.0001) and p.min() > f32(-127.5)
+    rng = np.random.default_rng(11)
+    mb = (rng.integers(9, 255, 20000, dtype=np.uint32) << 23) | rng.integers(0, 1 << 23, 20000, dtype=np.uint32)
+    amax = np.concatenate([mb, np.array([0x04800000, 0x7F7FFFFF, 0x7F000000, 0x7E800000], np.uint32)]).view(f32)
+    inv = F.fmul(F.Q127, F.recip_f(amax))
+    with np.errstate(over="ignore"):
+        assert (amax * inv < f32(127.5)).all()
+    assert (inv == 0).any()                                  # maxima near 2^128 give inv = 0
+
+
+def test_rounding_constant_gives_the_q8_byte():
+    """rint(t) mod 256 as the low byte of RN(t + 1.5 * 2^23): exhaustive over every fp32 t with
+    0.5 <= |t| < 128 (the sum lies in [2^23, 2^24), where the spacing is 1 and ties go to even, as
+    rint's do), and every |t| < 0.5 gives 0 (random values, every subnormal, +-0)."""
+    for e in range(-1, 7):
+        t = ((np.uint32(e + 127) << np.uint32(23)) | np.arange(1 << 23, dtype=np.uint32)).view(f32)
+        for v in (t, -t):
+            want = np.rint(v).astype(np.int64).astype(np.int8)
+            assert (rounding_constant_byte(v) == want).all(), e
+    rng = np.random.default_rng(5)
+    small = np.concatenate([rng.uniform(-0.5, 0.5, 1 << 20).astype(f32),
+                            np.arange(1, 1 << 23, 97, dtype=np.uint32).view(f32),
+                            np.array([0.0, -0.0, 0.49999997, -0.49999997, 0.5, -0.5], f32)])
+    small = small[np.abs(small) <= 0.5]
+    assert (rounding_constant_byte(small) == 0).all()
 
 
 def test_partial_sums_above_2_pow_minus_100_absorb_subnormal_addends():

@@ -528,6 +528,46 @@ def test_fused_quant_gemm_matches_separate_ops(K, M):
         assert same(host(y), want), mismatch(host(y), want)
 
 
+def q8_tie_rows(rng, M, K):
+    """Rows whose elements sit on q8 ties (x * inv = k + 1/2 up to one rounding) and at the
+    extremes: maxima from 2^-118 (the smallest fast-path maximum) to 2^127, subnormal and zero
+    elements, +-amax, and values just inside the maximum."""
+    rows = []
+    for i in range(M):
+        amax = f32(np.ldexp(rng.uniform(1, 2), int(rng.integers(-118, 127)))) if i > 1 else \
+            [np.uint32(0x04800000).view(f32), np.uint32(0x7F7FFFFF).view(f32)][i]
+        inv = F.fmul(F.Q127, F.recip_f(np.array([amax], f32)))[0]
+        with np.errstate(all="ignore"):
+            ties = ((rng.integers(-127, 127, K) + f32(0.5)) / inv).astype(f32)
+            near = (amax * rng.uniform(-1, 1, K)).astype(f32)
+        x = np.where(rng.random(K) < 0.5, ties, near).astype(f32)
+        x[~np.isfinite(x)] = 0.0
+        x = np.clip(x, -amax, amax).astype(f32)
+        x[rng.integers(0, K, 3)] = np.uint32(rng.integers(1, 1 << 23)).view(f32)   # subnormals
+        x[0], x[-1] = amax, -amax if K > 1 else amax
+        x[rng.integers(0, K, 2)] = -0.0
+        rows.append(x)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("K", [16, 1024, 2048, 3072])
+def test_fused_quantizer_on_q8_ties_and_row_extremes(K):
+    """The fast q8 form (rint by the 1.5 * 2^23 rounding constant, no clamp) on the values where a
+    wrong rounding or clamp would show: exact ties, +-amax, the smallest and largest fast-path
+    maxima; the fused kernel's quantized row and the standalone quantizer against the oracle."""
+    rng = np.random.default_rng(K + 77)
+    x = q8_tie_rows(rng, 6, K)
+    q, s = F.quant_rows(x)
+    qg, sg = ops.quant_rows(cuda(x))
+    assert same(host(qg), q) and same(host(sg), s)
+    W = rng.integers(-128, 128, (96, K), dtype=np.int8)
+    sc = rng.uniform(1e-3, 1e-2, 96).astype(f32)
+    for m in range(x.shape[0]):
+        outs = ops.quant_gemm_rowcol(cuda(x[m:m + 1]), [(cuda(W), cuda(sc))], return_q=True)
+        assert same(host(outs[0]), q[m:m + 1]) and same(host(outs[1]), s[m:m + 1]), m
+        assert same(host(outs[2]), G.gemm_rowcol(q[m:m + 1], s[m:m + 1], W, sc)), m
+
+
 @pytest.mark.parametrize("Ns", [[64, 32, 32], [48, 96], [128, 64, 32, 32], [96, 32, 160, 32]])
 @pytest.mark.parametrize("K,M", [(1024, 1), (2048, 4), (16, 1)])
 def test_fused_equal_row_pieces(Ns, K, M):
