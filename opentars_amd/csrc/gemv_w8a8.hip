@@ -58,8 +58,25 @@ bool simple_epi(const RowColEpilogue& e, bool need_srow) {
   return (!need_srow || e.srow != nullptr) && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0;
 }
 
+// What the first loads need leads the kernel arguments as scalars (preloaded into SGPRs at wave
+// launch); the epilogue's other fields follow in `a` and are read through the kernel-argument
+// segment once the streams are in flight.
+struct W8A8Kernargs {
+  const int8_t* A;
+  int64_t lda;
+  const int8_t* W;
+  const float* scol;
+  const float* srow;
+  int K, N, M, scol_per_tensor;
+  W8A8Args a;
+};
+constexpr size_t kW8A8ArgsOffset = offsetof(W8A8Kernargs, a);
+static_assert(kW8A8ArgsOffset == 56, "the preloaded scalars take 56 bytes before the argument block");
+
 template <int L, int CPL, int U, int MR, bool SIMPLE>
-__global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
+__global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(const int8_t* A, int64_t lda, const int8_t* W,
+                                                             const float* scol, const float* srow, int K, int N,
+                                                             int M, int per_tensor, W8A8Args a) {
   static_assert(MR == 1 || CPL > 0, "several activation rows need the register-held activations");
   static_assert(MR * U <= L, "one epilogue lane per (row, weight row)");
   constexpr int kSlots = 64 / L;
@@ -68,8 +85,8 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   const int slot = lane / L;
   const int sub = lane % L;
   const int m0 = blockIdx.y * MR;
-  const int C = a.K >> 4;
-  const int bx = xcd_block(blockIdx.x, gridDim.x);
+  const int C = K >> 4;
+  const int bx = xcd_block(blockIdx.x, (N + kWaves * kSlots * U - 1) / (kWaves * kSlots * U));  // the grid's x extent
   const int n0 = (bx * (kWaves * kSlots) + wave * kSlots + slot) * U;
   const v4i zero = {0, 0, 0, 0};
 
@@ -87,9 +104,14 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   const int e = kScatter ? scatter_row<kScatter ? kE : 1>(lane) : sub;
   const int ne = n0 + e % U, me = m0 + e / U;
   const bool owner = kScatter ? scatter_owner<kScatter ? kE : 1>(lane) : sub < kE;
-  const bool epi_lane = owner && ne < a.N && (MR == 1 || me < a.M);  // MR = 1: grid.y == M
+  const bool epi_lane = owner && ne < N && (MR == 1 || me < M);  // MR = 1: grid.y == M
   const int nc = epi_lane ? ne : 0, mc = epi_lane ? me : 0;
   float sr = 0.0f, sc = 0.0f, bi = 0.0f;
+  // the epilogue's fields: their loads are issued after the streams and waited for at first use
+  const KArg ka = kernarg_at(kW8A8ArgsOffset);
+  void* Y;
+  int64_t ldy;
+  RowColEpilogue epi{};
 
   if constexpr (CPL > 0) {
     // one batch of loads: activations, epilogue operands, weights (rows past N and chunks past K
@@ -98,34 +120,39 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
     v4i xv[MR][CPL];
 #pragma unroll
     for (int r = 0; r < MR; ++r) {
-      const bool live = MR == 1 || m0 + r < a.M;
-      const v4i* xrow = reinterpret_cast<const v4i*>(a.A + (live ? m0 + r : 0) * a.lda);
+      const bool live = MR == 1 || m0 + r < M;
+      const v4i* xrow = reinterpret_cast<const v4i*>(A + (live ? m0 + r : 0) * lda);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
         xv[r][j] = *(c < C ? xrow + c : xrow);
       }
     }
-    sc = a.epi.load_scol(nc);
-    bi = a.epi.load_bias(nc);
-    sr = a.epi.load_srow(mc);
-    const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
+    sc = scol[per_tensor ? 0 : nc];
+    sr = *(srow ? srow + mc : scol);
+    const v4i* wbase = reinterpret_cast<const v4i*>(W);
     v4i wv[U][CPL];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int n = n0 + u;
-      const v4i* wrow = reinterpret_cast<const v4i*>(a.W + static_cast<int64_t>(n) * a.K);
+      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        wv[u][j] = __builtin_nontemporal_load(n < a.N && c < C ? wrow + c : wbase);
+        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : wbase);
       }
     }
     issue_fence();
-    pin_sgpr(a.Y);
-    pin_sgpr(a.ldy);
-    pin_sgpr(a.epi.act);
-    pin_sgpr(a.epi.out);
+    Y = kload<void*>(ka + offsetof(W8A8Args, Y));
+    ldy = kload<int64_t>(ka + offsetof(W8A8Args, ldy));
+    if constexpr (!SIMPLE) {
+      const KArg ke = ka + offsetof(W8A8Args, epi);
+      epi = RowColEpilogue{srow, scol, per_tensor, kload<const float*>(ke + offsetof(RowColEpilogue, bias)),
+                           kload<int>(ke + offsetof(RowColEpilogue, act)), kload<int>(ke + offsetof(RowColEpilogue, out)),
+                           kload<float>(ke + offsetof(RowColEpilogue, out_scale))};
+      bi = *(epi.bias ? epi.bias + nc : scol);
+    }
+    issue_fence();
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
       if (sub + j * L >= C)
@@ -138,19 +165,28 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[r][u] = dot16(wv[u][j], xv[r][j], acc[r][u]);
   } else {
-    sc = a.epi.load_scol(nc);
-    bi = a.epi.load_bias(nc);
-    sr = a.epi.load_srow(mc);
-    const v4i* xrow = reinterpret_cast<const v4i*>(a.A + m0 * a.lda);
-    const v4i* wbase = reinterpret_cast<const v4i*>(a.W);
+    sc = scol[per_tensor ? 0 : nc];
+    sr = *(srow ? srow + mc : scol);
+    Y = kload<void*>(ka + offsetof(W8A8Args, Y));
+    ldy = kload<int64_t>(ka + offsetof(W8A8Args, ldy));
+    if constexpr (!SIMPLE) {
+      const KArg ke = ka + offsetof(W8A8Args, epi);
+      epi = RowColEpilogue{srow, scol, per_tensor, kload<const float*>(ke + offsetof(RowColEpilogue, bias)),
+                           kload<int>(ke + offsetof(RowColEpilogue, act)), kload<int>(ke + offsetof(RowColEpilogue, out)),
+                           kload<float>(ke + offsetof(RowColEpilogue, out_scale))};
+      bi = *(epi.bias ? epi.bias + nc : scol);
+    }
+    issue_fence();
+    const v4i* xrow = reinterpret_cast<const v4i*>(A + m0 * lda);
+    const v4i* wbase = reinterpret_cast<const v4i*>(W);
     for (int c = sub; c < C; c += L) {
       const v4i xv = xrow[c];
       v4i wv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int n = n0 + u;
-        wv[u] = load_stream_pred(reinterpret_cast<const v4i*>(a.W + static_cast<int64_t>(n) * a.K) + c, wbase,
-                                 n < a.N, zero);
+        wv[u] = load_stream_pred(reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K) + c, wbase,
+                                 n < N, zero);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) acc[0][u] = dot16(wv[u], xv, acc[0][u]);
@@ -178,10 +214,10 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(W8A8Args a) {
   }
   if (epi_lane) {
     if constexpr (SIMPLE) {
-      reinterpret_cast<float*>(static_cast<char*>(a.Y) + me * a.ldy)[ne] = simple_epilogue(mine, sr, sc);
+      reinterpret_cast<float*>(static_cast<char*>(Y) + me * ldy)[ne] = simple_epilogue(mine, sr, sc);
     } else {
-      const float y = a.epi.apply(mine, sr, a.epi.srow != nullptr, sc, bi);
-      store_out(a.Y, me * a.ldy, ne, a.epi.out, y, a.epi.out_scale);
+      const float y = epi.apply(mine, sr, srow != nullptr, sc, bi);
+      store_out(Y, me * ldy, ne, epi.out, y, epi.out_scale);
     }
   }
 }
@@ -337,14 +373,6 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_ksplit_rows_kernel(KSplitA
 // (epilogue operands, outputs, the optional quantized-row outputs) is read from `a` after the
 // streams are issued. The first workgroup of matrix 0 also stores the quantized row and its scale
 // (the ROW_QUANT outputs the golden model writes).
-// A field of the kernel-argument segment read as a volatile scalar load: issued where it stands
-// (not sunk to its first use), so its latency overlaps the streams already in flight.
-typedef const __attribute__((address_space(4))) char* KArg;
-template <class T>
-__device__ __forceinline__ T kload(KArg p) {
-  return *reinterpret_cast<const volatile __attribute__((address_space(4))) T*>(p);
-}
-
 // The kernel's arguments as laid out in the kernel-argument segment (natural alignment, in order).
 struct QuantGemvKernargs {
   const float* x;
@@ -413,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   // the epilogue operands' addresses from the kernel arguments: read here, through the
   // kernel-argument segment (volatile: the loads stay here instead of sinking to their use), and
   // waited for only after the row maximum
-  KArg ka = (KArg)__builtin_amdgcn_kernarg_segment_ptr() + kQuantGemvArgsOffset;
+  KArg ka = kernarg_at(kQuantGemvArgsOffset);
   KArg kg = ka + offsetof(QuantGemvArgs, g) + z * sizeof(GemvGroup) + offsetof(GemvGroup, epi);
   const float* const scol = kload<const float*>(kg + offsetof(RowColEpilogue, scol));
   const int per_tensor = kload<int>(kg + offsetof(RowColEpilogue, scol_per_tensor));
@@ -563,15 +591,18 @@ hipError_t go(const W8A8Args& a, hipStream_t s) {
   const unsigned nb = (a.N + rows_per_block - 1) / rows_per_block;
   if constexpr (CPL > 0 && 4 * U <= L) {
     if (a.M >= 3) {
-      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 4, SIMPLE>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 4, SIMPLE>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a.A, a.lda,
+                       a.W, a.epi.scol, a.epi.srow, a.K, a.N, a.M, a.epi.scol_per_tensor, a);
       return hipGetLastError();
     }
     if (a.M == 2) {
-      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 2, SIMPLE>), dim3(nb, 1), dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 2, SIMPLE>), dim3(nb, 1), dim3(kThreads), 0, s, a.A, a.lda,
+                       a.W, a.epi.scol, a.epi.srow, a.K, a.N, a.M, a.epi.scol_per_tensor, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 1, SIMPLE>), dim3(nb, a.M), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 1, SIMPLE>), dim3(nb, a.M), dim3(kThreads), 0, s, a.A, a.lda,
+                       a.W, a.epi.scol, a.epi.srow, a.K, a.N, a.M, a.epi.scol_per_tensor, a);
   return hipGetLastError();
 }
 

@@ -71,6 +71,22 @@ __device__ __forceinline__ int xcd_block(int x, int n) {
   return r * per + min(r, rem) + k;
 }
 
+// Kernel-argument preloading (the library is built with -amdgpu-kernarg-preload-count): gfx950
+// places the leading scalar kernel arguments in SGPRs at wave launch, so a kernel whose first
+// loads need only those issues them without a kernel-argument round trip. Kernels on the latency
+// path take what their first loads need as leading scalars and the rest as a struct after them.
+// A field of that struct is read through the kernel-argument segment with kload: a volatile scalar
+// load that is issued where it stands (not sunk to its first use), so its latency overlaps the
+// streams already in flight.
+typedef const __attribute__((address_space(4))) char* KArg;
+template <class T>
+__device__ __forceinline__ T kload(KArg p) {
+  return *reinterpret_cast<const volatile __attribute__((address_space(4))) T*>(p);
+}
+__device__ __forceinline__ KArg kernarg_at(size_t offset) {
+  return (KArg)__builtin_amdgcn_kernarg_segment_ptr() + offset;
+}
+
 // Keeps the machine scheduler from moving instructions across this point. Used between groups of
 // loads whose issue order matters for the wait counters (activations before weights before
 // epilogue operands).

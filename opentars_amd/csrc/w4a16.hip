@@ -230,31 +230,44 @@ struct W4Smem {
   // then the digit planes: MR rows x 4 planes x 4C dwords (dynamic)
 };
 
+// What the first loads need (x, lda, the weight and scale pointers, M, N, K) leads the kernel
+// arguments as scalars, preloaded into SGPRs at wave launch; the epilogue's fields follow in `a`
+// and are read through the kernel-argument segment once the streams are in flight.
+struct W4Kernargs {
+  const void* x;
+  int64_t lda;
+  const uint8_t* Wp;
+  const uint16_t* ws;
+  int M, N, K;
+  W4Args a;
+};
+constexpr size_t kW4ArgsOffset = offsetof(W4Kernargs, a);
+static_assert(kW4ArgsOffset == 48, "the preloaded scalars take 48 bytes before the argument block");
+
 template <int NW, int U, int MR, int CPL, bool BF16, bool SIMPLE>
-__global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
+__global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int64_t lda, const uint8_t* Wp,
+                                                             const uint16_t* ws, int M, int N, int K, W4Args a) {
   static_assert(CPL >= 1 && CPL <= 4 && MR * U * 4 <= 64, "K <= 8192; one chain lane per bank");
   constexpr int NT = NW * 64;
   constexpr int AP = (CPL * 256 + NT - 1) / NT;       // aligner passes (K / 8 <= 256 CPL threads)
   using Smem = W4Smem<NW, U, MR, CPL>;
   __shared__ Smem sm;
   extern __shared__ __align__(16) uint32_t planes[];    // [MR][4][4C]
-  // every kernel argument the load batch needs, in one scalar round trip
-  __asm__ volatile("" : : "s"(a.x), "s"(a.lda), "s"(a.Wp), "s"(a.ws), "s"(a.M), "s"(a.N), "s"(a.K));
-  const int C = a.K >> 5;
-  const int G = a.K >> 7;
-  const int A = a.K >> 3;
+  const int C = K >> 5;
+  const int G = K >> 7;
+  const int A = K >> 3;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m0 = blockIdx.y * MR;
   const int n0 = (blockIdx.x * NW + wave) * U;
-  const int64_t row_bytes = a.K >> 1;
+  const int64_t row_bytes = K >> 1;
 
   // 1. activations (per pass: whole waves only; dead lanes of a live wave shadow group 0)
   uint32_t xb[MR][AP][8];
 #pragma unroll
   for (int r = 0; r < MR; ++r) {
-    const char* xrow = static_cast<const char*>(a.x) + min(m0 + r, a.M - 1) * a.lda;
+    const char* xrow = static_cast<const char*>(x) + min(m0 + r, M - 1) * lda;
 #pragma unroll
     for (int p = 0; p < AP; ++p) {
       const int t = p * NT + tid;
@@ -281,8 +294,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
   issue_fence();
   // the wave's group scales: halves [n0 G, (n0 + U) G) as dwords (G is even), clamped at the end
   const int ws_dw = (U * G) >> 1;
-  const uint32_t* ws32 = reinterpret_cast<const uint32_t*>(a.ws);
-  const int64_t ws_last = (static_cast<int64_t>(a.N) * G >> 1) - 1;
+  const uint32_t* ws32 = reinterpret_cast<const uint32_t*>(ws);
+  const int64_t ws_last = (static_cast<int64_t>(N) * G >> 1) - 1;
   constexpr int kWsPer = (U * 32 + 63) / 64;          // dwords per lane: U rows x G <= 64 halves
   uint32_t wsv[kWsPer];
 #pragma unroll
@@ -292,14 +305,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
   v4u wv[U][CPL];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const v4u* wrow = reinterpret_cast<const v4u*>(a.Wp + min(n0 + u, a.N - 1) * row_bytes);
+    const v4u* wrow = reinterpret_cast<const v4u*>(Wp + min(n0 + u, N - 1) * row_bytes);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) wv[u][j] = __builtin_nontemporal_load(wrow + min(lane + 64 * j, C - 1));
   }
   issue_fence();
+  // the epilogue's fields, their loads issued now and waited for at their first use
+  const KArg ka = kernarg_at(kW4ArgsOffset);
+  void* const Y = kload<void*>(ka + offsetof(W4Args, Y));
+  const int64_t ldy = kload<int64_t>(ka + offsetof(W4Args, ldy));
+  const float* const bias = SIMPLE ? nullptr : kload<const float*>(ka + offsetof(W4Args, bias));
+  const int act = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, act));
+  const int out = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, out));
+  const float out_scale = SIMPLE ? 0.0f : kload<float>(ka + offsetof(W4Args, out_scale));
   const int ce = lane >> 2, bank = lane & 3;          // chain lane: (m, u) = (ce / U, ce % U)
   const int ue = ce % U, me = ce / U;
-  const float bias_v = SIMPLE ? 0.0f : *(a.bias ? a.bias + min(n0 + ue, a.N - 1) : reinterpret_cast<const float*>(a.ws));
+  float bias_v = 0.0f;
 
   // 2. alignment into LDS digit planes
 #pragma unroll
@@ -321,6 +342,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
       }
     }
   }
+  if constexpr (!SIMPLE) bias_v = *(bias ? bias + min(n0 + ue, N - 1) : reinterpret_cast<const float*>(ws));
   // the wave's scales into its LDS slot (read back by other lanes of the wave after the barrier)
 #pragma unroll
   for (int i = 0; i < kWsPer; ++i)
@@ -358,7 +380,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
         for (int v = 1; v < 4; ++v)
           if (4 * k + v < U) d = q == v ? dots[4 * k + v] : d;
         const float term = fmul(fmul(i2f(d), from_fp16_bits(wsh[min(u, U - 1) * G + g])), xs);
-        if (u < U && c < C && n0 + u < a.N) sm.terms[wave][r * U + u][g] = term;
+        if (u < U && c < C && n0 + u < N) sm.terms[wave][r * U + u][g] = term;
       }
     }
   }
@@ -389,15 +411,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(W4Args a) {
   acc = chain_end(acc);
   const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
   const float other = lane_xor2(pair);
-  if (bank == 0 && ce < MR * U && n0 + ue < a.N && m0 + me < a.M) {
+  if (bank == 0 && ce < MR * U && n0 + ue < N && m0 + me < M) {
     float y = fadd(pair, other);
-    const int64_t yrow = static_cast<int64_t>(m0 + me) * a.ldy;
+    const int64_t yrow = static_cast<int64_t>(m0 + me) * ldy;
     if constexpr (SIMPLE) {
-      reinterpret_cast<float*>(static_cast<char*>(a.Y) + yrow)[n0 + ue] = ftz(y);
+      reinterpret_cast<float*>(static_cast<char*>(Y) + yrow)[n0 + ue] = ftz(y);
     } else {
-      if (a.bias) y = fadd(y, bias_v);
-      y = act_fn(y, a.act);
-      store_out(a.Y, yrow, n0 + ue, a.out, y, a.out_scale);
+      if (bias) y = fadd(y, bias_v);
+      y = act_fn(y, act);
+      store_out(Y, yrow, n0 + ue, out, y, out_scale);
     }
   }
 }
@@ -408,11 +430,11 @@ hipError_t go_w4(const W4Args& a, hipStream_t s) {
   const size_t lds = static_cast<size_t>(MR) * (a.K / 32) * 64;
   const bool simple = !a.bias && a.act == 0 && a.out == 0;
   if (a.bf16) {
-    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, true>), grid, dim3(NW * 64), lds, s, a);
-    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, false>), grid, dim3(NW * 64), lds, s, a);
+    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, true>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
+    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, false>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
   } else {
-    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, true>), grid, dim3(NW * 64), lds, s, a);
-    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, false>), grid, dim3(NW * 64), lds, s, a);
+    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, true>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
+    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, false>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
   }
   return hipGetLastError();
 }
