@@ -538,7 +538,9 @@ def fused_rows_per_wave(rows: int, K: int) -> int:
     while u < 4 and rows // (4 * 2 * u) >= 256:
         u *= 2
     wgs = -(-rows // (4 * u))
-    return 2 * u if 256 < wgs < 512 else u
+    if 256 < wgs < 512:
+        return 6 if K <= 1024 and -(-rows // 24) <= 256 else 2 * u
+    return u
 
 
 def kernel_instance(l: Launch) -> str:

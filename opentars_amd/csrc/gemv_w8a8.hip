@@ -436,8 +436,10 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   issue_fence();  // nothing that waits for the kernel-argument load moves above the streams
   // a whole-wave row (L = 64) ends its reduction scattered: the lane that stores row u is the
   // first lane holding u's total (wave_sum_scatter)
-  const int ne = n0 + (L == 64 ? scatter_row<U>(lane) : sub);
-  const bool epi_lane = (L == 64 ? scatter_owner<U>(lane) : sub < U) && ne < N;
+  constexpr int UP = U == 6 ? 8 : U;  // six rows reduce as eight (two zero rows)
+  const int eu = L == 64 ? scatter_row<UP>(lane) : sub;
+  const int ne = n0 + eu;
+  const bool epi_lane = (L == 64 ? scatter_owner<UP>(lane) : true) && eu < U && ne < N;
   // the epilogue operands' addresses from the kernel arguments: read here, through the
   // kernel-argument segment (volatile: the loads stay here instead of sinking to their use), and
   // waited for only after the row maximum
@@ -539,7 +541,10 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
 
   int mine = 0;
   if constexpr (L == 64) {
-    mine = wave_sum_scatter<U>(acc);
+    int accp[UP];
+#pragma unroll
+    for (int u = 0; u < UP; ++u) accp[u] = u < U ? acc[u] : 0;
+    mine = wave_sum_scatter<UP>(accp);
   } else {
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[u] = group_sum<L>(acc[u]);
@@ -566,15 +571,15 @@ int plain_rows_per_wave(int64_t rows) { return rows < 32768 ? 1 : 4; }
 // Fused quantize + GEMV: every workgroup re-quantizes the activation row, so U is the largest of
 // 1, 2, 4 that still leaves >= 256 workgroups, doubled when the grid would fill one wave of
 // workgroups and part of a second (256 < workgroups < 512). Measured: q/k/v (4096 rows, K = 1024)
-// 3.15 us at U = 4 (3.59 at 2, 3.43 at 8); gate/up (6144 rows) 3.65 us at U = 8 (3.72 at 4);
+// 3.15 us at U = 4 (3.59 at 2, 3.43 at 8); gate/up (6144 rows) 3.65 us at U = 8 (3.72 at 4),
+// or six rows per wave where the chunks fit one per lane (K <= 1024): 256 workgroups, one per CU;
 // o (K = 2048) and down (K = 3072), 1024 rows, 2.85 / 3.11 us at U = 1 (3.10 / 3.38 at 2); the
 // head (151936 rows) 25.5 us at U = 4 (26.7 at 8).
 int fused_rows_per_wave(int64_t rows, int K) {
-  (void)K;
   int u = 1;
   while (u < 4 && rows / (kWaves * 2 * u) >= 256) u *= 2;
   const int64_t wgs = (rows + kWaves * u - 1) / (kWaves * u);
-  if (wgs > 256 && wgs < 512) u *= 2;
+  if (wgs > 256 && wgs < 512) u = K <= 1024 && (rows + kWaves * 6 - 1) / (kWaves * 6) <= 256 ? 6 : 2 * u;
   return u;
 }
 
@@ -686,7 +691,7 @@ hipError_t dispatch(Args& a, int K, int u, hipStream_t s) {
   switch ((C + 63) / 64) {
     case 1:
       return u == 1 ? Go<64, 1, 1>::run(a, s) : u == 2 ? Go<64, 1, 2>::run(a, s)
-           : u == 4 ? Go<64, 1, 4>::run(a, s) : Go<64, 1, 8>::run(a, s);
+           : u == 4 ? Go<64, 1, 4>::run(a, s) : u == 6 ? Go<64, 1, 6>::run(a, s) : Go<64, 1, 8>::run(a, s);
     case 2:
       return u == 1 ? Go<64, 2, 1>::run(a, s) : u == 2 ? Go<64, 2, 2>::run(a, s) : Go<64, 2, 4>::run(a, s);
     case 3: return u == 1 ? Go<64, 3, 1>::run(a, s) : Go<64, 3, 2>::run(a, s);

@@ -584,6 +584,21 @@ def test_fused_equal_row_pieces(Ns, K, M):
         assert same(host(y), want), (Ns, mismatch(host(y), want))
 
 
+@pytest.mark.parametrize("Ns,K", [([3072, 3072], 1024), ([2992, 2992], 1024), ([2560, 2560, 512], 512),
+                                   ([3000 - 8, 3000 - 8], 768)])
+def test_fused_six_rows_per_wave(Ns, K):
+    """Launches of 5000-6500 rows at K <= 1024 run six weight rows per wave (the row sums reduced as
+    eight with two zero rows, 24 rows per workgroup): full and partial last row blocks."""
+    rng = np.random.default_rng(sum(Ns) + K)
+    x = rng.normal(0, 1, (1, K)).astype(f32)
+    Ws = [rng.integers(-128, 128, (N, K), dtype=np.int8) for N in Ns]
+    scs = [rng.uniform(1e-3, 1e-2, N).astype(f32) for N in Ns]
+    outs = ops.quant_gemm_rowcol(cuda(x), [(cuda(W), cuda(sc)) for W, sc in zip(Ws, scs)])
+    q, s = F.quant_rows(x)
+    for W, sc, y in zip(Ws, scs, outs):
+        assert same(host(y), G.gemm_rowcol(q, s, W, sc)), (Ns, mismatch(host(y), G.gemm_rowcol(q, s, W, sc)))
+
+
 def test_fused_qwen3_layer_groups_full_size():
     """q/k/v (2048 + 1024 + 1024 rows) and gate/up (2 x 3072 rows) at K = 1024, and the head."""
     rng = np.random.default_rng(123)
