@@ -63,7 +63,7 @@ SIGNATURES = {
     "tars_relu": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_uint32, c_int32, c_int32, c_void_p]),
     "tars_fdot": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_int32, c_uint32,
                           c_int32, c_int32, c_int32, c_void_p]),
-    "tars_queue_fusion_counts": (c_int, [POINTER(c_int64), c_int32]),
+    "tars_queue_fusion_counts": (c_int, [POINTER(c_int64), c_int32, c_int32]),
     "tars_embed_rows": (c_int, [c_void_p, c_int64, c_int64, c_int32, POINTER(c_int32), c_int32, c_int32, c_uint32,
                                 c_void_p, c_int64, c_void_p]),
     "tars_attention": (c_int, [POINTER(c_void_p), c_int64, POINTER(c_void_p), c_int64, POINTER(c_void_p), c_int64,

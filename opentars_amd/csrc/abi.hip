@@ -104,6 +104,95 @@ namespace tars {
 void set_last_error(const std::string& what) { g_last_error = what; }
 // The W8A8 kernel-family switch (tars_set_w8a8_path).
 int w8a8_path() { return g_w8a8_path; }
+
+// tars_quant_gemm_w8a8's checks and launch, with the gated product (QuantGemvArgs::prod) for the
+// queue executor's MLP fusion: prod rows must not overlap an input, the quantized rows or Y1, and
+// either are Y0's rows exactly (in place) or overlap no output.
+int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s, int32_t M, int32_t K,
+                            const tars_w8a8_out* outs, int32_t nouts, float* prod, int64_t ldprod, void* stream) {
+  g_last_error.clear();
+  if (!x || !outs) return fail(TARS_E_ARG, "NULL pointer");
+  if ((q == nullptr) != (s == nullptr)) return fail(TARS_E_ARG, "q and s are both given or both NULL");
+  if (nouts < 1 || nouts > tars::kMaxGroups) return fail(TARS_E_ARG, "1 <= nouts <= 4");
+  for (int i = 0; i < nouts; ++i) {
+    const tars_w8a8_out& o = outs[i];
+    if (!o.W || !o.scol || !o.Y) return fail(TARS_E_ARG, "NULL pointer in an output descriptor");
+    if (int rc = check_epilogue(o.act, o.out, o.out_scale_bits)) return rc;
+  }
+  if (K > 65535) return fail(TARS_E_FIELD, "K must fit the 16-bit field (|acc| < 2^31)");
+  if (M <= 0 || K <= 0 || K % 16) return fail(TARS_E_ALIGN, "M >= 1, K >= 16 and K % 16 == 0");
+  if (lda == 0) lda = 4LL * K;
+  if (q && ldq == 0) ldq = K;
+  if (lda < 4LL * K || lda % 16 || (q && (ldq < K || ldq % 16)))
+    return fail(TARS_E_ALIGN, "strides must be multiples of 16 holding a row");
+  if (!aligned(x, 16) || (q && (!aligned(q, 16) || !aligned(s, 16)))) return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+  std::vector<std::vector<Span>> yout(nouts);
+  std::vector<int64_t> ldys(nouts);
+  for (int i = 0; i < nouts; ++i) {
+    const tars_w8a8_out& o = outs[i];
+    const int64_t yrow = static_cast<int64_t>(o.N) * esize(o.out);
+    ldys[i] = o.ldy == 0 ? yrow : o.ldy;
+    if (o.N <= 0 || o.N % 16) return fail(TARS_E_ALIGN, "N >= 16 and N % 16 == 0");
+    if (ldys[i] < yrow || ldys[i] % 16) return fail(TARS_E_ALIGN, "output stride must be a multiple of 16 holding a row");
+    if (!aligned(o.W, 16) || !aligned(o.scol, 16) || !aligned(o.Y, 16) || (o.bias && !aligned(o.bias, 16)))
+      return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
+    if (!extent_ok(o.W, K, o.N, K) || !extent_ok(o.Y, ldys[i], M, yrow)) return fail(TARS_E_RANGE, "extent overflows");
+    yout[i] = rows(o.Y, ldys[i], M, yrow);
+  }
+  if (!extent_ok(x, lda, M, 4LL * K) || (q && !extent_ok(q, ldq, M, K))) return fail(TARS_E_RANGE, "extent overflows");
+  // inputs: x and every matrix's W / scol / bias; outputs: q, s and every Y
+  std::vector<Span> inputs = rows(x, lda, M, 4LL * K);
+  for (int i = 0; i < nouts; ++i) {
+    const tars_w8a8_out& o = outs[i];
+    auto w = one(o.W, static_cast<int64_t>(o.N) * K), sc = one(o.scol, 4LL * o.N);
+    inputs.insert(inputs.end(), w.begin(), w.end());
+    inputs.insert(inputs.end(), sc.begin(), sc.end());
+    if (o.bias) inputs.push_back(one(o.bias, 4LL * o.N)[0]);
+  }
+  std::vector<std::vector<Span>> outputs = yout;
+  bool prod_in_place = false;
+  if (prod) {  // the gated product: two fp32 matrices of one height, stored at prod (or in place over Y0)
+    if (nouts != 2 || outs[0].N != outs[1].N || outs[0].out != 0 || outs[1].out != 0)
+      return fail(TARS_E_ARG, "the gated product takes two fp32 outputs of one height");
+    if (!tars::quant_gemv_pairs_supported(K)) return fail(TARS_E_FIELD, "the gated product is not available at this K");
+    const int64_t prow = 4LL * outs[0].N;
+    if (ldprod == 0) ldprod = prow;
+    if (!aligned(prod, 16) || ldprod < prow || ldprod % 16) return fail(TARS_E_ALIGN, "product: 16-byte aligned rows");
+    if (!extent_ok(prod, ldprod, M, prow)) return fail(TARS_E_RANGE, "extent overflows");
+    prod_in_place = prod == outs[0].Y && (M == 1 || ldprod == ldys[0]);  // one row: the strides never apply
+    if (!prod_in_place) outputs.push_back(rows(prod, ldprod, M, prow));
+  }
+  if (q) {
+    outputs.push_back(rows(q, ldq, M, K));
+    outputs.push_back(one(s, 4LL * M));
+  }
+  for (size_t i = 0; i < outputs.size(); ++i) {
+    if (overlaps(inputs, outputs[i])) return fail(TARS_E_OVERLAP, "an output overlaps an input");
+    for (size_t j = 0; j < i; ++j)
+      if (overlaps(outputs[j], outputs[i])) return fail(TARS_E_OVERLAP, "two outputs overlap");
+  }
+  tars::QuantGemvArgs a{};
+  a.x = x;
+  a.lda = lda;
+  a.q = q;
+  a.ldq = ldq;
+  a.s = s;
+  a.M = M;
+  a.K = K;
+  a.ngroups = nouts;
+  a.prod = prod;
+  a.ldprod = ldprod;
+  for (int i = 0; i < nouts; ++i) {
+    const tars_w8a8_out& o = outs[i];
+    a.g[i].W = o.W;
+    a.g[i].epi = tars::RowColEpilogue{nullptr, o.scol, 0, o.bias, o.act, o.out, f32_of(o.out_scale_bits)};
+    a.g[i].Y = o.Y;
+    a.g[i].ldy = ldys[i];
+    a.g[i].N = o.N;
+  }
+  return launched(tars::launch_quant_gemv_w8a8(a, static_cast<hipStream_t>(stream)));
+}
+
 }  // namespace tars
 
 extern "C" {
@@ -182,73 +271,7 @@ int tars_gemm_w8a8(const int8_t* A, int64_t lda, const float* srow, const int8_t
 int tars_quant_gemm_w8a8(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s,
                          int32_t M, int32_t K, const tars_w8a8_out* outs, int32_t nouts,
                          void* stream) {
-  g_last_error.clear();
-  if (!x || !outs) return fail(TARS_E_ARG, "NULL pointer");
-  if ((q == nullptr) != (s == nullptr)) return fail(TARS_E_ARG, "q and s are both given or both NULL");
-  if (nouts < 1 || nouts > tars::kMaxGroups) return fail(TARS_E_ARG, "1 <= nouts <= 4");
-  for (int i = 0; i < nouts; ++i) {
-    const tars_w8a8_out& o = outs[i];
-    if (!o.W || !o.scol || !o.Y) return fail(TARS_E_ARG, "NULL pointer in an output descriptor");
-    if (int rc = check_epilogue(o.act, o.out, o.out_scale_bits)) return rc;
-  }
-  if (K > 65535) return fail(TARS_E_FIELD, "K must fit the 16-bit field (|acc| < 2^31)");
-  if (M <= 0 || K <= 0 || K % 16) return fail(TARS_E_ALIGN, "M >= 1, K >= 16 and K % 16 == 0");
-  if (lda == 0) lda = 4LL * K;
-  if (q && ldq == 0) ldq = K;
-  if (lda < 4LL * K || lda % 16 || (q && (ldq < K || ldq % 16)))
-    return fail(TARS_E_ALIGN, "strides must be multiples of 16 holding a row");
-  if (!aligned(x, 16) || (q && (!aligned(q, 16) || !aligned(s, 16)))) return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
-  std::vector<std::vector<Span>> yout(nouts);
-  std::vector<int64_t> ldys(nouts);
-  for (int i = 0; i < nouts; ++i) {
-    const tars_w8a8_out& o = outs[i];
-    const int64_t yrow = static_cast<int64_t>(o.N) * esize(o.out);
-    ldys[i] = o.ldy == 0 ? yrow : o.ldy;
-    if (o.N <= 0 || o.N % 16) return fail(TARS_E_ALIGN, "N >= 16 and N % 16 == 0");
-    if (ldys[i] < yrow || ldys[i] % 16) return fail(TARS_E_ALIGN, "output stride must be a multiple of 16 holding a row");
-    if (!aligned(o.W, 16) || !aligned(o.scol, 16) || !aligned(o.Y, 16) || (o.bias && !aligned(o.bias, 16)))
-      return fail(TARS_E_ALIGN, "pointers must be 16-byte aligned");
-    if (!extent_ok(o.W, K, o.N, K) || !extent_ok(o.Y, ldys[i], M, yrow)) return fail(TARS_E_RANGE, "extent overflows");
-    yout[i] = rows(o.Y, ldys[i], M, yrow);
-  }
-  if (!extent_ok(x, lda, M, 4LL * K) || (q && !extent_ok(q, ldq, M, K))) return fail(TARS_E_RANGE, "extent overflows");
-  // inputs: x and every matrix's W / scol / bias; outputs: q, s and every Y
-  std::vector<Span> inputs = rows(x, lda, M, 4LL * K);
-  for (int i = 0; i < nouts; ++i) {
-    const tars_w8a8_out& o = outs[i];
-    auto w = one(o.W, static_cast<int64_t>(o.N) * K), sc = one(o.scol, 4LL * o.N);
-    inputs.insert(inputs.end(), w.begin(), w.end());
-    inputs.insert(inputs.end(), sc.begin(), sc.end());
-    if (o.bias) inputs.push_back(one(o.bias, 4LL * o.N)[0]);
-  }
-  std::vector<std::vector<Span>> outputs = yout;
-  if (q) {
-    outputs.push_back(rows(q, ldq, M, K));
-    outputs.push_back(one(s, 4LL * M));
-  }
-  for (size_t i = 0; i < outputs.size(); ++i) {
-    if (overlaps(inputs, outputs[i])) return fail(TARS_E_OVERLAP, "an output overlaps an input");
-    for (size_t j = 0; j < i; ++j)
-      if (overlaps(outputs[j], outputs[i])) return fail(TARS_E_OVERLAP, "two outputs overlap");
-  }
-  tars::QuantGemvArgs a{};
-  a.x = x;
-  a.lda = lda;
-  a.q = q;
-  a.ldq = ldq;
-  a.s = s;
-  a.M = M;
-  a.K = K;
-  a.ngroups = nouts;
-  for (int i = 0; i < nouts; ++i) {
-    const tars_w8a8_out& o = outs[i];
-    a.g[i].W = o.W;
-    a.g[i].epi = tars::RowColEpilogue{nullptr, o.scol, 0, o.bias, o.act, o.out, f32_of(o.out_scale_bits)};
-    a.g[i].Y = o.Y;
-    a.g[i].ldy = ldys[i];
-    a.g[i].N = o.N;
-  }
-  return launched(tars::launch_quant_gemv_w8a8(a, static_cast<hipStream_t>(stream)));
+  return tars::quant_gemm_w8a8_checked(x, lda, q, ldq, s, M, K, outs, nouts, nullptr, 0, stream);
 }
 
 int tars_gemm_w8a8_ksplit(const int8_t* A, int64_t lda, const float* srow,

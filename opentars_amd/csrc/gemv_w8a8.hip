@@ -384,14 +384,18 @@ struct QuantGemvKernargs {
 constexpr size_t kQuantGemvArgsOffset = offsetof(QuantGemvKernargs, a);
 static_assert(kQuantGemvArgsOffset == 56, "the preloaded scalars take 56 bytes before the argument block");
 
-template <int L, int CPL, int U, bool SIMPLE>
+template <int L, int CPL, int U, bool SIMPLE, bool PAIR>
 __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* x, int64_t lda, const int8_t* W0,
                                                                    const int8_t* W1, const int8_t* W2,
                                                                    const int8_t* W3, int K, int N, QuantGemvArgs a) {
   extern __shared__ __align__(16) int8_t qsh[];  // the quantized row, K bytes
   __shared__ uint32_t wave_max[kWaves];
+  // PAIR: a wave's U rows are U / 2 row pairs (row n of matrix 0, row n of matrix 1), for the gated
+  // product; otherwise U rows of matrix z
+  static_assert(!PAIR || (L == 64 && CPL > 0 && U % 2 == 0), "row pairs on whole-wave rows");
   constexpr int kSlots = 64 / L;
-  constexpr int kRows = kWaves * kSlots * U;  // weight rows per workgroup
+  constexpr int UR = PAIR ? U / 2 : U;          // row indices per wave
+  constexpr int kRows = kWaves * kSlots * UR;  // row indices per workgroup
   const int z = blockIdx.z;
   const int8_t* W = z == 0 ? W0 : z == 1 ? W1 : z == 2 ? W2 : W3;
   const GemvGroup& gr = a.g[z];
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   const int m = blockIdx.y;
   const int C = K >> 4;
   const int K4 = K >> 2;
-  const int n0 = (xcd_block(blockIdx.x, nblk) * (kWaves * kSlots) + wave * kSlots + slot) * U;
+  const int n0 = (xcd_block(blockIdx.x, nblk) * (kWaves * kSlots) + wave * kSlots + slot) * UR;
   const v4i zero = {0, 0, 0, 0};
 
   // one batch of loads: the fp32 activations (the quantizer waits on them alone), the weights
@@ -424,22 +428,26 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   if constexpr (CPL > 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int n = n0 + u;
-      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K);
+      const int n = n0 + (PAIR ? u % UR : u);
+      const int8_t* Wu = PAIR && u >= UR ? W1 : W;
+      const v4i* wrow = reinterpret_cast<const v4i*>(Wu + static_cast<int64_t>(n) * K);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = sub + j * L;
-        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : reinterpret_cast<const v4i*>(W));
+        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : reinterpret_cast<const v4i*>(Wu));
       }
     }
   }
   issue_fence();  // nothing that waits for the kernel-argument load moves above the streams
   // a whole-wave row (L = 64) ends its reduction scattered: the lane that stores row u is the
   // first lane holding u's total (wave_sum_scatter)
+  // PAIR: values 2p and 2p + 1 are pair p's rows of matrices 0 and 1, which land on lanes l and
+  // l ^ 32 (scatter_row's bit 0 is lane bit 5); the lane of matrix 0's row finishes the pair
   constexpr int UP = U == 6 ? 8 : U;  // six rows reduce as eight (two zero rows)
   const int eu = L == 64 ? scatter_row<UP>(lane) : sub;
-  const int ne = n0 + eu;
-  const bool epi_lane = (L == 64 ? scatter_owner<UP>(lane) : true) && eu < U && ne < N;
+  const int er = PAIR ? eu >> 1 : eu;
+  const int ne = n0 + er;
+  const bool epi_lane = (L == 64 ? scatter_owner<UP>(lane) : true) && (!PAIR || lane < 32) && er < UR && ne < N;
   // the epilogue operands' addresses from the kernel arguments: read here, through the
   // kernel-argument segment (volatile: the loads stay here instead of sinking to their use), and
   // waited for only after the row maximum
@@ -450,7 +458,11 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   const float* const bias = SIMPLE ? nullptr : kload<const float*>(kg + offsetof(RowColEpilogue, bias));
   int8_t* const qout = kload<int8_t*>(ka + offsetof(QuantGemvArgs, q));  // the optional ROW_QUANT outputs
   const int64_t ldq = kload<int64_t>(ka + offsetof(QuantGemvArgs, ldq));
-  float sc, bi;
+  KArg kg1 = ka + offsetof(QuantGemvArgs, g) + sizeof(GemvGroup) + offsetof(GemvGroup, epi);  // PAIR: matrix 1
+  const float* const scol1 = PAIR ? kload<const float*>(kg1 + offsetof(RowColEpilogue, scol)) : nullptr;
+  const int per_tensor1 = PAIR ? kload<int>(kg1 + offsetof(RowColEpilogue, scol_per_tensor)) : 0;
+  const float* const bias1 = PAIR && !SIMPLE ? kload<const float*>(kg1 + offsetof(RowColEpilogue, bias)) : nullptr;
+  float sc, bi, sc1 = 0.0f, bi1 = 0.0f;
 
   // the workgroup quantizes row m into LDS
   uint32_t mx = 0;
@@ -471,6 +483,10 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   // kernel-argument load, which is then long done)
   sc = scol[per_tensor || !epi_lane ? 0 : ne];
   bi = *(bias ? bias + (epi_lane ? ne : 0) : scol);
+  if constexpr (PAIR) {
+    sc1 = scol1[per_tensor1 || !epi_lane ? 0 : ne];
+    bi1 = *(bias1 ? bias1 + (epi_lane ? ne : 0) : scol1);
+  }
   __syncthreads();
   // the row maximum is uniform: one scalar value, and a branch (not a select) between the q8 forms
   mx = flush_max_bits(__builtin_amdgcn_readfirstlane(max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]))));
@@ -540,11 +556,16 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   }
 
   int mine = 0;
+  int mine1 = 0;  // PAIR: the total of matrix 1's row, from lane l ^ 32
   if constexpr (L == 64) {
     int accp[UP];
 #pragma unroll
-    for (int u = 0; u < UP; ++u) accp[u] = u < U ? acc[u] : 0;
+    for (int u = 0; u < UP; ++u) {
+      const int src = PAIR ? (u & 1) * UR + (u >> 1) : u;  // PAIR: 2p -> row p of matrix 0, 2p + 1 -> of matrix 1
+      accp[u] = (PAIR ? (u >> 1) < UR : u < U) ? acc[min(src, U - 1)] : 0;
+    }
     mine = wave_sum_scatter<UP>(accp);
+    if constexpr (PAIR) mine1 = static_cast<int>(__builtin_amdgcn_permlane32_swap(mine, mine, false, false)[1]);
   } else {
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[u] = group_sum<L>(acc[u]);
@@ -553,7 +574,17 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
       if (sub == u) mine = acc[u];
   }
   if (epi_lane) {
-    if constexpr (SIMPLE) {
+    if constexpr (PAIR) {
+      // both outputs fp32: the stored values are ftz(y0), ftz(y1), which fmul flushes the same way
+      const GemvGroup& g1 = a.g[1];
+      const float y0 = SIMPLE ? simple_epilogue(mine, sr, sc) : gr.epi.apply(mine, sr, true, sc, bi);
+      const float y1 = SIMPLE ? simple_epilogue(mine1, sr, sc1) : g1.epi.apply(mine1, sr, true, sc1, bi1);
+      float* const y0row = reinterpret_cast<float*>(static_cast<char*>(gr.Y) + m * gr.ldy);
+      float* const prow = reinterpret_cast<float*>(reinterpret_cast<char*>(a.prod) + m * a.ldprod);
+      reinterpret_cast<float*>(static_cast<char*>(g1.Y) + m * g1.ldy)[ne] = ftz(y1);
+      if (prow != y0row) y0row[ne] = ftz(y0);
+      prow[ne] = fmul(y0, y1);
+    } else if constexpr (SIMPLE) {
       reinterpret_cast<float*>(static_cast<char*>(gr.Y) + m * gr.ldy)[ne] = simple_epilogue(mine, sr, sc);
     } else {
       const float y = gr.epi.apply(mine, sr, true, sc, bi);
@@ -628,9 +659,25 @@ int gcd(int a, int b) {
 // four pieces of 1024), so every z slice has the same number of workgroups. Each launch takes up
 // to four consecutive pieces of one height (the kernel's preloaded arguments hold four matrix
 // pointers and one N); other shapes take more than one launch.
+// Instances with row pairs (the gated product): whole-wave rows of up to four chunks per lane, one
+// to three pairs per wave.
+template <int L, int CPL, int U>
+constexpr bool kPairs = L == 64 && CPL >= 1 && CPL <= 4 && (U == 2 || U == 4 || U == 6);
+
 template <int L, int CPL, int U, bool SIMPLE>
 hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
+  if (a.prod) {  // two matrices of one height as row pairs, one launch, no pieces
+    if constexpr (kPairs<L, CPL, U>) {
+      const int N = a.g[0].N;
+      const unsigned blocks = (N + kWaves * (U / 2) - 1) / (kWaves * (U / 2));
+      const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
+      hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, true>), dim3(blocks, a.M, 1), dim3(kThreads), lds,
+                         s, a.x, a.lda, a.g[0].W, a.g[1].W, a.g[0].W, a.g[0].W, a.K, N, a);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
   int h = 0, rows = 0;
   for (int i = 0; i < a.ngroups; ++i) {
     h = gcd(h, a.g[i].N);
@@ -671,7 +718,7 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
     const int8_t* Wz[4];
     for (int i = 0; i < 4; ++i) Wz[i] = b.g[i < n ? i : 0].W;
     const unsigned blocks = (N + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE>), dim3(blocks, a.M, n), dim3(kThreads), lds, s,
+    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, false>), dim3(blocks, a.M, n), dim3(kThreads), lds, s,
                        a.x, a.lda, Wz[0], Wz[1], Wz[2], Wz[3], a.K, N, b);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -728,7 +775,14 @@ hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s) {
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
   int64_t rows = 0;
   for (int i = 0; i < a.ngroups; ++i) rows += a.g[i].N;
-  return dispatch<QuantGemvArgs, GoFused>(a, a.K, fused_rows_per_wave(rows, a.K), s);
+  int u = fused_rows_per_wave(rows, a.K);
+  if (a.prod) u = u == 1 ? 2 : u == 8 ? 4 : u;  // an even number of rows: whole pairs
+  return dispatch<QuantGemvArgs, GoFused>(a, a.K, u, s);
+}
+
+bool quant_gemv_pairs_supported(int K) {
+  const int C = K / 16;  // whole-wave rows (more than 32 chunks), at most four chunks per lane
+  return K % 16 == 0 && C > 32 && C <= 256;
 }
 
 // K split up to a total K of 8192: four waves per row (measured on MI355X at C2, K = 6912 in two

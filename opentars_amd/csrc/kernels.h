@@ -173,6 +173,12 @@ struct QuantGemvArgs {
   int M, K;
   GemvGroup g[kMaxPieces];
   int ngroups;  // matrix (piece) g runs as grid z = g
+  // Optional gated product (an MLP's act(gate) * up): with ngroups == 2 and equal N, rows n of
+  // matrix 0 and matrix 1 are computed by the same lane and fmul(y0[n], y1[n]) (the contract's
+  // ELT MUL of the two fp32 outputs) is also stored to prod[m * ldprod / 4 + n]. prod may be g[0].Y
+  // (in place: then only the product is stored there); fp32 outputs only.
+  float* prod;
+  int64_t ldprod;
 };
 
 // Row functions, elementwise ops, rotary embedding and fp32 dot products (rowops.hip). Row strides
@@ -321,6 +327,7 @@ hipError_t launch_fdot(const FdotArgs& a, hipStream_t s);
 hipError_t launch_quant_rows(const QuantArgs& a, hipStream_t s);
 hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s);
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s);
+bool quant_gemv_pairs_supported(int K);  // whether a.prod (the gated product) can run at this K
 hipError_t launch_gemm_w8a8_mfma(const W8A8Args& a, hipStream_t s);
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s);
 hipError_t launch_gemm_w8a8_ksplit_mfma(const KSplitArgs& a, hipStream_t s);

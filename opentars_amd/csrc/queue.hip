@@ -511,6 +511,8 @@ int launch(uint8_t* image, const Desc& d, hipStream_t stream, bool& needs_host) 
 namespace tars {
 void set_last_error(const std::string& what);
 int w8a8_path();
+int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s, int32_t M, int32_t K,
+                            const tars_w8a8_out* outs, int32_t nouts, float* prod, int64_t ldprod, void* stream);
 }  // namespace tars
 
 namespace {
@@ -527,7 +529,10 @@ u128 addr(const Desc& d, Field off) { return static_cast<u128>(d[F_BASE_ADDR]) +
 // of the queue; when the group's outputs overlap each other or any input of the group, the fused
 // call refuses before launching and the descriptors run one by one. `fused` = GEMMs folded in.
 // One ROW_QUANT (M = 1) and the GEMMs reading its output, as one tars_quant_gemm_w8a8 call.
-int launch_fused(uint8_t* image, const Desc& dq, const std::vector<Desc>& members, hipStream_t s) {
+// With `elt` (a gated group): the two GEMMs' ELT MUL runs in the same launch (the product of the
+// fp32 outputs stored at the ELT's output, see fuse_group).
+int launch_fused(uint8_t* image, const Desc& dq, const std::vector<Desc>& members, hipStream_t s,
+                 const Desc* elt = nullptr) {
   tars_w8a8_out outs[4];
   for (size_t k = 0; k < members.size(); ++k) {
     const Desc& d = members[k];
@@ -544,17 +549,36 @@ int launch_fused(uint8_t* image, const Desc& dq, const std::vector<Desc>& member
   }
   uint8_t* B = image + dq[F_BASE_ADDR];
   const Strides sq = strides(dq);
-  return tars_quant_gemm_w8a8(reinterpret_cast<const float*>(B + dq[F_A_OFF]), static_cast<int64_t>(sq.lda),
-                              reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
-                              reinterpret_cast<float*>(B + dq[F_SCALE_OFF]), 1, static_cast<int32_t>(dq[F_N]), outs,
-                              static_cast<int32_t>(members.size()), s);
+  float* prod = elt ? reinterpret_cast<float*>(image + (*elt)[F_BASE_ADDR] + (*elt)[F_Y_OFF]) : nullptr;
+  return tars::quant_gemm_w8a8_checked(reinterpret_cast<const float*>(B + dq[F_A_OFF]), static_cast<int64_t>(sq.lda),
+                                       reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
+                                       reinterpret_cast<float*>(B + dq[F_SCALE_OFF]), 1, static_cast<int32_t>(dq[F_N]),
+                                       outs, static_cast<int32_t>(members.size()), prod,
+                                       elt ? static_cast<int64_t>(strides(*elt).ldy) : 0, s);
+}
+
+// An MLP's gated product after a two-GEMM group (tars_mini/llm.py:620-624: the gate GEMM with its
+// activation, the up GEMM, then ELT MUL of their outputs): a dense fp32 ELT MUL with no activation
+// over one row whose A operand is exactly the first GEMM's output and whose B operand is exactly
+// the second's, both GEMMs storing fp32. The fused launch stores the second output, the product at
+// the ELT's output and, unless that is the first output itself (in place), the first output:
+// the same bytes as the three descriptors one by one (the ELT multiplies the stored fp32 values,
+// which are the kernel's flushed epilogue values).
+bool gated_elt(const Checked& e, const Desc& g0, const Desc& g1, uintptr_t image) {
+  const Desc& d = e.d;
+  return e.err == E_OK && !e.overlap && d[F_OPCODE] == OP_ELT && (d[F_CTRL] & 3) == ELT_MUL &&
+         act_code(d[F_EPI]) == 0 && out_code(d[F_EPI]) == OUT_FP32 && (d[F_HDR_RSV] & (3 | 4 | kStateFp16)) == BM_DENSE &&
+         d[F_M] == 1 && d[F_N] == g0[F_N] && d[F_N] == g1[F_N] && out_code(g0[F_EPI]) == OUT_FP32 &&
+         out_code(g1[F_EPI]) == OUT_FP32 && addr(d, F_A_OFF) == addr(g0, F_Y_OFF) && addr(d, F_W_OFF) == addr(g1, F_Y_OFF) &&
+         (image + d[F_BASE_ADDR] + d[F_Y_OFF]) % 16 == 0 && tars::quant_gemv_pairs_supported(static_cast<int>(g0[F_K]));
 }
 
 int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
                int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
-               int& fused, std::vector<Desc>& group) {
+               int& fused, std::vector<Desc>& group, Desc& elt, bool& gated) {
   fused = 0;
   group.clear();
+  gated = false;
   const Desc& dq = quant.d;
   if (!g_fusion || dq[F_OPCODE] != OP_ROW || dq[F_M] != 1 || (reinterpret_cast<uintptr_t>(image) + dq[F_BASE_ADDR]) % 16)
     return TARS_OK;
@@ -577,6 +601,22 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
       if (overlaps(rest, c.y)) return TARS_OK;
   }
   for (const Checked& c : members) group.push_back(c.d);
+  const int32_t je = i + 3;  // the gated product's ELT MUL, right after a two-GEMM group
+  if (members.size() == 2 && je < n && static_cast<uint64_t>(je) < in_image) {
+    const Checked e = check(q.data() + static_cast<size_t>(je) * kDescBytes, image_len, core_id, gemv_only);
+    if (gated_elt(e, members[0].d, members[1].d, reinterpret_cast<uintptr_t>(image)) &&
+        !(rest_lo < rest_hi && overlaps(rest, e.y))) {
+      const int rc = launch_fused(image, dq, group, s, &e.d);
+      if (rc == TARS_OK) {
+        fused = 3;
+        elt = e.d;
+        gated = true;
+        return rc;
+      }
+      if (rc != TARS_E_OVERLAP) return rc;
+      tars::set_last_error("");  // the product overlaps an operand: the ELT runs on its own
+    }
+  }
   const int rc = launch_fused(image, dq, group, s);
   if (rc == TARS_E_OVERLAP) {
     tars::set_last_error("");
@@ -883,6 +923,8 @@ struct Step {
   Desc second{};               // or: the second descriptor of a fused pair with d
   bool add_norm = false;       // d an ELT ADD, second its norm
   bool norm_rope = false;      // d a norm, second its RoPE
+  Desc elt{};                  // a gated group's ELT MUL (gated: group is gate and up)
+  bool gated = false;
 };
 
 struct Plan {
@@ -898,13 +940,16 @@ struct Plan {
 };
 
 // Fused launches run (diagnostics for tests and benchmarks): quantizer + GEMMs, attention,
-// residual ADD + norm, norm + RoPE; counted when a queue is dispatched and when a plan replays.
-std::atomic<int64_t> g_fused_launches[4];
+// residual ADD + norm, norm + RoPE, and (also counted as quantizer + GEMMs) the gated product's
+// ELT MUL folded into its GEMMs; counted when a queue is dispatched and when a plan replays.
+constexpr int kFusionKinds = 5;
+std::atomic<int64_t> g_fused_launches[kFusionKinds];
 
 void count_fused(const std::vector<Step>& steps) {
   for (const Step& st : steps) {
     const int k = !st.group.empty() ? 0 : !st.attn.empty() ? 1 : st.add_norm ? 2 : st.norm_rope ? 3 : -1;
     if (k >= 0) g_fused_launches[k].fetch_add(1, std::memory_order_relaxed);
+    if (st.gated) g_fused_launches[4].fetch_add(1, std::memory_order_relaxed);
   }
 }
 
@@ -921,7 +966,7 @@ int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) 
                    : st.norm_rope     ? launch_norm_rope_pair(image, st.d, st.second, s)
                    : !st.attn.empty() ? launch_attention_group(image, st.attn, s)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
-                                      : launch_fused(image, st.d, st.group, s);
+                                      : launch_fused(image, st.d, st.group, s, st.gated ? &st.elt : nullptr);
     if (rc != TARS_OK) return rc;
   }
   return TARS_OK;
@@ -1076,13 +1121,21 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     const u128 later = static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(i) + 1);
     int fused = 0;
     std::vector<Desc> group;
+    Desc elt{};
+    bool gated = false;
     if (int rc = fuse_group(image, c, q, i, in_image, n, later, q_end, image_len, core_id, gemv_only != 0, s, fused,
-                            group))
+                            group, elt, gated))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
       g_fused_launches[0].fetch_add(1, std::memory_order_relaxed);
-      if (cacheable) steps.push_back(Step{c.d, std::move(group), {}});
-      i += fused;  // the quantizer and `fused` GEMMs ran as one launch
+      if (gated) g_fused_launches[4].fetch_add(1, std::memory_order_relaxed);
+      if (cacheable) {
+        Step st{c.d, std::move(group), {}};
+        st.elt = elt;
+        st.gated = gated;
+        steps.push_back(std::move(st));
+      }
+      i += fused;  // the quantizer and `fused` GEMMs (and a gated product's ELT) ran as one launch
       continue;
     }
     std::vector<AttnHead> heads;
@@ -1168,10 +1221,11 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
   return TARS_OK;
 }
 
-int tars_queue_fusion_counts(int64_t* counts, int32_t reset) {
-  for (int k = 0; k < 4; ++k) {
+int tars_queue_fusion_counts(int64_t* counts, int32_t ncounts, int32_t reset) {
+  if (ncounts < 0) return TARS_E_ARG;
+  for (int k = 0; k < kFusionKinds; ++k) {
     const int64_t v = reset ? g_fused_launches[k].exchange(0) : g_fused_launches[k].load();
-    if (counts) counts[k] = v;
+    if (counts && k < ncounts) counts[k] = v;
   }
   return TARS_OK;
 }

@@ -546,6 +546,54 @@ def test_repeated_queue_replays_its_plan_on_new_data(seed):
         img = bytearray(gd)
 
 
+def add_gated_mlp(p: Program, N: int, K: int, act: int = 4, inplace: bool = True, gate_out: int = Q.OUT_FP32,
+                  swap: bool = False, prod_over_w: bool = False):
+    """An MLP's gated product (tars_mini/llm.py:620-624): ROW_QUANT of one row, the gate GEMM with
+    its activation (SiLU = 4, GELU = 3) and the up GEMM (QM_ROWCOL, fp32 out), then ELT MUL of their
+    outputs, in place over the gate's rows or apart. swap: the ELT reads up as A and gate as B;
+    prod_over_w: the product lands on the gate GEMM's weights (so it may only be written after the
+    GEMMs: the executor then runs the ELT on its own); gate_out: the gate GEMM's format. The
+    executor folds the ELT into the group only for A = gate, B = up, fp32 outputs, a product that
+    overlaps no operand of the group and K with whole-wave rows of at most four chunks per lane."""
+    q, ldq, s = add_quant(p, 1, K)
+    g = add_w8(p, 1, N, K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s, act=act, out=gate_out, bias=int(p.rng.integers(0, 2)))
+    u = add_w8(p, 1, N, K, Q.QM_ROWCOL, a=q, lda=ldq, srow=s, act=0, out=Q.OUT_FP32, bias=int(p.rng.integers(0, 2)))
+    y = g if inplace else Q.decode(p.descs[-2])["W_OFF"] if prod_over_w else p.alloc(4 * N)
+    a, b = (u, g) if swap else (g, u)
+    p.add(OPCODE=Q.OP_ELT, CTRL=Q.ELT_MUL, EPI=Q.epi(), HDR_RSV=Q.BM_DENSE, A_OFF=a, W_OFF=b, Y_OFF=y, M=1, N=N)
+
+
+@pytest.mark.parametrize("seed", range(3))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_gated_mlp_product(seed, fusion):
+    """ROW_QUANT -> gate GEMM (activation) -> up GEMM -> ELT MUL, which the executor runs as one
+    launch (the gate and up rows of each index on one lane, the product stored with the outputs):
+    the Qwen3-0.6B shape in place and apart, K = 2048 (two chunks per lane) with GELU, a height that
+    leaves a partial last block; not fused: a bf16 gate output, swapped operands, a product over the
+    gate's weights, K = 512 (16-lane rows). The images equal the oracle's."""
+    image = 24 << 20
+    p = Program(8500 + seed, image=image, qaddr=image - 0x10000)
+    add_gated_mlp(p, 3072, 1024)
+    add_gated_mlp(p, 3072, 1024, inplace=False)
+    add_gated_mlp(p, 512, 2048, act=3)
+    add_gated_mlp(p, 112, 768)
+    add_gated_mlp(p, 256, 1024, gate_out=Q.OUT_BF16)
+    add_gated_mlp(p, 256, 1024, inplace=False, swap=True)
+    add_gated_mlp(p, 256, 1024, inplace=False, prod_over_w=True)
+    add_gated_mlp(p, 256, 512)
+    prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs), qaddr=p.qaddr)
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    counts = NQ.fusion_counts()
+    assert counts["gated_mlp"] == (4 if fusion else 0) and counts["quant_gemm"] == (8 if fusion else 0), counts
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 def test_fusion_group_with_a_hazard_runs_one_by_one():
     """A decode row read by three GEMMs where the second GEMM writes over the third's weights: the
     fused launch would race, so the group runs descriptor by descriptor (the third GEMM then reads
@@ -848,18 +896,23 @@ def decode_step_image(seed: int, **shape):
     return dq, img
 
 
+@pytest.mark.parametrize("shape", ["small", "qwen3_width"])
 @pytest.mark.parametrize("fusion", [True, False])
-def test_whole_decode_step_matches_the_oracle(fusion):
+def test_whole_decode_step_matches_the_oracle(fusion, shape):
     """Every opcode of a decode step in one queue (RMSNorm, ROW_QUANT + q/k/v GEMMs, q/k norms per
     head, RoPE into the K cache, V straight into the cache, the attention triples, o, residual
     ELT_ADD, SiLU gate * up in place, down, final norm and a 4-block head): the image byte for byte,
-    on the first run and on two plan replays."""
-    dq, img = decode_step_image(5, layers=2, H=256, heads=4, kv_heads=2, hd=64, ff=512, vocab=1024, t0=40)
+    on the first run and on two plan replays. qwen3_width: one layer at Qwen3-0.6B's width (H =
+    1024, 16 heads of 128, ff = 3072), where the gate / up GEMMs and their ELT MUL run as one launch."""
+    dims = dict(small=dict(layers=2, H=256, heads=4, kv_heads=2, hd=64, ff=512, vocab=1024, t0=40),
+                qwen3_width=dict(layers=1, H=1024, heads=16, kv_heads=8, hd=128, ff=3072, vocab=2048, t0=40))[shape]
+    dq, img = decode_step_image(5, **dims)
     n = len(dq.descs)
     o = Q.Machine(img)
     ost = o.run_queue(dq.qaddr, n)
     assert ost.done, ost
     prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
     try:
         g = NQ.Machine(img)
         for rep in range(3):
@@ -869,5 +922,6 @@ def test_whole_decode_step_matches_the_oracle(fusion):
             assert gd == bytes(o.ddr), f"run {rep}: first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
     finally:
         NQ.set_fusion(prev)
+    assert NQ.fusion_counts()["gated_mlp"] == (3 * dims["layers"] if fusion and shape == "qwen3_width" else 0)
     logits = np.frombuffer(bytes(o.ddr[dq.logits:dq.logits + 4 * dq.vocab]), "<f4")
     assert np.isfinite(logits).all() and np.abs(logits).max() > 0
