@@ -74,6 +74,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--pmc-summary", nargs=5, metavar=("FETCH_CSV", "WRITE_CSV", "MFMA_CSV", "VALU_CSV", "DETAIL"),
                     help="write the per-config counter table from four --only-configs rocprofv3 passes and exit")
     ap.add_argument("--pmc-out", type=str, default=str(ROOT / "profiles" / "config_traffic.json"))
+    ap.add_argument("--pmc-step-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "DETAIL"),
+                    help="write the decode step's per-instance traffic from two rocprofv3 passes and exit")
+    ap.add_argument("--pmc-step-out", type=str, default=str(ROOT / "profiles" / "decode_step_traffic.json"))
     return ap.parse_args()
 
 
@@ -557,8 +560,11 @@ def kernel_instance(l: Launch) -> str:
         name, u, tail = "gemv_w8a8_kernel", plain_rows_per_wave(rows), ", 1"
     else:
         return l.kind
-    # the epilogue instance: true for QM_ROWCOL with fp32 output and no bias or activation
+    # the epilogue instance: true for QM_ROWCOL with fp32 output and no bias or activation; the
+    # fused kernel's last parameter (row pairs for a gated product) is false here
     tail += ", true" if simple else ", false"
+    if name == "quant_gemv_w8a8_kernel":
+        tail += ", false"
     c = K // 16
     if c <= 32:
         lanes = 8 if c <= 8 else 16 if c <= 16 else 32
@@ -668,7 +674,7 @@ COUNTER_FILE = ROOT / "profiles" / "config_traffic.json"
 CONFIG_KERNELS = {
     "c1_gemv_qwen3_gate_M1_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 1, true>", 196608),
     "lm_head_M1_K1024_N151936": ("gemv_w8a8_kernel<64, 1, 4, 1, true>", 2430976),
-    "lm_head_fused_quant_M1_K1024_N151936": ("quant_gemv_w8a8_kernel<64, 1, 4, true>", 2430976),
+    "lm_head_fused_quant_M1_K1024_N151936": ("quant_gemv_w8a8_kernel<64, 1, 4, true, false>", 2430976),
     "c2_gemma3_down_ksplit_3456+3456": ("gemv_w8a8_ksplit_rows_kernel<2, 4>", 294912),
     "c2_gemma3_down_ksplit_4096+2816": ("gemv_w8a8_ksplit_rows_kernel<2, 4>", 294912),
     "c4_prefill_M4_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 4, true>", 196608),
@@ -735,6 +741,38 @@ def pmc_summary(csvs: list, detail: str, out: str) -> int:
     Path(out).write_text(json.dumps({"fetch_scale": round(fetch_scale, 5), "write_scale": round(write_scale, 5),
                                      "calibration": "256 MiB device-to-device copy", "configs": table}, indent=1))
     print(f"{len(table)} configs; FETCH_SIZE x {fetch_scale:.4f}, WRITE_SIZE x {write_scale:.4f}", flush=True)
+    return 0
+
+
+def pmc_step_summary(fetch_csv: str, write_csv: str, detail: str, out: str) -> int:
+    """HBM traffic per launch of each decode-step kernel instance from two profiler passes over the
+    decode step (FETCH_SIZE, then WRITE_SIZE) and the first pass's --detail output (the instances'
+    algorithmic bytes per launch). Byte counters are scaled by what they read for the 1 GiB device
+    copy the bench makes. A kernel instance's dispatches of every grid are pooled: every timed graph
+    holds whole steps' launches of it, so the pool has the step's mix (q/k/v : head = 28 : 1)."""
+    P = [pmc_means(fetch_csv), pmc_means(write_csv)]
+    kernels = json.loads(Path(detail).read_text())["kernels"]
+    copy = max((k for k in P[0] if "copyBuffer" in k[0]), key=lambda k: P[0][k]["FETCH_SIZE"])
+    fetch_kib, write_kib = P[0][copy]["FETCH_SIZE"], P[1][copy]["WRITE_SIZE"]
+    fetch_scale, write_scale = (1 << 30) / (fetch_kib * 1024), (1 << 30) / (write_kib * 1024)
+    inst = {}
+    for name, k in kernels.items():
+        pooled = []
+        for i, c in enumerate(("FETCH_SIZE", "WRITE_SIZE")):
+            hits = [v for key, v in P[i].items() if f"::{name}(" in key[0]]
+            if not hits:
+                raise SystemExit(f"no dispatch of {name} in pass {i}")
+            n = sum(v["dispatches"] for v in hits)
+            pooled.append((n, sum(v[c] * v["dispatches"] for v in hits) / n))
+        rd, wr = pooled[0][1] * 1024 * fetch_scale, pooled[1][1] * 1024 * write_scale
+        inst[name] = {"read_bytes": round(rd), "write_bytes": round(wr), "traffic_bytes": round(rd + wr),
+                      "algorithmic_bytes": k["avg_bytes_per_launch"], "dispatches": pooled[0][0]}
+    Path(out).write_text(json.dumps({
+        "about": "HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per "
+                 "dispatch), each scaled by the same counter's reading for a 1 GiB device-to-device copy",
+        "fetch_copy_kib": fetch_kib, "write_copy_kib": write_kib, "fetch_scale": fetch_scale,
+        "write_scale": write_scale, "instances": inst}, indent=1))
+    print(f"{len(inst)} instances; FETCH_SIZE x {fetch_scale:.4f}, WRITE_SIZE x {write_scale:.4f}", flush=True)
     return 0
 
 
@@ -1085,6 +1123,8 @@ def main() -> int:
     args = parse()
     if args.pmc_summary:
         return pmc_summary(args.pmc_summary[:4], args.pmc_summary[4], args.pmc_out)
+    if args.pmc_step_summary:
+        return pmc_step_summary(*args.pmc_step_summary, args.pmc_step_out)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the matrix path runs on a single GPU here (sharding the "
               "output channels over several GPUs is not implemented); use --gpus 1", file=sys.stderr)

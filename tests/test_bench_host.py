@@ -1,6 +1,7 @@
 """bench.py's host-side pieces that need no GPU: the per-config profiler table built from
 rocprofv3 counter CSVs (the byte counters scaled by the calibration copy, one table entry per
-measured config), and its attachment to measured configs."""
+measured config), its attachment to measured configs, and the decode step's per-instance traffic
+table."""
 from __future__ import annotations
 
 import csv
@@ -93,3 +94,38 @@ def test_pmc_summary_refuses_a_missing_kernel(bench, tmp_path):
     detail.write_text(json.dumps({"configs": {}}))
     with pytest.raises(SystemExit, match="0 kernels match"):
         bench.pmc_summary(paths, str(detail), str(tmp_path / "o.json"))
+
+
+def test_pmc_step_summary_pools_grids_and_scales(bench, tmp_path):
+    """The decode step's per-instance traffic: one instance's dispatches of two grids (28 q/k/v-like
+    and one head-like per step) pooled by dispatch count, the byte counters scaled by the 1 GiB
+    copy's readings, the algorithmic bytes taken from the detail's kernels."""
+    name = "quant_gemv_w8a8_kernel<64, 1, 4, true, false>"
+    cols = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
+    paths = []
+    for c, copy_kib, small, big in (("FETCH_SIZE", 524288.0, 100.0, 1000.0), ("WRITE_SIZE", 1048576.0, 4.0, 40.0)):
+        p = tmp_path / f"{c}.csv"
+        with open(p, "w", newline="") as f:
+            w = csv.DictWriter(f, cols)
+            w.writeheader()
+            rows = [("__amd_rocclr_copyBuffer", 1 << 20, copy_kib)] + \
+                [(f"void tars::(anonymous namespace)::{name}(float const*, long)", 65536, small)] * 28 + \
+                [(f"void tars::(anonymous namespace)::{name}(float const*, long)", 2430976, big)]
+            for did, (kn, grid, v) in enumerate(rows):
+                w.writerow({"Dispatch_Id": did, "Kernel_Name": kn, "Grid_Size": grid, "Counter_Name": c,
+                            "Counter_Value": v})
+        paths.append(str(p))
+    detail = tmp_path / "detail.json"
+    detail.write_text(json.dumps({"kernels": {name: {"avg_bytes_per_launch": 9_492_233}}}))
+    out = tmp_path / "step.json"
+    assert bench.pmc_step_summary(paths[0], paths[1], str(detail), str(out)) == 0
+    t = json.loads(out.read_text())
+    assert t["fetch_scale"] == 2.0 and t["write_scale"] == 1.0
+    e = t["instances"][name]
+    assert e["dispatches"] == 29 and e["algorithmic_bytes"] == 9_492_233
+    assert e["read_bytes"] == round((28 * 100.0 + 1000.0) / 29 * 1024 * 2)
+    assert e["write_bytes"] == round((28 * 4.0 + 40.0) / 29 * 1024)
+    assert e["traffic_bytes"] == e["read_bytes"] + e["write_bytes"]
+    detail.write_text(json.dumps({"kernels": {"quant_gemv_w8a8_kernel<64, 2, 1, true, false>": {"avg_bytes_per_launch": 1}}}))
+    with pytest.raises(SystemExit, match="no dispatch"):
+        bench.pmc_step_summary(paths[0], paths[1], str(detail), str(out))
