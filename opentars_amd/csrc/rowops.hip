@@ -909,6 +909,9 @@ __global__ __launch_bounds__(256) void attn_split_scores_kernel(AttnArgs a) {
   constexpr int U = HD / 16, KF = 2;
   const int hg = blockIdx.x, t = threadIdx.x, g = t >> 4, l = t & 15;
   const int G = a.group, M = a.M, nk = a.nk;
+  // every argument the kernel reads, in one scalar round trip (see attn_split_pv_kernel)
+  __asm__ volatile("" : : "s"(a.q[hg * G]), "s"(a.ldq), "s"(a.k[hg * G]), "s"(a.ldk), "s"(a.keys_per_wg),
+                   "s"(a.scratch), "s"(a.ld_scratch), "s"(a.heads), "s"(a.sc), "s"(a.ldsc));
   const int jb = blockIdx.y * a.keys_per_wg, je = min(nk, jb + a.keys_per_wg);
   float qv[Q][U];
 #pragma unroll
@@ -1029,6 +1032,11 @@ __global__ __launch_bounds__(256) void attn_split_pv_kernel(AttnArgs a) {
   const int hg = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int G = a.group, M = a.M, nk = a.nk;  // G * M == Q
+  // every argument the kernel reads, in one scalar round trip: the argument block spans many cache
+  // lines, and a field first read mid-kernel (the softmax's causal_k, pr, the outputs' fields)
+  // stalled there for a scalar cache miss each
+  __asm__ volatile("" : : "s"(a.v[hg * G]), "s"(a.ldv), "s"(a.scratch), "s"(a.ld_scratch), "s"(a.causal_k),
+                   "s"(a.pr), "s"(a.ldpr), "s"(a.att[hg * G]), "s"(a.ldatt), "s"(a.out), "s"(a.out_scale));
   const int ldp = static_cast<int>(a.ld_scratch);
   const int NS = (nk + SR - 1) / SR;
   const char* vbase = static_cast<const char*>(a.v[hg * G]) + c * ROWB;
