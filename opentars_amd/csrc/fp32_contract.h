@@ -146,10 +146,11 @@ __device__ __forceinline__ float recip_f(float x) {
 // to that coefficient. Other x take their result from the range tests; on the way their steps
 // stay free of NaN (r and the coefficients are finite unless x is infinite, and then no product
 // pairs an infinity with a zero and no sum pairs opposite infinities). No NaN arises, so the result
-// needs no canonicalization.
+// needs no canonicalization. A NaN x runs the same steps (their values are dropped) and returns the
+// canonical NaN.
 __device__ __forceinline__ float exp_f(float x) {
   x = ftz(x);
-  if (is_nan(x)) return ffrom(kCanonNaN);
+  const bool nan = is_nan(x);  // taken by a select at the end: the steps below run branch-free
   float n = rintf(__fmul_rn(x, ffrom(kLog2e)));
   n = fminf(fmaxf(n, -200.0f), 200.0f);
   const float r = __fadd_rn(__fadd_rn(x, __fmul_rn(n, ffrom(kNegLn2Hi))), __fmul_rn(n, ffrom(kNegLn2Lo)));
@@ -158,10 +159,8 @@ __device__ __forceinline__ float exp_f(float x) {
   float p = ffrom(0x3AB60B61u);
 #pragma unroll
   for (int i = 0; i < 6; ++i) p = __fadd_rn(__fmul_rn(p, r), ffrom(coeffs[i]));
-  float y = add_to_exponent(p, static_cast<int>(n));
-  if (x >= ffrom(kExpHi)) y = ffrom(kExpo);
-  else if (x <= ffrom(kExpLo)) y = 0.0f;
-  return y;
+  const float y = add_to_exponent(p, static_cast<int>(n));
+  return nan ? ffrom(kCanonNaN) : x >= ffrom(kExpHi) ? ffrom(kExpo) : x <= ffrom(kExpLo) ? 0.0f : y;
 }
 
 __device__ __forceinline__ float relu_plain(float x) { return x > 0.0f ? x : 0.0f; }

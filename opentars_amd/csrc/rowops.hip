@@ -960,25 +960,23 @@ __device__ __forceinline__ int softmax_rows_lds(float* sp, int ldp, int M, int n
 #pragma unroll
   for (int i = 0; i < Q; ++i) V[i] = causal_k > 0 ? min(nk, causal_k + i % M) : nk;
   __syncthreads();  // the rows are complete
+  // the maximum key of each row's valid keys, a NaN counting as 0xFFFFFFFF (above every other key:
+  // +inf's is 0xFF800000), branch-free, then one whole-wave maximum per row
   uint32_t key[Q];
-  int nan[Q];
 #pragma unroll
-  for (int i = 0; i < Q; ++i) key[i] = 0, nan[i] = 0;
+  for (int i = 0; i < Q; ++i) key[i] = 0;
   for (int j = t; j < nk; j += 256) {
 #pragma unroll
     for (int i = 0; i < Q; ++i) {
       const float x = sp[i * ldp + j];
-      if (j < V[i]) {
-        if (is_nan(x)) nan[i] = 1;
-        else key[i] = max(key[i], fmax_key(x));
-      }
+      const uint32_t k = is_nan(x) ? 0xFFFFFFFFu : fmax_key(x);
+      key[i] = j < V[i] ? max(key[i], k) : key[i];
     }
   }
 #pragma unroll
   for (int i = 0; i < Q; ++i) {
-    key[i] = static_cast<uint32_t>(group_reduce<64>(static_cast<int>(key[i]), OpMaxU{}));
-    nan[i] = group_reduce<64>(nan[i], OpOr{});
-    if (lane == 0) red[i][t >> 6] = nan[i] ? 0xFFFFFFFFu : key[i];
+    key[i] = wave_max_u32(key[i]);
+    if (lane == 0) red[i][t >> 6] = key[i];
   }
   __syncthreads();
   float nmx[Q];
@@ -1066,9 +1064,18 @@ __global__ __launch_bounds__(256) void attn_split_pv_kernel(AttnArgs a) {
   // V elements need their own test only when fp32 and some probability is above 1 or NaN (as in
   // attn_kernel)
   const bool vtest = __syncthreads_or(above1) && !VHALF;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the slots' reads stay after the barrier
   const int i = t / DS, d = t % DS;
   const bool active = i < Q;
   float acc = 0.0f;
+  if (NS <= SLOTS - 1) {
+    // every stage was issued before the softmax, has landed (each wave's wait_vmcnt<0> above) and is
+    // visible (the barrier): the stages sit in consecutive slots, so the chains run over all keys in
+    // one pipelined pass, without the per-stage waits and barrier pairs
+    if (active) acc = pv_stage<VHALF, SR, ROWB>(acc, ring, d, sp + i * ldp, nk, vtest);
+    if (active) store_out(a.att[hg * G + i / M], (i % M) * a.ldatt, c * DS + d, a.out, chain_end(acc), a.out_scale);
+    return;
+  }
   for (int st = 0; st < NS; ++st) {
     if (st + SLOTS - 1 < NS) issue(st + SLOTS - 1);
     wait_stages_ahead<L, SLOTS - 1>(min(NS - 1 - st, SLOTS - 1));

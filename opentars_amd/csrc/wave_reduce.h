@@ -120,6 +120,16 @@ __device__ __forceinline__ bool scatter_owner(int lane) {
   else return (lane & 14) == 0;
 }
 
+// The unsigned maximum over the wave's 64 lanes, in every lane (DPP within the 16-lane rows, then
+// the rows' exchanges by permlane swaps: no v_readlane round trip through scalar registers).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  const int m = group_reduce<16>(static_cast<int>(v), OpMaxU{});
+  const auto a = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+  const uint32_t h = max(static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(h, h, false, false);
+  return max(static_cast<uint32_t>(b[0]), static_cast<uint32_t>(b[1]));
+}
+
 // Lane i receives lane (i ^ 1) / (i ^ 2)'s value (within its quad).
 __device__ __forceinline__ int lane_xor1(int v) { return dpp<kDppQuadXor1>(v); }
 __device__ __forceinline__ int lane_xor2(int v) { return dpp<kDppQuadXor2>(v); }
