@@ -369,10 +369,12 @@ int tars_set_queue_fusion(int on);
 /* Fused launches tars_run_queue has run (diagnostics for tests and benchmarks, not part of the
  * reference's interface), counted per kind since the last reset: counts[0] decode-row quantizer +
  * GEMMs, counts[1] attention (per-head FDOT / softmax / FDOT triples), counts[2] residual ELT ADD +
- * norm, counts[3] norm + RoPE, counts[4] an MLP's gated product (the ELT MUL of a gate and an up
- * GEMM folded into their quantizer + GEMMs launch, which counts[0] also counts). A replayed launch
- * plan counts its fused launches again. The first ncounts (up to 5) are written to counts, which
- * may be NULL; reset != 0 zeroes the counts after reading them. Process-wide. */
+ * norm, counts[3] (norm, RoPE) pairs, counts[4] an MLP's gated product (the ELT MUL of a gate and
+ * an up GEMM folded into their quantizer + GEMMs launch, which counts[0] also counts), counts[5]
+ * launches that ran two adjacent independent (norm, RoPE) pairs, such as a decoder layer's q and
+ * k (counts[3] counts both pairs). A replayed launch plan counts its fused launches again. The
+ * first ncounts (up to 6) are written to counts, which may be NULL; reset != 0 zeroes the counts
+ * after reading them. Process-wide. */
 int tars_queue_fusion_counts(int64_t* counts, int32_t ncounts, int32_t reset);
 
 /* Launch plans in tars_run_queue (benchmark and test control): 1 (default) keeps, for up to 8

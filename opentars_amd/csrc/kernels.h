@@ -319,6 +319,8 @@ hipError_t launch_add_norm(const EltArgs& e, const RowArgs& r, hipStream_t s);
 // A LayerNorm / RMSNorm / L2Norm with an fp32 output and the RoPE (fp32 output) of its output rows
 // in one launch (rows within add_norm_supported's bounds): the norm's output is written, then rotated.
 hipError_t launch_norm_rope(const RowArgs& r, const RopeArgs& p, hipStream_t s);
+// Two independent (norm, RoPE) jobs in one launch (r0.M + r1.M workgroups).
+hipError_t launch_norm_rope2(const RowArgs& r0, const RopeArgs& p0, const RowArgs& r1, const RopeArgs& p1, hipStream_t s);
 hipError_t launch_elt(const EltArgs& a, hipStream_t s);
 hipError_t launch_rope(const RopeArgs& a, hipStream_t s);
 hipError_t launch_relu(const ReluArgs& a, hipStream_t s);

@@ -853,7 +853,7 @@ int fuse_add_norm(uint8_t* image, const Checked& e, const std::vector<uint8_t>& 
 // when the RoPE's input rows are exactly the norm's output rows, both write fp32, the rows fit the
 // kernel, and neither output lands on an input of the pair (the norm's rows, gamma, beta, the
 // table), on the other output or on a later descriptor.
-int launch_norm_rope_pair(uint8_t* image, const Desc& rd, const Desc& pd, hipStream_t s) {
+tars::RopeArgs rope_args(uint8_t* image, const Desc& pd) {
   uint8_t* PB = image + pd[F_BASE_ADDR];
   tars::RopeArgs p{};
   p.x = PB + pd[F_A_OFF];
@@ -865,7 +865,15 @@ int launch_norm_rope_pair(uint8_t* image, const Desc& rd, const Desc& pd, hipStr
   p.ldy = static_cast<int64_t>(strides(pd).ldy);
   p.M = static_cast<int>(pd[F_M]);
   p.N = static_cast<int>(pd[F_N]);
-  const hipError_t err = tars::launch_norm_rope(norm_args(image, rd), p, s);
+  return p;
+}
+
+// One fused (norm, RoPE) pair, or two independent ones (r2 / p2 not null) in one launch.
+int launch_norm_rope_pair(uint8_t* image, const Desc& rd, const Desc& pd, hipStream_t s, const Desc* r2 = nullptr,
+                          const Desc* p2 = nullptr) {
+  const hipError_t err = r2 ? tars::launch_norm_rope2(norm_args(image, rd), rope_args(image, pd), norm_args(image, *r2),
+                                                      rope_args(image, *p2), s)
+                            : tars::launch_norm_rope(norm_args(image, rd), rope_args(image, pd), s);
   if (err != hipSuccess) {
     tars::set_last_error(std::string("HIP launch failed: ") + hipGetErrorString(err));
     return TARS_E_DEVICE;
@@ -873,9 +881,36 @@ int launch_norm_rope_pair(uint8_t* image, const Desc& rd, const Desc& pd, hipStr
   return TARS_OK;
 }
 
+// Whether descriptors (r, p) form a pair the norm_rope kernel runs (a norm with an fp32 output and
+// the RoPE of exactly its output rows, fp32), and the pair's reads and writes.
+bool norm_rope_pair(const Checked& r, const Checked& p, uintptr_t img, Segs& ins, Segs& outs) {
+  const Desc& rd = r.d;
+  const Desc& pd = p.d;
+  const uint64_t fn = rd[F_CTRL] & 7;
+  if (r.err != E_OK || r.overlap || p.err != E_OK || p.overlap || rd[F_OPCODE] != OP_ROW ||
+      (fn != ROW_LAYERNORM && fn != ROW_RMSNORM && fn != ROW_L2NORM) || out_code(rd[F_EPI]) != OUT_FP32 ||
+      pd[F_OPCODE] != OP_ROPE || out_code(pd[F_EPI]) != OUT_FP32 || (img + rd[F_BASE_ADDR]) % 16 ||
+      (img + pd[F_BASE_ADDR]) % 16 || pd[F_M] != rd[F_M] || pd[F_N] != rd[F_N] ||
+      !tars::add_norm_supported(static_cast<int>(rd[F_M]), static_cast<int>(rd[F_N])) ||
+      addr(pd, F_A_OFF) != addr(rd, F_Y_OFF) || strides(pd).lda != strides(rd).ldy)
+    return false;
+  ins.clear();
+  for (const Segs& x : r.reads) ins.insert(ins.end(), x.begin(), x.end());
+  const uint64_t tab_rows = (pd[F_M] - 1) / pd[F_GROUP_SIZE] + 1;
+  ins.push_back(interval(addr(pd, F_W_OFF), addr(pd, F_W_OFF) + static_cast<u128>(4 * pd[F_K]) * tab_rows));
+  outs = r.y;
+  outs.insert(outs.end(), p.y.begin(), p.y.end());
+  return true;
+}
+
+// A norm and the RoPE of its output rows as one launch (the pair's outputs disjoint, neither read
+// by the pair nor lying on a later descriptor). When the next two descriptors form another such
+// pair that neither reads nor writes what the first pair writes, and whose reads the first pair
+// does not write (a decoder's q and then k norm and rotation), both pairs run in the same launch.
+// `fused` = descriptors folded into descriptor i's launch (1 or 3).
 int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
                    int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
-                   int& fused, Desc& rope) {
+                   int& fused, Desc& rope, Desc& r2, Desc& rope2) {
   fused = 0;
   const Desc& rd = r.d;
   const uint64_t fn = rd[F_CTRL] & 7;
@@ -883,27 +918,32 @@ int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>&
       out_code(rd[F_EPI]) != OUT_FP32 || i + 1 >= n || static_cast<uint64_t>(i) + 1 >= in_image)
     return TARS_OK;
   const Checked p = check(q.data() + static_cast<size_t>(i + 1) * kDescBytes, image_len, core_id, gemv_only);
-  const Desc& pd = p.d;
   const uintptr_t img = reinterpret_cast<uintptr_t>(image);
-  if (r.err != E_OK || r.overlap || p.err != E_OK || p.overlap || pd[F_OPCODE] != OP_ROPE ||
-      out_code(pd[F_EPI]) != OUT_FP32 || (img + rd[F_BASE_ADDR]) % 16 || (img + pd[F_BASE_ADDR]) % 16 ||
-      pd[F_M] != rd[F_M] || pd[F_N] != rd[F_N] ||
-      !tars::add_norm_supported(static_cast<int>(rd[F_M]), static_cast<int>(rd[F_N])) ||
-      addr(pd, F_A_OFF) != addr(rd, F_Y_OFF) || strides(pd).lda != strides(rd).ldy)
-    return TARS_OK;
-  Segs ins;
-  for (const Segs& x : r.reads) ins.insert(ins.end(), x.begin(), x.end());
-  const uint64_t tab_rows = (pd[F_M] - 1) / pd[F_GROUP_SIZE] + 1;
-  ins.push_back(interval(addr(pd, F_W_OFF), addr(pd, F_W_OFF) + static_cast<u128>(4 * pd[F_K]) * tab_rows));
-  Segs outs = r.y;
-  outs.insert(outs.end(), p.y.begin(), p.y.end());
-  if (!pairwise_disjoint(outs) || overlaps(ins, outs) ||
-      (rest_lo < rest_hi && overlaps(Segs{interval(rest_lo, rest_hi)}, outs)))
-    return TARS_OK;
-  const int rc = launch_norm_rope_pair(image, rd, pd, s);
+  Segs ins, outs;
+  if (!norm_rope_pair(r, p, img, ins, outs)) return TARS_OK;
+  const Segs rest = {interval(rest_lo, rest_hi)};
+  if (!pairwise_disjoint(outs) || overlaps(ins, outs) || (rest_lo < rest_hi && overlaps(rest, outs))) return TARS_OK;
+  bool two = false;
+  Checked r1, p1;
+  if (i + 3 < n && static_cast<uint64_t>(i) + 3 < in_image) {
+    r1 = check(q.data() + static_cast<size_t>(i + 2) * kDescBytes, image_len, core_id, gemv_only);
+    p1 = check(q.data() + static_cast<size_t>(i + 3) * kDescBytes, image_len, core_id, gemv_only);
+    Segs ins1, outs1;
+    if (norm_rope_pair(r1, p1, img, ins1, outs1)) {
+      Segs all = outs;
+      all.insert(all.end(), outs1.begin(), outs1.end());
+      two = pairwise_disjoint(all) && !overlaps(ins1, all) && !overlaps(ins, outs1) &&
+            !(rest_lo < rest_hi && overlaps(rest, outs1));
+    }
+  }
+  const int rc = two ? launch_norm_rope_pair(image, rd, p.d, s, &r1.d, &p1.d) : launch_norm_rope_pair(image, rd, p.d, s);
   if (rc == TARS_OK) {
-    fused = 1;
-    rope = pd;
+    fused = two ? 3 : 1;
+    rope = p.d;
+    if (two) {
+      r2 = r1.d;
+      rope2 = p1.d;
+    }
   }
   return rc;
 }
@@ -923,6 +963,8 @@ struct Step {
   Desc second{};               // or: the second descriptor of a fused pair with d
   bool add_norm = false;       // d an ELT ADD, second its norm
   bool norm_rope = false;      // d a norm, second its RoPE
+  Desc third{}, fourth{};      // with norm_rope2: a second (norm, RoPE) pair in the same launch
+  bool norm_rope2 = false;
   Desc elt{};                  // a gated group's ELT MUL (gated: group is gate and up)
   bool gated = false;
 };
@@ -940,16 +982,18 @@ struct Plan {
 };
 
 // Fused launches run (diagnostics for tests and benchmarks): quantizer + GEMMs, attention,
-// residual ADD + norm, norm + RoPE, and (also counted as quantizer + GEMMs) the gated product's
+// residual ADD + norm, norm + RoPE pairs (two when two pairs share a launch), launches that ran two
+// such pairs, and (also counted as quantizer + GEMMs) the gated product's
 // ELT MUL folded into its GEMMs; counted when a queue is dispatched and when a plan replays.
-constexpr int kFusionKinds = 5;
+constexpr int kFusionKinds = 6;
 std::atomic<int64_t> g_fused_launches[kFusionKinds];
 
 void count_fused(const std::vector<Step>& steps) {
   for (const Step& st : steps) {
     const int k = !st.group.empty() ? 0 : !st.attn.empty() ? 1 : st.add_norm ? 2 : st.norm_rope ? 3 : -1;
-    if (k >= 0) g_fused_launches[k].fetch_add(1, std::memory_order_relaxed);
+    if (k >= 0) g_fused_launches[k].fetch_add(st.norm_rope2 ? 2 : 1, std::memory_order_relaxed);
     if (st.gated) g_fused_launches[4].fetch_add(1, std::memory_order_relaxed);
+    if (st.norm_rope2) g_fused_launches[5].fetch_add(1, std::memory_order_relaxed);
   }
 }
 
@@ -963,7 +1007,8 @@ int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) 
   for (const Step& st : steps) {
     bool needs_host = false;
     const int rc = st.add_norm        ? launch_add_norm_pair(image, st.d, st.second, s)
-                   : st.norm_rope     ? launch_norm_rope_pair(image, st.d, st.second, s)
+                   : st.norm_rope     ? launch_norm_rope_pair(image, st.d, st.second, s, st.norm_rope2 ? &st.third : nullptr,
+                                                          st.norm_rope2 ? &st.fourth : nullptr)
                    : !st.attn.empty() ? launch_attention_group(image, st.attn, s)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
                                       : launch_fused(image, st.d, st.group, s, st.gated ? &st.elt : nullptr);
@@ -1163,19 +1208,26 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       ++i;  // the ELT and its norm ran as one launch
       continue;
     }
-    Desc rope{};
+    Desc rope{}, norm2{}, rope2{};
     if (int rc = fuse_norm_rope(image, c, q, i, in_image, n, static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) *
-                                (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, rope))
+                                (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, rope,
+                                norm2, rope2))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
     if (fused) {
-      g_fused_launches[3].fetch_add(1, std::memory_order_relaxed);
+      g_fused_launches[3].fetch_add(fused == 3 ? 2 : 1, std::memory_order_relaxed);
+      if (fused == 3) g_fused_launches[5].fetch_add(1, std::memory_order_relaxed);
       if (cacheable) {
         Step st2{c.d, {}, {}};
         st2.second = rope;
         st2.norm_rope = true;
+        if (fused == 3) {
+          st2.third = norm2;
+          st2.fourth = rope2;
+          st2.norm_rope2 = true;
+        }
         steps.push_back(std::move(st2));
       }
-      ++i;  // the norm and its RoPE ran as one launch
+      i += fused;  // one or two (norm, RoPE) pairs ran as one launch
       continue;
     }
     bool needs_host = false;

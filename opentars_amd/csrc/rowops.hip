@@ -313,11 +313,10 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(EltArgs e, RowArg
 // elements): each workgroup normalizes its row as row_lds_kernel does and stores it; after a
 // workgroup barrier, which makes the row's stores visible to the workgroup, it rotates the stored
 // values as rope_fast_kernel does.
-__global__ __launch_bounds__(kRowThreads) void norm_rope_kernel(RowArgs r, RopeArgs p) {
-  __shared__ float v[kRowThreads * kRowE];
-  __shared__ float bcast;
-  __asm__ volatile("" : : "s"(r.x), "s"(r.lda), "s"(r.gamma), "s"(r.beta), "s"(r.N));
-  const int m = blockIdx.x, t = threadIdx.x, N = r.N;
+__device__ __forceinline__ void norm_rope_row(const RowArgs& r, const RopeArgs& p, int m, float* v, float* bcast) {
+  __asm__ volatile("" : : "s"(r.x), "s"(r.lda), "s"(r.gamma), "s"(r.beta), "s"(r.N), "s"(p.x), "s"(p.lda), "s"(p.tab),
+                   "s"(p.rows_per_pos), "s"(p.rot), "s"(p.y), "s"(p.ldy));
+  const int t = threadIdx.x, N = r.N;
   const float* x = frow(r.x, r.lda, m);
   float xv[kRowE], gv[kRowE], bv[kRowE];
 #pragma unroll
@@ -327,7 +326,7 @@ __global__ __launch_bounds__(kRowThreads) void norm_rope_kernel(RowArgs r, RopeA
     gv[u] = *(j < N ? r.gamma + j : x);
     bv[u] = *(r.beta && j < N ? r.beta + j : x);
   }
-  norm_in_regs(r, m, xv, gv, bv, v, &bcast);
+  norm_in_regs(r, m, xv, gv, bv, v, bcast);
   __syncthreads();
   const float* xr = frow(p.x, p.lda, m);
   const float* tb = p.tab + static_cast<int64_t>(static_cast<unsigned>(m) / static_cast<unsigned>(p.rows_per_pos)) * p.rot;
@@ -344,6 +343,16 @@ __global__ __launch_bounds__(kRowThreads) void norm_rope_kernel(RowArgs r, RopeA
     else o = ftz(xn);
     y[n] = ftz(o);
   }
+}
+
+// One or two independent (norm, RoPE) jobs in one launch (a decoder's q and k norms and rotations):
+// workgroups [0, M0) take job 0's rows, the rest job 1's.
+__global__ __launch_bounds__(kRowThreads) void norm_rope_kernel(RowArgs r0, RopeArgs p0, RowArgs r1, RopeArgs p1, int M0) {
+  __shared__ float v[kRowThreads * kRowE];
+  __shared__ float bcast;
+  const int m = blockIdx.x;
+  if (m < M0) norm_rope_row(r0, p0, m, v, &bcast);
+  else norm_rope_row(r1, p1, m - M0, v, &bcast);
 }
 
 // Longer rows: one 16-lane group per row, the lane's elements streamed in blocks.
@@ -1100,7 +1109,12 @@ dim3 row_grid(int M, int N, int per) {
 bool add_norm_supported(int M, int N) { return M >= 1 && M <= 65535 && N >= 1 && N <= kRowThreads * kRowE; }
 
 hipError_t launch_norm_rope(const RowArgs& r, const RopeArgs& p, hipStream_t s) {
-  hipLaunchKernelGGL(norm_rope_kernel, dim3(r.M), dim3(kRowThreads), 0, s, r, p);
+  hipLaunchKernelGGL(norm_rope_kernel, dim3(r.M), dim3(kRowThreads), 0, s, r, p, r, p, r.M);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_rope2(const RowArgs& r0, const RopeArgs& p0, const RowArgs& r1, const RopeArgs& p1, hipStream_t s) {
+  hipLaunchKernelGGL(norm_rope_kernel, dim3(r0.M + r1.M), dim3(kRowThreads), 0, s, r0, p0, r1, p1, r0.M);
   return hipGetLastError();
 }
 

@@ -510,6 +510,57 @@ def test_norm_then_rope(seed, fusion):
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
+def add_norm_rope_at(p: Program, M: int, N: int, rot: int, G: int, x: int = 0, y: int = 0, yr: int = 0):
+    """A (norm, RoPE) pair over dense rows of N fp32: the norm reads x and writes y, the RoPE reads
+    y and writes yr; each is a fresh region (x filled with random rows) when 0. Returns (x, y, yr)."""
+    rng = p.rng
+    if not x:
+        x, _ = stride_fields(p, M, 4 * N)
+        p.ddr[x:x + 4 * M * N] = rand_rows(p, M, N).tobytes()
+    y = y or p.alloc(4 * M * N)
+    yr = yr or p.alloc(4 * M * N)
+    g = p.put(rng.normal(1, 0.2, N).astype("<f4").tobytes())
+    fn = int(rng.choice([Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM]))
+    p.add(OPCODE=Q.OP_ROW, CTRL=fn, EPI=Q.epi(), A_OFF=x, Y_OFF=y, SCALE_OFF=g, W_OFF=f32bits(1e-6), M=M, N=N)
+    rows = (M - 1) // G + 1
+    fr = np.arange(rows, dtype=np.float32)[:, None] * rng.uniform(0.01, 1.0, rot // 2).astype(np.float32)[None, :]
+    t = p.put(np.concatenate([np.cos(fr), np.sin(fr)], 1).astype("<f4").tobytes())
+    p.add(OPCODE=Q.OP_ROPE, EPI=Q.epi(), A_OFF=y, W_OFF=t, Y_OFF=yr, M=M, N=N, K=rot, GROUP_SIZE=G)
+    return x, y, yr
+
+
+@pytest.mark.parametrize("seed", range(3))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_two_norm_rope_pairs_share_a_launch(seed, fusion):
+    """Adjacent (norm, RoPE) pairs, which the executor runs two to a launch when they are
+    independent: q / k shapes (merged), a pair whose norm reads the previous pair's RoPE output
+    (not merged), a pair whose norm writes over the previous pair's input (not merged), a pair whose
+    RoPE writes over the previous pair's RoPE output (not merged), two pairs that read the same
+    rows (merged) after a pair the fused kernel does not take; the images equal the oracle's."""
+    p = Program(8400 + seed)
+    add_norm_rope_at(p, 16, 128, 128, 16)                  # P1 + P2 merged
+    add_norm_rope_at(p, 8, 128, 128, 8)
+    _, _, yr3 = add_norm_rope_at(p, 4, 256, 128, 1)        # P3 alone: P4 reads its output
+    x4, _, _ = add_norm_rope_at(p, 4, 256, 64, 2, x=yr3)   # P4 alone: P5 writes over its input
+    _, _, yr5 = add_norm_rope_at(p, 4, 256, 256, 4, y=x4)  # P5 alone: P6 writes over its output
+    add_norm_rope_at(p, 2, 256, 128, 1, yr=yr5)            # P6 + P7 merged
+    add_norm_rope_at(p, 3, 1024, 1024, 3)
+    add_norm_rope_at(p, 2, 2080, 64, 1)                    # P8 not fused (rows past the kernel's limit)
+    x9, _, _ = add_norm_rope_at(p, 5, 512, 512, 5)         # P9 + P10 merged (both read x9)
+    add_norm_rope_at(p, 5, 512, 256, 1, x=x9)
+    prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    counts = NQ.fusion_counts()
+    assert (counts["norm_rope"], counts["norm_rope_two"]) == ((9, 3) if fusion else (0, 0)), counts
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 @pytest.mark.parametrize("seed", range(3))
 def test_host_copy_of_the_queue_gives_the_same_result(seed):
     p = random_program(200 + seed)
@@ -922,6 +973,9 @@ def test_whole_decode_step_matches_the_oracle(fusion, shape):
             assert gd == bytes(o.ddr), f"run {rep}: first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
     finally:
         NQ.set_fusion(prev)
-    assert NQ.fusion_counts()["gated_mlp"] == (3 * dims["layers"] if fusion and shape == "qwen3_width" else 0)
+    counts = NQ.fusion_counts()
+    assert counts["gated_mlp"] == (3 * dims["layers"] if fusion and shape == "qwen3_width" else 0), counts
+    # each layer's q and k (norm, RoPE) pairs run as one launch
+    assert counts["norm_rope_two"] == (3 * dims["layers"] if fusion else 0), counts
     logits = np.frombuffer(bytes(o.ddr[dq.logits:dq.logits + 4 * dq.vocab]), "<f4")
     assert np.isfinite(logits).all() and np.abs(logits).max() > 0
