@@ -107,9 +107,13 @@ int w8a8_path() { return g_w8a8_path; }
 
 // tars_quant_gemm_w8a8's checks and launch, with the gated product (QuantGemvArgs::prod) for the
 // queue executor's MLP fusion: prod rows must not overlap an input, the quantized rows or Y1, and
-// either are Y0's rows exactly (in place) or overlap no output.
+// either are Y0's rows exactly (in place) or overlap no output. With pro (the executor's fusion of a
+// residual ELT ADD and a norm in front of the quantizer): x is the ELT's A rows (the norm's input
+// rows without B), pro's rows and vectors join the inputs and its sum and norm rows the outputs,
+// and no output may overlap an input or another output (so no ELT in place).
 int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s, int32_t M, int32_t K,
-                            const tars_w8a8_out* outs, int32_t nouts, float* prod, int64_t ldprod, void* stream) {
+                            const tars_w8a8_out* outs, int32_t nouts, float* prod, int64_t ldprod, void* stream,
+                            const NormPrologue* pro) {
   g_last_error.clear();
   if (!x || !outs) return fail(TARS_E_ARG, "NULL pointer");
   if ((q == nullptr) != (s == nullptr)) return fail(TARS_E_ARG, "q and s are both given or both NULL");
@@ -166,6 +170,34 @@ int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq,
     outputs.push_back(rows(q, ldq, M, K));
     outputs.push_back(one(s, 4LL * M));
   }
+  NormPrologue p{};
+  if (pro) {
+    p = *pro;
+    if (p.fn != ROWFN_LAYERNORM && p.fn != ROWFN_RMSNORM && p.fn != ROWFN_L2NORM)
+      return fail(TARS_E_FIELD, "the norm prologue takes a LayerNorm, RMSNorm or L2Norm");
+    if (!tars::quant_gemv_norm_supported(K)) return fail(TARS_E_FIELD, "the norm prologue is not available at this K");
+    if (!p.gamma || !p.y || (p.B != nullptr) != (p.sum != nullptr))
+      return fail(TARS_E_ARG, "norm prologue: gamma and y, and B and sum together");
+    const int64_t row = 4LL * K;
+    if (p.ldb == 0) p.ldb = row;
+    if (p.ldsum == 0) p.ldsum = row;
+    if (p.ldy == 0) p.ldy = row;
+    if ((p.B && (p.ldb < row || p.ldb % 16 || p.ldsum < row || p.ldsum % 16)) || p.ldy < row || p.ldy % 16)
+      return fail(TARS_E_ALIGN, "norm prologue: strides must be multiples of 16 holding a row");
+    if (!aligned(p.gamma, 16) || (p.beta && !aligned(p.beta, 16)) || !aligned(p.y, 16) ||
+        (p.B && (!aligned(p.B, 16) || !aligned(p.sum, 16))))
+      return fail(TARS_E_ALIGN, "norm prologue: pointers must be 16-byte aligned");
+    if (!extent_ok(p.y, p.ldy, M, row) || (p.B && (!extent_ok(p.B, p.ldb, M, row) || !extent_ok(p.sum, p.ldsum, M, row))))
+      return fail(TARS_E_RANGE, "extent overflows");
+    inputs.push_back(one(p.gamma, row)[0]);
+    if (p.beta) inputs.push_back(one(p.beta, row)[0]);
+    if (p.B) {
+      const auto b = rows(p.B, p.ldb, M, row);
+      inputs.insert(inputs.end(), b.begin(), b.end());
+      outputs.push_back(rows(p.sum, p.ldsum, M, row));
+    }
+    outputs.push_back(rows(p.y, p.ldy, M, row));
+  }
   for (size_t i = 0; i < outputs.size(); ++i) {
     if (overlaps(inputs, outputs[i])) return fail(TARS_E_OVERLAP, "an output overlaps an input");
     for (size_t j = 0; j < i; ++j)
@@ -182,6 +214,7 @@ int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq,
   a.ngroups = nouts;
   a.prod = prod;
   a.ldprod = ldprod;
+  a.pro = p;
   for (int i = 0; i < nouts; ++i) {
     const tars_w8a8_out& o = outs[i];
     a.g[i].W = o.W;
@@ -271,7 +304,7 @@ int tars_gemm_w8a8(const int8_t* A, int64_t lda, const float* srow, const int8_t
 int tars_quant_gemm_w8a8(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s,
                          int32_t M, int32_t K, const tars_w8a8_out* outs, int32_t nouts,
                          void* stream) {
-  return tars::quant_gemm_w8a8_checked(x, lda, q, ldq, s, M, K, outs, nouts, nullptr, 0, stream);
+  return tars::quant_gemm_w8a8_checked(x, lda, q, ldq, s, M, K, outs, nouts, nullptr, 0, stream, nullptr);
 }
 
 int tars_gemm_w8a8_ksplit(const int8_t* A, int64_t lda, const float* srow,

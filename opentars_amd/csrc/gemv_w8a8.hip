@@ -22,6 +22,7 @@
 //
 // Roofline: HBM. Algorithmic bytes per row: K (weights) + 4 (scale) + 4 (output) (+4 bias).
 #include "kernels.h"
+#include "row_sums.h"
 
 namespace tars {
 namespace {
@@ -384,7 +385,7 @@ struct QuantGemvKernargs {
 constexpr size_t kQuantGemvArgsOffset = offsetof(QuantGemvKernargs, a);
 static_assert(kQuantGemvArgsOffset == 56, "the preloaded scalars take 56 bytes before the argument block");
 
-template <int L, int CPL, int U, bool SIMPLE, bool PAIR>
+template <int L, int CPL, int U, bool SIMPLE, bool PAIR, bool NORM>
 __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* x, int64_t lda, const int8_t* W0,
                                                                    const int8_t* W1, const int8_t* W2,
                                                                    const int8_t* W3, int K, int N, QuantGemvArgs a) {
@@ -393,6 +394,10 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   // PAIR: a wave's U rows are U / 2 row pairs (row n of matrix 0, row n of matrix 1), for the gated
   // product; otherwise U rows of matrix z
   static_assert(!PAIR || (L == 64 && CPL > 0 && U % 2 == 0), "row pairs on whole-wave rows");
+  // NORM: a.pro's residual add and norm form the quantizer's input row (whole-wave rows, K <= 2048)
+  static_assert(!NORM || (L == 64 && CPL >= 1 && CPL <= 2), "norm prologue on rows of at most 2048");
+  __shared__ __align__(16) float nrm[NORM ? 2048 : 4];
+  __shared__ float nrm_bcast;
   constexpr int kSlots = 64 / L;
   constexpr int UR = PAIR ? U / 2 : U;          // row indices per wave
   constexpr int kRows = kWaves * kSlots * UR;  // row indices per workgroup
@@ -463,6 +468,64 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   const int per_tensor1 = PAIR ? kload<int>(kg1 + offsetof(RowColEpilogue, scol_per_tensor)) : 0;
   const float* const bias1 = PAIR && !SIMPLE ? kload<const float*>(kg1 + offsetof(RowColEpilogue, bias)) : nullptr;
   float sc, bi, sc1 = 0.0f, bi1 = 0.0f;
+  // NORM: the prologue's operands (the residual rows, gamma, beta), loaded once their addresses
+  // are in, and its outputs
+  float4 rb[XV], gb[XV], bb[XV];
+  const float* pB = nullptr;
+  const float* pbeta = nullptr;
+  float* psum = nullptr;
+  float* py = nullptr;
+  int64_t ldsum = 0, ldpy = 0;
+  int pfn = 0;
+  float peps = 0.0f;
+  if constexpr (NORM) {
+    const KArg kp = ka + offsetof(QuantGemvArgs, pro);
+    pB = kload<const float*>(kp + offsetof(NormPrologue, B));
+    const int64_t ldb = kload<int64_t>(kp + offsetof(NormPrologue, ldb));
+    const float* const gamma = kload<const float*>(kp + offsetof(NormPrologue, gamma));
+    pbeta = kload<const float*>(kp + offsetof(NormPrologue, beta));
+    pfn = kload<int>(kp + offsetof(NormPrologue, fn));
+    peps = kload<float>(kp + offsetof(NormPrologue, eps));
+    psum = kload<float*>(kp + offsetof(NormPrologue, sum));
+    ldsum = kload<int64_t>(kp + offsetof(NormPrologue, ldsum));
+    py = kload<float*>(kp + offsetof(NormPrologue, y));
+    ldpy = kload<int64_t>(kp + offsetof(NormPrologue, ldy));
+    const float4* brow = reinterpret_cast<const float4*>(pB ? reinterpret_cast<const char*>(pB) + m * ldb
+                                                            : reinterpret_cast<const char*>(x) + m * lda);
+    const float4* g4 = reinterpret_cast<const float4*>(gamma);
+    const float4* b4 = reinterpret_cast<const float4*>(pbeta ? pbeta : gamma);
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      const int ii = i < K4 ? i : 0;
+      rb[j] = brow[ii];
+      gb[j] = g4[ii];
+      bb[j] = b4[ii];
+    }
+  }
+
+  // NORM: every workgroup forms the row (ftz(x + B), or ftz(x)) and its norm; the first
+  // workgroup stores both (the ELT's and the norm's outputs)
+  if constexpr (NORM) {
+    const bool store_pro = blockIdx.x == 0 && blockIdx.z == 0;
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      const float4 v = xr[j];
+      xr[j] = pB ? make_float4(ftz(fadd(act_fn(v.x, 0), rb[j].x)), ftz(fadd(act_fn(v.y, 0), rb[j].y)),
+                               ftz(fadd(act_fn(v.z, 0), rb[j].z)), ftz(fadd(act_fn(v.w, 0), rb[j].w)))
+                 : make_float4(ftz(v.x), ftz(v.y), ftz(v.z), ftz(v.w));
+      if (pB && psum && store_pro && i < K4) reinterpret_cast<float4*>(reinterpret_cast<char*>(psum) + m * ldsum)[i] = xr[j];
+    }
+    norm_row_f4<XV>(pfn, K, peps, xr, gb, bb, pbeta != nullptr, nrm, &nrm_bcast);
+    if (py && store_pro) {
+#pragma unroll
+      for (int j = 0; j < XV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < K4) reinterpret_cast<float4*>(reinterpret_cast<char*>(py) + m * ldpy)[i] = xr[j];
+      }
+    }
+  }
 
   // the workgroup quantizes row m into LDS
   uint32_t mx = 0;
@@ -664,6 +727,22 @@ int gcd(int a, int b) {
 template <int L, int CPL, int U>
 constexpr bool kPairs = L == 64 && CPL >= 1 && CPL <= 4 && (U == 2 || U == 4 || U == 6);
 
+// One launch of the fused kernel, with the norm prologue when b carries one (instances exist for
+// whole-wave rows of at most two chunks per lane; launch_quant_gemv_w8a8 refuses other K).
+template <int L, int CPL, int U, bool SIMPLE, bool PAIR>
+hipError_t launch_qg(dim3 grid, size_t lds, hipStream_t s, const int8_t* const* Wz, int N, const QuantGemvArgs& b) {
+  constexpr bool kNorm = L == 64 && CPL >= 1 && CPL <= 2;
+  if (b.pro.fn) {
+    if constexpr (!kNorm) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR, kNorm>), grid, dim3(kThreads), lds, s, b.x, b.lda,
+                       Wz[0], Wz[1], Wz[2], Wz[3], b.K, N, b);
+  } else {
+    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR, false>), grid, dim3(kThreads), lds, s, b.x, b.lda,
+                       Wz[0], Wz[1], Wz[2], Wz[3], b.K, N, b);
+  }
+  return hipGetLastError();
+}
+
 template <int L, int CPL, int U, bool SIMPLE>
 hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
   constexpr int rows_per_block = kWaves * (64 / L) * U;
@@ -672,9 +751,8 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
       const int N = a.g[0].N;
       const unsigned blocks = (N + kWaves * (U / 2) - 1) / (kWaves * (U / 2));
       const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
-      hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, true>), dim3(blocks, a.M, 1), dim3(kThreads), lds,
-                         s, a.x, a.lda, a.g[0].W, a.g[1].W, a.g[0].W, a.g[0].W, a.K, N, a);
-      return hipGetLastError();
+      const int8_t* const Wz[4] = {a.g[0].W, a.g[1].W, a.g[0].W, a.g[0].W};
+      return launch_qg<L, CPL, U, SIMPLE, true>(dim3(blocks, a.M, 1), lds, s, Wz, N, a);
     }
     return hipErrorInvalidValue;
   }
@@ -702,7 +780,8 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
     a.ngroups = np;
   }
   // launches of up to four consecutive matrices (pieces) of one height; only the first stores the
-  // quantized rows (outputs never overlap x, so every launch reads the same row)
+  // quantized rows and the norm prologue's outputs (outputs never overlap x, so every launch reads
+  // the same row)
   const size_t lds = static_cast<size_t>((a.K + 15) / 16 * 16);
   QuantGemvArgs b = a;
   for (int first = 0; first < a.ngroups;) {
@@ -713,14 +792,14 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
     if (first > 0) {
       b.q = nullptr;
       b.s = nullptr;
+      b.pro.sum = nullptr;
+      b.pro.y = nullptr;
     }
     const int N = b.g[0].N;
     const int8_t* Wz[4];
     for (int i = 0; i < 4; ++i) Wz[i] = b.g[i < n ? i : 0].W;
     const unsigned blocks = (N + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, false>), dim3(blocks, a.M, n), dim3(kThreads), lds, s,
-                       a.x, a.lda, Wz[0], Wz[1], Wz[2], Wz[3], a.K, N, b);
-    const hipError_t e = hipGetLastError();
+    const hipError_t e = launch_qg<L, CPL, U, SIMPLE, false>(dim3(blocks, a.M, n), lds, s, Wz, N, b);
     if (e != hipSuccess) return e;
     first += n;
   }
@@ -777,12 +856,18 @@ hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
   for (int i = 0; i < a.ngroups; ++i) rows += a.g[i].N;
   int u = fused_rows_per_wave(rows, a.K);
   if (a.prod) u = u == 1 ? 2 : u == 8 ? 4 : u;  // an even number of rows: whole pairs
+  if (a.pro.fn && !quant_gemv_norm_supported(a.K)) return hipErrorInvalidValue;
   return dispatch<QuantGemvArgs, GoFused>(a, a.K, u, s);
 }
 
 bool quant_gemv_pairs_supported(int K) {
   const int C = K / 16;  // whole-wave rows (more than 32 chunks), at most four chunks per lane
   return K % 16 == 0 && C > 32 && C <= 256;
+}
+
+bool quant_gemv_norm_supported(int K) {
+  const int C = K / 16;  // whole-wave rows (more than 32 chunks), at most two chunks per lane
+  return K % 16 == 0 && C > 32 && C <= 128;
 }
 
 // K split up to a total K of 8192: four waves per row (measured on MI355X at C2, K = 6912 in two

@@ -164,6 +164,24 @@ struct GemvGroup {
   int N;
 };
 
+// Optional residual add and norm in front of the fused quantizer (the executor's fusion of ELT ADD
+// -> LayerNorm / RMSNorm / L2Norm -> ROW_QUANT -> GEMMs; quant_gemv_norm_supported(K)): the
+// kernel's x rows are the ELT's A rows (the norm's input rows when B is null). Every workgroup
+// forms ftz(A + B) and its norm in registers and quantizes the norm's fp32 output values; the
+// first workgroup also stores the sum (at sum) and the norm's output (at y).
+struct NormPrologue {
+  int fn;               // a RowFn norm (ROWFN_LAYERNORM / RMSNORM / L2NORM); 0: no prologue
+  const float* B;       // rows added to x (nullptr: the norm reads x itself)
+  int64_t ldb;
+  float* sum;           // with B: the sum's rows (fp32)
+  int64_t ldsum;
+  const float* gamma;   // [K]
+  const float* beta;    // [K] or nullptr
+  float eps;
+  float* y;             // the norm's output rows (fp32)
+  int64_t ldy;
+};
+
 struct QuantGemvArgs {
   const float* x;        // [M, K] fp32 rows at stride lda bytes
   int64_t lda;
@@ -179,6 +197,7 @@ struct QuantGemvArgs {
   // (in place: then only the product is stored there); fp32 outputs only.
   float* prod;
   int64_t ldprod;
+  NormPrologue pro;  // pro.fn != 0: the residual add and norm in front of the quantizer
 };
 
 // Row functions, elementwise ops, rotary embedding and fp32 dot products (rowops.hip). Row strides
@@ -330,6 +349,7 @@ hipError_t launch_quant_rows(const QuantArgs& a, hipStream_t s);
 hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s);
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s);
 bool quant_gemv_pairs_supported(int K);  // whether a.prod (the gated product) can run at this K
+bool quant_gemv_norm_supported(int K);   // whether a.pro (a norm prologue) can run at this K
 hipError_t launch_gemm_w8a8_mfma(const W8A8Args& a, hipStream_t s);
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s);
 hipError_t launch_gemm_w8a8_ksplit_mfma(const KSplitArgs& a, hipStream_t s);

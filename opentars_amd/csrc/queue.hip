@@ -512,12 +512,20 @@ namespace tars {
 void set_last_error(const std::string& what);
 int w8a8_path();
 int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s, int32_t M, int32_t K,
-                            const tars_w8a8_out* outs, int32_t nouts, float* prod, int64_t ldprod, void* stream);
+                            const tars_w8a8_out* outs, int32_t nouts, float* prod, int64_t ldprod, void* stream,
+                            const NormPrologue* pro);
 }  // namespace tars
 
 namespace {
 
 bool g_fusion = true;
+
+float f32_bits(uint64_t v) {
+  const uint32_t b = static_cast<uint32_t>(v);
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
 
 u128 addr(const Desc& d, Field off) { return static_cast<u128>(d[F_BASE_ADDR]) + d[off]; }
 
@@ -530,9 +538,11 @@ u128 addr(const Desc& d, Field off) { return static_cast<u128>(d[F_BASE_ADDR]) +
 // call refuses before launching and the descriptors run one by one. `fused` = GEMMs folded in.
 // One ROW_QUANT (M = 1) and the GEMMs reading its output, as one tars_quant_gemm_w8a8 call.
 // With `elt` (a gated group): the two GEMMs' ELT MUL runs in the same launch (the product of the
-// fp32 outputs stored at the ELT's output, see fuse_group).
+// fp32 outputs stored at the ELT's output, see fuse_group). With `norm` (and `add`): the norm whose
+// output the quantizer reads (and the residual ELT ADD whose output the norm reads) run in the
+// same launch as its prologue (see fuse_norm_group).
 int launch_fused(uint8_t* image, const Desc& dq, const std::vector<Desc>& members, hipStream_t s,
-                 const Desc* elt = nullptr) {
+                 const Desc* elt = nullptr, const Desc* add = nullptr, const Desc* norm = nullptr) {
   tars_w8a8_out outs[4];
   for (size_t k = 0; k < members.size(); ++k) {
     const Desc& d = members[k];
@@ -550,11 +560,31 @@ int launch_fused(uint8_t* image, const Desc& dq, const std::vector<Desc>& member
   uint8_t* B = image + dq[F_BASE_ADDR];
   const Strides sq = strides(dq);
   float* prod = elt ? reinterpret_cast<float*>(image + (*elt)[F_BASE_ADDR] + (*elt)[F_Y_OFF]) : nullptr;
-  return tars::quant_gemm_w8a8_checked(reinterpret_cast<const float*>(B + dq[F_A_OFF]), static_cast<int64_t>(sq.lda),
-                                       reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
+  const float* x = reinterpret_cast<const float*>(B + dq[F_A_OFF]);
+  int64_t lda = static_cast<int64_t>(sq.lda);
+  tars::NormPrologue pro{};
+  if (norm) {  // one row: the strides never apply
+    const Desc& r = *norm;
+    uint8_t* RB = image + r[F_BASE_ADDR];
+    pro.fn = static_cast<int>(r[F_CTRL] & 7);
+    pro.gamma = reinterpret_cast<const float*>(RB + r[F_SCALE_OFF]);
+    pro.beta = has_bias(r[F_EPI]) ? reinterpret_cast<const float*>(RB + r[F_BIAS_OFF]) : nullptr;
+    pro.eps = f32_bits(r[F_W_OFF]);
+    pro.y = reinterpret_cast<float*>(RB + r[F_Y_OFF]);
+    x = reinterpret_cast<const float*>(RB + r[F_A_OFF]);
+    lda = 0;
+    if (add) {
+      const Desc& e = *add;
+      uint8_t* EB = image + e[F_BASE_ADDR];
+      x = reinterpret_cast<const float*>(EB + e[F_A_OFF]);
+      pro.B = reinterpret_cast<const float*>(EB + e[F_W_OFF]);
+      pro.sum = reinterpret_cast<float*>(EB + e[F_Y_OFF]);
+    }
+  }
+  return tars::quant_gemm_w8a8_checked(x, lda, reinterpret_cast<int8_t*>(B + dq[F_Y_OFF]), static_cast<int64_t>(sq.ldy),
                                        reinterpret_cast<float*>(B + dq[F_SCALE_OFF]), 1, static_cast<int32_t>(dq[F_N]),
                                        outs, static_cast<int32_t>(members.size()), prod,
-                                       elt ? static_cast<int64_t>(strides(*elt).ldy) : 0, s);
+                                       elt ? static_cast<int64_t>(strides(*elt).ldy) : 0, s, norm ? &pro : nullptr);
 }
 
 // An MLP's gated product after a two-GEMM group (tars_mini/llm.py:620-624: the gate GEMM with its
@@ -573,14 +603,17 @@ bool gated_elt(const Checked& e, const Desc& g0, const Desc& g1, uintptr_t image
          (image + d[F_BASE_ADDR] + d[F_Y_OFF]) % 16 == 0 && tars::quant_gemv_pairs_supported(static_cast<int>(g0[F_K]));
 }
 
+// With `norm` (and `add`), the prologue fuse_norm_group checked runs in the same launch.
 int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
                int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
-               int& fused, std::vector<Desc>& group, Desc& elt, bool& gated) {
+               int& fused, std::vector<Desc>& group, Desc& elt, bool& gated, const Desc* add = nullptr,
+               const Desc* norm = nullptr) {
   fused = 0;
   group.clear();
   gated = false;
   const Desc& dq = quant.d;
-  if (!g_fusion || dq[F_OPCODE] != OP_ROW || dq[F_M] != 1 || (reinterpret_cast<uintptr_t>(image) + dq[F_BASE_ADDR]) % 16)
+  if (!g_fusion || quant.err != E_OK || quant.overlap || dq[F_OPCODE] != OP_ROW || (dq[F_CTRL] & 7) != ROW_QUANT ||
+      dq[F_M] != 1 || (reinterpret_cast<uintptr_t>(image) + dq[F_BASE_ADDR]) % 16)
     return TARS_OK;
   std::vector<Checked> members;
   for (int32_t j = i + 1; j < n && static_cast<uint64_t>(j) < in_image && members.size() < 4; ++j) {
@@ -606,7 +639,7 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
     const Checked e = check(q.data() + static_cast<size_t>(je) * kDescBytes, image_len, core_id, gemv_only);
     if (gated_elt(e, members[0].d, members[1].d, reinterpret_cast<uintptr_t>(image)) &&
         !(rest_lo < rest_hi && overlaps(rest, e.y))) {
-      const int rc = launch_fused(image, dq, group, s, &e.d);
+      const int rc = launch_fused(image, dq, group, s, &e.d, add, norm);
       if (rc == TARS_OK) {
         fused = 3;
         elt = e.d;
@@ -617,7 +650,7 @@ int fuse_group(uint8_t* image, const Checked& quant, const std::vector<uint8_t>&
       tars::set_last_error("");  // the product overlaps an operand: the ELT runs on its own
     }
   }
-  const int rc = launch_fused(image, dq, group, s);
+  const int rc = launch_fused(image, dq, group, s, nullptr, add, norm);
   if (rc == TARS_E_OVERLAP) {
     tars::set_last_error("");
     group.clear();
@@ -763,13 +796,6 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
 // RMSNorm / L2Norm whose input rows are exactly the ELT's output rows, the rows fit the kernel, the
 // ELT runs in place or apart from its A rows, and no output of the pair lands on the ELT's B rows,
 // gamma, beta, the other output, the norm's input, or a later descriptor.
-float f32_bits(uint64_t v) {
-  const uint32_t b = static_cast<uint32_t>(v);
-  float f;
-  std::memcpy(&f, &b, 4);
-  return f;
-}
-
 // The kernel arguments of a LayerNorm / RMSNorm / L2Norm descriptor (as tars_row_op builds them).
 tars::RowArgs norm_args(uint8_t* image, const Desc& rd) {
   uint8_t* RB = image + rd[F_BASE_ADDR];
@@ -846,6 +872,70 @@ int fuse_add_norm(uint8_t* image, const Checked& e, const std::vector<uint8_t>& 
     norm = rd;
   }
   return rc;
+}
+
+// A residual ELT ADD and its norm (or a norm alone) in front of a decode-row quantizer group: the
+// ELT (dense fp32, no activation, fp32 output), the LayerNorm / RMSNorm / L2Norm of exactly its
+// output (fp32 output), then a ROW_QUANT of exactly the norm's output with the GEMMs fuse_group
+// takes, all on one row (tars_mini/llm.py:640, 699, 767: a residual add, then the next norm and
+// projections). They run as one launch whose every workgroup forms the sum and the norm in
+// registers (the first workgroup stores both), bit-identical to the descriptors in order. Refused
+// when the prologue's outputs land on a later descriptor, or (the fused call's checks) on an input
+// or another output of the launch, which excludes an ELT in place; and when K is outside the
+// kernel's prologue instances. `fused` = descriptors after i folded into i's launch.
+int fuse_norm_group(uint8_t* image, const Checked& c, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
+                    int32_t n, u128 queue_addr, u128 q_end, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
+                    int& fused, bool& has_add, Desc& add, Desc& norm, Desc& quant, std::vector<Desc>& group, Desc& elt,
+                    bool& gated) {
+  fused = 0;
+  has_add = false;
+  if (!g_fusion) return TARS_OK;
+  const Desc& d = c.d;
+  auto is_norm = [](const Desc& r) {
+    const uint64_t fn = r[F_CTRL] & 7;
+    return r[F_OPCODE] == OP_ROW && (fn == ROW_LAYERNORM || fn == ROW_RMSNORM || fn == ROW_L2NORM) &&
+           out_code(r[F_EPI]) == OUT_FP32 && r[F_M] == 1;
+  };
+  if (d[F_OPCODE] == OP_ELT) {
+    if ((d[F_CTRL] & 3) != ELT_ADD || d[F_HDR_RSV] != 0 || act_code(d[F_EPI]) != 0 || out_code(d[F_EPI]) != OUT_FP32 ||
+        d[F_M] != 1)
+      return TARS_OK;
+    has_add = true;
+  } else if (!is_norm(d)) {
+    return TARS_OK;
+  }
+  const int32_t ir = has_add ? i + 1 : i, iq = ir + 1;
+  if (iq + 1 >= n || static_cast<uint64_t>(iq) + 1 >= in_image) return TARS_OK;
+  const Checked r = has_add ? check(q.data() + static_cast<size_t>(ir) * kDescBytes, image_len, core_id, gemv_only) : c;
+  const Desc& rd = r.d;
+  if (r.err != E_OK || r.overlap || !is_norm(rd) || !tars::quant_gemv_norm_supported(static_cast<int>(rd[F_N])) ||
+      (has_add && (d[F_N] != rd[F_N] || addr(rd, F_A_OFF) != addr(d, F_Y_OFF))))
+    return TARS_OK;
+  const Checked qc = check(q.data() + static_cast<size_t>(iq) * kDescBytes, image_len, core_id, gemv_only);
+  const Desc& dq = qc.d;
+  if (qc.err != E_OK || qc.overlap || dq[F_OPCODE] != OP_ROW || (dq[F_CTRL] & 7) != ROW_QUANT || dq[F_N] != rd[F_N] ||
+      addr(dq, F_A_OFF) != addr(rd, F_Y_OFF))
+    return TARS_OK;
+  const uintptr_t img = reinterpret_cast<uintptr_t>(image);
+  auto aligned16 = [&](const Desc& x, Field f) { return (img + x[F_BASE_ADDR] + x[f]) % 16 == 0; };
+  if (!aligned16(rd, F_A_OFF) || !aligned16(rd, F_Y_OFF) || !aligned16(rd, F_SCALE_OFF) ||
+      (has_bias(rd[F_EPI]) && !aligned16(rd, F_BIAS_OFF)) ||
+      (has_add && (!aligned16(d, F_A_OFF) || !aligned16(d, F_W_OFF) || !aligned16(d, F_Y_OFF))))
+    return TARS_OK;
+  Segs outs = r.y;
+  if (has_add) outs.insert(outs.end(), c.y.begin(), c.y.end());
+  const u128 later = queue_addr + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(i) + 1);
+  if (later < q_end && overlaps(Segs{interval(later, q_end)}, outs)) return TARS_OK;
+  int fq = 0;
+  const int rc = fuse_group(image, qc, q, iq, in_image, n,
+                            queue_addr + static_cast<u128>(kDescBytes) * (static_cast<uint64_t>(iq) + 1), q_end, image_len,
+                            core_id, gemv_only, s, fq, group, elt, gated, has_add ? &d : nullptr, &rd);
+  if (rc != TARS_OK || fq == 0) return rc;
+  fused = (iq - i) + fq;
+  add = d;
+  norm = rd;
+  quant = dq;
+  return TARS_OK;
 }
 
 // A norm with an fp32 output followed by the RoPE of its output rows (a decoder's q / k norm and
@@ -967,6 +1057,8 @@ struct Step {
   bool norm_rope2 = false;
   Desc elt{};                  // a gated group's ELT MUL (gated: group is gate and up)
   bool gated = false;
+  Desc pro_add{}, pro_norm{};  // with pro: the group's prologue (pro_has_add: the ELT ADD, then the norm)
+  bool pro = false, pro_has_add = false;
 };
 
 struct Plan {
@@ -983,9 +1075,10 @@ struct Plan {
 
 // Fused launches run (diagnostics for tests and benchmarks): quantizer + GEMMs, attention,
 // residual ADD + norm, norm + RoPE pairs (two when two pairs share a launch), launches that ran two
-// such pairs, and (also counted as quantizer + GEMMs) the gated product's
-// ELT MUL folded into its GEMMs; counted when a queue is dispatched and when a plan replays.
-constexpr int kFusionKinds = 6;
+// such pairs, and (also counted as quantizer + GEMMs) the gated product's ELT MUL folded into its
+// GEMMs and a norm (with its residual ADD) in front of the quantizer; counted when a queue is
+// dispatched and when a plan replays.
+constexpr int kFusionKinds = 7;
 std::atomic<int64_t> g_fused_launches[kFusionKinds];
 
 void count_fused(const std::vector<Step>& steps) {
@@ -994,6 +1087,7 @@ void count_fused(const std::vector<Step>& steps) {
     if (k >= 0) g_fused_launches[k].fetch_add(st.norm_rope2 ? 2 : 1, std::memory_order_relaxed);
     if (st.gated) g_fused_launches[4].fetch_add(1, std::memory_order_relaxed);
     if (st.norm_rope2) g_fused_launches[5].fetch_add(1, std::memory_order_relaxed);
+    if (st.pro) g_fused_launches[6].fetch_add(1, std::memory_order_relaxed);
   }
 }
 
@@ -1011,7 +1105,8 @@ int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) 
                                                           st.norm_rope2 ? &st.fourth : nullptr)
                    : !st.attn.empty() ? launch_attention_group(image, st.attn, s)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
-                                      : launch_fused(image, st.d, st.group, s, st.gated ? &st.elt : nullptr);
+                                      : launch_fused(image, st.d, st.group, s, st.gated ? &st.elt : nullptr,
+                                                     st.pro_has_add ? &st.pro_add : nullptr, st.pro ? &st.pro_norm : nullptr);
     if (rc != TARS_OK) return rc;
   }
   return TARS_OK;
@@ -1192,6 +1287,30 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       if (cacheable) steps.push_back(Step{c.d, {}, std::move(heads)});
       i += 3 * fused - 1;  // `fused` heads of three descriptors ran as one launch
       continue;
+    }
+    {
+      bool has_add = false;
+      Desc add{}, nrm{}, quant{};
+      if (int rc = fuse_norm_group(image, c, q, i, in_image, n, static_cast<u128>(queue_addr), q_end, image_len, core_id,
+                                   gemv_only != 0, s, fused, has_add, add, nrm, quant, group, elt, gated))
+        return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+      if (fused) {
+        g_fused_launches[0].fetch_add(1, std::memory_order_relaxed);
+        g_fused_launches[6].fetch_add(1, std::memory_order_relaxed);
+        if (gated) g_fused_launches[4].fetch_add(1, std::memory_order_relaxed);
+        if (cacheable) {
+          Step st{quant, std::move(group), {}};
+          st.elt = elt;
+          st.gated = gated;
+          st.pro = true;
+          st.pro_has_add = has_add;
+          st.pro_add = add;
+          st.pro_norm = nrm;
+          steps.push_back(std::move(st));
+        }
+        i += fused;  // the (ELT and) norm, the quantizer and its GEMMs (and a gated ELT) ran as one launch
+        continue;
+      }
     }
     Desc norm{};
     if (int rc = fuse_add_norm(image, c, q, i, in_image, n, static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) *

@@ -18,25 +18,12 @@
 #include <type_traits>
 
 #include "kernels.h"
+#include "row_sums.h"
 
 namespace tars {
 namespace {
 
 constexpr int kRowThreads = 256;  // 16 row groups of 16 lanes
-
-__device__ __forceinline__ float fdpp_xor1(float v) { return __int_as_float(dpp<kDppQuadXor1>(__float_as_int(v))); }
-__device__ __forceinline__ float fdpp_xor2(float v) { return __int_as_float(dpp<kDppQuadXor2>(__float_as_int(v))); }
-__device__ __forceinline__ float fdpp_half(float v) { return __int_as_float(dpp<kDppRowHalfMirror>(__float_as_int(v))); }
-__device__ __forceinline__ float fdpp_mirror(float v) { return __int_as_float(dpp<kDppRowMirror>(__float_as_int(v))); }
-
-// The pairwise fold of a 16-lane group's partial chain sums (every lane receives the row sum,
-// canonicalized).
-__device__ __forceinline__ float fold16(float v) {
-  v = fadd_chain(v, fdpp_xor1(v));
-  v = fadd_chain(v, fdpp_xor2(v));
-  v = fadd_chain(v, fdpp_half(v));
-  return chain_end(fadd_chain(v, fdpp_mirror(v)));
-}
 
 __device__ __forceinline__ const float* frow(const void* base, int64_t ld, int m) {
   return reinterpret_cast<const float*>(static_cast<const char*>(base) + m * ld);
@@ -77,55 +64,6 @@ __device__ __forceinline__ void for_lane(const float* x, int l, int n, Fn&& f) {
   }
 }
 
-// The 16-lane chains of sum16 over rows of n values in LDS (row i at v + i * ld), of the values
-// (SQUARE: of fmul(v, v)): lane l of threads 16 i .. 16 i + 15 adds element l, l + 16, ... of row i
-// in order from +0, then the pairwise fold; row i's sum lands in bcast[i] for every thread of the
-// workgroup. v must hold contract results.
-template <bool SQUARE>
-__device__ __forceinline__ void lds_sum16_rows(const float* v, int ld, int rows, int n, float* bcast) {
-  __syncthreads();  // v complete
-  if (static_cast<int>(threadIdx.x) < 16 * rows) {
-    const int l = threadIdx.x & 15, i = threadIdx.x >> 4;
-    v += i * ld;
-    // the chain unflushed with its partial sums checked (its terms are flushed contract results),
-    // then with the flushes when one was subnormal
-    auto chain = [&](auto flushed) {
-      float acc = 0.0f;
-      uint32_t mk = ~0u;
-      auto step = [&](float t) {
-        if constexpr (decltype(flushed)::value) {
-          acc = fadd_chain(acc, t);
-        } else {
-          acc = __fadd_rn(acc, t);
-          mk = min(mk, sub_key(acc));
-        }
-      };
-      int j0 = 0;
-      for (; j0 + 16 * 8 <= n; j0 += 16 * 8) {
-        float t[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = SQUARE ? fmul(v[j0 + l + 16 * u], v[j0 + l + 16 * u]) : v[j0 + l + 16 * u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) step(t[u]);
-      }
-      for (int j = j0 + l; j < n; j += 16) step(SQUARE ? fmul(v[j], v[j]) : v[j]);
-      return mk < kSubKeyNormal ? ffrom(kCanonNaN) : acc;  // NaN marks "recompute" (a NaN sum recomputes too)
-    };
-    float acc = chain(std::false_type{});
-    if (__builtin_expect(is_nan(acc), 0)) acc = chain(std::true_type{});
-    acc = fold16(acc);
-    if (l == 0) bcast[i] = acc;
-  }
-  __syncthreads();
-}
-
-// The sum16 of v[0..n) in LDS (as lds_sum16_rows for one row), returned to every thread.
-template <bool SQUARE>
-__device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) {
-  lds_sum16_rows<SQUARE>(v, 0, 1, n, bcast);
-  return *bcast;
-}
-
 // Rows up to kLdsRow elements: one workgroup per row, the row staged in LDS; the elementwise work
 // (exp, differences, squares, outputs) spread over all 256 threads, only the fixed-order sums on
 // 16 lanes (golden.py:358-380; numerics.py:328-380).
@@ -159,12 +97,12 @@ __device__ __forceinline__ void norm_in_regs(const RowArgs& a, int m, float (&xv
       xv[u] = fadd(xv[u], nmean);  // d = x + -mean
       if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
     }
-    rs = rsqrt_f(fadd(fmul(lds_sum16<false>(v, N, bcast), kinv), a.eps));
+    rs = rsqrt_f(fadd(fmul(lds_sum16<false, true>(v, N, bcast), kinv), a.eps));
   } else {
 #pragma unroll
     for (int u = 0; u < kRowE; ++u)
       if (t + u * kRowThreads < N) v[t + u * kRowThreads] = fmul(xv[u], xv[u]);
-    const float ss = lds_sum16<false>(v, N, bcast);
+    const float ss = lds_sum16<false, true>(v, N, bcast);
     rs = rsqrt_f(fadd(a.fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, a.eps));
   }
 #pragma unroll
@@ -243,7 +181,7 @@ __global__ __launch_bounds__(kRowThreads) void row_lds_kernel(RowArgs a) {
     const float nmx = fneg(k == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k));
     __syncthreads();  // every thread has read red before v is rewritten
     for (int j = t; j < N; j += kRowThreads) v[j] = j < V ? exp_f(fadd(v[j], nmx)) : 0.0f;
-    const float r = recip_f(lds_sum16<false>(v, N, &bcast));
+    const float r = recip_f(lds_sum16<false, true>(v, N, &bcast));  // exp_f values: 0, normal, inf or NaN
     for (int j = t; j < N; j += kRowThreads) store_out(a.y, yrow, j, a.out, fmul(v[j], r), a.out_scale);
     return;
   }
@@ -754,7 +692,7 @@ __device__ __forceinline__ int softmax_lds(float* sp, int nk, int V, float* pr, 
   const float nmx = fneg(k4 == 0xFFFFFFFFu ? ffrom(kCanonNaN) : fmax_from_key(k4));
   __syncthreads();
   for (int j = t; j < nk; j += 256) sp[j] = j < V ? exp_f(fadd(sp[j], nmx)) : 0.0f;
-  const float r = recip_f(lds_sum16<false>(sp, nk, bcast));
+  const float r = recip_f(lds_sum16<false, true>(sp, nk, bcast));  // exp_f values: 0, normal, inf or NaN
   int above1 = 0;
   for (int j = t; j < nk; j += 256) {
     const float p = fmul(sp[j], r);
@@ -1001,7 +939,7 @@ __device__ __forceinline__ int softmax_rows_lds(float* sp, int ldp, int M, int n
 #pragma unroll
     for (int i = 0; i < Q; ++i) sp[i * ldp + j] = j < V[i] ? e[i] : 0.0f;
   }
-  lds_sum16_rows<false>(sp, ldp, Q, nk, bcast);
+  lds_sum16_rows<false, true>(sp, ldp, Q, nk, bcast);  // exp_f values: 0, normal, inf or NaN
   float r[Q];
 #pragma unroll
   for (int i = 0; i < Q; ++i) r[i] = recip_f(bcast[i]);

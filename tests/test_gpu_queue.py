@@ -645,6 +645,77 @@ def test_gated_mlp_product(seed, fusion):
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
+def add_norm_quant_group(p: Program, K: int, Ns, add: bool = True, gated: bool = False, inplace: bool = False,
+                         sum_over_gamma: bool = False, fn=None):
+    """[ELT ADD of two fp32 rows ->] norm (fp32 out) -> ROW_QUANT of the norm's output -> QM_ROWCOL
+    GEMMs of heights Ns reading it [-> the gated product's ELT MUL of the first two], one row: a
+    decoder's residual add, next norm and projections (tars_mini/llm.py:699-705, 767 and the next
+    layer's norm). inplace: the ELT writes over its A row; sum_over_gamma: over the norm's gamma.
+    Both make the executor run the norm apart from the quantizer group."""
+    rng = p.rng
+    g = p.put(rng.normal(1, 0.2, K).astype("<f4").tobytes())
+    x = p.put(rand_rows(p, 1, K).tobytes())
+    if add:
+        b = p.put(rand_rows(p, 1, K).tobytes())
+        y = x if inplace else g if sum_over_gamma else p.alloc(4 * K)
+        p.add(OPCODE=Q.OP_ELT, CTRL=Q.ELT_ADD, EPI=Q.epi(), A_OFF=x, W_OFF=b, Y_OFF=y, M=1, N=K)
+        x = y
+    fn = int(rng.choice([Q.ROW_LAYERNORM, Q.ROW_RMSNORM, Q.ROW_L2NORM])) if fn is None else fn
+    bias = int(rng.integers(0, 2))
+    bb = p.put(rng.normal(0, 0.1, K).astype("<f4").tobytes()) if bias else 0
+    h = p.alloc(4 * K)
+    p.add(OPCODE=Q.OP_ROW, CTRL=fn, EPI=Q.epi(bias=bias), A_OFF=x, Y_OFF=h, SCALE_OFF=g, BIAS_OFF=bb,
+          W_OFF=f32bits(float(rng.choice([1e-6, 1e-5, 0.0]))), M=1, N=K)
+    q, s = p.alloc(K), p.alloc(4)
+    p.add(OPCODE=Q.OP_ROW, CTRL=Q.ROW_QUANT, EPI=Q.epi(out=Q.OUT_INT8), A_OFF=h, Y_OFF=q, SCALE_OFF=s, M=1, N=K)
+    ys = []
+    for k, N in enumerate(Ns):
+        gate = gated and k == 0
+        ys.append(add_w8(p, 1, N, K, Q.QM_ROWCOL, a=q, lda=K, srow=s, act=4 if gate else None,
+                         out=Q.OUT_FP32 if gated else None, bias=int(rng.integers(0, 2))))
+    if gated:
+        p.add(OPCODE=Q.OP_ELT, CTRL=Q.ELT_MUL, EPI=Q.epi(), HDR_RSV=Q.BM_DENSE, A_OFF=ys[0], W_OFF=ys[1], Y_OFF=ys[0],
+              M=1, N=Ns[0])
+
+
+@pytest.mark.parametrize("seed", range(3))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_norm_prologue_groups(seed, fusion):
+    """Residual ELT ADD -> norm -> ROW_QUANT -> GEMMs, which the executor runs as one launch (every
+    workgroup forms the sum and the norm, the first stores them): q/k/v-like heights at K = 1024,
+    a gated MLP at K = 1024, a norm alone in front of the group (the first layer's and the final
+    norm), K = 2048 (two chunks per lane) and K = 768 (a partial chunk row), LayerNorm with and
+    without beta; not as one launch: an ELT in place, a sum over the norm's gamma (the ELT runs on
+    its own, the norm still in front of the quantizer), K = 512 (16-lane rows) and K = 2064 (three
+    chunks per lane). The images equal the oracle's."""
+    image = 24 << 20
+    p = Program(8700 + seed, image=image, qaddr=image - 0x10000)
+    add_norm_quant_group(p, 1024, (512, 256, 256))
+    add_norm_quant_group(p, 1024, (768, 768), gated=True)
+    add_norm_quant_group(p, 1024, (256, 256, 256, 256), add=False)
+    add_norm_quant_group(p, 2048, (256,), fn=Q.ROW_LAYERNORM)
+    add_norm_quant_group(p, 768, (320, 64))
+    add_norm_quant_group(p, 1024, (256,), add=False, fn=Q.ROW_LAYERNORM)
+    add_norm_quant_group(p, 1024, (256, 256), inplace=True)
+    add_norm_quant_group(p, 1024, (256,), sum_over_gamma=True)
+    add_norm_quant_group(p, 512, (256,))
+    add_norm_quant_group(p, 2064, (128,))
+    prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs), qaddr=p.qaddr)
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    counts = NQ.fusion_counts()
+    # the six groups in range and free of hazards took their norm (and ELT), the sum over gamma its norm
+    # alone; every group fused its GEMMs; the ELT in place and K = 512 ran as ELT + norm pairs
+    expect = (7, 10, 1, 2) if fusion else (0, 0, 0, 0)
+    assert tuple(counts[k] for k in ("norm_quant", "quant_gemm", "gated_mlp", "add_norm")) == expect, counts
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 def test_fusion_group_with_a_hazard_runs_one_by_one():
     """A decode row read by three GEMMs where the second GEMM writes over the third's weights: the
     fused launch would race, so the group runs descriptor by descriptor (the third GEMM then reads
@@ -977,5 +1048,7 @@ def test_whole_decode_step_matches_the_oracle(fusion, shape):
     assert counts["gated_mlp"] == (3 * dims["layers"] if fusion and shape == "qwen3_width" else 0), counts
     # each layer's q and k (norm, RoPE) pairs run as one launch
     assert counts["norm_rope_two"] == (3 * dims["layers"] if fusion else 0), counts
+    # at Qwen3 width every norm runs in front of its quantizer group: each layer's two and the final one
+    assert counts["norm_quant"] == (3 * (2 * dims["layers"] + 1) if fusion and shape == "qwen3_width" else 0), counts
     logits = np.frombuffer(bytes(o.ddr[dq.logits:dq.logits + 4 * dq.vocab]), "<f4")
     assert np.isfinite(logits).all() and np.abs(logits).max() > 0
