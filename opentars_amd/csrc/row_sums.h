@@ -55,14 +55,18 @@ __device__ __forceinline__ void lds_sum16_rows(const float* v, int ld, int rows,
           if constexpr (!SQUARE && !NONNEG) mk = min(mk, sub_key(acc));
         }
       };
+      // blocks of a lane's terms read from LDS together, then added: one LDS round trip per block
+      auto block = [&](int j0, auto size) {
+        constexpr int B = decltype(size)::value;
+        float t[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) t[u] = SQUARE ? fmul(v[j0 + l + 16 * u], v[j0 + l + 16 * u]) : v[j0 + l + 16 * u];
+#pragma unroll
+        for (int u = 0; u < B; ++u) step(t[u]);
+      };
       int j0 = 0;
-      for (; j0 + 16 * 8 <= n; j0 += 16 * 8) {
-        float t[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = SQUARE ? fmul(v[j0 + l + 16 * u], v[j0 + l + 16 * u]) : v[j0 + l + 16 * u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) step(t[u]);
-      }
+      for (; j0 + 16 * 32 <= n; j0 += 16 * 32) block(j0, std::integral_constant<int, 32>{});
+      for (; j0 + 16 * 8 <= n; j0 += 16 * 8) block(j0, std::integral_constant<int, 8>{});
       for (int j = j0 + l; j < n; j += 16) step(SQUARE ? fmul(v[j], v[j]) : v[j]);
       return mk < kSubKeyNormal ? ffrom(kCanonNaN) : acc;  // NaN marks "recompute" (a NaN sum recomputes too)
     };

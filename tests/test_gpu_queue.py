@@ -716,6 +716,25 @@ def test_norm_prologue_groups(seed, fusion):
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
+def test_an_int8_norm_is_not_taken_for_a_quantizer():
+    """A norm with an int8 output read by a QM_ROWCOL GEMM as its A row with the norm's gamma as the
+    row scale has a quantizer group's addresses, but it is a norm: the executor runs it as one."""
+    p = Program(8800)
+    K = 1024
+    x = p.put(rand_rows(p, 1, K).tobytes())
+    g = p.put(p.rng.uniform(0.5, 2.0, K).astype("<f4").tobytes())
+    y = p.alloc(K)
+    p.add(OPCODE=Q.OP_ROW, CTRL=Q.ROW_RMSNORM, EPI=Q.epi(out=Q.OUT_INT8), A_OFF=x, Y_OFF=y, SCALE_OFF=g,
+          W_OFF=f32bits(1e-6), M=1, N=K, OUT_SCALE=f32bits(0.05))
+    add_w8(p, 1, 256, K, Q.QM_ROWCOL, a=y, lda=K, srow=g)
+    NQ.fusion_counts(reset=True)
+    (o, ost), (g2, gst) = both(p.image(), len(p.descs))
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    assert NQ.fusion_counts()["quant_gemm"] == 0
+    gd = bytes(g2.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 def test_fusion_group_with_a_hazard_runs_one_by_one():
     """A decode row read by three GEMMs where the second GEMM writes over the third's weights: the
     fused launch would race, so the group runs descriptor by descriptor (the third GEMM then reads
