@@ -176,6 +176,7 @@ int quant_gemm_w8a8_checked(const float* x, int64_t lda, int8_t* q, int64_t ldq,
     if (p.fn != ROWFN_LAYERNORM && p.fn != ROWFN_RMSNORM && p.fn != ROWFN_L2NORM)
       return fail(TARS_E_FIELD, "the norm prologue takes a LayerNorm, RMSNorm or L2Norm");
     if (!tars::quant_gemv_norm_supported(K)) return fail(TARS_E_FIELD, "the norm prologue is not available at this K");
+    if (M != 1) return fail(TARS_E_FIELD, "the norm prologue takes one row");
     if (!p.gamma || !p.y || (p.B != nullptr) != (p.sum != nullptr))
       return fail(TARS_E_ARG, "norm prologue: gamma and y, and B and sum together");
     const int64_t row = 4LL * K;

@@ -284,20 +284,26 @@ __device__ __forceinline__ uint16_t to_fp16_bits(float x) {
 // 127 + j (m in [1, 4)); seed bits(y0) = 0x5F3759DF - (bits(m) >> 1); three correction-form Newton
 // steps y <- y + y * (1/2 + -(1/2 * ((m * y) * y))), each op one rounded contract step; then -k is
 // added to y's exponent field. +-0 -> +-inf, +inf -> +0, negative or NaN -> canonical NaN.
+//
+// As in recip_f, the Newton steps run on raw rounded operations: they depend only on m, and for
+// every m in [1, 4) each product and sum is a positive normal value or exactly 0 (y stays in
+// [0.48, 1.01]; 1/2 - (1/2)(m y^2) is exact by Sterbenz, so 0 or at least 2^-25 in magnitude), so
+// the contract's flush and canonicalize wrappers change nothing (checked exhaustively on the CPU).
+// The special inputs take their results by selects.
 __device__ __forceinline__ float rsqrt_f(float x) {
   const uint32_t xb = fbits(ftz(x));
   const uint32_t mag = xb & 0x7FFFFFFFu;
-  if (mag > kExpo || ((xb & kSign) && mag != 0)) return ffrom(kCanonNaN);
-  if (mag == 0) return ffrom((xb & kSign) | kExpo);
-  if (xb == kExpo) return 0.0f;
   const int E = static_cast<int>((xb >> 23) & 0xFFu) - 127;
   const int j = E & 1, k = E >> 1;  // arithmetic shift: floor, so E = 2k + j for E < 0 too
   const uint32_t mb = (xb & kMant) | (static_cast<uint32_t>(127 + j) << 23);
   const float m = ffrom(mb), half = ffrom(kHalf);
   float y = ffrom(0x5F3759DFu - (mb >> 1));
 #pragma unroll
-  for (int i = 0; i < 3; ++i) y = fadd(y, fmul(y, fadd(half, fneg(fmul(half, fmul(fmul(m, y), y))))));
-  return add_to_exponent(y, -k);
+  for (int i = 0; i < 3; ++i)
+    y = __fadd_rn(y, __fmul_rn(y, __fadd_rn(half, -__fmul_rn(half, __fmul_rn(__fmul_rn(m, y), y)))));
+  const float r = add_to_exponent(y, -k);
+  const bool nan = mag > kExpo || ((xb & kSign) && mag != 0);
+  return nan ? ffrom(kCanonNaN) : mag == 0 ? ffrom((xb & kSign) | kExpo) : xb == kExpo ? 0.0f : r;
 }
 
 // Order key of the contract's fmax (numerics.py:293-303) on a flushed, non-NaN value: unsigned

@@ -385,10 +385,13 @@ struct QuantGemvKernargs {
 constexpr size_t kQuantGemvArgsOffset = offsetof(QuantGemvKernargs, a);
 static_assert(kQuantGemvArgsOffset == 56, "the preloaded scalars take 56 bytes before the argument block");
 
+// The kernel body. NORM (quant_gemv_norm_kernel, one activation row): pB0 and pgamma are the
+// prologue's residual row (x itself when there is none) and gamma, loaded before the weights so the
+// norm waits for them alone; matrix 3's pointer comes from a (W3 is null).
 template <int L, int CPL, int U, bool SIMPLE, bool PAIR, bool NORM>
-__global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* x, int64_t lda, const int8_t* W0,
-                                                                   const int8_t* W1, const int8_t* W2,
-                                                                   const int8_t* W3, int K, int N, QuantGemvArgs a) {
+__device__ __forceinline__ void quant_gemv_body(const float* x, int64_t lda, const int8_t* W0, const int8_t* W1,
+                                                const int8_t* W2, const int8_t* W3, int K, int N, const QuantGemvArgs& a,
+                                                const float* pB0, const float* pgamma) {
   extern __shared__ __align__(16) int8_t qsh[];  // the quantized row, K bytes
   __shared__ uint32_t wave_max[kWaves];
   // PAIR: a wave's U rows are U / 2 row pairs (row n of matrix 0, row n of matrix 1), for the gated
@@ -396,14 +399,16 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   static_assert(!PAIR || (L == 64 && CPL > 0 && U % 2 == 0), "row pairs on whole-wave rows");
   // NORM: a.pro's residual add and norm form the quantizer's input row (whole-wave rows, K <= 2048)
   static_assert(!NORM || (L == 64 && CPL >= 1 && CPL <= 2), "norm prologue on rows of at most 2048");
-  __shared__ __align__(16) float nrm[NORM ? 2048 : 4];
-  __shared__ float nrm_bcast;
+  __shared__ __align__(16) float nrm[NORM ? 4096 : 4];
   constexpr int kSlots = 64 / L;
   constexpr int UR = PAIR ? U / 2 : U;          // row indices per wave
   constexpr int kRows = kWaves * kSlots * UR;  // row indices per workgroup
   const int z = blockIdx.z;
   const int8_t* W = z == 0 ? W0 : z == 1 ? W1 : z == 2 ? W2 : W3;
-  const GemvGroup& gr = a.g[z];
+  if constexpr (NORM)
+    if (z == 3)
+      W = kload<const int8_t*>(kernarg_at(kQuantGemvArgsOffset) + offsetof(QuantGemvArgs, g) + 3 * sizeof(GemvGroup) +
+                               offsetof(GemvGroup, W));
   const int nblk = (N + kRows - 1) / kRows;  // the grid's x extent
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -427,6 +432,18 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
     for (int j = 0; j < XV; ++j) {
       const int i = threadIdx.x + j * kThreads;
       xr[j] = *(i < K4 ? xrow + i : xrow);
+    }
+  }
+  // NORM: the residual row and gamma (the prologue's operands: beta, rarely present, follows the
+  // weights), before the weights
+  float4 rb[XV], gb[XV], bb[XV];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      const int ii = i < K4 ? i : 0;
+      rb[j] = reinterpret_cast<const float4*>(pB0)[ii];
+      gb[j] = reinterpret_cast<const float4*>(pgamma)[ii];
     }
   }
   v4i wv[U][CPL > 0 ? CPL : 1];
@@ -467,10 +484,32 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   const float* const scol1 = PAIR ? kload<const float*>(kg1 + offsetof(RowColEpilogue, scol)) : nullptr;
   const int per_tensor1 = PAIR ? kload<int>(kg1 + offsetof(RowColEpilogue, scol_per_tensor)) : 0;
   const float* const bias1 = PAIR && !SIMPLE ? kload<const float*>(kg1 + offsetof(RowColEpilogue, bias)) : nullptr;
+  // the outputs' fields, read with the others: left to their use at the end, they cost a scalar
+  // cache miss there
+  float* const sout = kload<float*>(ka + offsetof(QuantGemvArgs, s));
+  const KArg kgz = ka + offsetof(QuantGemvArgs, g) + z * sizeof(GemvGroup);
+  void* const Yz = kload<void*>(kgz + offsetof(GemvGroup, Y));
+  const int64_t ldyz = kload<int64_t>(kgz + offsetof(GemvGroup, ldy));
+  const RowColEpilogue epi{nullptr, scol, per_tensor, bias, SIMPLE ? 0 : kload<int>(kg + offsetof(RowColEpilogue, act)),
+                           SIMPLE ? 0 : kload<int>(kg + offsetof(RowColEpilogue, out)),
+                           SIMPLE ? 0.0f : kload<float>(kg + offsetof(RowColEpilogue, out_scale))};
+  const KArg kgo1 = ka + offsetof(QuantGemvArgs, g) + sizeof(GemvGroup);  // PAIR: matrix 1's output, the product
+  void* const Y1 = PAIR ? kload<void*>(kgo1 + offsetof(GemvGroup, Y)) : nullptr;
+  const int64_t ldy1 = PAIR ? kload<int64_t>(kgo1 + offsetof(GemvGroup, ldy)) : 0;
+  const RowColEpilogue epi1{nullptr, scol1, per_tensor1, bias1,
+                            PAIR && !SIMPLE ? kload<int>(kg1 + offsetof(RowColEpilogue, act)) : 0, 0, 0.0f};
+  float* const prod = PAIR ? kload<float*>(ka + offsetof(QuantGemvArgs, prod)) : nullptr;
+  const int64_t ldprod = PAIR ? kload<int64_t>(ka + offsetof(QuantGemvArgs, ldprod)) : 0;
   float sc, bi, sc1 = 0.0f, bi1 = 0.0f;
-  // NORM: the prologue's operands (the residual rows, gamma, beta), loaded once their addresses
-  // are in, and its outputs
-  float4 rb[XV], gb[XV], bb[XV];
+  auto load_epilogue_operands = [&] {
+    sc = scol[per_tensor || !epi_lane ? 0 : ne];
+    bi = *(bias ? bias + (epi_lane ? ne : 0) : scol);
+    if constexpr (PAIR) {
+      sc1 = scol1[per_tensor1 || !epi_lane ? 0 : ne];
+      bi1 = *(bias1 ? bias1 + (epi_lane ? ne : 0) : scol1);
+    }
+  };
+  // NORM: the prologue's other fields and beta
   const float* pB = nullptr;
   const float* pbeta = nullptr;
   float* psum = nullptr;
@@ -481,8 +520,6 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   if constexpr (NORM) {
     const KArg kp = ka + offsetof(QuantGemvArgs, pro);
     pB = kload<const float*>(kp + offsetof(NormPrologue, B));
-    const int64_t ldb = kload<int64_t>(kp + offsetof(NormPrologue, ldb));
-    const float* const gamma = kload<const float*>(kp + offsetof(NormPrologue, gamma));
     pbeta = kload<const float*>(kp + offsetof(NormPrologue, beta));
     pfn = kload<int>(kp + offsetof(NormPrologue, fn));
     peps = kload<float>(kp + offsetof(NormPrologue, eps));
@@ -490,17 +527,11 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
     ldsum = kload<int64_t>(kp + offsetof(NormPrologue, ldsum));
     py = kload<float*>(kp + offsetof(NormPrologue, y));
     ldpy = kload<int64_t>(kp + offsetof(NormPrologue, ldy));
-    const float4* brow = reinterpret_cast<const float4*>(pB ? reinterpret_cast<const char*>(pB) + m * ldb
-                                                            : reinterpret_cast<const char*>(x) + m * lda);
-    const float4* g4 = reinterpret_cast<const float4*>(gamma);
-    const float4* b4 = reinterpret_cast<const float4*>(pbeta ? pbeta : gamma);
+    const float4* b4 = reinterpret_cast<const float4*>(pbeta ? pbeta : pgamma);
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       const int i = threadIdx.x + j * kThreads;
-      const int ii = i < K4 ? i : 0;
-      rb[j] = brow[ii];
-      gb[j] = g4[ii];
-      bb[j] = b4[ii];
+      bb[j] = b4[i < K4 ? i : 0];
     }
   }
 
@@ -512,12 +543,16 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
     for (int j = 0; j < XV; ++j) {
       const int i = threadIdx.x + j * kThreads;
       const float4 v = xr[j];
-      xr[j] = pB ? make_float4(ftz(fadd(act_fn(v.x, 0), rb[j].x)), ftz(fadd(act_fn(v.y, 0), rb[j].y)),
-                               ftz(fadd(act_fn(v.z, 0), rb[j].z)), ftz(fadd(act_fn(v.w, 0), rb[j].w)))
+      // the ELT's sum (the contract's fadd of flushed operands), canonicalized only where it is
+      // stored: the norm canonicalizes its own results
+      auto add = [](float a, float c) { return ftz(__fadd_rn(ftz(a), ftz(c))); };
+      xr[j] = pB ? make_float4(add(v.x, rb[j].x), add(v.y, rb[j].y), add(v.z, rb[j].z), add(v.w, rb[j].w))
                  : make_float4(ftz(v.x), ftz(v.y), ftz(v.z), ftz(v.w));
-      if (pB && psum && store_pro && i < K4) reinterpret_cast<float4*>(reinterpret_cast<char*>(psum) + m * ldsum)[i] = xr[j];
+      if (pB && psum && store_pro && i < K4)
+        reinterpret_cast<float4*>(reinterpret_cast<char*>(psum) + m * ldsum)[i] =
+            make_float4(canon(xr[j].x), canon(xr[j].y), canon(xr[j].z), canon(xr[j].w));
     }
-    norm_row_f4<XV>(pfn, K, peps, xr, gb, bb, pbeta != nullptr, nrm, &nrm_bcast);
+    norm_row_f4<XV>(pfn, K, peps, xr, gb, bb, pbeta != nullptr, nrm);
     if (py && store_pro) {
 #pragma unroll
       for (int j = 0; j < XV; ++j) {
@@ -544,12 +579,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   if (lane == 0) wave_max[wave] = mx;
   // the epilogue operands, once the activations are in (their addresses wait for the
   // kernel-argument load, which is then long done)
-  sc = scol[per_tensor || !epi_lane ? 0 : ne];
-  bi = *(bias ? bias + (epi_lane ? ne : 0) : scol);
-  if constexpr (PAIR) {
-    sc1 = scol1[per_tensor1 || !epi_lane ? 0 : ne];
-    bi1 = *(bias1 ? bias1 + (epi_lane ? ne : 0) : scol1);
-  }
+  load_epilogue_operands();
   __syncthreads();
   // the row maximum is uniform: one scalar value, and a branch (not a select) between the q8 forms
   mx = flush_max_bits(__builtin_amdgcn_readfirstlane(max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]))));
@@ -586,7 +616,7 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
       if (store_q) qg[i] = b;
     }
   }
-  if (store_q && threadIdx.x == 0) a.s[m] = sr;
+  if (store_q && threadIdx.x == 0) sout[m] = sr;
   __syncthreads();
 
   // exact int32 dot products
@@ -639,21 +669,46 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* 
   if (epi_lane) {
     if constexpr (PAIR) {
       // both outputs fp32: the stored values are ftz(y0), ftz(y1), which fmul flushes the same way
-      const GemvGroup& g1 = a.g[1];
-      const float y0 = SIMPLE ? simple_epilogue(mine, sr, sc) : gr.epi.apply(mine, sr, true, sc, bi);
-      const float y1 = SIMPLE ? simple_epilogue(mine1, sr, sc1) : g1.epi.apply(mine1, sr, true, sc1, bi1);
-      float* const y0row = reinterpret_cast<float*>(static_cast<char*>(gr.Y) + m * gr.ldy);
-      float* const prow = reinterpret_cast<float*>(reinterpret_cast<char*>(a.prod) + m * a.ldprod);
-      reinterpret_cast<float*>(static_cast<char*>(g1.Y) + m * g1.ldy)[ne] = ftz(y1);
+      const float y0 = SIMPLE ? simple_epilogue(mine, sr, sc) : epi.apply(mine, sr, true, sc, bi);
+      const float y1 = SIMPLE ? simple_epilogue(mine1, sr, sc1) : epi1.apply(mine1, sr, true, sc1, bi1);
+      float* const y0row = reinterpret_cast<float*>(static_cast<char*>(Yz) + m * ldyz);
+      float* const prow = reinterpret_cast<float*>(reinterpret_cast<char*>(prod) + m * ldprod);
+      reinterpret_cast<float*>(static_cast<char*>(Y1) + m * ldy1)[ne] = ftz(y1);
       if (prow != y0row) y0row[ne] = ftz(y0);
       prow[ne] = fmul(y0, y1);
     } else if constexpr (SIMPLE) {
-      reinterpret_cast<float*>(static_cast<char*>(gr.Y) + m * gr.ldy)[ne] = simple_epilogue(mine, sr, sc);
+      reinterpret_cast<float*>(static_cast<char*>(Yz) + m * ldyz)[ne] = simple_epilogue(mine, sr, sc);
     } else {
-      const float y = gr.epi.apply(mine, sr, true, sc, bi);
-      store_out(gr.Y, m * gr.ldy, ne, gr.epi.out, y, gr.epi.out_scale);
+      const float y = epi.apply(mine, sr, true, sc, bi);
+      store_out(Yz, m * ldyz, ne, epi.out, y, epi.out_scale);
     }
   }
+}
+
+template <int L, int CPL, int U, bool SIMPLE, bool PAIR>
+__global__ __launch_bounds__(kThreads) void quant_gemv_w8a8_kernel(const float* x, int64_t lda, const int8_t* W0,
+                                                                   const int8_t* W1, const int8_t* W2,
+                                                                   const int8_t* W3, int K, int N, QuantGemvArgs a) {
+  quant_gemv_body<L, CPL, U, SIMPLE, PAIR, false>(x, lda, W0, W1, W2, W3, K, N, a, nullptr, nullptr);
+}
+
+// With the norm prologue (a.pro; one activation row): the residual row B (x itself when the norm
+// reads x alone) and gamma lead the preloaded arguments in place of lda and matrix 3's pointer.
+struct QuantGemvNormKernargs {
+  const float* x;
+  const float* B;
+  const float* gamma;
+  const int8_t* W[3];
+  int K, N;
+  QuantGemvArgs a;
+};
+static_assert(offsetof(QuantGemvNormKernargs, a) == kQuantGemvArgsOffset, "both kernels' argument blocks at 56");
+
+template <int L, int CPL, int U, bool SIMPLE, bool PAIR>
+__global__ __launch_bounds__(kThreads) void quant_gemv_norm_kernel(const float* x, const float* B, const float* gamma,
+                                                                   const int8_t* W0, const int8_t* W1, const int8_t* W2,
+                                                                   int K, int N, QuantGemvArgs a) {
+  quant_gemv_body<L, CPL, U, SIMPLE, PAIR, true>(x, 0, W0, W1, W2, nullptr, K, N, a, B, gamma);
 }
 
 // Rows per wave (measured on MI355X with the kernels above, weights cold). A launch wants at least
@@ -733,11 +788,14 @@ template <int L, int CPL, int U, bool SIMPLE, bool PAIR>
 hipError_t launch_qg(dim3 grid, size_t lds, hipStream_t s, const int8_t* const* Wz, int N, const QuantGemvArgs& b) {
   constexpr bool kNorm = L == 64 && CPL >= 1 && CPL <= 2;
   if (b.pro.fn) {
-    if constexpr (!kNorm) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR, kNorm>), grid, dim3(kThreads), lds, s, b.x, b.lda,
-                       Wz[0], Wz[1], Wz[2], Wz[3], b.K, N, b);
+    if constexpr (!kNorm) {
+      return hipErrorInvalidValue;
+    } else {
+      hipLaunchKernelGGL((quant_gemv_norm_kernel<L, CPL, U, SIMPLE, PAIR>), grid, dim3(kThreads), lds, s, b.x,
+                         b.pro.B ? b.pro.B : b.x, b.pro.gamma, Wz[0], Wz[1], Wz[2], b.K, N, b);
+    }
   } else {
-    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR, false>), grid, dim3(kThreads), lds, s, b.x, b.lda,
+    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR>), grid, dim3(kThreads), lds, s, b.x, b.lda,
                        Wz[0], Wz[1], Wz[2], Wz[3], b.K, N, b);
   }
   return hipGetLastError();

@@ -165,10 +165,10 @@ struct GemvGroup {
 };
 
 // Optional residual add and norm in front of the fused quantizer (the executor's fusion of ELT ADD
-// -> LayerNorm / RMSNorm / L2Norm -> ROW_QUANT -> GEMMs; quant_gemv_norm_supported(K)): the
-// kernel's x rows are the ELT's A rows (the norm's input rows when B is null). Every workgroup
-// forms ftz(A + B) and its norm in registers and quantizes the norm's fp32 output values; the
-// first workgroup also stores the sum (at sum) and the norm's output (at y).
+// -> LayerNorm / RMSNorm / L2Norm -> ROW_QUANT -> GEMMs; quant_gemv_norm_supported(K); one row, so
+// the strides are unused): the kernel's x row is the ELT's A row (the norm's input row when B is
+// null). Every workgroup forms ftz(A + B) and its norm in registers and quantizes the norm's fp32
+// output values; the first workgroup also stores the sum (at sum) and the norm's output (at y).
 struct NormPrologue {
   int fn;               // a RowFn norm (ROWFN_LAYERNORM / RMSNORM / L2NORM); 0: no prologue
   const float* B;       // rows added to x (nullptr: the norm reads x itself)

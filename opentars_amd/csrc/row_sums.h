@@ -86,42 +86,91 @@ __device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) 
   return *bcast;
 }
 
+// The sum16 of v[0..n) in LDS run by every wave on its own: all four 16-lane rows of the wave run
+// the same chains (lane l the elements l, l + 16, ... of v, the reads broadcast), so after the fold
+// every lane holds the sum and no barrier or broadcast through LDS follows. The caller orders v's
+// writes before the call. NONNEG as for lds_sum16_rows.
+template <bool NONNEG>
+__device__ __forceinline__ float wave_sum16(const float* v, int n) {
+  const int l = threadIdx.x & 15;
+  auto chain = [&](auto flushed) {
+    float acc = 0.0f;
+    uint32_t mk = ~0u;
+    auto step = [&](float t) {
+      if constexpr (decltype(flushed)::value) {
+        acc = fadd_chain(acc, t);
+      } else {
+        acc = __fadd_rn(acc, t);
+        if constexpr (!NONNEG) mk = min(mk, sub_key(acc));
+      }
+    };
+    auto block = [&](int j0, auto size) {
+      constexpr int B = decltype(size)::value;
+      float t[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) t[u] = v[j0 + l + 16 * u];
+#pragma unroll
+      for (int u = 0; u < B; ++u) step(t[u]);
+    };
+    int j0 = 0;
+    for (; j0 + 16 * 32 <= n; j0 += 16 * 32) block(j0, std::integral_constant<int, 32>{});
+    for (; j0 + 16 * 8 <= n; j0 += 16 * 8) block(j0, std::integral_constant<int, 8>{});
+    for (int j = j0 + l; j < n; j += 16) step(v[j]);
+    return mk < kSubKeyNormal ? ffrom(kCanonNaN) : acc;  // NaN marks "recompute" (a NaN sum recomputes too)
+  };
+  float acc = chain(std::false_type{});
+  if constexpr (!NONNEG)
+    if (__builtin_expect(is_nan(acc), 0)) acc = chain(std::true_type{});
+  return fold16(acc);
+}
+
 // The norm (LayerNorm / RMSNorm / L2Norm, golden.py:358-380) of one row of N values held as
 // float4s by the 256 threads of a workgroup: thread t holds elements 4 (t + 256 j) .. 4 (t + 256 j)
-// + 3 in x[j] (float4 index t + 256 j < N / 4; others ignored), already flushed; g and b hold gamma
-// and beta there. v: LDS for N floats, bcast: one LDS float. On return x holds the norm's output
-// values as an fp32 output stores them: the values and sums of the row kernels' norm, in the same
-// order.
+// + 3 in x[j] (float4 index t + 256 j < N / 4; others ignored), flushed (NaN payloads are free: every
+// NaN result is canonicalized); g and b hold gamma and beta there. v: LDS for 2 N floats. On return
+// x holds the norm's output values as an fp32 output stores them: the values and sums of the row
+// kernels' norm, in the same order. Every wave runs the sums itself (wave_sum16), so the norm takes
+// one workgroup barrier (two for LayerNorm, whose squared differences go to v + N).
+//
+// The contract's operations are written out where their wrappers are identities: a square of a
+// flushed value is the raw product flushed (its NaN payload only feeds a sum that is canonicalized
+// at its end), and the output chain fmul(fmul(x, rs), g) (+ beta) takes its inputs flushed once and
+// canonicalizes once at the end (an intermediate NaN stays NaN to the end).
 template <int XV>
 __device__ __forceinline__ void norm_row_f4(int fn, int N, float eps, float4 (&x)[XV], const float4 (&g)[XV],
-                                            const float4 (&b)[XV], bool beta, float* v, float* bcast) {
+                                            const float4 (&b)[XV], bool beta, float* v) {
   const int t = threadIdx.x, N4 = N >> 2;
   float4* v4 = reinterpret_cast<float4*>(v);
   const float kinv = recip_f(i2f(N));
-  auto square = [](float4 a) { return make_float4(fmul(a.x, a.x), fmul(a.y, a.y), fmul(a.z, a.z), fmul(a.w, a.w)); };
+  auto sq = [](float a) { return ftz(__fmul_rn(a, a)); };
+  auto square = [&](float4 a) { return make_float4(sq(a.x), sq(a.y), sq(a.z), sq(a.w)); };
   float rs;
   if (fn == ROWFN_LAYERNORM) {
 #pragma unroll
     for (int j = 0; j < XV; ++j)
       if (t + 256 * j < N4) v4[t + 256 * j] = x[j];
-    const float nmean = fneg(fmul(lds_sum16<false>(v, N, bcast), kinv));
+    __syncthreads();
+    const float nmean = fneg(fmul(wave_sum16<false>(v, N), kinv));
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       x[j] = make_float4(fadd(x[j].x, nmean), fadd(x[j].y, nmean), fadd(x[j].z, nmean), fadd(x[j].w, nmean));
-      if (t + 256 * j < N4) v4[t + 256 * j] = square(x[j]);
+      if (t + 256 * j < N4) v4[N4 + t + 256 * j] = square(x[j]);
     }
-    rs = rsqrt_f(fadd(fmul(lds_sum16<false, true>(v, N, bcast), kinv), eps));
+    __syncthreads();
+    rs = rsqrt_f(fadd(fmul(wave_sum16<true>(v + N, N), kinv), eps));
   } else {
 #pragma unroll
     for (int j = 0; j < XV; ++j)
       if (t + 256 * j < N4) v4[t + 256 * j] = square(x[j]);
-    const float ss = lds_sum16<false, true>(v, N, bcast);
+    __syncthreads();
+    const float ss = wave_sum16<true>(v, N);
     rs = rsqrt_f(fadd(fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, eps));
   }
+  // rs is canonical and never subnormal (rsqrt_f's results are 0, normal, infinite or the NaN)
   auto out = [&](float xe, float ge, float be) {
-    float y = fmul(fmul(xe, rs), ge);
-    if (beta) y = fadd(y, be);
-    return ftz(y);
+    float y = ftz(__fmul_rn(ftz(__fmul_rn(xe, rs)), ftz(ge)));
+    if (beta) y = ftz(__fadd_rn(y, ftz(be)));
+    return canon(y);
   };
 #pragma unroll
   for (int j = 0; j < XV; ++j)

@@ -33,6 +33,31 @@ def test_recip_newton_steps_stay_normal_and_match_the_wrapped_steps():
     assert (y_raw.view(np.uint32) == y_ref.view(np.uint32)).all()
 
 
+def test_rsqrt_newton_steps_stay_normal_and_match_the_wrapped_steps():
+    """rsqrt_f's Newton loop depends only on m in [1, 4) (exponent field 127 or 128): for all 2^24
+    of them, the raw operations never produce a subnormal, infinity or NaN and give the wrapped
+    loop's bits."""
+    from oracle import rowops as R
+    mbits = np.concatenate([np.arange(1 << 23, dtype=np.uint32) | np.uint32(e << 23) for e in (127, 128)])
+    m = mbits.view(f32)
+    y_raw = (np.uint32(R.RSQRT_SEED) - (mbits >> np.uint32(1))).view(f32)
+    y_ref = y_raw.copy()
+    tiny, half = f32(2.0 ** -126), f32(0.5)
+    for _ in range(3):
+        p = m * y_raw
+        t = p * y_raw
+        h = half * t
+        d = half - h
+        u = y_raw * d
+        for v in (p, t, h, d, u):
+            assert np.isfinite(v).all()
+            assert ((v == 0) | (np.abs(v) >= tiny)).all()
+        y_raw = y_raw + u
+        assert (y_raw > f32(0.4)).all() and (y_raw < f32(1.1)).all()
+        y_ref = F.fadd(y_ref, F.fmul(y_ref, F.fadd(half, F.neg(F.fmul(half, F.fmul(F.fmul(m, y_ref), y_ref))))))
+    assert (y_raw.view(np.uint32) == y_ref.view(np.uint32)).all()
+
+
 def test_q8_with_flushed_multiplier():
     """q8(x, inv) == clamp(rint(nan->0(ftz(x) * inv))) whenever inv is an fmul output (flushed,
     canonical): random bit patterns for x, and multipliers covering 0, inf, NaN and the range."""
