@@ -399,7 +399,7 @@ __device__ __forceinline__ void quant_gemv_body(const float* x, int64_t lda, con
   static_assert(!PAIR || (L == 64 && CPL > 0 && U % 2 == 0), "row pairs on whole-wave rows");
   // NORM: a.pro's residual add and norm form the quantizer's input row (whole-wave rows, K <= 2048)
   static_assert(!NORM || (L == 64 && CPL >= 1 && CPL <= 2), "norm prologue on rows of at most 2048");
-  __shared__ __align__(16) float nrm[NORM ? 4096 : 4];
+  __shared__ __align__(16) float nrm[NORM ? 2 * (2048 + 64) : 4];
   constexpr int kSlots = 64 / L;
   constexpr int UR = PAIR ? U / 2 : U;          // row indices per wave
   constexpr int kRows = kWaves * kSlots * UR;  // row indices per workgroup
@@ -924,8 +924,8 @@ bool quant_gemv_pairs_supported(int K) {
 }
 
 bool quant_gemv_norm_supported(int K) {
-  const int C = K / 16;  // whole-wave rows (more than 32 chunks), at most two chunks per lane
-  return K % 16 == 0 && C > 32 && C <= 128;
+  const int C = K / 16;  // whole-wave rows (more than 32 chunks), at most two chunks per lane, whole float4s
+  return K % 64 == 0 && C > 32 && C <= 128;  // of each chain lane's terms
 }
 
 // K split up to a total K of 8192: four waves per row (measured on MI355X at C2, K = 6912 in two

@@ -86,13 +86,15 @@ __device__ __forceinline__ float lds_sum16(const float* v, int n, float* bcast) 
   return *bcast;
 }
 
-// The sum16 of v[0..n) in LDS run by every wave on its own: all four 16-lane rows of the wave run
-// the same chains (lane l the elements l, l + 16, ... of v, the reads broadcast), so after the fold
-// every lane holds the sum and no barrier or broadcast through LDS follows. The caller orders v's
-// writes before the call. NONNEG as for lds_sum16_rows.
+// The sum16 of a row of n values (n % 64 == 0) held in LDS transposed for the chains: element e at
+// v[(e % 16) * S + e / 16] (S = n / 16 + 4: chain lane l's terms are contiguous, read 16 bytes at a
+// time). Run by every wave on its own: all four 16-lane rows of the wave run the same chains (the
+// reads broadcast), so after the fold every lane holds the sum and no barrier or broadcast through
+// LDS follows. The caller orders v's writes before the call. NONNEG as for lds_sum16_rows.
 template <bool NONNEG>
-__device__ __forceinline__ float wave_sum16(const float* v, int n) {
-  const int l = threadIdx.x & 15;
+__device__ __forceinline__ float wave_sum16_t(const float* v, int n, int S) {
+  const float4* row = reinterpret_cast<const float4*>(v + (threadIdx.x & 15) * S);
+  const int n4 = n >> 6;  // float4s of each lane's terms
   auto chain = [&](auto flushed) {
     float acc = 0.0f;
     uint32_t mk = ~0u;
@@ -104,18 +106,26 @@ __device__ __forceinline__ float wave_sum16(const float* v, int n) {
         if constexpr (!NONNEG) mk = min(mk, sub_key(acc));
       }
     };
-    auto block = [&](int j0, auto size) {
-      constexpr int B = decltype(size)::value;
-      float t[B];
+    int k = 0;
+    for (; k + 8 <= n4; k += 8) {
+      float4 t[8];
 #pragma unroll
-      for (int u = 0; u < B; ++u) t[u] = v[j0 + l + 16 * u];
+      for (int u = 0; u < 8; ++u) t[u] = row[k + u];
 #pragma unroll
-      for (int u = 0; u < B; ++u) step(t[u]);
-    };
-    int j0 = 0;
-    for (; j0 + 16 * 32 <= n; j0 += 16 * 32) block(j0, std::integral_constant<int, 32>{});
-    for (; j0 + 16 * 8 <= n; j0 += 16 * 8) block(j0, std::integral_constant<int, 8>{});
-    for (int j = j0 + l; j < n; j += 16) step(v[j]);
+      for (int u = 0; u < 8; ++u) {
+        step(t[u].x);
+        step(t[u].y);
+        step(t[u].z);
+        step(t[u].w);
+      }
+    }
+    for (; k < n4; ++k) {
+      const float4 t = row[k];
+      step(t.x);
+      step(t.y);
+      step(t.z);
+      step(t.w);
+    }
     return mk < kSubKeyNormal ? ffrom(kCanonNaN) : acc;  // NaN marks "recompute" (a NaN sum recomputes too)
   };
   float acc = chain(std::false_type{});
@@ -124,13 +134,14 @@ __device__ __forceinline__ float wave_sum16(const float* v, int n) {
   return fold16(acc);
 }
 
-// The norm (LayerNorm / RMSNorm / L2Norm, golden.py:358-380) of one row of N values held as
-// float4s by the 256 threads of a workgroup: thread t holds elements 4 (t + 256 j) .. 4 (t + 256 j)
-// + 3 in x[j] (float4 index t + 256 j < N / 4; others ignored), flushed (NaN payloads are free: every
-// NaN result is canonicalized); g and b hold gamma and beta there. v: LDS for 2 N floats. On return
-// x holds the norm's output values as an fp32 output stores them: the values and sums of the row
-// kernels' norm, in the same order. Every wave runs the sums itself (wave_sum16), so the norm takes
-// one workgroup barrier (two for LayerNorm, whose squared differences go to v + N).
+// The norm (LayerNorm / RMSNorm / L2Norm, golden.py:358-380) of one row of N values (N % 64 == 0)
+// held as float4s by the 256 threads of a workgroup: thread t holds elements 4 (t + 256 j) ..
+// 4 (t + 256 j) + 3 in x[j] (float4 index t + 256 j < N / 4; others ignored), flushed (NaN payloads
+// are free: every NaN result is canonicalized); g and b hold gamma and beta there. v: LDS for
+// 2 (N + 64) floats. On return x holds the norm's output values as an fp32 output stores them: the
+// values and sums of the row kernels' norm, in the same order. Every wave runs the sums itself
+// (wave_sum16_t), so the norm takes one workgroup barrier (two for LayerNorm, whose squared
+// differences go to a second buffer).
 //
 // The contract's operations are written out where their wrappers are identities: a square of a
 // flushed value is the raw product flushed (its NaN payload only feeds a sum that is canonicalized
@@ -139,31 +150,38 @@ __device__ __forceinline__ float wave_sum16(const float* v, int n) {
 template <int XV>
 __device__ __forceinline__ void norm_row_f4(int fn, int N, float eps, float4 (&x)[XV], const float4 (&g)[XV],
                                             const float4 (&b)[XV], bool beta, float* v) {
-  const int t = threadIdx.x, N4 = N >> 2;
-  float4* v4 = reinterpret_cast<float4*>(v);
+  const int t = threadIdx.x, N4 = N >> 2, S = (N >> 4) + 4;
   const float kinv = recip_f(i2f(N));
   auto sq = [](float a) { return ftz(__fmul_rn(a, a)); };
-  auto square = [&](float4 a) { return make_float4(sq(a.x), sq(a.y), sq(a.z), sq(a.w)); };
+  // element e of float4 index i (e = 4 i + c) to its transposed place
+  auto put = [&](float* w, int i, float4 a) {
+    const int r = (i & 3) * 4, col = i >> 2;
+    w[r * S + col] = a.x;
+    w[(r + 1) * S + col] = a.y;
+    w[(r + 2) * S + col] = a.z;
+    w[(r + 3) * S + col] = a.w;
+  };
   float rs;
   if (fn == ROWFN_LAYERNORM) {
 #pragma unroll
     for (int j = 0; j < XV; ++j)
-      if (t + 256 * j < N4) v4[t + 256 * j] = x[j];
+      if (t + 256 * j < N4) put(v, t + 256 * j, x[j]);
     __syncthreads();
-    const float nmean = fneg(fmul(wave_sum16<false>(v, N), kinv));
+    const float nmean = fneg(fmul(wave_sum16_t<false>(v, N, S), kinv));
+    float* v2 = v + 16 * S;
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       x[j] = make_float4(fadd(x[j].x, nmean), fadd(x[j].y, nmean), fadd(x[j].z, nmean), fadd(x[j].w, nmean));
-      if (t + 256 * j < N4) v4[N4 + t + 256 * j] = square(x[j]);
+      if (t + 256 * j < N4) put(v2, t + 256 * j, make_float4(sq(x[j].x), sq(x[j].y), sq(x[j].z), sq(x[j].w)));
     }
     __syncthreads();
-    rs = rsqrt_f(fadd(fmul(wave_sum16<true>(v + N, N), kinv), eps));
+    rs = rsqrt_f(fadd(fmul(wave_sum16_t<true>(v2, N, S), kinv), eps));
   } else {
 #pragma unroll
     for (int j = 0; j < XV; ++j)
-      if (t + 256 * j < N4) v4[t + 256 * j] = square(x[j]);
+      if (t + 256 * j < N4) put(v, t + 256 * j, make_float4(sq(x[j].x), sq(x[j].y), sq(x[j].z), sq(x[j].w)));
     __syncthreads();
-    const float ss = wave_sum16<true>(v, N);
+    const float ss = wave_sum16_t<true>(v, N, S);
     rs = rsqrt_f(fadd(fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, eps));
   }
   // rs is canonical and never subnormal (rsqrt_f's results are 0, normal, infinite or the NaN)
