@@ -373,9 +373,11 @@ int tars_set_queue_fusion(int on);
  * an up GEMM folded into their quantizer + GEMMs launch, which counts[0] also counts), counts[5]
  * launches that ran two adjacent independent (norm, RoPE) pairs, such as a decoder layer's q and
  * k (counts[3] counts both pairs), counts[6] quantizer + GEMMs launches that also ran the norm in
- * front of the quantizer and the residual ELT ADD before it (which counts[0] also counts). A
- * replayed launch plan counts its fused launches again. The first ncounts (up to 7) are written to
- * counts, which may be NULL; reset != 0 zeroes the counts after reading them. Process-wide. */
+ * front of the quantizer and the residual ELT ADD before it (which counts[0] also counts),
+ * counts[7] attention launches whose scores kernel also ran the layer's q and k norm + RoPE pairs
+ * (counted in counts[1] and, as two pairs, in counts[3]). A replayed launch plan counts its fused
+ * launches again. The first ncounts (up to 8) are written to counts, which may be NULL; reset != 0
+ * zeroes the counts after reading them. Process-wide. */
 int tars_queue_fusion_counts(int64_t* counts, int32_t ncounts, int32_t reset);
 
 /* Launch plans in tars_run_queue (benchmark and test control): 1 (default) keeps, for up to 8

@@ -281,6 +281,22 @@ struct FdotArgs {
 // head's scores, probabilities and outputs are the golden's, and the scores and probabilities of
 // the last head are written to sc / pr (the buffers all heads share).
 constexpr int kAttnMaxHeads = 32, kAttnMaxKeys = 4080;  // 4080 keys: the scores row and the V ring fit 64 KiB of LDS
+// A norm (RowFn LayerNorm / RMSNorm / L2Norm, fp32 output) and the full-width RoPE (rot == hd) of
+// its output rows, run inside the split scores kernel (AttnArgs::rope): one row per query head, or
+// per K / V head group.
+struct AttnNormRope {
+  const float* x;        // the norm's input rows (row r: query head r, or K / V head group r)
+  int64_t ldx;
+  const float* gamma;    // [hd]
+  const float* beta;     // [hd] or nullptr
+  float eps;
+  int fn;
+  float* n;              // the norm's output rows
+  int64_t ldn;
+  const float* tab;      // RoPE table rows [cos(0..hd/2-1), sin(0..hd/2-1)]; row r / rows_per_pos
+  int rows_per_pos;
+};
+
 struct AttnArgs {
   const float* q[kAttnMaxHeads];   // head h: query rows [M, hd] at ldq
   const float* k[kAttnMaxHeads];   // K rows [nk, hd] at ldk (fp32)
@@ -302,6 +318,16 @@ struct AttnArgs {
   // K / V head group, keys per scores workgroup
   int64_t ld_scratch;
   int group, keys_per_wg;
+  // rope > 0 (query heads per K / V head; one query row per head, the split form, hd a multiple
+  // of 32, rq.fn == rk.fn): the scores kernel first runs the q and k norm + RoPE (the executor's fusion of a
+  // decoder's q and k norm and rotation with its attention). Head h's query row q[h] is the RoPE of
+  // the norm of row h of rq.x; key row rope_key of head h's keys (k[h]) is that of row h / rope of
+  // rk.x, which the workgroups whose keys include it form in registers, use, and store (several
+  // store the same values when a workgroup's group holds fewer heads than a K / V head serves). The
+  // workgroups of the first key chunk store the query rows (norm outputs and q rows), the new key's
+  // workgroups its norm output.
+  int rope, rope_key;  // rope_key: the key row the k RoPE writes
+  AttnNormRope rq, rk;
 };
 bool attention_supported(int hd, int nk);
 // Split form limits: query rows per head group (heads sharing K / V times M) and probabilities a

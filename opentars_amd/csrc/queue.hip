@@ -712,8 +712,38 @@ tars::AttnArgs attention_args(uint8_t* image, const std::vector<AttnHead>& heads
   return a;
 }
 
-int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, hipStream_t s) {
+// The q / k norm + RoPE prologue of an attention launch: the q norm, q RoPE, k norm and k RoPE
+// descriptors, and the query heads per K / V head.
+struct RopePrologue {
+  Desc qn, qr, kn, kr;
+  int qpk = 0, key = 0;  // query heads per K / V head; the key row the k RoPE writes
+};
+
+tars::AttnNormRope norm_rope_args(uint8_t* image, const Desc& rd, const Desc& pd) {
+  uint8_t* RB = image + rd[F_BASE_ADDR];
+  tars::AttnNormRope p{};
+  p.x = reinterpret_cast<const float*>(RB + rd[F_A_OFF]);
+  p.ldx = static_cast<int64_t>(strides(rd).lda);
+  p.gamma = reinterpret_cast<const float*>(RB + rd[F_SCALE_OFF]);
+  p.beta = has_bias(rd[F_EPI]) ? reinterpret_cast<const float*>(RB + rd[F_BIAS_OFF]) : nullptr;
+  p.eps = f32_bits(rd[F_W_OFF]);
+  p.fn = static_cast<int>(rd[F_CTRL] & 7);
+  p.n = reinterpret_cast<float*>(RB + rd[F_Y_OFF]);
+  p.ldn = static_cast<int64_t>(strides(rd).ldy);
+  p.tab = reinterpret_cast<const float*>(image + pd[F_BASE_ADDR] + pd[F_W_OFF]);
+  p.rows_per_pos = static_cast<int>(pd[F_GROUP_SIZE]);
+  return p;
+}
+
+int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, hipStream_t s,
+                           const RopePrologue* pro = nullptr) {
   tars::AttnArgs a = attention_args(image, heads);
+  if (pro) {
+    a.rope = pro->qpk;
+    a.rope_key = pro->key;
+    a.rq = norm_rope_args(image, pro->qn, pro->qr);
+    a.rk = norm_rope_args(image, pro->kn, pro->kr);
+  }
   a.scratch = tars::attention_workspace(s);  // the split form's scores, when the device has its scratch
   a.scratch_floats = a.scratch ? tars::kAttnScratchFloats : 0;
   const hipError_t e = tars::launch_attention(a, s);
@@ -742,14 +772,17 @@ bool attention_triple(const Checked& nt, const Checked& sm, const Checked& nn, u
   return true;
 }
 
-int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
-                   int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
-                   int& fused, std::vector<AttnHead>& group) {
-  fused = 0;
+// The heads of an attention group starting at descriptor i (each a triple the fused kernel runs,
+// all of one shape and sharing the score / probability buffers), with the group's inputs (q, K, V)
+// and outputs (scores, probabilities, attention rows). False when there is no such group or its
+// outputs meet each other or its inputs.
+bool collect_attention(const Checked& first, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image, int32_t n,
+                       uint64_t image_len, int core_id, bool gemv_only, uintptr_t img, std::vector<AttnHead>& group,
+                       Segs& ins, Segs& outs) {
   group.clear();
-  if (!g_fusion || first.d[F_OPCODE] != OP_FDOT || (first.d[F_CTRL] & 1)) return TARS_OK;
-  const uintptr_t img = reinterpret_cast<uintptr_t>(image);
-  Segs ins, atts, sc_y, pr_y;
+  ins.clear();
+  if (!g_fusion || first.d[F_OPCODE] != OP_FDOT || (first.d[F_CTRL] & 1)) return false;
+  Segs atts, sc_y, pr_y;
   for (int32_t j = i; j + 2 < n && static_cast<uint64_t>(j + 2) < in_image &&
                       group.size() < static_cast<size_t>(tars::kAttnMaxHeads);
        j += 3) {
@@ -777,11 +810,26 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
     atts.insert(atts.end(), nn.y.begin(), nn.y.end());
     group.push_back(AttnHead{nt.d, sm.d, nn.d});
   }
-  if (group.empty()) return TARS_OK;
-  Segs outs = sc_y;
+  if (group.empty()) return false;
+  outs = sc_y;
   outs.insert(outs.end(), pr_y.begin(), pr_y.end());
   outs.insert(outs.end(), atts.begin(), atts.end());
-  if (!pairwise_disjoint(outs) || overlaps(ins, outs) || (rest_lo < rest_hi && overlaps(Segs{interval(rest_lo, rest_hi)}, outs))) {
+  if (!pairwise_disjoint(outs) || overlaps(ins, outs)) {
+    group.clear();
+    return false;
+  }
+  return true;
+}
+
+int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
+                   int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
+                   int& fused, std::vector<AttnHead>& group) {
+  fused = 0;
+  Segs ins, outs;
+  if (!collect_attention(first, q, i, in_image, n, image_len, core_id, gemv_only, reinterpret_cast<uintptr_t>(image),
+                         group, ins, outs))
+    return TARS_OK;
+  if (rest_lo < rest_hi && overlaps(Segs{interval(rest_lo, rest_hi)}, outs)) {
     group.clear();
     return TARS_OK;
   }
@@ -998,10 +1046,64 @@ bool norm_rope_pair(const Checked& r, const Checked& p, uintptr_t img, Segs& ins
 // pair that neither reads nor writes what the first pair writes, and whose reads the first pair
 // does not write (a decoder's q and then k norm and rotation), both pairs run in the same launch.
 // `fused` = descriptors folded into descriptor i's launch (1 or 3).
+// A decoder's q and k (norm, RoPE) pairs and the attention group right after them, as one attention
+// launch whose scores kernel runs the pairs first (AttnArgs::rope). Taken when the attention has one
+// query row per head, both norms are of one kind, every RoPE rotates the whole row, the q pair has
+// a row per head whose RoPE
+// rows are exactly the heads' query rows, the k pair a row per K / V head whose RoPE row g is exactly
+// one key row (the same for every head) of that head's keys (the heads of a K / V head
+// consecutive), the attention's split form runs, and no write of the launch lands where it could
+// change what another part reads: the pairs' outputs apart from the pairs' inputs and from every K
+// and V row (the new key row aside), the attention's outputs apart from the pairs' inputs and
+// outputs, nothing on a later descriptor.
+bool rope_attention(uint8_t* image, const Checked& r, const Checked& p, const Checked& r1, const Checked& p1,
+                    const Segs& pins, const Segs& pouts, const std::vector<AttnHead>& heads, const Segs& ains,
+                    const Segs& aouts, const Segs& rest, hipStream_t s, RopePrologue& pro) {
+  (void)ains;
+  const size_t H = heads.size();
+  const Desc& nt0 = heads[0].nt;
+  const uint64_t hd = nt0[F_K], nk = nt0[F_N], ldk = b_stride(nt0).first;
+  const uint64_t Hk = r1.d[F_M];
+  if (nt0[F_M] != 1 || hd % 32 || r.d[F_N] != hd || r.d[F_M] != H || p.d[F_K] != hd || r1.d[F_N] != hd ||
+      p1.d[F_K] != hd || Hk == 0 || H % Hk || ldk < 4 * hd || (r.d[F_CTRL] & 7) != (r1.d[F_CTRL] & 7))
+    return false;
+  const uint64_t qpk = H / Hk;
+  // the key row the k RoPE writes: its row 0 lands on a key row of head 0's keys
+  const u128 k0 = addr(nt0, F_W_OFF), r0 = addr(p1.d, F_Y_OFF);
+  if (r0 < k0 || (r0 - k0) % ldk || (r0 - k0) / ldk >= nk) return false;
+  const uint64_t key = static_cast<uint64_t>((r0 - k0) / ldk);
+  Segs kv;  // every K row but the new ones, and every V row
+  for (size_t h = 0; h < H; ++h) {
+    const Desc& nt = heads[h].nt;
+    const Desc& nn = heads[h].nn;
+    if (addr(nt, F_A_OFF) != addr(p.d, F_Y_OFF) + static_cast<u128>(h) * strides(p.d).ldy ||
+        addr(nt, F_W_OFF) + static_cast<u128>(key) * ldk != addr(p1.d, F_Y_OFF) + static_cast<u128>(h / qpk) * strides(p1.d).ldy ||
+        (h % qpk && addr(nt, F_W_OFF) != addr(heads[h - 1].nt, F_W_OFF)))
+      return false;
+    if (key > 0) kv.push_back(strided_span(addr(nt, F_W_OFF), ldk, key, 4 * hd));
+    if (key + 1 < nk) kv.push_back(strided_span(addr(nt, F_W_OFF) + static_cast<u128>(key + 1) * ldk, ldk, nk - 1 - key, 4 * hd));
+    kv.push_back(strided_span(addr(nn, F_W_OFF), b_stride(nn).first, nk, b_stride(nn).second));
+  }
+  const float* ws = tars::attention_workspace(s);
+  if (!ws || !tars::attention_split_fits(static_cast<int>(H), 1, static_cast<int>(nk), tars::kAttnScratchFloats))
+    return false;
+  Segs pall = pins;  // the pairs' inputs and outputs
+  pall.insert(pall.end(), pouts.begin(), pouts.end());
+  Segs new_keys = p1.y;
+  Segs others;  // the pairs' outputs but the new key rows
+  for (const Checked* c : {&r, &p, &r1}) others.insert(others.end(), c->y.begin(), c->y.end());
+  if (overlaps(others, kv) || overlaps(new_keys, Segs(kv.begin(), kv.end())) || overlaps(aouts, pall) ||
+      (!rest.empty() && (overlaps(rest, pouts) || overlaps(rest, aouts))))
+    return false;
+  pro = RopePrologue{r.d, p.d, r1.d, p1.d, static_cast<int>(qpk), static_cast<int>(key)};
+  return true;
+}
+
 int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>& q, int32_t i, uint64_t in_image,
                    int32_t n, u128 rest_lo, u128 rest_hi, uint64_t image_len, int core_id, bool gemv_only, hipStream_t s,
-                   int& fused, Desc& rope, Desc& r2, Desc& rope2) {
+                   int& fused, Desc& rope, Desc& r2, Desc& rope2, std::vector<AttnHead>& heads, RopePrologue& pro) {
   fused = 0;
+  heads.clear();
   const Desc& rd = r.d;
   const uint64_t fn = rd[F_CTRL] & 7;
   if (!g_fusion || rd[F_OPCODE] != OP_ROW || (fn != ROW_LAYERNORM && fn != ROW_RMSNORM && fn != ROW_L2NORM) ||
@@ -1015,16 +1117,33 @@ int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>&
   if (!pairwise_disjoint(outs) || overlaps(ins, outs) || (rest_lo < rest_hi && overlaps(rest, outs))) return TARS_OK;
   bool two = false;
   Checked r1, p1;
+  Segs ins1, outs1;
   if (i + 3 < n && static_cast<uint64_t>(i) + 3 < in_image) {
     r1 = check(q.data() + static_cast<size_t>(i + 2) * kDescBytes, image_len, core_id, gemv_only);
     p1 = check(q.data() + static_cast<size_t>(i + 3) * kDescBytes, image_len, core_id, gemv_only);
-    Segs ins1, outs1;
     if (norm_rope_pair(r1, p1, img, ins1, outs1)) {
       Segs all = outs;
       all.insert(all.end(), outs1.begin(), outs1.end());
       two = pairwise_disjoint(all) && !overlaps(ins1, all) && !overlaps(ins, outs1) &&
             !(rest_lo < rest_hi && overlaps(rest, outs1));
     }
+  }
+  if (two && i + 4 < n && static_cast<uint64_t>(i) + 4 < in_image) {  // and the attention after them
+    const Checked first = check(q.data() + static_cast<size_t>(i + 4) * kDescBytes, image_len, core_id, gemv_only);
+    Segs ains, aouts;
+    if (first.err == E_OK && !first.overlap &&
+        collect_attention(first, q, i + 4, in_image, n, image_len, core_id, gemv_only, img, heads, ains, aouts)) {
+      Segs pins = ins, pouts = outs;
+      pins.insert(pins.end(), ins1.begin(), ins1.end());
+      pouts.insert(pouts.end(), outs1.begin(), outs1.end());
+      if (rope_attention(image, r, p, r1, p1, pins, pouts, heads, ains, aouts,
+                         rest_lo < rest_hi ? rest : Segs{}, s, pro)) {
+        const int rc = launch_attention_group(image, heads, s, &pro);
+        if (rc == TARS_OK) fused = 3 + 3 * static_cast<int>(heads.size());
+        return rc;
+      }
+    }
+    heads.clear();
   }
   const int rc = two ? launch_norm_rope_pair(image, rd, p.d, s, &r1.d, &p1.d) : launch_norm_rope_pair(image, rd, p.d, s);
   if (rc == TARS_OK) {
@@ -1059,6 +1178,8 @@ struct Step {
   bool gated = false;
   Desc pro_add{}, pro_norm{};  // with pro: the group's prologue (pro_has_add: the ELT ADD, then the norm)
   bool pro = false, pro_has_add = false;
+  bool rope = false;           // attn: the q and k (norm, RoPE) pairs run in the attention launch
+  RopePrologue rope_pro;
 };
 
 struct Plan {
@@ -1076,9 +1197,10 @@ struct Plan {
 // Fused launches run (diagnostics for tests and benchmarks): quantizer + GEMMs, attention,
 // residual ADD + norm, norm + RoPE pairs (two when two pairs share a launch), launches that ran two
 // such pairs, and (also counted as quantizer + GEMMs) the gated product's ELT MUL folded into its
-// GEMMs and a norm (with its residual ADD) in front of the quantizer; counted when a queue is
-// dispatched and when a plan replays.
-constexpr int kFusionKinds = 7;
+// GEMMs and a norm (with its residual ADD) in front of the quantizer, and (also counted as
+// attention and as two norm + RoPE pairs) attention launches that ran a layer's q and k norm + RoPE
+// pairs; counted when a queue is dispatched and when a plan replays.
+constexpr int kFusionKinds = 8;
 std::atomic<int64_t> g_fused_launches[kFusionKinds];
 
 void count_fused(const std::vector<Step>& steps) {
@@ -1088,6 +1210,10 @@ void count_fused(const std::vector<Step>& steps) {
     if (st.gated) g_fused_launches[4].fetch_add(1, std::memory_order_relaxed);
     if (st.norm_rope2) g_fused_launches[5].fetch_add(1, std::memory_order_relaxed);
     if (st.pro) g_fused_launches[6].fetch_add(1, std::memory_order_relaxed);
+    if (st.rope) {
+      g_fused_launches[3].fetch_add(2, std::memory_order_relaxed);
+      g_fused_launches[7].fetch_add(1, std::memory_order_relaxed);
+    }
   }
 }
 
@@ -1103,7 +1229,7 @@ int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) 
     const int rc = st.add_norm        ? launch_add_norm_pair(image, st.d, st.second, s)
                    : st.norm_rope     ? launch_norm_rope_pair(image, st.d, st.second, s, st.norm_rope2 ? &st.third : nullptr,
                                                           st.norm_rope2 ? &st.fourth : nullptr)
-                   : !st.attn.empty() ? launch_attention_group(image, st.attn, s)
+                   : !st.attn.empty() ? launch_attention_group(image, st.attn, s, st.rope ? &st.rope_pro : nullptr)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
                                       : launch_fused(image, st.d, st.group, s, st.gated ? &st.elt : nullptr,
                                                      st.pro_has_add ? &st.pro_add : nullptr, st.pro ? &st.pro_norm : nullptr);
@@ -1328,10 +1454,25 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       continue;
     }
     Desc rope{}, norm2{}, rope2{};
+    std::vector<AttnHead> rheads;
+    RopePrologue rpro;
     if (int rc = fuse_norm_rope(image, c, q, i, in_image, n, static_cast<u128>(queue_addr) + static_cast<u128>(kDescBytes) *
                                 (static_cast<uint64_t>(i) + 2), q_end, image_len, core_id, gemv_only != 0, s, fused, rope,
-                                norm2, rope2))
+                                norm2, rope2, rheads, rpro))
       return queue_fail(rc, "descriptor " + std::to_string(i) + ": " + tars_last_error());
+    if (fused && !rheads.empty()) {
+      g_fused_launches[1].fetch_add(1, std::memory_order_relaxed);
+      g_fused_launches[3].fetch_add(2, std::memory_order_relaxed);
+      g_fused_launches[7].fetch_add(1, std::memory_order_relaxed);
+      if (cacheable) {
+        Step st2{c.d, {}, std::move(rheads)};
+        st2.rope = true;
+        st2.rope_pro = rpro;
+        steps.push_back(std::move(st2));
+      }
+      i += fused;  // the q and k (norm, RoPE) pairs and the attention ran as one attention launch
+      continue;
+    }
     if (fused) {
       g_fused_launches[3].fetch_add(fused == 3 ? 2 : 1, std::memory_order_relaxed);
       if (fused == 3) g_fused_launches[5].fetch_add(1, std::memory_order_relaxed);

@@ -851,33 +851,173 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 // [c * keys_per_wg, (c + 1) * keys_per_wg): 16-lane group g takes keys g, g + 16, ... of the chunk,
 // KF at a time, each K row loaded once for all Q queries. Scores go to scratch row h * M + m (and,
 // for the last head, to its score rows).
+// The norm and full-width RoPE (AttnNormRope) of row `row` of U * 16 values, held by one 16-lane
+// group in sum16 order (lane l: elements l + 16 u): the row sums are the lane's chain and the
+// fold, as the row kernels' (golden.py:358-380); each rotation partner (element n +- hd / 2) is on
+// the same lane (u +- U / 2). yn: the norm's output values, yr: the RoPE's, as fp32 outputs store
+// them (norm_rope_kernel's values). p may differ between the groups of a wave; fn may not.
+template <int U>
+__device__ __forceinline__ void group_norm_rope(const AttnNormRope& p, int fn, int row, float (&yn)[U], float (&yr)[U]) {
+  static_assert(U % 2 == 0, "rotation partners on the same lane");
+  const int l = threadIdx.x & 15;
+  const float* x = frow(p.x, p.ldx, row);
+  const float* tb = p.tab + static_cast<int64_t>(static_cast<unsigned>(row) / static_cast<unsigned>(p.rows_per_pos)) * (16 * U);
+  float xv[U], gv[U], bv[U], tc[U / 2], ts[U / 2];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    xv[u] = x[l + 16 * u];
+    gv[u] = p.gamma[l + 16 * u];
+    bv[u] = p.beta ? p.beta[l + 16 * u] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < U / 2; ++u) {
+    tc[u] = tb[l + 16 * u];
+    ts[u] = tb[8 * U + l + 16 * u];
+  }
+  const float kinv = recip_f(i2f(16 * U));
+#pragma unroll
+  for (int u = 0; u < U; ++u) xv[u] = ftz(xv[u]);
+  // the lane's chain: unflushed with the check of the row kernels (NONNEG: terms that never make a
+  // subnormal partial sum), then the fold
+  auto lane_sum = [&](const float (&t)[U], auto nonneg) {
+    float acc = 0.0f;
+    uint32_t mk = ~0u;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc = __fadd_rn(acc, t[u]);
+      if constexpr (!decltype(nonneg)::value) mk = min(mk, sub_key(acc));
+    }
+    if constexpr (!decltype(nonneg)::value) {
+      if (__builtin_expect(mk < kSubKeyNormal || is_nan(acc), 0)) {
+        acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = fadd_chain(acc, t[u]);
+      }
+    }
+    return fold16(acc);
+  };
+  // the contract's operations written out where their wrappers are identities (as norm_row_f4): a
+  // square of a flushed value is the raw product flushed (its NaN payload only feeds a sum that is
+  // canonicalized at its end); the output and rotation chains take their inputs flushed once and
+  // canonicalize once at the end (an intermediate NaN stays NaN to the end)
+  float sq[U];
+  float rs;
+  if (fn == ROWFN_LAYERNORM) {
+    const float nmean = fneg(fmul(lane_sum(xv, std::false_type{}), kinv));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xv[u] = fadd(xv[u], nmean);
+      sq[u] = ftz(__fmul_rn(xv[u], xv[u]));
+    }
+    rs = rsqrt_f(fadd(fmul(lane_sum(sq, std::true_type{}), kinv), p.eps));
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) sq[u] = ftz(__fmul_rn(xv[u], xv[u]));
+    const float ss = lane_sum(sq, std::true_type{});
+    rs = rsqrt_f(fadd(fn == ROWFN_RMSNORM ? fmul(ss, kinv) : ss, p.eps));
+  }
+  // rs is canonical and never subnormal (rsqrt_f's results are 0, normal, infinite or the NaN)
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float y = ftz(__fmul_rn(ftz(__fmul_rn(xv[u], rs)), ftz(gv[u])));
+    if (p.beta) y = ftz(__fadd_rn(y, ftz(bv[u])));
+    yn[u] = canon(y);
+  }
+  // RoPE of the stored norm values: fadd(fmul(xn, tc), +-fmul(xp, ts)), flushed, canonicalized once
+#pragma unroll
+  for (int u = 0; u < U / 2; ++u) {
+    const float c = ftz(tc[u]), sn = ftz(ts[u]);
+    const float a0 = ftz(__fmul_rn(yn[u], c)), b0 = ftz(__fmul_rn(yn[u + U / 2], sn));
+    const float a1 = ftz(__fmul_rn(yn[u + U / 2], c)), b1 = ftz(__fmul_rn(yn[u], sn));
+    yr[u] = canon(ftz(__fadd_rn(a0, -b0)));
+    yr[u + U / 2] = canon(ftz(__fadd_rn(a1, b1)));
+  }
+}
+
 template <int HD, int Q>
 __global__ __launch_bounds__(256) void attn_split_scores_kernel(AttnArgs a) {
   constexpr int U = HD / 16, KF = 2;
   const int hg = blockIdx.x, t = threadIdx.x, g = t >> 4, l = t & 15;
   const int G = a.group, M = a.M, nk = a.nk;
-  // every argument the kernel reads, in one scalar round trip (see attn_split_pv_kernel)
+  // every argument the kernel reads, in one scalar round trip (see attn_split_pv_kernel), the
+  // norm + RoPE fields included (read where first used, they measured as a wait of microseconds)
   __asm__ volatile("" : : "s"(a.q[hg * G]), "s"(a.ldq), "s"(a.k[hg * G]), "s"(a.ldk), "s"(a.keys_per_wg),
-                   "s"(a.scratch), "s"(a.ld_scratch), "s"(a.heads), "s"(a.sc), "s"(a.ldsc));
+                   "s"(a.scratch), "s"(a.ld_scratch), "s"(a.heads), "s"(a.sc), "s"(a.ldsc), "s"(a.rope), "s"(a.rope_key));
+  __asm__ volatile("" : : "s"(a.rq.x), "s"(a.rq.ldx), "s"(a.rq.gamma), "s"(a.rq.beta), "s"(a.rq.eps), "s"(a.rq.fn),
+                   "s"(a.rq.n), "s"(a.rq.ldn), "s"(a.rq.tab), "s"(a.rq.rows_per_pos));
+  __asm__ volatile("" : : "s"(a.rk.x), "s"(a.rk.ldx), "s"(a.rk.gamma), "s"(a.rk.beta), "s"(a.rk.eps), "s"(a.rk.fn),
+                   "s"(a.rk.n), "s"(a.rk.ldn), "s"(a.rk.tab), "s"(a.rk.rows_per_pos));
   const int jb = blockIdx.y * a.keys_per_wg, je = min(nk, jb + a.keys_per_wg);
-  float qv[Q][U];
-#pragma unroll
-  for (int i = 0; i < Q; ++i) {
-    const float* qr = frow(a.q[hg * G + i / M], a.ldq, i % M);
-#pragma unroll
-    for (int u = 0; u < U; ++u) qv[i][u] = ftz(qr[l + 16 * u]);
-  }
   const float* kb = a.k[hg * G];
-  for (int j0 = jb + g; j0 < je; j0 += 16 * KF) {
-    float kv[KF][U];
+  // this 16-lane group's first key rows, issued before anything else
+  auto load_keys = [&](float (&kv)[KF][U], int j0) {
 #pragma unroll
     for (int c = 0; c < KF; ++c) {
       const float* kr = frow(kb, a.ldk, min(j0 + 16 * c, nk - 1));  // clamped: computed and dropped
 #pragma unroll
       for (int u = 0; u < U; ++u) kv[c][u] = kr[l + 16 * u];
     }
+  };
+  int j0 = jb + g;
+  float kv[KF][U];
+  load_keys(kv, j0);
+  float qv[Q][U];
+  // rope: the new key row when this workgroup's keys include it (its loads read the cache before
+  // it is written and are replaced by these values)
+  const bool new_key = a.rope && jb <= a.rope_key && a.rope_key < je;
+  float knew[U];
+  if (a.rope) {
+    // one query row per head; 16-lane group r < Q forms query row r of the group (head hg * G + r),
+    // group Q the new key row (the groups of one wave run side by side), and they share the rows
+    // through LDS
+    __shared__ __align__(16) float rows[kAttnSplitMaxQ + 1][HD];
+    const bool qrow = g < Q, krow = g == Q && new_key;
+    if (qrow || krow) {
+      const AttnNormRope p = qrow ? a.rq : a.rk;
+      const int r = qrow ? hg * G + g : hg * G / a.rope;  // the query head, or the K / V head
+      float yn[U], yr[U];
+      group_norm_rope<U>(p, a.rq.fn, r, yn, yr);
+#pragma unroll
+      for (int u = 0; u < U; ++u) rows[g][l + 16 * u] = yr[u];
+      if (krow || blockIdx.y == 0) {  // the norm's output, and the RoPE's (the query row, or the cache row)
+        float* nrow = reinterpret_cast<float*>(reinterpret_cast<char*>(p.n) + r * p.ldn);
+        float* orow = qrow ? const_cast<float*>(a.q[r]) : const_cast<float*>(frow(kb, a.ldk, a.rope_key));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          nrow[l + 16 * u] = yn[u];
+          orow[l + 16 * u] = yr[u];
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < Q; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u) qv[i][u] = rows[i][l + 16 * u];
+    if (new_key) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) knew[u] = rows[Q][l + 16 * u];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const float* qr = frow(a.q[hg * G + i / M], a.ldq, i % M);
+#pragma unroll
+      for (int u = 0; u < U; ++u) qv[i][u] = ftz(qr[l + 16 * u]);
+    }
+  }
+  for (; j0 < je; j0 += 16 * KF) {
+    if (new_key) {
+#pragma unroll
+      for (int c = 0; c < KF; ++c)
+        if (j0 + 16 * c == a.rope_key) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) kv[c][u] = knew[u];
+        }
+    }
     float acc[Q][KF];
     score_chains<U, KF, Q>(qv, kv, acc);
+    if (j0 + 16 * KF < je) load_keys(kv, j0 + 16 * KF);  // the next rows, while these scores are stored
 #pragma unroll
     for (int i = 0; i < Q; ++i)
 #pragma unroll
@@ -1211,7 +1351,10 @@ bool attention_split_fits(int heads, int M, int nk, int64_t scratch_floats) {
 
 hipError_t launch_attention(const AttnArgs& in, hipStream_t s) {
   const dim3 grid(in.heads), block(256);
-  if (in.scratch && attention_split_fits(in.heads, in.M, in.nk, in.scratch_floats)) {
+  const bool split = in.scratch && attention_split_fits(in.heads, in.M, in.nk, in.scratch_floats);
+  if (in.rope && !(split && in.M == 1 && in.hd % 32 == 0 && in.rope_key >= 0 && in.rope_key < in.nk))
+    return hipErrorInvalidValue;  // split form only
+  if (split) {
     // the split form: scratch rows of the scores, 32 keys per scores workgroup (more past 512 keys,
     // at most 16 chunks)
     AttnArgs a = in;

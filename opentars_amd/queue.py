@@ -189,14 +189,17 @@ def set_fusion(on: bool) -> bool:
     return bool(_lib.lib().tars_set_queue_fusion(int(on)))
 
 
-FUSION_KINDS = ("quant_gemm", "attention", "add_norm", "norm_rope", "gated_mlp", "norm_rope_two", "norm_quant")
+FUSION_KINDS = ("quant_gemm", "attention", "add_norm", "norm_rope", "gated_mlp", "norm_rope_two", "norm_quant",
+                "rope_attention")
 
 
 def fusion_counts(reset: bool = False) -> dict:
     """Fused launches run_queue has run since the last reset, per kind (FUSION_KINDS). A gated_mlp
     launch (an MLP's ELT MUL folded into its gate / up GEMMs) and a norm_quant launch (a norm, and
     the residual add before it, run in front of a quantizer group) also count as quant_gemm;
-    norm_rope counts (norm, RoPE) pairs and norm_rope_two the launches that ran two of them. A
+    norm_rope counts (norm, RoPE) pairs and norm_rope_two the launches that ran two of them; a
+    rope_attention launch (an attention whose scores kernel ran the layer's q and k norm + RoPE pairs)
+    also counts as attention and as two norm_rope pairs. A
     replayed launch plan counts its fused launches again. Diagnostics for tests and benchmarks."""
     arr = (ctypes.c_int64 * len(FUSION_KINDS))()
     _lib.lib().tars_queue_fusion_counts(arr, len(FUSION_KINDS), int(reset))

@@ -980,6 +980,75 @@ def test_attention_with_values_the_flushes_change(heads, kv_heads, hd, M, t0, v_
     assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
 
 
+def rope_attention_program(seed: int, heads: int, kv_heads: int, hd: int, t0: int, fn: int = Q.ROW_RMSNORM,
+                           beta: bool = False, rot: int = 0, key_row: int = -1, qn_over_v: bool = False) -> Program:
+    """One decode layer's q / k norms and rotations and its attention (tars_mini/llm.py:705-746): the
+    q norm of a row per query head and its RoPE, the k norm of a row per K / V head and its RoPE into
+    key row t0 of the cache (key_row: another row), then the per-head FDOT_NT / softmax / FDOT_NN
+    triples over the cache's keys rounded up to 16 (t0 + 1 valid). rot: the RoPE's rotated width (hd
+    when 0); qn_over_v: the q norm writes over V rows."""
+    p = Program(seed, image=ATT_IMAGE, qaddr=ATT_QADDR)
+    rng = p.rng
+    nk, rot = (t0 + 16) // 16 * 16, rot or hd
+    kc = p.put(rng.normal(0, 1, (nk, kv_heads * hd)).astype("<f4").tobytes())
+    vc = p.put(rng.normal(0, 1, (nk, kv_heads * hd)).astype("<f4").tobytes())
+    qx = p.put(rand_rows(p, heads, hd).tobytes())
+    kx = p.put(rand_rows(p, kv_heads, hd).tobytes())
+    ang = rng.uniform(0, 6.3, rot // 2).astype(np.float32)
+    tab = p.put(np.concatenate([np.cos(ang), np.sin(ang)]).astype("<f4").tobytes())
+    qn = vc + 4 * kv_heads * hd if qn_over_v else p.alloc(4 * heads * hd)
+    qr, kn = p.alloc(4 * heads * hd), p.alloc(4 * kv_heads * hd)
+    for x, rows, y in ((qx, heads, qn), (kx, kv_heads, kn)):
+        g = p.put(rng.normal(1, 0.2, hd).astype("<f4").tobytes())
+        bb = p.put(rng.normal(0, 0.1, hd).astype("<f4").tobytes()) if beta else 0
+        p.add(OPCODE=Q.OP_ROW, CTRL=fn, EPI=Q.epi(bias=int(beta)), A_OFF=x, Y_OFF=y, SCALE_OFF=g, BIAS_OFF=bb,
+              W_OFF=f32bits(1e-6), M=rows, N=hd)
+        ry = qr if y == qn else kc + 4 * (t0 if key_row < 0 else key_row) * kv_heads * hd
+        p.add(OPCODE=Q.OP_ROPE, EPI=Q.epi(), A_OFF=y, W_OFF=tab, Y_OFF=ry, M=rows, N=hd, K=rot, GROUP_SIZE=rows)
+    sc, pr, att = p.alloc(4 * nk), p.alloc(4 * nk), p.alloc(4 * heads * hd)
+    for h in range(heads):
+        kv = h // (heads // kv_heads)
+        p.add(OPCODE=Q.OP_FDOT, CTRL=0, EPI=Q.epi(), A_OFF=qr + 4 * h * hd, W_OFF=kc + 4 * kv * hd, Y_OFF=sc, M=1,
+              N=nk, K=hd, GROUP_SIZE=4 * kv_heads * hd // 16)
+        p.add(OPCODE=Q.OP_ROW, CTRL=Q.ROW_SOFTMAX, EPI=Q.epi(), A_OFF=sc, Y_OFF=pr, M=1, N=nk, K=t0 + 1)
+        p.add(OPCODE=Q.OP_FDOT, CTRL=1, EPI=Q.epi(), A_OFF=pr, W_OFF=vc + 4 * kv * hd, Y_OFF=att + 4 * h * hd, M=1,
+              N=hd, K=nk, GROUP_SIZE=4 * kv_heads * hd // 16)
+    return p
+
+
+@pytest.mark.parametrize("fusion", [True, False])
+@pytest.mark.parametrize("heads,kv_heads,hd,t0,fn,beta,rot,key_row,qn_over_v,fused", [
+    (16, 8, 128, 250, Q.ROW_RMSNORM, False, 0, -1, False, True),     # Qwen3-0.6B
+    (4, 2, 64, 40, Q.ROW_LAYERNORM, True, 0, -1, False, True),       # LayerNorm with beta
+    (8, 2, 128, 300, Q.ROW_L2NORM, False, 0, -1, False, True),       # four query heads per K / V head
+    (4, 1, 256, 17, Q.ROW_RMSNORM, False, 0, -1, False, True),       # head dim 256, one K / V head
+    (4, 2, 128, 60, Q.ROW_RMSNORM, False, 64, -1, False, False),     # partial rotation: apart
+    (4, 2, 128, 60, Q.ROW_RMSNORM, False, 0, 59, False, True),       # the k RoPE on another key row
+    (4, 2, 128, 64, Q.ROW_RMSNORM, False, 0, -1, False, True),       # the new key in a later key chunk
+    (4, 2, 128, 60, Q.ROW_RMSNORM, False, 0, -1, True, False),       # the q norm over V rows: apart
+])
+def test_rope_pairs_fold_into_the_attention(fusion, heads, kv_heads, hd, t0, fn, beta, rot, key_row, qn_over_v,
+                                            fused):
+    """A layer's q and k (norm, RoPE) pairs and its attention, which the executor runs as one
+    attention launch whose scores kernel forms the query rows and the new key row itself (storing
+    the norm and RoPE outputs), when the rotation is full width, the k RoPE writes exactly one key row
+    per K / V head and no output of the pairs lands on a K / V row; otherwise the pairs and the
+    attention run as their own launches. The images equal the oracle's."""
+    p = rope_attention_program(heads * 31 + t0, heads, kv_heads, hd, t0, fn, beta, rot, key_row, qn_over_v)
+    prev = NQ.set_fusion(fusion)
+    NQ.fusion_counts(reset=True)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs), ATT_QADDR)
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    counts = NQ.fusion_counts()
+    assert counts["rope_attention"] == int(fusion and fused), counts
+    assert counts["attention"] == int(fusion), counts
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
 def test_attention_heads_that_depend_on_each_other_run_in_order():
     """The last head reads the first head's output as its q rows: not concurrent, so not fused as
     one group; the image still equals the oracle's in-order run."""
@@ -1065,8 +1134,8 @@ def test_whole_decode_step_matches_the_oracle(fusion, shape):
         NQ.set_fusion(prev)
     counts = NQ.fusion_counts()
     assert counts["gated_mlp"] == (3 * dims["layers"] if fusion and shape == "qwen3_width" else 0), counts
-    # each layer's q and k (norm, RoPE) pairs run as one launch
-    assert counts["norm_rope_two"] == (3 * dims["layers"] if fusion else 0), counts
+    # each layer's q and k (norm, RoPE) pairs run in its attention launch
+    assert counts["rope_attention"] == (3 * dims["layers"] if fusion else 0), counts
     # at Qwen3 width every norm runs in front of its quantizer group: each layer's two and the final one
     assert counts["norm_quant"] == (3 * (2 * dims["layers"] + 1) if fusion and shape == "qwen3_width" else 0), counts
     logits = np.frombuffer(bytes(o.ddr[dq.logits:dq.logits + 4 * dq.vocab]), "<f4")
