@@ -934,19 +934,21 @@ __device__ __forceinline__ void group_norm_rope(const AttnNormRope& p, int fn, i
   }
 }
 
-template <int HD, int Q>
+template <int HD, int Q, bool ROPE>
 __global__ __launch_bounds__(256) void attn_split_scores_kernel(AttnArgs a) {
   constexpr int U = HD / 16, KF = 2;
   const int hg = blockIdx.x, t = threadIdx.x, g = t >> 4, l = t & 15;
   const int G = a.group, M = a.M, nk = a.nk;
-  // every argument the kernel reads, in one scalar round trip (see attn_split_pv_kernel), the
-  // norm + RoPE fields included (read where first used, they measured as a wait of microseconds)
+  // every argument the kernel reads, in one scalar round trip (see attn_split_pv_kernel); ROPE:
+  // the norm + RoPE fields too (read where first used, they measured as a wait of microseconds)
   __asm__ volatile("" : : "s"(a.q[hg * G]), "s"(a.ldq), "s"(a.k[hg * G]), "s"(a.ldk), "s"(a.keys_per_wg),
-                   "s"(a.scratch), "s"(a.ld_scratch), "s"(a.heads), "s"(a.sc), "s"(a.ldsc), "s"(a.rope), "s"(a.rope_key));
-  __asm__ volatile("" : : "s"(a.rq.x), "s"(a.rq.ldx), "s"(a.rq.gamma), "s"(a.rq.beta), "s"(a.rq.eps), "s"(a.rq.fn),
-                   "s"(a.rq.n), "s"(a.rq.ldn), "s"(a.rq.tab), "s"(a.rq.rows_per_pos));
-  __asm__ volatile("" : : "s"(a.rk.x), "s"(a.rk.ldx), "s"(a.rk.gamma), "s"(a.rk.beta), "s"(a.rk.eps), "s"(a.rk.fn),
-                   "s"(a.rk.n), "s"(a.rk.ldn), "s"(a.rk.tab), "s"(a.rk.rows_per_pos));
+                   "s"(a.scratch), "s"(a.ld_scratch), "s"(a.heads), "s"(a.sc), "s"(a.ldsc));
+  if constexpr (ROPE) {
+    __asm__ volatile("" : : "s"(a.rope), "s"(a.rope_key), "s"(a.rq.x), "s"(a.rq.ldx), "s"(a.rq.gamma), "s"(a.rq.beta),
+                     "s"(a.rq.eps), "s"(a.rq.fn), "s"(a.rq.n), "s"(a.rq.ldn), "s"(a.rq.tab), "s"(a.rq.rows_per_pos));
+    __asm__ volatile("" : : "s"(a.rk.x), "s"(a.rk.ldx), "s"(a.rk.gamma), "s"(a.rk.beta), "s"(a.rk.eps), "s"(a.rk.fn),
+                     "s"(a.rk.n), "s"(a.rk.ldn), "s"(a.rk.tab), "s"(a.rk.rows_per_pos));
+  }
   const int jb = blockIdx.y * a.keys_per_wg, je = min(nk, jb + a.keys_per_wg);
   const float* kb = a.k[hg * G];
   // this 16-lane group's first key rows, issued before anything else
@@ -960,13 +962,21 @@ __global__ __launch_bounds__(256) void attn_split_scores_kernel(AttnArgs a) {
   };
   int j0 = jb + g;
   float kv[KF][U];
-  load_keys(kv, j0);
   float qv[Q][U];
-  // rope: the new key row when this workgroup's keys include it (its loads read the cache before
+  if constexpr (!ROPE) {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const float* qr = frow(a.q[hg * G + i / M], a.ldq, i % M);
+#pragma unroll
+      for (int u = 0; u < U; ++u) qv[i][u] = ftz(qr[l + 16 * u]);
+    }
+  }
+  load_keys(kv, j0);
+  // ROPE: the new key row when this workgroup's keys include it (its loads read the cache before
   // it is written and are replaced by these values)
-  const bool new_key = a.rope && jb <= a.rope_key && a.rope_key < je;
+  const bool new_key = ROPE && jb <= a.rope_key && a.rope_key < je;
   float knew[U];
-  if (a.rope) {
+  if constexpr (ROPE) {
     // one query row per head; 16-lane group r < Q forms query row r of the group (head hg * G + r),
     // group Q the new key row (the groups of one wave run side by side), and they share the rows
     // through LDS
@@ -997,13 +1007,6 @@ __global__ __launch_bounds__(256) void attn_split_scores_kernel(AttnArgs a) {
     if (new_key) {
 #pragma unroll
       for (int u = 0; u < U; ++u) knew[u] = rows[Q][l + 16 * u];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < Q; ++i) {
-      const float* qr = frow(a.q[hg * G + i / M], a.ldq, i % M);
-#pragma unroll
-      for (int u = 0; u < U; ++u) qv[i][u] = ftz(qr[l + 16 * u]);
     }
   }
   for (; j0 < je; j0 += 16 * KF) {
@@ -1280,7 +1283,8 @@ int query_group(const AttnArgs& a) {
 
 template <int HD, int Q>
 void launch_split_q(const AttnArgs& a, dim3 gs, dim3 gp, hipStream_t s) {
-  hipLaunchKernelGGL((attn_split_scores_kernel<HD, Q>), gs, dim3(256), 0, s, a);
+  if (a.rope) hipLaunchKernelGGL((attn_split_scores_kernel<HD, Q, true>), gs, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((attn_split_scores_kernel<HD, Q, false>), gs, dim3(256), 0, s, a);
   if (a.v_fp16) hipLaunchKernelGGL((attn_split_pv_kernel<HD, true, Q>), gp, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((attn_split_pv_kernel<HD, false, Q>), gp, dim3(256), 0, s, a);
 }
