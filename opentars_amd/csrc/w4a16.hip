@@ -318,8 +318,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
   const int act = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, act));
   const int out = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, out));
   const float out_scale = SIMPLE ? 0.0f : kload<float>(ka + offsetof(W4Args, out_scale));
-  const int ce = lane >> 2, bank = lane & 3;          // chain lane: (m, u) = (ce / U, ce % U)
+  // chain lanes. One activation row and at most four rows per wave: lane 4 b + u (b, u < 4) runs
+  // bank b of row u, its terms gathered from the four 16-lane rows by permlane swaps (kRegChain);
+  // otherwise lane 4 (m U + u) + b, its terms through LDS.
+  constexpr bool kRegChain = MR == 1 && U <= 4;
+  const int ce = kRegChain ? (lane & 3) : lane >> 2, bank = kRegChain ? (lane >> 2) & 3 : lane & 3;
   const int ue = ce % U, me = ce / U;
+  const bool chain_lane = kRegChain ? lane < 16 && (lane & 3) < U : ce < MR * U;
   float bias_v = 0.0f;
 
   // 2. alignment into LDS digit planes
@@ -352,6 +357,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
   // 3. dots and terms
   const uint16_t* wsh = reinterpret_cast<const uint16_t*>(sm.ws[wave]);
   const int q = lane & 3;
+  float T[CPL];  // kRegChain: this lane's term of chunk j (row q, group (lane >> 2) + 16 j)
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
@@ -380,20 +386,36 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
         for (int v = 1; v < 4; ++v)
           if (4 * k + v < U) d = q == v ? dots[4 * k + v] : d;
         const float term = fmul(fmul(i2f(d), from_fp16_bits(wsh[min(u, U - 1) * G + g])), xs);
-        if (u < U && c < C && n0 + u < N) sm.terms[wave][r * U + u][g] = term;
+        if constexpr (kRegChain) T[j] = term;
+        else if (u < U && c < C && n0 + u < N) sm.terms[wave][r * U + u][g] = term;
       }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // 4. bank chains (at most G / 4 <= 4 CPL steps)
+  // 4. bank chains (at most G / 4 <= 4 CPL steps): step i adds group g = bank + 4 i
   constexpr int kSteps = 4 * CPL;
-  const float* trow = sm.terms[wave][ce < MR * U ? ce : 0];
   float tv[kSteps];
+  if constexpr (kRegChain) {
+    // group g = bank + 4 i is on lane 4 b + u + 16 (i & 3), chunk i >> 2: for a lane of row 0,
+    // the lanes 16, 32 and 48 above it, gathered with permlane swaps (no LDS, no barrier)
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) tv[i] = trow[bank + 4 * i];  // index <= 16 CPL - 1 < kTermStride
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t t0 = __float_as_uint(T[j]);
+      const uint32_t t1 = __builtin_amdgcn_permlane16_swap(t0, t0, false, false)[1];  // lane + 16 (row 2: + 48)
+      const uint32_t t2 = __builtin_amdgcn_permlane32_swap(t0, t0, false, false)[1];  // lane + 32
+      const uint32_t t3 = __builtin_amdgcn_permlane32_swap(t1, t1, false, false)[1];  // lane + 48
+      tv[4 * j] = T[j];
+      tv[4 * j + 1] = __uint_as_float(t1);
+      tv[4 * j + 2] = __uint_as_float(t2);
+      tv[4 * j + 3] = __uint_as_float(t3);
+    }
+  } else {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* trow = sm.terms[wave][ce < MR * U ? ce : 0];
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) tv[i] = trow[bank + 4 * i];  // index <= 16 CPL - 1 < kTermStride
+  }
   float acc = 0.0f;
   uint32_t mk = ~0u;
 #pragma unroll
@@ -409,9 +431,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
       if (bank + 4 * i < G) acc = fadd_chain(acc, tv[i]);
   }
   acc = chain_end(acc);
-  const float pair = fadd(acc, lane_xor1(acc));  // bank 0: b0 + b1, bank 2: b2 + b3
-  const float other = lane_xor2(pair);
-  if (bank == 0 && ce < MR * U && n0 + ue < N && m0 + me < M) {
+  // bank 0: b0 + b1, bank 2: b2 + b3 (the next bank's lane: 1 above, or 4 above by a row rotation)
+  const float pair = fadd(acc, kRegChain ? __int_as_float(dpp<kDppRowRor12>(__float_as_int(acc))) : lane_xor1(acc));
+  const float other = kRegChain ? __int_as_float(dpp<kDppRowRor8>(__float_as_int(pair))) : lane_xor2(pair);
+  if (bank == 0 && chain_lane && n0 + ue < N && m0 + me < M) {
     float y = fadd(pair, other);
     const int64_t yrow = static_cast<int64_t>(m0 + me) * ldy;
     if constexpr (SIMPLE) {

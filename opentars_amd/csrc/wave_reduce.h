@@ -74,7 +74,7 @@ __device__ __forceinline__ int swap16_sum(int a, int b) {
   const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
   return static_cast<int>(r[0]) + static_cast<int>(r[1]);
 }
-constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128, kDppRowRor12 = 0x12C;  // lane i <- lane (i - n) mod 16 of its row
 
 // Every lane ends with the total over the wave's 64 lanes of one of its U (1, 2, 4 or 8) values,
 // value scatter_row<U>(lane); exact int32 sums, so the order of the adds does not matter.
