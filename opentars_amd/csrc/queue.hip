@@ -1057,9 +1057,8 @@ bool norm_rope_pair(const Checked& r, const Checked& p, uintptr_t img, Segs& ins
 // and V row (the new key row aside), the attention's outputs apart from the pairs' inputs and
 // outputs, nothing on a later descriptor.
 bool rope_attention(uint8_t* image, const Checked& r, const Checked& p, const Checked& r1, const Checked& p1,
-                    const Segs& pins, const Segs& pouts, const std::vector<AttnHead>& heads, const Segs& ains,
-                    const Segs& aouts, const Segs& rest, hipStream_t s, RopePrologue& pro) {
-  (void)ains;
+                    const Segs& pins, const Segs& pouts, const std::vector<AttnHead>& heads, const Segs& aouts,
+                    const Segs& rest, hipStream_t s, RopePrologue& pro) {
   const size_t H = heads.size();
   const Desc& nt0 = heads[0].nt;
   const uint64_t hd = nt0[F_K], nk = nt0[F_N], ldk = b_stride(nt0).first;
@@ -1092,7 +1091,7 @@ bool rope_attention(uint8_t* image, const Checked& r, const Checked& p, const Ch
   Segs new_keys = p1.y;
   Segs others;  // the pairs' outputs but the new key rows
   for (const Checked* c : {&r, &p, &r1}) others.insert(others.end(), c->y.begin(), c->y.end());
-  if (overlaps(others, kv) || overlaps(new_keys, Segs(kv.begin(), kv.end())) || overlaps(aouts, pall) ||
+  if (overlaps(others, kv) || overlaps(new_keys, kv) || overlaps(aouts, pall) ||
       (!rest.empty() && (overlaps(rest, pouts) || overlaps(rest, aouts))))
     return false;
   pro = RopePrologue{r.d, p.d, r1.d, p1.d, static_cast<int>(qpk), static_cast<int>(key)};
@@ -1136,8 +1135,7 @@ int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>&
       Segs pins = ins, pouts = outs;
       pins.insert(pins.end(), ins1.begin(), ins1.end());
       pouts.insert(pouts.end(), outs1.begin(), outs1.end());
-      if (rope_attention(image, r, p, r1, p1, pins, pouts, heads, ains, aouts,
-                         rest_lo < rest_hi ? rest : Segs{}, s, pro)) {
+      if (rope_attention(image, r, p, r1, p1, pins, pouts, heads, aouts, rest_lo < rest_hi ? rest : Segs{}, s, pro)) {
         const int rc = launch_attention_group(image, heads, s, &pro);
         if (rc == TARS_OK) fused = 3 + 3 * static_cast<int>(heads.size());
         return rc;
