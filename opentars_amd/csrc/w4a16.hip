@@ -67,7 +67,8 @@ __device__ __forceinline__ void load_chunk_bits(const void* x, int64_t lda, int 
 
 // Aligns NE elements held by each of GL consecutive lanes that together form one 128-wide group
 // (NE * GL == 128; every lane of the wave must call it, dead lanes on shadow data). Inputs are raw
-// fp32 encodings (not flushed). Outputs the signed mantissas and the group's fp32 scale encoding.
+// fp32 encodings (not flushed). Outputs the signed mantissas (their low 16 bits: int16 values) and
+// the group's fp32 scale encoding.
 template <int NE, int GL>
 __device__ __forceinline__ void align_elems(const uint32_t* xraw, int* mant, uint32_t& scale_bits) {
   static_assert(NE * GL == kGroup, "a group is 128 elements");
@@ -86,9 +87,13 @@ __device__ __forceinline__ void align_elems(const uint32_t* xraw, int* mant, uin
     // and so does an unflushed subnormal input (|x * 2^(140 - e_eff)| < 2^-126 * 2^124), so no
     // flush is needed. Equal to the shift rule for every significand and shift (exhaustive CPU
     // check) and on real rows, flushed or not (CPU check against the aligner's restatement).
+    // One fma per element: x * p is exact and |x * p| < 2^14, so RN(x * p + 1.5 * 2^23) is
+    // 1.5 * 2^23 + rint(x * p) (ties to even; its ulp is 1) and the encoding's low 16 bits are the
+    // mantissa as an int16, the only bits the digit planes and the aligned rows take.
     const float p = __uint_as_float(static_cast<uint32_t>(267 - e_eff) << 23);
 #pragma unroll
-    for (int i = 0; i < NE; ++i) mant[i] = static_cast<int>(__builtin_rintf(__uint_as_float(xraw[i]) * p));
+    for (int i = 0; i < NE; ++i)
+      mant[i] = static_cast<int>(__float_as_uint(__builtin_fmaf(__uint_as_float(xraw[i]), p, 12582912.0f)));
     scale_bits = static_cast<uint32_t>(e_eff - 13) << 23;
     return;
   }
@@ -385,7 +390,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
 #pragma unroll
         for (int v = 1; v < 4; ++v)
           if (4 * k + v < U) d = q == v ? dots[4 * k + v] : d;
-        const float term = fmul(fmul(i2f(d), from_fp16_bits(wsh[min(u, U - 1) * G + g])), xs);
+        // the contract's fmul(fmul(i2f(d), ws), xs) with its wrappers where they act: i2f(d) is exact
+        // (|d| <= 2^24) and the fp16 scale is an fp32 normal, infinity or NaN, so the first product
+        // is 0, at least 2^-24 in magnitude, infinite or NaN (no flush); the second is flushed; a NaN
+        // payload only feeds the chains, whose results are canonicalized
+        const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), from_fp16_bits(wsh[min(u, U - 1) * G + g])), xs));
         if constexpr (kRegChain) T[j] = term;
         else if (u < U && c < C && n0 + u < N) sm.terms[wave][r * U + u][g] = term;
       }

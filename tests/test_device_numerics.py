@@ -92,6 +92,20 @@ def test_rne_shift_by_add_equals_the_reference_rounding():
         assert fast.max() <= (1 << 14) or sh < 10  # mantissas stay within 16384 for sh >= 10
 
 
+def test_magic_number_rounding_gives_the_int16_mantissa():
+    """RN(v + 1.5 * 2^23) for every v = k / 2^j with |v| < 2^14 (k an integer, the exact products
+    x * 2^(140 - e_eff) the aligner rounds) has the low 16 bits of rint(v) (ties to even), two's
+    complement: checked over every multiple of 1/8 in range (the ties x.5 among them), and on the
+    values just above and below each tie."""
+    k = np.arange(-(1 << 17), 1 << 17, dtype=np.int64)
+    v8 = k.astype(f32) / f32(8)
+    ties = np.arange(-(1 << 14), 1 << 14).astype(f32) + f32(0.5)
+    for v in (v8, np.nextafter(ties, f32(np.inf)), np.nextafter(ties, f32(-np.inf))):
+        v = v[np.abs(v) < 2 ** 14]
+        got = (v + f32(12582912.0)).view(np.uint32) & 0xFFFF
+        assert (got == (np.rint(v).astype(np.int64) & 0xFFFF)).all()
+
+
 def test_rne_shift_equals_a_power_of_two_product_rounded_to_even():
     """The aligner's finite-group fast path computes a mantissa as rint(x * 2^(140 - e_eff)) in
     fp32 (one exact power-of-two product, then round-half-even): for a 24-bit significand sig of
@@ -137,12 +151,15 @@ def test_aligner_fast_path_matches_the_oracle_on_finite_groups():
         p = ((267 - e_eff).astype(np.uint32) << 23).view(f32)[:, :, None]              # 2^(140 - e_eff)
         with np.errstate(under="ignore"):
             fast = np.rint(xf * p).astype(np.int64)
+            # the kernel's form: one fma (x * p is exact), the low 16 bits of RN(x * p + 1.5 * 2^23)
+            fma16 = ((xf * p + f32(12582912.0)).view(np.uint32) & 0xFFFF).astype(np.int64)
         want = q.astype(np.int64).reshape(fast.shape)
         # flushed inputs: every finite group; unflushed inputs (the kernel's fast path): groups with
         # emax >= 16, where a subnormal input times 2^(140 - e_eff) <= 2^124 stays below 1/4
         sel = np.ones_like(emax, bool) if flushed else emax >= 16
         assert sel.sum() > 100
         assert (fast[sel] == want[sel]).all()
+        assert (fma16[sel] == (want[sel] & 0xFFFF)).all()
 
 
 def test_q8_fast_path_for_rows_with_a_normal_maximum():
