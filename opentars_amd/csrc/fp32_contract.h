@@ -401,10 +401,12 @@ __device__ __forceinline__ uint32_t max_abs_bits4(uint32_t m, float4 v) {
 }
 __device__ __forceinline__ uint32_t flush_max_bits(uint32_t m) { return m < 0x00800000u ? 0u : m; }
 
-// amax encoding (an unsigned max of |x| encodings; any NaN encoding wins) -> (inv, s)
+// amax encoding (an unsigned max of |x| encodings; any NaN encoding wins) -> (inv, s). inv is the
+// contract's fmul(127, recip_f(amax)) written out: recip_f's result is 0, at least 2^-126, infinite
+// or the canonical NaN, so 127 times it is never subnormal and needs only the canonicalization.
 __device__ __forceinline__ void quant_scales(uint32_t amax_bits, float& inv, float& s) {
   const float amax = ffrom(amax_bits > kExpo ? kCanonNaN : amax_bits);
-  inv = fmul(ffrom(kQ127), recip_f(amax));
+  inv = canon(__fmul_rn(ffrom(kQ127), recip_f(amax)));
   s = fmul(amax, ffrom(kInv127));
 }
 

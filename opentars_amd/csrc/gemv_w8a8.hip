@@ -49,9 +49,13 @@ __device__ __forceinline__ int dot16(v4i w, v4i x, int acc) {
 // The epilogue of QM_ROWCOL with fp32 output and neither bias nor activation (the decode-step
 // linears and the lm_head): the golden's steps fmul(fmul(i2f(acc), srow), scol) and the output
 // flush, with the general epilogue's code (every activation and output format) compiled out, which
-// a cold launch otherwise fetches (measured: 0.05 - 0.2 us per launch).
+// a cold launch otherwise fetches (measured: 0.05 - 0.2 us per launch). The contract's wrappers
+// are written out where they act: i2f(acc) is 0 or at least 1 in magnitude (no flush), the scales
+// are flushed (off the dependent path), each product's output is flushed, and a NaN stays NaN to
+// the one canonicalization at the end.
 __device__ __forceinline__ float simple_epilogue(int acc, float sr, float sc) {
-  return ftz(fmul(fmul(i2f(acc), sr), sc));
+  const float p = ftz(__fmul_rn(i2f(acc), ftz(sr)));
+  return canon(ftz(__fmul_rn(p, ftz(sc))));
 }
 
 // Whether an epilogue is that simple one (plain GEMV: it also needs a row scale).
