@@ -579,7 +579,7 @@ __device__ __forceinline__ void quant_gemv_body(const float* x, int64_t lda, con
   } else {
     for (int i = threadIdx.x; i < K4; i += kThreads) mx = max_abs_bits4(mx, xrow[i]);
   }
-  mx = group_max<64>(mx);
+  mx = wave_max_u32(mx);  // DPP within rows, then permlane swaps (no lane reads)
   if (lane == 0) wave_max[wave] = mx;
   // the epilogue operands, once the activations are in (their addresses wait for the
   // kernel-argument load, which is then long done)

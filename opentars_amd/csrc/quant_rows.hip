@@ -24,7 +24,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
       mx = max_abs_bits4(mx, row[4 * c + j]);
     }
   }
-  mx = group_max<64>(mx);
+  mx = wave_max_u32(mx);  // DPP within rows, then permlane swaps (no lane reads)
   __shared__ uint32_t wave_max[kThreads / 64];
   __shared__ float inv_shared;
   if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mx;
