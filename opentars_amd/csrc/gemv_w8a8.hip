@@ -415,7 +415,7 @@ __device__ __forceinline__ void quant_gemv_body(const float* x, int64_t lda, con
                                offsetof(GemvGroup, W));
   const int nblk = (N + kRows - 1) / kRows;  // the grid's x extent
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // a scalar: row addresses on the SALU
   const int slot = lane / L;
   const int sub = lane % L;
   const int m = blockIdx.y;
@@ -425,9 +425,9 @@ __device__ __forceinline__ void quant_gemv_body(const float* x, int64_t lda, con
   const v4i zero = {0, 0, 0, 0};
 
   // one batch of loads: the fp32 activations (the quantizer waits on them alone), the weights
-  // (rows past N and chunks past K read the matrix start: rows past N are never stored and a
-  // chunk past K meets a zero activation chunk), then the epilogue operands, whose addresses come
-  // from the kernel-argument load
+  // (rows past N read row N - 1 and chunks past K chunk C - 1, or with NORM the matrix start: rows
+  // past N are never stored and a chunk past K meets a zero activation chunk), then the epilogue
+  // operands, whose addresses come from the kernel-argument load
   constexpr int XV = CPL > 0 ? (L == 64 ? CPL : 1) : 1;  // float4s of the row per thread (K <= 1024 XV)
   const float4* xrow = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(x) + m * lda);
   float4 xr[XV];
@@ -456,11 +456,17 @@ __device__ __forceinline__ void quant_gemv_body(const float* x, int64_t lda, con
     for (int u = 0; u < U; ++u) {
       const int n = n0 + (PAIR ? u % UR : u);
       const int8_t* Wu = PAIR && u >= UR ? W1 : W;
-      const v4i* wrow = reinterpret_cast<const v4i*>(Wu + static_cast<int64_t>(n) * K);
+      if constexpr (NORM) {  // (measured: the clamped form below made the prologue kernels slower)
+        const v4i* wrow = reinterpret_cast<const v4i*>(Wu + static_cast<int64_t>(n) * K);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = sub + j * L;
-        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : reinterpret_cast<const v4i*>(Wu));
+        for (int j = 0; j < CPL; ++j) {
+          const int c = sub + j * L;
+          wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : reinterpret_cast<const v4i*>(Wu));
+        }
+      } else {
+        const v4i* wrow = reinterpret_cast<const v4i*>(Wu + static_cast<int64_t>(min(n, N - 1)) * K);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) wv[u][j] = __builtin_nontemporal_load(wrow + min(sub + j * L, C - 1));
       }
     }
   }
