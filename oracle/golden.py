@@ -123,13 +123,15 @@ def gemm_w4(x, Wp, ws_bits, bias=None, act: int = F.ACT_NONE, out: int = OUT_FP3
 
 
 # ---------------------------------------------------------------- host weight formats
-def quantize_weight(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Per-output-channel symmetric INT8 in float64 (compiler.py:47-57): s = amax / 127 (1.0 for
-    an all-zero row), q = rint(w / s) clipped to +-127; s stored as fp32."""
+def quantize_weight(w: np.ndarray, per_channel: bool = True) -> tuple[np.ndarray, np.ndarray]:
+    """Symmetric INT8 in float64 (compiler.py:51-57), per output channel (QM_ROWCOL / QM_CHANNEL
+    scales, int8 [N, K] plus fp32 [N]) or per tensor (QM_TENSOR, fp32 [1]): s = amax / 127 (1.0
+    for an all-zero row or tensor), q = rint(w / s) ties to even, clipped to +-127; s stored as
+    fp32 after the float64 quotient."""
     w = np.asarray(w, np.float64)
-    amax = np.abs(w).max(axis=1)
+    amax = np.abs(w).max(axis=1) if per_channel else np.array([np.abs(w).max()])
     s = np.where(amax > 0, amax / 127.0, 1.0)
-    q = np.clip(np.rint(w / s[:, None]), -127, 127).astype(np.int8)
+    q = np.clip(np.rint(w / (s[:, None] if per_channel else s[0])), -127, 127).astype(np.int8)
     return q, s.astype(np.float32)
 
 

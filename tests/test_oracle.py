@@ -138,6 +138,96 @@ def test_kat_quantize_weight4():
     assert (q[1, 64] & 15) == k["q_1_64_lo"] and (q[1, 64] >> 4) == k["q_1_64_hi"]
 
 
+def test_kat_fp16_storage():
+    """Every binary16 pattern widens exactly and every finite one narrows back to itself; the
+    reference's three narrowing KATs (test_fp16_state.py:28-39)."""
+    k = KAT["fp16_storage"]
+    h = np.arange(65536, dtype=np.uint16)
+    wide = F.from_fp16_bits(h)
+    for i in range(0, 65536, 1):
+        v = struct.unpack("<e", int(h[i]).to_bytes(2, "little"))[0]
+        got = int(wide.view(np.uint32)[i])
+        if v != v:
+            assert got == int(k["nan_from_bits_result_bits"], 16)
+        else:
+            assert got == struct.unpack("<I", struct.pack("<f", v))[0], hex(i)
+    finite = np.isfinite(wide)
+    assert k["every_finite_pattern_round_trips"]
+    assert same_bits(F.to_fp16_bits(wide[finite]), h[finite])
+    assert wide[1] == val(k["from_bits_0x0001"])
+    x = np.array([val(v) for v in k["to_bits_x"]], f32)
+    assert F.to_fp16_bits(x).tolist() == [int(b, 16) for b in k["to_bits_h"]]
+
+
+def fp16_bits_exact(x: np.float32) -> int:
+    """binary16 encoding of an fp32 value by exact rational rounding: the nearest multiple of
+    the binade's spacing (2^-24 below 2^-14), ties to the even multiple, 65520 and up to
+    infinity, NaN to 0x7E00."""
+    v = float(x)
+    if v != v:
+        return 0x7E00
+    sign = 0x8000 if np.signbit(x) else 0
+    a = Fraction(abs(v)) if abs(v) != float("inf") else None
+    if a is None or a >= 65520:
+        return sign | 0x7C00
+    e = -14
+    while e < 15 and a >= Fraction(2) ** (e + 1):
+        e += 1
+    step = Fraction(2) ** (e - 10)
+    n = round(a / step)                      # Fraction rounds half to even
+    if a < Fraction(2) ** -14:
+        return sign | n                      # subnormal (n = 1024 is the smallest normal)
+    if n == 2048:
+        e, n = e + 1, 1024
+    return sign | ((e + 15) << 10) | (n - 1024)
+
+
+def test_to_fp16_bits_against_exact_rounding():
+    """to_fp16_bits (numerics.py:14-18) against rounding by exact rationals: every half-way
+    point between adjacent finite halves and its two fp32 neighbours, both signs, the overflow
+    edge, subnormals, and random fp32 encodings."""
+    a = np.arange(0x7BFF, dtype=np.uint16).view(np.float16).astype(f32)
+    b = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(f32)
+    mid = (a + b) * f32(0.5)
+    pick = np.random.default_rng(5).choice(mid.size, 3000, replace=False)
+    m = mid[pick]
+    rnd = np.random.default_rng(6).integers(0, 2 ** 32, 3000, dtype=np.uint32).view(f32)
+    edge = np.array([65504, 65519.996, 65520, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14,
+                     -0.0, 0.0, np.inf, -np.inf, np.nan], f32)
+    x = np.concatenate([m, -m, np.nextafter(m, f32(0)), np.nextafter(m, f32(np.inf)), edge, rnd])
+    got = F.to_fp16_bits(x)
+    want = np.array([fp16_bits_exact(v) for v in x], np.uint16)
+    assert same_bits(got, want)
+
+
+def test_quantize_weight_against_exact_arithmetic():
+    """The host INT8 weight quantizer (compiler.py:51-57) against exact rationals: the scale is
+    the float64 nearest amax/127 (1.0 for an all-zero row), each q the nearest integer to the
+    float64 nearest w/s, ties to even, within +-127; the scale stored as the fp32 nearest it.
+    Per channel and per tensor."""
+    rng = np.random.default_rng(11)
+    w = rng.normal(0, 0.3, (6, 40))
+    w[2] = 0.0
+    w[3, :6] = [127.0, 2.5, -2.5, 3.5, -0.5, 1.5]
+    w[3, 6:] = 0.0
+    for per_channel in (True, False):
+        q, s = G.quantize_weight(w, per_channel)
+        rows = w if per_channel else w.reshape(1, -1)
+        assert q.shape == w.shape and q.dtype == np.int8 and s.dtype == f32
+        assert s.shape == ((w.shape[0],) if per_channel else (1,))
+        for r in range(rows.shape[0]):
+            amax = max(abs(Fraction(float(t))) for t in rows[r])
+            s64 = float(amax / 127) if amax else 1.0
+            assert s[r] == f32(struct.unpack("<f", struct.pack("<f", s64))[0])
+            want = [max(-127, min(127, round(Fraction(float(Fraction(float(t)) / Fraction(s64))))))
+                    for t in rows[r]]
+            got = (q if per_channel else q.reshape(1, -1))[r].tolist()
+            assert got == want
+    q, s = G.quantize_weight(w)
+    assert s[2] == 1.0 and (q[2] == 0).all()
+    assert s[3] == 1.0 and q[3, :6].tolist() == [127, 2, -2, 4, 0, 2]
+
+
 def test_kat_align_extremes():
     k = KAT["align_extremes"]
     x = np.zeros((4, 128), f32)
