@@ -5,8 +5,9 @@
  * pointer (hipMalloc'd or a torch CUDA/HIP tensor's data_ptr) except where noted; `stream` is a
  * hipStream_t (NULL = the null stream). Work is enqueued on `stream` and is stream-ordered with
  * whatever else the caller puts there; nothing synchronizes the host. No entry point allocates,
- * except that tars_attention and the attention in tars_run_queue allocate one 1 MiB scratch buffer
- * per device at their first use there (tars_attention_noalloc never does).
+ * except that tars_attention and the attention in tars_run_queue allocate a 1 MiB scores scratch
+ * per (device, stream) at a stream's first use there, and tars_run_queue one per launch plan that
+ * runs attention (tars_attention_noalloc never does).
  *
  * Every entry point validates its arguments on the host before it launches anything and returns
  * a status. On a non-zero status nothing was launched and nothing was written, mirroring the
@@ -230,6 +231,9 @@ int tars_relu(const float* x, int64_t lda, int32_t act, void* y, int64_t ldy, in
  *   table [rows, cols] at ld_table bytes (>= 2 cols, even); ids: host array of n indexes in
  *   [0, rows), any n >= 1; dst fp32 at ldd bytes (>= 4 cols, a multiple of 4); dst must not
  *   overlap the table's extent (its row gaps included).
+ * The ids travel as kernel arguments, 64 per launch. Every check runs before the first launch;
+ * the one exception to "nothing written on a non-zero status" is TARS_E_DEVICE from the runtime
+ * refusing a later launch, which leaves the rows of the launches before it written.
  */
 int tars_embed_rows(const uint16_t* table, int64_t ld_table, int64_t rows, int32_t cols,
                     const int32_t* ids, int32_t n, int32_t scaled, uint32_t scale_bits, float* dst,
@@ -262,9 +266,12 @@ int tars_fdot(const float* A, int64_t lda, const void* B, int64_t ldb, int32_t n
  * Consecutive heads with equal k and v pointers (2 or 4 query heads per K / V head) are run
  * together. When such a group has at most 4 query rows in all (heads in the group times M) and
  * the scores fit, the work is split over many workgroups through a 1 MiB device scratch buffer
- * that the library allocates on the device at its first use there and keeps until the process
- * ends (calls that overlap in time on one device race on it); otherwise, or while the stream is
- * capturing a graph before that first use, one workgroup per head. The bits are the same.
+ * of the call's stream, which the library allocates at the stream's first use on the device and
+ * keeps until the process ends (each stream has its own, up to 64 streams per device, so calls on
+ * different streams may overlap in time; a graph captured from a stream keeps that stream's
+ * scratch, so replay it ordered with the stream's other attention calls); otherwise (more streams,
+ * or a stream capturing a graph before its first use), one workgroup per head. The bits are the
+ * same.
  */
 int tars_attention(const float* const* q, int64_t ldq, const float* const* k, int64_t ldk,
                    const void* const* v, int64_t ldv, int32_t v_fp16, void* const* att, int64_t ldatt,
@@ -332,6 +339,10 @@ typedef struct tars_queue_status {
  * ContractError; st->op_idx names it, nothing of it ran), TARS_E_ARG, or TARS_E_DEVICE.
  * core_id: the executing core's id (CORE_ID must match); gemv_only: the KV260 profile (a conv or
  * a GEMM with K > 4096 is E_OPCODE), golden.py:48-50.
+ * Fused attention uses the split form's scores scratch of `stream` (as tars_attention) when the
+ * queue runs op by op, and the launch plan's own scratch when it replays as a graph, so queues on
+ * different images may run on different streams at once. Each plan that runs attention holds
+ * 1 MiB of device memory; evicting a plan (more than 8 cached) frees it, which waits for the device.
  */
 int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int32_t n,
                    const uint8_t* host_queue, int32_t core_id, int32_t gemv_only,

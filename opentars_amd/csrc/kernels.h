@@ -334,8 +334,10 @@ bool attention_supported(int hd, int nk);
 // P V workgroup holds in LDS; output columns per P V workgroup.
 constexpr int kAttnSplitMaxQ = 4, kAttnSplitProbs = 4096, kAttnSplitCols = 32;
 bool attention_split_fits(int heads, int M, int nk, int64_t scratch_floats);
-// The split form's scratch on the current device: kAttnScratchFloats floats allocated at the first
-// call there (not while `s` is capturing a graph) and kept until the process ends; null when none.
+// The split form's scratch of stream `s` on the current device: kAttnScratchFloats floats allocated
+// at the stream's first call (not while `s` is capturing a graph), kept until the process ends;
+// each stream its own (up to 64 per device), so calls on different streams never share one; null
+// when none.
 constexpr int64_t kAttnScratchFloats = int64_t{1} << 18;
 float* attention_workspace(hipStream_t s);
 // The same size of scratch as a file-scope device array on the current device (no allocation;

@@ -735,7 +735,9 @@ tars::AttnNormRope norm_rope_args(uint8_t* image, const Desc& rd, const Desc& pd
   return p;
 }
 
-int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, hipStream_t s,
+// scratch: the split form's scores between its two launches (null: one workgroup per head). An
+// eager dispatch passes its stream's workspace, a launch plan the scratch it owns.
+int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, hipStream_t s, float* scratch,
                            const RopePrologue* pro = nullptr) {
   tars::AttnArgs a = attention_args(image, heads);
   if (pro) {
@@ -744,7 +746,7 @@ int launch_attention_group(uint8_t* image, const std::vector<AttnHead>& heads, h
     a.rq = norm_rope_args(image, pro->qn, pro->qr);
     a.rk = norm_rope_args(image, pro->kn, pro->kr);
   }
-  a.scratch = tars::attention_workspace(s);  // the split form's scores, when the device has its scratch
+  a.scratch = scratch;
   a.scratch_floats = a.scratch ? tars::kAttnScratchFloats : 0;
   const hipError_t e = tars::launch_attention(a, s);
   if (e != hipSuccess) {
@@ -833,7 +835,7 @@ int fuse_attention(uint8_t* image, const Checked& first, const std::vector<uint8
     group.clear();
     return TARS_OK;
   }
-  const int rc = launch_attention_group(image, group, s);
+  const int rc = launch_attention_group(image, group, s, tars::attention_workspace(s));
   if (rc == TARS_OK) fused = static_cast<int>(group.size());
   return rc;
 }
@@ -1136,7 +1138,7 @@ int fuse_norm_rope(uint8_t* image, const Checked& r, const std::vector<uint8_t>&
       pins.insert(pins.end(), ins1.begin(), ins1.end());
       pouts.insert(pouts.end(), outs1.begin(), outs1.end());
       if (rope_attention(image, r, p, r1, p1, pins, pouts, heads, aouts, rest_lo < rest_hi ? rest : Segs{}, s, pro)) {
-        const int rc = launch_attention_group(image, heads, s, &pro);
+        const int rc = launch_attention_group(image, heads, s, tars::attention_workspace(s), &pro);
         if (rc == TARS_OK) fused = 3 + 3 * static_cast<int>(heads.size());
         return rc;
       }
@@ -1189,8 +1191,19 @@ struct Plan {
   std::vector<uint8_t> bytes;
   std::vector<Step> steps;
   hipGraphExec_t exec = nullptr;
+  // The split attention's scores scratch of the plan's graph (allocated with the graph when a step
+  // runs attention): the plan's own, so replays on any stream never share it with eager work or with
+  // another plan. Freed with the graph (hipFree waits for the device first).
+  float* scratch = nullptr;
   uint64_t last_use = 0;
 };
+
+void drop_graph(Plan& p) {
+  if (p.exec) (void)hipGraphExecDestroy(p.exec);
+  if (p.scratch) (void)hipFree(p.scratch);
+  p.exec = nullptr;
+  p.scratch = nullptr;
+}
 
 // Fused launches run (diagnostics for tests and benchmarks): quantizer + GEMMs, attention,
 // residual ADD + norm, norm + RoPE pairs (two when two pairs share a launch), launches that ran two
@@ -1221,13 +1234,13 @@ std::vector<Plan> g_plans;
 uint64_t g_plan_clock = 0;
 bool g_graphs = true;
 
-int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) {
+int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s, float* scratch) {
   for (const Step& st : steps) {
     bool needs_host = false;
     const int rc = st.add_norm        ? launch_add_norm_pair(image, st.d, st.second, s)
                    : st.norm_rope     ? launch_norm_rope_pair(image, st.d, st.second, s, st.norm_rope2 ? &st.third : nullptr,
                                                           st.norm_rope2 ? &st.fourth : nullptr)
-                   : !st.attn.empty() ? launch_attention_group(image, st.attn, s, st.rope ? &st.rope_pro : nullptr)
+                   : !st.attn.empty() ? launch_attention_group(image, st.attn, s, scratch, st.rope ? &st.rope_pro : nullptr)
                    : st.group.empty() ? launch(image, st.d, s, needs_host)
                                       : launch_fused(image, st.d, st.group, s, st.gated ? &st.elt : nullptr,
                                                      st.pro_has_add ? &st.pro_add : nullptr, st.pro ? &st.pro_norm : nullptr);
@@ -1238,6 +1251,15 @@ int replay_steps(uint8_t* image, const std::vector<Step>& steps, hipStream_t s) 
 
 // The graph of a plan's launches (captured on a private default-priority stream).
 int capture(Plan& p) {
+  const bool attn = std::any_of(p.steps.begin(), p.steps.end(), [](const Step& st) { return !st.attn.empty(); });
+  if (attn && !p.scratch) {
+    void* m = nullptr;
+    if (hipMalloc(&m, static_cast<size_t>(tars::kAttnScratchFloats) * sizeof(float)) != hipSuccess) {
+      (void)hipGetLastError();
+      return TARS_E_DEVICE;
+    }
+    p.scratch = static_cast<float*>(m);
+  }
   hipStream_t cs = nullptr;
   if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return TARS_E_DEVICE;
   hipGraph_t g = nullptr;
@@ -1245,7 +1267,7 @@ int capture(Plan& p) {
   if (hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) != hipSuccess) {
     rc = TARS_E_DEVICE;
   } else {
-    rc = replay_steps(p.image, p.steps, cs);
+    rc = replay_steps(p.image, p.steps, cs, p.scratch);
     if (hipStreamEndCapture(cs, &g) != hipSuccess && rc == TARS_OK) rc = TARS_E_DEVICE;
   }
   if (rc == TARS_OK && hipGraphInstantiate(&p.exec, g, nullptr, nullptr, 0) != hipSuccess) {
@@ -1352,6 +1374,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
       Plan& p = g_plans[k];
       if (!same_key(p)) continue;
       if (!p.exec && capture(p) != TARS_OK) {  // no graph for this plan: forget it, run the queue as usual
+        drop_graph(p);
         g_plans.erase(g_plans.begin() + static_cast<std::ptrdiff_t>(k));
         break;
       }
@@ -1511,7 +1534,7 @@ int tars_run_queue(uint8_t* image, uint64_t image_len, uint64_t queue_addr, int3
     if (g_plans.size() >= kMaxPlans) {
       auto lru = std::min_element(g_plans.begin(), g_plans.end(),
                                   [](const Plan& a, const Plan& b) { return a.last_use < b.last_use; });
-      if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
+      drop_graph(*lru);
       g_plans.erase(lru);
     }
     Plan p;
@@ -1545,8 +1568,7 @@ int tars_set_queue_graphs(int on) {
   const int prev = g_graphs ? 1 : 0;
   g_graphs = on != 0;
   if (!g_graphs) {
-    for (Plan& p : g_plans)
-      if (p.exec) (void)hipGraphExecDestroy(p.exec);
+    for (Plan& p : g_plans) drop_graph(p);
     g_plans.clear();
   }
   return prev;

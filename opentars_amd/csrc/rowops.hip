@@ -16,6 +16,8 @@
 // thousand elements, tens of dependent steps per lane).
 #include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "kernels.h"
 #include "row_sums.h"
@@ -1304,23 +1306,35 @@ void launch_split(const AttnArgs& a, hipStream_t s) {
 }  // namespace
 
 float* attention_workspace(hipStream_t s) {
+  // One scratch per (device, stream): work on one stream runs in order, so two calls can share a
+  // scratch only when they are ordered; calls on different streams get different scratches and
+  // may overlap in time. At most kMaxStreams streams per device get one; further streams (and a
+  // stream that is capturing a graph when it would get its first) run the one-workgroup-per-head
+  // form, which needs none.
   constexpr int kMaxDevices = 64;
+  constexpr size_t kMaxStreams = 64;
   static std::mutex mu;
-  static float* ws[kMaxDevices] = {};
+  static std::vector<std::pair<hipStream_t, float*>> ws[kMaxDevices];
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
-  if (!ws[dev]) {
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
-    void* p = nullptr;
-    if (hipMalloc(&p, static_cast<size_t>(kAttnScratchFloats) * sizeof(float)) != hipSuccess) {
-      (void)hipGetLastError();  // no scratch: the one-workgroup-per-head form runs instead
-      return nullptr;
-    }
-    ws[dev] = static_cast<float*>(p);
+  for (const auto& e : ws[dev])
+    if (e.first == s) return e.second;
+  if (ws[dev].size() >= kMaxStreams) return nullptr;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+  // hipMalloc outside any graph capture this thread may have open on another stream
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, static_cast<size_t>(kAttnScratchFloats) * sizeof(float));
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
   }
-  return ws[dev];
+  ws[dev].emplace_back(s, static_cast<float*>(p));
+  return static_cast<float*>(p);
 }
 
 // The scores scratch of tars_attention_noalloc: a file-scope device array (each GPU holds its own

@@ -243,7 +243,11 @@ class TokenRows:
                                           torch.cuda.current_stream().cuda_stream))
 
     def write(self, image: torch.Tensor, pos: int, tokens: Iterable[int]) -> None:
-        ids = np.ascontiguousarray(np.fromiter((int(t) for t in tokens), np.int64), np.int32)
+        wide = np.fromiter((int(t) for t in tokens), np.int64)
+        if wide.size and (wide.min() < 0 or wide.max() >= self.lay.vocab):
+            bad = wide[(wide < 0) | (wide >= self.lay.vocab)][0]
+            raise IndexError(f"token id {bad} is outside the vocabulary of {self.lay.vocab} rows")
+        ids = np.ascontiguousarray(wide, np.int32)
         if pos + ids.size > self.lay.positions:
             raise OverflowError(f"context full ({self.lay.positions} tokens)")
         off, ld = self.lay.x0

@@ -110,6 +110,31 @@ def test_attention_twice_in_a_row_and_without_the_shared_rows():
         assert np.array_equal(bits(got), bits(want))
 
 
+def test_attention_on_two_streams_at_once():
+    """Calls on two streams overlap in time: each stream's split form has its own scores scratch,
+    so every call's output matches the oracle (one shared scratch would mix their scores)."""
+    data = []
+    for i, (heads, kv_heads, t0) in enumerate(((16, 8, 250), (16, 8, 170))):
+        q, kc, vdev, vval, nk = layer(700 + i, heads, kv_heads, 128, 1, t0, False, False)
+        want = oracle_attention(q, kc, vval, heads, kv_heads, 128, t0 + 1, OUT_FP32, None)[0]
+        dev = [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (q, kc, vdev)]
+        data.append((dev, want, heads, kv_heads, t0))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    torch.cuda.synchronize()
+    for rep in range(16):
+        for j in (0, 1):
+            (q, kc, v), _, heads, kv_heads, t0 = data[j]
+            with torch.cuda.stream(streams[j]):
+                att = torch.empty((1, heads * 128), dtype=torch.float32, device="cuda")
+                ops.attention(q, kc, v, heads, kv_heads, causal_k=t0 + 1, att=att)
+                outs[j].append(att)
+    torch.cuda.synchronize()
+    for j in (0, 1):
+        for rep, att in enumerate(outs[j]):
+            assert np.array_equal(bits(att.cpu().numpy()), bits(data[j][1])), f"stream {j}, call {rep}"
+
+
 def test_attention_refusals():
     q = torch.zeros((1, 256), device="cuda")
     kc = torch.zeros((32, 128), device="cuda")

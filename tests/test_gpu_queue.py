@@ -1076,6 +1076,35 @@ def test_attention_plan_replays_with_new_cache_data():
         assert bytes(g.ddr) == bytes(o.ddr), f"replay {rep}: first differing byte at {first_diff(bytes(g.ddr), bytes(o.ddr)):#x}"
 
 
+@pytest.mark.parametrize("graphs", [False, True])
+def test_attention_queues_on_two_streams_at_once(graphs):
+    """Two images' attention queues run on two streams at once, op by op (each stream's own scores
+    scratch) or as launch plans (each plan's own): both images end as the oracle's."""
+    progs = [attention_program(21 + i, 16, 8, 128, 1, 250 - 80 * i, False) for i in range(2)]
+    imgs = [p.image() for p in progs]
+    want = []
+    for p, img in zip(progs, imgs):
+        o = Q.Machine(bytearray(img))
+        assert o.run_queue(ATT_QADDR, len(p.descs)).done
+        want.append(bytes(o.ddr))
+    descs = [bytes(img[ATT_QADDR:ATT_QADDR + 64 * len(p.descs)]) for p, img in zip(progs, imgs)]
+    prev = NQ.set_graphs(graphs)
+    try:
+        ms = [NQ.Machine(img) for img in imgs]
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        torch.cuda.synchronize()
+        for rep in range(8):
+            for j in (0, 1):
+                with torch.cuda.stream(streams[j]):
+                    assert ms[j].run_queue(ATT_QADDR, len(progs[j].descs), descs[j]).done
+        torch.cuda.synchronize()
+        for j in (0, 1):
+            got = bytes(ms[j].ddr)
+            assert got == want[j], f"image {j}: first differing byte at {first_diff(got, want[j]):#x}"
+    finally:
+        NQ.set_graphs(prev)
+
+
 def decode_step_image(seed: int, **shape):
     """A whole decode step of a small Qwen3-style model (bench.DecodeQueue, the reference's lowering
     of one token: tars_mini/llm.py:614-640, 705-767) in a host image with seeded data."""
