@@ -12,11 +12,10 @@
 //    MFMA operand registers, and the int32 partial tiles meet in LDS for the golden fp32 epilogue
 //    (or, for a K split, the per-block epilogue and the in-order fp32 adds across blocks). Used for
 //    chunk rows (M <= 16) and for K blocks that are not a whole number of stages.
-//  * mfma_staged_kernel<BM, BN, WM, WN, KS, S>: prompt rows. The tile's A and W rows are staged
-//    in LDS by direct global -> LDS loads in a ring of S stages of KS bytes of K, every wave of
-//    the workgroup reading the shared operands from LDS (64 x 64 tiles cut the L2 -> CU operand
-//    traffic to half that of 32 x 32 tiles); each wave owns whole 16 x 16 output tiles over the
-//    full K, so there is no cross-wave reduction.
+//  * mfma_tile_kernel<BM, BN, WM, WN, KS, S>: prompt rows. The tile's A and W rows are staged
+//    in LDS by direct global -> LDS loads of 4 rows x 256 bytes in a ring of S stages of KS bytes
+//    of K, every wave of the workgroup reading the shared operands from LDS; each wave owns whole
+//    16 x 16 output tiles over the full K, so there is no cross-wave reduction.
 //
 // Roofline: at M = 4 HBM (every weight byte read once); at M = 256 the int32 MFMA work is small
 // (1.6 GOP) and the kernels are bound by operand traffic from L2 into the CUs and by the fixed
@@ -236,25 +235,45 @@ hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// ------------------------------------------------------------------------------------ staged
+// ------------------------------------------------------------------------------------ tiles
 // Prompt-row tiles with the operands staged in LDS by direct global -> LDS loads
 // (global_load_lds_dwordx4: 64 lanes x 16 bytes land in a 1 KiB LDS block in lane order, with no
 // VGPR round trip, so a wave keeps several stages of loads in flight at no register cost).
 //
-// LDS layout of one stage (KS bytes of K): 1 KiB blocks (g, kb), g over the 16-row groups of the
-// tile's BM A rows then its BN W rows, kb over the stage's 64-byte k blocks. Lane l's 16 bytes in
-// a block are row 16 g + l % 16, bytes 64 kb + 16 (l / 16) .. + 15, at offset 16 l: exactly the
-// MFMA operand a lane supplies, so the MFMA reads are one contiguous ds_read_b128 per wave and
-// A and W share the byte -> (instruction, lane) map.
+// Each 1 KiB load covers 4 rows x 256 contiguous bytes of K (16 lanes per row). Measured on
+// MI355X, a tile streams from L2 into LDS twice as fast that way as with loads of 16 rows x 64
+// bytes (each load then touches 4 rows' cache lines instead of 16). A stage holds KS bytes of K
+// of the tile's BM A rows and BN W rows: per 16-row group, KS / 256 blocks of 16 rows x 256 bytes,
+// row r of a block at byte 256 r and its 16-byte chunk c in slot c ^ r (the lane that fills slot
+// s of row r reads chunk s ^ r). An MFMA operand read takes one chunk of each of 16 rows; with the
+// swizzle the 16 chunks sit in 16 distinct slots, so a ds_read_b128 covers every bank once.
 //
 // S stage slots form a ring: stage st + S - 1 is issued into the slot of stage st - 1 (free since
 // the barrier that ended st - 1), then each wave waits until only its later stages' loads are
-// outstanding (vmcnt counts this wave's own loads), a barrier makes every wave's loads of stage st
-// visible, and the waves run its MFMAs. WM x WN waves each own TI x TJ 16 x 16 output tiles over
-// the full K, so the int32 sums need no reduction; the epilogue runs in MFMA layout (D transposed:
-// W is the MFMA's first operand, so lane l holds 4 consecutive columns of row l % 16) with a 4-wide
-// store. K blocks (a K split) run one after another through the same pipeline, their fp32
-// partials added in block order.
+// outstanding (vmcnt counts this wave's own loads, in issue order), a barrier makes every wave's
+// loads of stage st visible, and the waves run its MFMAs. WM x WN waves each own TI x TJ 16 x 16
+// output tiles over the full K, so the int32 sums need no reduction. K blocks (a K split) run one
+// after another through the same ring, their fp32 partials added in block order.
+//
+// Latency: the fields the first loads need are the leading scalar kernel arguments (preloaded
+// into SGPRs at wave launch, so no kernel-argument round trip precedes the first loads); the
+// epilogue operands are loaded before the first stage (loads complete in issue order, so a load
+// issued after a stage's would also have to land before the wait for that stage returns). The
+// output tile goes through LDS (the ring is free after the last stage) and is stored row by row,
+// consecutive threads writing consecutive 16-byte pieces of a row.
+
+// The fields of a tile launch that its first loads do not need: the later blocks of a K split
+// and the general epilogue.
+struct TileTail {
+  const int8_t* W[kMaxBlocks];
+  int K[kMaxBlocks];
+  int koff[kMaxBlocks];
+  int nseg;
+  const float* bias;
+  int scol_per_tensor, act, out;
+  float out_scale;
+};
+
 // Stage st of this wave's L blocks into its ring slot (st % S).
 template <int L, int NW, int KS, int S>
 __device__ __forceinline__ void issue_stage(int8_t* lds, const int8_t* const (&src)[L], int wave, int st) {
@@ -263,62 +282,72 @@ __device__ __forceinline__ void issue_stage(int8_t* lds, const int8_t* const (&s
   for (int u = 0; u < L; ++u) stage16(src[u] + static_cast<int64_t>(KS) * st, slot + 1024 * (wave + u * NW));
 }
 
-template <int BM, int BN, int WM, int WN, int KS, int S, bool SIMPLE>
-__global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
-  constexpr int NW = WM * WN, TI = BM / 16 / WM, TJ = BN / 16 / WN, GA = BM / 16, G = (BM + BN) / 16;
-  constexpr int KBS = KS / 64, BLK = G * KBS, L = BLK / NW, SLOT = 1024 * BLK;
-  static_assert(TI >= 1 && TJ >= 1 && BLK % NW == 0 && L * (S - 1) < 64, "stage shape");
-  extern __shared__ __align__(16) int8_t lds[];  // [S][BLK] 1 KiB blocks
-  // every kernel argument the first stages need (with the grid size), in one scalar round trip
-  __asm__ volatile("" : : "s"(a.A), "s"(a.lda), "s"(a.nseg), "s"(a.seg[0].W), "s"(a.seg[0].K), "s"(a.seg[0].koff),
-                   "s"(a.M), "s"(a.N), "s"(a.epi.scol), "s"(a.epi.srow), "s"(a.epi.bias), "s"(a.epi.scol_per_tensor),
-                   "s"(gridDim.x), "s"(gridDim.y));
+template <int BM, int BN, int WM, int WN, int KS, int S, bool SIMPLE, bool KSPLIT>
+__global__ __launch_bounds__(64 * WM * WN) void mfma_tile_kernel(const int8_t* A, const int8_t* W, const float* scol,
+                                                                 const float* srow, int lda, int K, int M, int N, int mt,
+                                                                 int ldy, void* Y, TileTail tl) {
+  constexpr int NW = WM * WN, NT = 64 * NW, TI = BM / 16 / WM, TJ = BN / 16 / WN, GA = BM / 16, G = (BM + BN) / 16;
+  constexpr int KQ = KS / 256, BLK = G * KQ * 4, L = BLK / NW, SLOT = 1024 * BLK;
+  constexpr int TP = BN + 4;  // output tile pitch in LDS (floats; rows land on distinct banks)
+  static_assert(TI >= 1 && TJ >= 1 && KS % 256 == 0 && BLK % NW == 0 && L * (S - 1) < 64, "stage shape");
+  static_assert(BM * TP * 4 <= S * SLOT, "the output tile reuses the stage ring");
+  __shared__ __align__(16) int8_t lds[S * SLOT];
   const v4i zero = {0, 0, 0, 0};
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane & 15, lg = lane >> 4;
-  const int mt = gridDim.y, G8 = gridDim.x * gridDim.y;
-  const int b = blockIdx.y * gridDim.x + blockIdx.x;
-  const int t = (G8 % 8 == 0) ? (b % 8) * (G8 / 8) + b / 8 : b;  // XCD-contiguous tiles, as above
+  // Tile order: the hardware deals workgroup ids round-robin over the 8 XCDs (id % 8). With the
+  // grid a multiple of 8, XCD x gets the contiguous tile range [x * G8 / 8, (x + 1) * G8 / 8), M
+  // tiles fastest, so each XCD's L2 holds 1/8 of the weight rows instead of all of them.
+  const int G8 = mt * ((N + BN - 1) / BN);
+  const int b = blockIdx.x;
+  const int t = (G8 % 8 == 0) ? (b % 8) * (G8 / 8) + b / 8 : b;
   const int m0 = (t % mt) * BM, n0 = (t / mt) * BN;
 
   // Epilogue operands of this lane's outputs: rows (wm TI + i) 16 + li, columns
-  // (wn TJ + j) 16 + 4 lg + v; loaded once the first stages are in flight.
+  // (wn TJ + j) 16 + 4 lg + v. Every load is unconditional (an absent operand reads scol).
   float sr[TI], sc[TJ][4], bi[TJ][4], chain[TI][TJ][4];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int n = min(n0 + (wn * TJ + j) * 16 + 4 * lg + v, N - 1);
+      if constexpr (SIMPLE) {
+        sc[j][v] = scol[n];
+      } else {
+        sc[j][v] = scol[tl.scol_per_tensor ? 0 : n];
+        bi[j][v] = *(tl.bias ? tl.bias + n : scol);
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < TI; ++i) sr[i] = *(srow ? srow + min(m0 + (wm * TI + i) * 16 + li, M - 1) : scol);
+  issue_fence();
 
-  for (int sgi = 0; sgi < a.nseg; ++sgi) {
-    const Seg sg = sgi == 0 ? a.seg[0] : a.seg[sgi];  // the first block's fields are already loaded
-    const int NS = sg.K / KS;
+  const int nseg = KSPLIT ? tl.nseg : 1;
+  for (int sgi = 0; sgi < nseg; ++sgi) {
+    const int8_t* Wg = (KSPLIT && sgi) ? tl.W[sgi] : W;
+    const int Kg = (KSPLIT && sgi) ? tl.K[sgi] : K;
+    const int ko = (KSPLIT && sgi) ? tl.koff[sgi] : 0;
+    const int NS = Kg / KS;
     // This lane's source of each block it loads. A row past the matrix is clamped to the last
     // row: it feeds only outputs that are not stored.
     const int8_t* src[L];
 #pragma unroll
     for (int u = 0; u < L; ++u) {
-      const int blk = wave + u * NW, g = blk / KBS, kb = blk % KBS;
+      const int i = wave + u * NW, quad = i & 3, kq = (i >> 2) % KQ, g = (i >> 2) / KQ;
+      const int r = 4 * quad + lg, chunk = li ^ r;
       if (g < GA) {
-        const int r = min(m0 + 16 * g + li, a.M - 1);
-        src[u] = a.A + static_cast<int64_t>(r) * a.lda + sg.koff + 64 * kb + 16 * lg;
+        const int row = min(m0 + 16 * g + r, M - 1);
+        src[u] = A + static_cast<int64_t>(row) * lda + ko + 256 * kq + 16 * chunk;
       } else {
-        const int r = min(n0 + 16 * (g - GA) + li, a.N - 1);
-        src[u] = sg.W + static_cast<int64_t>(r) * sg.K + 64 * kb + 16 * lg;
+        const int row = min(n0 + 16 * (g - GA) + r, N - 1);
+        src[u] = Wg + static_cast<int64_t>(row) * Kg + 256 * kq + 16 * chunk;
       }
     }
 #pragma unroll
     for (int st = 0; st < S - 1; ++st)
       if (st < NS) issue_stage<L, NW, KS, S>(lds, src, wave, st);
-    if (sgi == 0) {
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int n = min(n0 + (wn * TJ + j) * 16 + 4 * lg + v, a.N - 1);
-          sc[j][v] = a.epi.load_scol(n);
-          bi[j][v] = a.epi.load_bias(n);
-        }
-#pragma unroll
-      for (int i = 0; i < TI; ++i) sr[i] = a.epi.load_srow(min(m0 + (wm * TI + i) * 16 + li, a.M - 1));
-    }
     v4i acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -329,26 +358,18 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
         issue_stage<L, NW, KS, S>(lds, src, wave, st + S - 1);
         wait_vmcnt<L * (S - 1)>();
       } else {
-        const int ahead = NS - 1 - st;  // stages issued after st (fewer than S - 1)
-        if constexpr (S >= 4) {
-          if (ahead == 2) wait_vmcnt<2 * L>();
-        }
-        if constexpr (S >= 3) {
-          if (ahead == 1) wait_vmcnt<L>();
-        }
-        static_assert(S <= 4, "waits above cover at most 2 stages ahead");
-        if (ahead == 0) wait_vmcnt<0>();
+        wait_stages_ahead<L, S - 2>(NS - 1 - st);  // fewer than S - 1 stages were issued after st
       }
       __builtin_amdgcn_s_barrier();
-      const int8_t* slot = lds + SLOT * (st % S) + 16 * lane;
+      const int8_t* slot = lds + SLOT * (st % S) + 256 * li;
 #pragma unroll
-      for (int kb = 0; kb < KBS; ++kb) {
+      for (int kb = 0; kb < KS / 64; ++kb) {
+        const int off = 4096 * (kb / 4) + 16 * ((4 * (kb % 4) + lg) ^ li);
         v4i fa[TI], fw[TJ];
 #pragma unroll
-        for (int i = 0; i < TI; ++i) fa[i] = *reinterpret_cast<const v4i*>(slot + 1024 * (KBS * (wm * TI + i) + kb));
+        for (int i = 0; i < TI; ++i) fa[i] = *reinterpret_cast<const v4i*>(slot + 4096 * KQ * (wm * TI + i) + off);
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          fw[j] = *reinterpret_cast<const v4i*>(slot + 1024 * (KBS * (GA + wn * TJ + j) + kb));
+        for (int j = 0; j < TJ; ++j) fw[j] = *reinterpret_cast<const v4i*>(slot + 4096 * KQ * (GA + wn * TJ + j) + off);
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -357,69 +378,123 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_staged_kernel(MfmaArgs a) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot are done
       __builtin_amdgcn_s_barrier();        // ... and every wave's, before the slot is refilled
     }
+    // W is the MFMA's first operand, so lane l holds columns 4 lg .. 4 lg + 3 of row li
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float y = SIMPLE ? fmul(fmul(i2f(acc[i][j][v]), sr[i]), sc[j][v])
-                                 : a.epi.apply(acc[i][j][v], sr[i], a.epi.srow != nullptr, sc[j][v], bi[j][v]);
+          float y;
+          if constexpr (SIMPLE) {
+            y = fmul(fmul(i2f(acc[i][j][v]), sr[i]), sc[j][v]);
+          } else {
+            y = i2f(acc[i][j][v]);
+            if (srow) y = fmul(y, sr[i]);
+            y = fmul(y, sc[j][v]);
+            if (tl.bias) y = fadd(y, bi[j][v]);
+            y = act_fn(y, tl.act);
+          }
           chain[i][j][v] = sgi == 0 ? y : fadd(chain[i][j][v], y);
         }
   }
+  // The output tile through LDS (every wave passed the last stage's barrier, so the ring is free),
+  // then stored row by row.
+  float* tile = reinterpret_cast<float*>(lds);
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int m = m0 + (wm * TI + i) * 16 + li, n = n0 + (wn * TJ + j) * 16 + 4 * lg;
-      if (m < a.M && n < a.N) {
-        if constexpr (SIMPLE) {
-          *reinterpret_cast<float4*>(static_cast<char*>(a.Y) + m * a.ldy + 4 * n) =
-              make_float4(ftz(chain[i][j][0]), ftz(chain[i][j][1]), ftz(chain[i][j][2]), ftz(chain[i][j][3]));
-        } else {
-          store_out4(a.Y, m * a.ldy, n, a.epi.out, chain[i][j], a.epi.out_scale);
-        }
+    for (int j = 0; j < TJ; ++j)
+      *reinterpret_cast<float4*>(tile + ((wm * TI + i) * 16 + li) * TP + (wn * TJ + j) * 16 + 4 * lg) =
+          make_float4(chain[i][j][0], chain[i][j][1], chain[i][j][2], chain[i][j][3]);
+  __syncthreads();
+  constexpr int CH = BM * BN / 4, PER = (CH + NT - 1) / NT;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int c = static_cast<int>(threadIdx.x) + p * NT;
+    const int row = c / (BN / 4), cq = c % (BN / 4);
+    const int m = m0 + row, n = n0 + 4 * cq;
+    if ((CH % NT == 0 || c < CH) && m < M && n < N) {
+      const float4 v = *reinterpret_cast<const float4*>(tile + row * TP + 4 * cq);
+      if constexpr (SIMPLE) {
+        *reinterpret_cast<float4*>(static_cast<char*>(Y) + static_cast<int64_t>(m) * ldy + 4 * n) =
+            make_float4(ftz(v.x), ftz(v.y), ftz(v.z), ftz(v.w));
+      } else {
+        const float y4[4] = {v.x, v.y, v.z, v.w};
+        store_out4(Y, static_cast<int64_t>(m) * ldy, n, tl.out, y4, tl.out_scale);
       }
     }
+  }
 }
 
 template <int BM, int BN, int WM, int WN, int KS, int S>
-hipError_t go_staged(const MfmaArgs& a, hipStream_t s) {
-  constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * KS;
-  static_assert(lds <= 65536, "stage ring exceeds 64 KiB of LDS");
-  const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
+  static_assert(static_cast<size_t>(S) * (BM + BN) * KS <= 163840, "stage ring exceeds 160 KiB of LDS");
+  const int mt = (a.M + BM - 1) / BM, nt = (a.N + BN - 1) / BN;
+  TileTail tl{};
+  for (int i = 0; i < a.nseg; ++i) {
+    tl.W[i] = a.seg[i].W;
+    tl.K[i] = a.seg[i].K;
+    tl.koff[i] = a.seg[i].koff;
+  }
+  tl.nseg = a.nseg;
+  tl.bias = a.epi.bias;
+  tl.scol_per_tensor = a.epi.scol_per_tensor;
+  tl.act = a.epi.act;
+  tl.out = a.epi.out;
+  tl.out_scale = a.epi.out_scale;
   // QM_ROWCOL with fp32 output and neither bias nor activation (every K split): the general
   // epilogue's code compiled out, as in the GEMV kernels
   const RowColEpilogue& e = a.epi;
-  if (e.srow && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0)
-    hipLaunchKernelGGL((mfma_staged_kernel<BM, BN, WM, WN, KS, S, true>), grid, dim3(64 * WM * WN), lds, s, a);
-  else
-    hipLaunchKernelGGL((mfma_staged_kernel<BM, BN, WM, WN, KS, S, false>), grid, dim3(64 * WM * WN), lds, s, a);
+  const bool simple = e.srow && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0;
+  const int8_t* A = a.A + a.seg[0].koff;
+  const int lda = static_cast<int>(a.lda), ldy = static_cast<int>(a.ldy);
+  const dim3 grid(mt * nt), block(64 * WM * WN);
+#define TARS_TILE(SIMPLE, KSPLIT)                                                                                      \
+  hipLaunchKernelGGL((mfma_tile_kernel<BM, BN, WM, WN, KS, S, SIMPLE, KSPLIT>), grid, block, 0, s, A, a.seg[0].W,      \
+                     e.scol, e.srow, lda, a.seg[0].K, a.M, a.N, mt, ldy, a.Y, tl)
+  if (a.nseg > 1) {
+    if (simple) TARS_TILE(true, true);
+    else TARS_TILE(false, true);
+  } else {
+    if (simple) TARS_TILE(true, false);
+    else TARS_TILE(false, false);
+  }
+#undef TARS_TILE
   return hipGetLastError();
 }
 
 // ------------------------------------------------------------------------------------ dispatch
 // Chunk rows (M <= 16): the direct kernel with one 16-column tile per workgroup and 8 waves over
 // K (the weights have no reuse, so the most workgroups and the most weight bytes in flight).
-// Prompt rows: the staged kernel when every K block is a whole number of stages -- 64 x 64 tiles
-// (16 waves, 128-byte stages, 4 slots) once they alone give about 192 or more workgroups, else
-// 32 x 32 tiles (4 waves, 256-byte stages, 3 slots) -- and the direct kernel's 32 x 32 tiles with
-// 4 waves over K otherwise. Measured on MI355X with the weights cold (rotated over 384 MiB):
-// M=256 K=1024 N=3072 10.7 -> 8.0 us, M=256 K=3072 N=1024 10.6 -> 9.1 us,
-// M=1024 K=1024 N=3072 28.9 -> 17.6 us, M=64 K=1024 N=3072 6.8 -> 5.6 us, bit-identical.
+// Prompt rows, when every K block is a whole number of stages (K a multiple of 256): the LDS tile
+// kernel, its tile chosen by measurement on MI355X with the weights cold, bit-identical across
+// tiles; the direct kernel's 32 x 32 tiles with 4 waves over K otherwise.
+//  * 64 x 48 tiles (4 waves of 16 x 48, 256-byte stages, 3 slots) when they give one to 1.25
+//    workgroups per CU: M=256 K=1024 N=3072 7.5 -> 5.5 us (the 64 x 64 / 16-row-load tiles before);
+//  * 64 x 64 tiles (4 waves of 32 x 32, 256-byte stages, 3 slots) when they give 512 or more:
+//    M=1024 K=1024 N=3072 16.5 -> 15.8 us;
+//  * 32 x 32 tiles (4 waves of 16 x 16) with 1024-byte stages in 2 slots when K is a multiple of
+//    1024 and they give at most 1.25 workgroups per CU: M=256 K=3072 N=1024 8.6 -> 5.9 us;
+//  * 32 x 32 tiles with 256-byte stages in 3 slots otherwise: M=64 K=1024 N=3072 5.2 -> 3.8 us.
 bool whole_stages(const MfmaArgs& a, int ks) {
   for (int i = 0; i < a.nseg; ++i)
     if (a.seg[i].K % ks) return false;
   return true;
 }
 
+int64_t tiles(const MfmaArgs& a, int bm, int bn) {
+  return static_cast<int64_t>((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
+}
+
 hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
-  const int64_t tiles64 = static_cast<int64_t>((a.M + 63) / 64) * ((a.N + 63) / 64);
-  if (tiles64 >= 192 && whole_stages(a, 128)) return go_staged<64, 64, 4, 4, 128, 4>(a, s);
-  if (whole_stages(a, 256)) return go_staged<32, 32, 2, 2, 256, 3>(a, s);
-  return go_direct<2, 2, 4, 1>(a, s);
+  if (!whole_stages(a, 256)) return go_direct<2, 2, 4, 1>(a, s);
+  const int64_t t48 = tiles(a, 64, 48), t32 = tiles(a, 32, 32);
+  if (t48 >= 192 && t48 <= 320) return go_tile<64, 48, 4, 1, 256, 3>(a, s);
+  if (tiles(a, 64, 64) >= 512) return go_tile<64, 64, 2, 2, 256, 3>(a, s);
+  if (t32 <= 320 && whole_stages(a, 1024)) return go_tile<32, 32, 2, 2, 1024, 2>(a, s);
+  return go_tile<32, 32, 2, 2, 256, 3>(a, s);
 }
 
 }  // namespace

@@ -270,12 +270,12 @@ def test_ksplit_gemv_block_shapes(split, M):
     assert same(host(y), want), mismatch(host(y), want)
 
 
-@pytest.mark.parametrize("M,N,blocks", [(17, 208, [4096, 2816]), (45, 208, [4096, 2816]), (200, 3072, [256, 384]),
-                                          (33, 96, [1040, 256])])
+@pytest.mark.parametrize("M,N,blocks", [(17, 208, [4096, 2816]), (45, 208, [4096, 2816]), (200, 3072, [256, 512]),
+                                          (100, 1040, [2048, 1024]), (33, 96, [1040, 256])])
 def test_ksplit_staged_prompt_tiles(M, N, blocks):
-    """The K split on the LDS-staged prompt tiles: 32 x 32 tiles with 256-byte stages, 64 x 64
-    tiles with 128-byte stages (M=200, N=3072), and a block that is not a whole number of stages
-    (1040), which takes the direct tiles."""
+    """The K split on the LDS tile kernel: 32 x 32 tiles with 256-byte stages (M=17, 45), 64 x 48
+    tiles (M=200, N=3072), 32 x 32 tiles with 1024-byte stages (M=100, N=1040, blocks of whole
+    KiB), and a block that is not a whole number of stages (1040), which takes the direct tiles."""
     x, q, s, W, scol, _ = w8_inputs(M * 31 + N, M, N, sum(blocks))
     parts = np.split(W, np.cumsum(blocks)[:-1], axis=1)
     parts = [np.ascontiguousarray(b) for b in parts]
@@ -320,17 +320,37 @@ def test_epilogue_matrix_prompt_tiles(qm, act, out):
 @pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
 @pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
                                      (ACT_GELU, OUT_FP32), (ACT_SOFTPLUS, OUT_BF16)])
-@pytest.mark.parametrize("M,N", [(45, 80), (200, 3072 + 16)])
-def test_epilogue_matrix_staged_tiles(qm, act, out, M, N):
-    """The LDS-staged prompt tiles (K a multiple of 256: 32 x 32 tiles at N=80, 64 x 64 tiles at
-    N=3088) through every scale mode and output format with a bias, ragged last row and column
-    tiles, a huge scale and int8 -128."""
-    rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, M, N, "staged")).encode()))
-    K = 256 * int(rng.integers(1, 5))
+@pytest.mark.parametrize("M,N,K", [(45, 80, 768), (45, 80, 2048), (200, 3072 + 16, 512)])
+def test_epilogue_matrix_staged_tiles(qm, act, out, M, N, K):
+    """The LDS tile kernel (K a multiple of 256) through every scale mode and output format with a
+    bias, ragged last row and column tiles, a huge scale and int8 -128: 32 x 32 tiles with
+    256-byte stages (K=768), with 1024-byte stages (K=2048), and 64 x 48 tiles (M=200, N=3088)."""
+    rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, M, N, K, "staged")).encode()))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
     sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
     sc[N // 3] = 3e30
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32)
+    osc = f32(5.0) if out == OUT_INT8 else None
+    y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc), cuda(b),
+                        act=act, out=out, out_scale=osc)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("qm,act,out", [("rowcol", ACT_NONE, OUT_FP32), ("channel", ACT_SILU, OUT_BF16),
+                                        ("tensor", ACT_RELU, OUT_INT8)])
+def test_large_prompt_tiles(qm, act, out):
+    """The 64 x 64 tiles the tile kernel takes when they give 512 or more workgroups (M=1040,
+    N=2064: ragged last row and column tiles) through three scale modes and output formats."""
+    rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, "large")).encode()))
+    M, N, K = 1040, 2064, 256
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
     if qm == "tensor":
         sc = sc[:1]
     srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
