@@ -12,8 +12,12 @@ and replayed; `value` = algorithmic HBM bytes of the step / step time.
 Also reported: each single-GPU workload of the path ("configs": Qwen3-0.6B decode shapes, the
 lm_head, the K-split projections, M = 4 / 256 prefill, W4A16 group-128) as us/call, GB/s and
 roofline fraction (and TOPS for the prefill GEMM), each rotated over >= 512 MiB of distinct weight
-copies so the 256 MB MALL cannot serve it; per-kernel durations from HIP events around each launch
-of the decode step; the same decode step as a 313-descriptor queue through the library's queue
+copies so the 256 MB MALL cannot serve it, each with the numpy oracle's golden path timed on one
+core on the inputs of its first copy and checked bit for bit against the GPU's output; per row of
+the decode step (kernel instance and role: q/k/v, o, gate/up, down, head) the dispatch durations
+from the dispatches' own start and end timestamps (the roofline row is the one with the most
+dispatch time per step), beside the time each launch adds to a dependent chain of graph launches;
+the same decode step as a 313-descriptor queue through the library's queue
 executor ("queue_executor", host clock, end to end); a whole Qwen3-0.6B decode step at position 250
 (norms, quantizers, every linear, q/k norms, RoPE, the attention, residual adds, SiLU * up and the
 head: 1910 descriptors) through the same executor ("queue_whole_decode_step_t250"); and the CPU
@@ -77,6 +81,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--pmc-step-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "DETAIL"),
                     help="write the decode step's per-instance traffic from two rocprofv3 passes and exit")
     ap.add_argument("--pmc-step-out", type=str, default=str(ROOT / "profiles" / "decode_step_traffic.json"))
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "DETAIL"),
+                    help="summarize a rocprofv3 --kernel-trace run of the decode step per row (kernel, grid)")
+    ap.add_argument("--trace-out", type=str, default=str(ROOT / "profiles" / "decode_step_kernels.json"))
     return ap.parse_args()
 
 
@@ -576,6 +583,30 @@ def kernel_instance(l: Launch) -> str:
     return f"{name}<64, {cpl}, {u}{tail}>"
 
 
+def role(l: Launch) -> str:
+    """The projection group a decode-step launch serves, the layer index dropped: qkv, o, gate_up,
+    down or head."""
+    return l.name.split(".", 1)[1] if l.name.startswith("L") and "." in l.name else l.name
+
+
+def fused_grid_items(l: Launch) -> int:
+    """Work-items of a fused quantizer + GEMV dispatch (rocprofv3's grid size): matrices of unequal
+    height cut into pieces of their greatest common height, one 256-thread workgroup per 4 U rows
+    of a piece (mirrors go_fused in gemv_w8a8.hip for whole-wave rows and no row pairs)."""
+    import math
+    ns = [d.N for d in l.operands["descs"]]
+    h = 0
+    for n in ns:
+        h = math.gcd(h, n)
+    u = fused_rows_per_wave(sum(ns), l.args[6])
+    return -(-h // (4 * u)) * (sum(ns) // h) * 256
+
+
+def row_key(l: Launch) -> str:
+    """A decode-step launch's kernel instance and role, as the measurement rows name them."""
+    return f"{kernel_instance(l)} @ {role(l)}"
+
+
 def replay_fixed_s(torch, lib, busy_graph, reps: int = 10) -> float:
     """The fixed cost of one graph replay as instance_times times it (events around a single replay
     queued behind other work): graphs of 1 and of 29 tiny launches (a 16-element quant_rows) timed
@@ -601,16 +632,15 @@ def replay_fixed_s(torch, lib, busy_graph, reps: int = 10) -> float:
 
 
 def instance_times(torch, step_graph, launches, fixed_s: float, reps: int = 5) -> dict:
-    """Average launch duration of every kernel instance in the step: HIP events around a graph of
-    that instance's launches from the step (same buffers, step order), less one graph replay's fixed
-    cost (fixed_s, replay_fixed_s), i.e. the time each launch adds to a dependent chain. Before each
-    timed replay the full step and then the largest other instance are replayed, so at least ~300
-    MB (more than the 256 MB MALL) stream between two uses of any weight and every timed launch
-    starts cold. (Events around one launch at a time cannot time it: the event packets alone add
-    several microseconds.)"""
+    """The time each launch adds to a dependent chain of graph launches, per kernel instance and
+    role (row_key): HIP events around a graph of that row's launches from the step (same buffers,
+    step order), less one graph replay's fixed cost (fixed_s, replay_fixed_s), launch gaps
+    included. Before each timed replay the full step and then the largest other row are replayed,
+    so at least ~300 MB (more than the 256 MB MALL) stream between two uses of any weight and every
+    timed launch starts cold."""
     fams = {}
     for l in launches:
-        fams.setdefault(kernel_instance(l), []).append(l)
+        fams.setdefault(row_key(l), []).append(l)
     graphs = {name: capture(torch, ls) for name, ls in fams.items()}
     size = {name: sum(l.nbytes for l in ls) for name, ls in fams.items()}
     out = {}
@@ -636,6 +666,56 @@ def instance_times(torch, step_graph, launches, fixed_s: float, reps: int = 5) -
                      "GBps": round(size[name] / (avg_s * len(ls)) / 1e9, 1),
                      "hbm_frac": round(size[name] / (avg_s * len(ls)) / HBM_PEAK, 4)}
     del graphs
+    return out
+
+
+def dispatch_times(torch, lib, launches, steps: int = 4) -> dict:
+    """Kernel duration of every decode-step launch from its dispatch's own start and end timestamps
+    (tars_time_next_launch: HIP events that the dispatch records, on the stream it runs on; the
+    same timestamps rocprofv3's kernel trace reads), over `steps` passes of the step's launches in
+    model order after two untimed passes. Each pass streams all 601 MB of weights (above the 256 MB
+    MALL), so every dispatch reads its weights cold. Per row (kernel instance and role): dispatches
+    timed, mean and median microseconds per dispatch, the work-items of the dispatch, algorithmic
+    bytes per launch and the HBM fraction they give."""
+    import statistics
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(len(launches) * steps)]
+    for a, b in ev:  # the events exist once recorded
+        a.record()
+        b.record()
+    for _ in range(2):
+        for l in launches:
+            l(stream.cuda_stream)
+    torch.cuda.synchronize()
+    k = 0
+    for _ in range(steps):
+        for l in launches:
+            a, b = ev[k]
+            k += 1
+            lib.tars_time_next_launch(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event))
+            l(stream.cuda_stream)
+    torch.cuda.synchronize()
+    rows, k = {}, 0
+    for _ in range(steps):
+        for l in launches:
+            a, b = ev[k]
+            k += 1
+            r = rows.setdefault(row_key(l), {"us": [], "bytes": l.nbytes, "n_per_step": 0, "l": l})
+            r["us"].append(a.elapsed_time(b) * 1e3)
+    for l in launches:
+        rows[row_key(l)]["n_per_step"] += 1
+    out = {}
+    for key, r in rows.items():
+        avg = sum(r["us"]) / len(r["us"])
+        l = r["l"]
+        out[key] = {"kernel": kernel_instance(l), "role": role(l),
+                    "grid_items": fused_grid_items(l) if l.kind == "quant_gemm_w8a8" else None,
+                    "launches_per_step": r["n_per_step"], "dispatches_timed": len(r["us"]),
+                    "avg_bytes_per_launch": r["bytes"], "avg_us_per_dispatch": round(avg, 3),
+                    "median_us_per_dispatch": round(statistics.median(r["us"]), 3),
+                    "us_per_step": round(avg * r["n_per_step"], 2),
+                    "GBps": round(r["bytes"] / avg / 1e3, 1), "hbm_frac": round(r["bytes"] / avg / 1e3 / (HBM_PEAK / 1e9), 4)}
     return out
 
 
@@ -681,8 +761,8 @@ CONFIG_KERNELS = {
     "c4_prefill_M4_K3072_N1024": ("gemv_w8a8_kernel<64, 3, 1, 4, true>", 65536),
     "c4_prefill_M4_K1024_N3072_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 98304),
     "c4_prefill_M4_K3072_N1024_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 32768),
-    "c4_prefill_M256_K1024_N3072": ("mfma_staged_kernel<64, 64, 4, 4, 128, 4, true>", 196608),
-    "c4_prefill_M256_K3072_N1024": ("mfma_staged_kernel<32, 32, 2, 2, 256, 3, true>", 65536),
+    "c4_prefill_M256_K1024_N3072": ("mfma_tile_kernel<64, 48, 4, 1, 256, 3, true, false>", 65536),
+    "c4_prefill_M256_K3072_N1024": ("mfma_tile_kernel<32, 32, 2, 2, 1024, 2, true, false>", 65536),
     "c5_w4a16_M1_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 1, 1, false, true>", 196608),
     "c5_w4a16_M1_K6144_N1536": ("gemv_w4a16_kernel<8, 1, 1, 3, false, true>", 98304),
     "c5_w4a16_M4_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 2, 1, false, true>", 393216),
@@ -745,34 +825,92 @@ def pmc_summary(csvs: list, detail: str, out: str) -> int:
 
 
 def pmc_step_summary(fetch_csv: str, write_csv: str, detail: str, out: str) -> int:
-    """HBM traffic per launch of each decode-step kernel instance from two profiler passes over the
-    decode step (FETCH_SIZE, then WRITE_SIZE) and the first pass's --detail output (the instances'
-    algorithmic bytes per launch). Byte counters are scaled by what they read for the 1 GiB device
-    copy the bench makes. A kernel instance's dispatches of every grid are pooled: every timed graph
-    holds whole steps' launches of it, so the pool has the step's mix (q/k/v : head = 28 : 1)."""
+    """HBM traffic per launch of each decode-step row (kernel instance and grid, roofline_rows in
+    the first pass's --detail output) from two profiler passes over the decode step (FETCH_SIZE,
+    then WRITE_SIZE). Byte counters are scaled by what they read for the 1 GiB device copy the
+    bench makes."""
     P = [pmc_means(fetch_csv), pmc_means(write_csv)]
-    kernels = json.loads(Path(detail).read_text())["kernels"]
+    rows = json.loads(Path(detail).read_text())["roofline_rows"]
     copy = max((k for k in P[0] if "copyBuffer" in k[0]), key=lambda k: P[0][k]["FETCH_SIZE"])
     fetch_kib, write_kib = P[0][copy]["FETCH_SIZE"], P[1][copy]["WRITE_SIZE"]
     fetch_scale, write_scale = (1 << 30) / (fetch_kib * 1024), (1 << 30) / (write_kib * 1024)
-    inst = {}
-    for name, k in kernels.items():
-        pooled = []
-        for i, c in enumerate(("FETCH_SIZE", "WRITE_SIZE")):
-            hits = [v for key, v in P[i].items() if f"::{name}(" in key[0]]
-            if not hits:
-                raise SystemExit(f"no dispatch of {name} in pass {i}")
-            n = sum(v["dispatches"] for v in hits)
-            pooled.append((n, sum(v[c] * v["dispatches"] for v in hits) / n))
-        rd, wr = pooled[0][1] * 1024 * fetch_scale, pooled[1][1] * 1024 * write_scale
-        inst[name] = {"read_bytes": round(rd), "write_bytes": round(wr), "traffic_bytes": round(rd + wr),
-                      "algorithmic_bytes": k["avg_bytes_per_launch"], "dispatches": pooled[0][0]}
+    res = {}
+    for key, r in rows.items():
+        m = []
+        for i in range(2):
+            hits = [v for k, v in P[i].items() if f"::{r['kernel']}(" in k[0] and k[1] == r["grid_items"]]
+            if len(hits) != 1:
+                raise SystemExit(f"{len(hits)} dispatch groups match {key} (grid {r['grid_items']}) in pass {i}")
+            m.append(hits[0])
+        rd, wr = m[0]["FETCH_SIZE"] * 1024 * fetch_scale, m[1]["WRITE_SIZE"] * 1024 * write_scale
+        res[key] = {"kernel": r["kernel"], "role": r["role"], "grid_items": r["grid_items"],
+                    "read_bytes": round(rd), "write_bytes": round(wr), "traffic_bytes": round(rd + wr),
+                    "algorithmic_bytes": r["avg_bytes_per_launch"],
+                    "traffic_over_algorithmic": round((rd + wr) / r["avg_bytes_per_launch"], 3),
+                    "dispatches": m[0]["dispatches"]}
     Path(out).write_text(json.dumps({
         "about": "HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per "
-                 "dispatch), each scaled by the same counter's reading for a 1 GiB device-to-device copy",
+                 "dispatch), each scaled by the same counter's reading for a 1 GiB device-to-device copy; "
+                 "one row per kernel instance and grid size (the decode step's roles)",
         "fetch_copy_kib": fetch_kib, "write_copy_kib": write_kib, "fetch_scale": fetch_scale,
-        "write_scale": write_scale, "instances": inst}, indent=1))
-    print(f"{len(inst)} instances; FETCH_SIZE x {fetch_scale:.4f}, WRITE_SIZE x {write_scale:.4f}", flush=True)
+        "write_scale": write_scale, "rows": res}, indent=1))
+    print(f"{len(res)} rows; FETCH_SIZE x {fetch_scale:.4f}, WRITE_SIZE x {write_scale:.4f}", flush=True)
+    return 0
+
+
+def trace_grid(row: dict) -> int:
+    """Work-items of a dispatch in a rocprofv3 kernel-trace CSV row."""
+    if "Grid_Size" in row:
+        return int(row["Grid_Size"])
+    return int(row["Grid_Size_X"]) * int(row.get("Grid_Size_Y") or 1) * int(row.get("Grid_Size_Z") or 1)
+
+
+def trace_summary(trace_csv: str, detail: str, out: str) -> int:
+    """Per decode-step row (kernel instance and grid size, roofline_rows in the same run's --detail
+    output), the rocprofv3 kernel trace's dispatch durations (end minus start timestamp): count,
+    mean, median and minimum; the HBM fraction that the mean gives for the row's algorithmic bytes
+    per launch, beside bench.py's own dispatch-timed figure from the same run. Writes out (JSON)
+    and the same name with .md."""
+    import csv
+    import statistics
+    durs = {}
+    with open(trace_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], trace_grid(row))
+            durs.setdefault(key, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    line = json.loads(Path(detail).read_text())
+    rows, roof = line["roofline_rows"], line["roofline"]
+    table = {}
+    for key, r in rows.items():
+        hits = [k for k in durs if f"::{r['kernel']}(" in k[0] and k[1] == r["grid_items"]]
+        if len(hits) != 1:
+            raise SystemExit(f"{len(hits)} dispatch groups match {key} (grid {r['grid_items']})")
+        d = durs[hits[0]]
+        avg = sum(d) / len(d)
+        table[key] = {"kernel": r["kernel"], "role": r["role"], "grid_items": r["grid_items"],
+                      "launches_per_step": r["launches_per_step"], "trace_dispatches": len(d),
+                      "trace_avg_us": round(avg, 3), "trace_median_us": round(statistics.median(d), 3),
+                      "trace_min_us": round(min(d), 3), "algorithmic_bytes": r["avg_bytes_per_launch"],
+                      "hbm_frac_from_trace": round(r["avg_bytes_per_launch"] / avg / 1e3 / (HBM_PEAK / 1e9), 4),
+                      "bench_avg_us_per_dispatch": r["avg_us_per_dispatch"], "bench_hbm_frac": r["hbm_frac"]}
+    dom = next(k for k, r in rows.items() if r["kernel"] == roof["kernel"] and r["avg_us_per_dispatch"] == roof["avg_us_per_dispatch"])
+    summary = {"about": "rocprofv3 --kernel-trace dispatch durations per decode-step row (kernel instance and grid "
+                        "size) against bench.py's own dispatch-timed figures from the same run",
+               "line_roofline": {k: roof[k] for k in ("kernel", "shape", "frac", "avg_us_per_dispatch", "avg_bytes_per_launch")},
+               "roofline_row": dom, "frac_from_trace": table[dom]["hbm_frac_from_trace"],
+               "trace_over_bench_duration": round(table[dom]["trace_avg_us"] / roof["avg_us_per_dispatch"], 4),
+               "rows": table}
+    Path(out).write_text(json.dumps(summary, indent=1))
+    md = [f"| Row (kernel instance @ role) | Work-items | Launches / step | Trace dispatches | Trace mean µs | Trace median µs | "
+          f"Trace min µs | Algorithmic MB / launch | HBM frac (trace mean) | bench.py µs / dispatch | bench.py HBM frac |",
+          "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for key, t in sorted(table.items(), key=lambda kv: -kv[1]["trace_avg_us"] * kv[1]["launches_per_step"]):
+        md.append(f"| `{key}` | {t['grid_items']} | {t['launches_per_step']} | {t['trace_dispatches']} | {t['trace_avg_us']} | "
+                  f"{t['trace_median_us']} | {t['trace_min_us']} | {t['algorithmic_bytes'] / 1e6:.3f} | "
+                  f"{t['hbm_frac_from_trace']} | {t['bench_avg_us_per_dispatch']} | {t['bench_hbm_frac']} |")
+    Path(out).with_suffix(".table.md").write_text("\n".join(md) + "\n")
+    print(json.dumps({k: summary[k] for k in ("line_roofline", "roofline_row", "frac_from_trace", "trace_over_bench_duration")}),
+          flush=True)
     return 0
 
 
@@ -796,8 +934,43 @@ def attach_counters(res: dict) -> None:
                          "source": "profiles/config_traffic.json (rocprofv3 --pmc)"}
 
 
-def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
+def cpu_config_baseline(fn, gpu_out, nbytes: int, ops: int, min_s: float = 0.3) -> dict:
+    """The oracle's golden-path restatement of one config call (fn: numpy, on the host copies of
+    the GPU run's first weight copy and its inputs) on one pinned core: microseconds per call over
+    at least min_s seconds (at least one call), the same algorithmic bytes and ops per second as
+    the GPU figure, and whether its output equals the GPU's for that copy bit for bit."""
+    mask = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {min(mask)})
+    try:
+        want = fn()
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= min_s:
+                break
+    finally:
+        os.sched_setaffinity(0, mask)
+    t = el / calls
+    r = {"us_per_call": round(t * 1e6, 1), "GBps": round(nbytes / t / 1e9, 4), "calls": calls, "cores": 1,
+         "bit_exact_vs_gpu": bool(np.ascontiguousarray(want).tobytes() == np.ascontiguousarray(gpu_out).tobytes())}
+    if ops:
+        r["GOPS"] = round(ops / t / 1e9, 3)
+    return r
+
+
+def config_suite(torch, lib, seed: int, attention: bool = True, cpu: bool = True) -> dict:
     from opentars_amd import ops
+    from oracle import golden as G
+    from oracle import numerics as F
+    host = lambda t: t.cpu().numpy()
+
+    def rerun_first(ls, y):
+        """The GPU output of the rotation's first copy (launched once more after the timing)."""
+        ls[0](torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return host(y)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed + 1)
     res = {}
@@ -815,6 +988,11 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
         ls = rotated(torch, make, N * K)
         r = measure_config(torch, ls)
         r.update(M=M, N=N, K=K)
+        if cpu:
+            W0, sc0 = holds[0]
+            qn, sn, Wn, scn = host(q), host(s), host(W0), host(sc0)
+            r["cpu_baseline"] = cpu_config_baseline(lambda: G.gemm_rowcol(qn, sn, Wn, scn), rerun_first(ls, y),
+                                                    ls[0].nbytes, ls[0].ops)
         del ls, holds
         torch.cuda.empty_cache()
         return r
@@ -831,7 +1009,16 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
         holds.append((W, sc))
         return fused_launch(lib, x, [(W, sc, y)], "head")
     ls = rotated(torch, make_head, QWEN3_VOCAB * 1024)
-    res["lm_head_fused_quant_M1_K1024_N151936"] = dict(measure_config(torch, ls), M=1, N=QWEN3_VOCAB, K=1024)
+    r = dict(measure_config(torch, ls), M=1, N=QWEN3_VOCAB, K=1024)
+    if cpu:
+        W0, sc0 = holds[0]
+        xn, Wn, scn = host(x), host(W0), host(sc0)
+
+        def head_cpu():
+            qn, sn = F.quant_rows(xn)
+            return G.gemm_rowcol(qn, sn, Wn, scn)
+        r["cpu_baseline"] = cpu_config_baseline(head_cpu, rerun_first(ls, y), ls[0].nbytes, ls[0].ops)
+    res["lm_head_fused_quant_M1_K1024_N151936"] = r
     del ls, holds
     torch.cuda.empty_cache()
     for split in ((3456, 3456), (4096, 2816)):
@@ -848,6 +1035,11 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
         ls = rotated(torch, make, 1152 * 6912)
         r = measure_config(torch, ls)
         r.update(M=1, N=1152, K=6912, blocks=list(split))
+        if cpu:
+            bl0, sc0 = holds[0]
+            qn, sn, bln, scn = host(q), host(s), [host(b) for b in bl0], host(sc0)
+            r["cpu_baseline"] = cpu_config_baseline(lambda: G.gemm_rowcol_ksplit(qn, sn, bln, scn),
+                                                    rerun_first(ls, y), ls[0].nbytes, ls[0].ops)
         res[f"c2_gemma3_down_ksplit_{split[0]}+{split[1]}"] = r
         log(f"c2 {split}: {r['us_per_call']} us")
         del ls, holds
@@ -878,6 +1070,11 @@ def config_suite(torch, lib, seed: int, attention: bool = True) -> dict:
         ls = rotated(torch, make, N * K // 2)
         r = measure_config(torch, ls)
         r.update(M=M, N=N, K=K)
+        if cpu and M == 1:
+            Wp0, ws0 = holds[0]
+            xn, Wpn, wsn = host(x), host(Wp0), host(ws0).view(np.uint16)
+            r["cpu_baseline"] = cpu_config_baseline(lambda: G.gemm_w4(xn, Wpn, wsn), rerun_first(ls, y),
+                                                    ls[0].nbytes, ls[0].ops)
         res[f"c5_w4a16_M{M}_K{K}_N{N}"] = r
         log(f"c5 M={M} K={K} N={N}: {r['us_per_call']} us")
         del ls, holds
@@ -1125,6 +1322,8 @@ def main() -> int:
         return pmc_summary(args.pmc_summary[:4], args.pmc_summary[4], args.pmc_out)
     if args.pmc_step_summary:
         return pmc_step_summary(*args.pmc_step_summary, args.pmc_step_out)
+    if args.trace_summary:
+        return trace_summary(*args.trace_summary, args.trace_out)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the matrix path runs on a single GPU here (sharding the "
               "output channels over several GPUs is not implemented); use --gpus 1", file=sys.stderr)
@@ -1147,7 +1346,7 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-        configs = config_suite(torch, lib, args.seed, attention=False)
+        configs = config_suite(torch, lib, args.seed, attention=False, cpu=not args.no_cpu_baseline)
         out = {"configs": configs}
         if args.detail:
             Path(args.detail).write_text(json.dumps(out, indent=1))
@@ -1176,16 +1375,22 @@ def main() -> int:
     t_wall = time.perf_counter() - t_wall
     step_s = e0.elapsed_time(e1) / 1e3 / args.steps
 
-    log(f"step {step_s * 1e6:.1f} us; per-instance timing")
+    log(f"step {step_s * 1e6:.1f} us; per-row timing")
     fixed_s = replay_fixed_s(torch, lib, graph)
     kernels = instance_times(torch, graph, launches, fixed_s)
-    dom_name = max(kernels, key=lambda k: kernels[k]["s_per_step"])
-    dom = kernels[dom_name]
     instances_sum_s = sum(v.pop("s_per_step") for v in kernels.values())
+    rows = dispatch_times(torch, lib, launches)
+    for key, r in rows.items():
+        k = kernels[key]
+        r["in_graph_chain_us_per_launch"] = k["avg_us_per_launch"]
+        r["in_graph_chain_us_per_launch_with_replay_cost"] = k["avg_us_per_launch_with_replay_cost"]
+    # the dominant row: the kernel instance and shape with the most dispatch time per step
+    dom_key = max(rows, key=lambda k: rows[k]["us_per_step"])
+    dom = rows[dom_key]
     traffic = None
     tfile = ROOT / "profiles" / "decode_step_traffic.json"
     if tfile.exists():
-        entry = json.loads(tfile.read_text()).get("instances", {}).get(dom_name)
+        entry = json.loads(tfile.read_text()).get("rows", {}).get(dom_key)
         if entry and entry.get("algorithmic_bytes") == dom["avg_bytes_per_launch"]:
             traffic = entry["traffic_bytes"]
 
@@ -1218,7 +1423,7 @@ def main() -> int:
     log("whole decode step through the executor")
     full = None if args.no_queue else full_decode_step(torch, lib, args.seed)
     log("per-config measurements")
-    configs = {} if args.no_configs else config_suite(torch, lib, args.seed)
+    configs = {} if args.no_configs else config_suite(torch, lib, args.seed, cpu=not args.no_cpu_baseline)
     log("cpu baseline")
     cpu = None if args.no_cpu_baseline else cpu_baseline(unfused, args.cpu_seconds, (l0_x, l0_out))
 
@@ -1243,13 +1448,23 @@ def main() -> int:
         "unfused_golden_sequence": {"launches_per_step": len(unfused), "ms_per_step": round(unfused_s * 1e3, 4),
                                     "GBps": round(sum(l.nbytes for l in unfused) / unfused_s / 1e9, 1)},
         "hbm_frac": round(value * 1e9 / HBM_PEAK, 4),
-        "roofline": {"bound": "hbm", "kernel": dom_name,
-                     "achieved": round(dom["avg_bytes_per_launch"] / dom["avg_us_per_launch"] / 1e3, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(dom["avg_bytes_per_launch"] / dom["avg_us_per_launch"] / 1e3 / (HBM_PEAK / 1e9), 4),
+        "roofline": {"bound": "hbm", "kernel": dom["kernel"],
+                     "shape": f"{dom['role']} launches, {dom['grid_items']} work-items per dispatch",
+                     "achieved": dom["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": dom["hbm_frac"],
                      "traffic": traffic, "traffic_source": "profiles/decode_step_traffic.json (rocprofv3 --pmc)",
                      "avg_bytes_per_launch": dom["avg_bytes_per_launch"],
-                     "avg_us_per_launch": dom["avg_us_per_launch"]},
+                     "avg_us_per_dispatch": dom["avg_us_per_dispatch"], "dispatches_timed": dom["dispatches_timed"],
+                     "duration_source": "each dispatch's own start and end timestamps (HIP events recorded by the "
+                                        "dispatch, tars_time_next_launch), as rocprofv3's kernel trace reads them; "
+                                        "profiles/decode_step_kernels.md",
+                     "in_graph_chain": {
+                         "avg_us_per_launch": dom["in_graph_chain_us_per_launch"],
+                         "frac": round(dom["avg_bytes_per_launch"] / dom["in_graph_chain_us_per_launch"] / 1e3 / (HBM_PEAK / 1e9), 4),
+                         "avg_us_per_launch_with_replay_cost": dom["in_graph_chain_us_per_launch_with_replay_cost"],
+                         "frac_with_replay_cost": round(dom["avg_bytes_per_launch"] / dom["in_graph_chain_us_per_launch_with_replay_cost"] / 1e3 / (HBM_PEAK / 1e9), 4),
+                         "about": "the time a launch adds to a dependent chain of graph launches (launch gap "
+                                  "included), with and without one graph replay's fixed cost"}},
+        "roofline_rows": rows,
         "lm_head": {k: configs.get(k) for k in ("lm_head_M1_K1024_N151936", "lm_head_fused_quant_M1_K1024_N151936")},
         "kernels": kernels,
         # the instances' per-launch times (each instance timed as its own graph, less one replay's

@@ -96,10 +96,10 @@ def test_pmc_summary_refuses_a_missing_kernel(bench, tmp_path):
         bench.pmc_summary(paths, str(detail), str(tmp_path / "o.json"))
 
 
-def test_pmc_step_summary_pools_grids_and_scales(bench, tmp_path):
-    """The decode step's per-instance traffic: one instance's dispatches of two grids (28 q/k/v-like
-    and one head-like per step) pooled by dispatch count, the byte counters scaled by the 1 GiB
-    copy's readings, the algorithmic bytes taken from the detail's kernels."""
+def test_pmc_step_summary_separates_grids_and_scales(bench, tmp_path):
+    """The decode step's traffic per row: one kernel instance's dispatches of two grids (28 q/k/v-like
+    and one head-like per step) kept apart by grid size, the byte counters scaled by the 1 GiB
+    copy's readings, the algorithmic bytes taken from the detail's rows."""
     name = "quant_gemv_w8a8_kernel<64, 1, 4, true, false>"
     cols = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
     paths = []
@@ -116,16 +116,54 @@ def test_pmc_step_summary_pools_grids_and_scales(bench, tmp_path):
                             "Counter_Value": v})
         paths.append(str(p))
     detail = tmp_path / "detail.json"
-    detail.write_text(json.dumps({"kernels": {name: {"avg_bytes_per_launch": 9_492_233}}}))
+    rows = {f"{name} @ qkv": {"kernel": name, "role": "qkv", "grid_items": 65536, "avg_bytes_per_launch": 4_229_120},
+            f"{name} @ head": {"kernel": name, "role": "head", "grid_items": 2430976, "avg_bytes_per_launch": 156_806_144}}
+    detail.write_text(json.dumps({"roofline_rows": rows}))
     out = tmp_path / "step.json"
     assert bench.pmc_step_summary(paths[0], paths[1], str(detail), str(out)) == 0
     t = json.loads(out.read_text())
     assert t["fetch_scale"] == 2.0 and t["write_scale"] == 1.0
-    e = t["instances"][name]
-    assert e["dispatches"] == 29 and e["algorithmic_bytes"] == 9_492_233
-    assert e["read_bytes"] == round((28 * 100.0 + 1000.0) / 29 * 1024 * 2)
-    assert e["write_bytes"] == round((28 * 4.0 + 40.0) / 29 * 1024)
-    assert e["traffic_bytes"] == e["read_bytes"] + e["write_bytes"]
-    detail.write_text(json.dumps({"kernels": {"quant_gemv_w8a8_kernel<64, 2, 1, true, false>": {"avg_bytes_per_launch": 1}}}))
-    with pytest.raises(SystemExit, match="no dispatch"):
+    q, h = t["rows"][f"{name} @ qkv"], t["rows"][f"{name} @ head"]
+    assert q["dispatches"] == 28 and h["dispatches"] == 1
+    assert q["read_bytes"] == round(100.0 * 1024 * 2) and h["read_bytes"] == round(1000.0 * 1024 * 2)
+    assert q["write_bytes"] == round(4.0 * 1024) and h["write_bytes"] == round(40.0 * 1024)
+    assert q["traffic_bytes"] == q["read_bytes"] + q["write_bytes"] and q["algorithmic_bytes"] == 4_229_120
+    rows[f"{name} @ qkv"]["grid_items"] = 12345
+    detail.write_text(json.dumps({"roofline_rows": rows}))
+    with pytest.raises(SystemExit, match="0 dispatch groups"):
         bench.pmc_step_summary(paths[0], paths[1], str(detail), str(out))
+
+
+def test_trace_summary_per_row(bench, tmp_path):
+    """Kernel-trace durations per row (instance and grid) against the line's figures: the mean
+    over a row's dispatches, the HBM fraction it gives for the row's algorithmic bytes, and the
+    roofline row's ratio of trace to bench duration."""
+    name = "quant_gemv_w8a8_kernel<64, 1, 6, true, false>"
+    other = "quant_gemv_w8a8_kernel<64, 3, 1, true, false>"
+    p = tmp_path / "kernel_trace.csv"
+    with open(p, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp",
+                               "End_Timestamp"])
+        w.writeheader()
+        for i, d in enumerate((2000, 2200, 2400)):
+            w.writerow({"Kernel_Name": f"void tars::(anonymous namespace)::{name}(float const*)", "Grid_Size_X": 65536,
+                        "Grid_Size_Y": 1, "Grid_Size_Z": 1, "Start_Timestamp": 10_000 * i, "End_Timestamp": 10_000 * i + d})
+        w.writerow({"Kernel_Name": f"void tars::(anonymous namespace)::{other}(float const*)", "Grid_Size_X": 65536,
+                    "Grid_Size_Y": 1, "Grid_Size_Z": 1, "Start_Timestamp": 0, "End_Timestamp": 1500})
+    rows = {f"{name} @ gate_up": {"kernel": name, "role": "gate_up", "grid_items": 65536, "launches_per_step": 28,
+                                  "avg_bytes_per_launch": 6_344_704, "avg_us_per_dispatch": 2.25, "hbm_frac": 0.35},
+            f"{other} @ down": {"kernel": other, "role": "down", "grid_items": 65536, "launches_per_step": 28,
+                                "avg_bytes_per_launch": 3_166_208, "avg_us_per_dispatch": 1.5, "hbm_frac": 0.26}}
+    roof = {"kernel": name, "shape": "gate_up", "frac": 0.35, "avg_us_per_dispatch": 2.25, "avg_bytes_per_launch": 6_344_704}
+    detail = tmp_path / "detail.json"
+    detail.write_text(json.dumps({"roofline_rows": rows, "roofline": roof}))
+    out = tmp_path / "kernels.json"
+    assert bench.trace_summary(str(p), str(detail), str(out)) == 0
+    t = json.loads(out.read_text())
+    r = t["rows"][f"{name} @ gate_up"]
+    assert r["trace_dispatches"] == 3 and r["trace_avg_us"] == 2.2 and r["trace_min_us"] == 2.0
+    assert r["hbm_frac_from_trace"] == round(6_344_704 / 2.2 / 1e3 / 8000, 4)
+    assert t["roofline_row"] == f"{name} @ gate_up" and t["trace_over_bench_duration"] == round(2.2 / 2.25, 4)
+    assert t["rows"][f"{other} @ down"]["trace_dispatches"] == 1
+    assert (tmp_path / "kernels.table.md").read_text().count("\n") == 4
+
