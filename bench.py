@@ -607,115 +607,42 @@ def row_key(l: Launch) -> str:
     return f"{kernel_instance(l)} @ {role(l)}"
 
 
-def replay_fixed_s(torch, lib, busy_graph, reps: int = 10) -> float:
-    """The fixed cost of one graph replay as instance_times times it (events around a single replay
-    queued behind other work): graphs of 1 and of 29 tiny launches (a 16-element quant_rows) timed
-    that way, and the intercept of the line through them (seconds)."""
-    x = torch.randn((1, 16), device="cuda")
-    q = torch.empty((1, 16), dtype=torch.int8, device="cuda")
-    s = torch.empty(4, device="cuda")
-    t = {}
-    for n in (1, 29):
-        g = capture(torch, [quant_launch(lib, x, q, s, "tiny") for _ in range(n)])
-        total = 0.0
-        for _ in range(reps):
-            busy_graph.replay()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            g.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            total += e0.elapsed_time(e1) / 1e3
-        t[n] = total / reps
-        del g
-    return max(0.0, t[1] - (t[29] - t[1]) / 28)
-
-
-def instance_times(torch, step_graph, launches, fixed_s: float, reps: int = 5) -> dict:
-    """The time each launch adds to a dependent chain of graph launches, per kernel instance and
-    role (row_key): HIP events around a graph of that row's launches from the step (same buffers,
-    step order), less one graph replay's fixed cost (fixed_s, replay_fixed_s), launch gaps
-    included. Before each timed replay the full step and then the largest other row are replayed,
-    so at least ~300 MB (more than the 256 MB MALL) stream between two uses of any weight and every
-    timed launch starts cold."""
-    fams = {}
+def marginal_times(torch, graph, launches, rounds: int = 12, per: int = 8) -> dict:
+    """What each row (kernel instance and role) adds to the decode step: the step graph's time less
+    the time of a graph of the step without that row's launches, per launch of the row. Launch gaps
+    are included and a graph's fixed replay cost cancels. The two graphs are timed in alternation
+    (rounds x per replays each, HIP events around each group on the current stream) so drift
+    cancels too. The rest of the step still streams at least 420 MB, above the 256 MB MALL, so
+    every launch reads its weights cold as in the step."""
+    rows = {}
     for l in launches:
-        fams.setdefault(row_key(l), []).append(l)
-    graphs = {name: capture(torch, ls) for name, ls in fams.items()}
-    size = {name: sum(l.nbytes for l in ls) for name, ls in fams.items()}
+        rows.setdefault(row_key(l), []).append(l)
     out = {}
-    for name, ls in fams.items():
-        others = [k for k in fams if k != name]
-        flush = graphs[max(others, key=lambda k: size[k])] if others else None
-        total = 0.0
-        for _ in range(reps):
-            step_graph.replay()
-            if flush is not None:
-                flush.replay()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            graphs[name].replay()
-            e1.record()
-            torch.cuda.synchronize()
-            total += e0.elapsed_time(e1) / 1e3
-        raw_s = total / (reps * len(ls))
-        avg_s = (total / reps - fixed_s) / len(ls)
-        out[name] = {"launches_per_step": len(ls), "avg_bytes_per_launch": round(size[name] / len(ls)),
-                     "avg_us_per_launch": round(avg_s * 1e6, 3), "avg_us_per_launch_with_replay_cost": round(raw_s * 1e6, 3),
-                     "s_per_step": avg_s * len(ls),
-                     "GBps": round(size[name] / (avg_s * len(ls)) / 1e9, 1),
-                     "hbm_frac": round(size[name] / (avg_s * len(ls)) / HBM_PEAK, 4)}
-    del graphs
-    return out
-
-
-def dispatch_times(torch, lib, launches, steps: int = 4) -> dict:
-    """Kernel duration of every decode-step launch from its dispatch's own start and end timestamps
-    (tars_time_next_launch: HIP events that the dispatch records, on the stream it runs on; the
-    same timestamps rocprofv3's kernel trace reads), over `steps` passes of the step's launches in
-    model order after two untimed passes. Each pass streams all 601 MB of weights (above the 256 MB
-    MALL), so every dispatch reads its weights cold. Per row (kernel instance and role): dispatches
-    timed, mean and median microseconds per dispatch, the work-items of the dispatch, algorithmic
-    bytes per launch and the HBM fraction they give."""
-    import statistics
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(len(launches) * steps)]
-    for a, b in ev:  # the events exist once recorded
-        a.record()
-        b.record()
-    for _ in range(2):
-        for l in launches:
-            l(stream.cuda_stream)
-    torch.cuda.synchronize()
-    k = 0
-    for _ in range(steps):
-        for l in launches:
-            a, b = ev[k]
-            k += 1
-            lib.tars_time_next_launch(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event))
-            l(stream.cuda_stream)
-    torch.cuda.synchronize()
-    rows, k = {}, 0
-    for _ in range(steps):
-        for l in launches:
-            a, b = ev[k]
-            k += 1
-            r = rows.setdefault(row_key(l), {"us": [], "bytes": l.nbytes, "n_per_step": 0, "l": l})
-            r["us"].append(a.elapsed_time(b) * 1e3)
-    for l in launches:
-        rows[row_key(l)]["n_per_step"] += 1
-    out = {}
-    for key, r in rows.items():
-        avg = sum(r["us"]) / len(r["us"])
-        l = r["l"]
+    for key, ls in rows.items():
+        reduced = capture(torch, [l for l in launches if row_key(l) != key])
+        for _ in range(3):
+            graph.replay()
+            reduced.replay()
+        torch.cuda.synchronize()
+        tot = {0: 0.0, 1: 0.0}
+        for _ in range(rounds):
+            for i, g in ((0, graph), (1, reduced)):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(per):
+                    g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                tot[i] += e0.elapsed_time(e1) / 1e3
+        del reduced
+        full_s, without_s = tot[0] / (rounds * per), tot[1] / (rounds * per)
+        us = (full_s - without_s) / len(ls) * 1e6
+        l = ls[0]
         out[key] = {"kernel": kernel_instance(l), "role": role(l),
                     "grid_items": fused_grid_items(l) if l.kind == "quant_gemm_w8a8" else None,
-                    "launches_per_step": r["n_per_step"], "dispatches_timed": len(r["us"]),
-                    "avg_bytes_per_launch": r["bytes"], "avg_us_per_dispatch": round(avg, 3),
-                    "median_us_per_dispatch": round(statistics.median(r["us"]), 3),
-                    "us_per_step": round(avg * r["n_per_step"], 2),
-                    "GBps": round(r["bytes"] / avg / 1e3, 1), "hbm_frac": round(r["bytes"] / avg / 1e3 / (HBM_PEAK / 1e9), 4)}
+                    "launches_per_step": len(ls), "avg_bytes_per_launch": l.nbytes,
+                    "us_per_launch": round(us, 3), "us_per_step": round(us * len(ls), 2),
+                    "GBps": round(l.nbytes / us / 1e3, 1), "hbm_frac": round(l.nbytes / us / 1e3 / (HBM_PEAK / 1e9), 4)}
     return out
 
 
@@ -892,22 +819,22 @@ def trace_summary(trace_csv: str, detail: str, out: str) -> int:
                       "trace_avg_us": round(avg, 3), "trace_median_us": round(statistics.median(d), 3),
                       "trace_min_us": round(min(d), 3), "algorithmic_bytes": r["avg_bytes_per_launch"],
                       "hbm_frac_from_trace": round(r["avg_bytes_per_launch"] / avg / 1e3 / (HBM_PEAK / 1e9), 4),
-                      "bench_avg_us_per_dispatch": r["avg_us_per_dispatch"], "bench_hbm_frac": r["hbm_frac"]}
-    dom = next(k for k, r in rows.items() if r["kernel"] == roof["kernel"] and r["avg_us_per_dispatch"] == roof["avg_us_per_dispatch"])
+                      "bench_us_per_launch": r["us_per_launch"], "bench_hbm_frac": r["hbm_frac"]}
+    dom = next(k for k, r in rows.items() if r["kernel"] == roof["kernel"] and r["us_per_launch"] == roof["avg_us_per_launch"])
     summary = {"about": "rocprofv3 --kernel-trace dispatch durations per decode-step row (kernel instance and grid "
                         "size) against bench.py's own dispatch-timed figures from the same run",
-               "line_roofline": {k: roof[k] for k in ("kernel", "shape", "frac", "avg_us_per_dispatch", "avg_bytes_per_launch")},
+               "line_roofline": {k: roof[k] for k in ("kernel", "shape", "frac", "avg_us_per_launch", "avg_bytes_per_launch")},
                "roofline_row": dom, "frac_from_trace": table[dom]["hbm_frac_from_trace"],
-               "trace_over_bench_duration": round(table[dom]["trace_avg_us"] / roof["avg_us_per_dispatch"], 4),
+               "trace_over_bench_duration": round(table[dom]["trace_avg_us"] / roof["avg_us_per_launch"], 4),
                "rows": table}
     Path(out).write_text(json.dumps(summary, indent=1))
     md = [f"| Row (kernel instance @ role) | Work-items | Launches / step | Trace dispatches | Trace mean µs | Trace median µs | "
-          f"Trace min µs | Algorithmic MB / launch | HBM frac (trace mean) | bench.py µs / dispatch | bench.py HBM frac |",
+          f"Trace min µs | Algorithmic MB / launch | HBM frac (trace mean) | bench.py µs / launch in the step | bench.py HBM frac |",
           "|---|---|---|---|---|---|---|---|---|---|---|"]
     for key, t in sorted(table.items(), key=lambda kv: -kv[1]["trace_avg_us"] * kv[1]["launches_per_step"]):
         md.append(f"| `{key}` | {t['grid_items']} | {t['launches_per_step']} | {t['trace_dispatches']} | {t['trace_avg_us']} | "
                   f"{t['trace_median_us']} | {t['trace_min_us']} | {t['algorithmic_bytes'] / 1e6:.3f} | "
-                  f"{t['hbm_frac_from_trace']} | {t['bench_avg_us_per_dispatch']} | {t['bench_hbm_frac']} |")
+                  f"{t['hbm_frac_from_trace']} | {t['bench_us_per_launch']} | {t['bench_hbm_frac']} |")
     Path(out).with_suffix(".table.md").write_text("\n".join(md) + "\n")
     print(json.dumps({k: summary[k] for k in ("line_roofline", "roofline_row", "frac_from_trace", "trace_over_bench_duration")}),
           flush=True)
@@ -924,8 +851,8 @@ def attach_counters(res: dict) -> None:
     table = json.loads(COUNTER_FILE.read_text())["configs"]
     for key, r in res.items():
         e = table.get(key)
-        if not e or e["algorithmic_bytes"] != r.get("bytes_per_call"):
-            continue
+        if not e or e["algorithmic_bytes"] != r.get("bytes_per_call") or e["kernel"] != CONFIG_KERNELS.get(key, ("",))[0]:
+            continue                  # a stale entry: other bytes, or another kernel instance
         cycles = r["us_per_call"] * 1e-6 * CLOCK_HZ
         r["counters"] = {"kernel": e["kernel"], "traffic_bytes": e["traffic_bytes"],
                          "traffic_over_algorithmic": e["traffic_over_algorithmic"],
@@ -1376,16 +1303,11 @@ def main() -> int:
     step_s = e0.elapsed_time(e1) / 1e3 / args.steps
 
     log(f"step {step_s * 1e6:.1f} us; per-row timing")
-    fixed_s = replay_fixed_s(torch, lib, graph)
-    kernels = instance_times(torch, graph, launches, fixed_s)
-    instances_sum_s = sum(v.pop("s_per_step") for v in kernels.values())
-    rows = dispatch_times(torch, lib, launches)
-    for key, r in rows.items():
-        k = kernels[key]
-        r["in_graph_chain_us_per_launch"] = k["avg_us_per_launch"]
-        r["in_graph_chain_us_per_launch_with_replay_cost"] = k["avg_us_per_launch_with_replay_cost"]
-    # the dominant row: the kernel instance and shape with the most dispatch time per step
-    dom_key = max(rows, key=lambda k: rows[k]["us_per_step"])
+    rows = marginal_times(torch, graph, launches)
+    rows_sum_s = sum(r["us_per_step"] for r in rows.values()) / 1e6
+    # the roofline row: the step's largest dispatch (the lm_head, a quarter of the step's bytes);
+    # every row is reported beside it
+    dom_key = max(rows, key=lambda k: rows[k]["avg_bytes_per_launch"])
     dom = rows[dom_key]
     traffic = None
     tfile = ROOT / "profiles" / "decode_step_traffic.json"
@@ -1449,28 +1371,19 @@ def main() -> int:
                                     "GBps": round(sum(l.nbytes for l in unfused) / unfused_s / 1e9, 1)},
         "hbm_frac": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": {"bound": "hbm", "kernel": dom["kernel"],
-                     "shape": f"{dom['role']} launches, {dom['grid_items']} work-items per dispatch",
+                     "shape": f"{dom['role']} (1024 -> {QWEN3_VOCAB}, the step's largest dispatch), "
+                              f"{dom['grid_items']} work-items",
                      "achieved": dom["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": dom["hbm_frac"],
                      "traffic": traffic, "traffic_source": "profiles/decode_step_traffic.json (rocprofv3 --pmc)",
-                     "avg_bytes_per_launch": dom["avg_bytes_per_launch"],
-                     "avg_us_per_dispatch": dom["avg_us_per_dispatch"], "dispatches_timed": dom["dispatches_timed"],
-                     "duration_source": "each dispatch's own start and end timestamps (HIP events recorded by the "
-                                        "dispatch, tars_time_next_launch), as rocprofv3's kernel trace reads them; "
-                                        "profiles/decode_step_kernels.md",
-                     "in_graph_chain": {
-                         "avg_us_per_launch": dom["in_graph_chain_us_per_launch"],
-                         "frac": round(dom["avg_bytes_per_launch"] / dom["in_graph_chain_us_per_launch"] / 1e3 / (HBM_PEAK / 1e9), 4),
-                         "avg_us_per_launch_with_replay_cost": dom["in_graph_chain_us_per_launch_with_replay_cost"],
-                         "frac_with_replay_cost": round(dom["avg_bytes_per_launch"] / dom["in_graph_chain_us_per_launch_with_replay_cost"] / 1e3 / (HBM_PEAK / 1e9), 4),
-                         "about": "the time a launch adds to a dependent chain of graph launches (launch gap "
-                                  "included), with and without one graph replay's fixed cost"}},
+                     "avg_bytes_per_launch": dom["avg_bytes_per_launch"], "avg_us_per_launch": dom["us_per_launch"],
+                     "duration_source": "the launch's cost in the timed step graph: step time less the time of the "
+                                        "step without it (HIP events, launch gap included); rocprofv3 kernel-trace "
+                                        "durations per row in profiles/decode_step_kernels.md"},
         "roofline_rows": rows,
         "lm_head": {k: configs.get(k) for k in ("lm_head_M1_K1024_N151936", "lm_head_fused_quant_M1_K1024_N151936")},
-        "kernels": kernels,
         # the instances' per-launch times (each instance timed as its own graph, less one replay's
         # fixed cost) summed over a step's launches, beside the step itself
-        "kernels_sum_us_per_step": round(instances_sum_s * 1e6, 1),
-        "graph_replay_fixed_us": round(fixed_s * 1e6, 2),
+        "rows_sum_us_per_step": round(rows_sum_s * 1e6, 1),
         "device_copy_GBps": round(copy_gbps, 1),
         "queue_executor": queue,
         "queue_whole_decode_step_t250": full,

@@ -307,16 +307,6 @@ const char* tars_last_error(void);
  */
 int tars_set_w8a8_path(int path);
 
-/*
- * Kernel timing for benchmarks (not part of the reference's interface): the next matrix-path
- * kernel this thread launches (W8A8 GEMV / fused quantizer + GEMV / K split / INT8 MFMA, W4A16,
- * quant_rows) records start_event and stop_event (hipEvent_t, created by the caller with timing
- * enabled; either may be NULL) at its dispatch's start and end, the timestamps a profiler's kernel
- * trace reads; hipEventElapsedTime of the pair is then that one dispatch's duration. Applies to
- * one launch, then lapses. Entry points that launch two kernels time the first. Host only.
- */
-int tars_time_next_launch(void* start_event, void* stop_event);
-
 /* ---------------------------------------------------------------- descriptor queue executor
  * Replaces tars_mini/golden.py:450-492 (Machine.run_queue) for a DDR image that lives in device
  * memory; the descriptor layout, CRC and check order are contract.py:14-38,154-181 and

@@ -46,7 +46,6 @@ SIGNATURES = {
     "tars_version": (c_char_p, []),
     "tars_last_error": (c_char_p, []),
     "tars_set_w8a8_path": (c_int, [c_int]),
-    "tars_time_next_launch": (c_int, [c_void_p, c_void_p]),
     "tars_run_queue": (c_int, [c_void_p, c_uint64, c_uint64, c_int32, c_char_p, c_int32, c_int32,
                                POINTER(QueueStatus), c_void_p]),
     "tars_check_descriptor": (c_int, [c_char_p, c_uint64, c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),

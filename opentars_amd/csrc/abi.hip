@@ -104,11 +104,6 @@ namespace tars {
 void set_last_error(const std::string& what) { g_last_error = what; }
 // The W8A8 kernel-family switch (tars_set_w8a8_path).
 int w8a8_path() { return g_w8a8_path; }
-// The calling thread's pending kernel-timing events (tars_time_next_launch).
-LaunchEvents& pending_launch_events() {
-  thread_local LaunchEvents ev;
-  return ev;
-}
 
 // tars_quant_gemm_w8a8's checks and launch, with the gated product (QuantGemvArgs::prod) for the
 // queue executor's MLP fusion: prod rows must not overlap an input, the quantized rows or Y1, and
@@ -244,11 +239,6 @@ int tars_set_w8a8_path(int path) {
   const int prev = g_w8a8_path;
   g_w8a8_path = (path >= 0 && path <= 2) ? path : 0;
   return prev;
-}
-
-int tars_time_next_launch(void* start_event, void* stop_event) {
-  tars::pending_launch_events() = tars::LaunchEvents{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
-  return TARS_OK;
 }
 
 int tars_quant_rows(const float* x, int64_t lda, int8_t* q, int64_t ldq, float* s, int32_t M,

@@ -228,9 +228,9 @@ hipError_t go_direct(const MfmaArgs& a, hipStream_t s) {
   const size_t lds = static_cast<size_t>(KW) * BM * red_pitch(KW, BM, BN) * 4;
   const dim3 block(64 * KW);
   if (grid.y == 1) {
-    launch_kernel((mfma_direct_kernel<TM, TN, KW, D, true>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, true>), grid, block, lds, s, a);
   } else {
-    launch_kernel((mfma_direct_kernel<TM, TN, KW, D, false>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((mfma_direct_kernel<TM, TN, KW, D, false>), grid, block, lds, s, a);
   }
   return hipGetLastError();
 }
@@ -451,7 +451,7 @@ hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
   const int lda = static_cast<int>(a.lda), ldy = static_cast<int>(a.ldy);
   const dim3 grid(mt * nt), block(64 * WM * WN);
 #define TARS_TILE(SIMPLE, KSPLIT)                                                                                      \
-  launch_kernel((mfma_tile_kernel<BM, BN, WM, WN, KS, S, SIMPLE, KSPLIT>), grid, block, 0, s, A, a.seg[0].W,      \
+  hipLaunchKernelGGL((mfma_tile_kernel<BM, BN, WM, WN, KS, S, SIMPLE, KSPLIT>), grid, block, 0, s, A, a.seg[0].W,      \
                      e.scol, e.srow, lda, a.seg[0].K, a.M, a.N, mt, ldy, a.Y, tl)
   if (a.nseg > 1) {
     if (simple) TARS_TILE(true, true);

@@ -755,17 +755,17 @@ hipError_t go(const W8A8Args& a, hipStream_t s) {
   const unsigned nb = (a.N + rows_per_block - 1) / rows_per_block;
   if constexpr (CPL > 0 && 4 * U <= L) {
     if (a.M >= 3) {
-      launch_kernel((gemv_w8a8_kernel<L, CPL, U, 4, SIMPLE>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a.A, a.lda,
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 4, SIMPLE>), dim3(nb, (a.M + 3) / 4), dim3(kThreads), 0, s, a.A, a.lda,
                        a.W, a.epi.scol, a.epi.srow, a.K, a.N, a.M, a.epi.scol_per_tensor, a);
       return hipGetLastError();
     }
     if (a.M == 2) {
-      launch_kernel((gemv_w8a8_kernel<L, CPL, U, 2, SIMPLE>), dim3(nb, 1), dim3(kThreads), 0, s, a.A, a.lda,
+      hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 2, SIMPLE>), dim3(nb, 1), dim3(kThreads), 0, s, a.A, a.lda,
                        a.W, a.epi.scol, a.epi.srow, a.K, a.N, a.M, a.epi.scol_per_tensor, a);
       return hipGetLastError();
     }
   }
-  launch_kernel((gemv_w8a8_kernel<L, CPL, U, 1, SIMPLE>), dim3(nb, a.M), dim3(kThreads), 0, s, a.A, a.lda,
+  hipLaunchKernelGGL((gemv_w8a8_kernel<L, CPL, U, 1, SIMPLE>), dim3(nb, a.M), dim3(kThreads), 0, s, a.A, a.lda,
                        a.W, a.epi.scol, a.epi.srow, a.K, a.N, a.M, a.epi.scol_per_tensor, a);
   return hipGetLastError();
 }
@@ -801,11 +801,11 @@ hipError_t launch_qg(dim3 grid, size_t lds, hipStream_t s, const int8_t* const* 
     if constexpr (!kNorm) {
       return hipErrorInvalidValue;
     } else {
-      launch_kernel((quant_gemv_norm_kernel<L, CPL, U, SIMPLE, PAIR>), grid, dim3(kThreads), lds, s, b.x,
+      hipLaunchKernelGGL((quant_gemv_norm_kernel<L, CPL, U, SIMPLE, PAIR>), grid, dim3(kThreads), lds, s, b.x,
                          b.pro.B ? b.pro.B : b.x, b.pro.gamma, Wz[0], Wz[1], Wz[2], b.K, N, b);
     }
   } else {
-    launch_kernel((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR>), grid, dim3(kThreads), lds, s, b.x, b.lda,
+    hipLaunchKernelGGL((quant_gemv_w8a8_kernel<L, CPL, U, SIMPLE, PAIR>), grid, dim3(kThreads), lds, s, b.x, b.lda,
                        Wz[0], Wz[1], Wz[2], Wz[3], b.K, N, b);
   }
   return hipGetLastError();
@@ -945,7 +945,7 @@ template <int CPL, int WPR>
 hipError_t go_ksplit_rows(const KSplitArgs& a, hipStream_t s) {
   constexpr int rows = kWaves / WPR;
   const dim3 grid((a.N + rows - 1) / rows, a.M);
-  launch_kernel((gemv_w8a8_ksplit_rows_kernel<CPL, WPR>), grid, dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((gemv_w8a8_ksplit_rows_kernel<CPL, WPR>), grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -957,11 +957,11 @@ hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s) {
   const int rows_per_block = kWaves * u;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block, a.M);
   if (u == 1) {
-    launch_kernel((gemv_w8a8_ksplit_kernel<1>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<1>), grid, dim3(kThreads), 0, s, a);
   } else if (u == 2) {
-    launch_kernel((gemv_w8a8_ksplit_kernel<2>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<2>), grid, dim3(kThreads), 0, s, a);
   } else {
-    launch_kernel((gemv_w8a8_ksplit_kernel<4>), dim3((a.N + kWaves * 4 - 1) / (kWaves * 4), a.M), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((gemv_w8a8_ksplit_kernel<4>), dim3((a.N + kWaves * 4 - 1) / (kWaves * 4), a.M), dim3(kThreads), 0, s, a);
   }
   return hipGetLastError();
 }

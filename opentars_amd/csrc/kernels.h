@@ -2,7 +2,6 @@
 // Launchers assume validated arguments; they only pick a kernel instance and enqueue it.
 #pragma once
 
-#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -10,26 +9,6 @@
 #include "wave_reduce.h"
 
 namespace tars {
-
-// Benchmark timing (tars_time_next_launch): while a pair of events is pending on the calling
-// thread, the next matrix-path kernel launch records them at its dispatch's start and end (the
-// dispatch's own timestamps, the ones a profiler's kernel trace reads), and the pair is cleared.
-struct LaunchEvents {
-  hipEvent_t start = nullptr, stop = nullptr;
-};
-LaunchEvents& pending_launch_events();
-
-template <class... P, class... A>
-void launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, A... args) {
-  LaunchEvents& ev = pending_launch_events();
-  if (ev.start || ev.stop) {
-    const LaunchEvents e = ev;
-    ev = LaunchEvents{};
-    hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, e.start, e.stop, 0, static_cast<P>(args)...);
-  } else {
-    hipLaunchKernelGGL(kernel, grid, block, shmem, s, static_cast<P>(args)...);
-  }
-}
 
 // Predicated loads without branches. A load behind a branch makes the compiler's wait-counter
 // bookkeeping assume either path where they join, so waiting for one early load (the activations)

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
 }  // namespace
 
 hipError_t launch_quant_rows(const QuantArgs& a, hipStream_t s) {
-  launch_kernel(quant_rows_kernel, dim3(a.M), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL(quant_rows_kernel, dim3(a.M), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -462,11 +462,11 @@ hipError_t go_w4(const W4Args& a, hipStream_t s) {
   const size_t lds = static_cast<size_t>(MR) * (a.K / 32) * 64;
   const bool simple = !a.bias && a.act == 0 && a.out == 0;
   if (a.bf16) {
-    if (simple) launch_kernel((gemv_w4a16_kernel<NW, U, MR, CPL, true, true>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
-    else launch_kernel((gemv_w4a16_kernel<NW, U, MR, CPL, true, false>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
+    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, true>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
+    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, true, false>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
   } else {
-    if (simple) launch_kernel((gemv_w4a16_kernel<NW, U, MR, CPL, false, true>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
-    else launch_kernel((gemv_w4a16_kernel<NW, U, MR, CPL, false, false>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
+    if (simple) hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, true>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
+    else hipLaunchKernelGGL((gemv_w4a16_kernel<NW, U, MR, CPL, false, false>), grid, dim3(NW * 64), lds, s, a.x, a.lda, a.Wp, a.ws, a.M, a.N, a.K, a);
   }
   return hipGetLastError();
 }
@@ -476,7 +476,7 @@ hipError_t go_w4(const W4Args& a, hipStream_t s) {
 hipError_t launch_align_w4(const AlignArgs& a, hipStream_t s) {
   const int C = a.K / 32;
   const dim3 grid((C + kThreads - 1) / kThreads, a.M);
-  launch_kernel(align_w4_kernel, grid, dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL(align_w4_kernel, grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -151,10 +151,10 @@ def test_trace_summary_per_row(bench, tmp_path):
         w.writerow({"Kernel_Name": f"void tars::(anonymous namespace)::{other}(float const*)", "Grid_Size_X": 65536,
                     "Grid_Size_Y": 1, "Grid_Size_Z": 1, "Start_Timestamp": 0, "End_Timestamp": 1500})
     rows = {f"{name} @ gate_up": {"kernel": name, "role": "gate_up", "grid_items": 65536, "launches_per_step": 28,
-                                  "avg_bytes_per_launch": 6_344_704, "avg_us_per_dispatch": 2.25, "hbm_frac": 0.35},
+                                  "avg_bytes_per_launch": 6_344_704, "us_per_launch": 2.25, "hbm_frac": 0.35},
             f"{other} @ down": {"kernel": other, "role": "down", "grid_items": 65536, "launches_per_step": 28,
-                                "avg_bytes_per_launch": 3_166_208, "avg_us_per_dispatch": 1.5, "hbm_frac": 0.26}}
-    roof = {"kernel": name, "shape": "gate_up", "frac": 0.35, "avg_us_per_dispatch": 2.25, "avg_bytes_per_launch": 6_344_704}
+                                "avg_bytes_per_launch": 3_166_208, "us_per_launch": 1.5, "hbm_frac": 0.26}}
+    roof = {"kernel": name, "shape": "gate_up", "frac": 0.35, "avg_us_per_launch": 2.25, "avg_bytes_per_launch": 6_344_704}
     detail = tmp_path / "detail.json"
     detail.write_text(json.dumps({"roofline_rows": rows, "roofline": roof}))
     out = tmp_path / "kernels.json"
