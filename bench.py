@@ -682,8 +682,8 @@ CONFIG_KERNELS = {
     "c1_gemv_qwen3_gate_M1_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 1, true>", 196608),
     "lm_head_M1_K1024_N151936": ("gemv_w8a8_kernel<64, 1, 4, 1, true>", 2430976),
     "lm_head_fused_quant_M1_K1024_N151936": ("quant_gemv_w8a8_kernel<64, 1, 4, true, false>", 2430976),
-    "c2_gemma3_down_ksplit_3456+3456": ("gemv_w8a8_ksplit_rows_kernel<2, 4>", 294912),
-    "c2_gemma3_down_ksplit_4096+2816": ("gemv_w8a8_ksplit_rows_kernel<2, 4>", 294912),
+    "c2_gemma3_down_ksplit_3456+3456": ("gemv_w8a8_ksplit2_kernel<7, 1, 5>", 73920),
+    "c2_gemma3_down_ksplit_4096+2816": ("gemv_w8a8_ksplit2_kernel<7, 1, 5>", 73920),
     "c4_prefill_M4_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 4, true>", 196608),
     "c4_prefill_M4_K3072_N1024": ("gemv_w8a8_kernel<64, 3, 1, 4, true>", 65536),
     "c4_prefill_M4_K1024_N3072_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 98304),

@@ -21,6 +21,8 @@
 //    rows, so each 128-byte line of the output is written from one XCD's L2.
 //
 // Roofline: HBM. Algorithmic bytes per row: K (weights) + 4 (scale) + 4 (output) (+4 bias).
+#include <algorithm>
+
 #include "kernels.h"
 #include "row_sums.h"
 
@@ -224,6 +226,99 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(const int8_t* A, in
       const float y = epi.apply(mine, sr, srow != nullptr, sc, bi);
       store_out(Y, me * ldy, ne, epi.out, y, epi.out_scale);
     }
+  }
+}
+
+// ---- K split in two blocks, one wave per row (the Gemma 3 down projection's 4096 + 2816) ----
+// The concatenated row of both blocks is cut into 16-byte chunks like a plain row: lane `sub` takes
+// chunks sub, sub + 64, ... (every chunk of the row in one batch of loads, the activation chunks
+// held in registers); a chunk below C0 = K0 / 16 is block 0's (W0, rows K0 bytes apart), the rest
+// block 1's (W1, rows K1 bytes apart). Each lane keeps one exact int32 sum per block and row; the
+// wave's sums end scattered over the lanes (wave_sum_scatter, the block in lane bit 5), and one
+// permlane32 swap hands block 1's total to the lane 32 below, which forms both blocks' fp32
+// partials (i2f(acc) * srow) * scol and adds them in block order (llm.py:303-321,
+// golden.py:411-412). The first loads need only the leading scalar arguments (preloaded); the
+// output pointer and stride follow in `t`.
+struct KSplit2Tail {
+  void* Y;
+  int64_t ldy;
+};
+struct KSplit2Kernargs {
+  const int8_t *A, *W0, *W1;
+  const float *scol, *srow;
+  int lda, K0, K1, N;
+  KSplit2Tail t;
+};
+static_assert(offsetof(KSplit2Kernargs, t) == 56, "the preloaded scalars take 56 bytes before the tail");
+
+template <int CPL, int U, int NWG>
+__global__ __launch_bounds__(64 * NWG) void gemv_w8a8_ksplit2_kernel(const int8_t* A, const int8_t* W0, const int8_t* W1,
+                                                                     const float* scol, const float* srow, int lda,
+                                                                     int K0, int K1, int N, KSplit2Tail t) {
+  constexpr int kE = 2 * U;  // (row, block) sums per wave: value 2 u + b
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int m = blockIdx.y;
+  const int C0 = K0 >> 4, C = C0 + (K1 >> 4);
+  const int bx = xcd_block(blockIdx.x, (N + NWG * U - 1) / (NWG * U));  // the grid's x extent
+  const int n0 = (bx * NWG + wave) * U;
+  const v4i zero = {0, 0, 0, 0};
+  const int e = scatter_row<kE>(lane);
+  const int ne = n0 + (e >> 1);
+  const bool epi_lane = scatter_owner<kE>(lane) && (e & 1) == 0 && ne < N;
+  const int nc = epi_lane ? ne : 0;
+
+  // one batch of loads: activations, epilogue operands, weights (a chunk past the row re-reads the
+  // row's last chunk and is zeroed on the activation side; a row past N re-reads row N - 1, never
+  // stored)
+  const v4i* xrow = reinterpret_cast<const v4i*>(A + static_cast<int64_t>(m) * lda);
+  v4i xv[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) xv[j] = xrow[min(lane + 64 * j, C - 1)];
+  const float sc = scol[nc];
+  const float sr = *(srow ? srow + m : scol);
+  v4i wv[U][CPL];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int n = min(n0 + u, N - 1);
+    const v4i* r0 = reinterpret_cast<const v4i*>(W0 + static_cast<int64_t>(n) * K0);
+    const v4i* r1 = reinterpret_cast<const v4i*>(W1 + static_cast<int64_t>(n) * K1) - C0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = min(lane + 64 * j, C - 1);
+      wv[u][j] = __builtin_nontemporal_load(c < C0 ? r0 + c : r1 + c);
+    }
+  }
+  issue_fence();
+  const KArg ka = kernarg_at(offsetof(KSplit2Kernargs, t));
+  void* const Y = kload<void*>(ka + offsetof(KSplit2Tail, Y));
+  const int64_t ldy = kload<int64_t>(ka + offsetof(KSplit2Tail, ldy));
+  issue_fence();
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+    if (lane + 64 * j >= C) xv[j] = zero;
+  int v[kE];
+#pragma unroll
+  for (int i = 0; i < kE; ++i) v[i] = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int d = dot16(wv[u][j], xv[j], 0);
+      const bool first = lane + 64 * j < C0;
+      v[2 * u] += first ? d : 0;
+      v[2 * u + 1] += first ? 0 : d;
+    }
+  const int mine = wave_sum_scatter<kE>(v);
+  const int other = static_cast<int>(__builtin_amdgcn_permlane32_swap(mine, mine, false, false)[1]);  // lane + 32
+  if (epi_lane) {
+    float y0 = i2f(mine), y1 = i2f(other);
+    if (srow) {
+      y0 = fmul(y0, sr);
+      y1 = fmul(y1, sr);
+    }
+    const float y = fadd(fmul(y0, sc), fmul(y1, sc));
+    reinterpret_cast<float*>(static_cast<char*>(Y) + m * ldy)[ne] = ftz(y);
   }
 }
 
@@ -949,9 +1044,47 @@ hipError_t go_ksplit_rows(const KSplitArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Two blocks of a total K up to 8192 (the Gemma 3 down projection): one wave per row with every
+// chunk in flight (gemv_w8a8_ksplit2_kernel), ceil(N / 256) waves per workgroup (4 to 8) so the
+// grid gives each CU at most one workgroup; four rows per wave past 32768 rows. Measured on MI355X
+// at K = 4096 + 2816 and 3456 + 3456, N = 1152 (weights cold): 4.54 us with four waves per row
+// (1152 workgroups, each reading the 6.9 KB quantized row) -> 3.84 us one row per wave in 4-wave
+// workgroups (288) -> 3.49 us in 5-wave workgroups (231); 6- and 8-wave workgroups 3.53 / 3.66 us;
+// two rows per wave 3.6 - 3.8 us; the activation row staged once per workgroup in LDS 3.77 us.
+template <int CPL, int U, int NWG>
+hipError_t go_ks2(const KSplitArgs& a, hipStream_t s) {
+  const KSplit2Tail t{a.Y, a.ldy};
+  hipLaunchKernelGGL((gemv_w8a8_ksplit2_kernel<CPL, U, NWG>), dim3((a.N + NWG * U - 1) / (NWG * U), a.M), dim3(64 * NWG),
+                     0, s, a.A, a.W[0], a.W[1], a.scol, a.srow, static_cast<int>(a.lda), a.K[0], a.K[1], a.N, t);
+  return hipGetLastError();
+}
+
+template <int CPL>
+hipError_t go_ksplit2(const KSplitArgs& a, hipStream_t s) {
+  if (a.N >= 32768) return go_ks2<CPL, 4, 4>(a, s);
+  switch (std::min(8, std::max(4, (a.N + 255) / 256))) {
+    case 4: return go_ks2<CPL, 1, 4>(a, s);
+    case 5: return go_ks2<CPL, 1, 5>(a, s);
+    case 6: return go_ks2<CPL, 1, 6>(a, s);
+    default: return go_ks2<CPL, 1, 8>(a, s);
+  }
+}
+
 hipError_t launch_gemv_w8a8_ksplit(const KSplitArgs& a, hipStream_t s) {
   int ctot = 0;
   for (int i = 0; i < a.nblocks; ++i) ctot += a.K[i] >> 4;
+  if (a.nblocks == 2 && ctot <= 512 && a.koff[1] == a.K[0] && a.lda <= INT32_MAX) {
+    switch ((ctot + 63) / 64) {
+      case 1: return go_ksplit2<1>(a, s);
+      case 2: return go_ksplit2<2>(a, s);
+      case 3: return go_ksplit2<3>(a, s);
+      case 4: return go_ksplit2<4>(a, s);
+      case 5: return go_ksplit2<5>(a, s);
+      case 6: return go_ksplit2<6>(a, s);
+      case 7: return go_ksplit2<7>(a, s);
+      default: return go_ksplit2<8>(a, s);
+    }
+  }
   if (ctot <= 512) return ctot <= 256 ? go_ksplit_rows<1, 4>(a, s) : go_ksplit_rows<2, 4>(a, s);
   const int u = ksplit_rows_per_wave(a.N);
   const int rows_per_block = kWaves * u;

@@ -249,6 +249,20 @@ def test_ksplit_both_paths_agree():
     assert same(outs[0], want) and same(outs[1], want)
 
 
+@pytest.mark.parametrize("N,split", [(n, sp) for n in (80, 1040, 1152, 1296, 2064)
+                                     for sp in ([3456, 3456], [16, 8176], [1040, 2048])] + [(32784, [512, 512])])
+def test_ksplit_two_blocks_whole_row_waves(N, split):
+    """Two K blocks (the whole-row kernel: one wave per row, 4 to 8 waves per workgroup by N, four
+    rows per wave from 32768 rows): block boundaries inside a lane's chunks, a first block of one
+    chunk, a total of exactly 8192, ragged last workgroups."""
+    K = sum(split)
+    x, q, s, W, scol, _ = w8_inputs(N + K, 1, N, K)
+    blocks = [np.ascontiguousarray(W[:, :split[0]]), np.ascontiguousarray(W[:, split[0]:])]
+    y = ops.gemm_rowcol_ksplit(cuda(q), cuda(s), [cuda(b) for b in blocks], cuda(scol))
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("split", [[16], [16, 32], [48, 1040, 16], [4096, 4096], [4096, 4112], [1024] * 8,
                                    [2816, 3456, 16], [7168, 1024]])
 @pytest.mark.parametrize("M", [1, 3])
