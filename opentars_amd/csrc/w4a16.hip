@@ -249,6 +249,17 @@ struct W4Kernargs {
 constexpr size_t kW4ArgsOffset = offsetof(W4Kernargs, a);
 static_assert(kW4ArgsOffset == 48, "the preloaded scalars take 48 bytes before the argument block");
 
+// The MFMA form's leading scalars: x, the weight and scale pointers, lda, M, N, K.
+struct W4MfmaKernargs {
+  const void* x;
+  const uint8_t* Wp;
+  const uint16_t* ws;
+  int lda, M, N, K;
+  W4Args a;
+};
+constexpr size_t kW4MfmaArgsOffset = offsetof(W4MfmaKernargs, a);
+static_assert(kW4MfmaArgsOffset == 40, "the preloaded scalars take 40 bytes before the argument block");
+
 template <int NW, int U, int MR, int CPL, bool BF16, bool SIMPLE>
 __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int64_t lda, const uint8_t* Wp,
                                                              const uint16_t* ws, int M, int N, int K, W4Args a) {
@@ -471,6 +482,247 @@ hipError_t go_w4(const W4Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------- GEMM on INT8 MFMA
+// Prefill chunks (M >= 2): the group dots on v_mfma_i32_16x16x64_i8. An aligned mantissa a
+// (|a| <= 2^14) is split as a = 256 h + l with l its low byte sign-extended (in [-128, 127]) and
+// h = (a - l) / 256 (in [-64, 64]); a weight w in [-8, 7] is taken as u = w + 8 in [0, 15] (its
+// nibble with the top bit flipped, no sign extension). Then over a 128-wide group
+//   dot = sum a w = 256 sum h u + sum l u - 8 sum a,
+// every sum exact in int32 (|sum h u| <= 2^17, |sum a| <= 2^21, |dot| <= 2^24), so the group's
+// dot is the reference's exactly. The MFMA sums over 64 k: lane l supplies 16 bytes of activation
+// row l % 16 and of weight row l % 16; with the weights' packed nibble order (byte b of the
+// group's 64 bytes holds k = 2 b and 2 b + 1), one instruction takes the group's even k (the low
+// nibbles) and a second its odd k (the high nibbles), and the activation side is laid out in LDS
+// in the same order: [group][parity][h or l][lane quarter][row][16 bytes], so each operand is one
+// ds_read_b128 per lane.
+//
+// A workgroup owns MT activation rows (rows past M repeat row M - 1 and are never stored) and TT
+// tiles of 16 weight rows; NW waves, NW / TT per tile, split the tile's groups. The workgroup
+// loads its MT rows and aligns them once (8 elements per thread, 16 threads per group, the
+// group's exponent maximum by DPP; align_elems) into the LDS operands, the per-group scales and
+// 8 sum a; only then does each wave issue its weight loads (issued before, they would hold up
+// the alignment's instructions behind them). After a barrier each wave runs 4 MFMAs per group
+// for all its groups, keeping the dots in registers (lane l ends with rows 4 (l / 16) .. + 3,
+// weight row l % 16), then forms the fp32 terms (i2f(dot) * ws) * xs into LDS; after a second
+// barrier a lane per (row, weight row, bank) runs bank b's chain over groups b, b + 4, ... in
+// order from +0 (golden.py:315-319) and each quad folds (b0 + b1) + (b2 + b3) before bias,
+// activation and conversion.
+//
+// Roofline: HBM for the weights (K / 2 + K / 64 bytes per weight row), read once per MT rows; the
+// per-(row, group) fp32 terms and chains are VALU work, one MFMA tile's 16 x 16 outputs per lane
+// set whatever M is.
+template <int MT, int TT, int NW, int GMAX, bool BF16, bool SIMPLE>
+__global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x, const uint8_t* Wp, const uint16_t* ws,
+                                                                  int lda, int M, int N, int K, W4Args a) {
+  constexpr int NT = NW * 64, WPT = NW / TT, GW = (GMAX + WPT - 1) / WPT;
+  constexpr int TP = (GMAX * 16 + NT - 1) / NT;  // alignment passes per row (K / 8 tasks per row)
+  static_assert(NW % TT == 0 && (MT == 4 || MT == 8), "waves split evenly over tiles");
+  __shared__ __align__(16) int8_t aop[GMAX * 256 * MT];  // [g][parity][h, l][quarter][row][16 B]
+  __shared__ __align__(16) float xs_t[GMAX][MT];
+  __shared__ __align__(16) int s8_t[GMAX][MT];
+  __shared__ float terms[TT][16][MT][GMAX + 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lq = lane >> 4;
+  const int G = K >> 7, TK = K >> 3;
+  const int m0 = blockIdx.y * MT;
+  const int tile = wave % TT, part = wave / TT;
+  const int nt0 = (blockIdx.x * TT + tile) * 16;
+  const int gpw = (G + WPT - 1) / WPT, ga = part * gpw, gb = min(G, ga + gpw);
+
+  // 1. the activation rows (task (r, t): row m0 + r, elements 8 t .. 8 t + 7; a dead task reads
+  //    the row's first group; rows past M read the last row)
+  uint32_t xb[MT][TP][8];
+#pragma unroll
+  for (int r = 0; r < MT; ++r) {
+    const char* xrow = static_cast<const char*>(x) + static_cast<int64_t>(min(m0 + r, M - 1)) * lda;
+#pragma unroll
+    for (int p = 0; p < TP; ++p) {
+      if (p * NT >= TK) continue;  // uniform
+      const int t = p * NT + tid;
+      const int tt = t < TK ? t : (t & 15);
+      if constexpr (BF16) {
+        const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * tt);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xb[r][p][2 * j] = v[j] << 16;
+          xb[r][p][2 * j + 1] = v[j] & 0xFFFF0000u;
+        }
+      } else {
+        const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * tt);
+        const v4u v0 = src[0], v1 = src[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xb[r][p][j] = v0[j];
+          xb[r][p][4 + j] = v1[j];
+        }
+      }
+    }
+  }
+  issue_fence();
+
+  // 2. alignment into the LDS operands: task t's elements are k = 8 t' .. 8 t' + 7 of group
+  //    t / 16 (t' = t % 16): quarter q = t' / 4, even k at bytes 4 (t' % 4) .. + 3 of the even
+  //    parity's 16, odd k likewise
+#pragma unroll
+  for (int r = 0; r < MT; ++r) {
+#pragma unroll
+    for (int p = 0; p < TP; ++p) {
+      if (p * NT + wave * 64 >= TK) continue;  // wave-uniform: a wave with no live task
+      const int t = p * NT + tid;
+      int mant[8];
+      uint32_t sb;
+      align_elems<8, 16>(xb[r][p], mant, sb);
+      int sum = 0;
+      uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int am = static_cast<int16_t>(mant[e]);   // the mantissa: its low 16 bits, signed
+        const int lo = static_cast<int8_t>(am);
+        const int hi = (am - lo) >> 8;
+        sum += am;
+        hw[e & 1] |= static_cast<uint32_t>(hi & 0xFF) << (8 * (e >> 1));
+        lw[e & 1] |= static_cast<uint32_t>(lo & 0xFF) << (8 * (e >> 1));
+      }
+      sum = group_sum<16>(sum);
+      if (t < TK) {
+        const int g = t >> 4, tq = t & 15, q = tq >> 2;
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+          int8_t* base = aop + ((((g * 2 + par) * 2) * 4 + q) * MT + r) * 16 + 4 * (tq & 3);
+          *reinterpret_cast<uint32_t*>(base) = hw[par];                 // h
+          *reinterpret_cast<uint32_t*>(base + 4 * MT * 16) = lw[par];   // l
+        }
+        if (tq == 0) {
+          xs_t[g][r] = ffrom(sb);
+          s8_t[g][r] = 8 * sum;
+        }
+      }
+    }
+  }
+  // 3. this wave's weights (row nt0 + l % 16, the 16 bytes of quarter l / 16 of each of its groups)
+  //    and their fp16 scales; rows past N read the last row, groups past the wave's range group ga
+  const int nr = min(nt0 + li, N - 1);
+  const uint8_t* wrow = Wp + static_cast<int64_t>(nr) * (K >> 1) + 16 * lq;
+  v4u wv[GW];
+  uint32_t wsv[GW];
+#pragma unroll
+  for (int i = 0; i < GW; ++i) {
+    const int g = min(ga + i < gb ? ga + i : ga, G - 1);
+    wv[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + 64 * g));
+    wsv[i] = ws[static_cast<int64_t>(nr) * G + g];
+  }
+  issue_fence();
+  const KArg ka = kernarg_at(kW4MfmaArgsOffset);
+  void* const Y = kload<void*>(ka + offsetof(W4Args, Y));
+  const int64_t ldy = kload<int64_t>(ka + offsetof(W4Args, ldy));
+  const float* const bias = SIMPLE ? nullptr : kload<const float*>(ka + offsetof(W4Args, bias));
+  const int act = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, act));
+  const int out = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, out));
+  const float out_scale = SIMPLE ? 0.0f : kload<float>(ka + offsetof(W4Args, out_scale));
+
+  __syncthreads();
+
+  // 4. the MFMAs of every group of this wave (dots in registers), then their terms into LDS
+  const v4i zero = {0, 0, 0, 0};
+  int dots[GW][4];
+#pragma unroll
+  for (int i = 0; i < GW; ++i) {
+    if (ga + i >= gb) break;  // uniform
+    const int g = ga + i;
+    v4i ah[2], al[2];
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int8_t* base = aop + ((((g * 2 + par) * 2) * 4 + lq) * MT + min(li, MT - 1)) * 16;
+      ah[par] = li < MT ? *reinterpret_cast<const v4i*>(base) : zero;
+      al[par] = li < MT ? *reinterpret_cast<const v4i*>(base + 4 * MT * 16) : zero;
+    }
+    v4i blo, bhi;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      blo[d] = static_cast<int>((wv[i][d] & 0x0F0F0F0Fu) ^ 0x08080808u);
+      bhi[d] = static_cast<int>(((wv[i][d] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u);
+    }
+    v4i accH = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[0], blo, zero, 0, 0, 0);
+    accH = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[1], bhi, accH, 0, 0, 0);
+    v4i accL = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[0], blo, zero, 0, 0, 0);
+    accL = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[1], bhi, accL, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dots[i][v] = accH[v] * 256 + accL[v];
+  }
+  // lane l holds rows 4 (l / 16) .. + 3 of weight row l % 16: quarters past MT / 4 hold padding rows
+  const int mq = min(4 * lq, MT - 4);
+  const bool live_rows = 4 * lq < MT;
+#pragma unroll
+  for (int i = 0; i < GW; ++i) {
+    const int g = ga + i;
+    if (g >= gb) break;  // uniform
+    const float4 xs4 = *reinterpret_cast<const float4*>(&xs_t[g][mq]);
+    const int4 s84 = *reinterpret_cast<const int4*>(&s8_t[g][mq]);
+    const float wsf = from_fp16_bits(wsv[i]);
+    const float xsv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+    const int s8v[4] = {s84.x, s84.y, s84.z, s84.w};
+    float t4[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      // the contract's fmul(fmul(i2f(d), ws), xs) with its wrappers where they act (see the GEMV)
+      t4[v] = ftz(__fmul_rn(__fmul_rn(i2f(dots[i][v] - s8v[v]), wsf), xsv[v]));
+    if (live_rows) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) terms[tile][li][mq + v][g] = t4[v];
+    }
+  }
+  __syncthreads();
+
+  // 5. chains: chain c = (tile, weight row, row, bank); the quad's four banks fold into bank 0
+  constexpr int NCH = TT * 16 * MT * 4, CP = (NCH + NT - 1) / NT;
+#pragma unroll
+  for (int pc = 0; pc < CP; ++pc) {
+    const int c = pc * NT + tid;
+    if (pc * NT >= NCH) break;  // uniform
+    const int cc = c < NCH ? c : 0;
+    const int bank = cc & 3, o = cc >> 2;
+    const int m = o % MT, n = (o / MT) % 16, tl = o / (MT * 16);
+    float acc = 0.0f;
+    for (int g = bank; g < G; g += 4) acc = fadd_chain(acc, terms[tl][n][m][g]);
+    acc = chain_end(acc);
+    const float pair = fadd(acc, lane_xor1(acc));
+    const float other = lane_xor2(pair);
+    const int ng = (blockIdx.x * TT + tl) * 16 + n, mg = m0 + m;
+    if (c < NCH && bank == 0 && ng < N && mg < M) {
+      float y = fadd(pair, other);
+      const int64_t yrow = static_cast<int64_t>(mg) * ldy;
+      if constexpr (SIMPLE) {
+        reinterpret_cast<float*>(static_cast<char*>(Y) + yrow)[ng] = ftz(y);
+      } else {
+        if (bias) y = fadd(y, bias[ng]);
+        y = act_fn(y, act);
+        store_out(Y, yrow, ng, out, y, out_scale);
+      }
+    }
+  }
+}
+
+template <int MT, int TT, int NW, int GMAX>
+hipError_t go_w4_mfma(const W4Args& a, hipStream_t s) {
+  const dim3 grid((a.N + 16 * TT - 1) / (16 * TT), (a.M + MT - 1) / MT), block(NW * 64);
+  const bool simple = !a.bias && a.act == 0 && a.out == 0;
+  const int lda = static_cast<int>(a.lda);
+#define TARS_W4M(BF, SI)                                                                                          \
+  hipLaunchKernelGGL((gemm_w4a16_mfma_kernel<MT, TT, NW, GMAX, BF, SI>), grid, block, 0, s, a.x, a.Wp, a.ws, lda, \
+                     a.M, a.N, a.K, a)
+  if (a.bf16) {
+    if (simple) TARS_W4M(true, true);
+    else TARS_W4M(true, false);
+  } else {
+    if (simple) TARS_W4M(false, true);
+    else TARS_W4M(false, false);
+  }
+#undef TARS_W4M
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_align_w4(const AlignArgs& a, hipStream_t s) {
@@ -494,10 +746,33 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
 // most 2048 k (one chunk per lane) 4 rows per wave in 4-wave workgroups (K = 1536, N = 12288:
 // 4.5 us; 3-, 8- and 12-wave workgroups within 0.2 us, 1 or 2 rows per wave 5.4 - 7.5 us); longer
 // rows one row per wave in 8-wave workgroups (K = 6144, N = 1536: 4.1 - 4.6 us; 4 rows per wave
-// 4.9 us, 12-wave workgroups 7.9 us). Prefill chunks: two activation rows per block, 4 rows per
-// wave (M = 4 / 8 at K = 1536, N = 12288: 11.3 / 19.4 us; four rows per block 12.7 / 20.0 us).
+// 4.9 us, 12-wave workgroups 7.9 us).
+// Several rows: the MFMA form where it is faster than the per-lane form (two activation rows per
+// block, 4 rows per wave), both bit-exact. K = 1536, N = 12288 at M = 2 / 4 / 8 / 16 / 32: per-lane
+// 5.2 / 8.4 / 14.0 / 24.3 / 42.3 us; MFMA 6.4 / 6.5 (4-row tiles, one weight tile per workgroup)
+// / 9.0 (4-row tiles, two weight tiles) / 12.1 / 22.1 us (8-row tiles, two weight tiles). K =
+// 1536, N = 3072 at M = 4 / 8 / 16: per-lane 4.1 / 4.8 / 7.0 us, MFMA 4.5 / 5.1 / 6.0 us. K =
+// 6144, N = 1536 (96 weight tiles) at M = 4 / 8 / 16 / 32: per-lane 6.4 / 9.0 / 11.7 / 19.0 us,
+// MFMA 8.0 / 8.1 (4-row tiles, 16 waves) / 9.0 (8-row tiles) / 12.6 us (8-row tiles, two weight
+// tiles). 16-row tiles ran 21 - 49 us (their x staging spills).
 hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
   const int cpl = (a.K / 32 + 63) / 64;  // chunks per lane
+  if (a.M >= 3 && a.lda <= INT32_MAX) {
+    const int G = a.K / 128;
+    if (a.K <= 2048) {
+      if (a.N >= 8192) {
+        if (a.M <= 4) return go_w4_mfma<4, 1, 4, 16>(a, s);
+        if (a.M <= 8) return go_w4_mfma<4, 2, 4, 16>(a, s);
+        return go_w4_mfma<8, 2, 4, 16>(a, s);
+      }
+      if (a.M > 16) return go_w4_mfma<8, 2, 8, 16>(a, s);
+      if (a.M > 8) return go_w4_mfma<4, 1, 4, 16>(a, s);
+    } else if (a.M > 4) {
+      if (a.M <= 8 || G > 48) return go_w4_mfma<4, 1, 16, 64>(a, s);
+      if (a.M <= 16) return go_w4_mfma<8, 1, 16, 48>(a, s);
+      return go_w4_mfma<8, 2, 16, 48>(a, s);
+    }
+  }
   if (a.M >= 2) return go_cpl<4, 4, 2>(a, cpl, s);
   return cpl == 1 ? go_cpl<4, 4, 1>(a, cpl, s) : go_cpl<8, 1, 1>(a, cpl, s);
 }

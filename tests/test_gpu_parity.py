@@ -492,15 +492,45 @@ def test_w4_shapes_bf16_bias_act(K, M):
     assert same(host(y2), G.gemm_w4(x, Wp, ws, out=OUT_INT8, out_scale=f32(0.25)))
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (3, 1536, 8192), (9, 2048, 80),              # 4-row tiles, one weight tile per workgroup
+    (7, 768, 8192),                              # 4-row tiles, two weight tiles
+    (16, 1536, 8208),                            # 8-row tiles, two weight tiles, 4 waves
+    (20, 512, 304),                              # 8-row tiles, two weight tiles, 8 waves
+    (5, 8192, 48), (12, 8192, 32),               # K > 2048: 4-row tiles, 16 waves, 64 groups
+    (12, 6144, 96), (24, 3072, 112),             # K > 2048: 8-row tiles, one / two weight tiles
+    (2, 256, 16), (3, 4096, 8192), (8, 1024, 256)])  # the per-lane form
+@pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
+def test_w4a16_mfma_shapes(M, K, N, epi):
+    """Every launch shape of the W4A16 GEMM at M >= 2, the INT8-MFMA form's (4- and 8-row
+    activation tiles, one or two weight tiles per workgroup, groups split over 4 to 16 waves) and
+    the per-lane form's beside them: K from 256 to 8192, ragged last tiles, fp16 group scales that
+    are subnormal, zero and infinite, and every output format."""
+    x, Wp, ws, rng = w4_inputs(M * 1000 + K + N, M, N, K)
+    ws = ws.copy()
+    ws[0, 0], ws[1 % N, K // 128 - 1], ws[2 % N, 0] = 0x0001, 0x0000, 0x7C00
+    kw = {}
+    if epi == "bias_silu_bf16":
+        kw = dict(bias=rng.normal(0, 1, N).astype(f32), act=ACT_SILU, out=OUT_BF16)
+    elif epi == "int8":
+        kw = dict(out=OUT_INT8, out_scale=f32(0.125))
+    dkw = {k: (cuda(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+    y = ops.gemm_w4(cuda(x), cuda(Wp), cuda(ws), **dkw)
+    want = G.gemm_w4(x, Wp, ws, **kw)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("K", [1024, 6144])
+@pytest.mark.parametrize("M", [6, 12])
 @pytest.mark.parametrize("bf16", [False, True])
-def test_w4_gemm_special_groups(K, bf16):
-    """The GEMV's in-kernel aligner on groups that leave its fast path: all-zero, tiny (largest
-    exponent below 16), subnormal inputs inside normal groups, +-inf, NaN, and the largest finite
-    values, in rows whose other groups are ordinary (so waves of both kinds meet in one launch)."""
+def test_w4_gemm_special_groups(K, M, bf16):
+    """The in-kernel aligners (the per-lane form's at M = 6, K = 1024, the MFMA form's otherwise)
+    on groups that leave their fast path: all-zero, tiny (largest exponent below 16), subnormal
+    inputs inside normal groups, +-inf, NaN, and the largest finite values, in rows whose other
+    groups are ordinary (so waves of both kinds meet in one launch)."""
     rng = np.random.default_rng(K + bf16)
-    x, Wp, ws, _ = w4_inputs(K * 3 + bf16, 6, 64, K)
-    g = x.reshape(6, K // 128, 128)
+    x, Wp, ws, _ = w4_inputs(K * 3 + bf16 + M, M, 64, K)
+    g = x.reshape(M, K // 128, 128)
     g[0, 1] = 0.0                                                  # all-zero group
     g[0, 2] = rng.normal(0, 1, 128) * np.float32(2.0 ** -115)      # emax < 16
     g[1, 0, ::7] = np.array([1, 0x80000003, 0x007FFFFF], np.uint32).view(f32).repeat(7)[:19]  # subnormals
@@ -508,7 +538,7 @@ def test_w4_gemm_special_groups(K, bf16):
     g[3, K // 128 - 1, 17] = np.nan                                # NaN group
     g[4, 1] = np.float32(3.3e38) * np.sign(rng.normal(0, 1, 128)).astype(f32)
     g[5] = rng.normal(0, 1, (K // 128, 128)) * np.exp2(rng.integers(-126, 100, (K // 128, 1)))
-    x = g.reshape(6, K).astype(f32)
+    x = g.reshape(M, K).astype(f32)
     xin = F.to_bf16_bits(x) if bf16 else x
     y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16)
     want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16)
