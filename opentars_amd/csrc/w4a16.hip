@@ -467,6 +467,158 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
   }
 }
 
+// One activation row with K split over the waves of a workgroup. Wave w owns groups 4 w .. 4 w + 3
+// (one per bank; the last wave two when G % 4 == 2) of the workgroup's 4 RS weight rows, and
+// aligns just those groups of the activation itself (lane l: group 4 w + l / 16, elements
+// 8 (l % 16) .. + 7), so no alignment waits behind a workgroup barrier and each wave's work does
+// not grow with K. Lane 16 u + 4 g + q streams quarter q of group 4 w + g of row 4 s + u for each
+// row set s; the four aligner lanes 16 g + 4 q .. + 3 hold that quarter's 32 elements, so the
+// chunk's four digit planes are one 16-byte read each from the wave's own LDS slot (a wave
+// barrier, no workgroup one). The quad adds its four chunk dots and lane q = 0 stores the group's
+// term (i2f(dot) * ws) * xs in the workgroup's term rows; after the one workgroup barrier, wave
+// 0's lane 4 r + b runs bank b's chain of row r over groups b, b + 4, ... in order from +0
+// (golden.py:315-319) and each quad folds (b0 + b1) + (b2 + b3).
+// Roofline: HBM, K / 2 + K / 64 bytes per weight row; the activation (2 or 4 bytes per element)
+// is read once per workgroup, from L2.
+template <int RS, bool BF16, bool SIMPLE>
+__global__ __launch_bounds__(1024) void gemv_w4a16_kslice_kernel(const void* x, int64_t lda, const uint8_t* Wp,
+                                                                 const uint16_t* ws, int M, int N, int K, W4Args a) {
+  constexpr int R = 4 * RS;
+  __shared__ __align__(16) uint32_t planes[16][4][64];   // [wave][digit plane][aligner lane]
+  __shared__ float xs_t[16][4];                          // [wave][group of the wave]
+  __shared__ float terms[R][kTermStride];                // [row][group]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = K >> 7;
+  const int g0 = 4 * wave, ng = min(4, G - g0);  // 2 or 4 (G is even)
+  const int n0 = blockIdx.x * R;
+
+  // 1. the wave's groups of the activation (lanes of a group past the wave's last shadow its
+  //    first), then the weight chunks and their fp16 scales (rows past N read row N - 1)
+  const int gl = lane >> 4;
+  const int xg = g0 + (gl < ng ? gl : 0);
+  uint32_t xb[8];
+  if constexpr (BF16) {
+    const v4u v = *reinterpret_cast<const v4u*>(static_cast<const char*>(x) + 2 * (xg * kGroup + 8 * (lane & 15)));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xb[2 * j] = v[j] << 16;
+      xb[2 * j + 1] = v[j] & 0xFFFF0000u;
+    }
+  } else {
+    const v4u* src = reinterpret_cast<const v4u*>(static_cast<const char*>(x) + 4 * (xg * kGroup + 8 * (lane & 15)));
+    const v4u v0 = src[0], v1 = src[1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xb[j] = v0[j];
+      xb[4 + j] = v1[j];
+    }
+  }
+  issue_fence();
+  const int u = lane >> 4, gq = (lane >> 2) & 3, q = lane & 3;
+  const int wg = g0 + (gq < ng ? gq : 0);
+  v4u wv[RS];
+  uint32_t wsv[RS];
+#pragma unroll
+  for (int s = 0; s < RS; ++s) {
+    const int64_t row = min(n0 + 4 * s + u, N - 1);
+    wv[s] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(Wp + row * (K >> 1) + 64 * wg + 16 * q));
+    wsv[s] = ws[row * G + wg];
+  }
+  issue_fence();
+  const KArg ka = kernarg_at(kW4ArgsOffset);
+  void* const Y = kload<void*>(ka + offsetof(W4Args, Y));
+  const float* const bias = SIMPLE ? nullptr : kload<const float*>(ka + offsetof(W4Args, bias));
+  const int act = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, act));
+  const int out = SIMPLE ? 0 : kload<int>(ka + offsetof(W4Args, out));
+  const float out_scale = SIMPLE ? 0.0f : kload<float>(ka + offsetof(W4Args, out_scale));
+
+  // 2. alignment into the wave's digit planes and group scales
+  {
+    int mant[8];
+    uint32_t sb;
+    align_elems<8, 16>(xb, mant, sb);
+    uint32_t d[4];
+    digit_planes(mant, d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) planes[wave][i][lane] = d[i];
+    if ((lane & 15) == 0) xs_t[wave][gl] = ffrom(sb);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // 3. dots and terms
+  v4u xp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xp[i] = *reinterpret_cast<const v4u*>(&planes[wave][i][16 * gq + 4 * q]);
+  const float xs = xs_t[wave][gq];
+#pragma unroll
+  for (int s = 0; s < RS; ++s) {
+    int d = chunk_dot_digits(wv[s], xp);
+    d += lane_xor1(d);
+    d += lane_xor2(d);
+    // the contract's fmul(fmul(i2f(d), ws), xs) with its wrappers where they act (see the GEMV)
+    const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), from_fp16_bits(wsv[s])), xs));
+    if (q == 0 && gq < ng) terms[4 * s + u][g0 + gq] = term;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // 4. chains: lane 4 r + b runs bank b of row r (lanes past the last row read row 0)
+  const int r = lane >> 2, bank = lane & 3;
+  const float* trow = terms[r < R ? r : 0];
+  float tv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tv[i] = bank + 4 * i < G ? trow[bank + 4 * i] : 0.0f;
+  float acc = 0.0f;
+  uint32_t mk = ~0u;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (bank + 4 * i < G) {
+      acc = __fadd_rn(acc, tv[i]);
+      mk = min(mk, sub_key(acc));
+    }
+  if (__builtin_expect(mk < kSubKeyNormal, 0)) {
+    acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (bank + 4 * i < G) acc = fadd_chain(acc, tv[i]);
+  }
+  acc = chain_end(acc);
+  const float pair = fadd(acc, lane_xor1(acc));
+  const float other = lane_xor2(pair);
+  const int n = n0 + r;
+  if (bank == 0 && r < R && n < N) {
+    float y = fadd(pair, other);
+    if constexpr (SIMPLE) {
+      static_cast<float*>(Y)[n] = ftz(y);
+    } else {
+      if (bias) y = fadd(y, bias[n]);
+      y = act_fn(y, act);
+      store_out(Y, 0, n, out, y, out_scale);
+    }
+  }
+}
+
+template <int RS>
+hipError_t go_w4_kslice(const W4Args& a, hipStream_t s) {
+  const dim3 grid((a.N + 4 * RS - 1) / (4 * RS)), block(64 * ((a.K / 128 + 3) / 4));
+  const bool simple = !a.bias && a.act == 0 && a.out == 0;
+#define TARS_W4K(BF, SI)                                                                                      \
+  hipLaunchKernelGGL((gemv_w4a16_kslice_kernel<RS, BF, SI>), grid, block, 0, s, a.x, a.lda, a.Wp, a.ws, a.M, \
+                     a.N, a.K, a)
+  if (a.bf16) {
+    if (simple) TARS_W4K(true, true);
+    else TARS_W4K(true, false);
+  } else {
+    if (simple) TARS_W4K(false, true);
+    else TARS_W4K(false, false);
+  }
+#undef TARS_W4K
+  return hipGetLastError();
+}
+
 template <int NW, int U, int MR, int CPL>
 hipError_t go_w4(const W4Args& a, hipStream_t s) {
   const dim3 grid((a.N + NW * U - 1) / (NW * U), (a.M + MR - 1) / MR);
@@ -746,7 +898,11 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
 // most 2048 k (one chunk per lane) 4 rows per wave in 4-wave workgroups (K = 1536, N = 12288:
 // 4.5 us; 3-, 8- and 12-wave workgroups within 0.2 us, 1 or 2 rows per wave 5.4 - 7.5 us); longer
 // rows one row per wave in 8-wave workgroups (K = 6144, N = 1536: 4.1 - 4.6 us; 4 rows per wave
-// 4.9 us, 12-wave workgroups 7.9 us).
+// 4.9 us, 12-wave workgroups 7.9 us). Past 2048 k the K-split form where it measured faster:
+// 16 rows per workgroup from N = 4096 (K = 6144, N = 4096 / 8192: 5.9 / 9.4 -> 5.1 / 7.1 us;
+// K = 3072, N = 4096: 4.6 -> 4.1 us; K = 8192, N = 8192: 12.0 -> 9.3 us), and at K = 8192 with
+// fewer rows 4 or 8 rows per workgroup (N = 1024 / 2048: 4.5 / 5.3 -> 3.8 / 4.5 us); K = 6144 at
+// N <= 2048 stays on whole-row waves (N = 1536: 3.7 us, K-split 3.9 - 4.4 us).
 // Several rows: the MFMA form where it is faster than the per-lane form (two activation rows per
 // block, 4 rows per wave), both bit-exact. K = 1536, N = 12288 at M = 2 / 4 / 8 / 16 / 32: per-lane
 // 5.2 / 8.4 / 14.0 / 24.3 / 42.3 us; MFMA 6.4 / 6.5 (4-row tiles, one weight tile per workgroup)
@@ -774,6 +930,10 @@ hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
     }
   }
   if (a.M >= 2) return go_cpl<4, 4, 2>(a, cpl, s);
+  if (cpl >= 2) {
+    if (a.N >= 4096) return go_w4_kslice<4>(a, s);
+    if (a.K > 6144) return a.N <= 1024 ? go_w4_kslice<1>(a, s) : go_w4_kslice<2>(a, s);
+  }
   return cpl == 1 ? go_cpl<4, 4, 1>(a, cpl, s) : go_cpl<8, 1, 1>(a, cpl, s);
 }
 

@@ -520,6 +520,56 @@ def test_w4a16_mfma_shapes(M, K, N, epi):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("K,N", [(8192, 1008), (8192, 2048), (6400, 1040), (6144, 4096), (2304, 4096),
+                                 (3328, 4112)])
+@pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
+def test_w4a16_ksplit_waves(K, N, epi):
+    """One activation row with K split over the waves of a workgroup (K > 2048 at N >= 4096, and
+    K > 6144): 4, 8 and 16 weight rows per workgroup, a last wave with two groups (G % 4 == 2 at
+    K = 2304, 3328, 6400), bf16 activations on half the cases, every output format."""
+    x, Wp, ws, rng = w4_inputs(K + N, 1, N, K)
+    ws = ws.copy()
+    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1] = 0x0001, 0x0000, 0x7C00
+    bf16 = (K // 256) % 2 == 0
+    xin = F.to_bf16_bits(x) if bf16 else x
+    kw = {}
+    if epi == "bias_silu_bf16":
+        kw = dict(bias=rng.normal(0, 1, N).astype(f32), act=ACT_SILU, out=OUT_BF16)
+    elif epi == "int8":
+        kw = dict(out=OUT_INT8, out_scale=f32(0.125))
+    dkw = {k: (cuda(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16, **dkw)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16, **kw)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("K,N", [(8192, 64), (2304, 4096)])
+@pytest.mark.parametrize("kind", ["mixed", "inf", "nan"])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_w4a16_ksplit_special_groups(K, N, kind, bf16):
+    """The K-split form's per-wave aligner on one row's special groups: all-zero, tiny (largest
+    exponent below 16), subnormals inside a normal group and the largest finite values beside
+    ordinary groups; an infinite group; a NaN group (waves of both kinds in one launch)."""
+    rng = np.random.default_rng(K + N + bf16)
+    x, Wp, ws, _ = w4_inputs(K * 5 + bf16, 1, N, K)
+    g = x.reshape(K // 128, 128)
+    if kind == "mixed":
+        g[1] = 0.0
+        g[2] = rng.normal(0, 1, 128) * np.float32(2.0 ** -115)
+        g[5, ::7] = np.array([1, 0x80000003, 0x007FFFFF], np.uint32).view(f32).repeat(7)[:19]
+        g[9] = np.float32(3.3e38) * np.sign(rng.normal(0, 1, 128)).astype(f32)
+    elif kind == "inf":
+        g[7, 5], g[7, 9] = np.inf, -np.inf
+        g[8, 3] = np.inf
+    else:
+        g[K // 128 - 1, 17] = np.nan
+    x = g.reshape(1, K).astype(f32)
+    xin = F.to_bf16_bits(x) if bf16 else x
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("K", [1024, 6144])
 @pytest.mark.parametrize("M", [6, 12])
 @pytest.mark.parametrize("bf16", [False, True])
