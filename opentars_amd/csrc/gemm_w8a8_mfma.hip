@@ -306,20 +306,22 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma_tile_kernel(const int8_t* A
   const int m0 = (t % mt) * BM, n0 = (t / mt) * BN;
 
   // Epilogue operands of this lane's outputs: rows (wm TI + i) 16 + li, columns
-  // (wn TJ + j) 16 + 4 lg + v. Every load is unconditional (an absent operand reads scol).
+  // (wn TJ + j) 16 + 4 lg + v, the four columns of a lane as one 16-byte load (every vector
+  // memory instruction costs issue time, whatever its width). N % 16 == 0, so a 16-column block
+  // lies wholly inside or wholly past the matrix; one past it reads the last block (its outputs
+  // are not stored). A per-tensor scale (one float) and an absent bias take the general
+  // instance's uniform branches instead.
   float sr[TI], sc[TJ][4], bi[TJ][4], chain[TI][TJ][4];
 #pragma unroll
-  for (int j = 0; j < TJ; ++j)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int n = min(n0 + (wn * TJ + j) * 16 + 4 * lg + v, N - 1);
-      if constexpr (SIMPLE) {
-        sc[j][v] = scol[n];
-      } else {
-        sc[j][v] = scol[tl.scol_per_tensor ? 0 : n];
-        bi[j][v] = *(tl.bias ? tl.bias + n : scol);
-      }
-    }
+  for (int j = 0; j < TJ; ++j) {
+    const int nb = min(n0 + (wn * TJ + j) * 16, N - 16) + 4 * lg;
+    float4 c4, b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (SIMPLE || !tl.scol_per_tensor) c4 = *reinterpret_cast<const float4*>(scol + nb);
+    else c4 = make_float4(scol[0], scol[0], scol[0], scol[0]);
+    if (!SIMPLE && tl.bias) b4 = *reinterpret_cast<const float4*>(tl.bias + nb);
+    sc[j][0] = c4.x, sc[j][1] = c4.y, sc[j][2] = c4.z, sc[j][3] = c4.w;
+    bi[j][0] = b4.x, bi[j][1] = b4.y, bi[j][2] = b4.z, bi[j][3] = b4.w;
+  }
 #pragma unroll
   for (int i = 0; i < TI; ++i) sr[i] = *(srow ? srow + min(m0 + (wm * TI + i) * 16 + li, M - 1) : scol);
   issue_fence();
@@ -474,8 +476,10 @@ hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
 //    workgroups per CU: M=256 K=1024 N=3072 7.5 -> 5.5 us (the 64 x 64 / 16-row-load tiles before);
 //  * 64 x 64 tiles (4 waves of 32 x 32, 256-byte stages, 3 slots) when they give 512 or more:
 //    M=1024 K=1024 N=3072 16.5 -> 15.8 us;
-//  * 32 x 32 tiles (4 waves of 16 x 16) with 1024-byte stages in 2 slots when K is a multiple of
-//    1024 and they give at most 1.25 workgroups per CU: M=256 K=3072 N=1024 8.6 -> 5.9 us;
+//  * 32 x 32 tiles (4 waves of 16 x 16) with 512-byte stages in 3 slots when K is a multiple of
+//    1024 and they give at most 1.25 workgroups per CU: M=256 K=3072 N=1024 8.6 -> 5.9 us with
+//    1024-byte stages in 2 slots, 5.76 us with these (K = 1024 / 2048 / 4096 at N = 1024: 4.04 /
+//    4.86 / 6.72 -> 3.77 / 4.77 / 6.68 us; 512-byte stages in 4 slots 0.1 - 0.3 us slower);
 //  * 32 x 32 tiles with 256-byte stages in 3 slots otherwise: M=64 K=1024 N=3072 5.2 -> 3.8 us.
 bool whole_stages(const MfmaArgs& a, int ks) {
   for (int i = 0; i < a.nseg; ++i)
@@ -493,7 +497,7 @@ hipError_t run(const MfmaArgs& a, hipStream_t s) {
   const int64_t t48 = tiles(a, 64, 48), t32 = tiles(a, 32, 32);
   if (t48 >= 192 && t48 <= 320) return go_tile<64, 48, 4, 1, 256, 3>(a, s);
   if (tiles(a, 64, 64) >= 512) return go_tile<64, 64, 2, 2, 256, 3>(a, s);
-  if (t32 <= 320 && whole_stages(a, 1024)) return go_tile<32, 32, 2, 2, 1024, 2>(a, s);
+  if (t32 <= 320 && whole_stages(a, 1024)) return go_tile<32, 32, 2, 2, 512, 3>(a, s);
   return go_tile<32, 32, 2, 2, 256, 3>(a, s);
 }
 

@@ -288,8 +288,9 @@ def test_ksplit_gemv_block_shapes(split, M):
                                           (100, 1040, [2048, 1024]), (33, 96, [1040, 256])])
 def test_ksplit_staged_prompt_tiles(M, N, blocks):
     """The K split on the LDS tile kernel: 32 x 32 tiles with 256-byte stages (M=17, 45), 64 x 48
-    tiles (M=200, N=3072), 32 x 32 tiles with 1024-byte stages (M=100, N=1040, blocks of whole
-    KiB), and a block that is not a whole number of stages (1040), which takes the direct tiles."""
+    tiles (M=200, N=3072), 32 x 32 tiles with 512-byte stages in 3 slots (M=100, N=1040, blocks
+    of whole KiB), and a block that is not a whole number of stages (1040), which takes the direct
+    tiles."""
     x, q, s, W, scol, _ = w8_inputs(M * 31 + N, M, N, sum(blocks))
     parts = np.split(W, np.cumsum(blocks)[:-1], axis=1)
     parts = [np.ascontiguousarray(b) for b in parts]
@@ -338,7 +339,8 @@ def test_epilogue_matrix_prompt_tiles(qm, act, out):
 def test_epilogue_matrix_staged_tiles(qm, act, out, M, N, K):
     """The LDS tile kernel (K a multiple of 256) through every scale mode and output format with a
     bias, ragged last row and column tiles, a huge scale and int8 -128: 32 x 32 tiles with
-    256-byte stages (K=768), with 1024-byte stages (K=2048), and 64 x 48 tiles (M=200, N=3088)."""
+    256-byte stages (K=768), with 512-byte stages in 3 slots (K=2048), and 64 x 48 tiles (M=200,
+    N=3088)."""
     rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, M, N, K, "staged")).encode()))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
