@@ -151,12 +151,13 @@ _MAGIC_ADDEND = "0x4b400000"  # 1.5 * 2^23
 
 def _fp32_fmas_other_than_rounding(dis: str) -> list:
     """Every fused fp32 multiply-add in `dis` except the W4A16 aligner's mantissa rounding, which is
-    RN(x * p + 1.5 * 2^23) in `align_w4_kernel` and `gemv_w4a16_kernel`: `v_fmaak_f32` with that
-    literal addend, or `v_fmac_f32` whose accumulator's last write is a move of that literal."""
+    RN(x * p + 1.5 * 2^23) in `align_w4_kernel` and the W4A16 GEMM kernels (`gemv_w4a16_kernel`,
+    `gemv_w4a16_kslice_kernel`, `gemm_w4a16_mfma_kernel`): `v_fmaak_f32` with that literal addend,
+    or `v_fmac_f32` whose accumulator's last write is a move of that literal."""
     bad, fn, body = [], "", []
 
     def check(fn, body):
-        rounding_ok = "align_w4" in fn or "gemv_w4a16" in fn
+        rounding_ok = "align_w4" in fn or "w4a16" in fn
         for i, ins in enumerate(body):
             m = re.match(r"(v_(?:fma|fmac|mad|fmaak|fmamk|mac)_f32\w*)\s+(.*)", ins)
             if not m:
