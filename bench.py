@@ -656,15 +656,48 @@ def rotated(torch, make, per_copy_bytes: int):
 CONFIG_REPS = 2000
 
 
+def time_graph_replays(torch, g, reps: int, warmup: int) -> tuple[float, list[float]]:
+    """Seconds per replay over `reps` back-to-back replays, and each replay's own seconds (an event
+    recorded after every replay on the current stream)."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record()
+    for i in range(reps):
+        g.replay()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) / 1e3 for i in range(reps)]
+    return ev[0].elapsed_time(ev[-1]) / 1e3 / reps, per
+
+
+def quantiles(xs: list[float], qs=(0.1, 0.5, 0.9)) -> list[float]:
+    """Linear-interpolation quantiles of `xs` (numpy's default method)."""
+    s = sorted(xs)
+    out = []
+    for q in qs:
+        p = q * (len(s) - 1)
+        i = int(p)
+        out.append(s[i] + (s[min(i + 1, len(s) - 1)] - s[i]) * (p - i))
+    return out
+
+
 def measure_config(torch, launches, reps_target: int | None = None) -> dict:
+    """One config's launches (rotated over distinct weight copies) as a graph, replayed back to back:
+    the mean µs per call over every replay (two events around the whole run), then, in a second
+    run with an event after every replay, the p10 / median / p90 of each replay's per-call time
+    (kept apart so the per-replay events do not touch the mean)."""
     reps_target = reps_target or CONFIG_REPS
     g = capture(torch, launches)
     reps = max(3, reps_target // len(launches))
     t = time_graph(torch, g, reps, warmup=2) / len(launches)
+    _, per = time_graph_replays(torch, g, reps, warmup=0)
     nbytes, ops = launches[0].nbytes, launches[0].ops
     r = {"us_per_call": round(t * 1e6, 3), "GBps": round(nbytes / t / 1e9, 1),
          "hbm_frac": round(nbytes / t / HBM_PEAK, 4), "bytes_per_call": nbytes,
-         "distinct_copies": len(launches)}
+         "distinct_copies": len(launches), "replays": reps,
+         "us_per_call_p10_p50_p90": [round(v * 1e6 / len(launches), 3) for v in quantiles(per)]}
     if ops:
         r["TOPS"] = round(ops / t / 1e12, 2)
         r["int8_peak_frac"] = round(ops / t / INT8_PEAK, 5)

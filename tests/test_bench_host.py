@@ -167,3 +167,12 @@ def test_trace_summary_per_row(bench, tmp_path):
     assert t["rows"][f"{other} @ down"]["trace_dispatches"] == 1
     assert (tmp_path / "kernels.table.md").read_text().count("\n") == 4
 
+
+
+def test_quantiles_match_numpy(bench):
+    """The per-config p10 / median / p90 use numpy's default (linear) quantiles."""
+    import numpy as np
+    rng = np.random.default_rng(7)
+    for n in (1, 2, 3, 10, 11, 500):
+        xs = list(rng.normal(3.0, 0.2, n))
+        assert np.allclose(bench.quantiles(xs), np.quantile(xs, [0.1, 0.5, 0.9]), rtol=0, atol=1e-12)
