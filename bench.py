@@ -1044,6 +1044,9 @@ def config_suite(torch, lib, seed: int, attention: bool = True, cpu: bool = True
         ad = res["attention_decode_qwen3_t250"]
         log(f"attention t=250: {ad['op_by_op']['us_per_layer']} us per layer op by op, "
             f"{ad['fused_op']['us_per_layer']} us fused")
+    for r in res.values():
+        # every config's inputs come from one CUDA generator with this seed, drawn in config order
+        r["inputs_seed"] = seed + 1
     attach_counters(res)
     return res
 
