@@ -503,22 +503,24 @@ def test_w4_shapes_bf16_bias_act(K, M):
     (12, 6144, 96), (24, 3072, 112),             # K > 2048: 8-row tiles, one / two weight tiles
     (2, 256, 16), (3, 4096, 8192), (8, 1024, 256)])  # the per-lane form
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
-def test_w4a16_mfma_shapes(M, K, N, epi):
+@pytest.mark.parametrize("bf16", [False, True])
+def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
     """Every launch shape of the W4A16 GEMM at M >= 2, the INT8-MFMA form's (4- and 8-row
     activation tiles, one or two weight tiles per workgroup, groups split over 4 to 16 waves) and
     the per-lane form's beside them: K from 256 to 8192, ragged last tiles, fp16 group scales that
-    are subnormal, zero and infinite, and every output format."""
+    are subnormal, zero and infinite, fp32 and bf16 activation rows, and every output format."""
     x, Wp, ws, rng = w4_inputs(M * 1000 + K + N, M, N, K)
     ws = ws.copy()
     ws[0, 0], ws[1 % N, K // 128 - 1], ws[2 % N, 0] = 0x0001, 0x0000, 0x7C00
+    xin = F.to_bf16_bits(x) if bf16 else x
     kw = {}
     if epi == "bias_silu_bf16":
         kw = dict(bias=rng.normal(0, 1, N).astype(f32), act=ACT_SILU, out=OUT_BF16)
     elif epi == "int8":
         kw = dict(out=OUT_INT8, out_scale=f32(0.125))
     dkw = {k: (cuda(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
-    y = ops.gemm_w4(cuda(x), cuda(Wp), cuda(ws), **dkw)
-    want = G.gemm_w4(x, Wp, ws, **kw)
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16, **dkw)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16, **kw)
     assert same(host(y), want), mismatch(host(y), want)
 
 
