@@ -121,9 +121,23 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(const int8_t* A, in
   RowColEpilogue epi{};
 
   if constexpr (CPL > 0) {
-    // one batch of loads: activations, epilogue operands, weights (rows past N and chunks past K
+    // one batch of loads: weights, activations, epilogue operands (rows past N and chunks past K
     // read the matrix start; a chunk past K is zeroed on the activation side, which zeroes its
-    // products, and rows past N are never stored)
+    // products, and rows past N are never stored). The weights go first: they come from HBM and
+    // are the call's long pole, nothing runs before every load of the batch has landed, and each
+    // load instruction costs issue time.
+    const v4i* wbase = reinterpret_cast<const v4i*>(W);
+    v4i wv[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int n = n0 + u;
+      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = sub + j * L;
+        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : wbase);
+      }
+    }
     v4i xv[MR][CPL];
 #pragma unroll
     for (int r = 0; r < MR; ++r) {
@@ -137,18 +151,6 @@ __global__ __launch_bounds__(kThreads) void gemv_w8a8_kernel(const int8_t* A, in
     }
     sc = scol[per_tensor ? 0 : nc];
     sr = *(srow ? srow + mc : scol);
-    const v4i* wbase = reinterpret_cast<const v4i*>(W);
-    v4i wv[U][CPL];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int n = n0 + u;
-      const v4i* wrow = reinterpret_cast<const v4i*>(W + static_cast<int64_t>(n) * K);
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = sub + j * L;
-        wv[u][j] = __builtin_nontemporal_load(n < N && c < C ? wrow + c : wbase);
-      }
-    }
     issue_fence();
     Y = kload<void*>(ka + offsetof(W8A8Args, Y));
     ldy = kload<int64_t>(ka + offsetof(W8A8Args, ldy));
@@ -270,7 +272,9 @@ __global__ __launch_bounds__(64 * NWG) void gemv_w8a8_ksplit2_kernel(const int8_
 
   // one batch of loads: activations, epilogue operands, weights (a chunk past the row re-reads the
   // row's last chunk and is zeroed on the activation side; a row past N re-reads row N - 1, never
-  // stored)
+  // stored). The activations go first: loads complete in issue order, so each chunk's dot can run
+  // as its weights land (weights first, every dot waited for the last activation load: 3.48 ->
+  // 3.72 us at C2).
   const v4i* xrow = reinterpret_cast<const v4i*>(A + static_cast<int64_t>(m) * lda);
   v4i xv[CPL];
 #pragma unroll
