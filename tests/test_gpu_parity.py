@@ -524,6 +524,26 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (1, 1536, 256), (1, 6144, 64),               # whole-row waves: one chunk per lane, three
+    (1, 8192, 64), (1, 2304, 4096),              # K split over the waves: 4 and 16 rows per workgroup
+    (2, 1024, 64),                               # the per-lane form with two activation rows
+    (3, 1536, 8192), (12, 6144, 96), (20, 512, 304)])  # the MFMA form: 4- and 8-row tiles
+@pytest.mark.parametrize("bf16", [False, True])
+def test_w4_strided_rows_and_untouched_gaps(M, K, N, bf16):
+    """Every W4A16 kernel form on activation rows and output rows with a gap after each (lda and
+    ldy above the row): the dense result, and the output gaps left as they were."""
+    x, Wp, ws, _ = w4_inputs(M * 7 + K + N + bf16, M, N, K)
+    xin = F.to_bf16_bits(x) if bf16 else x
+    xbig = np.concatenate([xin, np.zeros((M, 64), xin.dtype)], axis=1)
+    ybig = torch.full((M, N + 12), -7.0, dtype=torch.float32, device="cuda")
+    ops.gemm_w4(cuda(xbig)[:, :K], cuda(Wp), cuda(ws), y=ybig[:, :N], x_is_bf16=bf16)
+    yb = host(ybig)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16)
+    assert same(yb[:, :N].copy(), want), mismatch(yb[:, :N].copy(), want)
+    assert (yb[:, N:] == -7.0).all()
+
+
 @pytest.mark.parametrize("K,N", [(8192, 1008), (8192, 2048), (6400, 1040), (6144, 4096), (2304, 4096),
                                  (3328, 4112)])
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
