@@ -537,9 +537,9 @@ def time_graph(torch, g, reps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
-def plain_rows_per_wave(rows: int) -> int:
+def plain_rows_per_wave(rows: int, M: int = 1, K: int = 1024) -> int:
     """The plain GEMV's rows-per-wave rule (gemv_w8a8.hip, plain_rows_per_wave)."""
-    return 1 if rows < 32768 else 4
+    return 4 if rows >= 32768 else 2 if M >= 3 and rows >= 2048 and K <= 8192 else 1
 
 
 def fused_rows_per_wave(rows: int, K: int) -> int:
@@ -717,7 +717,7 @@ CONFIG_KERNELS = {
     "lm_head_fused_quant_M1_K1024_N151936": ("quant_gemv_w8a8_kernel<64, 1, 4, true, false>", 2430976),
     "c2_gemma3_down_ksplit_3456+3456": ("gemv_w8a8_ksplit2_kernel<7, 1, 5>", 73920),
     "c2_gemma3_down_ksplit_4096+2816": ("gemv_w8a8_ksplit2_kernel<7, 1, 5>", 73920),
-    "c4_prefill_M4_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 1, 4, true>", 196608),
+    "c4_prefill_M4_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 2, 4, true>", 98304),
     "c4_prefill_M4_K3072_N1024": ("gemv_w8a8_kernel<64, 3, 1, 4, true>", 65536),
     "c4_prefill_M4_K1024_N3072_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 98304),
     "c4_prefill_M4_K3072_N1024_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 32768),

@@ -823,8 +823,14 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_norm_kernel(const float* 
 // Rows per wave (measured on MI355X with the kernels above, weights cold). A launch wants at least
 // 256 workgroups (one per CU); below that, more rows per wave only lengthen each wave's chain.
 // Plain GEMV: 1 row per wave below 32768 rows (K = 1024, N = 3072: 2.76 us at U = 1, 2.78 at 2,
-// 3.04 at 4; M = 4 rows of activations: 3.30 us at U = 1 vs 3.66 at 2), 4 above (the head).
-int plain_rows_per_wave(int64_t rows) { return rows < 32768 ? 1 : 4; }
+// 3.04 at 4), 4 above (the head). Three or more activation rows (4 per workgroup row, the weight
+// loads issued first): 2 rows per wave where that still leaves >= 256 workgroups, which halves
+// the activation loads per weight row (M = 4, K = 1024, N = 3072: 2.83 -> 2.66 us; K = 2048,
+// N = 2048: 2.99 -> 2.80 us; with 1024 rows, 2.25 / 2.66 us at U = 1 against 2.36 / 2.89 at 2).
+// Rows of more than 8192 k (no activation chunks held in registers) keep one row per wave.
+int plain_rows_per_wave(int64_t rows, int M, int K) {
+  return rows >= 32768 ? 4 : (M >= 3 && rows >= 2048 && K <= 8192) ? 2 : 1;
+}
 
 // Fused quantize + GEMV: every workgroup re-quantizes the activation row, so U is the largest of
 // 1, 2, 4 that still leaves >= 256 workgroups, doubled when the grid would fill one wave of
@@ -1015,7 +1021,7 @@ struct GoFused {
 }  // namespace
 
 hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s) {
-  return dispatch<const W8A8Args, GoPlain>(a, a.K, plain_rows_per_wave(a.N), s);
+  return dispatch<const W8A8Args, GoPlain>(a, a.K, plain_rows_per_wave(a.N, a.M, a.K), s);
 }
 
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
