@@ -1024,7 +1024,34 @@ hipError_t launch_gemv_w8a8(const W8A8Args& a, hipStream_t s) {
   return dispatch<const W8A8Args, GoPlain>(a, a.K, plain_rows_per_wave(a.N, a.M, a.K), s);
 }
 
+// Consecutive matrices that continue one another (weights, column scales, biases and outputs each
+// directly after the previous matrix's, one epilogue) run as one taller matrix: the same rows with
+// the same arithmetic, in one launch of the full height instead of equal pieces in grid z (an
+// exported lm_head's row blocks, 4 x 37984 rows of one embedding, then run as the one 151936-row
+// launch the direct call gives the whole head).
+static void merge_continuing(QuantGemvArgs& a) {
+  int n = 0;
+  for (int i = 0; i < a.ngroups; ++i) {
+    const GemvGroup& c = a.g[i];
+    if (n > 0) {
+      GemvGroup& p = a.g[n - 1];
+      const int64_t r = p.N;
+      const RowColEpilogue &pe = p.epi, &ce = c.epi;
+      const bool same_epi = !pe.scol_per_tensor && !ce.scol_per_tensor && pe.act == ce.act && pe.out == ce.out &&
+                            pe.out_scale == ce.out_scale && (pe.bias == nullptr) == (ce.bias == nullptr);
+      if (same_epi && c.W == p.W + r * a.K && ce.scol == pe.scol + r && (!pe.bias || ce.bias == pe.bias + r) &&
+          c.ldy == p.ldy && c.Y == static_cast<char*>(p.Y) + r * out_bytes(pe.out) && r + c.N <= INT32_MAX) {
+        p.N += c.N;
+        continue;
+      }
+    }
+    a.g[n++] = c;
+  }
+  a.ngroups = n;
+}
+
 hipError_t launch_quant_gemv_w8a8(QuantGemvArgs& a, hipStream_t s) {
+  if (!a.prod) merge_continuing(a);
   int64_t rows = 0;
   for (int i = 0; i < a.ngroups; ++i) rows += a.g[i].N;
   int u = fused_rows_per_wave(rows, a.K);
