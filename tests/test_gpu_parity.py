@@ -499,7 +499,7 @@ def test_w4_shapes_bf16_bias_act(K, M):
     (7, 768, 8192),                              # 4-row tiles, two weight tiles
     (16, 1536, 8208),                            # 8-row tiles, two weight tiles, 4 waves
     (20, 512, 304),                              # 8-row tiles, two weight tiles, 8 waves
-    (5, 8192, 48), (12, 8192, 32),               # K > 2048: 4-row tiles, 16 waves, 64 groups
+    (12, 8192, 32),                              # K > 2048: 4-row tiles, 16 waves, 64 groups
     (12, 6144, 96), (24, 3072, 112),             # K > 2048: 8-row tiles, one / two weight tiles
     (2, 256, 16), (3, 4096, 8192), (8, 1024, 256)])  # the per-lane form
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
@@ -512,6 +512,32 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
     x, Wp, ws, rng = w4_inputs(M * 1000 + K + N, M, N, K)
     ws = ws.copy()
     ws[0, 0], ws[1 % N, K // 128 - 1], ws[2 % N, 0] = 0x0001, 0x0000, 0x7C00
+    xin = F.to_bf16_bits(x) if bf16 else x
+    kw = {}
+    if epi == "bias_silu_bf16":
+        kw = dict(bias=rng.normal(0, 1, N).astype(f32), act=ACT_SILU, out=OUT_BF16)
+    elif epi == "int8":
+        kw = dict(out=OUT_INT8, out_scale=f32(0.125))
+    dkw = {k: (cuda(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16, **dkw)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16, **kw)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (2, 6144, 1536), (4, 8192, 1008), (5, 8192, 48),        # 8-wave workgroups, one row per wave
+    (4, 6144, 1536), (3, 3072, 1040), (8, 3072, 1024),      # two rows per wave (ragged N = 1040)
+    (2, 4096, 8192), (6, 6144, 1536), (7, 4096, 2048),      # four rows per wave
+    (2, 2304, 8208)])                                       # wider: the 4-row waves of 4-wave workgroups
+@pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
+def test_w4a16_two_row_blocks_past_2048(M, K, N, epi):
+    """The per-lane W4A16 form with two activation rows per workgroup past 2048 k (M = 2 to 8): every
+    workgroup shape its rule picks, bf16 activations on half the cases, every output format, fp16
+    scales that are subnormal, zero and infinite."""
+    x, Wp, ws, rng = w4_inputs(M * 13 + K + N, M, N, K)
+    ws = ws.copy()
+    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1] = 0x0001, 0x0000, 0x7C00
+    bf16 = (K // 256 + M) % 2 == 0
     xin = F.to_bf16_bits(x) if bf16 else x
     kw = {}
     if epi == "bias_silu_bf16":
@@ -598,7 +624,7 @@ def test_w4a16_ksplit_special_groups(K, N, kind, bf16):
 @pytest.mark.parametrize("M", [6, 12])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_w4_gemm_special_groups(K, M, bf16):
-    """The in-kernel aligners (the per-lane form's at M = 6, K = 1024, the MFMA form's otherwise)
+    """The in-kernel aligners (the per-lane form's at M = 6, the MFMA form's at M = 12)
     on groups that leave their fast path: all-zero, tiny (largest exponent below 16), subnormal
     inputs inside normal groups, +-inf, NaN, and the largest finite values, in rows whose other
     groups are ordinary (so waves of both kinds meet in one launch)."""

@@ -400,11 +400,12 @@ def test_chains_whose_partial_sums_are_subnormal(seed, fusion):
         y, ldy16 = stride_fields(p, M, 4 * N)
         p.add(OPCODE=Q.OP_FDOT, CTRL=nn, EPI=Q.epi(), A_OFF=a, W_OFF=w, Y_OFF=y, M=M, N=N, K=K, GROUP_SIZE=gs,
               LDA16=lda16, LDY16=ldy16)
-    # the per-lane form (M <= 2, and M = 4 on a narrow matrix); the K split over waves (M = 1,
-    # K = 6400: 50 groups, the last wave two); the INT8 MFMA form with 4-row tiles (M = 12), 8-row
-    # tiles over two weight tiles (M = 20), and 4-row tiles over 16 waves (M = 6, K = 3072)
+    # the per-lane form (M <= 2, M = 4 on a narrow matrix, and M = 6 past 2048 k in 8-wave
+    # workgroups); the K split over waves (M = 1, K = 6400: 50 groups, the last wave two); the INT8
+    # MFMA form with 4-row tiles (M = 12), 8-row tiles over two weight tiles (M = 20), and 8-row
+    # tiles over 16 waves (M = 12, K = 3072)
     for M, N, K in ((1, 256, 1280), (2, 64, 1536), (4, 32, 1280), (1, 64, 6400), (12, 32, 1280),
-                    (20, 64, 1280), (6, 48, 3072)):
+                    (20, 64, 1280), (6, 48, 3072), (12, 48, 3072)):
         add_w4_cancelling(p, M, N, K)
     prev = NQ.set_fusion(fusion)
     try:
