@@ -904,13 +904,16 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
 // fewer rows 4 or 8 rows per workgroup (N = 1024 / 2048: 4.5 / 5.3 -> 3.8 / 4.5 us); K = 6144 at
 // N <= 2048 stays on whole-row waves (N = 1536: 3.7 us, K-split 3.9 - 4.4 us).
 // Several rows: the MFMA form where it is faster than the per-lane form (two activation rows per
-// block), both bit-exact. Past 2048 k and up to 8 rows, the per-lane form in 8-wave workgroups
-// with the fewest rows per wave that keep the grid at most 256 workgroups, which beat both the
-// 4-row waves tuned at 1536 k and the MFMA form: M = 2 / 4 / 8 at K = 6144, N = 1536: 6.35 / 6.43
-// / 8.12 -> 4.72 / 5.58 / 7.54 us; at K = 3072, N = 1024: 4.35 / 4.44 / 6.21 -> 3.50 / 3.63 / 4.16
-// us; M = 4 / 8 at K = 8192, N = 1024: 8.08 / 8.91 -> 6.17 / 7.27 us; at K = 4096, N = 2048: 4.53 /
-// 7.33 -> 4.29 / 5.47 us (M = 16 at K = 6144: MFMA 9.2 us, per-lane 11.3 - 15.5 us). Wider
-// matrices keep the 4-row waves (M <= 2, and M <= 4 past 2048 k) or the MFMA form. K = 1536, N = 12288 at M = 2 / 4 / 8 / 16 / 32: per-lane
+// block), both bit-exact. Up to 8 rows, the per-lane form in 8-wave workgroups with the fewest rows
+// per wave that keep the grid at most 256 workgroups, which beat both the 4-row waves tuned at
+// K = 1536, N = 12288 and the MFMA form: M = 2 / 4 / 8 at K = 6144, N = 1536: 6.35 / 6.43 / 8.12 ->
+// 4.72 / 5.58 / 7.54 us; at K = 3072, N = 1024: 4.35 / 4.44 / 6.21 -> 3.50 / 3.63 / 4.16 us; M = 4 /
+// 8 at K = 8192, N = 1024: 8.08 / 8.91 -> 6.17 / 7.27 us; at K = 4096, N = 2048: 4.53 / 7.33 -> 4.29
+// / 5.47 us; M = 2 at K = 2048, N = 2048: 3.08 -> 2.87 us; M = 4 at K = 1536, N = 3072: 4.06 ->
+// 3.58 us; M = 7 at K = 768, N = 2048: 3.93 -> 3.58 us (M = 2 at K = 512, N = 4096: 2.96 -> 3.05 us;
+// M = 16 at K = 6144: MFMA 9.2 us, per-lane 11.3 - 15.5 us). Wider matrices keep the 4-row waves of
+// 4-wave workgroups (M = 2: K = 1536, N = 12288 5.1 us; M = 6 / 8 at N = 3072: 4.6 / 4.7 us) or the
+// MFMA form. K = 1536, N = 12288 at M = 2 / 4 / 8 / 16 / 32: per-lane
 // 5.2 / 8.4 / 14.0 / 24.3 / 42.3 us; MFMA 6.4 / 6.5 (4-row tiles, one weight tile per workgroup)
 // / 9.0 (4-row tiles, two weight tiles) / 12.1 / 22.1 us (8-row tiles, two weight tiles). K =
 // 1536, N = 3072 at M = 4 / 8 / 16: per-lane 4.1 / 4.8 / 7.0 us, MFMA 4.5 / 5.1 / 6.0 us. K =
@@ -919,9 +922,9 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
 // tiles). 16-row tiles ran 21 - 49 us (their x staging spills).
 hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
   const int cpl = (a.K / 32 + 63) / 64;  // chunks per lane
-  if (a.M >= 2 && a.M <= 8 && cpl >= 2) {
-    // past 2048 k: two activation rows per workgroup in 8-wave workgroups, the fewest rows per wave
-    // (1, 2, 4) that keep the grid at most 256 workgroups
+  if (a.M >= 2 && a.M <= 8) {
+    // two activation rows per workgroup in 8-wave workgroups, the fewest rows per wave (1, 2, 4)
+    // that keep the grid at most 256 workgroups
     const int64_t mb = (a.M + 1) / 2;
     auto wgs = [&](int u) { return static_cast<int64_t>((a.N + 8 * u - 1) / (8 * u)) * mb; };
     if (wgs(1) <= 256) return go_cpl<8, 1, 2>(a, cpl, s);

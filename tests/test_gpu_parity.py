@@ -526,14 +526,17 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
 
 @pytest.mark.parametrize("M,K,N", [
     (2, 6144, 1536), (4, 8192, 1008), (5, 8192, 48),        # 8-wave workgroups, one row per wave
+    (2, 2048, 2048), (4, 1024, 1024),
     (4, 6144, 1536), (3, 3072, 1040), (8, 3072, 1024),      # two rows per wave (ragged N = 1040)
+    (4, 2048, 2048), (5, 2048, 1024),
     (2, 4096, 8192), (6, 6144, 1536), (7, 4096, 2048),      # four rows per wave
-    (2, 2304, 8208)])                                       # wider: the 4-row waves of 4-wave workgroups
+    (4, 1536, 3072), (7, 768, 2048),
+    (2, 2304, 8208), (6, 1024, 3072)])                      # wider: the 4-row waves of 4-wave workgroups
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
-def test_w4a16_two_row_blocks_past_2048(M, K, N, epi):
-    """The per-lane W4A16 form with two activation rows per workgroup past 2048 k (M = 2 to 8): every
-    workgroup shape its rule picks, bf16 activations on half the cases, every output format, fp16
-    scales that are subnormal, zero and infinite."""
+def test_w4a16_two_row_blocks(M, K, N, epi):
+    """The per-lane W4A16 form with two activation rows per workgroup (M = 2 to 8): every workgroup
+    shape its rule picks, one to four chunks per lane, bf16 activations on half the cases, every
+    output format, fp16 scales that are subnormal, zero and infinite."""
     x, Wp, ws, rng = w4_inputs(M * 13 + K + N, M, N, K)
     ws = ws.copy()
     ws[0, 0], ws[1, K // 128 - 1], ws[2, 1] = 0x0001, 0x0000, 0x7C00
