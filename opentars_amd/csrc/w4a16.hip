@@ -637,120 +637,126 @@ hipError_t go_w4(const W4Args& a, hipStream_t s) {
 // ---------------------------------------------------------------------------- GEMM on INT8 MFMA
 // Prefill chunks (M >= 2): the group dots on v_mfma_i32_16x16x64_i8. An aligned mantissa a
 // (|a| <= 2^14) is split as a = 256 h + l with l its low byte sign-extended (in [-128, 127]) and
-// h = (a - l) / 256 (in [-64, 64]); a weight w in [-8, 7] is taken as u = w + 8 in [0, 15] (its
-// nibble with the top bit flipped, no sign extension). Then over a 128-wide group
+// h = (a - l) / 256 = (a + 128) >> 8 (in [-64, 64]); a weight w in [-8, 7] is taken as u = w + 8
+// in [0, 15] (its nibble with the top bit flipped, no sign extension). Then over a 128-wide group
 //   dot = sum a w = 256 sum h u + sum l u - 8 sum a,
 // every sum exact in int32 (|sum h u| <= 2^17, |sum a| <= 2^21, |dot| <= 2^24), so the group's
-// dot is the reference's exactly. The MFMA sums over 64 k: lane l supplies 16 bytes of activation
+// dot is the reference's exactly. The MFMA sums over 64 k: lane l supplies 16 bytes of operand
 // row l % 16 and of weight row l % 16; with the weights' packed nibble order (byte b of the
 // group's 64 bytes holds k = 2 b and 2 b + 1), one instruction takes the group's even k (the low
-// nibbles) and a second its odd k (the high nibbles), and the activation side is laid out in LDS
-// in the same order: [group][parity][h or l][lane quarter][row][16 bytes], so each operand is one
-// ds_read_b128 per lane.
+// nibbles) and a second its odd k (the high nibbles).
+//
+// The operand's 16 rows hold both halves: row i < MT is h of activation row i, row MT + i its l
+// (MT = 8 fills the 16 rows; with MT = 4, rows 8-15 repeat rows 0-7). LDS holds them in the
+// MFMA's order, [group][parity][lane quarter][row][16 bytes], so each operand is one ds_read_b128
+// per lane. A group's two MFMAs leave sum h u and sum l u of every activation row in one
+// accumulator (lane l: operand rows 4 (l / 16) .. + 3 against weight row l % 16); a permlane swap
+// across the lane halves (MT = 8) or the 16-lane rows (MT = 4) brings each row's two sums to one
+// lane, so every lane forms MT / 4 of the tile's MT x 16 terms and none idles.
 //
 // A workgroup owns MT activation rows (rows past M repeat row M - 1 and are never stored) and TT
-// tiles of 16 weight rows; NW waves, NW / TT per tile, split the tile's groups. The workgroup
-// loads its MT rows and aligns them once (8 elements per thread, 16 threads per group, the
-// group's exponent maximum by DPP; align_elems) into the LDS operands, the per-group scales and
-// 8 sum a; only then does each wave issue its weight loads (issued before, they would hold up
-// the alignment's instructions behind them). After a barrier each wave runs 4 MFMAs per group
-// for all its groups, keeping the dots in registers (lane l ends with rows 4 (l / 16) .. + 3,
-// weight row l % 16), then forms the fp32 terms (i2f(dot) * ws) * xs into LDS; after a second
-// barrier a lane per (row, weight row, bank) runs bank b's chain over groups b, b + 4, ... in
-// order from +0 (golden.py:315-319) and each quad folds (b0 + b1) + (b2 + b3) before bias,
-// activation and conversion.
+// tiles of 16 weight rows; NW waves, NW / TT per tile, split the tile's groups. Phases:
+//   1. the MT rows are loaded as MT * K / 8 tasks of 8 elements spread over every thread (a
+//      16-lane unit is one group of one row);
+//   2. they are aligned once (the group's exponent maximum by DPP; align_elems) into the LDS
+//      operands: the int16 mantissas paired by byte permutes, h as byte 1 of each pair plus 128
+//      (one packed 16-bit add), l as byte 0; each group's scale and 8 sum a beside them;
+//   3. only then does each wave issue its weight loads (issued before, they held up the
+//      alignment's instructions behind them);
+//   4. after a barrier each wave runs its groups' MFMAs and forms the fp32 terms
+//      (i2f(dot) * ws) * xs into LDS;
+//   5. after a second barrier a lane per (row, weight row, bank) runs bank b's chain over groups
+//      b, b + 4, ... in order from +0 (golden.py:315-319), and each quad folds
+//      (b0 + b1) + (b2 + b3) before bias, activation and conversion.
 //
 // Roofline: HBM for the weights (K / 2 + K / 64 bytes per weight row), read once per MT rows; the
-// per-(row, group) fp32 terms and chains are VALU work, one MFMA tile's 16 x 16 outputs per lane
-// set whatever M is.
+// alignment, the per-(row, group) fp32 terms and the chains are VALU work.
 template <int MT, int TT, int NW, int GMAX, bool BF16, bool SIMPLE>
 __global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x, const uint8_t* Wp, const uint16_t* ws,
                                                                   int lda, int M, int N, int K, W4Args a) {
   constexpr int NT = NW * 64, WPT = NW / TT, GW = (GMAX + WPT - 1) / WPT;
-  constexpr int TP = (GMAX * 16 + NT - 1) / NT;  // alignment passes per row (K / 8 tasks per row)
+  constexpr int R16 = 2 * MT, LGM = MT == 8 ? 3 : 2;
+  constexpr int TR = (MT * GMAX * 16 + NT - 1) / NT;  // alignment rounds over MT * K / 8 tasks
+  constexpr int TPL = MT / 4;                          // terms per lane and group
   static_assert(NW % TT == 0 && (MT == 4 || MT == 8), "waves split evenly over tiles");
-  __shared__ __align__(16) int8_t aop[GMAX * 256 * MT];  // [g][parity][h, l][quarter][row][16 B]
-  __shared__ __align__(16) float xs_t[GMAX][MT];
-  __shared__ __align__(16) int s8_t[GMAX][MT];
+  __shared__ __align__(16) int8_t aop[GMAX * 128 * R16];  // [g][parity][quarter][h rows, l rows][16 B]
+  __shared__ __align__(16) int2 xs8[GMAX][MT];             // (scale encoding, 8 sum a)
   __shared__ float terms[TT][16][MT][GMAX + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lq = lane >> 4;
-  const int G = K >> 7, TK = K >> 3;
+  const int G = K >> 7, units = MT * G;
   const int m0 = blockIdx.y * MT;
   const int tile = wave % TT, part = wave / TT;
   const int nt0 = (blockIdx.x * TT + tile) * 16;
   const int gpw = (G + WPT - 1) / WPT, ga = part * gpw, gb = min(G, ga + gpw);
 
-  // 1. the activation rows (task (r, t): row m0 + r, elements 8 t .. 8 t + 7; a dead task reads
-  //    the row's first group; rows past M read the last row)
-  uint32_t xb[MT][TP][8];
+  // 1. the activation rows: task T is element block T % 16 of unit T / 16 = (group u >> LGM, row
+  //    u % MT); a dead task reads row 0's first group; rows past M read the last row
+  uint32_t xb[TR][8];
 #pragma unroll
-  for (int r = 0; r < MT; ++r) {
+  for (int rd = 0; rd < TR; ++rd) {
+    if (rd * NT >= units * 16) continue;  // uniform
+    const int T = rd * NT + tid;
+    const int u = T >> 4 < units ? T >> 4 : 0;
+    const int r = u & (MT - 1), t = ((u >> LGM) << 4) | (T & 15);
     const char* xrow = static_cast<const char*>(x) + static_cast<int64_t>(min(m0 + r, M - 1)) * lda;
+    if constexpr (BF16) {
+      const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * t);
 #pragma unroll
-    for (int p = 0; p < TP; ++p) {
-      if (p * NT >= TK) continue;  // uniform
-      const int t = p * NT + tid;
-      const int tt = t < TK ? t : (t & 15);
-      if constexpr (BF16) {
-        const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * tt);
+      for (int j = 0; j < 4; ++j) {
+        xb[rd][2 * j] = v[j] << 16;
+        xb[rd][2 * j + 1] = v[j] & 0xFFFF0000u;
+      }
+    } else {
+      const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * t);
+      const v4u v0 = src[0], v1 = src[1];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          xb[r][p][2 * j] = v[j] << 16;
-          xb[r][p][2 * j + 1] = v[j] & 0xFFFF0000u;
-        }
-      } else {
-        const v4u* src = reinterpret_cast<const v4u*>(xrow + 32 * tt);
-        const v4u v0 = src[0], v1 = src[1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          xb[r][p][j] = v0[j];
-          xb[r][p][4 + j] = v1[j];
-        }
+      for (int j = 0; j < 4; ++j) {
+        xb[rd][j] = v0[j];
+        xb[rd][4 + j] = v1[j];
       }
     }
   }
   issue_fence();
 
-  // 2. alignment into the LDS operands: task t's elements are k = 8 t' .. 8 t' + 7 of group
-  //    t / 16 (t' = t % 16): quarter q = t' / 4, even k at bytes 4 (t' % 4) .. + 3 of the even
-  //    parity's 16, odd k likewise
+  // 2. alignment into the LDS operands: task (row r, group g, block tq) holds k = 8 tq .. 8 tq + 7:
+  //    quarter q = tq / 4, even k at bytes 4 (tq % 4) .. + 3 of the even parity's 16, odd k likewise
+  typedef uint16_t v2h __attribute__((ext_vector_type(2)));
+  typedef short v2s __attribute__((ext_vector_type(2)));
+  const auto add128 = [](uint32_t p) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, p) + (v2h){128, 128});
+  };
 #pragma unroll
-  for (int r = 0; r < MT; ++r) {
+  for (int rd = 0; rd < TR; ++rd) {
+    if (rd * NT + wave * 64 >= units * 16) continue;  // wave-uniform: a wave with no live task
+    const int T = rd * NT + tid;
+    int mant[8];
+    uint32_t sb;
+    align_elems<8, 16>(xb[rd], mant, sb);
+    // int16 pairs: p[0] = (k0, k2), p[1] = (k4, k6), p[2] = (k1, k3), p[3] = (k5, k7)
+    uint32_t p[4];
 #pragma unroll
-    for (int p = 0; p < TP; ++p) {
-      if (p * NT + wave * 64 >= TK) continue;  // wave-uniform: a wave with no live task
-      const int t = p * NT + tid;
-      int mant[8];
-      uint32_t sb;
-      align_elems<8, 16>(xb[r][p], mant, sb);
-      int sum = 0;
-      uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
+    for (int j = 0; j < 4; ++j) {
+      const int e = (j & 1) * 4 + (j >> 1);
+      p[j] = __builtin_amdgcn_perm(static_cast<uint32_t>(mant[e + 2]), static_cast<uint32_t>(mant[e]), 0x05040100u);
+    }
+    int sum = 0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int am = static_cast<int16_t>(mant[e]);   // the mantissa: its low 16 bits, signed
-        const int lo = static_cast<int8_t>(am);
-        const int hi = (am - lo) >> 8;
-        sum += am;
-        hw[e & 1] |= static_cast<uint32_t>(hi & 0xFF) << (8 * (e >> 1));
-        lw[e & 1] |= static_cast<uint32_t>(lo & 0xFF) << (8 * (e >> 1));
+    for (int j = 0; j < 4; ++j) sum = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, p[j]), (v2s){1, 1}, sum, false);
+    sum = group_sum<16>(sum);
+    if (T >> 4 < units) {
+      const int u = T >> 4, r = u & (MT - 1), g = u >> LGM, tq = T & 15, q = tq >> 2;
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const uint32_t lo = __builtin_amdgcn_perm(p[2 * par + 1], p[2 * par], 0x06040200u);
+        const uint32_t hi = __builtin_amdgcn_perm(add128(p[2 * par + 1]), add128(p[2 * par]), 0x07050301u);
+        int8_t* base = aop + (((g * 2 + par) * 4 + q) * R16 + r) * 16 + 4 * (tq & 3);
+        *reinterpret_cast<uint32_t*>(base) = hi;                // h: row r
+        *reinterpret_cast<uint32_t*>(base + MT * 16) = lo;      // l: row MT + r
       }
-      sum = group_sum<16>(sum);
-      if (t < TK) {
-        const int g = t >> 4, tq = t & 15, q = tq >> 2;
-#pragma unroll
-        for (int par = 0; par < 2; ++par) {
-          int8_t* base = aop + ((((g * 2 + par) * 2) * 4 + q) * MT + r) * 16 + 4 * (tq & 3);
-          *reinterpret_cast<uint32_t*>(base) = hw[par];                 // h
-          *reinterpret_cast<uint32_t*>(base + 4 * MT * 16) = lw[par];   // l
-        }
-        if (tq == 0) {
-          xs_t[g][r] = ffrom(sb);
-          s8_t[g][r] = 8 * sum;
-        }
-      }
+      if (tq == 0) xs8[g][r] = make_int2(static_cast<int>(sb), 8 * sum);
     }
   }
   // 3. this wave's weights (row nt0 + l % 16, the 16 bytes of quarter l / 16 of each of its groups)
@@ -776,53 +782,54 @@ __global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x,
 
   __syncthreads();
 
-  // 4. the MFMAs of every group of this wave (dots in registers), then their terms into LDS
+  // 4. per group two MFMAs: accumulator row 4 (l / 16) + v of lane l is h (rows < MT) or l (rows
+  //    MT ..) of an activation row, against weight row l % 16. After the swaps lane l holds the pair
+  //    of activation row rows[j] in (hv[j], lv[j]): MT = 8: 4 (lq % 2) + lq / 2 + 2 j; MT = 4: lq.
+  int rows[TPL];
+  if constexpr (MT == 8) {
+    rows[0] = 4 * (lq & 1) + (lq >> 1);
+    rows[1] = rows[0] + 2;
+  } else {
+    rows[0] = lq;
+  }
   const v4i zero = {0, 0, 0, 0};
-  int dots[GW][4];
 #pragma unroll
   for (int i = 0; i < GW; ++i) {
     if (ga + i >= gb) break;  // uniform
     const int g = ga + i;
-    v4i ah[2], al[2];
-#pragma unroll
-    for (int par = 0; par < 2; ++par) {
-      const int8_t* base = aop + ((((g * 2 + par) * 2) * 4 + lq) * MT + min(li, MT - 1)) * 16;
-      ah[par] = li < MT ? *reinterpret_cast<const v4i*>(base) : zero;
-      al[par] = li < MT ? *reinterpret_cast<const v4i*>(base + 4 * MT * 16) : zero;
-    }
+    const int8_t* base = aop + (((g * 2) * 4 + lq) * R16 + (li & (R16 - 1))) * 16;
+    const v4i a0 = *reinterpret_cast<const v4i*>(base);
+    const v4i a1 = *reinterpret_cast<const v4i*>(base + 4 * R16 * 16);
     v4i blo, bhi;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       blo[d] = static_cast<int>((wv[i][d] & 0x0F0F0F0Fu) ^ 0x08080808u);
       bhi[d] = static_cast<int>(((wv[i][d] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u);
     }
-    v4i accH = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[0], blo, zero, 0, 0, 0);
-    accH = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[1], bhi, accH, 0, 0, 0);
-    v4i accL = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[0], blo, zero, 0, 0, 0);
-    accL = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[1], bhi, accL, 0, 0, 0);
+    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, blo, zero, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bhi, acc, 0, 0, 0);
+    int dot[TPL];
+    if constexpr (MT == 8) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dots[i][v] = accH[v] * 256 + accL[v];
-  }
-  // lane l holds rows 4 (l / 16) .. + 3 of weight row l % 16: quarters past MT / 4 hold padding rows
-  const int mq = min(4 * lq, MT - 4);
-  const bool live_rows = 4 * lq < MT;
-#pragma unroll
-  for (int i = 0; i < GW; ++i) {
-    const int g = ga + i;
-    if (g >= gb) break;  // uniform
-    const float4 xs4 = *reinterpret_cast<const float4*>(&xs_t[g][mq]);
-    const int4 s84 = *reinterpret_cast<const int4*>(&s8_t[g][mq]);
+      for (int j = 0; j < 2; ++j) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(acc[2 * j]),
+                                                         static_cast<uint32_t>(acc[2 * j + 1]), false, false);
+        dot[j] = static_cast<int>(sw[0]) * 256 + static_cast<int>(sw[1]);
+      }
+    } else {
+      const auto s01 = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(acc[0]), static_cast<uint32_t>(acc[1]),
+                                                        false, false);
+      const auto s23 = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(acc[2]), static_cast<uint32_t>(acc[3]),
+                                                        false, false);
+      dot[0] = lq < 2 ? static_cast<int>(s01[0]) * 256 + static_cast<int>(s01[1])
+                      : static_cast<int>(s23[0]) * 256 + static_cast<int>(s23[1]);
+    }
     const float wsf = from_fp16_bits(wsv[i]);
-    const float xsv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
-    const int s8v[4] = {s84.x, s84.y, s84.z, s84.w};
-    float t4[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
+    for (int j = 0; j < TPL; ++j) {
+      const int2 e = xs8[g][rows[j]];
       // the contract's fmul(fmul(i2f(d), ws), xs) with its wrappers where they act (see the GEMV)
-      t4[v] = ftz(__fmul_rn(__fmul_rn(i2f(dots[i][v] - s8v[v]), wsf), xsv[v]));
-    if (live_rows) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) terms[tile][li][mq + v][g] = t4[v];
+      terms[tile][li][rows[j]][g] = ftz(__fmul_rn(__fmul_rn(i2f(dot[j] - e.y), wsf), ffrom(static_cast<uint32_t>(e.x))));
     }
   }
   __syncthreads();
@@ -903,49 +910,55 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
 // K = 3072, N = 4096: 4.6 -> 4.1 us; K = 8192, N = 8192: 12.0 -> 9.3 us), and at K = 8192 with
 // fewer rows 4 or 8 rows per workgroup (N = 1024 / 2048: 4.5 / 5.3 -> 3.8 / 4.5 us); K = 6144 at
 // N <= 2048 stays on whole-row waves (N = 1536: 3.7 us, K-split 3.9 - 4.4 us).
-// Several rows: the MFMA form where it is faster than the per-lane form (two activation rows per
-// block), both bit-exact. Up to 8 rows, the per-lane form in 8-wave workgroups with the fewest rows
-// per wave that keep the grid at most 256 workgroups, which beat both the 4-row waves tuned at
-// K = 1536, N = 12288 and the MFMA form: M = 2 / 4 / 8 at K = 6144, N = 1536: 6.35 / 6.43 / 8.12 ->
-// 4.72 / 5.58 / 7.54 us; at K = 3072, N = 1024: 4.35 / 4.44 / 6.21 -> 3.50 / 3.63 / 4.16 us; M = 4 /
-// 8 at K = 8192, N = 1024: 8.08 / 8.91 -> 6.17 / 7.27 us; at K = 4096, N = 2048: 4.53 / 7.33 -> 4.29
-// / 5.47 us; M = 2 at K = 2048, N = 2048: 3.08 -> 2.87 us; M = 4 at K = 1536, N = 3072: 4.06 ->
-// 3.58 us; M = 7 at K = 768, N = 2048: 3.93 -> 3.58 us (M = 2 at K = 512, N = 4096: 2.96 -> 3.05 us;
-// M = 16 at K = 6144: MFMA 9.2 us, per-lane 11.3 - 15.5 us). Wider matrices keep the 4-row waves of
-// 4-wave workgroups (M = 2: K = 1536, N = 12288 5.1 us; M = 6 / 8 at N = 3072: 4.6 / 4.7 us) or the
-// MFMA form. K = 1536, N = 12288 at M = 2 / 4 / 8 / 16 / 32: per-lane
-// 5.2 / 8.4 / 14.0 / 24.3 / 42.3 us; MFMA 6.4 / 6.5 (4-row tiles, one weight tile per workgroup)
-// / 9.0 (4-row tiles, two weight tiles) / 12.1 / 22.1 us (8-row tiles, two weight tiles). K =
-// 1536, N = 3072 at M = 4 / 8 / 16: per-lane 4.1 / 4.8 / 7.0 us, MFMA 4.5 / 5.1 / 6.0 us. K =
-// 6144, N = 1536 (96 weight tiles) at M = 4 / 8 / 16 / 32: per-lane 6.4 / 9.0 / 11.7 / 19.0 us,
-// MFMA 8.0 / 8.1 (4-row tiles, 16 waves) / 9.0 (8-row tiles) / 12.6 us (8-row tiles, two weight
-// tiles). 16-row tiles ran 21 - 49 us (their x staging spills).
+// Several rows (swept over M = 2 - 32 and 15 (K, N) pairs from 512 x 4096 to 8192 x 4096; every
+// form bit-exact):
+//   * the per-lane form, two activation rows per workgroup in 8-wave workgroups, with the fewest
+//     rows per wave (1, 2; 4 only from 1536 to 4096 k) that keep the grid at most 256 workgroups,
+//     up to 8 rows: K = 6144, N = 1536: M = 2 / 4: 4.7 / 5.6 us; K = 3072, N = 1024: M = 2 - 8:
+//     3.5 - 4.2 us; K = 2048, N = 2048: M = 2 - 8: 2.9 - 3.6 us; at M = 2 it is always the per-lane
+//     form (the 4-row waves of 4-wave workgroups past those grids: K = 1536, N = 12288: 5.1 us);
+//   * otherwise the MFMA form. Up to 2048 k: M <= 4 on 4-row tiles, 4 waves above N = 8192 (K =
+//     1536, N = 12288: 5.7 us) and 8 below (K = 1024, N = 3072: 3.3 us; K = 2048, N = 8192: 5.2
+//     us); more rows on 8-row tiles, 8 waves per weight tile while the grid stays at most 256
+//     workgroups (K = 1536, N = 3072: M = 8 4.3 us), else two weight tiles of 16 waves while that
+//     holds (M = 16: 4.4 us; K = 2048, N = 8192, M = 8: 5.6 us), else 8 waves per tile with one,
+//     two or four tiles per workgroup, the fewest that keep the grid at most 768 workgroups (K =
+//     1536, N = 12288: M = 8 / 16 / 32: 6.7 / 9.9 / 16.6 us); with at most 128 workgroups of 8-row
+//     tiles, 4-row tiles (twice the workgroups; K = 1024, N = 1024, M = 16: 3.2 against 3.7 us).
+//     Past 2048 k, 16 waves per workgroup and the tile shape (4 rows; 8 rows; 8 rows and two
+//     weight tiles) with the largest grid of at most 256 workgroups: K = 6144, N = 1536: M = 8 /
+//     16 / 32: 6.6 / 7.8 / 11.6 us; K = 3072, N = 4096: M = 8 / 16: 6.0 / 8.5 us.
+// The 8-row tiles with the two halves of the mantissa in the operand rows replaced tiles that
+// took them in separate MFMAs (4 rows per tile and masked operand rows): K = 1536, N = 12288:
+// M = 4 / 8 / 16 / 32: 6.3 / 9.1 / 12.5 / 22.1 -> 5.7 / 6.7 / 9.9 / 16.6 us.
 hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
   const int cpl = (a.K / 32 + 63) / 64;  // chunks per lane
+  const int G = a.K / 128;
+  const int64_t n16 = (a.N + 15) / 16;
   if (a.M >= 2 && a.M <= 8) {
-    // two activation rows per workgroup in 8-wave workgroups, the fewest rows per wave (1, 2, 4)
-    // that keep the grid at most 256 workgroups
     const int64_t mb = (a.M + 1) / 2;
     auto wgs = [&](int u) { return static_cast<int64_t>((a.N + 8 * u - 1) / (8 * u)) * mb; };
     if (wgs(1) <= 256) return go_cpl<8, 1, 2>(a, cpl, s);
     if (wgs(2) <= 256) return go_cpl<8, 2, 2>(a, cpl, s);
-    if (wgs(4) <= 256) return go_cpl<8, 4, 2>(a, cpl, s);
+    if ((a.M == 2 || (a.K >= 1536 && a.K <= 4096)) && wgs(4) <= 256) return go_cpl<8, 4, 2>(a, cpl, s);
   }
   if (a.M >= 3 && a.lda <= INT32_MAX) {
-    const int G = a.K / 128;
-    if (a.K <= 2048) {
-      if (a.N >= 8192) {
-        if (a.M <= 4) return go_w4_mfma<4, 1, 4, 16>(a, s);
-        if (a.M <= 8) return go_w4_mfma<4, 2, 4, 16>(a, s);
-        return go_w4_mfma<8, 2, 4, 16>(a, s);
-      }
-      if (a.M > 16) return go_w4_mfma<8, 2, 8, 16>(a, s);
-      if (a.M > 8) return go_w4_mfma<4, 1, 4, 16>(a, s);
-    } else if (a.M > 4) {
-      if (a.M <= 8 || G > 48) return go_w4_mfma<4, 1, 16, 64>(a, s);
-      if (a.M <= 16) return go_w4_mfma<8, 1, 16, 48>(a, s);
+    const int64_t mb4 = (a.M + 3) / 4, mb8 = (a.M + 7) / 8;
+    if (G <= 16) {
+      if (a.M <= 4) return a.N > 8192 ? go_w4_mfma<4, 1, 4, 16>(a, s) : go_w4_mfma<4, 1, 8, 16>(a, s);
+      if (n16 * mb8 <= 128) return go_w4_mfma<4, 1, 8, 16>(a, s);
+      if (n16 * mb8 <= 256) return go_w4_mfma<8, 1, 8, 16>(a, s);
+      if ((n16 + 1) / 2 * mb8 <= 256) return go_w4_mfma<8, 2, 16, 16>(a, s);
+      if (n16 * mb8 <= 768) return go_w4_mfma<8, 1, 8, 16>(a, s);
+      if ((n16 + 1) / 2 * mb8 <= 768) return go_w4_mfma<8, 2, 8, 16>(a, s);
+      return go_w4_mfma<8, 4, 8, 16>(a, s);
+    }
+    if (G <= 48) {
+      if (n16 * mb4 <= 256) return go_w4_mfma<4, 1, 16, 48>(a, s);
+      if (n16 * mb8 <= 256) return go_w4_mfma<8, 1, 16, 48>(a, s);
       return go_w4_mfma<8, 2, 16, 48>(a, s);
     }
+    return go_w4_mfma<4, 1, 16, 64>(a, s);
   }
   if (a.M >= 2) return go_cpl<4, 4, 2>(a, cpl, s);
   if (cpl >= 2) {

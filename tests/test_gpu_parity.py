@@ -495,20 +495,25 @@ def test_w4_shapes_bf16_bias_act(K, M):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    (3, 1536, 8192), (9, 2048, 80),              # 4-row tiles, one weight tile per workgroup
-    (7, 768, 8192),                              # 4-row tiles, two weight tiles
-    (16, 1536, 8208),                            # 8-row tiles, two weight tiles, 4 waves
-    (20, 512, 304),                              # 8-row tiles, two weight tiles, 8 waves
-    (12, 8192, 32),                              # K > 2048: 4-row tiles, 16 waves, 64 groups
-    (12, 6144, 96), (24, 3072, 112),             # K > 2048: 8-row tiles, one / two weight tiles
-    (2, 256, 16), (3, 4096, 8192), (8, 1024, 256)])  # the per-lane form
+    (3, 1536, 8208),                             # 4-row tiles, 4 waves
+    (4, 1024, 3072), (9, 2048, 80),              # 4-row tiles, 8 waves
+    (7, 768, 4096), (20, 512, 1040),             # 8-row tiles, 8 waves, one weight tile
+    (16, 1536, 3088),                            # 8-row tiles, two weight tiles of 16 waves
+    (16, 1536, 8208),                            # 8-row tiles, two weight tiles of 8 waves
+    (129, 256, 1456),                            # 8-row tiles, four weight tiles
+    (12, 6144, 96), (8, 6144, 1536),             # K > 2048: 4-row tiles, 16 waves
+    (24, 3072, 1040),                            # K > 2048: 8-row tiles, one weight tile
+    (24, 3072, 1424), (3, 4096, 8192),           # K > 2048: 8-row tiles, two weight tiles
+    (12, 8192, 32),                              # 64 groups: 4-row tiles, 16 waves
+    (2, 256, 16), (8, 1024, 256)])               # the per-lane form
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
-    """Every launch shape of the W4A16 GEMM at M >= 2, the INT8-MFMA form's (4- and 8-row
-    activation tiles, one or two weight tiles per workgroup, groups split over 4 to 16 waves) and
-    the per-lane form's beside them: K from 256 to 8192, ragged last tiles, fp16 group scales that
-    are subnormal, zero and infinite, fp32 and bf16 activation rows, and every output format."""
+    """Every launch shape of the W4A16 GEMM at M >= 3 on INT8 MFMA (4- and 8-row activation
+    tiles, one, two or four weight tiles per workgroup, groups split over 4 to 16 waves; 8 rows
+    past M on the 4-row tiles and rows past M in the last 8-row tile), and the per-lane form
+    beside them: K from 256 to 8192, ragged last tiles, fp16 group scales that are subnormal, zero
+    and infinite, fp32 and bf16 activation rows, and every output format."""
     x, Wp, ws, rng = w4_inputs(M * 1000 + K + N, M, N, K)
     ws = ws.copy()
     ws[0, 0], ws[1 % N, K // 128 - 1], ws[2 % N, 0] = 0x0001, 0x0000, 0x7C00
@@ -529,9 +534,9 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
     (2, 2048, 2048), (4, 1024, 1024),
     (4, 6144, 1536), (3, 3072, 1040), (8, 3072, 1024),      # two rows per wave (ragged N = 1040)
     (4, 2048, 2048), (5, 2048, 1024),
-    (2, 4096, 8192), (6, 6144, 1536), (7, 4096, 2048),      # four rows per wave
-    (4, 1536, 3072), (7, 768, 2048),
-    (2, 2304, 8208), (6, 1024, 3072)])                      # wider: the 4-row waves of 4-wave workgroups
+    (2, 4096, 8192), (8, 2048, 2048), (7, 4096, 2048),      # four rows per wave
+    (4, 1536, 3072), (2, 512, 8192),
+    (2, 2304, 8208), (2, 1536, 12304)])                     # wider (M = 2): 4-row waves of 4-wave workgroups
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
 def test_w4a16_two_row_blocks(M, K, N, epi):
     """The per-lane W4A16 form with two activation rows per workgroup (M = 2 to 8): every workgroup
@@ -557,7 +562,7 @@ def test_w4a16_two_row_blocks(M, K, N, epi):
     (1, 1536, 256), (1, 6144, 64),               # whole-row waves: one chunk per lane, three
     (1, 8192, 64), (1, 2304, 4096),              # K split over the waves: 4 and 16 rows per workgroup
     (2, 1024, 64),                               # the per-lane form with two activation rows
-    (3, 1536, 8192), (12, 6144, 96), (20, 512, 304)])  # the MFMA form: 4- and 8-row tiles
+    (3, 1536, 8192), (12, 6144, 96), (20, 512, 1040)])  # the MFMA form: 4- and 8-row tiles
 @pytest.mark.parametrize("bf16", [False, True])
 def test_w4_strided_rows_and_untouched_gaps(M, K, N, bf16):
     """Every W4A16 kernel form on activation rows and output rows with a gap after each (lda and
@@ -624,15 +629,16 @@ def test_w4a16_ksplit_special_groups(K, N, kind, bf16):
 
 
 @pytest.mark.parametrize("K", [1024, 6144])
-@pytest.mark.parametrize("M", [6, 12])
+@pytest.mark.parametrize("M", [6, 12, 16])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_w4_gemm_special_groups(K, M, bf16):
-    """The in-kernel aligners (the per-lane form's at M = 6, the MFMA form's at M = 12)
-    on groups that leave their fast path: all-zero, tiny (largest exponent below 16), subnormal
-    inputs inside normal groups, +-inf, NaN, and the largest finite values, in rows whose other
-    groups are ordinary (so waves of both kinds meet in one launch)."""
+    """The in-kernel aligners (the per-lane form's at M = 6, the MFMA form's 4-row tiles at M = 12
+    and 8-row tiles at M = 16) on groups that leave their fast path: all-zero, tiny (largest
+    exponent below 16), subnormal inputs inside normal groups, +-inf, NaN, and the largest finite
+    values, in rows whose other groups are ordinary (so waves of both kinds meet in one launch)."""
     rng = np.random.default_rng(K + bf16)
-    x, Wp, ws, _ = w4_inputs(K * 3 + bf16 + M, M, 64, K)
+    N = 64 if M < 16 else (2064 if K == 1024 else 1040)
+    x, Wp, ws, _ = w4_inputs(K * 3 + bf16 + M, M, N, K)
     g = x.reshape(M, K // 128, 128)
     g[0, 1] = 0.0                                                  # all-zero group
     g[0, 2] = rng.normal(0, 1, 128) * np.float32(2.0 ** -115)      # emax < 16

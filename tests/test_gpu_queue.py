@@ -400,16 +400,35 @@ def test_chains_whose_partial_sums_are_subnormal(seed, fusion):
         y, ldy16 = stride_fields(p, M, 4 * N)
         p.add(OPCODE=Q.OP_FDOT, CTRL=nn, EPI=Q.epi(), A_OFF=a, W_OFF=w, Y_OFF=y, M=M, N=N, K=K, GROUP_SIZE=gs,
               LDA16=lda16, LDY16=ldy16)
-    # the per-lane form (M <= 2, M = 4 on a narrow matrix, and M = 6 past 2048 k in 8-wave
-    # workgroups); the K split over waves (M = 1, K = 6400: 50 groups, the last wave two); the INT8
-    # MFMA form with 4-row tiles (M = 12), 8-row tiles over two weight tiles (M = 20), and 8-row
-    # tiles over 16 waves (M = 12, K = 3072)
+    # the per-lane form in 8-wave workgroups (M = 2, 4 and 6); the K split over waves (M = 1,
+    # K = 6400: 50 groups, the last wave two); the INT8 MFMA form's 4-row tiles over 8 waves (M = 12
+    # and 20) and over 16 waves (M = 12, K = 3072)
     for M, N, K in ((1, 256, 1280), (2, 64, 1536), (4, 32, 1280), (1, 64, 6400), (12, 32, 1280),
                     (20, 64, 1280), (6, 48, 3072), (12, 48, 3072)):
         add_w4_cancelling(p, M, N, K)
     prev = NQ.set_fusion(fusion)
     try:
         (o, ost), (g, gst) = both(p.image(), len(p.descs))
+    finally:
+        NQ.set_fusion(prev)
+    assert ost.done and same_status(ost, gst), (ost, gst)
+    gd = bytes(g.ddr)
+    assert gd == bytes(o.ddr), f"first differing byte at {first_diff(gd, bytes(o.ddr)):#x}"
+
+
+@pytest.mark.parametrize("fusion", [True, False])
+def test_w4_banks_subnormal_on_8row_tiles(fusion):
+    """add_w4_cancelling on the INT8 MFMA form's 8-row tiles, whose lanes take each row's h and l
+    sums from a permlane swap: one weight tile of 8 waves (M = 20, N = 688), two weight tiles of 16
+    waves (N = 1376), and past 2048 k one weight tile of 16 waves (M = 16, K = 3072, N = 1040); the
+    matrices need a larger image than the other chain cases."""
+    image = 1 << 23
+    p = Program(7100, image=image, qaddr=image - 0x10000)
+    for M, N, K in ((20, 688, 1280), (20, 1376, 1280), (16, 1040, 3072)):
+        add_w4_cancelling(p, M, N, K)
+    prev = NQ.set_fusion(fusion)
+    try:
+        (o, ost), (g, gst) = both(p.image(), len(p.descs), qaddr=p.qaddr)
     finally:
         NQ.set_fusion(prev)
     assert ost.done and same_status(ost, gst), (ost, gst)
