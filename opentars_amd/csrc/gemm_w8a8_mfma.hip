@@ -473,7 +473,8 @@ hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
 // kernel, its tile chosen by measurement on MI355X with the weights cold, bit-identical across
 // tiles; the direct kernel's 32 x 32 tiles with 4 waves over K otherwise.
 //  * 64 x 48 tiles (4 waves of 16 x 48, 256-byte stages, 3 slots) when they give one to 1.25
-//    workgroups per CU: M=256 K=1024 N=3072 7.5 -> 5.5 us (the 64 x 64 / 16-row-load tiles before);
+//    workgroups per CU: M=256 K=1024 N=3072 7.5 -> 5.5 us (the 64 x 64 / 16-row-load tiles before;
+//    4 / 5 slots 5.70 / 5.89 us against 5.40, 512-byte stages in 2 slots 5.41 us);
 //  * 64 x 64 tiles (4 waves of 32 x 32, 256-byte stages, 3 slots) when they give 512 or more:
 //    M=1024 K=1024 N=3072 16.5 -> 15.8 us;
 //  * 32 x 32 tiles (4 waves of 16 x 16) with 512-byte stages in 3 slots when K is a multiple of

@@ -1087,7 +1087,9 @@ hipError_t go_ksplit_rows(const KSplitArgs& a, hipStream_t s) {
 // at K = 4096 + 2816 and 3456 + 3456, N = 1152 (weights cold): 4.54 us with four waves per row
 // (1152 workgroups, each reading the 6.9 KB quantized row) -> 3.84 us one row per wave in 4-wave
 // workgroups (288) -> 3.49 us in 5-wave workgroups (231); 6- and 8-wave workgroups 3.53 / 3.66 us;
-// two rows per wave 3.6 - 3.8 us; the activation row staged once per workgroup in LDS 3.77 us.
+// two rows per wave 3.6 - 3.8 us; the activation row staged once per workgroup in LDS 3.77 us,
+// and by global -> LDS loads (no VGPR round trip, one barrier) 3.58 / 3.62 us, with two rows per
+// wave in 4-wave workgroups 3.36 - 3.43 / 3.46 us.
 template <int CPL, int U, int NWG>
 hipError_t go_ks2(const KSplitArgs& a, hipStream_t s) {
   const KSplit2Tail t{a.Y, a.ldy};
