@@ -692,16 +692,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x,
   const int nt0 = (blockIdx.x * TT + tile) * 16;
   const int gpw = (G + WPT - 1) / WPT, ga = part * gpw, gb = min(G, ga + gpw);
 
-  // 1. the activation rows: task T is element block T % 16 of unit T / 16 = (group u >> LGM, row
-  //    u % MT); a dead task reads row 0's first group; rows past M read the last row
+  // 1. the activation rows: thread t takes element block t % 16 of row (t / 16) % MT in every
+  //    round, of group (t / 16) / MT + rd * GPR in round rd (each wave one group per round); a task
+  //    past the last group reads it again (never stored); rows past M read the last row
+  constexpr int GPR = NT / 16 / MT;  // groups per alignment round
+  static_assert(GPR * 16 * MT == NT, "a thread keeps its row and block in every round");
+  const int tq = tid & 15, r = (tid >> 4) & (MT - 1), g0 = tid >> (4 + LGM);
+  const char* xrow = static_cast<const char*>(x) + static_cast<int64_t>(min(m0 + r, M - 1)) * lda;
   uint32_t xb[TR][8];
 #pragma unroll
   for (int rd = 0; rd < TR; ++rd) {
     if (rd * NT >= units * 16) continue;  // uniform
-    const int T = rd * NT + tid;
-    const int u = T >> 4 < units ? T >> 4 : 0;
-    const int r = u & (MT - 1), t = ((u >> LGM) << 4) | (T & 15);
-    const char* xrow = static_cast<const char*>(x) + static_cast<int64_t>(min(m0 + r, M - 1)) * lda;
+    const int t = (min(g0 + rd * GPR, G - 1) << 4) | tq;
     if constexpr (BF16) {
       const v4u v = *reinterpret_cast<const v4u*>(xrow + 16 * t);
 #pragma unroll
@@ -728,10 +730,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x,
   const auto add128 = [](uint32_t p) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, p) + (v2h){128, 128});
   };
+  int8_t* const abase = aop + ((tq >> 2) * R16 + r) * 16 + 4 * (tq & 3);  // group 0, even parity, h
 #pragma unroll
   for (int rd = 0; rd < TR; ++rd) {
     if (rd * NT + wave * 64 >= units * 16) continue;  // wave-uniform: a wave with no live task
-    const int T = rd * NT + tid;
+    const int g = g0 + rd * GPR;
     int mant[8];
     uint32_t sb;
     align_elems<8, 16>(xb[rd], mant, sb);
@@ -746,13 +749,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x,
 #pragma unroll
     for (int j = 0; j < 4; ++j) sum = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, p[j]), (v2s){1, 1}, sum, false);
     sum = group_sum<16>(sum);
-    if (T >> 4 < units) {
-      const int u = T >> 4, r = u & (MT - 1), g = u >> LGM, tq = T & 15, q = tq >> 2;
+    if (g < G) {
 #pragma unroll
       for (int par = 0; par < 2; ++par) {
         const uint32_t lo = __builtin_amdgcn_perm(p[2 * par + 1], p[2 * par], 0x06040200u);
         const uint32_t hi = __builtin_amdgcn_perm(add128(p[2 * par + 1]), add128(p[2 * par]), 0x07050301u);
-        int8_t* base = aop + (((g * 2 + par) * 4 + q) * R16 + r) * 16 + 4 * (tq & 3);
+        int8_t* base = abase + (g * 2 + par) * 4 * R16 * 16;
         *reinterpret_cast<uint32_t*>(base) = hi;                // h: row r
         *reinterpret_cast<uint32_t*>(base + MT * 16) = lo;      // l: row MT + r
       }
