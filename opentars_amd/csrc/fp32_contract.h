@@ -262,6 +262,15 @@ __device__ __forceinline__ float from_fp16_bits(uint32_t h) {
   return ffrom(e == 31 ? special : (e == 0 ? sub : normal));
 }
 
+// binary16 bits -> fp32 by the conversion instruction (v_cvt_f32_f16): exact for every finite and
+// infinite input, subnormals included (binary16 denormals are kept), so equal to from_fp16_bits
+// except that a NaN keeps its sign and payload instead of becoming the canonical NaN. For values
+// whose NaNs meet a canonicalization before anything is stored: the W4A16 group scales, which only
+// feed the bank chains that chain_end canonicalizes.
+__device__ __forceinline__ float fp16_to_f32_keep_nan(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
 // numerics.py:14-18: fp32 -> binary16 bits, round to nearest even with gradual underflow, signed
 // zero, NaN -> 0x7E00. Integer rounding of the significand for normal results; for results below
 // 2^-14 the exact product x * 2^24 (a power-of-two scaling) rounded to an integer is the subnormal's

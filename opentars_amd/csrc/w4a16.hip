@@ -405,7 +405,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
         // (|d| <= 2^24) and the fp16 scale is an fp32 normal, infinity or NaN, so the first product
         // is 0, at least 2^-24 in magnitude, infinite or NaN (no flush); the second is flushed; a NaN
         // payload only feeds the chains, whose results are canonicalized
-        const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), from_fp16_bits(wsh[min(u, U - 1) * G + g])), xs));
+        const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), fp16_to_f32_keep_nan(wsh[min(u, U - 1) * G + g])), xs));
         if constexpr (kRegChain) T[j] = term;
         else if (u < U && c < C && n0 + u < N) sm.terms[wave][r * U + u][g] = term;
       }
@@ -559,7 +559,7 @@ __global__ __launch_bounds__(1024) void gemv_w4a16_kslice_kernel(const void* x, 
     d += lane_xor1(d);
     d += lane_xor2(d);
     // the contract's fmul(fmul(i2f(d), ws), xs) with its wrappers where they act (see the GEMV)
-    const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), from_fp16_bits(wsv[s])), xs));
+    const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), fp16_to_f32_keep_nan(wsv[s])), xs));
     if (q == 0 && gq < ng) terms[4 * s + u][g0 + gq] = term;
   }
   __syncthreads();
@@ -826,7 +826,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_w4a16_mfma_kernel(const void* x,
       dot[0] = lq < 2 ? static_cast<int>(s01[0]) * 256 + static_cast<int>(s01[1])
                       : static_cast<int>(s23[0]) * 256 + static_cast<int>(s23[1]);
     }
-    const float wsf = from_fp16_bits(wsv[i]);
+    const float wsf = fp16_to_f32_keep_nan(wsv[i]);
 #pragma unroll
     for (int j = 0; j < TPL; ++j) {
       const int2 e = xs8[g][rows[j]];

@@ -484,6 +484,8 @@ def test_w4a16_prefill_chunks(K, N, M):
 @pytest.mark.parametrize("M", [1, 3])
 def test_w4_shapes_bf16_bias_act(K, M):
     x, Wp, ws, rng = w4_inputs(K + M, M, 48, K)
+    ws = ws.copy()
+    ws[5, 1], ws[6, 0], ws[7, 1] = 0x7E01, 0xFC05, 0x0003          # NaN scales (payloads), a subnormal
     x = (x * np.exp2(rng.integers(-30, 30, (M, K // 128, 1))).repeat(128, axis=2).reshape(M, K)).astype(f32)
     xb = F.to_bf16_bits(x)
     b = rng.normal(0, 1, 48).astype(f32)
@@ -512,11 +514,13 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
     """Every launch shape of the W4A16 GEMM at M >= 3 on INT8 MFMA (4- and 8-row activation
     tiles, one, two or four weight tiles per workgroup, groups split over 4 to 16 waves; 8 rows
     past M on the 4-row tiles and rows past M in the last 8-row tile), and the per-lane form
-    beside them: K from 256 to 8192, ragged last tiles, fp16 group scales that are subnormal, zero
-    and infinite, fp32 and bf16 activation rows, and every output format."""
+    beside them: K from 256 to 8192, ragged last tiles, fp16 group scales that are subnormal, zero,
+    infinite and NaN (payloads of both signs), fp32 and bf16 activation rows, and every output
+    format."""
     x, Wp, ws, rng = w4_inputs(M * 1000 + K + N, M, N, K)
     ws = ws.copy()
     ws[0, 0], ws[1 % N, K // 128 - 1], ws[2 % N, 0] = 0x0001, 0x0000, 0x7C00
+    ws[3 % N, 1], ws[4 % N, 0] = 0x7E01, 0xFC05                    # NaNs with payloads, both signs
     xin = F.to_bf16_bits(x) if bf16 else x
     kw = {}
     if epi == "bias_silu_bf16":
@@ -541,10 +545,10 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
 def test_w4a16_two_row_blocks(M, K, N, epi):
     """The per-lane W4A16 form with two activation rows per workgroup (M = 2 to 8): every workgroup
     shape its rule picks, one to four chunks per lane, bf16 activations on half the cases, every
-    output format, fp16 scales that are subnormal, zero and infinite."""
+    output format, fp16 scales that are subnormal, zero, infinite and NaN."""
     x, Wp, ws, rng = w4_inputs(M * 13 + K + N, M, N, K)
     ws = ws.copy()
-    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1] = 0x0001, 0x0000, 0x7C00
+    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1], ws[3, 2] = 0x0001, 0x0000, 0x7C00, 0xFC05
     bf16 = (K // 256 + M) % 2 == 0
     xin = F.to_bf16_bits(x) if bf16 else x
     kw = {}
@@ -587,7 +591,7 @@ def test_w4a16_ksplit_waves(K, N, epi):
     K = 2304, 3328, 6400), bf16 activations on half the cases, every output format."""
     x, Wp, ws, rng = w4_inputs(K + N, 1, N, K)
     ws = ws.copy()
-    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1] = 0x0001, 0x0000, 0x7C00
+    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1], ws[3, 2] = 0x0001, 0x0000, 0x7C00, 0x7E01
     bf16 = (K // 256) % 2 == 0
     xin = F.to_bf16_bits(x) if bf16 else x
     kw = {}
