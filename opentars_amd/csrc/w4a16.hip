@@ -406,8 +406,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
         // is 0, at least 2^-24 in magnitude, infinite or NaN (no flush); the second is flushed; a NaN
         // payload only feeds the chains, whose results are canonicalized
         const float term = ftz(__fmul_rn(__fmul_rn(i2f(d), fp16_to_f32_keep_nan(wsh[min(u, U - 1) * G + g])), xs));
-        if constexpr (kRegChain) T[j] = term;
-        else if (u < U && c < C && n0 + u < N) sm.terms[wave][r * U + u][g] = term;
+        // a chunk past the row (its group past the last) gives the term +0, which the chains add
+        // as a no-op (below)
+        if constexpr (kRegChain) T[j] = c < C ? term : 0.0f;
+        else if (u < U && n0 + u < N) sm.terms[wave][r * U + u][c >> 2] = c < C ? term : 0.0f;
       }
     }
   }
@@ -436,19 +438,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
 #pragma unroll
     for (int i = 0; i < kSteps; ++i) tv[i] = trow[bank + 4 * i];  // index <= 16 CPL - 1 < kTermStride
   }
+  // every chain runs all 4 CPL steps: the steps past the row's last group add +0, and a sum that
+  // starts from +0 never becomes -0 under round-to-nearest (x + y is -0 only when both are -0), so
+  // adding +0 leaves it (and its subnormal key, and the flushed recompute) unchanged
   float acc = 0.0f;
   uint32_t mk = ~0u;
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i)
-    if (bank + 4 * i < G) {
-      acc = __fadd_rn(acc, tv[i]);
-      mk = min(mk, sub_key(acc));
-    }
+  for (int i = 0; i < kSteps; ++i) {
+    acc = __fadd_rn(acc, tv[i]);
+    mk = min(mk, sub_key(acc));
+  }
   if (__builtin_expect(mk < kSubKeyNormal, 0)) {
     acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kSteps; ++i)
-      if (bank + 4 * i < G) acc = fadd_chain(acc, tv[i]);
+    for (int i = 0; i < kSteps; ++i) acc = fadd_chain(acc, tv[i]);
   }
   acc = chain_end(acc);
   // bank 0: b0 + b1, bank 2: b2 + b3 (the next bank's lane: 1 above, or 4 above by a row rotation)
