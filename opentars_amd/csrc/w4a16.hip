@@ -438,9 +438,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
 #pragma unroll
     for (int i = 0; i < kSteps; ++i) tv[i] = trow[bank + 4 * i];  // index <= 16 CPL - 1 < kTermStride
   }
-  // every chain runs all 4 CPL steps: the steps past the row's last group add +0, and a sum that
-  // starts from +0 never becomes -0 under round-to-nearest (x + y is -0 only when both are -0), so
-  // adding +0 leaves it (and its subnormal key, and the flushed recompute) unchanged
+  // the unflushed chain runs all 4 CPL steps: the steps past the row's last group add +0, and a
+  // sum that starts from +0 never becomes -0 under round-to-nearest (x + y is -0 only when both are
+  // -0), so adding +0 leaves it and its subnormal key unchanged. The flushed recompute stops at the
+  // last group: a negative subnormal partial sum flushes to -0, which a +0 step would turn into +0
   float acc = 0.0f;
   uint32_t mk = ~0u;
 #pragma unroll
@@ -451,7 +452,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_w4a16_kernel(const void* x, int6
   if (__builtin_expect(mk < kSubKeyNormal, 0)) {
     acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kSteps; ++i) acc = fadd_chain(acc, tv[i]);
+    for (int i = 0; i < kSteps; ++i)
+      if (bank + 4 * i < G) acc = fadd_chain(acc, tv[i]);
   }
   acc = chain_end(acc);
   // bank 0: b0 + b1, bank 2: b2 + b3 (the next bank's lane: 1 above, or 4 above by a row rotation)

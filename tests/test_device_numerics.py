@@ -270,6 +270,37 @@ def test_partial_sums_above_2_pow_minus_100_absorb_subnormal_addends():
     assert (key(sub) < tiny).all()
 
 
+def test_plus_zero_steps_leave_unflushed_chains_but_not_flushed_ones():
+    """The W4A16 GEMV runs its unflushed bank chains over every register step, the steps past a
+    row's last group adding +0, and recomputes a chain with the contract's flushing adds (stopping
+    at the last group) when a partial sum is subnormal. Unflushed, a sum that starts at +0 is never
+    -0 under round-to-nearest (only -0 + -0 gives -0), so a +0 step changes no bit of it (chains
+    of signed zeros, subnormals, normals near the subnormal range, cancelling pairs, infinities);
+    flushed, a chain can end at -0 (a negative subnormal partial sum flushed), where a +0 step
+    would give +0."""
+    rng = np.random.default_rng(23)
+    pool = np.array([0.0, -0.0, 2.0 ** -149, -2.0 ** -149, 2.0 ** -126, -2.0 ** -126, 1.5, -1.5,
+                     np.inf, -np.inf], f32)
+    for _ in range(3000):
+        n = int(rng.integers(1, 10))
+        t = np.where(rng.random(n) < 0.4, rng.choice(pool, n),
+                     (rng.normal(0, 1, n) * np.exp2(rng.integers(-140, -110, n))).astype(f32)).astype(f32)
+        for i in range(1, n):
+            if rng.random() < 0.3:
+                t[i] = -t[i - 1]                                    # exact cancellation
+        acc = f32(0.0)
+        with np.errstate(all="ignore"):
+            for v in t:
+                acc = f32(acc + v)
+                assert not (acc == 0 and np.signbit(acc))
+            padded = f32(acc + f32(0.0))
+        assert np.isnan(acc) or padded.view(np.uint32) == acc.view(np.uint32)
+    a = f32(2.0 ** -125)
+    ends = F.fadd(F.fadd(f32(0.0), a), -f32(a + f32(3 * 2.0 ** -148)))   # a - (a + 3 2^-148), flushed
+    assert ends == 0 and np.signbit(ends)
+    assert not np.signbit(F.fadd(ends, f32(0.0)))
+
+
 def test_balanced_hex_digit_planes_reconstruct_every_mantissa():
     """The W4A16 GEMV writes each aligned mantissa a (|a| <= 2^14) as four balanced base-16 digits
     and dots each digit plane with the weight nibbles on v_dot8_i32_i4 (signed 4-bit operands).

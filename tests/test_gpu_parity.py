@@ -632,6 +632,50 @@ def test_w4a16_ksplit_special_groups(K, N, kind, bf16):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+def w4_chains_ending_at_minus_zero(M: int, N: int, K: int):
+    """Inputs whose every bank chain ends in a negative subnormal partial sum, which the contract's
+    flushed adds turn into -0: in each bank (groups b, b + 4, ...) the last two groups hold the same
+    activations (magnitudes 2^-108 to 2^-106 with one sign pattern for every row, element 5 at
+    2^-115) and opposite weights (5 with the activation's sign, then -5), except element 5 of the
+    last, one lower; with every group scale 2^-20 the first term is normal (about 2^-118), both are
+    exact, and they add to -a_5 2^-20 xs (about -2^-134); the bank's other groups are zero (terms
+    +0)."""
+    G_ = K // 128
+    rng = np.random.default_rng(K + M)
+    x = np.zeros((M, K), f32)
+    w = rng.integers(-6, 7, (N, K)).astype(np.int64)
+    for b in range(4):
+        g1, g2 = list(range(b, G_, 4))[-2:]
+        sgn = rng.choice(np.array([-1, 1]), 128)
+        sgn[5] = 1
+        blk = ((np.abs(rng.normal(0, 1, (M, 128))) % 2 + 1) * sgn * 2.0 ** -108).astype(f32)
+        blk[:, 5] = f32(2.0 ** -115)
+        x[:, g1 * 128:(g1 + 1) * 128] = blk
+        x[:, g2 * 128:(g2 + 1) * 128] = blk
+        w[:, g1 * 128:(g1 + 1) * 128] = 5 * sgn
+        w[:, g2 * 128:(g2 + 1) * 128] = -5 * sgn
+        w[:, g2 * 128 + 5] -= 1
+    nib = (w & 15).astype(np.uint8)
+    Wp = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    ws = np.full((N, G_), 0x0010, np.uint16)
+    return x, Wp, ws
+
+
+@pytest.mark.parametrize("M,K", [(1, 1280), (1, 1536), (1, 6144), (1, 8192), (2, 1536), (12, 1536), (12, 6144)])
+def test_w4_bank_chains_ending_at_minus_zero(M, K):
+    """Every bank's flushed chain ends at -0 (w4_chains_ending_at_minus_zero), so every output is
+    -0 only if no +0 is added after a bank's last group: the whole-row waves (their unflushed chains
+    run every register step, the steps past the last group adding +0, and are recomputed with the
+    flushes when a partial sum is subnormal; 10, 12 and 48 groups), the K split over waves, the
+    per-lane form with two activation rows and the MFMA form."""
+    N = 64
+    x, Wp, ws = w4_chains_ending_at_minus_zero(M, N, K)
+    want = G.gemm_w4(x, Wp, ws)
+    assert (want.view(np.uint32) == 0x80000000).all()
+    y = ops.gemm_w4(cuda(x), cuda(Wp), cuda(ws))
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 @pytest.mark.parametrize("K", [1024, 6144])
 @pytest.mark.parametrize("M", [6, 12, 16])
 @pytest.mark.parametrize("bf16", [False, True])
