@@ -730,7 +730,7 @@ CONFIG_KERNELS = {
     "c4_prefill_M256_K1024_N3072": ("mfma_tile_kernel<64, 48, 4, 1, 256, 3, true, false>", 65536),
     "c4_prefill_M256_K3072_N1024": ("mfma_tile_kernel<32, 32, 2, 2, 512, 3, true, false>", 65536),
     "c5_w4a16_M1_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 1, 1, false, true>", 196608),
-    "c5_w4a16_M1_K6144_N1536": ("gemv_w4a16_kernel<8, 1, 1, 3, false, true>", 98304),
+    "c5_w4a16_M1_K6144_N1536": ("gemv_w4a16_kernel<4, 2, 1, 3, false, true>", 49152),
     "c5_w4a16_M4_K1536_N12288": ("gemm_w4a16_mfma_kernel<4, 1, 4, 16, false, true>", 196608),
     "c5_w4a16_M4_K6144_N1536": ("gemv_w4a16_kernel<8, 2, 2, 3, false, true>", 98304),
     "c5_w4a16_M8_K1536_N12288": ("gemm_w4a16_mfma_kernel<8, 1, 8, 16, false, true>", 393216),

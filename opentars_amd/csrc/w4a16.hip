@@ -908,15 +908,17 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
   }
 }
 
-// Shapes by measurement on MI355X (weights cold, graph replays): one activation row: rows of at
+// Shapes by measurement on MI355X (weights cold, graph replays). One activation row: rows of at
 // most 2048 k (one chunk per lane) 4 rows per wave in 4-wave workgroups (K = 1536, N = 12288:
-// 4.5 us; 3-, 8- and 12-wave workgroups within 0.2 us, 1 or 2 rows per wave 5.4 - 7.5 us); longer
-// rows one row per wave in 8-wave workgroups (K = 6144, N = 1536: 4.1 - 4.6 us; 4 rows per wave
-// 4.9 us, 12-wave workgroups 7.9 us). Past 2048 k the K-split form where it measured faster:
-// 16 rows per workgroup from N = 4096 (K = 6144, N = 4096 / 8192: 5.9 / 9.4 -> 5.1 / 7.1 us;
-// K = 3072, N = 4096: 4.6 -> 4.1 us; K = 8192, N = 8192: 12.0 -> 9.3 us), and at K = 8192 with
-// fewer rows 4 or 8 rows per workgroup (N = 1024 / 2048: 4.5 / 5.3 -> 3.8 / 4.5 us); K = 6144 at
-// N <= 2048 stays on whole-row waves (N = 1536: 3.7 us, K-split 3.9 - 4.4 us).
+// 4.0 us; 2-, 3-, 6- and 8-wave workgroups and 1 to 3 rows per wave 0.1 - 3 us slower). Longer
+// rows (swept over K = 2304 - 8192 and N = 512 - 12288): the fewest weight rows per workgroup (4,
+// 8, 12, 16 in 4-wave workgroups; 24, 32 in 8-wave ones) that keep the grid at most 256
+// workgroups, 4 only up to 3072 k, and 24 rows past N = 8192; at N <= 1024 past 6144 k the
+// K-split form below. Against one row per wave in 8-wave workgroups and the K-split form from
+// N = 4096: K = 6144: N = 1536 / 2048 / 3072 / 4096 / 6144 / 8192 / 12288: 3.44 / 3.67 / 5.00 /
+// 4.97 / 6.59 / 7.38 / 10.53 -> 3.25 / 3.38 / 4.00 / 4.50 / 5.71 / 6.64 / 8.79 us; K = 2304,
+// N = 3072: 3.82 -> 2.96 us; K = 8192, N = 2048 / 4096: 4.33 / 6.37 -> 3.97 / 6.01 us (K = 8192,
+// N = 1024: K split 3.75 us, 8 rows per workgroup 3.84 us).
 // Several rows (swept over M = 2 - 32 and 15 (K, N) pairs from 512 x 4096 to 8192 x 4096; every
 // form bit-exact):
 //   * the per-lane form, two activation rows per workgroup in 8-wave workgroups, with the fewest
@@ -968,11 +970,16 @@ hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
     return go_w4_mfma<4, 1, 16, 64>(a, s);
   }
   if (a.M >= 2) return go_cpl<4, 4, 2>(a, cpl, s);
-  if (cpl >= 2) {
-    if (a.N >= 4096) return go_w4_kslice<4>(a, s);
-    if (a.K > 6144) return a.N <= 1024 ? go_w4_kslice<1>(a, s) : go_w4_kslice<2>(a, s);
+  if (cpl == 1) return go_cpl<4, 4, 1>(a, cpl, s);
+  if (a.N <= 1024) {
+    if (a.K > 6144) return go_w4_kslice<1>(a, s);
+    if (a.K <= 3072) return go_cpl<4, 1, 1>(a, cpl, s);
   }
-  return cpl == 1 ? go_cpl<4, 4, 1>(a, cpl, s) : go_cpl<8, 1, 1>(a, cpl, s);
+  if (a.N <= 2048) return go_cpl<4, 2, 1>(a, cpl, s);
+  if (a.N <= 3072) return go_cpl<4, 3, 1>(a, cpl, s);
+  if (a.N <= 4096) return go_cpl<4, 4, 1>(a, cpl, s);
+  if (a.N <= 8192 && a.N > 6144) return go_cpl<8, 4, 1>(a, cpl, s);
+  return go_cpl<8, 3, 1>(a, cpl, s);
 }
 
 }  // namespace tars

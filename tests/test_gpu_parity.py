@@ -564,7 +564,8 @@ def test_w4a16_two_row_blocks(M, K, N, epi):
 
 @pytest.mark.parametrize("M,K,N", [
     (1, 1536, 256), (1, 6144, 64),               # whole-row waves: one chunk per lane, three
-    (1, 8192, 64), (1, 2304, 4096),              # K split over the waves: 4 and 16 rows per workgroup
+    (1, 2304, 4096),                             # whole-row waves, 16 rows per workgroup
+    (1, 8192, 64),                               # K split over the waves
     (2, 1024, 64),                               # the per-lane form with two activation rows
     (3, 1536, 8192), (12, 6144, 96), (20, 512, 1040)])  # the MFMA form: 4- and 8-row tiles
 @pytest.mark.parametrize("bf16", [False, True])
@@ -582,13 +583,41 @@ def test_w4_strided_rows_and_untouched_gaps(M, K, N, bf16):
     assert (yb[:, N:] == -7.0).all()
 
 
-@pytest.mark.parametrize("K,N", [(8192, 1008), (8192, 2048), (6400, 1040), (6144, 4096), (2304, 4096),
-                                 (3328, 4112)])
+@pytest.mark.parametrize("K,N", [
+    (2304, 1008), (3072, 528),                   # 4 weight rows per workgroup
+    (6144, 1536), (8192, 2032), (6144, 1024),    # 8
+    (5120, 2560), (2560, 3008),                  # 12
+    (4096, 4096), (6144, 3088),                  # 16
+    (3072, 6144), (2304, 12288),                 # 24 (also past N = 8192)
+    (2304, 8192), (4096, 7008)])                 # 32
+@pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
+def test_w4a16_whole_row_shapes(K, N, epi):
+    """One activation row past 2048 k on whole-row waves: every workgroup shape of the rule (4 to
+    32 weight rows per workgroup, 4 and 8 waves, 1 to 4 rows per wave), ragged N, bf16 activations
+    on half the cases, every output format, fp16 scales that are subnormal, zero, infinite and
+    NaN."""
+    x, Wp, ws, rng = w4_inputs(K * 3 + N, 1, N, K)
+    ws = ws.copy()
+    ws[0, 0], ws[1, K // 128 - 1], ws[2, 1], ws[3, 2] = 0x0001, 0x0000, 0x7C00, 0xFE01
+    bf16 = (K // 256 + N) % 2 == 0
+    xin = F.to_bf16_bits(x) if bf16 else x
+    kw = {}
+    if epi == "bias_silu_bf16":
+        kw = dict(bias=rng.normal(0, 1, N).astype(f32), act=ACT_SILU, out=OUT_BF16)
+    elif epi == "int8":
+        kw = dict(out=OUT_INT8, out_scale=f32(0.125))
+    dkw = {k: (cuda(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16, **dkw)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16, **kw)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("K,N", [(8192, 1008), (8192, 64), (6400, 1024), (7424, 528), (6656, 16)])
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
 def test_w4a16_ksplit_waves(K, N, epi):
-    """One activation row with K split over the waves of a workgroup (K > 2048 at N >= 4096, and
-    K > 6144): 4, 8 and 16 weight rows per workgroup, a last wave with two groups (G % 4 == 2 at
-    K = 2304, 3328, 6400), bf16 activations on half the cases, every output format."""
+    """One activation row with K split over the waves of a workgroup (past 6144 k at N <= 1024): 4
+    weight rows per workgroup, ragged N, a last wave with two groups (G % 4 == 2 at K = 6400,
+    7424), bf16 activations on half the cases, every output format."""
     x, Wp, ws, rng = w4_inputs(K + N, 1, N, K)
     ws = ws.copy()
     ws[0, 0], ws[1, K // 128 - 1], ws[2, 1], ws[3, 2] = 0x0001, 0x0000, 0x7C00, 0x7E01
@@ -605,7 +634,7 @@ def test_w4a16_ksplit_waves(K, N, epi):
     assert same(host(y), want), mismatch(host(y), want)
 
 
-@pytest.mark.parametrize("K,N", [(8192, 64), (2304, 4096)])
+@pytest.mark.parametrize("K,N", [(8192, 64), (6400, 512)])
 @pytest.mark.parametrize("kind", ["mixed", "inf", "nan"])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_w4a16_ksplit_special_groups(K, N, kind, bf16):
