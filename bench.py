@@ -734,7 +734,7 @@ CONFIG_KERNELS = {
     "c5_w4a16_M4_K1536_N12288": ("gemm_w4a16_mfma_kernel<4, 1, 4, 16, false, true>", 196608),
     "c5_w4a16_M4_K6144_N1536": ("gemv_w4a16_kernel<8, 2, 2, 3, false, true>", 98304),
     "c5_w4a16_M8_K1536_N12288": ("gemm_w4a16_mfma_kernel<8, 1, 8, 16, false, true>", 393216),
-    "c5_w4a16_M8_K6144_N1536": ("gemm_w4a16_mfma_kernel<4, 1, 16, 48, false, true>", 196608),
+    "c5_w4a16_M8_K6144_N1536": ("gemv_w4a16_kernel<8, 3, 2, 3, false, true>", 131072),
 }
 
 

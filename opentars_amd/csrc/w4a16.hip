@@ -922,10 +922,13 @@ hipError_t go_cpl(const W4Args& a, int cpl, hipStream_t s) {
 // Several rows (swept over M = 2 - 32 and 15 (K, N) pairs from 512 x 4096 to 8192 x 4096; every
 // form bit-exact):
 //   * the per-lane form, two activation rows per workgroup in 8-wave workgroups, with the fewest
-//     rows per wave (1, 2; 4 only from 1536 to 4096 k) that keep the grid at most 256 workgroups,
-//     up to 8 rows: K = 6144, N = 1536: M = 2 / 4: 4.7 / 5.6 us; K = 3072, N = 1024: M = 2 - 8:
-//     3.5 - 4.2 us; K = 2048, N = 2048: M = 2 - 8: 2.9 - 3.6 us; at M = 2 it is always the per-lane
-//     form (the 4-row waves of 4-wave workgroups past those grids: K = 1536, N = 12288: 5.1 us);
+//     rows per wave (1, 2; 3 from 1536 to 6144 k; 4 from 1536 to 4096 k; 3 and 4 at any K at
+//     M = 2) that keep the grid at most 256 workgroups, up to 8 rows: K = 6144, N = 1536: M = 2 /
+//     4 / 8: 4.4 / 5.3 / 6.2 us; K = 3072, N = 1024: M = 2 - 8: 3.3 - 4.0 us; K = 2048, N = 2048:
+//     M = 2 - 8: 2.8 - 3.6 us (three rows per wave: K = 6144, N = 3072, M = 4: 7.1 -> 6.5 us;
+//     K = 4096, N = 1536, M = 7: 5.2 -> 4.7 us; past 6144 k it lost to the MFMA form: K = 8192,
+//     N = 1536, M = 8: 8.2 against 7.9 us); at M = 2 it is always the per-lane form (the 4-row
+//     waves of 4-wave workgroups past those grids: K = 1536, N = 12288: 5.1 us);
 //   * otherwise the MFMA form. Up to 2048 k: M <= 4 on 4-row tiles, 4 waves above N = 8192 (K =
 //     1536, N = 12288: 5.7 us) and 8 below (K = 1024, N = 3072: 3.3 us; K = 2048, N = 8192: 5.2
 //     us); more rows on 8-row tiles, 8 waves per weight tile while the grid stays at most 256
@@ -949,6 +952,7 @@ hipError_t launch_gemv_w4a16(const W4Args& a, hipStream_t s) {
     auto wgs = [&](int u) { return static_cast<int64_t>((a.N + 8 * u - 1) / (8 * u)) * mb; };
     if (wgs(1) <= 256) return go_cpl<8, 1, 2>(a, cpl, s);
     if (wgs(2) <= 256) return go_cpl<8, 2, 2>(a, cpl, s);
+    if ((a.M == 2 || a.K >= 1536) && a.K <= 6144 && wgs(3) <= 256) return go_cpl<8, 3, 2>(a, cpl, s);
     if ((a.M == 2 || (a.K >= 1536 && a.K <= 4096)) && wgs(4) <= 256) return go_cpl<8, 4, 2>(a, cpl, s);
   }
   if (a.M >= 3 && a.lda <= INT32_MAX) {

@@ -503,7 +503,7 @@ def test_w4_shapes_bf16_bias_act(K, M):
     (16, 1536, 3088),                            # 8-row tiles, two weight tiles of 16 waves
     (16, 1536, 8208),                            # 8-row tiles, two weight tiles of 8 waves
     (129, 256, 1456),                            # 8-row tiles, four weight tiles
-    (12, 6144, 96), (8, 6144, 1536),             # K > 2048: 4-row tiles, 16 waves
+    (12, 6144, 96), (6, 6144, 2048),             # K > 2048: 4-row tiles, 16 waves
     (24, 3072, 1040),                            # K > 2048: 8-row tiles, one weight tile
     (24, 3072, 1424), (3, 4096, 8192),           # K > 2048: 8-row tiles, two weight tiles
     (12, 8192, 32),                              # 64 groups: 4-row tiles, 16 waves
@@ -538,8 +538,9 @@ def test_w4a16_mfma_shapes(M, K, N, epi, bf16):
     (2, 2048, 2048), (4, 1024, 1024),
     (4, 6144, 1536), (3, 3072, 1040), (8, 3072, 1024),      # two rows per wave (ragged N = 1040)
     (4, 2048, 2048), (5, 2048, 1024),
+    (8, 6144, 1536), (4, 1536, 3072), (2, 6144, 5120),      # three rows per wave
     (2, 4096, 8192), (8, 2048, 2048), (7, 4096, 2048),      # four rows per wave
-    (4, 1536, 3072), (2, 512, 8192),
+    (2, 512, 8192),
     (2, 2304, 8208), (2, 1536, 12304)])                     # wider (M = 2): 4-row waves of 4-wave workgroups
 @pytest.mark.parametrize("epi", ["plain", "bias_silu_bf16", "int8"])
 def test_w4a16_two_row_blocks(M, K, N, epi):
