@@ -17,11 +17,14 @@
 // the chunk's dot is P0 + 16 P1 + 256 P2 + 4096 P3 (16 dot instructions per chunk and row; the
 // former byte split needed 28 instructions).
 //
-// The per-group fp32 terms (i2f(dot) * ws) * xs go to the wave's own LDS rows (the quad's four
-// lanes form the terms of four different rows in one instruction stream); four lanes per row
-// then run the four bank chains (group g goes to bank g % 4, added in g order from +0) and
-// combine (b0 + b1) + (b2 + b3) before bias, activation and conversion. The only workgroup
-// barrier is the one after the alignment.
+// The per-group fp32 terms (i2f(dot) * ws) * xs meet in four bank chains per output (group g goes
+// to bank g % 4, added in g order from +0), combined as (b0 + b1) + (b2 + b3) before bias,
+// activation and conversion: with one activation row the terms stay in registers and the chain
+// lanes gather them by permlane swaps; otherwise they go through the wave's own LDS rows (the
+// quad's four lanes form the terms of four different rows in one instruction stream). The only
+// workgroup barrier is the one after the alignment. Two more forms follow the GEMV: one
+// activation row with K split over the waves of a workgroup, and the INT8 MFMA form for prefill
+// chunks.
 //
 // Roofline: HBM. Algorithmic bytes per row: K/2 (weights) + K/64 (fp16 scales) + 4 (output). The
 // kernels also carry VALU work per weight byte (dots, terms, chains) that measured as the larger
