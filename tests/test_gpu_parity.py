@@ -459,6 +459,40 @@ def w4_inputs(seed: int, M: int, N: int, K: int):
     return x, Wp, ws, rng
 
 
+def random_w4_shape(rng):
+    """A W4A16 launch shape drawn across every form's rule boundaries: M from 1 to 40, K a multiple
+    of 256 up to 8192, N a multiple of 16, the product bounded so the oracle stays quick."""
+    M = int(rng.choice([1, 1, 1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 33, 40]))
+    K = 256 * int(rng.integers(1, 33))
+    N = 16 * int(rng.integers(1, max(2, min(1024, 40_000_000 // (M * K * 16)) + 1)))
+    return M, K, N
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_w4a16_random_shapes(seed):
+    """Random shapes (random_w4_shape) through the automatic launch rule: whichever form and
+    workgroup shape it picks, the result matches the oracle bit for bit, with random bf16 rows, an
+    epilogue, and subnormal, zero, infinite and NaN group scales."""
+    rng = np.random.default_rng(900 + seed)
+    M, K, N = random_w4_shape(rng)
+    x, Wp, ws, _ = w4_inputs(seed * 7919 + M + K + N, M, N, K)
+    ws = ws.copy()
+    for v in (0x0001, 0x0000, 0x7C00, 0xFE01):
+        ws[rng.integers(0, N), rng.integers(0, K // 128)] = v
+    bf16 = bool(rng.integers(0, 2))
+    xin = F.to_bf16_bits(x) if bf16 else x
+    epi = int(rng.integers(0, 3))
+    kw = {}
+    if epi == 1:
+        kw = dict(bias=rng.normal(0, 1, N).astype(f32), act=ACT_SILU, out=OUT_BF16)
+    elif epi == 2:
+        kw = dict(out=OUT_INT8, out_scale=f32(0.125))
+    dkw = {k: (cuda(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+    y = ops.gemm_w4(cuda(xin), cuda(Wp), cuda(ws), x_is_bf16=bf16, **dkw)
+    want = G.gemm_w4(xin, Wp, ws, x_is_bf16=bf16, **kw)
+    assert same(host(y), want), (M, K, N, mismatch(host(y), want))
+
+
 @pytest.mark.parametrize("K,N", [(1536, 12288), (6144, 1536)])
 @pytest.mark.parametrize("seed", range(2))
 def test_c5_w4a16_gemma4(K, N, seed):
