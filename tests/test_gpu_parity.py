@@ -437,6 +437,64 @@ def test_gemv_family_for_prefill_rows_matches():
     assert same(y, G.gemm_rowcol(q, s, W, scol))
 
 
+def random_w8_case(rng):
+    """A W8A8 GEMM drawn across the launch rules of both families: M from 1 to 300, K and N multiples
+    of 16 (K sometimes a whole number of MFMA stages), a scale mode, bias, activation and output
+    format, the product bounded so the oracle stays quick."""
+    M = int(rng.choice([1, 1, 1, 2, 3, 4, 5, 8, 12, 16, 17, 33, 64, 100, 256, 300]))
+    K = 256 * int(rng.integers(1, 25)) if rng.random() < 0.5 else 16 * int(rng.integers(1, 600))
+    N = 16 * int(rng.integers(1, max(2, min(2048, 60_000_000 // (M * K * 16)) + 1)))
+    qm = str(rng.choice(["tensor", "channel", "rowcol"]))
+    act, out = [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16), (ACT_GELU, OUT_FP32),
+                (ACT_SOFTPLUS, OUT_INT8)][int(rng.integers(0, 5))]
+    return M, K, N, qm, bool(rng.integers(0, 2)), act, out
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_w8a8_random_shapes(seed):
+    """Random GEMMs (random_w8_case) through the automatic path rule and, on every third case, the
+    other family forced: bit-exact against the oracle whichever kernel and launch shape run."""
+    rng = np.random.default_rng(700 + seed)
+    M, K, N, qm, bias, act, out = random_w8_case(rng)
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32) if bias else None
+    osc = f32(5.0) if out == OUT_INT8 else None
+    path = ["auto", "auto", "gemv" if M > 4 else "mfma"][seed % 3]
+    prev = ops.set_w8a8_path(path)
+    try:
+        y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc),
+                            None if b is None else cuda(b), act=act, out=out, out_scale=osc)
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), ((M, K, N, qm, path), mismatch(host(y), want))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_ksplit_random_blocks(seed):
+    """The K split over random block counts (1 to 5) and block widths (multiples of 16, total K
+    up to 9000) at random M and N: bit-exact against the oracle's block-ordered partials."""
+    rng = np.random.default_rng(800 + seed)
+    M = int(rng.choice([1, 1, 2, 3, 4, 7, 17, 40]))
+    nb = int(rng.integers(1, 6))
+    ks = [16 * int(rng.integers(1, max(2, 9000 // (16 * nb)))) for _ in range(nb)]
+    N = 16 * int(rng.integers(1, max(2, min(256, 30_000_000 // (M * sum(ks) * 16)) + 1)))
+    x, q, s, W, scol, _ = w8_inputs(seed * 31 + M, M, N, sum(ks))
+    blocks, c0 = [], 0
+    for k in ks:
+        blocks.append(np.ascontiguousarray(W[:, c0:c0 + k]))
+        c0 += k
+    qg, sg = ops.quant_rows(cuda(x))
+    y = ops.gemm_rowcol_ksplit(qg, sg, [cuda(b) for b in blocks], cuda(scol))
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(host(y), want), ((M, ks, N), mismatch(host(y), want))
+
+
 # ------------------------------------------------------------------------------ W4A16 (config 5)
 @pytest.mark.parametrize("i", range(8))
 def test_w4_reference_vectors(i):
