@@ -6,7 +6,7 @@
 // and B use the same map: each dot product is then the exact sum over the instruction's 64 k.
 // Integer accumulation is exact, so K may be split across waves and summed in any order.
 //
-// Two kernel families:
+// Three kernel families:
 //  * mfma_direct_kernel<TM, TN, KW, D>: a workgroup owns a 16 TM x 16 TN output tile and KW waves
 //    that split its K range; every wave loads its share of all 16 (TM + TN) rows straight into
 //    MFMA operand registers, and the int32 partial tiles meet in LDS for the golden fp32 epilogue
@@ -16,6 +16,9 @@
 //    in LDS by direct global -> LDS loads of 4 rows x 256 bytes in a ring of S stages of KS bytes
 //    of K, every wave of the workgroup reading the shared operands from LDS; each wave owns whole
 //    16 x 16 output tiles over the full K, so there is no cross-wave reduction.
+//  * mfma_panel_kernel<KQ>: prompt rows at K = 1024 on 64 x 48 tiles. The whole K of the tile's
+//    rows is resident in LDS, loaded in three phases, and each 16-column block of the output is
+//    computed and stored as its weight rows land.
 //
 // Roofline: at M = 4 HBM (every weight byte read once); at M = 256 the int32 MFMA work is small
 // (1.6 GOP) and the kernels are bound by operand traffic from L2 into the CUs and by the fixed
@@ -466,6 +469,159 @@ hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------ panels
+// 64 x 48 prompt-row tiles with the whole K (256 KQ bytes) resident in LDS. The tile's 112 rows are
+// loaded in three phases, each wave issuing its loads in phase order: the 64 A rows with the first
+// 16 weight rows, then the next 16 weight rows, then the last 16. The output's three 16-column
+// blocks are computed and put through the epilogue as their weight rows land, and the first
+// blocks' stores overlap the later loads. (Through a ring over K every output waits for the last
+// stage, and the whole tile's stores leave together after it.) LDS layout, swizzle and load shape
+// are mfma_tile_kernel's: 16-row groups of KQ blocks of 16 rows x 256 bytes, each global -> LDS
+// load 4 rows x 256 bytes. Wave w owns output rows 16 w .. 16 w + 15 and keeps its A operands in
+// registers across the three blocks.
+//
+// vmcnt counts stores as well as loads, so a wait for the last phase's loads also waits for every
+// store issued before it to complete. Block 1's store is therefore issued after that wait (issued
+// before it, the wait took ~0.2 us longer); block 0's store, issued earlier, has completed by then.
+// The epilogue operands are loaded after the first phase's loads, so the wait for that phase covers
+// them and they do not delay its first loads.
+template <int KQ, bool SIMPLE>
+__global__ __launch_bounds__(256) void mfma_panel_kernel(const int8_t* A, const int8_t* W, const float* scol,
+                                                        const float* srow, int lda, int K, int M, int N, int mt,
+                                                        int ldy, void* Y, TileTail tl) {
+  constexpr int GA = 4, GB = 3, NKB = 4 * KQ, GRP = 4096 * KQ;  // A / W 16-row groups, 64-k steps
+  static_assert(KQ >= 1 && 7 * KQ < 64 && (GA + GB) * GRP <= 163840, "panel shape");
+  __shared__ __align__(16) int8_t lds[(GA + GB) * GRP];
+  const v4i zero = {0, 0, 0, 0};
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  // the tile order of mfma_tile_kernel: each XCD a contiguous range of tiles, M tiles fastest
+  const int G8 = mt * ((N + 47) / 48);
+  const int b = blockIdx.x;
+  const int t = (G8 % 8 == 0) ? (b % 8) * (G8 / 8) + b / 8 : b;
+  const int m0 = (t % mt) * 64, n0 = (t / mt) * 48;
+  const int m = m0 + 16 * wave + li;  // this lane's output row
+
+  // This wave's load u: 16-row group u / KQ (A groups first), K block u % KQ, rows 4 wave .. + 3
+  // of the group (lane: row 4 wave + lg, 16-byte chunk li ^ row), landing at LDS byte
+  // 1024 (4 u + wave). Rows past the matrix are clamped to its last row: they feed only outputs
+  // that are not stored.
+  auto load = [&](int u) {
+    const int g = u / KQ, kq = u % KQ, r = 4 * wave + lg;
+    const int8_t* row = g < GA ? A + static_cast<int64_t>(min(m0 + 16 * g + r, M - 1)) * lda
+                               : W + static_cast<int64_t>(min(n0 + 16 * (g - GA) + r, N - 1)) * K;
+    stage16(row + 256 * kq + 16 * (li ^ r), lds + 1024 * (4 * u + wave));
+  };
+#pragma unroll
+  for (int u = 0; u < (GA + 1) * KQ; ++u) load(u);
+  issue_fence();
+  // Epilogue operands of this lane's outputs (row m, columns n0 + 16 j + 4 lg .. + 3); a 16-column
+  // block past N reads the last block (its outputs are not stored).
+  float sc[GB][4], bi[GB][4];
+#pragma unroll
+  for (int j = 0; j < GB; ++j) {
+    const int nb = min(n0 + 16 * j, N - 16) + 4 * lg;
+    float4 c4, b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (SIMPLE || !tl.scol_per_tensor) c4 = *reinterpret_cast<const float4*>(scol + nb);
+    else c4 = make_float4(scol[0], scol[0], scol[0], scol[0]);
+    if (!SIMPLE && tl.bias) b4 = *reinterpret_cast<const float4*>(tl.bias + nb);
+    sc[j][0] = c4.x, sc[j][1] = c4.y, sc[j][2] = c4.z, sc[j][3] = c4.w;
+    bi[j][0] = b4.x, bi[j][1] = b4.y, bi[j][2] = b4.z, bi[j][3] = b4.w;
+  }
+  const float sr = *(srow ? srow + min(m, M - 1) : scol);
+  issue_fence();
+#pragma unroll
+  for (int u = (GA + 1) * KQ; u < (GA + GB) * KQ; ++u) load(u);
+
+  auto store = [&](int j, const float (&y)[4]) {
+    const int n = n0 + 16 * j + 4 * lg;
+    if (m < M && n < N) {
+      if constexpr (SIMPLE) {
+        *reinterpret_cast<float4*>(static_cast<char*>(Y) + static_cast<int64_t>(m) * ldy + 4 * n) =
+            make_float4(ftz(y[0]), ftz(y[1]), ftz(y[2]), ftz(y[3]));
+      } else {
+        store_out4(Y, static_cast<int64_t>(m) * ldy, n, tl.out, y, tl.out_scale);
+      }
+    }
+  };
+  const int8_t* const rd = lds + 256 * li;
+  // phase 0: at most the last two groups' loads of this wave outstanding, then every wave's
+  wait_vmcnt<2 * KQ>();
+  __builtin_amdgcn_s_barrier();
+  v4i fa[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+    fa[kb] = *reinterpret_cast<const v4i*>(rd + GRP * wave + 4096 * (kb / 4) + 16 * ((4 * (kb % 4) + lg) ^ li));
+  float y1[4];
+#pragma unroll
+  for (int j = 0; j < GB; ++j) {
+    if (j == 1) {
+      // the last group's loads may still be outstanding, and block 0's store issued after them
+      // (loads complete in issue order, so at most KQ outstanding covers both cases)
+      wait_vmcnt<KQ>();
+      __builtin_amdgcn_s_barrier();
+    } else if (j == 2) {
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      store(1, y1);
+    }
+    // two exact int32 chains over alternate k steps (integer adds are order-free)
+    v4i acc0 = zero, acc1 = zero;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const v4i fw = *reinterpret_cast<const v4i*>(rd + GRP * (GA + j) + 4096 * (kb / 4) +
+                                                   16 * ((4 * (kb % 4) + lg) ^ li));
+      if (kb & 1) acc1 = mfma(fw, fa[kb], acc1);
+      else acc0 = mfma(fw, fa[kb], acc0);
+    }
+    const v4i acc = acc0 + acc1;
+    // W is the MFMA's first operand, so lane l holds columns 4 lg .. 4 lg + 3 of row li
+    float y[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if constexpr (SIMPLE) {
+        y[v] = fmul(fmul(i2f(acc[v]), sr), sc[j][v]);
+      } else {
+        float z = i2f(acc[v]);
+        if (srow) z = fmul(z, sr);
+        z = fmul(z, sc[j][v]);
+        if (tl.bias) z = fadd(z, bi[j][v]);
+        y[v] = act_fn(z, tl.act);
+      }
+    }
+    if (j == 1) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) y1[v] = y[v];
+    } else {
+      store(j, y);
+    }
+  }
+}
+
+template <int KQ>
+hipError_t go_panel(const MfmaArgs& a, hipStream_t s) {
+  const int mt = (a.M + 63) / 64, nt = (a.N + 47) / 48;
+  TileTail tl{};
+  tl.nseg = 1;
+  tl.bias = a.epi.bias;
+  tl.scol_per_tensor = a.epi.scol_per_tensor;
+  tl.act = a.epi.act;
+  tl.out = a.epi.out;
+  tl.out_scale = a.epi.out_scale;
+  const RowColEpilogue& e = a.epi;
+  const bool simple = e.srow && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0;
+  const int lda = static_cast<int>(a.lda), ldy = static_cast<int>(a.ldy);
+  const dim3 grid(mt * nt), block(256);
+  if (simple)
+    hipLaunchKernelGGL((mfma_panel_kernel<KQ, true>), grid, block, 0, s, a.A + a.seg[0].koff, a.seg[0].W, e.scol,
+                       e.srow, lda, a.seg[0].K, a.M, a.N, mt, ldy, a.Y, tl);
+  else
+    hipLaunchKernelGGL((mfma_panel_kernel<KQ, false>), grid, block, 0, s, a.A + a.seg[0].koff, a.seg[0].W, e.scol,
+                       e.srow, lda, a.seg[0].K, a.M, a.N, mt, ldy, a.Y, tl);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------------------------ dispatch
 // Chunk rows (M <= 16): the direct kernel with one 16-column tile per workgroup and 8 waves over
 // K (the weights have no reuse, so the most workgroups and the most weight bytes in flight).
@@ -474,7 +630,10 @@ hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
 // tiles; the direct kernel's 32 x 32 tiles with 4 waves over K otherwise.
 //  * 64 x 48 tiles (4 waves of 16 x 48, 256-byte stages, 3 slots) when they give one to 1.25
 //    workgroups per CU: M=256 K=1024 N=3072 7.5 -> 5.5 us (the 64 x 64 / 16-row-load tiles before;
-//    4 / 5 slots 5.70 / 5.89 us against 5.40, 512-byte stages in 2 slots 5.41 us);
+//    4 / 5 slots 5.70 / 5.89 us against 5.40, 512-byte stages in 2 slots 5.41 us); at K = 1024 the
+//    panel form of the same tiles instead: 5.41 -> 4.79 us (5.04 us with block 1's store issued
+//    before the last wait and the epilogue operands before the first loads; block 2 in two K
+//    halves 4.86 us);
 //  * 64 x 64 tiles (4 waves of 32 x 32, 256-byte stages, 3 slots) when they give 512 or more:
 //    M=1024 K=1024 N=3072 16.5 -> 15.8 us;
 //  * 32 x 32 tiles (4 waves of 16 x 16) with 512-byte stages in 3 slots when K is a multiple of
@@ -496,7 +655,10 @@ hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
   if (!whole_stages(a, 256)) return go_direct<2, 2, 4, 1>(a, s);
   const int64_t t48 = tiles(a, 64, 48), t32 = tiles(a, 32, 32);
-  if (t48 >= 192 && t48 <= 320) return go_tile<64, 48, 4, 1, 256, 3>(a, s);
+  if (t48 >= 192 && t48 <= 320) {
+    if (a.nseg == 1 && a.seg[0].K == 1024) return go_panel<4>(a, s);
+    return go_tile<64, 48, 4, 1, 256, 3>(a, s);
+  }
   if (tiles(a, 64, 64) >= 512) return go_tile<64, 64, 2, 2, 256, 3>(a, s);
   if (t32 <= 320 && whole_stages(a, 1024)) return go_tile<32, 32, 2, 2, 512, 3>(a, s);
   return go_tile<32, 32, 2, 2, 256, 3>(a, s);

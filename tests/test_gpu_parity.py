@@ -335,12 +335,14 @@ def test_epilogue_matrix_prompt_tiles(qm, act, out):
 @pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
 @pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
                                      (ACT_GELU, OUT_FP32), (ACT_SOFTPLUS, OUT_BF16)])
-@pytest.mark.parametrize("M,N,K", [(45, 80, 768), (45, 80, 2048), (200, 3072 + 16, 512)])
+@pytest.mark.parametrize("M,N,K", [(45, 80, 768), (45, 80, 2048), (200, 3072 + 16, 512), (200, 3072 + 16, 1024),
+                                   (131, 4608, 1024)])
 def test_epilogue_matrix_staged_tiles(qm, act, out, M, N, K):
-    """The LDS tile kernel (K a multiple of 256) through every scale mode and output format with a
+    """The LDS tile kernels (K a multiple of 256) through every scale mode and output format with a
     bias, ragged last row and column tiles, a huge scale and int8 -128: 32 x 32 tiles with
-    256-byte stages (K=768), with 512-byte stages in 3 slots (K=2048), and 64 x 48 tiles (M=200,
-    N=3088)."""
+    256-byte stages (K=768), with 512-byte stages in 3 slots (K=2048), 64 x 48 tiles (M=200,
+    N=3088, K=512), and the 64 x 48 tiles with the whole K resident (K=1024; at M=131 three of the
+    last row tile's four waves have no row to store)."""
     rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, M, N, K, "staged")).encode()))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
