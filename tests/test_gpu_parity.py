@@ -204,6 +204,24 @@ def test_strided_rows_and_untouched_gaps():
         assert (yb[:, N:] == -7.0).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(200, 3072, 1024), (200, 3088, 512), (100, 1040, 2048), (1040, 2064, 256)])
+def test_strided_rows_prompt_tiles(M, N, K):
+    """The LDS tile kernels on strided A and Y rows: the whole-K panels (K=1024), 64 x 48 tiles with
+    256-byte stages (K=512), 32 x 32 tiles with 512-byte stages (K=2048) and 64 x 64 tiles; the dense
+    result, and the gaps left as they were."""
+    rng = np.random.default_rng(M * 31 + N + K)
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-3, 1e-2, N).astype(f32)
+    sr = rng.uniform(0.5, 2, M).astype(f32)
+    abig = cuda(np.concatenate([A, np.zeros((M, 256), np.int8)], axis=1))
+    ybig = torch.full((M, N + 20), -7.0, dtype=torch.float32, device="cuda")
+    ops.gemm_rowcol(abig[:, :K], cuda(sr), cuda(W), cuda(sc), y=ybig[:, :N])
+    yb = host(ybig)
+    assert same(yb[:, :N].copy(), G.gemm_rowcol(A, sr, W, sc))
+    assert (yb[:, N:] == -7.0).all()
+
+
 def test_overlap_is_refused_and_nothing_is_written():
     rng = np.random.default_rng(3)
     buf = torch.zeros(64 * 1024 + 4096, dtype=torch.int8, device="cuda")
