@@ -653,7 +653,8 @@ int64_t tiles(const MfmaArgs& a, int bm, int bn) {
 
 hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
-  if (!whole_stages(a, 256)) return go_direct<2, 2, 4, 1>(a, s);
+  // the LDS tile kernels take 32-bit row strides; the direct kernel any
+  if (!whole_stages(a, 256) || a.lda > INT32_MAX || a.ldy > INT32_MAX) return go_direct<2, 2, 4, 1>(a, s);
   const int64_t t48 = tiles(a, 64, 48), t32 = tiles(a, 32, 32);
   if (t48 >= 192 && t48 <= 320) {
     if (a.nseg == 1 && a.seg[0].K == 1024) return go_panel<4>(a, s);
