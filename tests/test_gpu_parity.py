@@ -204,11 +204,13 @@ def test_strided_rows_and_untouched_gaps():
         assert (yb[:, N:] == -7.0).all()
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 3072, 1024), (200, 3088, 512), (100, 1040, 2048), (1040, 2064, 256)])
+@pytest.mark.parametrize("M,N,K", [(200, 3072, 1024), (129, 3072, 1024), (300, 3072, 1024), (200, 3088, 512),
+                                   (100, 1040, 2048), (1040, 2064, 256)])
 def test_strided_rows_prompt_tiles(M, N, K):
-    """The LDS tile kernels on strided A and Y rows: the whole-K panels (K=1024), 64 x 48 tiles with
-    256-byte stages (K=512), 32 x 32 tiles with 512-byte stages (K=2048) and 64 x 64 tiles; the dense
-    result, and the gaps left as they were."""
+    """The LDS tile kernels on strided A and Y rows: the whole-K panels (K=1024 at 256, 192 and 320
+    tiles, the rule's middle and ends), 64 x 48 tiles with 256-byte stages (K=512), 32 x 32 tiles
+    with 512-byte stages (K=2048) and 64 x 64 tiles; the dense result, and the gaps left as they
+    were."""
     rng = np.random.default_rng(M * 31 + N + K)
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
