@@ -497,6 +497,33 @@ def test_w8a8_random_shapes(seed):
     assert same(host(y), want), ((M, K, N, qm, path), mismatch(host(y), want))
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_w8a8_random_panels(seed):
+    """Random GEMMs that the whole-K panel rule takes (K = 1024, 192 to 320 tiles of 64 x 48, ragged
+    last row and column tiles), every scale mode, bias, activation and output format: bit-exact
+    against the oracle."""
+    rng = np.random.default_rng(900 + seed)
+    mt = int(rng.integers(3, 6))
+    M = 64 * mt - int(rng.integers(0, 63))
+    nt = int(rng.integers(-(-192 // mt), 320 // mt + 1))
+    N, K = 48 * nt - 16 * int(rng.integers(0, 3)), 1024
+    qm = str(rng.choice(["tensor", "channel", "rowcol"]))
+    act, out = [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16), (ACT_GELU, OUT_FP32),
+                (ACT_SOFTPLUS, OUT_INT8)][int(rng.integers(0, 5))]
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32) if rng.random() < 0.5 else None
+    osc = f32(5.0) if out == OUT_INT8 else None
+    y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc),
+                        None if b is None else cuda(b), act=act, out=out, out_scale=osc)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), ((M, N, qm, act, out), mismatch(host(y), want))
+
+
 @pytest.mark.parametrize("seed", range(24))
 def test_ksplit_random_blocks(seed):
     """The K split over random block counts (1 to 5) and block widths (multiples of 16, total K
