@@ -16,7 +16,7 @@
 //    in LDS by direct global -> LDS loads of 4 rows x 256 bytes in a ring of S stages of KS bytes
 //    of K, every wave of the workgroup reading the shared operands from LDS; each wave owns whole
 //    16 x 16 output tiles over the full K, so there is no cross-wave reduction.
-//  * mfma_panel_kernel<KQ>: prompt rows at K = 1024 on 64 x 48 tiles. The whole K of the tile's
+//  * mfma_panel_kernel<KQ>: prompt rows at K <= 1280 on 64 x 48 tiles. The whole K of the tile's
 //    rows is resident in LDS, loaded in three phases, and each 16-column block of the output is
 //    computed and stored as its weight rows land.
 //
@@ -630,10 +630,11 @@ hipError_t go_panel(const MfmaArgs& a, hipStream_t s) {
 // tiles; the direct kernel's 32 x 32 tiles with 4 waves over K otherwise.
 //  * 64 x 48 tiles (4 waves of 16 x 48, 256-byte stages, 3 slots) when they give one to 1.25
 //    workgroups per CU: M=256 K=1024 N=3072 7.5 -> 5.5 us (the 64 x 64 / 16-row-load tiles before;
-//    4 / 5 slots 5.70 / 5.89 us against 5.40, 512-byte stages in 2 slots 5.41 us); at K = 1024 the
-//    panel form of the same tiles instead: 5.41 -> 4.79 us (5.04 us with block 1's store issued
-//    before the last wait and the epilogue operands before the first loads; block 2 in two K
-//    halves 4.86 us);
+//    4 / 5 slots 5.70 / 5.89 us against 5.40, 512-byte stages in 2 slots 5.41 us); with one K block
+//    of at most 1280 the panel form of the same tiles instead: K = 1024 5.41 -> 4.71 us (5.04 us
+//    with block 1's store issued before the last wait and the epilogue operands before the first
+//    loads; block 2 in two K halves 4.86 us), K = 256 / 512 / 768 / 1280 at N = 3072: 3.91 / 4.45 /
+//    4.92 / 5.89 -> 3.63 / 3.96 / 4.27 / 5.26 us;
 //  * 64 x 64 tiles (4 waves of 32 x 32, 256-byte stages, 3 slots) when they give 512 or more:
 //    M=1024 K=1024 N=3072 16.5 -> 15.8 us;
 //  * 32 x 32 tiles (4 waves of 16 x 16) with 512-byte stages in 3 slots when K is a multiple of
@@ -657,7 +658,15 @@ hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (!whole_stages(a, 256) || a.lda > INT32_MAX || a.ldy > INT32_MAX) return go_direct<2, 2, 4, 1>(a, s);
   const int64_t t48 = tiles(a, 64, 48), t32 = tiles(a, 32, 32);
   if (t48 >= 192 && t48 <= 320) {
-    if (a.nseg == 1 && a.seg[0].K == 1024) return go_panel<4>(a, s);
+    if (a.nseg == 1 && a.seg[0].K <= 1280) {
+      switch (a.seg[0].K / 256) {
+        case 1: return go_panel<1>(a, s);
+        case 2: return go_panel<2>(a, s);
+        case 3: return go_panel<3>(a, s);
+        case 4: return go_panel<4>(a, s);
+        default: return go_panel<5>(a, s);
+      }
+    }
     return go_tile<64, 48, 4, 1, 256, 3>(a, s);
   }
   if (tiles(a, 64, 64) >= 512) return go_tile<64, 64, 2, 2, 256, 3>(a, s);

@@ -204,13 +204,13 @@ def test_strided_rows_and_untouched_gaps():
         assert (yb[:, N:] == -7.0).all()
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 3072, 1024), (129, 3072, 1024), (300, 3072, 1024), (200, 3088, 512),
-                                   (100, 1040, 2048), (1040, 2064, 256)])
+@pytest.mark.parametrize("M,N,K", [(200, 3072, 1024), (129, 3072, 1024), (300, 3072, 1024), (200, 3088, 256),
+                                   (200, 3088, 1536), (100, 1040, 2048), (1040, 2064, 256)])
 def test_strided_rows_prompt_tiles(M, N, K):
     """The LDS tile kernels on strided A and Y rows: the whole-K panels (K=1024 at 256, 192 and 320
-    tiles, the rule's middle and ends), 64 x 48 tiles with 256-byte stages (K=512), 32 x 32 tiles
-    with 512-byte stages (K=2048) and 64 x 64 tiles; the dense result, and the gaps left as they
-    were."""
+    tiles, the rule's middle and ends; K=256), 64 x 48 tiles through the ring (K=1536), 32 x 32
+    tiles with 512-byte stages (K=2048) and 64 x 64 tiles; the dense result, and the gaps left as
+    they were."""
     rng = np.random.default_rng(M * 31 + N + K)
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
@@ -355,14 +355,14 @@ def test_epilogue_matrix_prompt_tiles(qm, act, out):
 @pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
 @pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
                                      (ACT_GELU, OUT_FP32), (ACT_SOFTPLUS, OUT_BF16)])
-@pytest.mark.parametrize("M,N,K", [(45, 80, 768), (45, 80, 2048), (200, 3072 + 16, 512), (200, 3072 + 16, 1024),
-                                   (131, 4608, 1024)])
+@pytest.mark.parametrize("M,N,K", [(45, 80, 768), (45, 80, 2048), (200, 3072 + 16, 1536), (200, 3072 + 16, 512),
+                                   (200, 3072 + 16, 1024), (131, 4608, 1280)])
 def test_epilogue_matrix_staged_tiles(qm, act, out, M, N, K):
     """The LDS tile kernels (K a multiple of 256) through every scale mode and output format with a
     bias, ragged last row and column tiles, a huge scale and int8 -128: 32 x 32 tiles with
-    256-byte stages (K=768), with 512-byte stages in 3 slots (K=2048), 64 x 48 tiles (M=200,
-    N=3088, K=512), and the 64 x 48 tiles with the whole K resident (K=1024; at M=131 three of the
-    last row tile's four waves have no row to store)."""
+    256-byte stages (K=768), with 512-byte stages in 3 slots (K=2048), 64 x 48 tiles through the
+    ring (M=200, N=3088, K=1536), and the 64 x 48 tiles with the whole K resident (K=512, 1024,
+    1280; at M=131 three of the last row tile's four waves have no row to store)."""
     rng = np.random.default_rng(zlib.crc32(repr((qm, act, out, M, N, K, "staged")).encode()))
     A = rng.integers(-128, 128, (M, K), dtype=np.int8)
     W = rng.integers(-128, 128, (N, K), dtype=np.int8)
@@ -499,14 +499,14 @@ def test_w8a8_random_shapes(seed):
 
 @pytest.mark.parametrize("seed", range(12))
 def test_w8a8_random_panels(seed):
-    """Random GEMMs that the whole-K panel rule takes (K = 1024, 192 to 320 tiles of 64 x 48, ragged
-    last row and column tiles), every scale mode, bias, activation and output format: bit-exact
-    against the oracle."""
+    """Random GEMMs that the whole-K panel rule takes (K from 256 to 1280, 192 to 320 tiles of
+    64 x 48, ragged last row and column tiles), every scale mode, bias, activation and output
+    format: bit-exact against the oracle."""
     rng = np.random.default_rng(900 + seed)
     mt = int(rng.integers(3, 6))
     M = 64 * mt - int(rng.integers(0, 63))
     nt = int(rng.integers(-(-192 // mt), 320 // mt + 1))
-    N, K = 48 * nt - 16 * int(rng.integers(0, 3)), 1024
+    N, K = 48 * nt - 16 * int(rng.integers(0, 3)), 256 * int(rng.integers(1, 6))
     qm = str(rng.choice(["tensor", "channel", "rowcol"]))
     act, out = [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16), (ACT_GELU, OUT_FP32),
                 (ACT_SOFTPLUS, OUT_INT8)][int(rng.integers(0, 5))]
