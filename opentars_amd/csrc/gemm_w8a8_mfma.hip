@@ -482,7 +482,8 @@ hipError_t go_tile(const MfmaArgs& a, hipStream_t s) {
 //
 // vmcnt counts stores as well as loads, so a wait for the last phase's loads also waits for every
 // store issued before it to complete. Block 1's store is therefore issued after that wait (issued
-// before it, the wait took ~0.2 us longer); block 0's store, issued earlier, has completed by then.
+// before it, the wait took ~0.2 us longer). Block 0's store goes out before block 1's work and has
+// usually completed by then (deferring it past the wait as well measured the same).
 // The epilogue operands are loaded after the first phase's loads, so the wait for that phase covers
 // them and they do not delay its first loads.
 template <int KQ, bool SIMPLE>
