@@ -725,8 +725,8 @@ CONFIG_KERNELS = {
     "c2_gemma3_down_ksplit_4096+2816": ("gemv_w8a8_ksplit2_kernel<7, 1, 5>", 73920),
     "c4_prefill_M4_K1024_N3072": ("gemv_w8a8_kernel<64, 1, 2, 4, true>", 98304),
     "c4_prefill_M4_K3072_N1024": ("gemv_w8a8_kernel<64, 3, 1, 4, true>", 65536),
-    "c4_prefill_M4_K1024_N3072_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 98304),
-    "c4_prefill_M4_K3072_N1024_mfma": ("mfma_direct_kernel<1, 1, 8, 1, true>", 32768),
+    "c4_prefill_M4_K1024_N3072_mfma": ("mfma_chunk_kernel<4, 2, true>", 49152),
+    "c4_prefill_M4_K3072_N1024_mfma": ("mfma_chunk_kernel<8, 2, true>", 32768),
     "c4_prefill_M256_K1024_N3072": ("mfma_panel_kernel<4, true>", 65536),
     "c4_prefill_M256_K3072_N1024": ("mfma_tile_kernel<32, 32, 2, 2, 512, 3, true, false>", 65536),
     "c5_w4a16_M1_K1536_N12288": ("gemv_w4a16_kernel<4, 4, 1, 1, false, true>", 196608),

@@ -18,14 +18,24 @@ namespace {
 thread_local std::string g_last_error;
 int g_w8a8_path = 0;  // 0 auto, 1 GEMV family, 2 MFMA family
 
-// Automatic family for a W8A8 product of M rows and N output channels: the dot-product GEMV
-// family (weights read once per 4 rows) up to 4 rows, and up to 16 rows when N < 2048 (too few
-// 16-column MFMA tiles to fill the chip); the INT8 MFMA family otherwise. Measured on MI355X at
-// K=1024 N=3072 and K=3072 N=1024: M=4 3.8 / 3.8 us (GEMV) vs 4.3 / 6.0 us (MFMA); M=16 6.8 /
-// 5.6 us vs 4.6 / 6.8 us.
-bool use_gemv(int M, int N) {
+// Automatic family for a W8A8 product of M rows, N output channels and K: the dot-product GEMV
+// family (weights read once per 4 rows), or the INT8 MFMA family. Measured on MI355X with the
+// weights cold, over M = 2 - 16 and 14 (K, N) pairs from 1024 x 1024 to 1024 x 151936:
+//  * M <= 2: the GEMV family everywhere;
+//  * M = 3 - 4: the GEMV family, except on the LDS-staged chunk-row MFMA kernel (K whole 256-byte
+//    blocks) at K >= 3072 and N >= 4096 (K = 4096, N = 4096: 6.2 -> 5.2 us; the decode chunk's own
+//    shapes stay on the GEMV family: K = 1024, N = 151936 28.7 against 42.5 us);
+//  * M = 5 - 8: two GEMV row blocks read the weights twice, so the chunk-row MFMA kernel from
+//    N = 4096 (K = 1024, N = 6144: 4.3 -> 3.6 us; N = 3072 ties, N <= 2048 keeps the GEMV family);
+//  * M = 9 - 16: the GEMV family while N < 2048 (too few 16-column MFMA tiles to fill the chip),
+//    the MFMA family otherwise (K = 1024, N = 3072, M = 12: 3.4 -> 3.0 us).
+bool use_gemv(int M, int N, int K) {
   if (g_w8a8_path != 0) return g_w8a8_path == 1;
-  return M <= 4 || (M <= 16 && N < 2048);
+  const bool chunk = K % 256 == 0;  // the MFMA family's chunk-row kernel takes this K
+  if (M <= 2) return true;
+  if (M <= 4) return !(chunk && K >= 3072 && N >= 4096);
+  if (M <= 8) return !(chunk && N >= 4096);
+  return M <= 16 && N < 2048;
 }
 
 int fail(int code, const char* what) {
@@ -297,7 +307,7 @@ int tars_gemm_w8a8(const int8_t* A, int64_t lda, const float* srow, const int8_t
   a.M = M;
   a.N = N;
   a.K = K;
-  const bool gemv = use_gemv(M, N);
+  const bool gemv = use_gemv(M, N, K);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return launched(gemv ? tars::launch_gemv_w8a8(a, s) : tars::launch_gemm_w8a8_mfma(a, s));
 }

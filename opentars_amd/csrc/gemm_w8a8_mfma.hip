@@ -6,12 +6,15 @@
 // and B use the same map: each dot product is then the exact sum over the instruction's 64 k.
 // Integer accumulation is exact, so K may be split across waves and summed in any order.
 //
-// Three kernel families:
+// Four kernel families:
+//  * mfma_chunk_kernel<KW, DB>: chunk rows (M <= 16) with one K block of whole 256-byte blocks: one
+//    16 x 16 output tile per workgroup, its weight and activation rows staged in LDS by each wave
+//    for its own share of K, the int32 partial tiles summed in LDS.
 //  * mfma_direct_kernel<TM, TN, KW, D>: a workgroup owns a 16 TM x 16 TN output tile and KW waves
 //    that split its K range; every wave loads its share of all 16 (TM + TN) rows straight into
 //    MFMA operand registers, and the int32 partial tiles meet in LDS for the golden fp32 epilogue
 //    (or, for a K split, the per-block epilogue and the in-order fp32 adds across blocks). Used for
-//    chunk rows (M <= 16) and for K blocks that are not a whole number of stages.
+//    K splits and for K blocks that are not a whole number of 256-byte stages.
 //  * mfma_tile_kernel<BM, BN, WM, WN, KS, S>: prompt rows. The tile's A and W rows are staged
 //    in LDS by direct global -> LDS loads of 4 rows x 256 bytes in a ring of S stages of KS bytes
 //    of K, every wave of the workgroup reading the shared operands from LDS; each wave owns whole
@@ -623,9 +626,135 @@ hipError_t go_panel(const MfmaArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------ chunk rows
+// Chunk rows (M <= 16) on one 16 x 16 output tile per workgroup, the tile's 16 weight rows and up
+// to 16 activation rows staged in LDS by global -> LDS loads of 4 rows x 256 bytes (the layout and
+// swizzle of mfma_tile_kernel's 16-row blocks), K split over the KW waves in 256-byte blocks. A
+// wave stages and reads only its own blocks, so it waits on its own loads and needs no workgroup
+// barrier until its int32 partial tile meets the others in LDS; wave 0 then forms the epilogue.
+template <int KW, int DB, bool SIMPLE>
+__global__ __launch_bounds__(64 * KW) void mfma_chunk_kernel(const int8_t* A, const int8_t* W, const float* scol,
+                                                            const float* srow, int lda, int K, int M, int N, int ldy,
+                                                            void* Y, TileTail tl) {
+  constexpr int SLOT = DB * 8192;
+  constexpr int RP = 20;             // int32 pitch of a partial tile's row in LDS
+  __shared__ __align__(16) int8_t lds[KW * SLOT];
+  __shared__ __align__(16) int32_t red[KW][16][RP];
+  const v4i zero = {0, 0, 0, 0};
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int nt = N >> 4, b = blockIdx.x;
+  const int n0 = 16 * ((nt % 8 == 0) ? (b % 8) * (nt / 8) + b / 8 : b);
+  // wave 0's epilogue operands: row li / 4 ... (thread t < 64: row t >> 2, columns 4 (t & 3) ..)
+  const int er = lane >> 2, ec = n0 + 4 * (lane & 3);
+  float sr = 0.0f, sc[4], bi[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave == 0) {
+    float4 c4 = (SIMPLE || !tl.scol_per_tensor) ? *reinterpret_cast<const float4*>(scol + ec)
+                                                : make_float4(scol[0], scol[0], scol[0], scol[0]);
+    sc[0] = c4.x, sc[1] = c4.y, sc[2] = c4.z, sc[3] = c4.w;
+    if (!SIMPLE && tl.bias) {
+      const float4 b4 = *reinterpret_cast<const float4*>(tl.bias + ec);
+      bi[0] = b4.x, bi[1] = b4.y, bi[2] = b4.z, bi[3] = b4.w;
+    }
+    sr = *(srow ? srow + min(er, M - 1) : scol);
+  }
+  issue_fence();
+  const int nb = K >> 8, b0 = nb * wave / KW, b1 = nb * (wave + 1) / KW;
+  const int aq = (M + 3) >> 2;       // activation row quads holding live rows
+  int8_t* const slot = lds + SLOT * wave;
+  v4i acc0 = zero, acc1 = zero;
+  for (int bb = b0; bb < b1; bb += DB) {
+    const int nbb = min(DB, b1 - bb);
+    // the previous batch's operand reads are done before its slot is refilled
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      if (d >= nbb) break;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 4 * q + lg, k = 256 * (bb + d) + 16 * (li ^ r);
+        stage16(W + static_cast<int64_t>(n0 + r) * K + k, slot + 8192 * d + 1024 * q);
+        if (q < aq) stage16(A + static_cast<int64_t>(min(r, M - 1)) * lda + k, slot + 8192 * d + 4096 + 1024 * q);
+      }
+    }
+    wait_vmcnt<0>();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      if (d >= nbb) break;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int off = 8192 * d + 256 * li + 16 * ((4 * kk + lg) ^ li);
+        const v4i fw = *reinterpret_cast<const v4i*>(slot + off);
+        const v4i fa = *reinterpret_cast<const v4i*>(slot + off + 4096);
+        if (kk & 1) acc1 = mfma(fw, fa, acc1);
+        else acc0 = mfma(fw, fa, acc0);
+      }
+    }
+  }
+  // W is the MFMA's first operand: lane l holds columns 4 lg .. 4 lg + 3 of row li
+  const v4i acc = acc0 + acc1;
+  *reinterpret_cast<v4i*>(&red[wave][li][4 * lg]) = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  v4i sum = *reinterpret_cast<const v4i*>(&red[0][er][4 * (lane & 3)]);
+#pragma unroll
+  for (int w = 1; w < KW; ++w) sum += *reinterpret_cast<const v4i*>(&red[w][er][4 * (lane & 3)]);
+  float y[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if constexpr (SIMPLE) {
+      y[v] = fmul(fmul(i2f(sum[v]), sr), sc[v]);
+    } else {
+      float z = i2f(sum[v]);
+      if (srow) z = fmul(z, sr);
+      z = fmul(z, sc[v]);
+      if (tl.bias) z = fadd(z, bi[v]);
+      y[v] = act_fn(z, tl.act);
+    }
+  }
+  if (er < M) {
+    if constexpr (SIMPLE) {
+      *reinterpret_cast<float4*>(static_cast<char*>(Y) + static_cast<int64_t>(er) * ldy + 4 * ec) =
+          make_float4(ftz(y[0]), ftz(y[1]), ftz(y[2]), ftz(y[3]));
+    } else {
+      store_out4(Y, static_cast<int64_t>(er) * ldy, ec, tl.out, y, tl.out_scale);
+    }
+  }
+}
+
+template <int KW, int DB = 2>
+hipError_t go_chunk(const MfmaArgs& a, hipStream_t s) {
+  TileTail tl{};
+  tl.nseg = 1;
+  tl.bias = a.epi.bias;
+  tl.scol_per_tensor = a.epi.scol_per_tensor;
+  tl.act = a.epi.act;
+  tl.out = a.epi.out;
+  tl.out_scale = a.epi.out_scale;
+  const RowColEpilogue& e = a.epi;
+  const bool simple = e.srow && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0;
+  const int lda = static_cast<int>(a.lda), ldy = static_cast<int>(a.ldy);
+  const dim3 grid(a.N / 16), block(64 * KW);
+  if (simple)
+    hipLaunchKernelGGL((mfma_chunk_kernel<KW, DB, true>), grid, block, 0, s, a.A + a.seg[0].koff, a.seg[0].W, e.scol,
+                       e.srow, lda, a.seg[0].K, a.M, a.N, ldy, a.Y, tl);
+  else
+    hipLaunchKernelGGL((mfma_chunk_kernel<KW, DB, false>), grid, block, 0, s, a.A + a.seg[0].koff, a.seg[0].W, e.scol,
+                       e.srow, lda, a.seg[0].K, a.M, a.N, ldy, a.Y, tl);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------------------------ dispatch
-// Chunk rows (M <= 16): the direct kernel with one 16-column tile per workgroup and 8 waves over
-// K (the weights have no reuse, so the most workgroups and the most weight bytes in flight).
+// Chunk rows (M <= 16): one 16-column tile per workgroup (the weights have no reuse, so the most
+// workgroups), on the LDS-staged chunk kernel when K is one block of whole 256-byte blocks (4
+// waves up to K = 1024, else 8, two blocks staged per batch; 16 waves, one block per batch, and 2
+// to 8 waves measured the same or slower): M = 4 K = 1024 N = 3072 / K = 3072 N = 1024 4.26 / 5.87
+// -> 2.92 / 3.62 us, M = 16 4.48 / 6.61 -> 3.10 / 4.16 us against the direct kernel (its 16-row x
+// 64-byte register loads touch twice the cache lines per instruction); the direct kernel with 8
+// waves over K otherwise.
 // Prompt rows, when every K block is a whole number of stages (K a multiple of 256): the LDS tile
 // kernel, its tile chosen by measurement on MI355X with the weights cold, bit-identical across
 // tiles; the direct kernel's 32 x 32 tiles with 4 waves over K otherwise.
@@ -654,7 +783,11 @@ int64_t tiles(const MfmaArgs& a, int bm, int bn) {
 }
 
 hipError_t run(const MfmaArgs& a, hipStream_t s) {
-  if (a.M <= 16) return go_direct<1, 1, 8, 1>(a, s);
+  if (a.M <= 16) {
+    if (a.nseg == 1 && a.seg[0].K % 256 == 0 && a.lda <= INT32_MAX && a.ldy <= INT32_MAX)
+      return a.seg[0].K <= 1024 ? go_chunk<4, 2>(a, s) : go_chunk<8, 2>(a, s);
+    return go_direct<1, 1, 8, 1>(a, s);
+  }
   // the LDS tile kernels take 32-bit row strides; the direct kernel any
   if (!whole_stages(a, 256) || a.lda > INT32_MAX || a.ldy > INT32_MAX) return go_direct<2, 2, 4, 1>(a, s);
   const int64_t t48 = tiles(a, 64, 48), t32 = tiles(a, 32, 32);

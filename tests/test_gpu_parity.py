@@ -150,6 +150,53 @@ def test_epilogue_matrix(path, M, qm, bias, act, out):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("M,K,N", [(3, 512, 48), (11, 2304, 80)])
+@pytest.mark.parametrize("qm", ["tensor", "channel", "rowcol"])
+@pytest.mark.parametrize("act,out", [(ACT_NONE, OUT_FP32), (ACT_RELU, OUT_INT8), (ACT_SILU, OUT_BF16),
+                                     (ACT_SOFTPLUS, OUT_INT8), (ACT_GELU, OUT_FP32)])
+def test_epilogue_matrix_chunk_rows(M, K, N, qm, act, out):
+    """The LDS-staged chunk-row MFMA kernel (M <= 16, K whole 256-byte blocks; 4 waves at K=512, 8 at
+    K=2304) through every scale mode and output format with a bias, a huge scale and int8 -128."""
+    rng = np.random.default_rng(zlib.crc32(repr((M, K, N, qm, act, out, "chunk")).encode()))
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sc = rng.uniform(1e-4, 3e-2, N).astype(f32)
+    sc[N // 2] = 3e30
+    if qm == "tensor":
+        sc = sc[:1]
+    srow = rng.uniform(0.1, 2.0, M).astype(f32) if qm == "rowcol" else None
+    b = rng.normal(0, 2, N).astype(f32)
+    osc = f32(5.0) if out == OUT_INT8 else None
+    prev = ops.set_w8a8_path("mfma")
+    try:
+        y = ops.gemm_rowcol(cuda(A), None if srow is None else cuda(srow), cuda(W), cuda(sc), cuda(b),
+                            act=act, out=out, out_scale=osc)
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol(A, srow, W, sc, b, act=act, out=out, out_scale=osc)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 13, 16])
+@pytest.mark.parametrize("K,N", [(256, 3072), (1024, 3072), (3072, 1024), (6912, 1152), (2560, 1040)])
+def test_mfma_chunk_rows(M, K, N):
+    """The chunk-row MFMA kernel at every row count and at K from one 256-byte block to 27 (waves
+    with no block, one, two and several batches), the plain epilogue, on strided A and Y rows
+    (the gaps left as they were) for odd M."""
+    x, q, s, W, scol, rng = w8_inputs(M * 131 + K + N, M, N, K)
+    strided = M % 2 == 1
+    abig = cuda(np.concatenate([q, np.zeros((M, 256), np.int8)], axis=1)) if strided else cuda(q)
+    ybig = torch.full((M, N + 20 if strided else N), -7.0, dtype=torch.float32, device="cuda")
+    prev = ops.set_w8a8_path("mfma")
+    try:
+        ops.gemm_rowcol(abig[:, :K], cuda(s), cuda(W), cuda(scol), y=ybig[:, :N])
+    finally:
+        ops.set_w8a8_path(prev)
+    yb, want = host(ybig), G.gemm_rowcol(q, s, W, scol)
+    assert same(yb[:, :N].copy(), want), mismatch(yb[:, :N].copy(), want)
+    assert (yb[:, N:] == -7.0).all()
+
+
 def test_gemv_nan_from_inf_scale_is_canonical():
     A = np.zeros((1, 16), np.int8)
     W = np.ones((16, 16), np.int8)
