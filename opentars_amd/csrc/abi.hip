@@ -38,6 +38,22 @@ bool use_gemv(int M, int N, int K) {
   return M <= 16 && N < 2048;
 }
 
+// Automatic family for a K split of M rows, N output channels and ktot in all. Measured on MI355X
+// with the weights cold at 4096 + 2816 and 3456 + 3456 (N = 1152), 4096 + 4096 (N = 2048) and
+// 2048 + 2048 (N = 1024), M = 2 - 16: the GEMV family (weights read once per row block) at M <= 2;
+// with every block whole 256-byte blocks, the chunk-row MFMA kernel at M = 3 from 12M weight bytes
+// (4096 + 4096: 9.5 -> 7.6 us), at M = 4 - 8 from 6M (4096 + 2816, M = 4: 7.3 -> 6.7 us; M = 8:
+// 11.8 -> 7.3 us) and at every M >= 9; otherwise the direct MFMA kernel from M = 5 (3456 + 3456:
+// M = 4 7.4 against 10.4 us, M = 8 11.8 against 10.8 us).
+bool use_gemv_ksplit(int M, int N, int ktot, bool chunk) {
+  if (M <= 2) return true;
+  if (!chunk) return M <= 4;
+  const int64_t nk = static_cast<int64_t>(N) * ktot;
+  if (M <= 3) return nk < (12 << 20);
+  if (M <= 8) return nk < (6 << 20);
+  return false;
+}
+
 int fail(int code, const char* what) {
   g_last_error = what;
   return code;
@@ -362,7 +378,9 @@ int tars_gemm_w8a8_ksplit(const int8_t* A, int64_t lda, const float* srow,
   a.ldy = ldy;
   a.M = M;
   a.N = N;
-  const bool gemv = g_w8a8_path == 1 || (g_w8a8_path == 0 && M == 1);  // the K-split GEMV reads W per row
+  bool chunk = true;  // every block a whole number of 256-byte blocks: the MFMA family's chunk-row kernel
+  for (int i = 0; i < nblocks; ++i) chunk = chunk && K_blocks[i] % 256 == 0;
+  const bool gemv = g_w8a8_path == 1 || (g_w8a8_path == 0 && use_gemv_ksplit(M, N, ktot, chunk));
   hipStream_t s = static_cast<hipStream_t>(stream);
   return launched(gemv ? tars::launch_gemv_w8a8_ksplit(a, s) : tars::launch_gemm_w8a8_ksplit_mfma(a, s));
 }

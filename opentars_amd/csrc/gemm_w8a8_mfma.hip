@@ -632,11 +632,13 @@ hipError_t go_panel(const MfmaArgs& a, hipStream_t s) {
 // swizzle of mfma_tile_kernel's 16-row blocks), K split over the KW waves in 256-byte blocks. A
 // wave stages and reads only its own blocks, so it waits on its own loads and needs no workgroup
 // barrier until its int32 partial tile meets the others in LDS; wave 0 then forms the epilogue.
-template <int KW, int DB, bool SIMPLE>
+// A K split (KSPLIT) runs its blocks one after another, each block's fp32 partial added in block
+// order (llm.py:303-321).
+template <int KW, int DB, bool SIMPLE, bool KSPLIT>
 __global__ __launch_bounds__(64 * KW) void mfma_chunk_kernel(const int8_t* A, const int8_t* W, const float* scol,
                                                             const float* srow, int lda, int K, int M, int N, int ldy,
                                                             void* Y, TileTail tl) {
-  constexpr int SLOT = DB * 8192;
+  constexpr int SLOT = DB * 8192;    // DB blocks: weights 4 KiB + activations 4 KiB each
   constexpr int RP = 20;             // int32 pitch of a partial tile's row in LDS
   __shared__ __align__(16) int8_t lds[KW * SLOT];
   __shared__ __align__(16) int32_t red[KW][16][RP];
@@ -646,9 +648,9 @@ __global__ __launch_bounds__(64 * KW) void mfma_chunk_kernel(const int8_t* A, co
   const int li = lane & 15, lg = lane >> 4;
   const int nt = N >> 4, b = blockIdx.x;
   const int n0 = 16 * ((nt % 8 == 0) ? (b % 8) * (nt / 8) + b / 8 : b);
-  // wave 0's epilogue operands: row li / 4 ... (thread t < 64: row t >> 2, columns 4 (t & 3) ..)
+  // wave 0's epilogue operands: thread t < 64 owns row t >> 2, columns n0 + 4 (t & 3) .. + 3
   const int er = lane >> 2, ec = n0 + 4 * (lane & 3);
-  float sr = 0.0f, sc[4], bi[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float sr = 0.0f, sc[4], bi[4] = {0.0f, 0.0f, 0.0f, 0.0f}, chain[4];
   if (wave == 0) {
     float4 c4 = (SIMPLE || !tl.scol_per_tensor) ? *reinterpret_cast<const float4*>(scol + ec)
                                                 : make_float4(scol[0], scol[0], scol[0], scol[0]);
@@ -660,75 +662,87 @@ __global__ __launch_bounds__(64 * KW) void mfma_chunk_kernel(const int8_t* A, co
     sr = *(srow ? srow + min(er, M - 1) : scol);
   }
   issue_fence();
-  const int nb = K >> 8, b0 = nb * wave / KW, b1 = nb * (wave + 1) / KW;
   const int aq = (M + 3) >> 2;       // activation row quads holding live rows
   int8_t* const slot = lds + SLOT * wave;
-  v4i acc0 = zero, acc1 = zero;
-  for (int bb = b0; bb < b1; bb += DB) {
-    const int nbb = min(DB, b1 - bb);
-    // the previous batch's operand reads are done before its slot is refilled
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_wave_barrier();
+  const int nseg = KSPLIT ? tl.nseg : 1;
+  for (int sgi = 0; sgi < nseg; ++sgi) {
+    const int8_t* const Wg = (KSPLIT && sgi) ? tl.W[sgi] : W;
+    const int Kg = (KSPLIT && sgi) ? tl.K[sgi] : K;
+    const int8_t* const Ag = A + ((KSPLIT && sgi) ? tl.koff[sgi] : 0);
+    const int nb = Kg >> 8, b0 = nb * wave / KW, b1 = nb * (wave + 1) / KW;
+    v4i acc0 = zero, acc1 = zero;
+    for (int bb = b0; bb < b1; bb += DB) {
+      const int nbb = min(DB, b1 - bb);
+      // the previous batch's operand reads are done before its slot is refilled
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      if (d >= nbb) break;
+      for (int d = 0; d < DB; ++d) {
+        if (d >= nbb) break;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = 4 * q + lg, k = 256 * (bb + d) + 16 * (li ^ r);
-        stage16(W + static_cast<int64_t>(n0 + r) * K + k, slot + 8192 * d + 1024 * q);
-        if (q < aq) stage16(A + static_cast<int64_t>(min(r, M - 1)) * lda + k, slot + 8192 * d + 4096 + 1024 * q);
+        for (int q = 0; q < 4; ++q) {
+          const int r = 4 * q + lg, k = 256 * (bb + d) + 16 * (li ^ r);
+          stage16(Wg + static_cast<int64_t>(n0 + r) * Kg + k, slot + 8192 * d + 1024 * q);
+          if (q < aq) stage16(Ag + static_cast<int64_t>(min(r, M - 1)) * lda + k, slot + 8192 * d + 4096 + 1024 * q);
+        }
+      }
+      wait_vmcnt<0>();
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        if (d >= nbb) break;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int off = 8192 * d + 256 * li + 16 * ((4 * kk + lg) ^ li);
+          const v4i fw = *reinterpret_cast<const v4i*>(slot + off);
+          const v4i fa = *reinterpret_cast<const v4i*>(slot + off + 4096);
+          if (kk & 1) acc1 = mfma(fw, fa, acc1);
+          else acc0 = mfma(fw, fa, acc0);
+        }
       }
     }
-    wait_vmcnt<0>();
-    __builtin_amdgcn_wave_barrier();
+    // W is the MFMA's first operand: lane l holds columns 4 lg .. 4 lg + 3 of row li
+    if (KSPLIT && sgi) __syncthreads();  // wave 0 has read the previous block's partial tiles
+    *reinterpret_cast<v4i*>(&red[wave][li][4 * lg]) = acc0 + acc1;
+    __syncthreads();
+    if (wave == 0) {
+      v4i sum = *reinterpret_cast<const v4i*>(&red[0][er][4 * (lane & 3)]);
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      if (d >= nbb) break;
+      for (int w = 1; w < KW; ++w) sum += *reinterpret_cast<const v4i*>(&red[w][er][4 * (lane & 3)]);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int off = 8192 * d + 256 * li + 16 * ((4 * kk + lg) ^ li);
-        const v4i fw = *reinterpret_cast<const v4i*>(slot + off);
-        const v4i fa = *reinterpret_cast<const v4i*>(slot + off + 4096);
-        if (kk & 1) acc1 = mfma(fw, fa, acc1);
-        else acc0 = mfma(fw, fa, acc0);
+      for (int v = 0; v < 4; ++v) {
+        float y;
+        if constexpr (SIMPLE) {
+          y = fmul(fmul(i2f(sum[v]), sr), sc[v]);
+        } else {
+          y = i2f(sum[v]);
+          if (srow) y = fmul(y, sr);
+          y = fmul(y, sc[v]);
+          if (tl.bias) y = fadd(y, bi[v]);
+          y = act_fn(y, tl.act);
+        }
+        chain[v] = sgi == 0 ? y : fadd(chain[v], y);
       }
     }
   }
-  // W is the MFMA's first operand: lane l holds columns 4 lg .. 4 lg + 3 of row li
-  const v4i acc = acc0 + acc1;
-  *reinterpret_cast<v4i*>(&red[wave][li][4 * lg]) = acc;
-  __syncthreads();
-  if (wave != 0) return;
-  v4i sum = *reinterpret_cast<const v4i*>(&red[0][er][4 * (lane & 3)]);
-#pragma unroll
-  for (int w = 1; w < KW; ++w) sum += *reinterpret_cast<const v4i*>(&red[w][er][4 * (lane & 3)]);
-  float y[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    if constexpr (SIMPLE) {
-      y[v] = fmul(fmul(i2f(sum[v]), sr), sc[v]);
-    } else {
-      float z = i2f(sum[v]);
-      if (srow) z = fmul(z, sr);
-      z = fmul(z, sc[v]);
-      if (tl.bias) z = fadd(z, bi[v]);
-      y[v] = act_fn(z, tl.act);
-    }
-  }
-  if (er < M) {
-    if constexpr (SIMPLE) {
-      *reinterpret_cast<float4*>(static_cast<char*>(Y) + static_cast<int64_t>(er) * ldy + 4 * ec) =
-          make_float4(ftz(y[0]), ftz(y[1]), ftz(y[2]), ftz(y[3]));
-    } else {
-      store_out4(Y, static_cast<int64_t>(er) * ldy, ec, tl.out, y, tl.out_scale);
-    }
+  if (wave != 0 || er >= M) return;
+  if constexpr (SIMPLE) {
+    *reinterpret_cast<float4*>(static_cast<char*>(Y) + static_cast<int64_t>(er) * ldy + 4 * ec) =
+        make_float4(ftz(chain[0]), ftz(chain[1]), ftz(chain[2]), ftz(chain[3]));
+  } else {
+    store_out4(Y, static_cast<int64_t>(er) * ldy, ec, tl.out, chain, tl.out_scale);
   }
 }
 
 template <int KW, int DB = 2>
 hipError_t go_chunk(const MfmaArgs& a, hipStream_t s) {
   TileTail tl{};
-  tl.nseg = 1;
+  for (int i = 0; i < a.nseg; ++i) {
+    tl.W[i] = a.seg[i].W;
+    tl.K[i] = a.seg[i].K;
+    tl.koff[i] = a.seg[i].koff;
+  }
+  tl.nseg = a.nseg;
   tl.bias = a.epi.bias;
   tl.scol_per_tensor = a.epi.scol_per_tensor;
   tl.act = a.epi.act;
@@ -738,12 +752,18 @@ hipError_t go_chunk(const MfmaArgs& a, hipStream_t s) {
   const bool simple = e.srow && !e.scol_per_tensor && !e.bias && e.act == 0 && e.out == 0;
   const int lda = static_cast<int>(a.lda), ldy = static_cast<int>(a.ldy);
   const dim3 grid(a.N / 16), block(64 * KW);
-  if (simple)
-    hipLaunchKernelGGL((mfma_chunk_kernel<KW, DB, true>), grid, block, 0, s, a.A + a.seg[0].koff, a.seg[0].W, e.scol,
-                       e.srow, lda, a.seg[0].K, a.M, a.N, ldy, a.Y, tl);
-  else
-    hipLaunchKernelGGL((mfma_chunk_kernel<KW, DB, false>), grid, block, 0, s, a.A + a.seg[0].koff, a.seg[0].W, e.scol,
-                       e.srow, lda, a.seg[0].K, a.M, a.N, ldy, a.Y, tl);
+  const int8_t* A = a.A + a.seg[0].koff;
+#define TARS_CHUNK(SIMPLE, KSPLIT)                                                                                 \
+  hipLaunchKernelGGL((mfma_chunk_kernel<KW, DB, SIMPLE, KSPLIT>), grid, block, 0, s, A, a.seg[0].W, e.scol, e.srow, \
+                     lda, a.seg[0].K, a.M, a.N, ldy, a.Y, tl)
+  if (a.nseg > 1) {
+    if (simple) TARS_CHUNK(true, true);
+    else TARS_CHUNK(false, true);
+  } else {
+    if (simple) TARS_CHUNK(true, false);
+    else TARS_CHUNK(false, false);
+  }
+#undef TARS_CHUNK
   return hipGetLastError();
 }
 
@@ -784,8 +804,11 @@ int64_t tiles(const MfmaArgs& a, int bm, int bn) {
 
 hipError_t run(const MfmaArgs& a, hipStream_t s) {
   if (a.M <= 16) {
-    if (a.nseg == 1 && a.seg[0].K % 256 == 0 && a.lda <= INT32_MAX && a.ldy <= INT32_MAX)
-      return a.seg[0].K <= 1024 ? go_chunk<4, 2>(a, s) : go_chunk<8, 2>(a, s);
+    if (whole_stages(a, 256) && a.lda <= INT32_MAX && a.ldy <= INT32_MAX) {
+      int ktot = 0;
+      for (int i = 0; i < a.nseg; ++i) ktot += a.seg[i].K;
+      return ktot <= 1024 ? go_chunk<4, 2>(a, s) : go_chunk<8, 2>(a, s);
+    }
     return go_direct<1, 1, 8, 1>(a, s);
   }
   // the LDS tile kernels take 32-bit row strides; the direct kernel any

@@ -302,6 +302,25 @@ def test_c2_gemma3_down_ksplit(split, M):
     assert same(host(y), want), mismatch(host(y), want)
 
 
+@pytest.mark.parametrize("M", [2, 3, 7, 16])
+@pytest.mark.parametrize("split,N", [([256, 512, 1024], 1040), ([4096, 2816], 1152), ([1024, 256], 80)])
+def test_ksplit_chunk_rows(M, split, N):
+    """The K split on the chunk-row MFMA kernel (every block whole 256-byte blocks, M <= 16): blocks
+    run one after another through the waves' LDS slots, partials added in block order."""
+    x, q, s, W, scol, _ = w8_inputs(M * 17 + N + len(split), M, N, sum(split))
+    blocks, c0 = [], 0
+    for k in split:
+        blocks.append(np.ascontiguousarray(W[:, c0:c0 + k]))
+        c0 += k
+    prev = ops.set_w8a8_path("mfma")
+    try:
+        y = ops.gemm_rowcol_ksplit(cuda(q), cuda(s), [cuda(b) for b in blocks], cuda(scol))
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol_ksplit(q, s, blocks, scol)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 def test_ksplit_both_paths_agree():
     x, q, s, W, scol, _ = w8_inputs(5, 2, 256, 6912)
     blocks = [np.ascontiguousarray(W[:, :4096]), np.ascontiguousarray(W[:, 4096:])]
