@@ -829,6 +829,18 @@ __global__ __launch_bounds__(kThreads) void quant_gemv_norm_kernel(const float* 
 // N = 2048: 2.99 -> 2.80 us; with 1024 rows, 2.25 / 2.66 us at U = 1 against 2.36 / 2.89 at 2).
 // Rows of more than 8192 k (no activation chunks held in registers) keep one row per wave.
 int plain_rows_per_wave(int64_t rows, int M, int K) {
+  if (K <= 512) {
+    // rows of at most 32 chunks: L = 8, 16 or 32 lanes per row, so a workgroup holds
+    // kWaves * (64 / L) * U rows; the fewest rows per wave (U = 1, 2, 4, 8) that keep the grid at
+    // most 1024 workgroups. Measured (weights cold): K = 512: N = 4096 M = 1 / 4 2.82 / 3.97 ->
+    // 2.21 / 2.69 us, N = 16384 M = 4 4.64 -> 3.92 us, N = 32768 M = 1 4.73 -> 4.64 us; K = 256,
+    // N = 4096 M = 1 2.66 -> 2.05 us; K = 128, N = 4096 M = 1 2.70 -> 2.04 us (against U = 8 at every N)
+    const int L = K <= 128 ? 8 : K <= 256 ? 16 : 32;
+    const int64_t per = static_cast<int64_t>(kWaves) * (64 / L);
+    int u = 1;
+    while (u < 8 && (rows + per * u - 1) / (per * u) > 1024) u *= 2;
+    return u;
+  }
   return rows >= 32768 ? 4 : (M >= 3 && rows >= 2048 && K <= 8192) ? 2 : 1;
 }
 
@@ -840,6 +852,7 @@ int plain_rows_per_wave(int64_t rows, int M, int K) {
 // o (K = 2048) and down (K = 3072), 1024 rows, 2.85 / 3.11 us at U = 1 (3.10 / 3.38 at 2); the
 // head (151936 rows) 25.5 us at U = 4 (26.7 at 8).
 int fused_rows_per_wave(int64_t rows, int K) {
+  if (K <= 512) return 8;  // rows of at most 32 chunks: 8 rows per lane group
   int u = 1;
   while (u < 4 && rows / (kWaves * 2 * u) >= 256) u *= 2;
   const int64_t wgs = (rows + kWaves * u - 1) / (kWaves * u);
@@ -984,9 +997,15 @@ hipError_t go_fused(QuantGemvArgs& a, hipStream_t s) {
 template <class Args, template <int, int, int> class Go>
 hipError_t dispatch(Args& a, int K, int u, hipStream_t s) {
   const int C = K / 16;
-  if (C <= 8) return Go<8, 1, 8>::run(a, s);
-  if (C <= 16) return Go<16, 1, 8>::run(a, s);
-  if (C <= 32) return Go<32, 1, 8>::run(a, s);
+  if (C <= 8)
+    return u == 1 ? Go<8, 1, 1>::run(a, s) : u == 2 ? Go<8, 1, 2>::run(a, s) : u == 4 ? Go<8, 1, 4>::run(a, s)
+                                                                               : Go<8, 1, 8>::run(a, s);
+  if (C <= 16)
+    return u == 1 ? Go<16, 1, 1>::run(a, s) : u == 2 ? Go<16, 1, 2>::run(a, s) : u == 4 ? Go<16, 1, 4>::run(a, s)
+                                                                                 : Go<16, 1, 8>::run(a, s);
+  if (C <= 32)
+    return u == 1 ? Go<32, 1, 1>::run(a, s) : u == 2 ? Go<32, 1, 2>::run(a, s) : u == 4 ? Go<32, 1, 4>::run(a, s)
+                                                                                 : Go<32, 1, 8>::run(a, s);
   switch ((C + 63) / 64) {
     case 1:
       return u == 1 ? Go<64, 1, 1>::run(a, s) : u == 2 ? Go<64, 1, 2>::run(a, s)

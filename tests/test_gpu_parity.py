@@ -197,6 +197,23 @@ def test_mfma_chunk_rows(M, K, N):
     assert (yb[:, N:] == -7.0).all()
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("K", [128, 256, 512])
+@pytest.mark.parametrize("N", [80, 1040, 4096, 32768])
+def test_gemv_short_rows(M, K, N):
+    """GEMV rows of at most 32 chunks (8, 16 or 32 lanes per row) at 1, 2, 4 and 8 rows per lane
+    group, as the rows-per-wave rule picks them by N, bias and SiLU: bit-exact against the oracle."""
+    x, q, s, W, scol, rng = w8_inputs(M * 1009 + K + N, M, N, K)
+    b = rng.normal(0, 1, N).astype(f32)
+    prev = ops.set_w8a8_path("gemv")
+    try:
+        y = ops.gemm_rowcol(cuda(q), cuda(s), cuda(W), cuda(scol), cuda(b), act=ACT_SILU)
+    finally:
+        ops.set_w8a8_path(prev)
+    want = G.gemm_rowcol(q, s, W, scol, b, act=ACT_SILU)
+    assert same(host(y), want), mismatch(host(y), want)
+
+
 def test_gemv_nan_from_inf_scale_is_canonical():
     A = np.zeros((1, 16), np.int8)
     W = np.ones((16, 16), np.int8)
