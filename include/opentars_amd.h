@@ -301,9 +301,10 @@ const char* tars_last_error(void);
 
 /*
  * Kernel-family selection for W8A8 (test and benchmark control, not part of the reference's
- * interface): 0 = automatic (dot-product GEMV family for M <= 2; for M <= 4 unless K >= 3072,
- * N >= 4096 and K % 256 == 0; for M <= 8 unless N >= 4096 and K % 256 == 0; for M <= 16 when
- * N < 2048; INT8 MFMA family otherwise; for tars_gemm_w8a8_ksplit the GEMV family for M <= 2, for
+ * interface): 0 = automatic, by measurement (the dot-product GEMV family for M <= 2; with
+ * K % 256 == 0 for M <= 4 unless K >= 4096 and N >= 4096, for M <= 8 while N < 4096 and for
+ * M <= 16 while N < 2048; with other K for M <= 16 unless M >= 9, N >= 3072 and K >= 256, or
+ * M >= 5 and N * K >= 12 MiB; INT8 MFMA family otherwise; for tars_gemm_w8a8_ksplit the GEMV family for M <= 2, for
  * M <= 4 when a block is not whole 256-byte blocks, else for M = 3 under 12 MiB of weights and
  * M <= 8 under 6 MiB), 1 = force the GEMV family for every M, 2 = force the MFMA family
  * for every M. Results are identical either way. Returns the previous setting. Process-wide.

@@ -20,22 +20,28 @@ int g_w8a8_path = 0;  // 0 auto, 1 GEMV family, 2 MFMA family
 
 // Automatic family for a W8A8 product of M rows, N output channels and K: the dot-product GEMV
 // family (weights read once per 4 rows), or the INT8 MFMA family. Measured on MI355X with the
-// weights cold, over M = 2 - 16 and 14 (K, N) pairs from 1024 x 1024 to 1024 x 151936:
+// weights cold, over M = 2 - 16 and 26 (K, N) pairs from 128 x 2048 to 1024 x 151936:
 //  * M <= 2: the GEMV family everywhere;
-//  * M = 3 - 4: the GEMV family, except on the LDS-staged chunk-row MFMA kernel (K whole 256-byte
-//    blocks) at K >= 3072 and N >= 4096 (K = 4096, N = 4096: 6.2 -> 5.2 us; the decode chunk's own
-//    shapes stay on the GEMV family: K = 1024, N = 151936 28.7 against 42.5 us);
-//  * M = 5 - 8: two GEMV row blocks read the weights twice, so the chunk-row MFMA kernel from
-//    N = 4096 (K = 1024, N = 6144: 4.3 -> 3.6 us; N = 3072 ties, N <= 2048 keeps the GEMV family);
-//  * M = 9 - 16: the GEMV family while N < 2048 (too few 16-column MFMA tiles to fill the chip),
-//    the MFMA family otherwise (K = 1024, N = 3072, M = 12: 3.4 -> 3.0 us).
+//  * K whole 256-byte blocks (the LDS-staged chunk-row MFMA kernel): at M = 3 - 4 the MFMA family
+//    from K = 4096 and N = 4096 (4096 x 4096: 6.2 -> 5.2 us; 3072 x 8192 stays: 7.0 against 8.0 us,
+//    and so does every Qwen3-0.6B chunk shape, the head's 1024 x 151936 28.7 against 42.5 us); at
+//    M = 5 - 8, where two GEMV row blocks read the weights twice, from N = 4096 (1024 x 6144, M = 6:
+//    4.3 -> 3.6 us; N = 3072 ties); at M = 9 - 16 from N = 2048 (1024 x 3072, M = 12: 3.4 -> 3.0 us);
+//  * other K (the direct MFMA kernel): the MFMA family at M = 9 - 16 from N = 3072 and K = 256
+//    (1040 x 3072, M = 16: 5.8 -> 5.3 us) and at M = 5 - 16 from 12 MiB of weights (4112 x 4096,
+//    M = 5: 11.5 -> 9.2 us); the GEMV family otherwise (128 x 4096, M = 16: 2.4 against 4.1 us);
+//  * M > 16: the MFMA family.
 bool use_gemv(int M, int N, int K) {
   if (g_w8a8_path != 0) return g_w8a8_path == 1;
-  const bool chunk = K % 256 == 0;  // the MFMA family's chunk-row kernel takes this K
   if (M <= 2) return true;
-  if (M <= 4) return !(chunk && K >= 3072 && N >= 4096);
-  if (M <= 8) return !(chunk && N >= 4096);
-  return M <= 16 && N < 2048;
+  if (K % 256 == 0) {
+    if (M <= 4) return !(K >= 4096 && N >= 4096);
+    if (M <= 8) return N < 4096;
+    return M <= 16 && N < 2048;
+  }
+  if (M > 16) return false;
+  const int64_t nk = static_cast<int64_t>(N) * K;
+  return !((M >= 9 && N >= 3072 && K >= 256) || (M >= 5 && nk >= (12 << 20)));
 }
 
 // Automatic family for a K split of M rows, N output channels and ktot in all. Measured on MI355X
